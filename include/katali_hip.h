@@ -1,0 +1,182 @@
+/* katali_hip.h — C ABI of libkatali_hip, the MI355X (gfx950) backend for
+ * katali-lab's quantized expert-GEMV path.
+ *
+ * The engine finds this library at run time (dlopen / LoadLibrary, see
+ * katali_hip_loader.h); nothing links against it at build time. Plain C types
+ * only: device buffers are `void *` handles returned by katali_hip_malloc.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository,
+ * V/ = vendor/katali_gguf_dense/):
+ *   - The loader API the dense shim calls, declared in the reference's absent
+ *     include/katali_cuda.h and visible at its call sites in
+ *     V/src/katali_dense_cuda.c:19,27-31,40-41,48,52-54,65-71:
+ *       katali_cuda_probe / _status / _malloc / _free / _upload / _download /
+ *       _supports_type / _matvec  ->  katali_hip_<same name>.
+ *   - The fused-MoE, q8_1/DP4A, self-test and bench entry points of the closed
+ *     katali_cuda.dll (README.md:13,17,21,99-102,149-171,308-310), which have
+ *     no published signatures: defined here.
+ *
+ * Conventions (from the reference's SDK contract, V/include/katali_gguf_sdk.h:22-69):
+ *   - every int-returning call returns KATALI_HIP_OK (0) or a negative code;
+ *     katali_hip_last_error() gives a message for the calling thread;
+ *   - structs carry struct_size for forward compatibility;
+ *   - tensors use the GGUF layout: dims[0] = cols contiguous, dims[1] = rows
+ *     (V/include/katali_gguf.h:67); types are ggml ids (Q4_K = 12, Q6_K = 14).
+ *   - compute calls are asynchronous on the library stream; katali_hip_download
+ *     and katali_hip_sync wait for them. One caller thread at a time.
+ */
+#ifndef KATALI_HIP_H
+#define KATALI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KATALI_HIP_ABI_VERSION 1
+
+#define KATALI_HIP_OK 0
+#define KATALI_HIP_E_INVALID (-1)     /* bad argument or unsupported shape */
+#define KATALI_HIP_E_NODEVICE (-2)    /* no usable gfx950 device */
+#define KATALI_HIP_E_RUNTIME (-3)     /* HIP runtime error */
+#define KATALI_HIP_E_UNSUPPORTED (-4) /* type / option not implemented */
+#define KATALI_HIP_E_NOMEM (-5)       /* device allocation failed */
+#define KATALI_HIP_E_TIMEOUT (-6)     /* in-kernel dependency wait expired */
+
+#define KATALI_HIP_TYPE_Q4_K 12u
+#define KATALI_HIP_TYPE_Q6_K 14u
+
+int         katali_hip_abi_version(void);
+const char *katali_hip_last_error(void);
+
+/* ---- loader API (replaces katali_cuda_* at V/src/katali_dense_cuda.c) ---- */
+
+/* Non-zero when a gfx950 device is usable (initialises it on first call).
+ * Replaces katali_cuda_probe (V/src/katali_dense_cuda.c:19). */
+int         katali_hip_probe(void);
+/* Human-readable reason for the probe result (device name, or why not).
+ * Replaces katali_cuda_status (V/src/katali_dense_cuda.c:19). */
+const char *katali_hip_status(void);
+/* Replaces katali_cuda_malloc (V/src/katali_dense_cuda.c:30-31,40). */
+int katali_hip_malloc(void **dev, size_t bytes);
+/* Replaces katali_cuda_free (V/src/katali_dense_cuda.c:27-28,76-78). */
+int katali_hip_free(void *dev);
+/* Synchronous host->device copy. Replaces katali_cuda_upload (:41,52,65). */
+int katali_hip_upload(void *dev, const void *host, size_t bytes);
+/* Waits for queued work, then device->host. Replaces katali_cuda_download (:54,70). */
+int katali_hip_download(void *host, const void *dev, size_t bytes);
+/* 1 for Q4_K and Q6_K. Replaces katali_cuda_supports_type (:48,67). */
+int katali_hip_supports_type(uint32_t ggml_type);
+/* y[rows] = W[rows x cols] . x with fp32 x and y, W in GGUF layout on the
+ * device. With KATALI_CUDA_DP4A=1 (or KATALI_HIP_DP4A=1) in the environment x
+ * is quantized to q8_1 inside the kernel and dotted with v_dot4; otherwise
+ * weights are dequantized and dotted in fp32. cols % 256 == 0.
+ * Replaces katali_cuda_matvec (V/src/katali_dense_cuda.c:53,69). */
+int katali_hip_matvec(uint32_t type, const void *w_dev, uint64_t rows, uint64_t cols,
+                      const float *x_dev, float *y_dev);
+
+/* ---- runtime helpers ------------------------------------------------------ */
+int katali_hip_sync(void);
+int katali_hip_memset(void *dev, int value, size_t bytes);
+/* Run library work on an external stream (a hipStream_t, NULL = library's). */
+int katali_hip_set_stream(void *hip_stream);
+
+/* ---- q8_1 activation path (README.md:17, "quantized once on the device") -- */
+/* n % 32 == 0; writes n/32 36-byte block_q8_1 (d f16, s f16 = d*sum(q), qs). */
+int katali_hip_quantize_q8_1(const float *x_dev, uint64_t n, void *q8_dev);
+/* y = W . x with x given as q8_1 blocks (int8 x int8 -> int32 dot4 path). */
+int katali_hip_matvec_q8(uint32_t type, const void *w_dev, uint64_t rows, uint64_t cols,
+                         const void *xq8_dev, float *y_dev);
+/* Same with an fp32 x that every workgroup quantizes to q8_1 in LDS (one
+ * launch, bit-identical to quantize_q8_1 followed by matvec_q8). */
+int katali_hip_matvec_dp4a(uint32_t type, const void *w_dev, uint64_t rows, uint64_t cols,
+                           const float *x_dev, float *y_dev);
+/* Exact per-block int32 sums of the q8 GEMV, from the same device routines:
+ * Q4_K -> isums[rows][cols/32], Q6_K -> isums[rows][cols/16] (sum of
+ * (q6-32)*q8 per 16 values). For self-tests. */
+int katali_hip_block_isums(uint32_t type, const void *w_dev, uint64_t rows, uint64_t cols,
+                           const void *xq8_dev, int32_t *isums_dev);
+
+/* ---- fused MoE layer (README.md:13, one GPU call per MoE layer) ----------- */
+typedef struct KataliHipMoe {
+    uint32_t struct_size;                  /* sizeof(KataliHipMoe) */
+    uint32_t gate_type, up_type, down_type;/* Q4_K / Q6_K (gate and up equal) */
+    uint32_t hidden;                       /* gate/up columns, down rows (%256) */
+    uint32_t ffn;                          /* expert intermediate size (%256) */
+    uint32_t n_expert;                     /* routed experts (<= 512) */
+    const void *gate_exps, *up_exps, *down_exps; /* device, GGUF stacked experts:
+                                              [n_expert][rows][row_bytes] */
+    const void *gate_shexp, *up_shexp, *down_shexp; /* optional always-on shared
+                                              expert (same types and ffn), weight 1 */
+} KataliHipMoe;
+
+typedef struct KataliHipMoeRoute {
+    uint32_t struct_size;                  /* sizeof(KataliHipMoeRoute) */
+    int32_t n_sel;                         /* experts per token, 1..16 */
+    /* Either router logits (the kernel takes the top n_sel, largest first,
+     * lower index on ties, and renormalises softmax over them) ... */
+    const float *logits;                   /* device [n_expert] or NULL */
+    const int32_t *step;                   /* optional device index: logits +=
+                                              (*step) * logits_stride */
+    uint64_t logits_stride;
+    /* ... or an explicit selection. */
+    const int32_t *ids;                    /* device [n_sel] */
+    const float *weights;                  /* device [n_sel] */
+    int32_t *ids_out;                      /* optional device outputs */
+    float *weights_out;
+} KataliHipMoeRoute;
+
+/* y[hidden] = sum_r w_r * Down_e(SiLU(Gate_e x) * Up_e x) (+ shared expert).
+ * x is fp32 (x_dev) or already q8_1 (xq8_dev); exactly one is non-NULL. The
+ * activation and the SiLU-GLU output are quantized to q8_1 inside the kernel;
+ * dots use int8 v_dot4 with fp32 scales; the expert sum is in rank order. */
+int katali_hip_moe_layer(const KataliHipMoe *moe, const KataliHipMoeRoute *route,
+                         const float *x_dev, const void *xq8_dev, float *y_dev);
+
+/* Debug variant: also writes gate/up outputs gu_dev[n_slots][2][ffn] (fp32) and
+ * the quantized SiLU-GLU output hq8_dev[n_slots][ffn/32][36] (slot n_sel is the
+ * shared expert). */
+int katali_hip_moe_layer_debug(const KataliHipMoe *moe, const KataliHipMoeRoute *route,
+                               const float *x_dev, const void *xq8_dev, float *y_dev,
+                               float *gu_dev, void *hq8_dev);
+
+/* Advance a device step index: *step = (*step + 1) % n_steps (one tiny launch). */
+int katali_hip_step_advance(int32_t *step_dev, int32_t n_steps);
+
+/* ---- per-token graphs (hipGraph capture of the library stream) ------------ */
+int katali_hip_graph_begin(void);
+int katali_hip_graph_end(void **graph);
+int katali_hip_graph_launch(void *graph);
+int katali_hip_graph_destroy(void *graph);
+
+/* ---- timing (HIP events on the library stream) ---------------------------- */
+int katali_hip_event_create(void **event);
+int katali_hip_event_record(void *event);
+/* Waits for `end`, then *ms = elapsed between the two records. */
+int katali_hip_event_elapsed(void *start, void *end, float *ms);
+int katali_hip_event_destroy(void *event);
+
+/* ---- options --------------------------------------------------------------- */
+/* "moe_mode": 0 = two launches per layer, 1 = one launch (default). */
+int katali_hip_set_option(const char *name, int64_t value);
+int64_t katali_hip_get_option(const char *name);
+
+/* ---- self-test and synthetic data for the harnesses ------------------------ */
+/* cuda-dp4a-selftest equivalent (README.md:17): a synthetic Q4_K and Q6_K
+ * GEMV whose activation is exactly representable in q8_1, dotted by the fp32
+ * and the v_dot4 kernels; report gets rel_L2 lines. 0 when both agree to 1e-5. */
+int katali_hip_selftest(char *report, size_t cap);
+/* Fill nblocks Q4_K/Q6_K blocks: uniform random bytes, then d (and dmin)
+ * |N(0, d_sigma)| as f16. Deterministic in seed. */
+int katali_hip_synth_fill(uint32_t type, void *dev, uint64_t nblocks, uint64_t seed, float d_sigma);
+/* n values of N(0, sigma). */
+int katali_hip_synth_normal(float *dev, uint64_t n, uint64_t seed, float sigma);
+/* Streaming device copy (bandwidth / counter calibration), bytes % 16 == 0. */
+int katali_hip_copy(void *dst_dev, const void *src_dev, size_t bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KATALI_HIP_H */

@@ -1,0 +1,529 @@
+// katali_hip.cpp — the C ABI of libkatali_hip (include/katali_hip.h).
+//
+// Owns the device selection, one library stream (default priority), the
+// scratch buffers the MoE kernel needs, and argument validation. Compute entry
+// points enqueue on the library stream and return immediately; download and
+// sync wait. State is process-global, single caller thread (the reference
+// shim's model, V/src/katali_dense_cuda.c:7-12), with a mutex around init.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/katali_hip.h"
+#include "kq_launch.h"
+
+namespace {
+
+thread_local std::string g_err;
+std::mutex g_init_mu;
+bool g_inited = false;
+bool g_usable = false;
+std::string g_status = "not probed";
+int g_device = 0;
+hipStream_t g_own_stream = nullptr;
+hipStream_t g_stream = nullptr;
+bool g_capturing = false;
+
+// MoE scratch
+uint8_t *g_hq8 = nullptr;
+size_t g_hq8_cap = 0;
+uint32_t *g_sync = nullptr;
+int32_t *g_err_dev = nullptr;
+
+int64_t g_moe_mode = 1;
+
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(KATALI_HIP_E_RUNTIME, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool env_on(const char *name) {
+    const char *e = getenv(name);
+    return e && (e[0] == '1' || e[0] == 'y' || e[0] == 'Y');
+}
+
+int init_locked() {
+    if (g_inited) return g_usable ? KATALI_HIP_OK : KATALI_HIP_E_NODEVICE;
+    g_inited = true;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) {
+        g_status = std::string("no HIP device (") + (e != hipSuccess ? hipGetErrorString(e) : "count 0") + ")";
+        return KATALI_HIP_E_NODEVICE;
+    }
+    const char *dv = getenv("KATALI_HIP_DEVICE");
+    g_device = dv ? atoi(dv) : 0;
+    if (g_device < 0 || g_device >= n) {
+        g_status = "KATALI_HIP_DEVICE out of range";
+        return KATALI_HIP_E_NODEVICE;
+    }
+    hipDeviceProp_t p;
+    if ((e = hipGetDeviceProperties(&p, g_device)) != hipSuccess) {
+        g_status = std::string("hipGetDeviceProperties: ") + hipGetErrorString(e);
+        return KATALI_HIP_E_NODEVICE;
+    }
+    if (strncmp(p.gcnArchName, "gfx950", 6) != 0) {
+        g_status = std::string("unsupported device ") + p.gcnArchName + " (libkatali_hip is built for gfx950)";
+        return KATALI_HIP_E_NODEVICE;
+    }
+    if ((e = hipSetDevice(g_device)) != hipSuccess ||
+        (e = hipStreamCreateWithFlags(&g_own_stream, hipStreamNonBlocking)) != hipSuccess) {
+        g_status = std::string("device init: ") + hipGetErrorString(e);
+        return KATALI_HIP_E_NODEVICE;
+    }
+    g_stream = g_own_stream;
+    const char *mm = getenv("KATALI_HIP_MOE_MODE");
+    if (mm) g_moe_mode = atoi(mm) ? 1 : 0;
+    char buf[256];
+    snprintf(buf, sizeof buf, "%s (%s, %d CUs, %.0f GiB)", p.name, p.gcnArchName, p.multiProcessorCount,
+             (double)p.totalGlobalMem / (1024.0 * 1024.0 * 1024.0));
+    g_status = buf;
+    g_usable = true;
+    return KATALI_HIP_OK;
+}
+
+int ensure() {
+    std::lock_guard<std::mutex> lk(g_init_mu);
+    int rc = init_locked();
+    if (rc != KATALI_HIP_OK) return fail(rc, "no usable device: %s", g_status.c_str());
+    hipError_t e = hipSetDevice(g_device);
+    return e == hipSuccess ? KATALI_HIP_OK : hip_fail(e, "hipSetDevice");
+}
+
+bool type_ok(uint32_t t) { return t == KATALI_HIP_TYPE_Q4_K || t == KATALI_HIP_TYPE_Q6_K; }
+
+int check_gemv(uint32_t type, const void *w, uint64_t rows, uint64_t cols, const void *x, const void *y) {
+    if (!type_ok(type)) return fail(KATALI_HIP_E_UNSUPPORTED, "type %u not supported (Q4_K=12, Q6_K=14)", type);
+    if (!w || !x || !y) return fail(KATALI_HIP_E_INVALID, "null buffer");
+    if (cols == 0 || cols % 256) return fail(KATALI_HIP_E_INVALID, "cols=%llu not a multiple of 256",
+                                             (unsigned long long)cols);
+    if (cols > 32768) return fail(KATALI_HIP_E_INVALID, "cols=%llu above 32768", (unsigned long long)cols);
+    if (rows > 0xFFFFFFFFull) return fail(KATALI_HIP_E_INVALID, "rows above 2^32");
+    return KATALI_HIP_OK;
+}
+
+int launched(hipError_t e, const char *what) { return e == hipSuccess ? KATALI_HIP_OK : hip_fail(e, what); }
+
+// MoE scratch: allocated outside any capture; grows only when not capturing.
+int moe_scratch(size_t hq8_bytes) {
+    if (!g_sync) {
+        if (g_capturing) return fail(KATALI_HIP_E_INVALID, "first MoE call must happen outside graph capture");
+        hipError_t e = hipMalloc((void **)&g_sync, kq::moe_sync_words() * 4);
+        if (e != hipSuccess) return hip_fail(e, "hipMalloc(moe sync)");
+        if ((e = hipMalloc((void **)&g_err_dev, 64)) != hipSuccess) return hip_fail(e, "hipMalloc(moe err)");
+        if ((e = hipMemset(g_sync, 0, kq::moe_sync_words() * 4)) != hipSuccess) return hip_fail(e, "hipMemset");
+        if ((e = hipMemset(g_err_dev, 0, 64)) != hipSuccess) return hip_fail(e, "hipMemset");
+    }
+    if (hq8_bytes > g_hq8_cap) {
+        if (g_capturing) return fail(KATALI_HIP_E_INVALID, "MoE scratch must grow outside graph capture");
+        if (g_hq8) {
+            hipError_t e = hipStreamSynchronize(g_stream);
+            if (e == hipSuccess) e = hipFree(g_hq8);
+            g_hq8 = nullptr;
+            g_hq8_cap = 0;
+            if (e != hipSuccess) return hip_fail(e, "release moe scratch");
+        }
+        size_t cap = hq8_bytes < (1u << 20) ? (1u << 20) : hq8_bytes;
+        hipError_t e = hipMalloc((void **)&g_hq8, cap);
+        if (e != hipSuccess) {
+            g_hq8 = nullptr;
+            g_hq8_cap = 0;
+            return hip_fail(e, "hipMalloc(moe scratch)");
+        }
+        g_hq8_cap = cap;
+    }
+    return KATALI_HIP_OK;
+}
+
+int moe_impl(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, const void *xq, float *y,
+             float *gu_dbg, void *hq8_dbg) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!m || !r || m->struct_size < sizeof(KataliHipMoe) || r->struct_size < sizeof(KataliHipMoeRoute))
+        return fail(KATALI_HIP_E_INVALID, "null or short MoE descriptor");
+    if (!type_ok(m->gate_type) || !type_ok(m->down_type) || m->up_type != m->gate_type)
+        return fail(KATALI_HIP_E_UNSUPPORTED, "MoE types gate=%u up=%u down=%u", m->gate_type, m->up_type, m->down_type);
+    if (!m->hidden || m->hidden % 256 || m->hidden > 16384 || !m->ffn || m->ffn % 256 || m->ffn > 16384)
+        return fail(KATALI_HIP_E_INVALID, "MoE hidden=%u ffn=%u (need multiples of 256, <= 16384)", m->hidden, m->ffn);
+    if (!m->n_expert || m->n_expert > 512) return fail(KATALI_HIP_E_INVALID, "n_expert=%u", m->n_expert);
+    if (!m->gate_exps || !m->up_exps || !m->down_exps || !y) return fail(KATALI_HIP_E_INVALID, "null buffer");
+    if ((x == nullptr) == (xq == nullptr)) return fail(KATALI_HIP_E_INVALID, "give exactly one of x_dev / xq8_dev");
+    if (r->n_sel < 1 || r->n_sel > 16 || (uint32_t)r->n_sel > m->n_expert)
+        return fail(KATALI_HIP_E_INVALID, "n_sel=%d", r->n_sel);
+    if (!r->logits && (!r->ids || !r->weights)) return fail(KATALI_HIP_E_INVALID, "need logits or ids+weights");
+    const bool shared = m->gate_shexp || m->up_shexp || m->down_shexp;
+    if (shared && !(m->gate_shexp && m->up_shexp && m->down_shexp))
+        return fail(KATALI_HIP_E_INVALID, "shared expert needs gate, up and down");
+    const uint32_t n_slots = (uint32_t)r->n_sel + (shared ? 1 : 0);
+    const size_t hq8_bytes = (size_t)n_slots * (m->ffn / 32) * 36;
+    if ((rc = moe_scratch(hq8_bytes))) return rc;
+
+    kq::MoeArgs a;
+    memset(&a, 0, sizeof a);
+    a.gate = (const uint8_t *)m->gate_exps;
+    a.up = (const uint8_t *)m->up_exps;
+    a.down = (const uint8_t *)m->down_exps;
+    a.gate_sh = (const uint8_t *)m->gate_shexp;
+    a.up_sh = (const uint8_t *)m->up_shexp;
+    a.down_sh = (const uint8_t *)m->down_shexp;
+    a.gate_type = m->gate_type;
+    a.up_type = m->up_type;
+    a.down_type = m->down_type;
+    a.hidden = m->hidden;
+    a.ffn = m->ffn;
+    a.n_expert = m->n_expert;
+    a.n_sel = r->n_sel;
+    a.has_shared = shared ? 1 : 0;
+    a.x = x;
+    a.xq = (const uint8_t *)xq;
+    a.logits = r->logits;
+    a.step = r->step;
+    a.logits_stride = r->logits_stride;
+    a.ids = r->ids;
+    a.wts = r->weights;
+    a.ids_out = r->ids_out;
+    a.wts_out = r->weights_out;
+    a.y = y;
+    a.hq8 = g_hq8;
+    a.sync = g_sync;
+    a.dbg_gu = gu_dbg;
+    a.err = g_err_dev;
+    int grid = 0;
+    rc = launched(kq::launch_moe(a, (int)g_moe_mode, g_stream, &grid), "moe launch");
+    if (rc) return rc;
+    if (hq8_dbg) {
+        hipError_t e = hipMemcpyAsync(hq8_dbg, g_hq8, hq8_bytes, hipMemcpyDeviceToDevice, g_stream);
+        if (e != hipSuccess) return hip_fail(e, "copy hq8");
+    }
+    return KATALI_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int katali_hip_abi_version(void) { return KATALI_HIP_ABI_VERSION; }
+const char *katali_hip_last_error(void) { return g_err.c_str(); }
+
+int katali_hip_probe(void) {
+    std::lock_guard<std::mutex> lk(g_init_mu);
+    return init_locked() == KATALI_HIP_OK ? 1 : 0;
+}
+
+const char *katali_hip_status(void) { return g_status.c_str(); }
+
+int katali_hip_malloc(void **dev, size_t bytes) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!dev) return fail(KATALI_HIP_E_INVALID, "null out pointer");
+    *dev = nullptr;
+    hipError_t e = hipMalloc(dev, bytes ? bytes : 1);
+    if (e != hipSuccess) return fail(KATALI_HIP_E_NOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    return KATALI_HIP_OK;
+}
+
+int katali_hip_free(void *dev) {
+    if (!dev) return KATALI_HIP_OK;
+    int rc = ensure();
+    if (rc) return rc;
+    hipError_t e = hipStreamSynchronize(g_stream);
+    if (e == hipSuccess) e = hipFree(dev);
+    return e == hipSuccess ? KATALI_HIP_OK : hip_fail(e, "hipFree");
+}
+
+int katali_hip_upload(void *dev, const void *host, size_t bytes) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!bytes) return KATALI_HIP_OK;
+    if (!dev || !host) return fail(KATALI_HIP_E_INVALID, "null buffer");
+    hipError_t e = hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, g_stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+    return e == hipSuccess ? KATALI_HIP_OK : hip_fail(e, "upload");
+}
+
+int katali_hip_download(void *host, const void *dev, size_t bytes) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!bytes) return katali_hip_sync();
+    if (!dev || !host) return fail(KATALI_HIP_E_INVALID, "null buffer");
+    hipError_t e = hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, g_stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+    return e == hipSuccess ? KATALI_HIP_OK : hip_fail(e, "download");
+}
+
+int katali_hip_supports_type(uint32_t t) { return type_ok(t) ? 1 : 0; }
+
+int katali_hip_matvec(uint32_t type, const void *w, uint64_t rows, uint64_t cols, const float *x, float *y) {
+    int rc = ensure();
+    if (rc || (rc = check_gemv(type, w, rows, cols, x, y))) return rc;
+    if (!rows) return KATALI_HIP_OK;
+    const int mode = (env_on("KATALI_CUDA_DP4A") || env_on("KATALI_HIP_DP4A")) ? 2 : 0;
+    return launched(kq::launch_gemv(type, (const uint8_t *)w, rows, cols, x, nullptr, y, mode, g_stream), "matvec");
+}
+
+int katali_hip_sync(void) {
+    int rc = ensure();
+    if (rc) return rc;
+    hipError_t e = hipStreamSynchronize(g_stream);
+    if (e != hipSuccess) return hip_fail(e, "sync");
+    if (g_err_dev) {
+        int32_t err = 0;
+        e = hipMemcpy(&err, g_err_dev, 4, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) return hip_fail(e, "read error word");
+        if (err) {
+            (void)hipMemset(g_err_dev, 0, 4);
+            if (err & 1) return fail(KATALI_HIP_E_TIMEOUT, "MoE dependency wait timed out (grid not co-resident?)");
+            return fail(KATALI_HIP_E_INVALID, "MoE expert id outside [0, n_expert) (bad ids or non-finite logits)");
+        }
+    }
+    return KATALI_HIP_OK;
+}
+
+int katali_hip_memset(void *dev, int value, size_t bytes) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!dev) return fail(KATALI_HIP_E_INVALID, "null buffer");
+    return launched(hipMemsetAsync(dev, value, bytes, g_stream), "memset");
+}
+
+int katali_hip_set_stream(void *s) {
+    int rc = ensure();
+    if (rc) return rc;
+    g_stream = s ? (hipStream_t)s : g_own_stream;
+    return KATALI_HIP_OK;
+}
+
+int katali_hip_quantize_q8_1(const float *x, uint64_t n, void *q8) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!x || !q8) return fail(KATALI_HIP_E_INVALID, "null buffer");
+    if (n % 32) return fail(KATALI_HIP_E_INVALID, "n=%llu not a multiple of 32", (unsigned long long)n);
+    if (!n) return KATALI_HIP_OK;
+    return launched(kq::launch_quantize_q8_1(x, n, (uint8_t *)q8, g_stream), "quantize_q8_1");
+}
+
+int katali_hip_matvec_q8(uint32_t type, const void *w, uint64_t rows, uint64_t cols, const void *xq8, float *y) {
+    int rc = ensure();
+    if (rc || (rc = check_gemv(type, w, rows, cols, xq8, y))) return rc;
+    if (!rows) return KATALI_HIP_OK;
+    return launched(kq::launch_gemv(type, (const uint8_t *)w, rows, cols, nullptr, (const uint8_t *)xq8, y, 1, g_stream),
+                    "matvec_q8");
+}
+
+int katali_hip_matvec_dp4a(uint32_t type, const void *w, uint64_t rows, uint64_t cols, const float *x, float *y) {
+    int rc = ensure();
+    if (rc || (rc = check_gemv(type, w, rows, cols, x, y))) return rc;
+    if (!rows) return KATALI_HIP_OK;
+    return launched(kq::launch_gemv(type, (const uint8_t *)w, rows, cols, x, nullptr, y, 2, g_stream), "matvec_dp4a");
+}
+
+int katali_hip_block_isums(uint32_t type, const void *w, uint64_t rows, uint64_t cols, const void *xq8, int32_t *out) {
+    int rc = ensure();
+    if (rc || (rc = check_gemv(type, w, rows, cols, xq8, out))) return rc;
+    if (!rows) return KATALI_HIP_OK;
+    return launched(kq::launch_isums(type, (const uint8_t *)w, rows, cols, (const uint8_t *)xq8, out, g_stream),
+                    "block_isums");
+}
+
+int katali_hip_moe_layer(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, const void *xq, float *y) {
+    return moe_impl(m, r, x, xq, y, nullptr, nullptr);
+}
+
+int katali_hip_moe_layer_debug(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, const void *xq,
+                               float *y, float *gu, void *hq8) {
+    return moe_impl(m, r, x, xq, y, gu, hq8);
+}
+
+int katali_hip_step_advance(int32_t *step, int32_t n_steps) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!step || n_steps < 1) return fail(KATALI_HIP_E_INVALID, "step/n_steps");
+    return launched(kq::launch_step_advance(step, n_steps, g_stream), "step_advance");
+}
+
+int katali_hip_graph_begin(void) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (g_capturing) return fail(KATALI_HIP_E_INVALID, "capture already active");
+    hipError_t e = hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamBeginCapture");
+    g_capturing = true;
+    return KATALI_HIP_OK;
+}
+
+int katali_hip_graph_end(void **graph) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!g_capturing) return fail(KATALI_HIP_E_INVALID, "no capture active");
+    g_capturing = false;
+    hipGraph_t gr = nullptr;
+    hipError_t e = hipStreamEndCapture(g_stream, &gr);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+    hipGraphExec_t ex = nullptr;
+    e = hipGraphInstantiate(&ex, gr, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(gr);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    if (!graph) {
+        (void)hipGraphExecDestroy(ex);
+        return fail(KATALI_HIP_E_INVALID, "null graph out");
+    }
+    *graph = (void *)ex;
+    return KATALI_HIP_OK;
+}
+
+int katali_hip_graph_launch(void *graph) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!graph) return fail(KATALI_HIP_E_INVALID, "null graph");
+    return launched(hipGraphLaunch((hipGraphExec_t)graph, g_stream), "hipGraphLaunch");
+}
+
+int katali_hip_graph_destroy(void *graph) {
+    if (!graph) return KATALI_HIP_OK;
+    hipError_t e = hipGraphExecDestroy((hipGraphExec_t)graph);
+    return e == hipSuccess ? KATALI_HIP_OK : hip_fail(e, "hipGraphExecDestroy");
+}
+
+int katali_hip_event_create(void **ev) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!ev) return fail(KATALI_HIP_E_INVALID, "null out pointer");
+    return launched(hipEventCreate((hipEvent_t *)ev), "hipEventCreate");
+}
+
+int katali_hip_event_record(void *ev) {
+    int rc = ensure();
+    if (rc) return rc;
+    return launched(hipEventRecord((hipEvent_t)ev, g_stream), "hipEventRecord");
+}
+
+int katali_hip_event_elapsed(void *a, void *b, float *ms) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!a || !b || !ms) return fail(KATALI_HIP_E_INVALID, "null argument");
+    hipError_t e = hipEventSynchronize((hipEvent_t)b);
+    if (e == hipSuccess) e = hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b);
+    return e == hipSuccess ? KATALI_HIP_OK : hip_fail(e, "hipEventElapsedTime");
+}
+
+int katali_hip_event_destroy(void *ev) {
+    if (!ev) return KATALI_HIP_OK;
+    return launched(hipEventDestroy((hipEvent_t)ev), "hipEventDestroy");
+}
+
+int katali_hip_set_option(const char *name, int64_t value) {
+    if (!name) return fail(KATALI_HIP_E_INVALID, "null option name");
+    if (!strcmp(name, "moe_mode")) {
+        if (value != 0 && value != 1) return fail(KATALI_HIP_E_INVALID, "moe_mode must be 0 or 1");
+        std::lock_guard<std::mutex> lk(g_init_mu);
+        init_locked();
+        g_moe_mode = value;
+        return KATALI_HIP_OK;
+    }
+    return fail(KATALI_HIP_E_UNSUPPORTED, "unknown option %s", name);
+}
+
+int64_t katali_hip_get_option(const char *name) {
+    if (name && !strcmp(name, "moe_mode")) return g_moe_mode;
+    return -1;
+}
+
+int katali_hip_synth_fill(uint32_t type, void *dev, uint64_t nblocks, uint64_t seed, float d_sigma) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!type_ok(type)) return fail(KATALI_HIP_E_UNSUPPORTED, "type %u", type);
+    if (!dev) return fail(KATALI_HIP_E_INVALID, "null buffer");
+    if (!nblocks) return KATALI_HIP_OK;
+    return launched(kq::launch_synth_blocks(type, (uint8_t *)dev, nblocks, seed, d_sigma, g_stream), "synth_fill");
+}
+
+int katali_hip_synth_normal(float *dev, uint64_t n, uint64_t seed, float sigma) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!dev) return fail(KATALI_HIP_E_INVALID, "null buffer");
+    if (!n) return KATALI_HIP_OK;
+    return launched(kq::launch_synth_normal(dev, n, seed, sigma, g_stream), "synth_normal");
+}
+
+int katali_hip_copy(void *dst, const void *src, size_t bytes) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!dst || !src || bytes % 16) return fail(KATALI_HIP_E_INVALID, "copy needs non-null buffers, bytes %% 16 == 0");
+    return launched(kq::launch_copy((const uint8_t *)src, (uint8_t *)dst, bytes, g_stream), "copy");
+}
+
+int katali_hip_selftest(char *report, size_t cap) {
+    int rc = ensure();
+    if (rc) return rc;
+    std::string rep;
+    int failures = 0;
+    const uint64_t rows = 512, cols = 2048;
+    // activation exactly representable in q8_1: per block d = 2^-6, q in
+    // [-127, 127] with |q[0]| = 127, so quantization reproduces it exactly
+    std::vector<float> x(cols);
+    uint64_t s = 0x9E3779B97F4A7C15ull;
+    for (uint64_t i = 0; i < cols; i++) {
+        s ^= s << 13; s ^= s >> 7; s ^= s << 17;
+        int q = (int)(s % 255) - 127;
+        if (i % 32 == 0) q = (s & 1) ? 127 : -127;
+        x[i] = (float)q / 64.0f;
+    }
+    for (uint32_t type : {KATALI_HIP_TYPE_Q4_K, KATALI_HIP_TYPE_Q6_K}) {
+        const uint64_t bb = type == KATALI_HIP_TYPE_Q4_K ? 144 : 210;
+        const uint64_t nbl = rows * cols / 256;
+        void *w = nullptr, *xd = nullptr, *y0 = nullptr, *y1 = nullptr;
+        if ((rc = katali_hip_malloc(&w, nbl * bb)) || (rc = katali_hip_malloc(&xd, cols * 4)) ||
+            (rc = katali_hip_malloc(&y0, rows * 4)) || (rc = katali_hip_malloc(&y1, rows * 4))) {
+            katali_hip_free(w); katali_hip_free(xd); katali_hip_free(y0); katali_hip_free(y1);
+            return rc;
+        }
+        std::vector<float> a(rows), b(rows);
+        rc = katali_hip_synth_fill(type, w, nbl, 1234 + type, 0.02f);
+        if (!rc) rc = katali_hip_upload(xd, x.data(), cols * 4);
+        if (!rc) rc = launched(kq::launch_gemv(type, (const uint8_t *)w, rows, cols, (const float *)xd, nullptr,
+                                               (float *)y0, 0, g_stream), "selftest fp32");
+        if (!rc) rc = katali_hip_matvec_dp4a(type, w, rows, cols, (const float *)xd, (float *)y1);
+        if (!rc) rc = katali_hip_download(a.data(), y0, rows * 4);
+        if (!rc) rc = katali_hip_download(b.data(), y1, rows * 4);
+        katali_hip_free(w); katali_hip_free(xd); katali_hip_free(y0); katali_hip_free(y1);
+        if (rc) return rc;
+        double num = 0, den = 0;
+        for (uint64_t i = 0; i < rows; i++) {
+            num += ((double)a[i] - b[i]) * ((double)a[i] - b[i]);
+            den += (double)a[i] * a[i];
+        }
+        const double rel = den > 0 ? sqrt(num / den) : sqrt(num);
+        const bool ok = rel <= 1e-5;
+        failures += ok ? 0 : 1;
+        char line[160];
+        snprintf(line, sizeof line, "dp4a-selftest %s %llux%llu: rel_L2(dp4a, fp32) = %.3e %s\n",
+                 type == KATALI_HIP_TYPE_Q4_K ? "Q4_K" : "Q6_K", (unsigned long long)rows, (unsigned long long)cols,
+                 rel, ok ? "PASS" : "FAIL");
+        rep += line;
+    }
+    if (report && cap) {
+        strncpy(report, rep.c_str(), cap - 1);
+        report[cap - 1] = 0;
+    }
+    return failures ? fail(KATALI_HIP_E_RUNTIME, "selftest: %d failure(s)", failures) : KATALI_HIP_OK;
+}
+
+}  // extern "C"

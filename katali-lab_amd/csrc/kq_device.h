@@ -1,0 +1,398 @@
+// kq_device.h — device-side building blocks for the Q4_K / Q6_K x q8_1 path on
+// gfx950 (CDNA4, wave64).
+//
+// Formats (the public GGUF block layouts, as decoded by the reference at
+// vendor/katali_gguf_dense/src/gguf_dtype.c:328-335,350-358,429-452,487-512):
+//   Q4_K  144 B / 256 values: d f16 @0, dmin f16 @2, 12 B packed 6-bit
+//         scales/mins @4, 128 B nibbles @16. qs[32g..32g+31] holds values
+//         64g..64g+31 in the low nibbles and 64g+32..64g+63 in the high ones.
+//   Q6_K  210 B / 256 values: ql[128] @0, qh[64] @128, int8 sc[16] @192,
+//         d f16 @208. Value e = 128n + 32t + l takes ql[64n+l+32(t&1)] (low
+//         nibble for t<2, high for t>=2) and bits 2t..2t+1 of qh[32n+l];
+//         scale sc[e/16].
+//   Q8_1   36 B / 32 values: d f16 @0, s f16 @2, int8 qs[32] @4.
+//
+// Work decomposition: one "item" is the share of a super-block that one lane
+// dots: 16 bytes of Q4_K nibbles (8 items per block, 32 values) or 48 bytes of
+// Q6_K ql/ql/qh (4 items per block, 64 values). Integer partial sums are exact
+// (v_dot4_i32_i8); scales are applied in fp32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kq {
+
+constexpr uint32_t T_F32 = 0, T_Q8_1 = 9, T_Q4_K = 12, T_Q6_K = 14;
+constexpr int WAVE = 64;
+
+// ---------------------------------------------------------------------------
+// scalar helpers
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float h2f(uint32_t h16) {
+    _Float16 h;
+    const uint16_t v = (uint16_t)h16;
+    __builtin_memcpy(&h, &v, 2);
+    return (float)h;
+}
+__device__ __forceinline__ uint32_t f2h_rne(float f) {
+    const _Float16 h = (_Float16)f;   // v_cvt_f16_f32, round to nearest even
+    uint16_t v;
+    __builtin_memcpy(&v, &h, 2);
+    return v;
+}
+// 16-byte load from any byte address (the gfx950 code model allows unaligned
+// global dwordx4 loads; the compiler emits them itself for byte-aligned memcpy).
+__device__ __forceinline__ uint4 ld16(const uint8_t *p) {
+    uint4 v;
+    __builtin_memcpy(&v, p, 16);
+    return v;
+}
+__device__ __forceinline__ uint2 ld8(const uint8_t *p) {
+    uint2 v;
+    __builtin_memcpy(&v, p, 8);
+    return v;
+}
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t *p) {
+    uint16_t v;
+    __builtin_memcpy(&v, p, 2);
+    return v;
+}
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+__device__ __forceinline__ float wave_sum_xor(float v, int width) {
+    for (int o = width >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+
+// exp by Cody-Waite reduction x = n*ln2 + r (ln2 split into a 15-bit high part,
+// exact for |n| <= 256, and a low correction) and a degree-7 Taylor polynomial
+// for e^r, |r| <= ln2/2, evaluated by Horner with fused multiply-adds. Every
+// step is an IEEE fp32 operation with a single rounding, so the CPU oracle
+// reproduces it bit for bit. Input clamped to [-80, 88].
+__device__ __forceinline__ float kq_expf(float x) {
+    x = fminf(fmaxf(x, -80.0f), 88.0f);
+    const float n = rintf(x * 1.44269502f);
+    float r = fmaf(-n, 0.693145752f, x);
+    r = fmaf(-n, 1.42860677e-06f, r);
+    float p = 1.0f / 5040.0f;
+    p = fmaf(p, r, 1.0f / 720.0f);
+    p = fmaf(p, r, 1.0f / 120.0f);
+    p = fmaf(p, r, 1.0f / 24.0f);
+    p = fmaf(p, r, 1.0f / 6.0f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    return p * __uint_as_float((uint32_t)((int)n + 127) << 23);
+}
+// SiLU-GLU: g / (1 + exp(-g)) * u (correctly rounded division).
+__device__ __forceinline__ float kq_silu_mul(float g, float u) {
+    const float e = kq_expf(-g);
+    const float den = 1.0f + e;
+    const float s = g / den;
+    return s * u;
+}
+
+// ---------------------------------------------------------------------------
+// q8_1 activation in LDS
+//   qs   int8[K]        the quantized values
+//   d8   float[K/32]    f16-decoded block scale (what dequantization uses)
+//   qs16 int[K/16]      exact sums of each 16-value half block
+// ---------------------------------------------------------------------------
+struct Act {
+    int8_t *qs;
+    float *d8;
+    int *qs16;
+};
+__host__ __device__ constexpr uint32_t act_bytes(uint32_t K) { return K + K / 8 + K / 4; }
+__device__ __forceinline__ Act act_carve(uint8_t *base, uint32_t K) {
+    Act a;
+    a.qs = (int8_t *)base;
+    a.d8 = (float *)(base + K);
+    a.qs16 = (int *)(base + K + K / 8);
+    return a;
+}
+
+// Quantize one 32-value block with 8 lanes x 4 values (lanes part=0..7 of an
+// aligned 8-lane group). Returns the packed 4 int8 of this lane; the block's
+// f16 d / s and half-block sums are returned through refs (valid in all 8 lanes).
+// Definition (block_q8_1): amax = max|x|; d = amax/127; id = d ? 1/d : 0;
+// q = roundf(x*id); d_f16 = rne(d); s_f16 = rne((float)sum(q) * d).
+__device__ __forceinline__ uint32_t quant_q8_1_part(float4 v, uint32_t &d16, uint32_t &s16,
+                                                    int &sum_lo, int &sum_hi, float &d_dec) {
+    float am = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    am = fmaxf(am, __shfl_xor(am, 1, WAVE));
+    am = fmaxf(am, __shfl_xor(am, 2, WAVE));
+    am = fmaxf(am, __shfl_xor(am, 4, WAVE));
+    const float d = am / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const int q0 = (int)roundf(v.x * id), q1 = (int)roundf(v.y * id);
+    const int q2 = (int)roundf(v.z * id), q3 = (int)roundf(v.w * id);
+    int s = q0 + q1 + q2 + q3;
+    s += __shfl_xor(s, 1, WAVE);
+    s += __shfl_xor(s, 2, WAVE);      // sum of this lane's half block (4 lanes)
+    const int other = __shfl_xor(s, 4, WAVE);
+    const int part = threadIdx.x & 7;
+    sum_lo = part < 4 ? s : other;
+    sum_hi = part < 4 ? other : s;
+    const int total = s + other;
+    d16 = f2h_rne(d);
+    s16 = f2h_rne((float)total * d);
+    d_dec = h2f(d16);
+    return (uint32_t)(q0 & 255) | ((uint32_t)(q1 & 255) << 8) | ((uint32_t)(q2 & 255) << 16) |
+           ((uint32_t)(q3 & 255) << 24);
+}
+
+// Stage an fp32 activation of K values (K % 256 == 0) into LDS as q8_1.
+// Block-wide; the caller synchronises afterwards.
+__device__ __forceinline__ void act_stage_from_f32(const float *__restrict__ x, uint32_t K, Act a) {
+    const uint32_t n = K / 32 * 8;   // 8 lanes per block
+    for (uint32_t t = threadIdx.x; t < n; t += blockDim.x) {
+        const uint32_t blk = t >> 3, part = t & 7;
+        const float4 v = *(const float4 *)(x + 32 * blk + 4 * part);
+        uint32_t d16, s16;
+        int lo, hi;
+        float dd;
+        const uint32_t q = quant_q8_1_part(v, d16, s16, lo, hi, dd);
+        *(uint32_t *)(a.qs + 32 * blk + 4 * part) = q;
+        if (part == 0) {
+            a.d8[blk] = dd;
+            a.qs16[2 * blk] = lo;
+            a.qs16[2 * blk + 1] = hi;
+        }
+    }
+}
+
+// Stage K values of global q8_1 blocks into LDS.
+__device__ __forceinline__ void act_stage_from_q8(const uint8_t *__restrict__ xq, uint32_t K, Act a) {
+    const uint32_t n = K / 32 * 8;
+    for (uint32_t t = threadIdx.x; t < n; t += blockDim.x) {
+        const uint32_t blk = t >> 3, part = t & 7;
+        const uint8_t *b = xq + 36 * blk;
+        const uint32_t q = *(const uint32_t *)(b + 4 + 4 * part);
+        *(uint32_t *)(a.qs + 32 * blk + 4 * part) = q;
+        int s = dot4(q, 0x01010101u, 0);
+        s += __shfl_xor(s, 1, WAVE);
+        s += __shfl_xor(s, 2, WAVE);
+        const int other = __shfl_xor(s, 4, WAVE);
+        if (part == 0) {
+            a.d8[blk] = h2f(ld_u16(b));
+            a.qs16[2 * blk] = s;
+            a.qs16[2 * blk + 1] = other;
+        }
+    }
+}
+
+// fp32 activation in LDS for the float-activation GEMV: x[K] plus exact-order
+// sums of every 16 values (xsum16[K/16], left to right).
+struct ActF {
+    float *x;
+    float *xs16;
+};
+__host__ __device__ constexpr uint32_t actf_bytes(uint32_t K) { return K * 4 + K / 4; }
+__device__ __forceinline__ ActF actf_carve(uint8_t *base, uint32_t K) {
+    ActF a;
+    a.x = (float *)base;
+    a.xs16 = (float *)(base + 4 * K);
+    return a;
+}
+__device__ __forceinline__ void actf_stage(const float *__restrict__ x, uint32_t K, ActF a) {
+    for (uint32_t t = threadIdx.x; t < K / 4; t += blockDim.x)
+        *(float4 *)(a.x + 4 * t) = *(const float4 *)(x + 4 * t);
+    __syncthreads();
+    for (uint32_t t = threadIdx.x; t < K / 16; t += blockDim.x) {
+        float s = 0.0f;
+        for (int i = 0; i < 16; i++) s += a.x[16 * t + i];
+        a.xs16[t] = s;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Q4_K item: lane chunk c (0..7) of a block = 16 bytes of nibbles
+//   group g = c/2, half hh = c%2: low nibbles -> values 64g+16hh+i (sub-block
+//   2g), high nibbles -> 64g+32+16hh+i (sub-block 2g+1), i = 0..15.
+// ---------------------------------------------------------------------------
+struct Q4K {
+    static constexpr uint32_t TYPE = T_Q4_K;
+    static constexpr int IPB = 8;          // items per block
+    static constexpr uint32_t BB = 144;    // block bytes
+    struct Raw {
+        uint4 h, q;
+    };
+    __device__ static __forceinline__ Raw load(const uint8_t *blk, int c) {
+        Raw r;
+        r.h = ld16(blk);
+        r.q = ld16(blk + 16 + 16 * c);
+        return r;
+    }
+    // exact partial sums over the lane's 16 low / 16 high values
+    __device__ static __forceinline__ void isums(const Raw &r, int c, const int8_t *actb, int &slo, int &shi) {
+        const int g = c >> 1, hh = c & 1;
+        const int8_t *al = actb + 64 * g + 16 * hh;
+        const int4 xl = *(const int4 *)al;
+        const int4 xh = *(const int4 *)(al + 32);
+        const uint32_t m = 0x0F0F0F0Fu;
+        slo = dot4(r.q.x & m, xl.x, 0);
+        slo = dot4(r.q.y & m, xl.y, slo);
+        slo = dot4(r.q.z & m, xl.z, slo);
+        slo = dot4(r.q.w & m, xl.w, slo);
+        shi = dot4((r.q.x >> 4) & m, xh.x, 0);
+        shi = dot4((r.q.y >> 4) & m, xh.y, shi);
+        shi = dot4((r.q.z >> 4) & m, xh.z, shi);
+        shi = dot4((r.q.w >> 4) & m, xh.w, shi);
+    }
+    // scale/min pairs for sub-blocks 2g and 2g+1 (get_scale_min_k4, two at once)
+    __device__ static __forceinline__ void scales(const Raw &r, int g, float &ds0, float &ds1, float &dm0,
+                                                  float &dm1) {
+        const uint32_t sh = 16u * (uint32_t)(g & 1);
+        const uint32_t p1 = r.h.y >> sh, p2 = r.h.z >> sh, p3 = r.h.w >> sh;
+        uint32_t sc, mn;
+        if (g < 2) {
+            sc = p1 & 0x3F3Fu;
+            mn = p2 & 0x3F3Fu;
+        } else {
+            sc = (p3 & 0x0F0Fu) | ((p1 >> 2) & 0x3030u);
+            mn = ((p3 >> 4) & 0x0F0Fu) | ((p2 >> 2) & 0x3030u);
+        }
+        const float d = h2f(r.h.x & 0xFFFFu), dmin = h2f(r.h.x >> 16);
+        ds0 = d * (float)(sc & 0xFFu);
+        ds1 = d * (float)((sc >> 8) & 0xFFu);
+        dm0 = dmin * (float)(mn & 0xFFu);
+        dm1 = dmin * (float)((mn >> 8) & 0xFFu);
+    }
+    // fp32 contribution of the item against a q8_1 activation (block b)
+    __device__ static __forceinline__ float dot_q8(const Raw &r, int c, const Act &a, uint32_t b) {
+        int slo, shi;
+        isums(r, c, a.qs + 256 * b, slo, shi);
+        const int g = c >> 1, hh = c & 1;
+        float ds0, ds1, dm0, dm1;
+        scales(r, g, ds0, ds1, dm0, dm1);
+        const uint32_t k = 8 * b + 2 * g;   // q8 block of the low nibbles
+        const float vlo = fmaf(ds0, (float)slo, -(dm0 * (float)a.qs16[2 * k + hh]));
+        const float vhi = fmaf(ds1, (float)shi, -(dm1 * (float)a.qs16[2 * k + 2 + hh]));
+        return fmaf(a.d8[k], vlo, a.d8[k + 1] * vhi);
+    }
+    // fp32 contribution of the item against a float activation (block b)
+    __device__ static __forceinline__ float dot_f32(const Raw &r, int c, const ActF &a, uint32_t b) {
+        const int g = c >> 1, hh = c & 1;
+        const float *xl = a.x + 256 * b + 64 * g + 16 * hh;
+        const float *xh = xl + 32;
+        const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+        float al = 0.0f, ah = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float4 vl = *(const float4 *)(xl + 4 * j);
+            const float4 vh = *(const float4 *)(xh + 4 * j);
+            const uint32_t lo = q[j] & 0x0F0F0F0Fu, hi = (q[j] >> 4) & 0x0F0F0F0Fu;
+            al = fmaf((float)(lo & 0xFFu), vl.x, al);
+            al = fmaf((float)((lo >> 8) & 0xFFu), vl.y, al);
+            al = fmaf((float)((lo >> 16) & 0xFFu), vl.z, al);
+            al = fmaf((float)(lo >> 24), vl.w, al);
+            ah = fmaf((float)(hi & 0xFFu), vh.x, ah);
+            ah = fmaf((float)((hi >> 8) & 0xFFu), vh.y, ah);
+            ah = fmaf((float)((hi >> 16) & 0xFFu), vh.z, ah);
+            ah = fmaf((float)(hi >> 24), vh.w, ah);
+        }
+        float ds0, ds1, dm0, dm1;
+        scales(r, g, ds0, ds1, dm0, dm1);
+        const float *s16 = a.xs16 + 16 * b + 4 * g + hh;
+        return fmaf(ds0, al, -(dm0 * s16[0])) + fmaf(ds1, ah, -(dm1 * s16[2]));
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Q6_K item: lane chunk c (0..3) of a block: half n = c/2, lane group k = c%2;
+// 48 bytes (ql[64n+16k..+15], ql[64n+32+16k..+15], qh[32n+16k..+15]) give
+// 4 x 16 values t = 0..3 at 128n + 32t + 16k + i with scale sc[8n+2t+k].
+// ---------------------------------------------------------------------------
+struct Q6K {
+    static constexpr uint32_t TYPE = T_Q6_K;
+    static constexpr int IPB = 4;
+    static constexpr uint32_t BB = 210;
+    struct Raw {
+        uint4 A, B, H;
+        uint2 sc;
+        uint32_t d;
+    };
+    __device__ static __forceinline__ Raw load(const uint8_t *blk, int c) {
+        const int n = c >> 1, k = c & 1;
+        Raw r;
+        r.A = ld16(blk + 64 * n + 16 * k);
+        r.B = ld16(blk + 64 * n + 32 + 16 * k);
+        r.H = ld16(blk + 128 + 32 * n + 16 * k);
+        r.sc = ld8(blk + 192 + 8 * n);
+        r.d = ld_u16(blk + 208);
+        return r;
+    }
+    // 6-bit values of quarter t for dword j (4 values), unsigned 0..63
+    __device__ static __forceinline__ uint32_t q6(uint32_t A, uint32_t B, uint32_t H, int t) {
+        const uint32_t m4 = 0x0F0F0F0Fu, m2 = 0x30303030u;
+        switch (t) {
+            case 0: return (A & m4) | ((H << 4) & m2);
+            case 1: return (B & m4) | ((H << 2) & m2);
+            case 2: return ((A >> 4) & m4) | (H & m2);
+            default: return ((B >> 4) & m4) | ((H >> 2) & m2);
+        }
+    }
+    // exact sums of (q6 - 32) * q8 for the four 16-value groups of the item
+    __device__ static __forceinline__ void isums(const Raw &r, int c, const Act &a, uint32_t b, int s[4]) {
+        const int n = c >> 1, k = c & 1;
+        const uint32_t A[4] = {r.A.x, r.A.y, r.A.z, r.A.w};
+        const uint32_t B[4] = {r.B.x, r.B.y, r.B.z, r.B.w};
+        const uint32_t H[4] = {r.H.x, r.H.y, r.H.z, r.H.w};
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const uint32_t e0 = 256 * b + 128 * n + 32 * t + 16 * k;
+            const int4 x = *(const int4 *)(a.qs + e0);
+            int acc = dot4(q6(A[0], B[0], H[0], t), x.x, 0);
+            acc = dot4(q6(A[1], B[1], H[1], t), x.y, acc);
+            acc = dot4(q6(A[2], B[2], H[2], t), x.z, acc);
+            acc = dot4(q6(A[3], B[3], H[3], t), x.w, acc);
+            s[t] = acc - 32 * a.qs16[e0 / 16];
+        }
+    }
+    __device__ static __forceinline__ float scale(const Raw &r, int k, int t) {
+        const uint32_t w = (t < 2) ? r.sc.x : r.sc.y;
+        const int sh = 8 * (2 * (t & 1) + k);
+        return (float)(int)(int8_t)(w >> sh);
+    }
+    __device__ static __forceinline__ float dot_q8(const Raw &r, int c, const Act &a, uint32_t b) {
+        int s[4];
+        isums(r, c, a, b, s);
+        const int n = c >> 1, k = c & 1;
+        const float d = h2f(r.d);
+        const uint32_t k8 = 8 * b + 4 * n;   // q8 block of quarter 0
+        float acc = a.d8[k8] * ((d * scale(r, k, 0)) * (float)s[0]);
+#pragma unroll
+        for (int t = 1; t < 4; t++) acc = fmaf(a.d8[k8 + t], (d * scale(r, k, t)) * (float)s[t], acc);
+        return acc;
+    }
+    __device__ static __forceinline__ float dot_f32(const Raw &r, int c, const ActF &a, uint32_t b) {
+        const int n = c >> 1, k = c & 1;
+        const uint32_t A[4] = {r.A.x, r.A.y, r.A.z, r.A.w};
+        const uint32_t B[4] = {r.B.x, r.B.y, r.B.z, r.B.w};
+        const uint32_t H[4] = {r.H.x, r.H.y, r.H.z, r.H.w};
+        const float d = h2f(r.d);
+        float acc = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const uint32_t e0 = 256 * b + 128 * n + 32 * t + 16 * k;
+            float s = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t v = q6(A[j], B[j], H[j], t);
+                const float4 x = *(const float4 *)(a.x + e0 + 4 * j);
+                s = fmaf((float)(v & 0xFFu), x.x, s);
+                s = fmaf((float)((v >> 8) & 0xFFu), x.y, s);
+                s = fmaf((float)((v >> 16) & 0xFFu), x.z, s);
+                s = fmaf((float)(v >> 24), x.w, s);
+            }
+            s = fmaf(-32.0f, a.xs16[e0 / 16], s);
+            acc = fmaf(d * scale(r, k, t), s, acc);
+        }
+        return acc;
+    }
+};
+
+}  // namespace kq

@@ -1,0 +1,348 @@
+// kq_gemv.hip — q8_1 quantization, dense Q4_K / Q6_K GEMV (fp32 and q8_1
+// activations), per-block integer sums, synthetic data and a copy kernel.
+//
+// GEMV layout: a row is nb = cols/256 super-blocks = nb*IPB lane items. S lanes
+// (a power of two dividing the item count, at most 64) share a row and each
+// takes IPL = items/S items (item = s + S*i, so a wave instruction walks
+// consecutive items of a row). A wave holds 64/S rows at a time, a 256-thread
+// workgroup 4x that, and each slot issues the loads of RPS rows before it
+// computes any of them. The activation is staged once per workgroup in LDS.
+#include "kq_device.h"
+#include "kq_launch.h"
+
+namespace kq {
+
+int device_cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+__global__ void __launch_bounds__(256) k_quantize_q8_1(const float *__restrict__ x, uint32_t nblk,
+                                                        uint8_t *__restrict__ out) {
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nblk * 8) return;   // whole 8-lane groups exit together
+    const uint32_t blk = t >> 3, part = t & 7;
+    const float4 v = *(const float4 *)(x + 32 * blk + 4 * part);
+    uint32_t d16, s16;
+    int lo, hi;
+    float dd;
+    const uint32_t q = quant_q8_1_part(v, d16, s16, lo, hi, dd);
+    uint8_t *b = out + 36 * blk;
+    *(uint32_t *)(b + 4 + 4 * part) = q;
+    if (part == 0) *(uint32_t *)b = d16 | (s16 << 16);
+}
+
+hipError_t launch_quantize_q8_1(const float *x, uint64_t n, uint8_t *out, hipStream_t s) {
+    const uint32_t nblk = (uint32_t)(n / 32);
+    const uint32_t threads = nblk * 8;
+    hipLaunchKernelGGL(k_quantize_q8_1, dim3((threads + 255) / 256), dim3(256), 0, s, x, nblk, out);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// GEMV
+// ---------------------------------------------------------------------------
+template <class QT, int IPL_T, int RPS, int MODE>
+__global__ void __launch_bounds__(256)
+    k_gemv(const uint8_t *__restrict__ w, uint32_t rows, uint32_t cols, uint64_t rb, uint32_t log2s,
+           const float *__restrict__ xf, const uint8_t *__restrict__ xq, float *__restrict__ y) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const Act a = act_carve(lds, cols);
+    const ActF af = actf_carve(lds, cols);
+    if constexpr (MODE == 0) actf_stage(xf, cols, af);
+    else if constexpr (MODE == 1) act_stage_from_q8(xq, cols, a);
+    else act_stage_from_f32(xf, cols, a);
+    __syncthreads();
+
+    const uint32_t S = 1u << log2s;
+    const uint32_t slots = WAVE >> log2s;
+    const uint32_t lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    const uint32_t slot = lane >> log2s, s = lane & (S - 1);
+    const uint32_t items = cols / 256 * QT::IPB;
+    const int IPL = IPL_T > 0 ? IPL_T : (int)(items >> log2s);
+    const uint32_t rows_iter = 4 * slots * RPS;
+
+    for (uint32_t base = blockIdx.x * rows_iter; base < rows; base += gridDim.x * rows_iter) {
+        float acc[RPS];
+        if constexpr (IPL_T > 0) {
+            typename QT::Raw raw[RPS][IPL_T];
+#pragma unroll
+            for (int r = 0; r < RPS; r++) {
+                const uint32_t row = base + r * (4 * slots) + wave * slots + slot;
+                if (row < rows) {
+                    const uint8_t *rp = w + (uint64_t)row * rb;
+#pragma unroll
+                    for (int i = 0; i < IPL_T; i++) {
+                        const uint32_t item = s + S * i;
+                        raw[r][i] = QT::load(rp + (item / QT::IPB) * QT::BB, item % QT::IPB);
+                    }
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < RPS; r++) {
+                const uint32_t row = base + r * (4 * slots) + wave * slots + slot;
+                float v = 0.0f;
+                if (row < rows) {
+#pragma unroll
+                    for (int i = 0; i < IPL_T; i++) {
+                        const uint32_t item = s + S * i;
+                        if constexpr (MODE == 0) v += QT::dot_f32(raw[r][i], item % QT::IPB, af, item / QT::IPB);
+                        else v += QT::dot_q8(raw[r][i], item % QT::IPB, a, item / QT::IPB);
+                    }
+                }
+                acc[r] = v;
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < RPS; r++) {
+                const uint32_t row = base + r * (4 * slots) + wave * slots + slot;
+                float v = 0.0f;
+                if (row < rows) {
+                    const uint8_t *rp = w + (uint64_t)row * rb;
+                    for (int i = 0; i < IPL; i++) {
+                        const uint32_t item = s + S * i;
+                        const typename QT::Raw raw = QT::load(rp + (item / QT::IPB) * QT::BB, item % QT::IPB);
+                        if constexpr (MODE == 0) v += QT::dot_f32(raw, item % QT::IPB, af, item / QT::IPB);
+                        else v += QT::dot_q8(raw, item % QT::IPB, a, item / QT::IPB);
+                    }
+                }
+                acc[r] = v;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RPS; r++) {
+            const float v = wave_sum_xor(acc[r], (int)S);
+            const uint32_t row = base + r * (4 * slots) + wave * slots + slot;
+            if (s == 0 && row < rows) y[row] = v;
+        }
+    }
+}
+
+static int ilog2(uint32_t v) {
+    int l = 0;
+    while ((1u << (l + 1)) <= v) l++;
+    return l;
+}
+
+// S = largest power of two <= 64 dividing the item count.
+static uint32_t lanes_per_row(uint32_t items) {
+    uint32_t s = 64;
+    while (s > 1 && items % s) s >>= 1;
+    return s;
+}
+
+template <class QT, int MODE>
+static hipError_t gemv_dispatch(const uint8_t *w, uint64_t rows, uint64_t cols, const float *xf, const uint8_t *xq,
+                                float *y, hipStream_t st) {
+    const uint32_t items = (uint32_t)(cols / 256) * QT::IPB;
+    const uint32_t S = lanes_per_row(items);
+    const uint32_t ipl = items / S;
+    const uint64_t rb = cols / 256 * QT::BB;
+    const uint32_t lds = MODE == 0 ? actf_bytes((uint32_t)cols) : act_bytes((uint32_t)cols);
+    const int cus = device_cu_count();
+    const uint32_t slots = 64 / S;
+    auto go = [&](auto kern, int rps) -> hipError_t {
+        const uint64_t rows_iter = 4ull * slots * rps;
+        uint64_t iters = (rows + rows_iter - 1) / rows_iter;
+        const uint64_t cap = 8ull * cus;
+        const uint32_t grid = (uint32_t)(iters < cap ? iters : cap);
+        if (lds > 64 * 1024) {
+            hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+        }
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, st, w, (uint32_t)rows, (uint32_t)cols, rb,
+                           (uint32_t)ilog2(S), xf, xq, y);
+        return hipGetLastError();
+    };
+    constexpr bool Q4 = QT::TYPE == T_Q4_K;
+    switch (ipl) {
+        case 1: return Q4 ? go(k_gemv<QT, 1, 4, MODE>, 4) : go(k_gemv<QT, 1, 2, MODE>, 2);
+        case 2: return Q4 ? go(k_gemv<QT, 2, 2, MODE>, 2) : go(k_gemv<QT, 2, 1, MODE>, 1);
+        case 3: return go(k_gemv<QT, 3, 1, MODE>, 1);
+        default: return go(k_gemv<QT, 0, 1, MODE>, 1);
+    }
+}
+
+hipError_t launch_gemv(uint32_t type, const uint8_t *w, uint64_t rows, uint64_t cols, const float *xf,
+                       const uint8_t *xq, float *y, int mode, hipStream_t s) {
+    if (type == T_Q4_K) {
+        if (mode == 0) return gemv_dispatch<Q4K, 0>(w, rows, cols, xf, xq, y, s);
+        if (mode == 1) return gemv_dispatch<Q4K, 1>(w, rows, cols, xf, xq, y, s);
+        return gemv_dispatch<Q4K, 2>(w, rows, cols, xf, xq, y, s);
+    }
+    if (mode == 0) return gemv_dispatch<Q6K, 0>(w, rows, cols, xf, xq, y, s);
+    if (mode == 1) return gemv_dispatch<Q6K, 1>(w, rows, cols, xf, xq, y, s);
+    return gemv_dispatch<Q6K, 2>(w, rows, cols, xf, xq, y, s);
+}
+
+// ---------------------------------------------------------------------------
+// Per-block integer sums through the same item routines the GEMV uses.
+// One thread per (row, block, item pair) for Q4_K (two half-items summed), one
+// per (row, block, item) for Q6_K.
+// ---------------------------------------------------------------------------
+template <class QT>
+__global__ void __launch_bounds__(256) k_isums(const uint8_t *__restrict__ w, uint32_t rows, uint32_t cols,
+                                               const uint8_t *__restrict__ xq, int32_t *__restrict__ out) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    Act a = act_carve(lds, cols);
+    act_stage_from_q8(xq, cols, a);
+    __syncthreads();
+    const uint32_t nb = cols / 256;
+    const uint64_t rb = (uint64_t)nb * QT::BB;
+    constexpr uint32_t per_blk = QT::TYPE == T_Q4_K ? 4 : 4;   // threads per block
+    const uint64_t total = (uint64_t)rows * nb * per_blk;
+    for (uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t c = (uint32_t)(t % per_blk);
+        const uint64_t rbk = t / per_blk;
+        const uint32_t b = (uint32_t)(rbk % nb);
+        const uint64_t row = rbk / nb;
+        const uint8_t *blk = w + row * rb + (uint64_t)b * QT::BB;
+        if constexpr (QT::TYPE == T_Q4_K) {
+            // group g = c: items 2g (hh=0) and 2g+1 (hh=1) cover sub-blocks 2g, 2g+1
+            int l0, h0, l1, h1;
+            Q4K::isums(Q4K::load(blk, 2 * c), 2 * c, a.qs + 256 * b, l0, h0);
+            Q4K::isums(Q4K::load(blk, 2 * c + 1), 2 * c + 1, a.qs + 256 * b, l1, h1);
+            int32_t *o = out + row * (cols / 32) + 8 * b + 2 * c;
+            o[0] = l0 + l1;
+            o[1] = h0 + h1;
+        } else {
+            int s4[4];
+            Q6K::isums(Q6K::load(blk, c), c, a, b, s4);
+            const int n = c >> 1, k = c & 1;
+            int32_t *o = out + row * (cols / 16) + 16 * b + 8 * n + k;
+            for (int tq = 0; tq < 4; tq++) o[2 * tq] = s4[tq];
+        }
+    }
+}
+
+hipError_t launch_isums(uint32_t type, const uint8_t *w, uint64_t rows, uint64_t cols, const uint8_t *xq,
+                        int32_t *out, hipStream_t s) {
+    const uint64_t total = rows * (cols / 256) * 4;
+    uint64_t grid = (total + 255) / 256;
+    if (grid > 4096) grid = 4096;
+    const uint32_t lds = act_bytes((uint32_t)cols);
+    if (type == T_Q4_K)
+        hipLaunchKernelGGL(k_isums<Q4K>, dim3((uint32_t)grid), dim3(256), lds, s, w, (uint32_t)rows, (uint32_t)cols,
+                           xq, out);
+    else
+        hipLaunchKernelGGL(k_isums<Q6K>, dim3((uint32_t)grid), dim3(256), lds, s, w, (uint32_t)rows, (uint32_t)cols,
+                           xq, out);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Synthetic data: counter-based splitmix64 stream, one 64-bit draw per 8 bytes.
+// Scale fields get |N(0, sigma)| (Box-Muller) encoded as f16.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+__device__ __forceinline__ float u01(uint64_t r) { return ((float)(r >> 40) + 0.5f) * (1.0f / 16777216.0f); }
+__device__ __forceinline__ float halfnormal(uint64_t key, float sigma) {
+    const uint64_t r = splitmix64(key);
+    const float u1 = u01(r), u2 = u01(splitmix64(r ^ 0x5DEECE66Dull));
+    return fabsf(sigma * sqrtf(-2.0f * logf(u1)) * cosf(6.28318530718f * u2));
+}
+
+__global__ void __launch_bounds__(256) k_synth_blocks(uint32_t type, uint8_t *__restrict__ dst, uint64_t nblocks,
+                                                      uint64_t seed, float sigma) {
+    const uint32_t bb = type == T_Q4_K ? 144 : 210;
+    const uint64_t total = nblocks * bb;
+    const uint64_t nwords = (total + 7) / 8;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nwords; i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t r = splitmix64(seed * 0x2545F4914F6CDD1Dull + i);
+        const uint64_t off = i * 8;
+        if (off + 8 <= total && (off & 7) == 0 && ((uintptr_t)dst & 7) == 0) {
+            *(uint64_t *)(dst + off) = r;
+        } else {
+            for (int k = 0; k < 8 && off + k < total; k++) dst[off + k] = (uint8_t)(r >> (8 * k));
+        }
+    }
+}
+
+__global__ void __launch_bounds__(256) k_synth_scales(uint32_t type, uint8_t *__restrict__ dst, uint64_t nblocks,
+                                                      uint64_t seed, float sigma) {
+    for (uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nblocks; b += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t key = (seed ^ 0xA0761D6478BD642Full) * 0x9E3779B97F4A7C15ull + 2 * b;
+        if (type == T_Q4_K) {
+            uint8_t *blk = dst + b * 144;
+            const uint32_t d = f2h_rne(halfnormal(key, sigma)), m = f2h_rne(halfnormal(key + 1, sigma));
+            blk[0] = (uint8_t)d; blk[1] = (uint8_t)(d >> 8);
+            blk[2] = (uint8_t)m; blk[3] = (uint8_t)(m >> 8);
+        } else {
+            uint8_t *blk = dst + b * 210;
+            const uint32_t d = f2h_rne(halfnormal(key, sigma));
+            blk[208] = (uint8_t)d; blk[209] = (uint8_t)(d >> 8);
+        }
+    }
+}
+
+hipError_t launch_synth_blocks(uint32_t type, uint8_t *dst, uint64_t nblocks, uint64_t seed, float sigma,
+                               hipStream_t s) {
+    const uint32_t bb = type == T_Q4_K ? 144 : 210;
+    const uint64_t nwords = (nblocks * bb + 7) / 8;
+    uint64_t grid = (nwords + 255) / 256;
+    if (grid > 16384) grid = 16384;
+    hipLaunchKernelGGL(k_synth_blocks, dim3((uint32_t)grid), dim3(256), 0, s, type, dst, nblocks, seed, sigma);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    uint64_t g2 = (nblocks + 255) / 256;
+    if (g2 > 16384) g2 = 16384;
+    hipLaunchKernelGGL(k_synth_scales, dim3((uint32_t)g2), dim3(256), 0, s, type, dst, nblocks, seed, sigma);
+    return hipGetLastError();
+}
+
+__global__ void __launch_bounds__(256) k_synth_normal(float *__restrict__ dst, uint64_t n, uint64_t seed, float sigma) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t r = splitmix64(seed * 0xD1B54A32D192ED03ull + i);
+        const float u1 = u01(r), u2 = u01(splitmix64(r ^ 0x5DEECE66Dull));
+        dst[i] = sigma * sqrtf(-2.0f * logf(u1)) * cosf(6.28318530718f * u2);
+    }
+}
+
+hipError_t launch_synth_normal(float *dst, uint64_t n, uint64_t seed, float sigma, hipStream_t s) {
+    uint64_t grid = (n + 255) / 256;
+    if (grid > 16384) grid = 16384;
+    hipLaunchKernelGGL(k_synth_normal, dim3((uint32_t)grid), dim3(256), 0, s, dst, n, seed, sigma);
+    return hipGetLastError();
+}
+
+__global__ void k_step_advance(int32_t *step, int32_t n) {
+    if (threadIdx.x == 0) {
+        const int32_t v = *step + 1;
+        *step = v >= n ? 0 : v;
+    }
+}
+
+hipError_t launch_step_advance(int32_t *step, int32_t n_steps, hipStream_t s) {
+    hipLaunchKernelGGL(k_step_advance, dim3(1), dim3(64), 0, s, step, n_steps);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Streaming copy, 16 B per lane per step (n % 16 == 0).
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) k_copy(const uint4 *__restrict__ src, uint4 *__restrict__ dst, uint64_t n16) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (uint64_t)gridDim.x * blockDim.x)
+        dst[i] = src[i];
+}
+
+hipError_t launch_copy(const uint8_t *src, uint8_t *dst, uint64_t n, hipStream_t s) {
+    const uint64_t n16 = n / 16;
+    uint64_t grid = (n16 + 255) / 256;
+    if (grid > 8192) grid = 8192;
+    hipLaunchKernelGGL(k_copy, dim3((uint32_t)grid), dim3(256), 0, s, (const uint4 *)src, (uint4 *)dst, n16);
+    return hipGetLastError();
+}
+
+}  // namespace kq

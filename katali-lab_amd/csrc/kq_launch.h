@@ -1,0 +1,68 @@
+// kq_launch.h — host-side launchers shared by the HIP translation units and the
+// C-ABI layer (katali_hip.cpp). All launchers enqueue on `stream` and return a
+// hipError_t; argument validation happens in the ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kq {
+
+// Compute units of the current device (cached per device; 256 if unknown).
+int device_cu_count();
+
+// q8_1 quantization of n fp32 values (n % 32 == 0) into 36-byte blocks.
+hipError_t launch_quantize_q8_1(const float *x, uint64_t n, uint8_t *out, hipStream_t s);
+
+// Dense GEMV y[rows] = W[rows x cols] . x.
+//  mode 0: fp32 activation (dequantize-and-FMA path)
+//  mode 1: q8_1 activation given as 36-byte blocks (xq)
+//  mode 2: fp32 activation quantized to q8_1 inside every workgroup
+hipError_t launch_gemv(uint32_t type, const uint8_t *w, uint64_t rows, uint64_t cols, const float *xf,
+                       const uint8_t *xq, float *y, int mode, hipStream_t s);
+
+// Per-block exact integer sums of a GEMV against a q8_1 activation:
+// Q4_K -> out[rows][cols/32], Q6_K -> out[rows][cols/16].
+hipError_t launch_isums(uint32_t type, const uint8_t *w, uint64_t rows, uint64_t cols, const uint8_t *xq,
+                        int32_t *out, hipStream_t s);
+
+// Synthetic data (bench and harness inputs).
+hipError_t launch_synth_blocks(uint32_t type, uint8_t *dst, uint64_t nblocks, uint64_t seed, float d_sigma,
+                               hipStream_t s);
+hipError_t launch_synth_normal(float *dst, uint64_t n, uint64_t seed, float sigma, hipStream_t s);
+
+// *step = (*step + 1) % n_steps
+hipError_t launch_step_advance(int32_t *step, int32_t n_steps, hipStream_t s);
+
+// Plain streaming copy (HBM counter calibration).
+hipError_t launch_copy(const uint8_t *src, uint8_t *dst, uint64_t n, hipStream_t s);
+
+// Fused MoE layer. Types: gate/up in {Q4_K, Q6_K}, down in {Q4_K, Q6_K}.
+struct MoeArgs {
+    const uint8_t *gate, *up, *down;          // stacked [n_expert][rows][row_bytes]
+    const uint8_t *gate_sh, *up_sh, *down_sh; // shared expert (NULL when absent)
+    uint32_t gate_type, up_type, down_type;
+    uint32_t hidden, ffn, n_expert;
+    int n_sel;                                // routed experts per token
+    int has_shared;
+    const float *x;          // fp32 activation [hidden] (or NULL)
+    const uint8_t *xq;       // q8_1 activation (or NULL)
+    const float *logits;     // router logits [n_expert] (or NULL: ids/wts given)
+    const int32_t *step;     // optional: logits += (*step) * logits_stride
+    uint64_t logits_stride;
+    const int32_t *ids;      // selected experts [n_sel] (when logits == NULL)
+    const float *wts;        // their weights [n_sel]
+    int32_t *ids_out;        // optional routing output
+    float *wts_out;
+    float *y;                // [hidden]
+    uint8_t *hq8;            // scratch [n_slots][ffn/32][36]
+    uint32_t *sync;          // scratch counters (zero at rest)
+    float *dbg_gu;           // optional [n_slots][2][ffn] gate/up outputs
+    int32_t *err;            // error word (non-zero on timeout)
+};
+// mode 0: two launches (gate/up+SiLU+quantize, then down+reduction)
+// mode 1: one launch with an in-kernel dependency wait
+hipError_t launch_moe(const MoeArgs &a, int mode, hipStream_t s, int *grid_out);
+uint64_t moe_sync_words();
+
+}  // namespace kq

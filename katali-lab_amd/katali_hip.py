@@ -1,0 +1,255 @@
+"""ctypes binding of libkatali_hip (include/katali_hip.h) for Python callers.
+
+This is the binding a Python maintainer would add for the library, and what
+the tests and bench.py drive. It loads the in-tree build (or KATALI_HIP_DLL)
+and raises if the library is missing: there is no CPU fallback here.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+DEFAULT_SO = os.path.join(PKG, "libkatali_hip.so")
+
+Q4_K, Q6_K = 12, 14
+BLOCK_BYTES = {Q4_K: 144, Q6_K: 210}
+
+_vp, _u64, _u32, _i32, _i64, _f32, _sz = (C.c_void_p, C.c_uint64, C.c_uint32, C.c_int32, C.c_int64,
+                                          C.c_float, C.c_size_t)
+
+# Every exported symbol with (restype, argtypes); include/katali_hip.h is the
+# source of truth and tests check the two agree.
+SIGNATURES = {
+    "katali_hip_abi_version": (C.c_int, []),
+    "katali_hip_last_error": (C.c_char_p, []),
+    "katali_hip_probe": (C.c_int, []),
+    "katali_hip_status": (C.c_char_p, []),
+    "katali_hip_malloc": (C.c_int, [C.POINTER(_vp), _sz]),
+    "katali_hip_free": (C.c_int, [_vp]),
+    "katali_hip_upload": (C.c_int, [_vp, _vp, _sz]),
+    "katali_hip_download": (C.c_int, [_vp, _vp, _sz]),
+    "katali_hip_supports_type": (C.c_int, [_u32]),
+    "katali_hip_matvec": (C.c_int, [_u32, _vp, _u64, _u64, _vp, _vp]),
+    "katali_hip_sync": (C.c_int, []),
+    "katali_hip_memset": (C.c_int, [_vp, C.c_int, _sz]),
+    "katali_hip_set_stream": (C.c_int, [_vp]),
+    "katali_hip_quantize_q8_1": (C.c_int, [_vp, _u64, _vp]),
+    "katali_hip_matvec_q8": (C.c_int, [_u32, _vp, _u64, _u64, _vp, _vp]),
+    "katali_hip_matvec_dp4a": (C.c_int, [_u32, _vp, _u64, _u64, _vp, _vp]),
+    "katali_hip_block_isums": (C.c_int, [_u32, _vp, _u64, _u64, _vp, _vp]),
+    "katali_hip_moe_layer": (C.c_int, [_vp, _vp, _vp, _vp, _vp]),
+    "katali_hip_moe_layer_debug": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "katali_hip_step_advance": (C.c_int, [_vp, _i32]),
+    "katali_hip_graph_begin": (C.c_int, []),
+    "katali_hip_graph_end": (C.c_int, [C.POINTER(_vp)]),
+    "katali_hip_graph_launch": (C.c_int, [_vp]),
+    "katali_hip_graph_destroy": (C.c_int, [_vp]),
+    "katali_hip_event_create": (C.c_int, [C.POINTER(_vp)]),
+    "katali_hip_event_record": (C.c_int, [_vp]),
+    "katali_hip_event_elapsed": (C.c_int, [_vp, _vp, C.POINTER(_f32)]),
+    "katali_hip_event_destroy": (C.c_int, [_vp]),
+    "katali_hip_set_option": (C.c_int, [C.c_char_p, _i64]),
+    "katali_hip_get_option": (_i64, [C.c_char_p]),
+    "katali_hip_selftest": (C.c_int, [C.c_char_p, _sz]),
+    "katali_hip_synth_fill": (C.c_int, [_u32, _vp, _u64, _u64, _f32]),
+    "katali_hip_synth_normal": (C.c_int, [_vp, _u64, _u64, _f32]),
+    "katali_hip_copy": (C.c_int, [_vp, _vp, _sz]),
+}
+
+
+class KataliHipMoe(C.Structure):
+    _fields_ = [("struct_size", _u32), ("gate_type", _u32), ("up_type", _u32), ("down_type", _u32),
+                ("hidden", _u32), ("ffn", _u32), ("n_expert", _u32),
+                ("gate_exps", _vp), ("up_exps", _vp), ("down_exps", _vp),
+                ("gate_shexp", _vp), ("up_shexp", _vp), ("down_shexp", _vp)]
+
+
+class KataliHipMoeRoute(C.Structure):
+    _fields_ = [("struct_size", _u32), ("n_sel", _i32), ("logits", _vp), ("step", _vp),
+                ("logits_stride", _u64), ("ids", _vp), ("weights", _vp),
+                ("ids_out", _vp), ("weights_out", _vp)]
+
+
+class HipError(RuntimeError):
+    def __init__(self, rc: int, msg: str):
+        super().__init__(f"katali_hip error {rc}: {msg}")
+        self.rc = rc
+
+
+def library_path() -> str:
+    return os.environ.get("KATALI_HIP_DLL") or DEFAULT_SO
+
+
+def load_library(path: str | None = None) -> C.CDLL:
+    path = path or library_path()
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} not built: run `python katali-lab_amd/build.py` "
+                                "(there is no CPU fallback in this binding)")
+    lib = C.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+class DeviceBuffer:
+    """A device allocation from katali_hip_malloc."""
+
+    def __init__(self, hip: "KataliHip", nbytes: int):
+        self.hip, self.nbytes = hip, int(nbytes)
+        p = _vp()
+        hip.check(hip.lib.katali_hip_malloc(C.byref(p), self.nbytes))
+        self.ptr = p.value
+
+    def upload(self, arr: np.ndarray) -> "DeviceBuffer":
+        arr = np.ascontiguousarray(arr)
+        assert arr.nbytes <= self.nbytes, (arr.nbytes, self.nbytes)
+        self.hip.check(self.hip.lib.katali_hip_upload(self.ptr, arr.ctypes.data, arr.nbytes))
+        return self
+
+    def download(self, dtype, count: int | None = None, offset: int = 0) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        count = (self.nbytes - offset) // dtype.itemsize if count is None else count
+        out = np.empty(count, dtype)
+        self.hip.check(self.hip.lib.katali_hip_download(out.ctypes.data, self.ptr + offset, out.nbytes))
+        return out
+
+    def free(self):
+        if self.ptr:
+            self.hip.lib.katali_hip_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class KataliHip:
+    """Numpy front end over the C ABI."""
+
+    def __init__(self, path: str | None = None):
+        self.lib = load_library(path)
+
+    # -- plumbing ---------------------------------------------------------
+    def check(self, rc: int) -> None:
+        if rc != 0:
+            raise HipError(rc, self.lib.katali_hip_last_error().decode(errors="replace"))
+
+    def probe(self) -> bool:
+        return bool(self.lib.katali_hip_probe())
+
+    def status(self) -> str:
+        return self.lib.katali_hip_status().decode(errors="replace")
+
+    def alloc(self, nbytes: int) -> DeviceBuffer:
+        return DeviceBuffer(self, nbytes)
+
+    def to_device(self, arr: np.ndarray) -> DeviceBuffer:
+        arr = np.ascontiguousarray(arr)
+        return DeviceBuffer(self, max(arr.nbytes, 1)).upload(arr)
+
+    def sync(self) -> None:
+        self.check(self.lib.katali_hip_sync())
+
+    def set_option(self, name: str, value: int) -> None:
+        self.check(self.lib.katali_hip_set_option(name.encode(), int(value)))
+
+    def get_option(self, name: str) -> int:
+        return int(self.lib.katali_hip_get_option(name.encode()))
+
+    # -- compute ----------------------------------------------------------
+    def quantize_q8_1(self, x: DeviceBuffer, n: int, out: DeviceBuffer) -> None:
+        self.check(self.lib.katali_hip_quantize_q8_1(x.ptr, n, out.ptr))
+
+    def matvec(self, t, w, rows, cols, x, y) -> None:
+        self.check(self.lib.katali_hip_matvec(t, w.ptr, rows, cols, x.ptr, y.ptr))
+
+    def matvec_q8(self, t, w, rows, cols, xq, y) -> None:
+        self.check(self.lib.katali_hip_matvec_q8(t, w.ptr, rows, cols, xq.ptr, y.ptr))
+
+    def matvec_dp4a(self, t, w, rows, cols, x, y) -> None:
+        self.check(self.lib.katali_hip_matvec_dp4a(t, w.ptr, rows, cols, x.ptr, y.ptr))
+
+    def block_isums(self, t, w, rows, cols, xq, out) -> None:
+        self.check(self.lib.katali_hip_block_isums(t, w.ptr, rows, cols, xq.ptr, out.ptr))
+
+    @staticmethod
+    def moe_desc(hidden, ffn, n_expert, gate, up, down, gate_type=Q4_K, down_type=Q6_K,
+                 shared=None) -> KataliHipMoe:
+        d = KataliHipMoe(C.sizeof(KataliHipMoe), gate_type, gate_type, down_type, hidden, ffn, n_expert,
+                         gate.ptr, up.ptr, down.ptr, None, None, None)
+        if shared is not None:
+            d.gate_shexp, d.up_shexp, d.down_shexp = shared[0].ptr, shared[1].ptr, shared[2].ptr
+        return d
+
+    @staticmethod
+    def moe_route(n_sel, logits=None, ids=None, weights=None, step=None, logits_stride=0,
+                  ids_out=None, weights_out=None) -> KataliHipMoeRoute:
+        p = lambda b: None if b is None else b.ptr  # noqa: E731
+        return KataliHipMoeRoute(C.sizeof(KataliHipMoeRoute), n_sel, p(logits), p(step), logits_stride,
+                                 p(ids), p(weights), p(ids_out), p(weights_out))
+
+    def moe_layer(self, desc, route, y, x=None, xq=None) -> None:
+        self.check(self.lib.katali_hip_moe_layer(C.byref(desc), C.byref(route),
+                                                 None if x is None else x.ptr,
+                                                 None if xq is None else xq.ptr, y.ptr))
+
+    def moe_layer_debug(self, desc, route, y, gu, hq8, x=None, xq=None) -> None:
+        self.check(self.lib.katali_hip_moe_layer_debug(C.byref(desc), C.byref(route),
+                                                       None if x is None else x.ptr,
+                                                       None if xq is None else xq.ptr, y.ptr, gu.ptr, hq8.ptr))
+
+    def step_advance(self, step: DeviceBuffer, n_steps: int) -> None:
+        self.check(self.lib.katali_hip_step_advance(step.ptr, n_steps))
+
+    # -- graphs and timing ---------------------------------------------------
+    def graph_begin(self) -> None:
+        self.check(self.lib.katali_hip_graph_begin())
+
+    def graph_end(self) -> int:
+        g = _vp()
+        self.check(self.lib.katali_hip_graph_end(C.byref(g)))
+        return g.value
+
+    def graph_launch(self, g: int) -> None:
+        self.check(self.lib.katali_hip_graph_launch(g))
+
+    def graph_destroy(self, g: int) -> None:
+        self.check(self.lib.katali_hip_graph_destroy(g))
+
+    def event(self) -> int:
+        e = _vp()
+        self.check(self.lib.katali_hip_event_create(C.byref(e)))
+        return e.value
+
+    def record(self, e: int) -> None:
+        self.check(self.lib.katali_hip_event_record(e))
+
+    def elapsed_ms(self, a: int, b: int) -> float:
+        ms = _f32()
+        self.check(self.lib.katali_hip_event_elapsed(a, b, C.byref(ms)))
+        return float(ms.value)
+
+    def event_destroy(self, e: int) -> None:
+        self.check(self.lib.katali_hip_event_destroy(e))
+
+    # -- harness helpers ---------------------------------------------------------
+    def selftest(self) -> tuple[int, str]:
+        buf = C.create_string_buffer(4096)
+        rc = self.lib.katali_hip_selftest(buf, 4096)
+        return rc, buf.value.decode()
+
+    def synth_fill(self, t, buf: DeviceBuffer, nblocks: int, seed: int, d_sigma: float = 0.02) -> None:
+        self.check(self.lib.katali_hip_synth_fill(t, buf.ptr, nblocks, seed, d_sigma))
+
+    def synth_normal(self, buf: DeviceBuffer, n: int, seed: int, sigma: float = 1.0) -> None:
+        self.check(self.lib.katali_hip_synth_normal(buf.ptr, n, seed, sigma))
+
+    def copy(self, dst: DeviceBuffer, src: DeviceBuffer, nbytes: int) -> None:
+        self.check(self.lib.katali_hip_copy(dst.ptr, src.ptr, nbytes))

@@ -1,0 +1,80 @@
+"""The C-ABI library loads and exports exactly what include/katali_hip.h
+declares (CPU only: no compute calls)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+import katali_hip as K
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "katali_hip.h")
+
+
+def declared(header: str) -> set[str]:
+    src = open(header).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return set(re.findall(r"\b(katali_hip_\w+)\s*\(", src))
+
+
+def test_library_built():
+    assert os.path.exists(K.DEFAULT_SO), "run python katali-lab_amd/build.py"
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    names = declared(HEADER)
+    assert len(names) >= 30
+    lib = ctypes.CDLL(K.DEFAULT_SO)
+    missing = [n for n in sorted(names) if not hasattr(lib, n)]
+    assert not missing, missing
+    assert names == set(K.SIGNATURES), (names ^ set(K.SIGNATURES))
+    out = subprocess.run(["nm", "-D", "--defined-only", K.DEFAULT_SO], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\bT (katali_hip_\w+)", out))
+    assert exported == names, exported ^ names
+
+
+def test_loads_and_reports_status():
+    hip = K.KataliHip()
+    assert hip.lib.katali_hip_abi_version() == 1
+    ok = hip.probe()
+    status = hip.status()
+    assert status and status != "not probed"
+    if not ok:
+        # no GPU here: every entry point must refuse cleanly, not crash
+        rc = hip.lib.katali_hip_matvec(12, None, 1, 256, None, None)
+        assert rc == -2
+        assert "no usable device" in hip.lib.katali_hip_last_error().decode()
+        p = ctypes.c_void_p()
+        assert hip.lib.katali_hip_malloc(ctypes.byref(p), 16) == -2
+
+
+def test_struct_layouts_match_header():
+    # field order and sizes of the two descriptors (checked against a C compile)
+    src = """
+#include <stdio.h>
+#include <stddef.h>
+#include "katali_hip.h"
+int main(void) {
+  printf("%zu %zu %zu %zu %zu %zu\\n", sizeof(KataliHipMoe), offsetof(KataliHipMoe, gate_exps),
+         offsetof(KataliHipMoe, down_shexp), sizeof(KataliHipMoeRoute),
+         offsetof(KataliHipMoeRoute, logits_stride), offsetof(KataliHipMoeRoute, weights_out));
+  return 0;
+}
+"""
+    import tempfile
+    with tempfile.TemporaryDirectory() as d:
+        c = os.path.join(d, "t.c")
+        open(c, "w").write(src)
+        exe = os.path.join(d, "t")
+        subprocess.run(["gcc", "-I" + os.path.join(REPO, "include"), c, "-o", exe], check=True)
+        vals = [int(v) for v in subprocess.run([exe], capture_output=True, text=True).stdout.split()]
+    M, R = K.KataliHipMoe, K.KataliHipMoeRoute
+    assert vals == [ctypes.sizeof(M), M.gate_exps.offset, M.down_shexp.offset, ctypes.sizeof(R),
+                    R.logits_stride.offset, R.weights_out.offset]
+
+
+@pytest.mark.parametrize("t,ok", [(12, 1), (14, 1), (0, 0), (2, 0), (13, 0)])
+def test_supports_type(t, ok):
+    assert K.KataliHip().lib.katali_hip_supports_type(t) == ok

@@ -1,0 +1,380 @@
+"""Pins the oracle's formats and integer/float building blocks (CPU only).
+
+Each check is independent of the oracle's own code: the compiled reference
+(oracle/_ref), numpy's IEEE conversions, blocks packed by hand from chosen
+values, brute-force integer sums over reference-decoded values, and closed
+forms (math.exp, float64 softmax).
+"""
+import math
+
+import numpy as np
+import pytest
+
+import kq_synth as S
+from oracle import Q4_K, Q6_K, Q8_1, row_bytes
+
+
+# ---------------------------------------------------------------------------
+# f16 (V/include/katali_gguf_fp.h:14-57)
+# ---------------------------------------------------------------------------
+def test_f16_to_f32_all_codes(oracle, refcpu):
+    codes = np.arange(65536, dtype=np.uint32)
+    ours = np.array([oracle.lib.kqo_f16_to_f32(int(c)) for c in codes], np.float32)
+    theirs = np.array([refcpu.lib.kref_f16_to_f32(int(c)) for c in codes], np.float32)
+    assert np.array_equal(ours.view(np.uint32), theirs.view(np.uint32))
+    # and against IEEE (numpy). A float returned through ctypes is widened to
+    # double, which quiets signalling NaNs, so NaN codes compare as NaN only.
+    ieee = codes.astype(np.uint16).view(np.float16).astype(np.float32)
+    nan = np.isnan(ieee)
+    assert np.array_equal(ours[~nan].view(np.uint32), ieee[~nan].view(np.uint32))
+    assert np.all(np.isnan(ours[nan]))
+
+
+def _f32_samples(rng, n):
+    bits = rng.integers(0, 2**32, size=n, dtype=np.uint64).astype(np.uint32)
+    special = np.array([0.0, -0.0, 1.0, -1.0, 0.5, 65504.0, 65519.99, 65520.0, 1e-8, 5.96e-8, 2.98e-8,
+                        2.9802322e-08, 6.1035156e-05, 6.0975552e-05, 0.000123, 3.0e38, np.inf, -np.inf],
+                       np.float32).view(np.uint32)
+    # every f16 value and the exact midpoints between neighbours (ties)
+    h = np.arange(0, 0x7C00, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float64)
+    mids = ((h[:-1] + h[1:]) / 2).astype(np.float32).view(np.uint32)
+    return np.concatenate([bits, special, h.astype(np.float32).view(np.uint32), mids])
+
+
+def test_f32_to_f16_ref_matches_reference(oracle, refcpu):
+    rng = np.random.default_rng(7)
+    xs = _f32_samples(rng, 100_000).view(np.float32)
+    xs = xs[~np.isnan(xs)]
+    ours = np.array([oracle.lib.kqo_f32_to_f16_ref(float(v)) for v in xs], np.uint16)
+    theirs = np.array([refcpu.lib.kref_f32_to_f16(float(v)) for v in xs], np.uint16)
+    assert np.array_equal(ours, theirs)
+
+
+def test_f32_to_f16_rne_matches_ieee(oracle):
+    rng = np.random.default_rng(8)
+    xs = _f32_samples(rng, 100_000).view(np.float32)
+    ours = np.array([oracle.lib.kqo_f32_to_f16_rne(float(v)) for v in xs], np.uint16)
+    with np.errstate(over="ignore"):
+        ieee = xs.astype(np.float16).view(np.uint16)
+    nan = np.isnan(xs)
+    assert np.array_equal(ours[~nan], ieee[~nan])
+    assert np.all((ours[nan] & 0x7C00) == 0x7C00) and np.all(ours[nan] & 0x3FF)
+
+
+def test_f16_round_trip_reference_values(oracle):
+    # the reference's own round-trip check (V/src/gguf_dtype.c:1234-1242)
+    for v in [0.0, 1.0, -1.0, 0.5, 65504.0, 0.000123]:
+        back = oracle.f16_to_f32(oracle.lib.kqo_f32_to_f16_ref(v))
+        assert abs(back - v) / (abs(v) + 1e-9) <= 2e-3
+
+
+# ---------------------------------------------------------------------------
+# Block layouts: hand-packed blocks with chosen values
+# ---------------------------------------------------------------------------
+def pack_q4k(d: float, dmin: float, sc: list[int], mn: list[int], q: np.ndarray) -> np.ndarray:
+    """Build one Q4_K block from 8 scales, 8 mins (6-bit) and 256 nibble values."""
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.array([d], np.float16).view(np.uint8)
+    blk[2:4] = np.array([dmin], np.float16).view(np.uint8)
+    s = np.zeros(12, np.uint8)
+    for j in range(8):
+        if j < 4:
+            s[j] |= sc[j] & 63
+            s[j + 4] |= mn[j] & 63
+        else:
+            s[j + 4] = (sc[j] & 15) | ((mn[j] & 15) << 4)
+            s[j - 4] |= (sc[j] >> 4) << 6
+            s[j] |= (mn[j] >> 4) << 6
+    blk[4:16] = s
+    for e in range(256):
+        g, within = e // 64, e % 64
+        byte = 16 + 32 * g + within % 32
+        blk[byte] |= (q[e] & 15) << (0 if within < 32 else 4)
+    return blk
+
+
+def pack_q6k(d: float, sc: list[int], q: np.ndarray) -> np.ndarray:
+    """Build one Q6_K block from 16 int8 scales and 256 values in [0, 63]."""
+    blk = np.zeros(210, np.uint8)
+    for e in range(256):
+        n, t, l = e // 128, (e % 128) // 32, e % 32
+        lb = 64 * n + l + 32 * (t & 1)
+        blk[lb] |= (q[e] & 15) << (0 if t < 2 else 4)
+        blk[128 + 32 * n + l] |= (q[e] >> 4) << (2 * t)
+    blk[192:208] = np.array(sc, np.int8).view(np.uint8)
+    blk[208:210] = np.array([d], np.float16).view(np.uint8)
+    return blk
+
+
+def test_q4k_layout_known_answer(oracle, refcpu):
+    rng = np.random.default_rng(1)
+    sc = [int(v) for v in rng.integers(0, 64, 8)]
+    mn = [int(v) for v in rng.integers(0, 64, 8)]
+    q = rng.integers(0, 16, 256)
+    blk = pack_q4k(1.0, 0.5, sc, mn, q)
+    want = np.array([sc[e // 32] * q[e] - 0.5 * mn[e // 32] for e in range(256)], np.float32)
+    assert np.array_equal(oracle.dequant(Q4_K, blk, 256), want)
+    assert np.array_equal(refcpu.dequant(Q4_K, blk, 256), want)
+
+
+def test_q6k_layout_known_answer(oracle, refcpu):
+    rng = np.random.default_rng(2)
+    sc = [int(v) for v in rng.integers(-128, 128, 16)]
+    q = rng.integers(0, 64, 256)
+    blk = pack_q6k(1.0, sc, q)
+    want = np.array([sc[e // 16] * (q[e] - 32) for e in range(256)], np.float32)
+    assert np.array_equal(oracle.dequant(Q6_K, blk, 256), want)
+    assert np.array_equal(refcpu.dequant(Q6_K, blk, 256), want)
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+def test_dequant_bit_exact_vs_reference(oracle, refcpu, t):
+    rng = np.random.default_rng(3)
+    w = S.matrix(rng, t, 16, 1024)
+    assert np.array_equal(oracle.dequant(t, w, 16 * 1024).view(np.uint32),
+                          refcpu.dequant(t, w, 16 * 1024).view(np.uint32))
+
+
+def test_q8_1_dequant_vs_reference(oracle, refcpu):
+    rng = np.random.default_rng(4)
+    b = rng.integers(0, 256, (8, 36), dtype=np.uint8)
+    b[:, 0:2] = np.abs(rng.normal(0, 0.1, (8, 1))).astype(np.float16).view(np.uint8)
+    b = b.reshape(-1)
+    assert np.array_equal(oracle.dequant(Q8_1, b, 256), refcpu.dequant(Q8_1, b, 256))
+
+
+# ---------------------------------------------------------------------------
+# q8_1 quantizer (public block_q8_1 definition)
+# ---------------------------------------------------------------------------
+def _unpack_q8(q8: np.ndarray):
+    blk = q8.reshape(-1, 36)
+    d = blk[:, 0:2].copy().view(np.float16).astype(np.float32).reshape(-1)
+    s = blk[:, 2:4].copy().view(np.float16).astype(np.float32).reshape(-1)
+    qs = blk[:, 4:].view(np.int8).astype(np.int32)
+    return d, s, qs
+
+
+def test_q8_1_invariants(oracle):
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal(32 * 512) * rng.choice([1e-3, 1.0, 50.0], 32 * 512)).astype(np.float32)
+    x[32 * 7: 32 * 8] = 0.0                      # an all-zero block
+    d, s, qs = _unpack_q8(oracle.quantize_q8_1(x))
+    xb = x.reshape(-1, 32)
+    amax = np.abs(xb).max(axis=1)
+    d32 = (amax / np.float32(127)).astype(np.float32)
+    assert np.all(np.abs(qs) <= 127)
+    nz = amax > 0
+    # the largest magnitude maps to +-127
+    assert np.all(np.abs(qs[nz]).max(axis=1) == 127)
+    # rounding error at most half a step (fp32 step d32; tiny slack for x*(1/d))
+    err = np.abs(xb - d32[:, None] * qs)
+    assert np.all(err <= d32[:, None] * (0.5 + 1e-5) + 1e-30)
+    # stored d is the f16 of d32; s is f16(d32 * sum q)
+    assert np.array_equal(d, d32.astype(np.float16).astype(np.float32))
+    assert np.array_equal(s, (d32 * qs.sum(axis=1)).astype(np.float32).astype(np.float16).astype(np.float32))
+    assert np.all(qs[~nz] == 0) and np.all(d[~nz] == 0)
+
+
+def test_q8_1_exact_on_representable(oracle):
+    rng = np.random.default_rng(6)
+    q = rng.integers(-127, 128, (64, 32))
+    q[:, 0] = np.where(rng.integers(0, 2, 64) == 1, 127, -127)
+    step = np.float32(2.0 ** -5)
+    x = (q * step).astype(np.float32).reshape(-1)
+    d, _, qs = _unpack_q8(oracle.quantize_q8_1(x))
+    assert np.array_equal(qs, q)
+    assert np.all(d == step)
+
+
+def test_q8_1_known_block(oracle):
+    x = np.arange(-16, 16, dtype=np.float32)              # amax 16
+    _, _, qs = _unpack_q8(oracle.quantize_q8_1(x))
+    d = np.float32(16) / np.float32(127)
+    inv = np.float32(1) / d
+    want = [int(math.floor(abs(float(np.float32(v) * inv)) + 0.5)) * (1 if v >= 0 else -1) for v in x]
+    assert qs.reshape(-1).tolist() == want
+    assert qs[0, 0] == -127 and qs[0, 16] == 0
+
+
+# ---------------------------------------------------------------------------
+# Integer block sums: brute force over reference-decoded values
+# ---------------------------------------------------------------------------
+def _unit_scale(t, w):
+    """Copy of w with every scale 1, d 1, min 0: the reference decoder then
+    returns the raw quant value (Q4_K) or quant-32 (Q6_K)."""
+    w = w.copy()
+    if t == Q4_K:
+        b = w.reshape(-1, 144)
+        b[:, 0:2] = np.array([1.0], np.float16).view(np.uint8)
+        b[:, 2:4] = 0
+        s = np.zeros(12, np.uint8)
+        s[0:4] = 1                      # sc[0..3] = 1, m[0..3] = 0
+        s[8:12] = 1                     # sc[4..7] low nibble 1, m high nibble 0
+        b[:, 4:16] = s
+    else:
+        b = w.reshape(-1, 210)
+        b[:, 192:208] = 1
+        b[:, 208:210] = np.array([1.0], np.float16).view(np.uint8)
+    return w
+
+
+@pytest.mark.parametrize("t,cols", [(Q4_K, 512), (Q6_K, 768), (Q4_K, 2048), (Q6_K, 256)])
+def test_block_isums_brute_force(oracle, refcpu, t, cols):
+    rng = np.random.default_rng(10 + cols)
+    rows = 6
+    w = S.matrix(rng, t, rows, cols)
+    q8 = oracle.quantize_q8_1(S.activation(rng, cols))
+    _, _, qs = _unpack_q8(q8)
+    qv = qs.reshape(-1).astype(np.int64)
+    vals = refcpu.dequant(t, _unit_scale(t, w), rows * cols).reshape(rows, cols).astype(np.int64)
+    group = 32 if t == Q4_K else 16
+    want = (vals * qv[None, :]).reshape(rows, cols // group, group).sum(axis=2)
+    got = oracle.isums(t, w, rows, cols, q8)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("t,cols", [(Q4_K, 2048), (Q6_K, 768), (Q6_K, 512), (Q4_K, 4096)])
+def test_q8_dot_vs_reference_on_dequantized_activation(oracle, refcpu, t, cols):
+    """The integer-composed q8 dot equals the reference's double-accumulated dot
+    of the same weights with the dequantized q8 activation (to float rounding)."""
+    rng = np.random.default_rng(20 + cols)
+    rows = 32
+    w = S.matrix(rng, t, rows, cols)
+    q8 = oracle.quantize_q8_1(S.activation(rng, cols))
+    xd = oracle.dequant(Q8_1, q8, cols)
+    got = oracle.matvec_q8(t, w, rows, cols, q8).astype(np.float64)
+    ref = refcpu.vec_dot_rows(t, w, rows, cols, xd, "ref").astype(np.float64)
+    rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    assert rel < 1e-6, rel
+
+
+# ---------------------------------------------------------------------------
+# exp / SiLU / router
+# ---------------------------------------------------------------------------
+def test_expf_error_bound(oracle):
+    xs = np.concatenate([np.linspace(-80, 88, 40001), np.linspace(-2, 2, 4001)]).astype(np.float32)
+    got = np.array([oracle.expf(float(v)) for v in xs], np.float64)
+    want = np.exp(xs.astype(np.float64))
+    ulp = np.spacing(want.astype(np.float32)).astype(np.float64)
+    assert np.max(np.abs(got - want) / ulp) <= 2.0
+    assert oracle.expf(0.0) == 1.0
+
+
+def test_silu_mul_vs_float64(oracle):
+    rng = np.random.default_rng(11)
+    g = (rng.standard_normal(4096) * 6).astype(np.float32)
+    u = rng.standard_normal(4096).astype(np.float32)
+    got = oracle.silu_mul(g, u).astype(np.float64)
+    g64 = g.astype(np.float64)
+    want = g64 / (1 + np.exp(-g64)) * u
+    assert np.max(np.abs(got - want) / (np.abs(want) + 1e-30)) < 1e-6
+
+
+def test_reference_silu_restatement_bit_exact(oracle, refcpu):
+    rng = np.random.default_rng(12)
+    for n in (8, 512, 768, 13):
+        g = (rng.standard_normal(n) * 5).astype(np.float32)
+        u = rng.standard_normal(n).astype(np.float32)
+        assert np.array_equal(oracle.silu_mul_ref(g, u).view(np.uint32), refcpu.silu_mul(g, u).view(np.uint32))
+
+
+@pytest.mark.parametrize("n_expert,k", [(128, 8), (256, 8), (128, 1), (64, 4), (128, 16)])
+def test_router_topk_vs_softmax_renorm(oracle, refcpu, n_expert, k):
+    rng = np.random.default_rng(n_expert + k)
+    logits = rng.standard_normal(n_expert).astype(np.float32)
+    logits[5] = logits[9] = logits.max() + 1.0         # a tie at the top: lower index first
+    ids, w = oracle.router_topk(logits, k)
+    order = sorted(range(n_expert), key=lambda e: (-float(logits[e]), e))[:k]
+    assert ids.tolist() == order
+    assert ids[0] == 5 and (k == 1 or ids[1] == 9)
+    p = np.exp(logits.astype(np.float64) - logits.max())
+    p /= p.sum()
+    want = p[order] / p[order].sum()
+    assert np.allclose(w, want, rtol=2e-6, atol=0)
+    # the reference's own softmax (gguf_kernels.c:74-80) then renormalise
+    ps = refcpu.softmax(logits).astype(np.float64)
+    assert np.allclose(w, ps[order] / ps[order].sum(), rtol=1e-5, atol=0)
+
+
+# ---------------------------------------------------------------------------
+# MoE composition: independent float64 composition over reference decoders
+# ---------------------------------------------------------------------------
+def _moe_problem(rng, hidden, ffn, n_expert, shared=False):
+    gate = S.matrix(rng, Q4_K, n_expert * ffn, hidden)
+    up = S.matrix(rng, Q4_K, n_expert * ffn, hidden)
+    down = S.matrix(rng, Q6_K, n_expert * hidden, ffn)
+    sh = None
+    if shared:
+        sh = (ffn, S.matrix(rng, Q4_K, ffn, hidden), S.matrix(rng, Q4_K, ffn, hidden),
+              S.matrix(rng, Q6_K, hidden, ffn))
+    return gate, up, down, sh
+
+
+def _moe_float64(refcpu, hidden, ffn, gate, up, down, sh, x, ids, w):
+    def deq(t, buf, rows, cols, idx):
+        rb = row_bytes(t, cols)
+        part = buf[idx * rows * rb:(idx + 1) * rows * rb]
+        return refcpu.dequant(t, part, rows * cols).reshape(rows, cols).astype(np.float64)
+    x64 = x.astype(np.float64)
+    y = np.zeros(hidden)
+    slots = [(int(e), float(wt), gate, up, down) for e, wt in zip(ids, w)]
+    if sh is not None:
+        slots.append((0, 1.0, sh[1], sh[2], sh[3]))
+    for e, wt, G, U, D in slots:
+        g = deq(Q4_K, G, ffn, hidden, e) @ x64
+        u = deq(Q4_K, U, ffn, hidden, e) @ x64
+        h = g / (1 + np.exp(-g)) * u
+        y += wt * (deq(Q6_K, D, hidden, ffn, e) @ h)
+    return y
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_moe_f32_path_vs_float64(oracle, refcpu, shared):
+    rng = np.random.default_rng(30 + shared)
+    hidden, ffn, n_expert = 512, 256, 6
+    gate, up, down, sh = _moe_problem(rng, hidden, ffn, n_expert, shared)
+    x = S.activation(rng, hidden)
+    ids, w = oracle.router_topk(rng.standard_normal(n_expert).astype(np.float32), 3)
+    desc = oracle.moe_desc(hidden, ffn, n_expert, gate, up, down, shared=sh)
+    got = oracle.moe_layer_f32(desc, x, ids, w).astype(np.float64)
+    want = _moe_float64(refcpu, hidden, ffn, gate, up, down, sh, x, ids, w)
+    assert np.linalg.norm(got - want) / np.linalg.norm(want) < 1e-5
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_moe_q8_path_vs_float64(oracle, refcpu, shared):
+    """q8_1 rounding of x and h costs ~1% (README.md:17 reports 7.2e-3 on real
+    weights); a wiring error (wrong expert, gate/up swapped, transposed down)
+    costs O(1)."""
+    rng = np.random.default_rng(40 + shared)
+    hidden, ffn, n_expert = 512, 256, 6
+    gate, up, down, sh = _moe_problem(rng, hidden, ffn, n_expert, shared)
+    x = S.activation(rng, hidden)
+    ids, w = oracle.router_topk(rng.standard_normal(n_expert).astype(np.float32), 3)
+    desc = oracle.moe_desc(hidden, ffn, n_expert, gate, up, down, shared=sh)
+    got = oracle.moe_layer_q8(desc, x, ids, w).astype(np.float64)
+    want = _moe_float64(refcpu, hidden, ffn, gate, up, down, sh, x, ids, w)
+    rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+    assert rel < 3e-2, rel
+
+
+def test_moe_q8_is_weighted_sum_of_single_experts(oracle):
+    rng = np.random.default_rng(50)
+    hidden, ffn, n_expert = 256, 256, 5
+    gate, up, down, _ = _moe_problem(rng, hidden, ffn, n_expert)
+    x = S.activation(rng, hidden)
+    desc = oracle.moe_desc(hidden, ffn, n_expert, gate, up, down)
+    ids = np.array([3, 0, 4], np.int32)
+    w = np.array([0.5, 0.3, 0.2], np.float32)
+    y = oracle.moe_layer_q8(desc, x, ids, w)
+    acc = np.zeros(hidden, np.float32)
+    for e, wt in zip(ids, w):
+        ye = oracle.moe_layer_q8(desc, x, np.array([e], np.int32), np.array([1.0], np.float32))
+        acc = (np.float32(wt) * ye + acc).astype(np.float32)      # fmaf order, checked loosely
+    assert np.allclose(y, acc, rtol=1e-6, atol=1e-6 * np.abs(y).max())
+    # stages come out consistently
+    y2, g, u, hq = oracle.moe_layer_q8(desc, x, ids, w, with_stages=True)
+    assert np.array_equal(y, y2)
+    h = oracle.silu_mul(g[1], u[1])
+    assert np.array_equal(oracle.quantize_q8_1(h), hq[1])
+    assert np.array_equal(oracle.moe_down_q8(desc, ids, w, hq), y)
