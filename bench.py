@@ -1,6 +1,6 @@
 """Benchmark of the quantized expert-GEMV path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload moe48|moe40cold|dense|qwen8b]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload moe48|moe40cold]
 
 Default workload (moe48): one decode token through 48 fused MoE layers,
 hidden 2048, 128 experts, top-8, gate/up 2048->768 Q4_K, down 768->2048 Q6_K,
@@ -154,7 +154,6 @@ def bench_moe(hip, name, steps, warmup, ring=64):
         "kernel_gbs": layer_bytes / (kernel_ms / 1e3) / 1e9,
         "layer_bytes": layer_bytes,
         "pool_gb": L * (n_expert * (2 * ffn * rb_g + hidden * rb_d)) / 1e9,
-        "moe_mode": hip.get_option("moe_mode"),
     }
     for bufs in layers:
         for b in bufs[:3]:
@@ -255,7 +254,6 @@ def main():
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", default="moe48", choices=sorted(MOE_WORKLOADS))
-    ap.add_argument("--moe-mode", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -267,8 +265,6 @@ def main():
     if not hip.probe():
         print(f"no usable gfx950 device: {hip.status()}", file=sys.stderr)
         sys.exit(1)
-    if args.moe_mode is not None:
-        hip.set_option("moe_mode", args.moe_mode)
     print(f"[bench] device: {hip.status()}; workload {args.workload}", file=sys.stderr, flush=True)
     res, shape = bench_moe(hip, args.workload, args.steps, args.warmup)
     print(f"[bench] gpu done: {res['value']:.1f} GB/s, {res['tok_s']:.1f} tok/s", file=sys.stderr, flush=True)
@@ -298,7 +294,6 @@ def main():
             "layers": L, "hidden": hidden, "ffn": ffn, "n_expert": n_expert, "n_sel": n_sel,
             "shared_expert": shared, "expert_pool_gb": round(res["pool_gb"], 2),
             "bytes_per_token": res["bytes_per_token"], "parallelism": "single GPU",
-            "moe_mode": res["moe_mode"],
         },
         "tok_s": round(res["tok_s"], 2),
         "hbm_frac": round(res["value"] / HBM_PEAK_GBS, 4),
@@ -309,7 +304,7 @@ def main():
             "unit": "GB/s",
             "frac": round(res["kernel_gbs"] / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "fused MoE layer (k_moe_fused)" if res["moe_mode"] == 1 else "MoE layer (k_moe_a + k_moe_b)",
+            "kernel": "MoE layer (k_moe_gu + k_moe_down, one graph node pair per layer)",
             "bytes_per_launch": res["layer_bytes"],
             "launch_ms_mean": round(res["kernel_ms_mean"], 5),
             "launch_ms_median": round(res["kernel_ms_median"], 5),

@@ -158,11 +158,6 @@ int katali_hip_event_record(void *event);
 int katali_hip_event_elapsed(void *start, void *end, float *ms);
 int katali_hip_event_destroy(void *event);
 
-/* ---- options --------------------------------------------------------------- */
-/* "moe_mode": 0 = two launches per layer, 1 = one launch (default). */
-int katali_hip_set_option(const char *name, int64_t value);
-int64_t katali_hip_get_option(const char *name);
-
 /* ---- self-test and synthetic data for the harnesses ------------------------ */
 /* cuda-dp4a-selftest equivalent (README.md:17): a synthetic Q4_K and Q6_K
  * GEMV whose activation is exactly representable in q8_1, dotted by the fp32

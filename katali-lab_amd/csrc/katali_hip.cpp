@@ -35,10 +35,8 @@ bool g_capturing = false;
 // MoE scratch
 uint8_t *g_hq8 = nullptr;
 size_t g_hq8_cap = 0;
-uint32_t *g_sync = nullptr;
+int32_t *g_route = nullptr;   // [ids | weights] from kernel A to kernel B
 int32_t *g_err_dev = nullptr;
-
-int64_t g_moe_mode = 1;
 
 int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 int fail(int code, const char *fmt, ...) {
@@ -90,8 +88,6 @@ int init_locked() {
         return KATALI_HIP_E_NODEVICE;
     }
     g_stream = g_own_stream;
-    const char *mm = getenv("KATALI_HIP_MOE_MODE");
-    if (mm) g_moe_mode = atoi(mm) ? 1 : 0;
     char buf[256];
     snprintf(buf, sizeof buf, "%s (%s, %d CUs, %.0f GiB)", p.name, p.gcnArchName, p.multiProcessorCount,
              (double)p.totalGlobalMem / (1024.0 * 1024.0 * 1024.0));
@@ -124,12 +120,11 @@ int launched(hipError_t e, const char *what) { return e == hipSuccess ? KATALI_H
 
 // MoE scratch: allocated outside any capture; grows only when not capturing.
 int moe_scratch(size_t hq8_bytes) {
-    if (!g_sync) {
+    if (!g_route) {
         if (g_capturing) return fail(KATALI_HIP_E_INVALID, "first MoE call must happen outside graph capture");
-        hipError_t e = hipMalloc((void **)&g_sync, kq::moe_sync_words() * 4);
-        if (e != hipSuccess) return hip_fail(e, "hipMalloc(moe sync)");
+        hipError_t e = hipMalloc((void **)&g_route, kq::moe_route_words() * 4);
+        if (e != hipSuccess) return hip_fail(e, "hipMalloc(moe routing scratch)");
         if ((e = hipMalloc((void **)&g_err_dev, 64)) != hipSuccess) return hip_fail(e, "hipMalloc(moe err)");
-        if ((e = hipMemset(g_sync, 0, kq::moe_sync_words() * 4)) != hipSuccess) return hip_fail(e, "hipMemset");
         if ((e = hipMemset(g_err_dev, 0, 64)) != hipSuccess) return hip_fail(e, "hipMemset");
     }
     if (hq8_bytes > g_hq8_cap) {
@@ -159,10 +154,12 @@ int moe_impl(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, 
     if (rc) return rc;
     if (!m || !r || m->struct_size < sizeof(KataliHipMoe) || r->struct_size < sizeof(KataliHipMoeRoute))
         return fail(KATALI_HIP_E_INVALID, "null or short MoE descriptor");
-    if (!type_ok(m->gate_type) || !type_ok(m->down_type) || m->up_type != m->gate_type)
-        return fail(KATALI_HIP_E_UNSUPPORTED, "MoE types gate=%u up=%u down=%u", m->gate_type, m->up_type, m->down_type);
-    if (!m->hidden || m->hidden % 256 || m->hidden > 16384 || !m->ffn || m->ffn % 256 || m->ffn > 16384)
-        return fail(KATALI_HIP_E_INVALID, "MoE hidden=%u ffn=%u (need multiples of 256, <= 16384)", m->hidden, m->ffn);
+    if (m->up_type != m->gate_type || !kq::moe_shape_supported(m->gate_type, m->down_type, m->hidden, m->ffn))
+        return fail(KATALI_HIP_E_UNSUPPORTED,
+                    "MoE gate=%u up=%u down=%u hidden=%u ffn=%u: need Q4_K gate/up, Q4_K or Q6_K down, "
+                    "hidden in {256,512,1024,2048,4096}, ffn a multiple of 256 (<= 16384)",
+                    m->gate_type, m->up_type, m->down_type, m->hidden, m->ffn);
+    if (m->ffn > 16384) return fail(KATALI_HIP_E_INVALID, "MoE ffn=%u above 16384", m->ffn);
     if (!m->n_expert || m->n_expert > 512) return fail(KATALI_HIP_E_INVALID, "n_expert=%u", m->n_expert);
     if (!m->gate_exps || !m->up_exps || !m->down_exps || !y) return fail(KATALI_HIP_E_INVALID, "null buffer");
     if ((x == nullptr) == (xq == nullptr)) return fail(KATALI_HIP_E_INVALID, "give exactly one of x_dev / xq8_dev");
@@ -203,11 +200,11 @@ int moe_impl(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, 
     a.wts_out = r->weights_out;
     a.y = y;
     a.hq8 = g_hq8;
-    a.sync = g_sync;
+    a.route_ids = g_route;
+    a.route_w = (float *)(g_route + kq::moe_route_words() / 2);
     a.dbg_gu = gu_dbg;
     a.err = g_err_dev;
-    int grid = 0;
-    rc = launched(kq::launch_moe(a, (int)g_moe_mode, g_stream, &grid), "moe launch");
+    rc = launched(kq::launch_moe(a, g_stream), "moe launch");
     if (rc) return rc;
     if (hq8_dbg) {
         hipError_t e = hipMemcpyAsync(hq8_dbg, g_hq8, hq8_bytes, hipMemcpyDeviceToDevice, g_stream);
@@ -290,7 +287,6 @@ int katali_hip_sync(void) {
         if (e != hipSuccess) return hip_fail(e, "read error word");
         if (err) {
             (void)hipMemset(g_err_dev, 0, 4);
-            if (err & 1) return fail(KATALI_HIP_E_TIMEOUT, "MoE dependency wait timed out (grid not co-resident?)");
             return fail(KATALI_HIP_E_INVALID, "MoE expert id outside [0, n_expert) (bad ids or non-finite logits)");
         }
     }
@@ -427,23 +423,6 @@ int katali_hip_event_elapsed(void *a, void *b, float *ms) {
 int katali_hip_event_destroy(void *ev) {
     if (!ev) return KATALI_HIP_OK;
     return launched(hipEventDestroy((hipEvent_t)ev), "hipEventDestroy");
-}
-
-int katali_hip_set_option(const char *name, int64_t value) {
-    if (!name) return fail(KATALI_HIP_E_INVALID, "null option name");
-    if (!strcmp(name, "moe_mode")) {
-        if (value != 0 && value != 1) return fail(KATALI_HIP_E_INVALID, "moe_mode must be 0 or 1");
-        std::lock_guard<std::mutex> lk(g_init_mu);
-        init_locked();
-        g_moe_mode = value;
-        return KATALI_HIP_OK;
-    }
-    return fail(KATALI_HIP_E_UNSUPPORTED, "unknown option %s", name);
-}
-
-int64_t katali_hip_get_option(const char *name) {
-    if (name && !strcmp(name, "moe_mode")) return g_moe_mode;
-    return -1;
 }
 
 int katali_hip_synth_fill(uint32_t type, void *dev, uint64_t nblocks, uint64_t seed, float d_sigma) {

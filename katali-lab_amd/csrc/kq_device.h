@@ -66,6 +66,35 @@ __device__ __forceinline__ float wave_sum_xor(float v, int width) {
     return v;
 }
 
+// Lane exchanges inside aligned groups of 4 / 8 / 16 lanes on the VALU (DPP),
+// no LDS round trip: quad_perm [1,0,3,2] and [2,3,0,1] (partner = lane ^ 1,
+// lane ^ 2), row_half_mirror (lane ^ 7 inside 8) and row_mirror (lane ^ 15
+// inside 16). A butterfly over masks {1, 2, 7} or {1, 2, 7, 15} visits every
+// lane of the group once, so it reduces exactly like the xor butterfly.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+
+// sum over aligned groups of W lanes (W a power of 2 up to 64), all lanes get
+// it; steps past 16 lanes cross DPP rows and go through ds_bpermute
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(W >= 1 && W <= 64 && (W & (W - 1)) == 0, "group_sum: W must be a power of 2 <= 64");
+    if constexpr (W >= 2) v += dpp_f<DPP_XOR1>(v);
+    if constexpr (W >= 4) v += dpp_f<DPP_XOR2>(v);
+    if constexpr (W >= 8) v += dpp_f<DPP_HALF_MIRROR>(v);
+    if constexpr (W >= 16) v += dpp_f<DPP_MIRROR>(v);
+    if constexpr (W >= 32) v += __shfl_xor(v, 16, WAVE);
+    if constexpr (W >= 64) v += __shfl_xor(v, 32, WAVE);
+    return v;
+}
+
 // exp by Cody-Waite reduction x = n*ln2 + r (ln2 split into a 15-bit high part,
 // exact for |n| <= 256, and a low correction) and a degree-7 Taylor polynomial
 // for e^r, |r| <= ln2/2, evaluated by Horner with fused multiply-adds. Every
@@ -122,17 +151,17 @@ __device__ __forceinline__ Act act_carve(uint8_t *base, uint32_t K) {
 __device__ __forceinline__ uint32_t quant_q8_1_part(float4 v, uint32_t &d16, uint32_t &s16,
                                                     int &sum_lo, int &sum_hi, float &d_dec) {
     float am = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    am = fmaxf(am, __shfl_xor(am, 1, WAVE));
-    am = fmaxf(am, __shfl_xor(am, 2, WAVE));
-    am = fmaxf(am, __shfl_xor(am, 4, WAVE));
+    am = fmaxf(am, dpp_f<DPP_XOR1>(am));
+    am = fmaxf(am, dpp_f<DPP_XOR2>(am));
+    am = fmaxf(am, dpp_f<DPP_HALF_MIRROR>(am));
     const float d = am / 127.0f;
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
     const int q0 = (int)roundf(v.x * id), q1 = (int)roundf(v.y * id);
     const int q2 = (int)roundf(v.z * id), q3 = (int)roundf(v.w * id);
     int s = q0 + q1 + q2 + q3;
-    s += __shfl_xor(s, 1, WAVE);
-    s += __shfl_xor(s, 2, WAVE);      // sum of this lane's half block (4 lanes)
-    const int other = __shfl_xor(s, 4, WAVE);
+    s += dpp_i<DPP_XOR1>(s);
+    s += dpp_i<DPP_XOR2>(s);          // sum of this lane's half block (4 lanes)
+    const int other = dpp_i<DPP_HALF_MIRROR>(s);
     const int part = threadIdx.x & 7;
     sum_lo = part < 4 ? s : other;
     sum_hi = part < 4 ? other : s;
@@ -173,9 +202,9 @@ __device__ __forceinline__ void act_stage_from_q8(const uint8_t *__restrict__ xq
         const uint32_t q = *(const uint32_t *)(b + 4 + 4 * part);
         *(uint32_t *)(a.qs + 32 * blk + 4 * part) = q;
         int s = dot4(q, 0x01010101u, 0);
-        s += __shfl_xor(s, 1, WAVE);
-        s += __shfl_xor(s, 2, WAVE);
-        const int other = __shfl_xor(s, 4, WAVE);
+        s += dpp_i<DPP_XOR1>(s);
+        s += dpp_i<DPP_XOR2>(s);
+        const int other = dpp_i<DPP_HALF_MIRROR>(s);
         if (part == 0) {
             a.d8[blk] = h2f(ld_u16(b));
             a.qs16[2 * blk] = s;
@@ -241,6 +270,19 @@ struct Q4K {
         shi = dot4((r.q.y >> 4) & m, xh.y, shi);
         shi = dot4((r.q.z >> 4) & m, xh.z, shi);
         shi = dot4((r.q.w >> 4) & m, xh.w, shi);
+    }
+    // integer sums of one 16-byte nibble chunk against preloaded activations
+    __device__ static __forceinline__ void isums_x(const uint4 &q, const int4 &xl, const int4 &xh, int &slo,
+                                                   int &shi) {
+        const uint32_t m = 0x0F0F0F0Fu;
+        slo = dot4(q.x & m, xl.x, 0);
+        slo = dot4(q.y & m, xl.y, slo);
+        slo = dot4(q.z & m, xl.z, slo);
+        slo = dot4(q.w & m, xl.w, slo);
+        shi = dot4((q.x >> 4) & m, xh.x, 0);
+        shi = dot4((q.y >> 4) & m, xh.y, shi);
+        shi = dot4((q.z >> 4) & m, xh.z, shi);
+        shi = dot4((q.w >> 4) & m, xh.w, shi);
     }
     // scale/min pairs for sub-blocks 2g and 2g+1 (get_scale_min_k4, two at once)
     __device__ static __forceinline__ void scales(const Raw &r, int g, float &ds0, float &ds1, float &dm0,

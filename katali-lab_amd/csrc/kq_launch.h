@@ -37,7 +37,7 @@ hipError_t launch_step_advance(int32_t *step, int32_t n_steps, hipStream_t s);
 // Plain streaming copy (HBM counter calibration).
 hipError_t launch_copy(const uint8_t *src, uint8_t *dst, uint64_t n, hipStream_t s);
 
-// Fused MoE layer. Types: gate/up in {Q4_K, Q6_K}, down in {Q4_K, Q6_K}.
+// MoE layer (two launches). Types: gate/up Q4_K; down Q4_K or Q6_K.
 struct MoeArgs {
     const uint8_t *gate, *up, *down;          // stacked [n_expert][rows][row_bytes]
     const uint8_t *gate_sh, *up_sh, *down_sh; // shared expert (NULL when absent)
@@ -56,13 +56,13 @@ struct MoeArgs {
     float *wts_out;
     float *y;                // [hidden]
     uint8_t *hq8;            // scratch [n_slots][ffn/32][36]
-    uint32_t *sync;          // scratch counters (zero at rest)
+    int32_t *route_ids;      // scratch [moe_route_words()/2]: routing from kernel A to kernel B
+    float *route_w;
     float *dbg_gu;           // optional [n_slots][2][ffn] gate/up outputs
-    int32_t *err;            // error word (non-zero on timeout)
+    int32_t *err;            // error word (bit 1: expert id out of range)
 };
-// mode 0: two launches (gate/up+SiLU+quantize, then down+reduction)
-// mode 1: one launch with an in-kernel dependency wait
-hipError_t launch_moe(const MoeArgs &a, int mode, hipStream_t s, int *grid_out);
-uint64_t moe_sync_words();
+bool moe_shape_supported(uint32_t gate_type, uint32_t down_type, uint32_t hidden, uint32_t ffn);
+hipError_t launch_moe(const MoeArgs &a, hipStream_t s);
+uint64_t moe_route_words();
 
 }  // namespace kq

@@ -1,25 +1,30 @@
-// kq_moe.hip — the fused per-layer MoE kernel.
+// kq_moe.hip — the MoE layer: two launches per layer.
 //
 // y = sum_slot w_slot * Down_e(q8(SiLU(Gate_e x) * Up_e x)) over the selected
 // experts (rank order) and an optional always-on shared expert (weight 1).
 //
-// Phase A unit = (slot, 32 intermediate rows): 32 gate + 32 up row dots
-//   against the layer activation (q8_1 in LDS), then h = SiLU(g)*u for those
-//   32 values is quantized to one q8_1 block inside the workgroup and written
-//   to the scratch hq8[slot][block].
-// Phase B unit = a tile of output rows: for every row and every slot the down
-//   row is dotted with that slot's h (q8_1 in LDS); the weighted sum over the
-//   slots is formed in a fixed order by one thread per row, so the result is
-//   deterministic (no float atomics).
-// Mode 0 runs A and B as two launches; mode 1 runs both in one launch: each
-// workgroup does its A units, publishes them with a device-scope counter, and
-// waits (bounded) for all A units before its B tile. The grid never exceeds
-// the co-resident capacity, and the last workgroup to finish resets the
-// counters, so back-to-back launches and graph replays need no memset.
+// Kernel A (k_moe_gu), one workgroup per (slot, 32 intermediate rows):
+//   route (every workgroup ranks the logits itself), then issue every weight
+//   load of its 32 gate + 32 up rows at once (16-byte nibble chunks and block
+//   headers in registers), quantize x to q8_1 in LDS and decode the headers
+//   into LDS scale records while the loads are in flight, dot with v_dot4
+//   against activation slices each lane reads once, reduce the 64 rows with a
+//   halving butterfly, and turn the 32 SiLU-GLU outputs into one q8_1 block
+//   written to scratch. Workgroup 0 also computes the routing weights and
+//   writes the routing for kernel B.
+// Kernel B (k_moe_down), one workgroup per tile of output rows:
+//   read the routing, issue the down-row loads of every (row, slot) pair of
+//   the tile, stage every slot's q8_1 h in LDS meanwhile, dot, and sum the
+//   slots in rank order in one thread per row (no float atomics, so results
+//   are deterministic).
+// The kernel boundary is the only dependency between the two phases: an
+// in-kernel grid dependency measured slower on gfx950 (agent-scope fences
+// write back / invalidate L2; atomic and poll round trips cost more than the
+// boundary).
 //
-// Routing: when logits are given, every workgroup computes the same top-k
-// (largest logit first, lower index on ties) and weights
-// w_r = exp(l_r - l_max) / sum_sel exp(l_j - l_max) (rank-order sum), which is
+// Routing: expert e's rank is the number of experts with a larger logit (or
+// an equal logit and a lower index); ranks 0..n_sel-1 are selected. Weights
+// w_r = exp(l_r - l_max) / sum_sel exp(l_j - l_max) in rank order, which is
 // softmax followed by renormalisation over the selection.
 #include "kq_device.h"
 #include "kq_launch.h"
@@ -28,7 +33,7 @@ namespace kq {
 
 constexpr int MAX_SEL = 16;
 constexpr int MAX_SLOTS = MAX_SEL + 1;
-constexpr uint32_t SPIN_LIMIT = 1u << 22;
+constexpr uint32_t MAX_EXPERT = 512;
 
 struct Route {
     int32_t ids[MAX_SLOTS];
@@ -41,171 +46,322 @@ __device__ __forceinline__ const float *route_logits(const MoeArgs &a) {
     return l;
 }
 
-// Wave 0 computes the routing into LDS; the caller synchronises.
-__device__ void route(const MoeArgs &a, Route *rt) {
-    if (threadIdx.x >= WAVE) return;
-    const int lane = threadIdx.x;
+// Block-wide routing into LDS: the selected ids (and, for explicit routing,
+// the given weights). `lg` is an LDS scratch of n_expert floats rounded up to
+// a multiple of 4 (padding ranks last) that keeps the logits for
+// route_publish. Every thread must already have issued `lv` = its logit loads
+// (see load_logits) so the global latency overlaps other loads. Ends with a
+// barrier.
+constexpr int LPT = MAX_EXPERT / 256;   // logits per thread
+__device__ __forceinline__ void load_logits(const MoeArgs &a, float (&lv)[LPT]) {
+    const float *src = a.logits ? route_logits(a) : nullptr;
+#pragma unroll
+    for (int i = 0; i < LPT; i++) {
+        const uint32_t e = threadIdx.x + 256 * i;
+        lv[i] = (src && e < a.n_expert) ? src[e] : -INFINITY;
+    }
+}
+
+__device__ void route_rank(const MoeArgs &a, Route *rt, float *lg, const float (&lv)[LPT]) {
+    const uint32_t t = threadIdx.x;
+    const uint32_t n4 = (a.n_expert + 3) & ~3u;
     if (a.logits) {
-        const float *lg = route_logits(a);
-        constexpr int MAXJ = 8;   // n_expert <= 512
-        float v[MAXJ];
-        uint32_t taken = 0;
 #pragma unroll
-        for (int j = 0; j < MAXJ; j++) {
-            const uint32_t e = lane + WAVE * j;
-            v[j] = e < a.n_expert ? lg[e] : -INFINITY;
-            if (e >= a.n_expert) taken |= 1u << j;
+        for (int i = 0; i < LPT; i++) {
+            const uint32_t e = t + 256 * i;
+            if (e < n4) lg[e] = lv[i] != lv[i] ? -INFINITY : lv[i];   // NaN and padding rank last
         }
-        for (int r = 0; r < a.n_sel; r++) {
-            float bv = -INFINITY;
-            int bi = 0x7FFFFFFF;
-#pragma unroll
-            for (int j = 0; j < MAXJ; j++) {
-                const int e = lane + WAVE * j;
-                if (!(taken & (1u << j)) && (v[j] > bv || (v[j] == bv && e < bi))) { bv = v[j]; bi = e; }
+        __syncthreads();
+        for (uint32_t e = t; e < a.n_expert; e += blockDim.x) {
+            const float v = lg[e];
+            uint32_t rank = 0;
+#pragma unroll 8
+            for (uint32_t j = 0; j < n4; j += 4) {
+                const float4 u = *(const float4 *)(lg + j);
+                rank += (u.x > v) | ((u.x == v) & (j + 0 < e));
+                rank += (u.y > v) | ((u.y == v) & (j + 1 < e));
+                rank += (u.z > v) | ((u.z == v) & (j + 2 < e));
+                rank += (u.w > v) | ((u.w == v) & (j + 3 < e));
             }
-            for (int o = WAVE / 2; o > 0; o >>= 1) {
-                const float ov = __shfl_xor(bv, o, WAVE);
-                const int oi = __shfl_xor(bi, o, WAVE);
-                if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-            }
-            if ((bi & (WAVE - 1)) == lane) taken |= 1u << (bi / WAVE);
-            if (lane == 0) rt->ids[r] = bi;
+            if (rank < (uint32_t)a.n_sel) rt->ids[rank] = (int32_t)e;   // ranks are a permutation
         }
-        if (lane == 0) {
-            const float lmax = lg[rt->ids[0]];
-            float e[MAX_SEL], sum = 0.0f;
-            for (int r = 0; r < a.n_sel; r++) {
-                e[r] = kq_expf(lg[rt->ids[r]] - lmax);
-                sum += e[r];
-            }
-            for (int r = 0; r < a.n_sel; r++) rt->w[r] = e[r] / sum;
-        }
-    } else if (lane < a.n_sel) {
-        rt->ids[lane] = a.ids[lane];
-        rt->w[lane] = a.wts[lane];
+    } else if (t < (uint32_t)a.n_sel) {
+        rt->ids[t] = a.ids[t];
+        rt->w[t] = a.wts[t];
     }
-    if (lane == 0) {
-        // an id outside the pool (bad input, or NaN-only logits) would index
-        // past the expert tensors: flag it and read expert 0 instead
-        for (int r = 0; r < a.n_sel; r++) {
-            if (rt->ids[r] < 0 || (uint32_t)rt->ids[r] >= a.n_expert) {
-                if (blockIdx.x == 0) atomicOr(a.err, 2);
-                rt->ids[r] = 0;
-            }
-        }
-        if (a.has_shared) {
-            rt->ids[a.n_sel] = -1;
-            rt->w[a.n_sel] = 1.0f;
-        }
+    if (t == 0 && a.has_shared) {
+        rt->ids[a.n_sel] = -1;
+        rt->w[a.n_sel] = 1.0f;
     }
+    __syncthreads();
+    // an id outside the pool (bad explicit ids) would index past the expert
+    // tensors: clamp it to 0 for addressing; workgroup 0 reports it
 }
 
-// Dot a list of rows against q8_1 activations. Lane-slot `ls` (S lanes each)
-// handles rows v = ls, ls + nls, ... < n; RPS rows are loaded before any is
-// computed. rowp(v) gives the row's bytes, actp(v) its activation, out(v, acc)
-// receives the result (called by the slot's lane 0).
-template <class QT, int IPL_T, int RPS, class RowP, class ActP, class Out>
-__device__ __forceinline__ void rows_dot(uint32_t n, uint32_t log2s, uint32_t ipl_rt, RowP rowp, ActP actp, Out out) {
-    const uint32_t S = 1u << log2s;
-    const uint32_t lane = threadIdx.x & (WAVE - 1);
-    const uint32_t ls = (threadIdx.x / WAVE) * (WAVE >> log2s) + (lane >> log2s);
-    const uint32_t nls = (blockDim.x / WAVE) * (WAVE >> log2s);
-    const uint32_t s = lane & (S - 1);
-    for (uint32_t v0 = ls; v0 < n; v0 += RPS * nls) {
-        float acc[RPS];
-        if constexpr (IPL_T > 0) {
-            typename QT::Raw raw[RPS][IPL_T];
-#pragma unroll
-            for (int r = 0; r < RPS; r++) {
-                const uint32_t v = v0 + r * nls;
-                if (v < n) {
-                    const uint8_t *rp = rowp(v);
-#pragma unroll
-                    for (int i = 0; i < IPL_T; i++) {
-                        const uint32_t item = s + S * i;
-                        raw[r][i] = QT::load(rp + (item / QT::IPB) * QT::BB, item % QT::IPB);
-                    }
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < RPS; r++) {
-                const uint32_t v = v0 + r * nls;
-                float x = 0.0f;
-                if (v < n) {
-                    const Act act = actp(v);
-#pragma unroll
-                    for (int i = 0; i < IPL_T; i++) {
-                        const uint32_t item = s + S * i;
-                        x += QT::dot_q8(raw[r][i], item % QT::IPB, act, item / QT::IPB);
-                    }
-                }
-                acc[r] = x;
-            }
-        } else {
-#pragma unroll
-            for (int r = 0; r < RPS; r++) {
-                const uint32_t v = v0 + r * nls;
-                float x = 0.0f;
-                if (v < n) {
-                    const uint8_t *rp = rowp(v);
-                    const Act act = actp(v);
-                    for (uint32_t i = 0; i < ipl_rt; i++) {
-                        const uint32_t item = s + S * i;
-                        x += QT::dot_q8(QT::load(rp + (item / QT::IPB) * QT::BB, item % QT::IPB), item % QT::IPB,
-                                        act, item / QT::IPB);
-                    }
-                }
-                acc[r] = x;
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < RPS; r++) {
-            const float x = wave_sum_xor(acc[r], (int)S);
-            const uint32_t v = v0 + r * nls;
-            if (s == 0 && v < n) out(v, x);
-        }
+// Workgroup 0 of kernel A: weights (when routing from logits), the routing
+// scratch for kernel B, the optional routing outputs, and the error bit.
+__device__ void route_publish(const MoeArgs &a, const Route *rt, const float *lg) {
+    if (threadIdx.x != 0) return;
+    int32_t ids[MAX_SEL];
+    bool bad = false;
+    for (int r = 0; r < a.n_sel; r++) {
+        const int32_t e = rt->ids[r];
+        bad |= e < 0 || (uint32_t)e >= a.n_expert;
+        ids[r] = e;
     }
+    float sum = 0.0f;
+    if (a.logits) {
+        // two passes over the same exp values: the rank-order sum, then the
+        // quotients
+        const float lmax = lg[ids[0]];
+        for (int r = 0; r < a.n_sel; r++) sum += kq_expf(lg[ids[r]] - lmax);
+    }
+    for (int r = 0; r < MAX_SLOTS; r++) {
+        int32_t e = -1;
+        float w = 0.0f;
+        if (r < a.n_sel) {
+            e = ids[r];
+            w = a.logits ? kq_expf(lg[e] - lg[ids[0]]) / sum : rt->w[r];
+            if (a.ids_out) a.ids_out[r] = e;
+            if (a.wts_out) a.wts_out[r] = w;
+        } else if (r == a.n_sel && a.has_shared) {
+            w = 1.0f;
+        }
+        a.route_ids[r] = (r < a.n_sel && (uint32_t)e >= a.n_expert) ? 0 : e;   // addressing stays in the pool
+        a.route_w[r] = w;
+    }
+    if (bad) atomicOr(a.err, 2);
 }
 
-struct Geo {
-    uint32_t log2s_a, ipl_a;   // gate/up rows (hidden columns)
-    uint32_t log2s_b, ipl_b;   // down rows (ffn columns)
-    uint64_t rb_g, rb_u, rb_d;
-    uint32_t n_slots, units_a, tile_b, units_b;
+// Sum R per-lane values over the 64 lanes of a wave for R rows at once: each
+// halving step sends the half of the rows the partner keeps (R/2 shuffles),
+// then the remaining offsets finish a plain butterfly. Afterwards every lane
+// holds the full sum of row (lane >> (6 - log2 R)) & (R - 1).
+template <int N, int OFF, int R>
+__device__ __forceinline__ void reduce_halve(float (&acc)[R], int lane) {
+    if constexpr (N > 1) {
+        constexpr int HALF = N / 2;
+        const bool upper = lane & OFF;
+#pragma unroll
+        for (int i = 0; i < HALF; i++) {
+            const float send = upper ? acc[i] : acc[i + HALF];
+            const float keep = upper ? acc[i + HALF] : acc[i];
+            acc[i] = keep + __shfl_xor(send, OFF, WAVE);
+        }
+        reduce_halve<HALF, OFF / 2, R>(acc, lane);
+    }
+}
+template <int R>
+__device__ __forceinline__ float reduce_rows(float (&acc)[R]) {
+    const int lane = threadIdx.x & 63;
+    reduce_halve<R, 32, R>(acc, lane);
+    constexpr int LOG = R >= 16 ? 4 : (R >= 8 ? 3 : (R >= 4 ? 2 : (R >= 2 ? 1 : 0)));
+    float v = acc[0];
+#pragma unroll
+    for (int off = 32 >> LOG; off > 0; off >>= 1) v += __shfl_xor(v, off, WAVE);
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// Kernel A: 64 Q4_K rows (32 gate + 32 up) per workgroup, NB blocks per row.
+// Wave w owns rows 16w..16w+15 (waves 0-1 gate, 2-3 up). Lane l always takes
+// the same lane item of every row it touches, so its activation slice (two
+// 16-byte q8 chunks, their scales and half-block sums) is read from LDS once:
+//   ITEMS = 8*NB >= 64: the k-th chunk is item 64*(k % M) + l of row k / M
+//                       (M = ITEMS/64 slices per lane);
+//   ITEMS < 64:         64/ITEMS rows share a wave instruction; the k-th
+//                       chunk is item l % ITEMS of row l / ITEMS + k*64/ITEMS.
+// Block headers are decoded once per (row, block) into LDS as
+// {d*sc[2g], d*sc[2g+1], dmin*m[2g], dmin*m[2g+1]} per group g.
+// ---------------------------------------------------------------------------
+struct LdsA {
+    uint32_t route, logits, xact, scl, gu, total;
 };
+__host__ __device__ inline LdsA lds_a(uint32_t hidden, uint32_t nb) {
+    LdsA L;
+    L.route = 0;
+    L.logits = 256;
+    L.xact = L.logits + MAX_EXPERT * 4;
+    L.scl = L.xact + act_bytes(hidden);
+    L.gu = L.scl + 64 * nb * 64;
+    L.total = L.gu + 64 * 4;
+    return L;
+}
 
-template <class QG, class QU, int IPL_A>
-__device__ void phase_a(const MoeArgs &a, const Geo &g, const Route *rt, const Act &xa, float *gu, uint32_t unit) {
+// the activation side of one lane item (constant over rows)
+struct XSlice {
+    int4 xl, xh;
+    float d8lo, d8hi, qlo, qhi;
+};
+__device__ __forceinline__ XSlice x_slice(const Act &xa, uint32_t it) {
+    const uint32_t b = it / 8, c = it % 8, g = c >> 1, hh = c & 1;
+    const int8_t *al = xa.qs + 256 * b + 64 * g + 16 * hh;
+    XSlice x;
+    x.xl = *(const int4 *)al;
+    x.xh = *(const int4 *)(al + 32);
+    const uint32_t k = 8 * b + 2 * g;
+    x.d8lo = xa.d8[k];
+    x.d8hi = xa.d8[k + 1];
+    x.qlo = (float)xa.qs16[2 * k + hh];
+    x.qhi = (float)xa.qs16[2 * k + 2 + hh];
+    return x;
+}
+// same arithmetic as Q4K::dot_q8, with the scales pre-decoded
+__device__ __forceinline__ float item_dot(const uint4 &q, const float4 &sc, const XSlice &x) {
+    int slo, shi;
+    Q4K::isums_x(q, x.xl, x.xh, slo, shi);
+    const float vlo = fmaf(sc.x, (float)slo, -(sc.z * x.qlo));
+    const float vhi = fmaf(sc.y, (float)shi, -(sc.w * x.qhi));
+    return fmaf(x.d8lo, vlo, x.d8hi * vhi);
+}
+
+template <int NB>
+__global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
+    constexpr int ITEMS = 8 * NB;              // lane items per row
+    constexpr int LPL = 2 * NB;                // 16 rows x ITEMS / 64 lanes
+    constexpr int GROUPS = LPL > 16 ? LPL / 16 : 1;
+    constexpr int RPG = 16 / GROUPS;           // rows per group
+    constexpr int LPG = RPG * ITEMS / 64;      // chunks per lane per group
+    constexpr int M = ITEMS >= 64 ? ITEMS / 64 : 1;   // activation slices per lane
+    constexpr int LOG_RPG = RPG == 16 ? 4 : (RPG == 8 ? 3 : (RPG == 4 ? 2 : (RPG == 2 ? 1 : 0)));
+    extern __shared__ __align__(16) uint8_t lds[];
+    const LdsA L = lds_a(a.hidden, NB);
+    Route *rt = (Route *)(lds + L.route);
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t nblk = a.ffn / 32;
-    const uint32_t slot = unit / nblk, jb = unit % nblk;
+    const uint32_t slot = blockIdx.x / nblk, jb = blockIdx.x % nblk;
+
+    // logits, then x (fp32), into registers; their latency overlaps
+    float lv[LPT];
+    load_logits(a, lv);
+    constexpr int XTASKS = 64 * NB;            // quantizer lane tasks (8 per 32-block)
+    constexpr int XPT = (XTASKS + 255) / 256;
+    float4 xv[XPT];
+    if (a.xq == nullptr) {
+#pragma unroll
+        for (int i = 0; i < XPT; i++)
+            if (tid + 256 * i < XTASKS) xv[i] = *(const float4 *)(a.x + 4 * (tid + 256 * i));
+    }
+    route_rank(a, rt, (float *)(lds + L.logits), lv);
+
+    const uint64_t rb = NB * 144;
     const uint8_t *gb, *ub;
     if ((int)slot < a.n_sel) {
-        const uint64_t e = (uint64_t)rt->ids[slot];
-        gb = a.gate + e * a.ffn * g.rb_g;
-        ub = a.up + e * a.ffn * g.rb_u;
+        int32_t id = rt->ids[slot];
+        if ((uint32_t)id >= a.n_expert) id = 0;   // bad explicit id: reported by workgroup 0
+        const uint64_t e = (uint64_t)id;
+        gb = a.gate + e * a.ffn * rb;
+        ub = a.up + e * a.ffn * rb;
     } else {
         gb = a.gate_sh;
         ub = a.up_sh;
     }
-    auto act = [&](uint32_t) -> Act { return xa; };
-    auto out = [&](uint32_t v, float x) { gu[v] = x; };
-    constexpr int RPS = IPL_A == 1 ? 4 : (IPL_A == 2 ? 2 : 1);
-    if constexpr (QG::TYPE == QU::TYPE) {
-        auto rowp = [&](uint32_t v) -> const uint8_t * {
-            return v < 32 ? gb + (uint64_t)(32 * jb + v) * g.rb_g : ub + (uint64_t)(32 * jb + v - 32) * g.rb_u;
-        };
-        rows_dot<QG, IPL_A, RPS>(64, g.log2s_a, g.ipl_a, rowp, act, out);
+    auto row_ptr = [&](uint32_t v) -> const uint8_t * {   // v in [0, 64)
+        return v < 32 ? gb + (uint64_t)(32 * jb + v) * rb : ub + (uint64_t)(32 * jb + v - 32) * rb;
+    };
+    auto chunk = [&](int grp, int k) -> const uint8_t * {
+        uint32_t r, it;
+        if constexpr (ITEMS >= 64) {
+            r = grp * RPG + k / M;
+            it = 64 * (k % M) + lane;
+        } else {
+            r = lane / ITEMS + k * (64 / ITEMS);
+            it = lane % ITEMS;
+        }
+        return row_ptr(16 * wave + r) + (it / 8) * 144 + 16 + 16 * (it % 8);
+    };
+
+    // all weight loads: block headers first (consumed first), then chunks
+    constexpr int HPT = (64 * NB + 255) / 256;
+    uint4 hv[HPT];
+#pragma unroll
+    for (int i = 0; i < HPT; i++) {
+        const uint32_t h = tid + 256 * i;
+        if (h < 64 * NB) hv[i] = ld16(row_ptr(h / NB) + (h % NB) * 144);
+    }
+    uint4 q[LPG];
+#pragma unroll
+    for (int k = 0; k < LPG; k++) q[k] = ld16(chunk(0, k));
+
+    // quantize x into LDS while the weights stream in
+    const Act xa = act_carve(lds + L.xact, a.hidden);
+    if (a.xq) {
+        act_stage_from_q8(a.xq, a.hidden, xa);
     } else {
-        auto rg = [&](uint32_t v) -> const uint8_t * { return gb + (uint64_t)(32 * jb + v) * g.rb_g; };
-        auto ru = [&](uint32_t v) -> const uint8_t * { return ub + (uint64_t)(32 * jb + v) * g.rb_u; };
-        auto ou = [&](uint32_t v, float x) { gu[32 + v] = x; };
-        rows_dot<QG, 0, 1>(32, g.log2s_a, g.ipl_a, rg, act, out);
-        rows_dot<QU, 0, 1>(32, g.log2s_a, g.ipl_a, ru, act, ou);
+#pragma unroll
+        for (int i = 0; i < XPT; i++) {
+            const uint32_t t = tid + 256 * i, blk = t >> 3, part = t & 7;
+            if (t >= XTASKS) break;
+            uint32_t d16, s16;
+            int lo, hi;
+            float dd;
+            const uint32_t qv = quant_q8_1_part(xv[i], d16, s16, lo, hi, dd);
+            *(uint32_t *)(xa.qs + 32 * blk + 4 * part) = qv;
+            if (part == 0) {
+                xa.d8[blk] = dd;
+                xa.qs16[2 * blk] = lo;
+                xa.qs16[2 * blk + 1] = hi;
+            }
+        }
+    }
+    // decode the 64*NB block headers into per-group scale quadruples
+    float4 *scl = (float4 *)(lds + L.scl);
+#pragma unroll
+    for (int i = 0; i < HPT; i++) {
+        const uint32_t h = tid + 256 * i;
+        if (h < 64 * NB) {
+            Q4K::Raw raw;
+            raw.h = hv[i];
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                float4 v;
+                Q4K::scales(raw, g, v.x, v.y, v.z, v.w);
+                scl[4 * h + g] = v;
+            }
+        }
     }
     __syncthreads();
-    if (threadIdx.x < 8) {
-        const uint32_t part = threadIdx.x, i0 = 4 * part;
+
+    XSlice xs[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) xs[m] = x_slice(xa, ITEMS >= 64 ? 64 * m + lane : lane % ITEMS);
+    float *gu = (float *)(lds + L.gu);
+#pragma unroll
+    for (int grp = 0; grp < GROUPS; grp++) {
+        if (grp > 0) {
+#pragma unroll
+            for (int k = 0; k < LPG; k++) q[k] = ld16(chunk(grp, k));
+        }
+        if constexpr (ITEMS >= 64) {
+            float acc[RPG];
+#pragma unroll
+            for (int r = 0; r < RPG; r++) acc[r] = 0.0f;
+#pragma unroll
+            for (int k = 0; k < LPG; k++) {
+                const uint32_t it = 64 * (k % M) + lane;
+                const uint32_t row = 16 * wave + grp * RPG + k / M;
+                const float4 sc = scl[4 * (row * NB + it / 8) + (it % 8) / 2];
+                acc[k / M] += item_dot(q[k], sc, xs[k % M]);
+            }
+            const float v = reduce_rows<RPG>(acc);
+            constexpr int SH = 6 - LOG_RPG;
+            const uint32_t r = (lane >> SH) & (RPG - 1);
+            if ((lane & ((1u << SH) - 1)) == 0) gu[16 * wave + grp * RPG + r] = v;
+        } else {
+            const uint32_t it = lane % ITEMS;
+#pragma unroll
+            for (int k = 0; k < LPG; k++) {
+                const uint32_t row = 16 * wave + lane / ITEMS + k * (64 / ITEMS);
+                const float4 sc = scl[4 * (row * NB + it / 8) + (it % 8) / 2];
+                const float v = group_sum<ITEMS>(item_dot(q[k], sc, xs[0]));
+                if (it == 0) gu[row] = v;
+            }
+        }
+    }
+    __syncthreads();
+
+    if (tid < 8) {
+        const uint32_t i0 = 4 * tid;
         float4 h;
         h.x = kq_silu_mul(gu[i0 + 0], gu[32 + i0 + 0]);
         h.y = kq_silu_mul(gu[i0 + 1], gu[32 + i0 + 1]);
@@ -214,217 +370,198 @@ __device__ void phase_a(const MoeArgs &a, const Geo &g, const Route *rt, const A
         uint32_t d16, s16;
         int lo, hi;
         float dd;
-        const uint32_t q = quant_q8_1_part(h, d16, s16, lo, hi, dd);
+        const uint32_t qv = quant_q8_1_part(h, d16, s16, lo, hi, dd);
         uint8_t *blk = a.hq8 + ((uint64_t)slot * nblk + jb) * 36;
-        *(uint32_t *)(blk + 4 + 4 * part) = q;
-        if (part == 0) *(uint32_t *)blk = d16 | (s16 << 16);
+        *(uint32_t *)(blk + 4 + 4 * tid) = qv;
+        if (tid == 0) *(uint32_t *)blk = d16 | (s16 << 16);
     }
-    if (a.dbg_gu && threadIdx.x < 64) {
-        const uint32_t v = threadIdx.x;
-        float *d = a.dbg_gu + (uint64_t)slot * 2 * a.ffn + (v < 32 ? 0 : a.ffn) + 32 * jb + (v & 31);
-        *d = gu[v];
+    if (a.dbg_gu && tid < 64) {
+        float *d = a.dbg_gu + (uint64_t)slot * 2 * a.ffn + (tid < 32 ? 0 : a.ffn) + 32 * jb + (tid & 31);
+        *d = gu[tid];
     }
+    if (blockIdx.x == 0) route_publish(a, rt, (const float *)(lds + L.logits));
 }
 
-template <class QD, int IPL_B>
-__device__ void phase_b(const MoeArgs &a, const Geo &g, const Route *rt, uint8_t *hl, float *res, uint32_t unit) {
-    const uint32_t nblk = a.ffn / 32;
-    const uint32_t row0 = unit * g.tile_b;
-    const uint32_t nrows = row0 + g.tile_b <= a.hidden ? g.tile_b : a.hidden - row0;
-    const uint32_t ab = act_bytes(a.ffn);
-    for (uint32_t sl = 0; sl < g.n_slots; sl++)
-        act_stage_from_q8(a.hq8 + (uint64_t)sl * nblk * 36, a.ffn, act_carve(hl + sl * ab, a.ffn));
-    __syncthreads();
-    const uint32_t ns = g.n_slots;
-    auto rowp = [&](uint32_t p) -> const uint8_t * {
-        const uint32_t r = p / ns, sl = p % ns;
-        const uint8_t *db = (int)sl < a.n_sel ? a.down + (uint64_t)rt->ids[sl] * a.hidden * g.rb_d : a.down_sh;
-        return db + (uint64_t)(row0 + r) * g.rb_d;
-    };
-    auto actp = [&](uint32_t p) -> Act { return act_carve(hl + (p % ns) * ab, a.ffn); };
-    auto out = [&](uint32_t p, float x) { res[p] = x; };
-    constexpr int RPS = IPL_B == 1 ? 2 : 1;
-    rows_dot<QD, IPL_B, RPS>(nrows * ns, g.log2s_b, g.ipl_b, rowp, actp, out);
-    __syncthreads();
-    for (uint32_t r = threadIdx.x; r < nrows; r += blockDim.x) {
-        float y = 0.0f;
-        for (uint32_t sl = 0; sl < ns; sl++) y = fmaf(rt->w[sl], res[r * ns + sl], y);
-        a.y[row0 + r] = y;
-    }
-}
-
-__device__ __forceinline__ void stage_x(const MoeArgs &a, const Act &xa) {
-    if (a.xq) act_stage_from_q8(a.xq, a.hidden, xa);
-    else act_stage_from_f32(a.x, a.hidden, xa);
-}
-
-// LDS layout (bytes): Route | x act | gu[64] | h acts | res
-struct LdsLayout {
-    uint32_t route, xact, gu, hacts, res, total;
+// ---------------------------------------------------------------------------
+// Kernel B: a tile of TR output rows x n_slots down rows per workgroup; one
+// lane-slot (S = QD::IPB lanes) per (row, slot) pair; every load issued before
+// the h activations are staged.
+// ---------------------------------------------------------------------------
+struct LdsB {
+    uint32_t route, hacts, res, total;
 };
-__host__ __device__ inline LdsLayout lds_layout(const MoeArgs &a, const Geo &g) {
-    LdsLayout L;
+__host__ __device__ inline LdsB lds_b(uint32_t ffn, uint32_t n_slots, uint32_t tr) {
+    LdsB L;
     L.route = 0;
-    L.xact = 256;
-    L.gu = L.xact + act_bytes(a.hidden);
-    L.hacts = L.gu + 64 * 4;
-    L.res = L.hacts + g.n_slots * act_bytes(a.ffn);
-    L.total = L.res + g.tile_b * g.n_slots * 4;
+    L.hacts = 256;
+    L.res = L.hacts + n_slots * act_bytes(ffn);
+    L.total = L.res + tr * n_slots * 4;
     return L;
 }
 
-template <class QG, class QU, int IPL_A>
-__global__ void __launch_bounds__(256) k_moe_a(MoeArgs a, Geo g) {
-    extern __shared__ __align__(16) uint8_t lds[];
-    const LdsLayout L = lds_layout(a, g);
-    Route *rt = (Route *)(lds + L.route);
-    route(a, rt);
-    const Act xa = act_carve(lds + L.xact, a.hidden);
-    stage_x(a, xa);
-    __syncthreads();
-    phase_a<QG, QU, IPL_A>(a, g, rt, xa, (float *)(lds + L.gu), blockIdx.x);
-}
-
-template <class QD, int IPL_B>
-__global__ void __launch_bounds__(256) k_moe_b(MoeArgs a, Geo g) {
-    extern __shared__ __align__(16) uint8_t lds[];
-    const LdsLayout L = lds_layout(a, g);
-    Route *rt = (Route *)(lds + L.route);
-    route(a, rt);
-    __syncthreads();
-    if (blockIdx.x == 0 && threadIdx.x < (uint32_t)a.n_sel) {
-        if (a.ids_out) a.ids_out[threadIdx.x] = rt->ids[threadIdx.x];
-        if (a.wts_out) a.wts_out[threadIdx.x] = rt->w[threadIdx.x];
-    }
-    phase_b<QD, IPL_B>(a, g, rt, lds + L.hacts, (float *)(lds + L.res), blockIdx.x);
-}
-
-template <class QG, class QU, class QD, int IPL_A, int IPL_B>
-__global__ void __launch_bounds__(256) k_moe_fused(MoeArgs a, Geo g) {
-    extern __shared__ __align__(16) uint8_t lds[];
-    const LdsLayout L = lds_layout(a, g);
-    Route *rt = (Route *)(lds + L.route);
-    route(a, rt);
-    const Act xa = act_carve(lds + L.xact, a.hidden);
-    stage_x(a, xa);
-    __syncthreads();
-    for (uint32_t u = blockIdx.x; u < g.units_a; u += gridDim.x) {
-        phase_a<QG, QU, IPL_A>(a, g, rt, xa, (float *)(lds + L.gu), u);
-        __threadfence();
-        __syncthreads();
-        if (threadIdx.x == 0) atomicAdd(&a.sync[0], 1u);
-    }
-    if (blockIdx.x == 0 && threadIdx.x < (uint32_t)a.n_sel) {
-        if (a.ids_out) a.ids_out[threadIdx.x] = rt->ids[threadIdx.x];
-        if (a.wts_out) a.wts_out[threadIdx.x] = rt->w[threadIdx.x];
-    }
-    __shared__ int ok;
-    if (threadIdx.x == 0) {
-        uint32_t spins = 0;
-        ok = 1;
-        while (__hip_atomic_load(&a.sync[0], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < g.units_a) {
-            __builtin_amdgcn_s_sleep(2);
-            if (++spins > SPIN_LIMIT) {
-                ok = 0;
-                atomicOr(a.err, 1);
-                break;
-            }
+// q8_1 h of every slot, staged from the scratch written by kernel A: 8 lanes
+// per 36-byte block (one dword of values each, lane 0 also the scale), loads
+// issued up front by load_h and finished by stage_h.
+constexpr int HT_MAX = 12;   // lane tasks per thread (n_slots * ffn/32 * 8 / blockDim)
+struct HLoad {
+    uint32_t q[HT_MAX];
+    uint32_t d[HT_MAX];
+};
+__device__ __forceinline__ void load_h(const uint8_t *hq8, uint32_t ntask, uint32_t first, HLoad &h) {
+#pragma unroll
+    for (int i = 0; i < HT_MAX; i++) {
+        const uint32_t t = first + threadIdx.x + blockDim.x * i;
+        if (t < ntask) {
+            const uint8_t *b = hq8 + (t >> 3) * 36;
+            h.q[i] = *(const uint32_t *)(b + 4 + 4 * (t & 7));
+            h.d[i] = ld_u16(b);
         }
     }
-    __syncthreads();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    if (ok) {
-        for (uint32_t u = blockIdx.x; u < g.units_b; u += gridDim.x)
-            phase_b<QD, IPL_B>(a, g, rt, lds + L.hacts, (float *)(lds + L.res), u);
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        __threadfence();
-        const uint32_t done = atomicAdd(&a.sync[1], 1u);
-        if (done == gridDim.x - 1) {
-            __hip_atomic_store(&a.sync[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&a.sync[1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __threadfence();
+}
+__device__ __forceinline__ void stage_h(uint8_t *hl, uint32_t ffn, uint32_t ntask, uint32_t first, const HLoad &h) {
+    const uint32_t nblk = ffn / 32, ab = act_bytes(ffn);
+#pragma unroll
+    for (int i = 0; i < HT_MAX; i++) {
+        const uint32_t t = first + threadIdx.x + blockDim.x * i;
+        if (t >= ntask) break;   // whole 8-lane groups leave together
+        const uint32_t blk = t >> 3, part = t & 7, slot = blk / nblk, kb = blk % nblk;
+        const Act act = act_carve(hl + slot * ab, ffn);
+        *(uint32_t *)(act.qs + 32 * kb + 4 * part) = h.q[i];
+        int s = dot4(h.q[i], 0x01010101u, 0);
+        s += dpp_i<DPP_XOR1>(s);
+        s += dpp_i<DPP_XOR2>(s);
+        const int other = dpp_i<DPP_HALF_MIRROR>(s);
+        if (part == 0) {
+            act.d8[kb] = h2f(h.d[i]);
+            act.qs16[2 * kb] = s;
+            act.qs16[2 * kb + 1] = other;
         }
     }
 }
 
-uint64_t moe_sync_words() { return 64; }
-
-static int ilog2u(uint32_t v) {
-    int l = 0;
-    while ((1u << (l + 1)) <= v) l++;
-    return l;
-}
-static uint32_t lanes_for(uint32_t items) {
-    uint32_t s = 64;
-    while (s > 1 && items % s) s >>= 1;
-    return s;
-}
-static uint32_t block_bytes(uint32_t t) { return t == T_Q4_K ? 144 : 210; }
-static uint32_t ipb(uint32_t t) { return t == T_Q4_K ? 8 : 4; }
-
-template <class QG, class QU, class QD, int IPL_A, int IPL_B>
-static hipError_t moe_go(const MoeArgs &a, const Geo &g, int mode, hipStream_t s, int *grid_out) {
-    const LdsLayout L = lds_layout(a, g);
-    if (mode == 0) {
-        hipLaunchKernelGGL((k_moe_a<QG, QU, IPL_A>), dim3(g.units_a), dim3(256), L.total, s, a, g);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        hipLaunchKernelGGL((k_moe_b<QD, IPL_B>), dim3(g.units_b), dim3(256), L.total, s, a, g);
-        if (grid_out) *grid_out = (int)g.units_b;
-        return hipGetLastError();
+template <class QD, int IPL>
+__global__ void __launch_bounds__(256) k_moe_down(MoeArgs a, uint32_t tr, uint32_t n_slots) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const LdsB L = lds_b(a.ffn, n_slots, tr);
+    Route *rt = (Route *)(lds + L.route);
+    const uint32_t tid = threadIdx.x;
+    // h loads first (they do not depend on the routing), then the routing
+    const uint32_t ntask = n_slots * (a.ffn / 32) * 8;
+    HLoad hv;
+    load_h(a.hq8, ntask, 0, hv);
+    int32_t rid = 0;
+    float rw = 0.0f;
+    if (tid < MAX_SLOTS) {
+        rid = a.route_ids[tid];
+        rw = a.route_w[tid];
     }
-    auto kern = k_moe_fused<QG, QU, QD, IPL_A, IPL_B>;
-    const int cus = device_cu_count();
-    int per_cu = 0;
-    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)kern, 256, L.total);
-    if (e != hipSuccess) return e;
-    if (per_cu < 1) return hipErrorInvalidConfiguration;
-    const uint32_t cap = (uint32_t)(per_cu * cus);
-    uint32_t want = g.units_a > g.units_b ? g.units_a : g.units_b;
-    const uint32_t grid = want < cap ? want : cap;
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), L.total, s, a, g);
-    if (grid_out) *grid_out = (int)grid;
+    if (tid < MAX_SLOTS) {
+        rt->ids[tid] = rid;
+        rt->w[tid] = rw;
+    }
+    __syncthreads();
+    const uint32_t S = QD::IPB;
+    const uint32_t ls = tid / S, s = tid % S;
+    const uint32_t row0 = blockIdx.x * tr;
+    const uint32_t nrows = row0 + tr <= a.hidden ? tr : a.hidden - row0;
+    const uint32_t npairs = nrows * n_slots;
+    const uint64_t rbd = (uint64_t)(a.ffn / 256) * QD::BB;
+    const uint32_t ipl = a.ffn / 256;
+    typename QD::Raw raw[IPL > 0 ? IPL : 1];
+    const bool active = ls < npairs;
+    uint32_t sl = 0;
+    const uint8_t *rp = nullptr;
+    if (active) {
+        const uint32_t r = ls / n_slots;
+        sl = ls % n_slots;
+        const uint8_t *db = (int)sl < a.n_sel ? a.down + (uint64_t)rt->ids[sl] * a.hidden * rbd : a.down_sh;
+        rp = db + (uint64_t)(row0 + r) * rbd;
+        if constexpr (IPL > 0) {
+#pragma unroll
+            for (int i = 0; i < IPL; i++) raw[i] = QD::load(rp + i * QD::BB, (int)s);
+        }
+    }
+    stage_h(lds + L.hacts, a.ffn, ntask, 0, hv);
+    for (uint32_t first = HT_MAX * blockDim.x; first < ntask; first += HT_MAX * blockDim.x) {
+        load_h(a.hq8, ntask, first, hv);   // only for n_slots * ffn > 12288
+        stage_h(lds + L.hacts, a.ffn, ntask, first, hv);
+    }
+    __syncthreads();
+    float x = 0.0f;
+    if (active) {
+        const Act act = act_carve(lds + L.hacts + sl * act_bytes(a.ffn), a.ffn);
+        if constexpr (IPL > 0) {
+#pragma unroll
+            for (int i = 0; i < IPL; i++) x += QD::dot_q8(raw[i], (int)s, act, i);
+        } else {
+            for (uint32_t i = 0; i < ipl; i++) x += QD::dot_q8(QD::load(rp + i * QD::BB, (int)s), (int)s, act, i);
+        }
+    }
+    x = group_sum<QD::IPB>(x);
+    float *res = (float *)(lds + L.res);
+    if (active && s == 0) res[ls] = x;
+    __syncthreads();
+    for (uint32_t i = tid; i < nrows; i += blockDim.x) {
+        float y = 0.0f;
+        for (uint32_t k = 0; k < n_slots; k++) y = fmaf(rt->w[k], res[i * n_slots + k], y);
+        a.y[row0 + i] = y;
+    }
+}
+
+uint64_t moe_route_words() { return 2 * MAX_SLOTS; }
+
+template <int NB>
+static hipError_t go_a(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
+    const LdsA L = lds_a(a.hidden, NB);
+    hipLaunchKernelGGL(k_moe_gu<NB>, dim3(n_slots * (a.ffn / 32)), dim3(256), L.total, s, a);
     return hipGetLastError();
 }
 
-template <class QG, class QU, class QD>
-static hipError_t moe_ipl(const MoeArgs &a, const Geo &g, int mode, hipStream_t s, int *grid_out) {
-    const uint32_t ia = g.ipl_a, ib = g.ipl_b;
-    if (ia == 1 && ib == 3) return moe_go<QG, QU, QD, 1, 3>(a, g, mode, s, grid_out);
-    if (ia == 1 && ib == 1) return moe_go<QG, QU, QD, 1, 1>(a, g, mode, s, grid_out);
-    if (ia == 2 && ib == 1) return moe_go<QG, QU, QD, 2, 1>(a, g, mode, s, grid_out);
-    if (ia == 2 && ib == 3) return moe_go<QG, QU, QD, 2, 3>(a, g, mode, s, grid_out);
-    return moe_go<QG, QU, QD, 0, 0>(a, g, mode, s, grid_out);
+template <class QD, int IPL>
+static hipError_t go_b(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
+    const uint32_t lane_slots = 256 / QD::IPB;
+    uint32_t tr = lane_slots / n_slots;
+    if (tr < 1) tr = 1;
+    const LdsB L = lds_b(a.ffn, n_slots, tr);
+    hipLaunchKernelGGL((k_moe_down<QD, IPL>), dim3((a.hidden + tr - 1) / tr), dim3(256), L.total, s, a, tr, n_slots);
+    return hipGetLastError();
 }
 
-hipError_t launch_moe(const MoeArgs &a, int mode, hipStream_t s, int *grid_out) {
-    Geo g;
-    const uint32_t items_a = a.hidden / 256 * ipb(a.gate_type);
-    const uint32_t sa = lanes_for(items_a);
-    g.log2s_a = ilog2u(sa);
-    g.ipl_a = items_a / sa;
-    const uint32_t items_b = a.ffn / 256 * ipb(a.down_type);
-    const uint32_t sb = lanes_for(items_b);
-    g.log2s_b = ilog2u(sb);
-    g.ipl_b = items_b / sb;
-    g.rb_g = (uint64_t)a.hidden / 256 * block_bytes(a.gate_type);
-    g.rb_u = (uint64_t)a.hidden / 256 * block_bytes(a.up_type);
-    g.rb_d = (uint64_t)a.ffn / 256 * block_bytes(a.down_type);
-    g.n_slots = (uint32_t)a.n_sel + (a.has_shared ? 1u : 0u);
-    g.units_a = g.n_slots * (a.ffn / 32);
-    const uint32_t lane_slots = 4 * (64 / sb);
-    uint32_t tile = lane_slots / g.n_slots;
-    if (tile < 1) tile = 1;
-    g.tile_b = tile;
-    g.units_b = (a.hidden + tile - 1) / tile;
-    const bool g4 = a.gate_type == T_Q4_K, u4 = a.up_type == T_Q4_K, d4 = a.down_type == T_Q4_K;
-    if (g4 && u4 && !d4) return moe_ipl<Q4K, Q4K, Q6K>(a, g, mode, s, grid_out);
-    if (g4 && u4 && d4) return moe_ipl<Q4K, Q4K, Q4K>(a, g, mode, s, grid_out);
-    if (!g4 && !u4 && !d4) return moe_ipl<Q6K, Q6K, Q6K>(a, g, mode, s, grid_out);
-    if (!g4 && !u4 && d4) return moe_ipl<Q6K, Q6K, Q4K>(a, g, mode, s, grid_out);
-    return hipErrorInvalidValue;   // mixed gate/up types are not instantiated
+bool moe_shape_supported(uint32_t gate_type, uint32_t down_type, uint32_t hidden, uint32_t ffn) {
+    if (gate_type != T_Q4_K || (down_type != T_Q4_K && down_type != T_Q6_K)) return false;
+    const uint32_t nb = hidden / 256;
+    if (hidden % 256 || !(nb == 1 || nb == 2 || nb == 4 || nb == 8 || nb == 16)) return false;
+    return ffn % 256 == 0 && ffn >= 256;
+}
+
+hipError_t launch_moe(const MoeArgs &a, hipStream_t s) {
+    const uint32_t n_slots = (uint32_t)a.n_sel + (a.has_shared ? 1u : 0u);
+    hipError_t e;
+    switch (a.hidden / 256) {
+        case 1: e = go_a<1>(a, n_slots, s); break;
+        case 2: e = go_a<2>(a, n_slots, s); break;
+        case 4: e = go_a<4>(a, n_slots, s); break;
+        case 8: e = go_a<8>(a, n_slots, s); break;
+        case 16: e = go_a<16>(a, n_slots, s); break;
+        default: return hipErrorInvalidValue;
+    }
+    if (e != hipSuccess) return e;
+    const uint32_t nbd = a.ffn / 256;
+    if (a.down_type == T_Q6_K) {
+        switch (nbd) {
+            case 1: return go_b<Q6K, 1>(a, n_slots, s);
+            case 2: return go_b<Q6K, 2>(a, n_slots, s);
+            case 3: return go_b<Q6K, 3>(a, n_slots, s);
+            case 4: return go_b<Q6K, 4>(a, n_slots, s);
+            default: return go_b<Q6K, 0>(a, n_slots, s);
+        }
+    }
+    switch (nbd) {
+        case 1: return go_b<Q4K, 1>(a, n_slots, s);
+        case 2: return go_b<Q4K, 2>(a, n_slots, s);
+        case 3: return go_b<Q4K, 3>(a, n_slots, s);
+        default: return go_b<Q4K, 0>(a, n_slots, s);
+    }
 }
 
 }  // namespace kq

@@ -51,8 +51,6 @@ SIGNATURES = {
     "katali_hip_event_record": (C.c_int, [_vp]),
     "katali_hip_event_elapsed": (C.c_int, [_vp, _vp, C.POINTER(_f32)]),
     "katali_hip_event_destroy": (C.c_int, [_vp]),
-    "katali_hip_set_option": (C.c_int, [C.c_char_p, _i64]),
-    "katali_hip_get_option": (_i64, [C.c_char_p]),
     "katali_hip_selftest": (C.c_int, [C.c_char_p, _sz]),
     "katali_hip_synth_fill": (C.c_int, [_u32, _vp, _u64, _u64, _f32]),
     "katali_hip_synth_normal": (C.c_int, [_vp, _u64, _u64, _f32]),
@@ -156,12 +154,6 @@ class KataliHip:
 
     def sync(self) -> None:
         self.check(self.lib.katali_hip_sync())
-
-    def set_option(self, name: str, value: int) -> None:
-        self.check(self.lib.katali_hip_set_option(name.encode(), int(value)))
-
-    def get_option(self, name: str) -> int:
-        return int(self.lib.katali_hip_get_option(name.encode()))
 
     # -- compute ----------------------------------------------------------
     def quantize_q8_1(self, x: DeviceBuffer, n: int, out: DeviceBuffer) -> None:

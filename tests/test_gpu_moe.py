@@ -9,8 +9,8 @@ Stage by stage against the oracle on the same inputs:
     h, and against the oracle's end-to-end q8 path whenever no h block
     quantized differently (a 1-ulp gate/up difference can move one q8 value
     across a rounding boundary; the test counts such blocks).
-Also: one-launch vs two-launch modes bit-identical, repeat launches bit-
-identical, graph replays equal to eager runs, bad arguments refused.
+Also: repeat launches bit-identical, graph replays equal to eager runs, bad
+arguments refused.
 """
 import numpy as np
 import pytest
@@ -75,8 +75,7 @@ def moes(hip, oracle):
     return get
 
 
-def run_layer(hip, m, x, n_sel, mode, logits=None, ids=None, w=None):
-    hip.set_option("moe_mode", mode)
+def run_layer(hip, m, x, n_sel, logits=None, ids=None, w=None):
     n_slots = n_sel + m.n_slots_extra
     y = hip.alloc(m.hidden * 4)
     gu = hip.alloc(n_slots * 2 * m.ffn * 4)
@@ -94,17 +93,16 @@ def run_layer(hip, m, x, n_sel, mode, logits=None, ids=None, w=None):
 
 
 @pytest.mark.parametrize("case", CASES, ids=[f"h{c[0]}_f{c[1]}_e{c[2]}_k{c[3]}{'_sh' if c[4] else ''}{'_q4down' if c[5] == Q4_K else ''}" for c in CASES])
-@pytest.mark.parametrize("mode", [0, 1])
-def test_moe_layer_parity(hip, oracle, moes, case, mode):
+def test_moe_layer_parity(hip, oracle, moes, case):
     hidden, ffn, n_expert, n_sel, shared, down_type = case
-    print(f"[moe] case={case} mode={mode}", flush=True)
+    print(f"[moe] case={case}", flush=True)
     m = moes(hidden, ffn, n_expert, shared, down_type)
-    rng = np.random.default_rng(hidden + ffn + n_sel + mode)
+    rng = np.random.default_rng(hidden + ffn + n_sel)
     x = S.activation(rng, hidden)
     logits = rng.standard_normal(n_expert).astype(np.float32)
     ids, w = oracle.router_topk(logits, n_sel)
 
-    y, gu, hq, ido, wo = run_layer(hip, m, x, n_sel, mode, logits=logits)
+    y, gu, hq, ido, wo = run_layer(hip, m, x, n_sel, logits=logits)
     # routing: same experts, bit-identical weights
     assert ido.tolist() == ids.tolist()
     assert np.array_equal(wo.view(np.uint32), w.view(np.uint32))
@@ -128,28 +126,27 @@ def test_moe_layer_parity(hip, oracle, moes, case, mode):
     assert rf < 3e-2
 
     # explicit ids/weights give the same bits as in-kernel routing
-    y2, *_ = run_layer(hip, m, x, n_sel, mode, ids=ids, w=w)
+    y2, *_ = run_layer(hip, m, x, n_sel, ids=ids, w=w)
     assert np.array_equal(y2.view(np.uint32), y.view(np.uint32))
 
 
 @pytest.mark.parametrize("case", CASES[:2], ids=["e128_k8", "e256_k8_sh"])
-def test_moe_modes_identical_and_repeatable(hip, oracle, moes, case):
+def test_moe_repeatable(hip, oracle, moes, case):
     hidden, ffn, n_expert, n_sel, shared, down_type = case
     m = moes(hidden, ffn, n_expert, shared, down_type)
     rng = np.random.default_rng(5)
     x = S.activation(rng, hidden)
     logits = rng.standard_normal(n_expert).astype(np.float32)
-    outs = [run_layer(hip, m, x, n_sel, mode, logits=logits)[0] for mode in (0, 1, 1, 0, 1)]
+    outs = [run_layer(hip, m, x, n_sel, logits=logits)[0] for _ in range(4)]
     for o in outs[1:]:
         assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
 
 
-def test_moe_fused_back_to_back_launches(hip, oracle, moes):
-    """Many one-launch layers in a row: the in-kernel counters must reset
-    themselves after every launch."""
+def test_moe_back_to_back_layers(hip, oracle, moes):
+    """Many layers queued back to back sharing the scratch: every output is
+    the one its own inputs give."""
     hidden, ffn, n_expert, n_sel = 2048, 768, 128, 8
     m = moes(hidden, ffn, n_expert, False, Q6_K)
-    hip.set_option("moe_mode", 1)
     rng = np.random.default_rng(6)
     L = 24
     xs = [S.activation(rng, hidden) for _ in range(L)]
@@ -164,6 +161,8 @@ def test_moe_fused_back_to_back_launches(hip, oracle, moes):
         ids, w = oracle.router_topk(lg[i], n_sel)
         want = oracle.moe_layer_q8(m.odesc, xs[i], ids, w)
         assert rel_l2(ys[i].download(np.float32), want) <= 1e-3
+        y1, *_ = run_layer(hip, m, xs[i], n_sel, logits=lg[i])
+        assert np.array_equal(y1.view(np.uint32), ys[i].download(np.uint32))
 
 
 def test_moe_graph_replay_matches_eager(hip, oracle, moes):
@@ -172,7 +171,6 @@ def test_moe_graph_replay_matches_eager(hip, oracle, moes):
     run, with eager work and syncs between replays."""
     hidden, ffn, n_expert, n_sel = 2048, 512, 256, 8
     m = moes(hidden, ffn, n_expert, True, Q6_K)
-    hip.set_option("moe_mode", 1)
     rng = np.random.default_rng(7)
     steps, layers = 4, 2
     logits = rng.standard_normal((steps, layers, n_expert)).astype(np.float32)
