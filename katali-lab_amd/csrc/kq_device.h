@@ -35,7 +35,12 @@ __device__ __forceinline__ float h2f(uint32_t h16) {
     __builtin_memcpy(&h, &v, 2);
     return (float)h;
 }
+// f32 -> f16, round to nearest even, of the ROUNDED f32 value. The empty asm
+// pins f in a register: without it the compiler may fuse the producing
+// multiply into a mixed-precision FMA that rounds the exact product straight
+// to f16 (one rounding instead of two), which differs on f16 ties.
 __device__ __forceinline__ uint32_t f2h_rne(float f) {
+    asm("" : "+v"(f));
     const _Float16 h = (_Float16)f;   // v_cvt_f16_f32, round to nearest even
     uint16_t v;
     __builtin_memcpy(&v, &h, 2);
@@ -65,6 +70,10 @@ __device__ __forceinline__ float wave_sum_xor(float v, int width) {
     for (int o = width >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
     return v;
 }
+
+// s_waitcnt immediate for "vmcnt(0)" alone on gfx9: vmcnt in bits 3:0 and
+// 15:14 (0), expcnt 6:4 and lgkmcnt 11:8 at their maxima (no wait).
+constexpr int VMCNT0 = 0x0F70;
 
 // Lane exchanges inside aligned groups of 4 / 8 / 16 lanes on the VALU (DPP),
 // no LDS round trip: quad_perm [1,0,3,2] and [2,3,0,1] (partner = lane ^ 1,
@@ -193,6 +202,18 @@ __device__ __forceinline__ void act_stage_from_f32(const float *__restrict__ x, 
     }
 }
 
+// Half-block sums of a q8_1 block held as 4 values per lane over an aligned
+// 8-lane group: lo = values 0..15, hi = 16..31 (valid in all 8 lanes).
+__device__ __forceinline__ void q8_part_sums(uint32_t q, int &lo, int &hi) {
+    int s = dot4(q, 0x01010101u, 0);
+    s += dpp_i<DPP_XOR1>(s);
+    s += dpp_i<DPP_XOR2>(s);          // sum of this lane's half block (4 lanes)
+    const int other = dpp_i<DPP_HALF_MIRROR>(s);
+    const bool low = (threadIdx.x & 7) < 4;
+    lo = low ? s : other;
+    hi = low ? other : s;
+}
+
 // Stage K values of global q8_1 blocks into LDS.
 __device__ __forceinline__ void act_stage_from_q8(const uint8_t *__restrict__ xq, uint32_t K, Act a) {
     const uint32_t n = K / 32 * 8;
@@ -201,14 +222,12 @@ __device__ __forceinline__ void act_stage_from_q8(const uint8_t *__restrict__ xq
         const uint8_t *b = xq + 36 * blk;
         const uint32_t q = *(const uint32_t *)(b + 4 + 4 * part);
         *(uint32_t *)(a.qs + 32 * blk + 4 * part) = q;
-        int s = dot4(q, 0x01010101u, 0);
-        s += dpp_i<DPP_XOR1>(s);
-        s += dpp_i<DPP_XOR2>(s);
-        const int other = dpp_i<DPP_HALF_MIRROR>(s);
+        int lo, hi;
+        q8_part_sums(q, lo, hi);
         if (part == 0) {
             a.d8[blk] = h2f(ld_u16(b));
-            a.qs16[2 * blk] = s;
-            a.qs16[2 * blk + 1] = other;
+            a.qs16[2 * blk] = lo;
+            a.qs16[2 * blk + 1] = hi;
         }
     }
 }

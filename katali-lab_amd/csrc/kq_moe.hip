@@ -35,10 +35,6 @@ constexpr int MAX_SEL = 16;
 constexpr int MAX_SLOTS = MAX_SEL + 1;
 constexpr uint32_t MAX_EXPERT = 512;
 
-struct Route {
-    int32_t ids[MAX_SLOTS];
-    float w[MAX_SLOTS];
-};
 
 __device__ __forceinline__ const float *route_logits(const MoeArgs &a) {
     const float *l = a.logits;
@@ -46,146 +42,236 @@ __device__ __forceinline__ const float *route_logits(const MoeArgs &a) {
     return l;
 }
 
-// Block-wide routing into LDS: the selected ids (and, for explicit routing,
-// the given weights). `lg` is an LDS scratch of n_expert floats rounded up to
-// a multiple of 4 (padding ranks last) that keeps the logits for
-// route_publish. Every thread must already have issued `lv` = its logit loads
-// (see load_logits) so the global latency overlaps other loads. Ends with a
-// barrier.
-constexpr int LPT = MAX_EXPERT / 256;   // logits per thread
-__device__ __forceinline__ void load_logits(const MoeArgs &a, float (&lv)[LPT]) {
-    const float *src = a.logits ? route_logits(a) : nullptr;
-#pragma unroll
-    for (int i = 0; i < LPT; i++) {
-        const uint32_t e = threadIdx.x + 256 * i;
-        lv[i] = (src && e < a.n_expert) ? src[e] : -INFINITY;
-    }
+// ---------------------------------------------------------------------------
+// Routing, computed by every wave on its own (no LDS, no barrier).
+//
+// Keys: a logit maps to an unsigned key that orders like the float, with NaN
+// ranked as -inf and -0 as +0; experts past n_expert get key 0 (below -inf).
+// Lane l holds the keys of experts l, l + 64, ... (C chunks of 64 experts).
+// Selection: a binary search over key bits with wave ballots finds T, the
+// n_sel-th largest key; every key > T is selected, and of the keys == T the
+// lowest expert indexes fill the rest. Ranking: for each selected expert in
+// turn (uniform loop over the set bits of the selection ballots), its rank is
+// a ballot count of the selected experts ordered before it (larger key, or
+// equal key and lower index); lane `rank` takes it. Lane r < n_sel ends with
+// the expert and the canonical logit of rank r.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t logit_key(float v) {
+    if (v != v) v = -INFINITY;
+    const uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_logit(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+__device__ __forceinline__ int popc_below(uint64_t m) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
-__device__ void route_rank(const MoeArgs &a, Route *rt, float *lg, const float (&lv)[LPT]) {
-    const uint32_t t = threadIdx.x;
-    const uint32_t n4 = (a.n_expert + 3) & ~3u;
-    if (a.logits) {
+struct WaveRoute {
+    int32_t id;     // lane r < n_sel: expert of rank r
+    float logit;    // its logit (canonical: NaN -> -inf, -0 -> +0)
+};
+
+// Issue the logit loads of one wave (lane l: experts l, l + 64, ...). The
+// address is clamped into the logits so the loads need no branch; keys of
+// experts past n_expert are replaced later.
+template <int C>
+__device__ __forceinline__ void load_keys(const MoeArgs &a, float (&lv)[C]) {
+    const uint32_t lane = threadIdx.x & 63;
+    const float *src = route_logits(a);
 #pragma unroll
-        for (int i = 0; i < LPT; i++) {
-            const uint32_t e = t + 256 * i;
-            if (e < n4) lg[e] = lv[i] != lv[i] ? -INFINITY : lv[i];   // NaN and padding rank last
-        }
-        __syncthreads();
-        for (uint32_t e = t; e < a.n_expert; e += blockDim.x) {
-            const float v = lg[e];
-            uint32_t rank = 0;
-#pragma unroll 8
-            for (uint32_t j = 0; j < n4; j += 4) {
-                const float4 u = *(const float4 *)(lg + j);
-                rank += (u.x > v) | ((u.x == v) & (j + 0 < e));
-                rank += (u.y > v) | ((u.y == v) & (j + 1 < e));
-                rank += (u.z > v) | ((u.z == v) & (j + 2 < e));
-                rank += (u.w > v) | ((u.w == v) & (j + 3 < e));
+    for (int i = 0; i < C; i++) lv[i] = src[min(lane + 64 * i, a.n_expert - 1)];
+}
+
+template <int C>
+__device__ __forceinline__ WaveRoute wave_topk(const MoeArgs &a, const float (&lv)[C]) {
+    const uint32_t lane = threadIdx.x & 63;
+    const int k = a.n_sel;
+    uint32_t key[C];
+#pragma unroll
+    for (int i = 0; i < C; i++) key[i] = (lane + 64 * i < a.n_expert) ? logit_key(lv[i]) : 0u;
+    // T = largest t with #{key >= t} >= k (then T is the k-th largest key)
+    uint32_t T = 0;
+#pragma unroll
+    for (int b = 31; b >= 0; b--) {
+        const uint32_t c = T | (1u << b);
+        int cnt = 0;
+#pragma unroll
+        for (int i = 0; i < C; i++) cnt += __popcll(__ballot(key[i] >= c));
+        T = cnt >= k ? c : T;
+    }
+    int gt = 0;
+#pragma unroll
+    for (int i = 0; i < C; i++) gt += __popcll(__ballot(key[i] > T));
+    const int need = k - gt;   // ties at T to take, lowest index first
+    uint64_t sm[C];
+    bool sel[C];
+    int eq_seen = 0;
+#pragma unroll
+    for (int i = 0; i < C; i++) {
+        const uint64_t eq = __ballot(key[i] == T);
+        sel[i] = key[i] > T || (key[i] == T && eq_seen + popc_below(eq) < need);
+        sm[i] = __ballot(sel[i]);
+        eq_seen += __popcll(eq);
+    }
+    WaveRoute r;
+    r.id = -1;
+    r.logit = 0.0f;
+    uint32_t rkey = 0;
+#pragma unroll
+    for (int j = 0; j < C; j++) {
+        uint64_t m = sm[j];
+        while (m) {   // uniform: n_sel iterations in total
+            const int src = __builtin_ctzll(m);
+            m &= m - 1;
+            const uint32_t x = (uint32_t)__builtin_amdgcn_readlane((int)key[j], src);
+            const uint32_t e = (uint32_t)src + 64 * j;
+            int rank = 0;
+#pragma unroll
+            for (int i = 0; i < C; i++) {
+                const uint32_t idx = lane + 64 * i;
+                rank += __popcll(__ballot(sel[i] && (key[i] > x || (key[i] == x && idx < e))));
             }
-            if (rank < (uint32_t)a.n_sel) rt->ids[rank] = (int32_t)e;   // ranks are a permutation
+            if ((int)lane == rank) {
+                r.id = (int32_t)e;
+                rkey = x;
+            }
         }
-    } else if (t < (uint32_t)a.n_sel) {
-        rt->ids[t] = a.ids[t];
-        rt->w[t] = a.wts[t];
     }
-    if (t == 0 && a.has_shared) {
-        rt->ids[a.n_sel] = -1;
-        rt->w[a.n_sel] = 1.0f;
-    }
-    __syncthreads();
-    // an id outside the pool (bad explicit ids) would index past the expert
-    // tensors: clamp it to 0 for addressing; workgroup 0 reports it
+    if ((int)lane < k) r.logit = key_logit(rkey);
+    return r;
 }
 
-// Workgroup 0 of kernel A: weights (when routing from logits), the routing
-// scratch for kernel B, the optional routing outputs, and the error bit.
-__device__ void route_publish(const MoeArgs &a, const Route *rt, const float *lg) {
-    if (threadIdx.x != 0) return;
-    int32_t ids[MAX_SEL];
-    bool bad = false;
-    for (int r = 0; r < a.n_sel; r++) {
-        const int32_t e = rt->ids[r];
-        bad |= e < 0 || (uint32_t)e >= a.n_expert;
-        ids[r] = e;
-    }
+// Routing weights w_r = exp(l_r - l_0) / sum_{j<n_sel} exp(l_j - l_0), the sum
+// taken in rank order (lane r < n_sel holds rank r).
+__device__ __forceinline__ float route_weight(float logit, int n_sel) {
+    const float l0 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(logit)));
+    const float ex = kq_expf(logit - l0);
     float sum = 0.0f;
-    if (a.logits) {
-        // two passes over the same exp values: the rank-order sum, then the
-        // quotients
-        const float lmax = lg[ids[0]];
-        for (int r = 0; r < a.n_sel; r++) sum += kq_expf(lg[ids[r]] - lmax);
-    }
-    for (int r = 0; r < MAX_SLOTS; r++) {
+    for (int r = 0; r < n_sel; r++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), r));
+    return ex / sum;
+}
+
+// Wave 0 of workgroup 0 of kernel A: the routing scratch for kernel B, the
+// optional routing outputs, and the error bit for ids outside the pool
+// (those are clamped to expert 0 for addressing).
+__device__ __forceinline__ void route_publish(const MoeArgs &a, int32_t id, float w) {
+    const int lane = (int)(threadIdx.x & 63);
+    const bool bad = lane < a.n_sel && (uint32_t)id >= a.n_expert;
+    if (lane < MAX_SLOTS) {
         int32_t e = -1;
-        float w = 0.0f;
-        if (r < a.n_sel) {
-            e = ids[r];
-            w = a.logits ? kq_expf(lg[e] - lg[ids[0]]) / sum : rt->w[r];
-            if (a.ids_out) a.ids_out[r] = e;
-            if (a.wts_out) a.wts_out[r] = w;
-        } else if (r == a.n_sel && a.has_shared) {
-            w = 1.0f;
+        float ww = 0.0f;
+        if (lane < a.n_sel) {
+            e = bad ? 0 : id;
+            ww = w;
+            if (a.ids_out) a.ids_out[lane] = id;
+            if (a.wts_out) a.wts_out[lane] = w;
+        } else if (lane == a.n_sel && a.has_shared) {
+            ww = 1.0f;
         }
-        a.route_ids[r] = (r < a.n_sel && (uint32_t)e >= a.n_expert) ? 0 : e;   // addressing stays in the pool
-        a.route_w[r] = w;
+        a.route_ids[lane] = e;
+        a.route_w[lane] = ww;
     }
-    if (bad) atomicOr(a.err, 2);
+    if (__ballot(bad) != 0 && lane == 0) atomicOr(a.err, 2);
 }
 
 // Sum R per-lane values over the 64 lanes of a wave for R rows at once: each
-// halving step sends the half of the rows the partner keeps (R/2 shuffles),
-// then the remaining offsets finish a plain butterfly. Afterwards every lane
-// holds the full sum of row (lane >> (6 - log2 R)) & (R - 1).
+// halving step sends the half of the rows the partner keeps, then the
+// remaining offsets finish a plain butterfly. Partners differ in lane bit 5
+// (v_permlane32_swap), bit 4 (v_permlane16_swap), then inside 16-lane rows
+// by DPP: lane ^ 15, lane ^ 7, lane ^ 2, lane ^ 1 (these masks span the low
+// 4 bits, so every lane's value is counted once). Afterwards every lane holds
+// the full sum of row (lane >> (6 - log2 R)) & (R - 1).
+//
+// v_permlane32_swap(X, Y) gives r0 = {X[0..31], Y[0..31]} and
+// r1 = {X[32..63], Y[32..63]} (lane halves), so r0 + r1 is X[l] + X[l+32] in
+// the lower half and Y[l-32] + Y[l] in the upper half; v_permlane16_swap does
+// the same for odd/even 16-lane rows.
+template <int OFF>
+__device__ __forceinline__ float swap_sum(float x, float y) {
+    static_assert(OFF == 32 || OFF == 16, "swap_sum crosses 32 or 16 lanes");
+    if constexpr (OFF == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+        return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    } else {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+        return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+}
+template <int OFF>
+__device__ __forceinline__ float row_partner(float v) {   // OFF in {8, 4, 2, 1}
+    if constexpr (OFF == 8) return dpp_f<DPP_MIRROR>(v);
+    else if constexpr (OFF == 4) return dpp_f<DPP_HALF_MIRROR>(v);
+    else if constexpr (OFF == 2) return dpp_f<DPP_XOR2>(v);
+    else return dpp_f<DPP_XOR1>(v);
+}
 template <int N, int OFF, int R>
 __device__ __forceinline__ void reduce_halve(float (&acc)[R], int lane) {
     if constexpr (N > 1) {
         constexpr int HALF = N / 2;
-        const bool upper = lane & OFF;
+        if constexpr (OFF >= 16) {
 #pragma unroll
-        for (int i = 0; i < HALF; i++) {
-            const float send = upper ? acc[i] : acc[i + HALF];
-            const float keep = upper ? acc[i + HALF] : acc[i];
-            acc[i] = keep + __shfl_xor(send, OFF, WAVE);
+            for (int i = 0; i < HALF; i++) acc[i] = swap_sum<OFF>(acc[i], acc[i + HALF]);
+        } else {
+            const bool upper = lane & OFF;
+#pragma unroll
+            for (int i = 0; i < HALF; i++) {
+                const float send = upper ? acc[i] : acc[i + HALF];
+                const float keep = upper ? acc[i + HALF] : acc[i];
+                acc[i] = keep + row_partner<OFF>(send);
+            }
         }
         reduce_halve<HALF, OFF / 2, R>(acc, lane);
     }
+}
+template <int OFF>
+__device__ __forceinline__ float butterfly_from(float v) {
+    if constexpr (OFF >= 16) v = swap_sum<OFF>(v, v);
+    else if constexpr (OFF >= 1) v += row_partner<OFF>(v);
+    if constexpr (OFF > 1) return butterfly_from<OFF / 2>(v);
+    else return v;
 }
 template <int R>
 __device__ __forceinline__ float reduce_rows(float (&acc)[R]) {
     const int lane = threadIdx.x & 63;
     reduce_halve<R, 32, R>(acc, lane);
     constexpr int LOG = R >= 16 ? 4 : (R >= 8 ? 3 : (R >= 4 ? 2 : (R >= 2 ? 1 : 0)));
-    float v = acc[0];
-#pragma unroll
-    for (int off = 32 >> LOG; off > 0; off >>= 1) v += __shfl_xor(v, off, WAVE);
-    return v;
+    if constexpr (LOG < 6) return butterfly_from<(32 >> LOG)>(acc[0]);
+    else return acc[0];
 }
 
 // ---------------------------------------------------------------------------
 // Kernel A: 64 Q4_K rows (32 gate + 32 up) per workgroup, NB blocks per row.
-// Wave w owns rows 16w..16w+15 (waves 0-1 gate, 2-3 up). Lane l always takes
-// the same lane item of every row it touches, so its activation slice (two
-// 16-byte q8 chunks, their scales and half-block sums) is read from LDS once:
+// Wave w owns rows 16w..16w+15 (waves 0-1 gate, 2-3 up) and runs on its own
+// until the gate/up exchange at the end: no workgroup barrier before that.
+// Lane l always takes the same lane item of every row it touches:
 //   ITEMS = 8*NB >= 64: the k-th chunk is item 64*(k % M) + l of row k / M
-//                       (M = ITEMS/64 slices per lane);
+//                       (M = ITEMS/64 items per lane);
 //   ITEMS < 64:         64/ITEMS rows share a wave instruction; the k-th
 //                       chunk is item l % ITEMS of row l / ITEMS + k*64/ITEMS.
-// Block headers are decoded once per (row, block) into LDS as
-// {d*sc[2g], d*sc[2g+1], dmin*m[2g], dmin*m[2g+1]} per group g.
+// x is quantized to q8_1 once per workgroup into LDS (8 lanes per 32-value
+// block) while the weights stream in; each lane then reads its items' q8
+// values once. The wave's 16*NB block headers are decoded once into a
+// wave-private LDS area as {d*sc[2g], d*sc[2g+1], dmin*m[2g], dmin*m[2g+1]}
+// per group g (a wavefront-scope sync, not a barrier, orders them).
 // ---------------------------------------------------------------------------
 struct LdsA {
-    uint32_t route, logits, xact, scl, gu, total;
+    uint32_t xact, scl, gu, total;
 };
 __host__ __device__ inline LdsA lds_a(uint32_t hidden, uint32_t nb) {
     LdsA L;
-    L.route = 0;
-    L.logits = 256;
-    L.xact = L.logits + MAX_EXPERT * 4;
-    L.scl = L.xact + act_bytes(hidden);
-    L.gu = L.scl + 64 * nb * 64;
+    L.xact = 0;
+    L.scl = L.xact + act_bytes(hidden);   // 4 waves x 16*nb headers x 4 groups x float4
+    L.gu = L.scl + 4 * 16 * nb * 64;
     L.total = L.gu + 64 * 4;
     return L;
+}
+
+__device__ __forceinline__ void wave_sync_lds() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // the activation side of one lane item (constant over rows)
@@ -215,40 +301,69 @@ __device__ __forceinline__ float item_dot(const uint4 &q, const float4 &sc, cons
     return fmaf(x.d8lo, vlo, x.d8hi * vhi);
 }
 
-template <int NB>
+template <int NB, int C>
 __global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
     constexpr int ITEMS = 8 * NB;              // lane items per row
     constexpr int LPL = 2 * NB;                // 16 rows x ITEMS / 64 lanes
     constexpr int GROUPS = LPL > 16 ? LPL / 16 : 1;
     constexpr int RPG = 16 / GROUPS;           // rows per group
     constexpr int LPG = RPG * ITEMS / 64;      // chunks per lane per group
-    constexpr int M = ITEMS >= 64 ? ITEMS / 64 : 1;   // activation slices per lane
+    constexpr int M = ITEMS >= 64 ? ITEMS / 64 : 1;   // items per lane
     constexpr int LOG_RPG = RPG == 16 ? 4 : (RPG == 8 ? 3 : (RPG == 4 ? 2 : (RPG == 2 ? 1 : 0)));
+    constexpr int WH = 16 * NB;                // block headers of one wave's rows
+    constexpr int HPL = (WH + 63) / 64;        // header loads per lane
     extern __shared__ __align__(16) uint8_t lds[];
     const LdsA L = lds_a(a.hidden, NB);
-    Route *rt = (Route *)(lds + L.route);
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t nblk = a.ffn / 32;
     const uint32_t slot = blockIdx.x / nblk, jb = blockIdx.x % nblk;
+    const bool publisher = blockIdx.x == 0 && wave == 0;
 
-    // logits, then x (fp32), into registers; their latency overlaps
-    float lv[LPT];
-    load_logits(a, lv);
+    // routing inputs, then x (fp32 or q8_1; lane task t covers values
+    // 4t..4t+3); their latencies overlap. Loads are clamped, not guarded: no
+    // branch sits around a load.
+    float lv[C];
+    int32_t eid = -1;
+    float ew = 0.0f;
+    if (a.logits) {
+        load_keys<C>(a, lv);
+    } else {
+        const uint32_t r = min(lane, (uint32_t)a.n_sel - 1);
+        eid = a.ids[r];
+        ew = a.wts[r];
+    }
     constexpr int XTASKS = 64 * NB;            // quantizer lane tasks (8 per 32-block)
     constexpr int XPT = (XTASKS + 255) / 256;
     float4 xv[XPT];
+    uint32_t xqv[XPT], xdv[XPT];
     if (a.xq == nullptr) {
 #pragma unroll
-        for (int i = 0; i < XPT; i++)
-            if (tid + 256 * i < XTASKS) xv[i] = *(const float4 *)(a.x + 4 * (tid + 256 * i));
+        for (int i = 0; i < XPT; i++) xv[i] = *(const float4 *)(a.x + 4 * min(tid + 256 * i, (uint32_t)XTASKS - 1));
+    } else {
+#pragma unroll
+        for (int i = 0; i < XPT; i++) {
+            const uint32_t t = min(tid + 256 * i, (uint32_t)XTASKS - 1);
+            const uint8_t *b = a.xq + (t >> 3) * 36;
+            xqv[i] = *(const uint32_t *)(b + 4 + 4 * (t & 7));
+            xdv[i] = ld_u16(b);
+        }
     }
-    route_rank(a, rt, (float *)(lds + L.logits), lv);
+    float route_l = 0.0f;
+    if (a.logits) {
+        const WaveRoute r = wave_topk<C>(a, lv);
+        eid = r.id;
+        route_l = r.logit;
+    }
+    // Drain the routing and x loads here, in one place: with loads issued
+    // under branches the compiler cannot tell which registers are still
+    // pending and would otherwise wait for the weight loads one by one.
+    __builtin_amdgcn_s_waitcnt(VMCNT0);
 
     const uint64_t rb = NB * 144;
     const uint8_t *gb, *ub;
     if ((int)slot < a.n_sel) {
-        int32_t id = rt->ids[slot];
-        if ((uint32_t)id >= a.n_expert) id = 0;   // bad explicit id: reported by workgroup 0
+        int32_t id = __builtin_amdgcn_readlane(eid, (int)slot);
+        if ((uint32_t)id >= a.n_expert) id = 0;   // bad explicit id: reported by route_publish
         const uint64_t e = (uint64_t)id;
         gb = a.gate + e * a.ffn * rb;
         ub = a.up + e * a.ffn * rb;
@@ -271,45 +386,55 @@ __global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
         return row_ptr(16 * wave + r) + (it / 8) * 144 + 16 + 16 * (it % 8);
     };
 
-    // all weight loads: block headers first (consumed first), then chunks
-    constexpr int HPT = (64 * NB + 255) / 256;
-    uint4 hv[HPT];
+    // every weight load of the wave: its block headers first, then chunks
+    uint4 hv[HPL];
 #pragma unroll
-    for (int i = 0; i < HPT; i++) {
-        const uint32_t h = tid + 256 * i;
-        if (h < 64 * NB) hv[i] = ld16(row_ptr(h / NB) + (h % NB) * 144);
+    for (int i = 0; i < HPL; i++) {
+        const uint32_t h = min(lane + 64 * i, (uint32_t)WH - 1);   // duplicates decode the same header
+        hv[i] = ld16(row_ptr(16 * wave + h / NB) + (h % NB) * 144);
     }
     uint4 q[LPG];
 #pragma unroll
     for (int k = 0; k < LPG; k++) q[k] = ld16(chunk(0, k));
+    if (publisher) {
+        if (a.logits) ew = route_weight(route_l, a.n_sel);
+        route_publish(a, eid, ew);
+    }
 
     // quantize x into LDS while the weights stream in
     const Act xa = act_carve(lds + L.xact, a.hidden);
-    if (a.xq) {
-        act_stage_from_q8(a.xq, a.hidden, xa);
-    } else {
 #pragma unroll
-        for (int i = 0; i < XPT; i++) {
-            const uint32_t t = tid + 256 * i, blk = t >> 3, part = t & 7;
-            if (t >= XTASKS) break;
+    for (int i = 0; i < XPT; i++) {
+        const uint32_t t = tid + 256 * i, blk = t >> 3, part = t & 7;
+        if (t >= XTASKS) break;   // whole 8-lane groups leave together
+        uint32_t qv;
+        int lo, hi;
+        float dd;
+        if (a.xq) {
+            qv = xqv[i];
+            q8_part_sums(qv, lo, hi);
+            dd = h2f(xdv[i]);
+        } else {
             uint32_t d16, s16;
-            int lo, hi;
-            float dd;
-            const uint32_t qv = quant_q8_1_part(xv[i], d16, s16, lo, hi, dd);
-            *(uint32_t *)(xa.qs + 32 * blk + 4 * part) = qv;
-            if (part == 0) {
-                xa.d8[blk] = dd;
-                xa.qs16[2 * blk] = lo;
-                xa.qs16[2 * blk + 1] = hi;
-            }
+            qv = quant_q8_1_part(xv[i], d16, s16, lo, hi, dd);
+        }
+        *(uint32_t *)(xa.qs + 32 * blk + 4 * part) = qv;
+        if (part == 0) {
+            xa.d8[blk] = dd;
+            xa.qs16[2 * blk] = lo;
+            xa.qs16[2 * blk + 1] = hi;
         }
     }
-    // decode the 64*NB block headers into per-group scale quadruples
-    float4 *scl = (float4 *)(lds + L.scl);
+    __syncthreads();   // x is ready long before the weights: off the critical path
+    XSlice xs[M];
 #pragma unroll
-    for (int i = 0; i < HPT; i++) {
-        const uint32_t h = tid + 256 * i;
-        if (h < 64 * NB) {
+    for (int m = 0; m < M; m++) xs[m] = x_slice(xa, ITEMS >= 64 ? 64 * m + lane : lane % ITEMS);
+    // decode the wave's headers into its own LDS area
+    float4 *scl = (float4 *)(lds + L.scl) + 4 * WH * wave;
+#pragma unroll
+    for (int i = 0; i < HPL; i++) {
+        const uint32_t h = lane + 64 * i;
+        if (h < WH) {
             Q4K::Raw raw;
             raw.h = hv[i];
 #pragma unroll
@@ -320,11 +445,8 @@ __global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
             }
         }
     }
-    __syncthreads();
+    wave_sync_lds();
 
-    XSlice xs[M];
-#pragma unroll
-    for (int m = 0; m < M; m++) xs[m] = x_slice(xa, ITEMS >= 64 ? 64 * m + lane : lane % ITEMS);
     float *gu = (float *)(lds + L.gu);
 #pragma unroll
     for (int grp = 0; grp < GROUPS; grp++) {
@@ -339,7 +461,7 @@ __global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
 #pragma unroll
             for (int k = 0; k < LPG; k++) {
                 const uint32_t it = 64 * (k % M) + lane;
-                const uint32_t row = 16 * wave + grp * RPG + k / M;
+                const uint32_t row = grp * RPG + k / M;   // within the wave
                 const float4 sc = scl[4 * (row * NB + it / 8) + (it % 8) / 2];
                 acc[k / M] += item_dot(q[k], sc, xs[k % M]);
             }
@@ -351,10 +473,10 @@ __global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
             const uint32_t it = lane % ITEMS;
 #pragma unroll
             for (int k = 0; k < LPG; k++) {
-                const uint32_t row = 16 * wave + lane / ITEMS + k * (64 / ITEMS);
+                const uint32_t row = lane / ITEMS + k * (64 / ITEMS);   // within the wave
                 const float4 sc = scl[4 * (row * NB + it / 8) + (it % 8) / 2];
                 const float v = group_sum<ITEMS>(item_dot(q[k], sc, xs[0]));
-                if (it == 0) gu[row] = v;
+                if (it == 0) gu[16 * wave + row] = v;
             }
         }
     }
@@ -379,62 +501,58 @@ __global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
         float *d = a.dbg_gu + (uint64_t)slot * 2 * a.ffn + (tid < 32 ? 0 : a.ffn) + 32 * jb + (tid & 31);
         *d = gu[tid];
     }
-    if (blockIdx.x == 0) route_publish(a, rt, (const float *)(lds + L.logits));
 }
 
 // ---------------------------------------------------------------------------
 // Kernel B: a tile of TR output rows x n_slots down rows per workgroup; one
-// lane-slot (S = QD::IPB lanes) per (row, slot) pair; every load issued before
-// the h activations are staged.
+// lane-slot (S = QD::IPB lanes) per (row, slot) pair. Order of work: the
+// routing and the q8_1 h loads (both written by kernel A, so L2/MALL hits),
+// then, once the routing is in, every down-weight load; h is staged into LDS
+// while the weights stream. Loads are clamped rather than guarded so the
+// compiler can count them (a load under a branch makes it wait for all).
 // ---------------------------------------------------------------------------
 struct LdsB {
-    uint32_t route, hacts, res, total;
+    uint32_t hacts, res, total;
 };
 __host__ __device__ inline LdsB lds_b(uint32_t ffn, uint32_t n_slots, uint32_t tr) {
     LdsB L;
-    L.route = 0;
-    L.hacts = 256;
+    L.hacts = 0;
     L.res = L.hacts + n_slots * act_bytes(ffn);
-    L.total = L.res + tr * n_slots * 4;
+    L.total = L.res + (tr * n_slots + MAX_SLOTS) * 4;   // padding: the unrolled slot sum reads past the tile
     return L;
 }
 
-// q8_1 h of every slot, staged from the scratch written by kernel A: 8 lanes
-// per 36-byte block (one dword of values each, lane 0 also the scale), loads
-// issued up front by load_h and finished by stage_h.
-constexpr int HT_MAX = 12;   // lane tasks per thread (n_slots * ffn/32 * 8 / blockDim)
+// q8_1 h of every slot: one lane per 16-byte half block (t = 2 * block + half),
+// so each lane's 16 values are exactly one half-block sum.
+constexpr int HT = 2;   // unrolled h tasks per thread (n_slots * ffn/32 * 2 <= 512); more go round a loop
 struct HLoad {
-    uint32_t q[HT_MAX];
-    uint32_t d[HT_MAX];
+    uint4 q[HT];
+    uint32_t d[HT];
 };
 __device__ __forceinline__ void load_h(const uint8_t *hq8, uint32_t ntask, uint32_t first, HLoad &h) {
 #pragma unroll
-    for (int i = 0; i < HT_MAX; i++) {
-        const uint32_t t = first + threadIdx.x + blockDim.x * i;
-        if (t < ntask) {
-            const uint8_t *b = hq8 + (t >> 3) * 36;
-            h.q[i] = *(const uint32_t *)(b + 4 + 4 * (t & 7));
-            h.d[i] = ld_u16(b);
-        }
+    for (int i = 0; i < HT; i++) {
+        const uint32_t t = min(first + threadIdx.x + 256 * i, ntask - 1);
+        const uint8_t *b = hq8 + (t >> 1) * 36;
+        h.q[i] = ld16(b + 4 + 16 * (t & 1));
+        h.d[i] = ld_u16(b);
     }
 }
 __device__ __forceinline__ void stage_h(uint8_t *hl, uint32_t ffn, uint32_t ntask, uint32_t first, const HLoad &h) {
     const uint32_t nblk = ffn / 32, ab = act_bytes(ffn);
 #pragma unroll
-    for (int i = 0; i < HT_MAX; i++) {
-        const uint32_t t = first + threadIdx.x + blockDim.x * i;
-        if (t >= ntask) break;   // whole 8-lane groups leave together
-        const uint32_t blk = t >> 3, part = t & 7, slot = blk / nblk, kb = blk % nblk;
-        const Act act = act_carve(hl + slot * ab, ffn);
-        *(uint32_t *)(act.qs + 32 * kb + 4 * part) = h.q[i];
-        int s = dot4(h.q[i], 0x01010101u, 0);
-        s += dpp_i<DPP_XOR1>(s);
-        s += dpp_i<DPP_XOR2>(s);
-        const int other = dpp_i<DPP_HALF_MIRROR>(s);
-        if (part == 0) {
-            act.d8[kb] = h2f(h.d[i]);
-            act.qs16[2 * kb] = s;
-            act.qs16[2 * kb + 1] = other;
+    for (int i = 0; i < HT; i++) {
+        const uint32_t t = first + threadIdx.x + 256 * i;
+        if (t < ntask) {
+            const uint32_t blk = t >> 1, half = t & 1, slot = blk / nblk, kb = blk % nblk;
+            const Act act = act_carve(hl + slot * ab, ffn);
+            *(uint4 *)(act.qs + 32 * kb + 16 * half) = h.q[i];
+            int sum = dot4(h.q[i].x, 0x01010101u, 0);
+            sum = dot4(h.q[i].y, 0x01010101u, sum);
+            sum = dot4(h.q[i].z, 0x01010101u, sum);
+            sum = dot4(h.q[i].w, 0x01010101u, sum);
+            act.qs16[2 * kb + half] = sum;
+            if (half == 0) act.d8[kb] = h2f(h.d[i]);
         }
     }
 }
@@ -443,23 +561,14 @@ template <class QD, int IPL>
 __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a, uint32_t tr, uint32_t n_slots) {
     extern __shared__ __align__(16) uint8_t lds[];
     const LdsB L = lds_b(a.ffn, n_slots, tr);
-    Route *rt = (Route *)(lds + L.route);
-    const uint32_t tid = threadIdx.x;
-    // h loads first (they do not depend on the routing), then the routing
-    const uint32_t ntask = n_slots * (a.ffn / 32) * 8;
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    // routing (lane r holds slot r), then the h loads
+    const int32_t rid = a.route_ids[min(lane, (uint32_t)MAX_SLOTS - 1)];
+    const float rw = a.route_w[min(lane, (uint32_t)MAX_SLOTS - 1)];
+    const uint32_t ntask = n_slots * (a.ffn / 32) * 2;
     HLoad hv;
     load_h(a.hq8, ntask, 0, hv);
-    int32_t rid = 0;
-    float rw = 0.0f;
-    if (tid < MAX_SLOTS) {
-        rid = a.route_ids[tid];
-        rw = a.route_w[tid];
-    }
-    if (tid < MAX_SLOTS) {
-        rt->ids[tid] = rid;
-        rt->w[tid] = rw;
-    }
-    __syncthreads();
+
     const uint32_t S = QD::IPB;
     const uint32_t ls = tid / S, s = tid % S;
     const uint32_t row0 = blockIdx.x * tr;
@@ -467,28 +576,25 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a, uint32_t tr, uint32
     const uint32_t npairs = nrows * n_slots;
     const uint64_t rbd = (uint64_t)(a.ffn / 256) * QD::BB;
     const uint32_t ipl = a.ffn / 256;
-    typename QD::Raw raw[IPL > 0 ? IPL : 1];
     const bool active = ls < npairs;
-    uint32_t sl = 0;
-    const uint8_t *rp = nullptr;
-    if (active) {
-        const uint32_t r = ls / n_slots;
-        sl = ls % n_slots;
-        const uint8_t *db = (int)sl < a.n_sel ? a.down + (uint64_t)rt->ids[sl] * a.hidden * rbd : a.down_sh;
-        rp = db + (uint64_t)(row0 + r) * rbd;
-        if constexpr (IPL > 0) {
+    const uint32_t lc = min(ls, npairs - 1);   // idle lane-slots load a real pair and drop it
+    const uint32_t sl = lc % n_slots, r = lc / n_slots;
+    const int32_t sid = __shfl(rid, (int)sl, WAVE);
+    const uint8_t *db = (int)sl < a.n_sel ? a.down + (uint64_t)sid * a.hidden * rbd : a.down_sh;
+    const uint8_t *rp = db + (uint64_t)(row0 + r) * rbd;
+    typename QD::Raw raw[IPL > 0 ? IPL : 1];
+    if constexpr (IPL > 0) {
 #pragma unroll
-            for (int i = 0; i < IPL; i++) raw[i] = QD::load(rp + i * QD::BB, (int)s);
-        }
+        for (int i = 0; i < IPL; i++) raw[i] = QD::load(rp + i * QD::BB, (int)s);
     }
     stage_h(lds + L.hacts, a.ffn, ntask, 0, hv);
-    for (uint32_t first = HT_MAX * blockDim.x; first < ntask; first += HT_MAX * blockDim.x) {
-        load_h(a.hq8, ntask, first, hv);   // only for n_slots * ffn > 12288
+    for (uint32_t first = HT * 256; first < ntask; first += HT * 256) {
+        load_h(a.hq8, ntask, first, hv);   // only when n_slots * ffn / 16 > 512
         stage_h(lds + L.hacts, a.ffn, ntask, first, hv);
     }
     __syncthreads();
     float x = 0.0f;
-    if (active) {
+    {
         const Act act = act_carve(lds + L.hacts + sl * act_bytes(a.ffn), a.ffn);
         if constexpr (IPL > 0) {
 #pragma unroll
@@ -501,10 +607,16 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a, uint32_t tr, uint32
     float *res = (float *)(lds + L.res);
     if (active && s == 0) res[ls] = x;
     __syncthreads();
-    for (uint32_t i = tid; i < nrows; i += blockDim.x) {
+    if (tid < nrows) {
+        // rank order, one fmaf per slot: y = w_{n-1} r_{n-1} + (... + (w_0 r_0 + 0))
         float y = 0.0f;
-        for (uint32_t k = 0; k < n_slots; k++) y = fmaf(rt->w[k], res[i * n_slots + k], y);
-        a.y[row0 + i] = y;
+#pragma unroll
+        for (int k = 0; k < MAX_SLOTS; k++) {
+            const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rw), k));
+            const float v = res[tid * n_slots + k];
+            y = k < (int)n_slots ? fmaf(w, v, y) : y;
+        }
+        a.y[row0 + tid] = y;
     }
 }
 
@@ -513,7 +625,13 @@ uint64_t moe_route_words() { return 2 * MAX_SLOTS; }
 template <int NB>
 static hipError_t go_a(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
     const LdsA L = lds_a(a.hidden, NB);
-    hipLaunchKernelGGL(k_moe_gu<NB>, dim3(n_slots * (a.ffn / 32)), dim3(256), L.total, s, a);
+    const dim3 grid(n_slots * (a.ffn / 32));
+    if (a.n_expert <= 128)
+        hipLaunchKernelGGL((k_moe_gu<NB, 2>), grid, dim3(256), L.total, s, a);
+    else if (a.n_expert <= 256)
+        hipLaunchKernelGGL((k_moe_gu<NB, 4>), grid, dim3(256), L.total, s, a);
+    else
+        hipLaunchKernelGGL((k_moe_gu<NB, 8>), grid, dim3(256), L.total, s, a);
     return hipGetLastError();
 }
 

@@ -510,11 +510,14 @@ void kqo_silu_mul_ref(float *gate, const float *up, uint64_t n) {
     for (uint64_t i = nv; i < n; i++) gate[i] = (gate[i] / (1.0f + expf(-gate[i]))) * up[i];
 }
 
-int kqo_router_topk(const float *logits, int n_expert, int k, int32_t *ids, float *w) {
+int kqo_router_topk(const float *logits_in, int n_expert, int k, int32_t *ids, float *w) {
     if (k <= 0 || k > n_expert || k > 64) return -1;
     unsigned char taken[4096];
+    float logits[4096];
     if (n_expert > 4096) return -1;
     memset(taken, 0, (size_t)n_expert);
+    /* a NaN logit ranks, and weighs, as -inf */
+    for (int e = 0; e < n_expert; e++) logits[e] = logits_in[e] != logits_in[e] ? -INFINITY : logits_in[e];
     for (int r = 0; r < k; r++) {
         int best = -1;
         for (int e = 0; e < n_expert; e++)

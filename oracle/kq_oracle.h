@@ -116,7 +116,8 @@ void  kqo_silu_mul_ref(float *gate, const float *up, uint64_t n);
 /* Top-k by logit (descending; equal logits -> lower index first), weights
  * renormalised over the selection: w_i = e_i / sum_sel e_j, e_i =
  * kqo_expf(l_i - l_max), sum in rank order. Equal to softmax followed by
- * renormalisation over the top k. */
+ * renormalisation over the top k. A NaN logit counts as -inf (rank and
+ * weight); -0 and +0 are equal logits. */
 int kqo_router_topk(const float *logits, int n_expert, int k, int32_t *ids, float *w);
 
 /* ---- MoE layer (configs 1, 2, 4) ----------------------------------------- */

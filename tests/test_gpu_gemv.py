@@ -62,6 +62,33 @@ def test_quantize_q8_1_bit_exact(hip, oracle, n):
     assert np.array_equal(got, oracle.quantize_q8_1(x))
 
 
+def f16_tie_blocks(oracle, n_blocks=200_000, seed=11):
+    """Blocks whose f32 product sum(q)*d sits exactly halfway between two f16
+    values while the exact product does not: a quantizer that rounds the
+    exact product straight to f16 (one rounding) writes a different s than
+    the defined f32-then-f16 (two roundings)."""
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((n_blocks, 32)) * 300.0).astype(np.float32)
+    q = oracle.quantize_q8_1(x.reshape(-1)).reshape(n_blocks, 36)
+    d = (np.max(np.abs(x), axis=1) / np.float32(127)).astype(np.float32)
+    tot = q[:, 4:].view(np.int8).astype(np.int64).sum(axis=1)
+    p32 = (tot.astype(np.float32) * d).astype(np.float32)
+    bits = np.abs(p32).view(np.uint32)
+    normal16 = (bits >= 0x38800000) & (bits < 0x477FE000)
+    tie = normal16 & ((bits & 0x1FFF) == 0x1000)
+    exact_differs = tot.astype(np.float64) * d.astype(np.float64) != p32.astype(np.float64)
+    return x[tie & exact_differs]
+
+
+def test_quantize_q8_1_f16_ties(hip, oracle):
+    x = f16_tie_blocks(oracle)
+    assert len(x) >= 4
+    x = np.ascontiguousarray(x.reshape(-1))
+    q = hip.alloc(x.size // 32 * 36)
+    hip.quantize_q8_1(hip.to_device(x), x.size, q)
+    assert np.array_equal(q.download(np.uint8), oracle.quantize_q8_1(x))
+
+
 @pytest.mark.parametrize("t,rows,cols", SHAPES, ids=[f"{'q4k' if s[0] == Q4_K else 'q6k'}_{s[1]}x{s[2]}" for s in SHAPES])
 def test_gemv_q8_parity(hip, oracle, t, rows, cols):
     print(f"[gemv_q8] type={t} rows={rows} cols={cols}", flush=True)

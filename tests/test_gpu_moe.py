@@ -130,6 +130,55 @@ def test_moe_layer_parity(hip, oracle, moes, case):
     assert np.array_equal(y2.view(np.uint32), y.view(np.uint32))
 
 
+ROUTE_CASES = [
+    # n_expert, n_sel, logits
+    (128, 8, "ties"),      # integer logits: many equal values across the cut
+    (256, 8, "normal"),
+    (512, 16, "ties"),
+    (512, 1, "special"),
+    (64, 16, "special"),   # NaN, +-inf, -0/+0 mixed in
+    (16, 16, "normal"),    # every expert selected
+    (200, 5, "special"),   # n_expert not a multiple of 64
+]
+
+
+def route_logits(rng, n_expert, kind):
+    if kind == "ties":
+        return rng.integers(-2, 3, n_expert).astype(np.float32)
+    v = rng.standard_normal(n_expert).astype(np.float32)
+    if kind == "special":
+        idx = rng.permutation(n_expert)
+        v[idx[0::7]] = np.nan
+        v[idx[1::11]] = -np.inf
+        v[idx[2::13]] = -0.0
+        v[idx[3::13]] = 0.0
+        v[idx[4]] = np.inf if n_expert > 100 else v[idx[4]]
+    return v
+
+
+@pytest.mark.parametrize("case", ROUTE_CASES, ids=[f"e{c[0]}_k{c[1]}_{c[2]}" for c in ROUTE_CASES])
+def test_moe_routing_matches_oracle(hip, oracle, moes, case):
+    """In-kernel top-k and weights against the oracle router: same experts in
+    the same order, bit-identical weights (ties to the lower index, NaN as
+    -inf, -0 equal to +0); the layer output follows the same selection."""
+    n_expert, n_sel, kind = case
+    print(f"[moe-route] case={case}", flush=True)
+    m = moes(256, 256, n_expert, False, Q4_K)
+    rng = np.random.default_rng(n_expert * 31 + n_sel)
+    x = S.activation(rng, 256)
+    logits = route_logits(rng, n_expert, kind)
+    ids, w = oracle.router_topk(logits, n_sel)
+    y, gu, hq, ido, wo = run_layer(hip, m, x, n_sel, logits=logits)
+    assert ido.tolist() == ids.tolist()
+    if np.all(np.isfinite(w)):
+        assert np.array_equal(wo.view(np.uint32), w.view(np.uint32))
+    else:   # +inf logit: inf - inf in the weights, NaN on both sides
+        assert np.array_equal(np.isnan(wo), np.isnan(w))
+        return
+    yd = oracle.moe_down_q8(m.odesc, ids, w, hq)
+    assert rel_l2(y, yd) <= 1e-5
+
+
 @pytest.mark.parametrize("case", CASES[:2], ids=["e128_k8", "e256_k8_sh"])
 def test_moe_repeatable(hip, oracle, moes, case):
     hidden, ffn, n_expert, n_sel, shared, down_type = case

@@ -296,6 +296,18 @@ def test_router_topk_vs_softmax_renorm(oracle, refcpu, n_expert, k):
     assert np.allclose(w, ps[order] / ps[order].sum(), rtol=1e-5, atol=0)
 
 
+def test_router_topk_nan_and_signed_zero(oracle):
+    """NaN ranks (and weighs) as -inf, ties by lower index; -0 equals +0."""
+    logits = np.array([np.nan, -np.inf, 0.5, -0.0, 0.0, np.nan, 0.5, -1.0], np.float32)
+    ids, w = oracle.router_topk(logits, 8)
+    # 0.5 (2, 6), then the zeros (3, 4), -1 (7), then -inf/NaN by index (0, 1, 5)
+    assert ids.tolist() == [2, 6, 3, 4, 7, 0, 1, 5]
+    assert np.all(w[5:] < 1e-30) and np.all(np.isfinite(w))
+    assert w[2] == w[3]
+    ids2, w2 = oracle.router_topk(np.where(np.isnan(logits), -np.inf, logits).astype(np.float32), 8)
+    assert ids2.tolist() == ids.tolist() and np.array_equal(w2, w)
+
+
 # ---------------------------------------------------------------------------
 # MoE composition: independent float64 composition over reference decoders
 # ---------------------------------------------------------------------------
