@@ -253,8 +253,10 @@ __device__ __forceinline__ float reduce_rows(float (&acc)[R]) {
 // x is quantized to q8_1 once per workgroup into LDS (8 lanes per 32-value
 // block) while the weights stream in; each lane then reads its items' q8
 // values once. The wave's 16*NB block headers are decoded once into a
-// wave-private LDS area as {d*sc[2g], d*sc[2g+1], dmin*m[2g], dmin*m[2g+1]}
-// per group g (a wavefront-scope sync, not a barrier, orders them).
+// wave-private LDS area as {d*sc[2g]*d8[k], d*sc[2g+1]*d8[k+1],
+// dmin*m[2g]*d8[k], dmin*m[2g+1]*d8[k+1]} per group g, where k and k+1 are
+// the q8_1 blocks of x that group meets (a wavefront-scope sync, not a
+// barrier, orders them).
 // ---------------------------------------------------------------------------
 struct LdsA {
     uint32_t xact, scl, gu, total;
@@ -268,6 +270,24 @@ __host__ __device__ inline LdsA lds_a(uint32_t hidden, uint32_t nb) {
     return L;
 }
 
+// max / sum over aligned 32-lane halves (every lane gets its half's result)
+__device__ __forceinline__ float max32(float v) {
+    v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+    v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_f<DPP_MIRROR>(v));
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ int sum32(int v) {
+    v += dpp_i<DPP_XOR1>(v);
+    v += dpp_i<DPP_XOR2>(v);
+    v += dpp_i<DPP_HALF_MIRROR>(v);
+    v += dpp_i<DPP_MIRROR>(v);
+    const auto r = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+    return (int)r[0] + (int)r[1];
+}
+
 __device__ __forceinline__ void wave_sync_lds() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -277,7 +297,7 @@ __device__ __forceinline__ void wave_sync_lds() {
 // the activation side of one lane item (constant over rows)
 struct XSlice {
     int4 xl, xh;
-    float d8lo, d8hi, qlo, qhi;
+    float qlo, qhi;   // integer sums of the lane's 16 low / 16 high x values
 };
 __device__ __forceinline__ XSlice x_slice(const Act &xa, uint32_t it) {
     const uint32_t b = it / 8, c = it % 8, g = c >> 1, hh = c & 1;
@@ -286,19 +306,16 @@ __device__ __forceinline__ XSlice x_slice(const Act &xa, uint32_t it) {
     x.xl = *(const int4 *)al;
     x.xh = *(const int4 *)(al + 32);
     const uint32_t k = 8 * b + 2 * g;
-    x.d8lo = xa.d8[k];
-    x.d8hi = xa.d8[k + 1];
     x.qlo = (float)xa.qs16[2 * k + hh];
     x.qhi = (float)xa.qs16[2 * k + 2 + hh];
     return x;
 }
-// same arithmetic as Q4K::dot_q8, with the scales pre-decoded
+// d8lo*(ds0*slo - dm0*qlo) + d8hi*(ds1*shi - dm1*qhi) with the x scales
+// folded into the decoded header (sc = {ds0*d8lo, ds1*d8hi, dm0*d8lo, dm1*d8hi})
 __device__ __forceinline__ float item_dot(const uint4 &q, const float4 &sc, const XSlice &x) {
     int slo, shi;
     Q4K::isums_x(q, x.xl, x.xh, slo, shi);
-    const float vlo = fmaf(sc.x, (float)slo, -(sc.z * x.qlo));
-    const float vhi = fmaf(sc.y, (float)shi, -(sc.w * x.qhi));
-    return fmaf(x.d8lo, vlo, x.d8hi * vhi);
+    return fmaf(sc.x, (float)slo, fmaf(sc.y, (float)shi, -fmaf(sc.z, x.qlo, sc.w * x.qhi)));
 }
 
 template <int NB, int C>
@@ -437,11 +454,14 @@ __global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
         if (h < WH) {
             Q4K::Raw raw;
             raw.h = hv[i];
+            const uint32_t b = h % NB;
+            const float4 dA = *(const float4 *)(xa.d8 + 8 * b), dB = *(const float4 *)(xa.d8 + 8 * b + 4);
+            const float d8[8] = {dA.x, dA.y, dA.z, dA.w, dB.x, dB.y, dB.z, dB.w};
 #pragma unroll
             for (int g = 0; g < 4; g++) {
-                float4 v;
-                Q4K::scales(raw, g, v.x, v.y, v.z, v.w);
-                scl[4 * h + g] = v;
+                float ds0, ds1, dm0, dm1;
+                Q4K::scales(raw, g, ds0, ds1, dm0, dm1);
+                scl[4 * h + g] = make_float4(ds0 * d8[2 * g], ds1 * d8[2 * g + 1], dm0 * d8[2 * g], dm1 * d8[2 * g + 1]);
             }
         }
     }
@@ -482,20 +502,19 @@ __global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
     }
     __syncthreads();
 
-    if (tid < 8) {
-        const uint32_t i0 = 4 * tid;
-        float4 h;
-        h.x = kq_silu_mul(gu[i0 + 0], gu[32 + i0 + 0]);
-        h.y = kq_silu_mul(gu[i0 + 1], gu[32 + i0 + 1]);
-        h.z = kq_silu_mul(gu[i0 + 2], gu[32 + i0 + 2]);
-        h.w = kq_silu_mul(gu[i0 + 3], gu[32 + i0 + 3]);
-        uint32_t d16, s16;
-        int lo, hi;
-        float dd;
-        const uint32_t qv = quant_q8_1_part(h, d16, s16, lo, hi, dd);
+    if (wave == 0) {
+        // one h value per lane (lanes 32..63 mirror 0..31), then the q8_1
+        // block across 32 lanes: same rules as quant_q8_1_part
+        const uint32_t j = lane & 31;
+        const float h = kq_silu_mul(gu[j], gu[32 + j]);
+        const float am = max32(fabsf(h));
+        const float d = am / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        const int qv = (int)roundf(h * id);
+        const int total = sum32(qv);
         uint8_t *blk = a.hq8 + ((uint64_t)slot * nblk + jb) * 36;
-        *(uint32_t *)(blk + 4 + 4 * tid) = qv;
-        if (tid == 0) *(uint32_t *)blk = d16 | (s16 << 16);
+        if (lane < 32) blk[4 + lane] = (uint8_t)(qv & 255);
+        if (lane == 0) *(uint32_t *)blk = f2h_rne(d) | (f2h_rne((float)total * d) << 16);
     }
     if (a.dbg_gu && tid < 64) {
         float *d = a.dbg_gu + (uint64_t)slot * 2 * a.ffn + (tid < 32 ? 0 : a.ffn) + 32 * jb + (tid & 31);
