@@ -1,19 +1,28 @@
 """Benchmark of the quantized expert-GEMV path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload moe48|moe40cold]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload moe48|moe40cold|gemv6144]
 
-Default workload (moe48): one decode token through 48 fused MoE layers,
+Workloads:
+  moe48     (default) one decode token through 48 fused MoE layers,
 hidden 2048, 128 experts, top-8, gate/up 2048->768 Q4_K, down 768->2048 Q6_K,
 random weights (independent seed per layer), N(0,1) activations and router
 logits. Every token draws new router logits (a ring of 64 steps), so each token
 touches a different 1.17 GB of the 18.8 GB expert pool: a cold working set far
 beyond L2 and the 256 MB MALL. The 48 layers and a step advance are captured
 in one hipGraph per token; a step is one replay.
+  moe40cold 40 MoE layers x 256 experts, gate/up 2048->512 Q4_K, down 512->2048
+            Q6_K, top-8 plus an always-on shared expert, 64-step logit ring.
+  gemv6144  dense Q4_K 6144x2048 GEMV, batch 1, fp32 x quantized to q8_1
+            inside the kernel; 144 distinct weight copies (1.02 GB) are cycled
+            so every GEMV reads cold weights; a step is one pass over them.
 
 Printed: ONE JSON line. value = algorithmic HBM GB/s of the whole token
 (selected expert weights + q8_1 activation + fp32 output, per layer) with
 everything resident in HBM; tok_s = tokens per second of the 48-layer chain;
-roofline = the fused MoE kernel alone (event-timed per launch);
+roofline = the dominant kernel work: one MoE layer (its two launches) or
+one GEMV, algorithmic bytes over the timed-region time per unit, with HBM
+traffic from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE profile when one
+exists for the workload (profiles/traffic_<workload>.txt);
 cpu_baseline = the reference's own CPU path (compiled from its sources into
 oracle/_ref) on a bounded sample of the same workload on this host.
 """
@@ -165,6 +174,133 @@ def bench_moe(hip, name, steps, warmup, ring=64):
 
 
 # ---------------------------------------------------------------------------
+# Dense GEMV over a cold rotating pool
+# ---------------------------------------------------------------------------
+GEMV_WORKLOADS = {
+    # name: type, rows, cols, copies
+    "gemv6144": (Q4_K, 6144, 2048, 144),
+}
+
+
+def gemv_bytes(t, rows, cols):
+    return rows * row_bytes(t, cols) + cols // 32 * 36 + rows * 4
+
+
+def bench_gemv(hip, name, steps, warmup):
+    t, rows, cols, copies = GEMV_WORKLOADS[name]
+    rb = row_bytes(t, cols)
+    pool = hip.alloc(copies * rows * rb)
+    hip.synth_fill(t, pool, copies * rows * cols // 256, 4242)
+    x = hip.alloc(cols * 4)
+    hip.synth_normal(x, cols, 77)
+    y = hip.alloc(copies * rows * 4)
+
+    class View:
+        def __init__(self, ptr):
+            self.ptr = ptr
+
+    ws = [View(pool.ptr + i * rows * rb) for i in range(copies)]
+    ys = [View(y.ptr + i * rows * 4) for i in range(copies)]
+
+    def step():
+        for i in range(copies):
+            hip.matvec_dp4a(t, ws[i], rows, cols, x, ys[i])
+
+    step()
+    hip.sync()
+    hip.graph_begin()
+    step()
+    graph = hip.graph_end()
+    for _ in range(warmup):
+        hip.graph_launch(graph)
+    hip.sync()
+    e0, e1 = hip.event(), hip.event()
+    t0 = time.perf_counter()
+    hip.record(e0)
+    for _ in range(steps):
+        hip.graph_launch(graph)
+    hip.record(e1)
+    ms = hip.elapsed_ms(e0, e1)
+    wall = time.perf_counter() - t0
+    hip.sync()
+    for e in (e0, e1):
+        hip.event_destroy(e)
+    hip.graph_destroy(graph)
+    unit_bytes = gemv_bytes(t, rows, cols)
+    per_gemv_ms = ms / steps / copies
+    res = {
+        "ms_per_step": ms / steps,
+        "wall_ms_per_step": wall * 1e3 / steps,
+        "value": unit_bytes / (per_gemv_ms / 1e3) / 1e9,
+        "unit_bytes": unit_bytes,
+        "unit_ms": per_gemv_ms,
+        "units_per_step": copies,
+        "pool_gb": copies * rows * rb / 1e9,
+    }
+    for b in (pool, x, y):
+        b.free()
+    return res, (t, rows, cols, copies)
+
+
+def cpu_baseline_gemv(shape, budget_s=12.0):
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    from oracle import RefCPU, ref_available, Oracle
+    t, rows, cols, _ = shape
+    threads = int(os.environ.get("KATALI_BENCH_CPU_THREADS", min(16, os.cpu_count() or 1)))
+    rng = np.random.default_rng(9)
+    bb = K.BLOCK_BYTES[t]
+    n = rows * cols // 256
+    w = np.frombuffer(rng.bytes(n * bb), np.uint8).reshape(n, bb).copy()
+    w[:, 0:4] = np.abs(rng.normal(0, 0.02, (n, 2))).astype(np.float16).view(np.uint8).reshape(n, 4)
+    w = w.reshape(-1)
+    x = rng.standard_normal(cols).astype(np.float32)
+    y = np.empty(rows, np.float32)
+    if ref_available():
+        ref = RefCPU()
+        kind = "reference"
+
+        def call():
+            ref.lib.katali_ggml_matvec(t, w.ctypes.data, rows, cols, x.ctypes.data, y.ctypes.data, threads, None, None, 0)
+    else:
+        o = Oracle()
+        kind = "port"
+
+        def call():
+            o.matvec_f32x(t, w, rows, cols, x, threads)
+    call()
+    t0 = time.perf_counter()
+    calls = 0
+    while time.perf_counter() - t0 < budget_s and calls < 20000:
+        call()
+        calls += 1
+    dt = time.perf_counter() - t0
+    ub = gemv_bytes(t, rows, cols)
+    return {
+        "value": calls * ub / dt / 1e9,
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": kind,
+        "sample": f"{calls} calls of the {rows}x{cols} {'Q4_K' if t == Q4_K else 'Q6_K'} GEMV (one weight matrix, "
+                  f"cache-resident as in the reference's own probe), "
+                  f"{'reference katali_ggml_matvec' if kind == 'reference' else 'oracle port of the reference AVX2 row loop'}, "
+                  f"{threads} threads, host {os.cpu_count()} logical CPUs",
+    }
+
+
+def read_traffic(workload):
+    """HBM bytes per unit from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    profile of this workload, if there is one."""
+    path = os.path.join(REPO, "profiles", f"traffic_{workload}.txt")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_unit:"):
+                return int(float(line.split(":", 1)[1]))
+    return None
+
+
+# ---------------------------------------------------------------------------
 # CPU baseline: the reference's own CPU path on a bounded sample
 # ---------------------------------------------------------------------------
 def cpu_baseline_moe(shape, budget_s=12.0):
@@ -253,8 +389,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--workload", default="moe48", choices=sorted(MOE_WORKLOADS))
+    ap.add_argument("--workload", default="moe48", choices=sorted(MOE_WORKLOADS) + sorted(GEMV_WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="run one plain copy kernel of MIB MiB before the workload (untimed), as the "
+                         "known-size reference for HBM counter profiles")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the expert-parallel "
@@ -266,16 +405,58 @@ def main():
         print(f"no usable gfx950 device: {hip.status()}", file=sys.stderr)
         sys.exit(1)
     print(f"[bench] device: {hip.status()}; workload {args.workload}", file=sys.stderr, flush=True)
-    res, shape = bench_moe(hip, args.workload, args.steps, args.warmup)
-    print(f"[bench] gpu done: {res['value']:.1f} GB/s, {res['tok_s']:.1f} tok/s", file=sys.stderr, flush=True)
-    L, hidden, ffn, n_expert, n_sel, shared = shape
+    if args.calibrate_copy > 0:
+        n = args.calibrate_copy << 20
+        a, b = hip.alloc(n), hip.alloc(n)
+        hip.memset(a, 1, n)
+        hip.copy(b, a, n)
+        hip.sync()
+        a.free()
+        b.free()
+        print(f"[bench] calibration copy: {n} bytes read + {n} bytes written", file=sys.stderr, flush=True)
+
+    traffic = read_traffic(args.workload)
+    if args.workload in MOE_WORKLOADS:
+        res, shape = bench_moe(hip, args.workload, args.steps, args.warmup)
+        L, hidden, ffn, n_expert, n_sel, shared = shape
+        unit_ms = res["ms_per_step"] / L
+        unit_bytes = res["layer_bytes"]
+        metric = "fused MoE layer HBM GB/s (% of ~8 TB/s peak) + decode tok/s, top-8 Q4_K"
+        config = {
+            "workload": f"{args.workload}: {L}-layer MoE decode, 1 token, hidden {hidden}, {n_expert} experts, "
+                        f"top-{n_sel}{' + shared expert' if shared else ''}, gate/up {hidden}->{ffn} Q4_K, "
+                        f"down {ffn}->{hidden} Q6_K, fp32 x quantized to q8_1 in the layer, new routing every "
+                        f"token from a 64-step logit ring, hipGraph per token",
+            "layers": L, "hidden": hidden, "ffn": ffn, "n_expert": n_expert, "n_sel": n_sel,
+            "shared_expert": shared, "expert_pool_gb": round(res["pool_gb"], 2),
+            "bytes_per_token": res["bytes_per_token"], "parallelism": "single GPU",
+        }
+        kernel = "MoE layer: k_moe_gu + k_moe_down (two launches per layer)"
+        extra = {"tok_s": round(res["tok_s"], 2),
+                 "eager_layer_ms_mean": round(res["kernel_ms_mean"], 5)}
+    else:
+        res, shape = bench_gemv(hip, args.workload, args.steps, args.warmup)
+        t, rows, cols, copies = shape
+        unit_ms = res["unit_ms"]
+        unit_bytes = res["unit_bytes"]
+        metric = "dense Q4_K GEMV HBM GB/s (% of ~8 TB/s peak), batch 1"
+        config = {
+            "workload": f"{args.workload}: {'Q4_K' if t == Q4_K else 'Q6_K'} {rows}x{cols} GEMV, batch 1, fp32 x "
+                        f"quantized to q8_1 inside the kernel, {copies} distinct weight copies "
+                        f"({res['pool_gb']:.2f} GB) cycled in one hipGraph",
+            "rows": rows, "cols": cols, "copies": copies, "parallelism": "single GPU",
+        }
+        kernel = "k_gemv (q8_1 activation quantized in the workgroup)"
+        extra = {}
+    print(f"[bench] gpu done: {res['value']:.1f} GB/s", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline_moe(shape)
+        cpu = cpu_baseline_moe(shape) if args.workload in MOE_WORKLOADS else cpu_baseline_gemv(shape)
         print(f"[bench] cpu baseline: {cpu['value']:.2f} GB/s ({cpu['kind']}, {cpu['cores']} threads)",
               file=sys.stderr, flush=True)
+    achieved = unit_bytes / (unit_ms / 1e3) / 1e9
     line = {
-        "metric": "fused MoE layer HBM GB/s (% of ~8 TB/s peak) + decode tok/s, top-8 Q4_K",
+        "metric": metric,
         "value": round(res["value"], 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -287,27 +468,19 @@ def main():
         "vs_baseline": None,
         "dtype": "q4_k/q6_k weights x q8_1 activations (int8 dot4, fp32 scales)",
         "data": "synthetic (random Q4_K/Q6_K blocks with d,dmin ~ |N(0,0.02)|; N(0,1) activations and router logits)",
-        "config": {
-            "workload": f"{args.workload}: {L}-layer MoE decode, 1 token, hidden {hidden}, {n_expert} experts, "
-                        f"top-{n_sel}{' + shared expert' if shared else ''}, gate/up {hidden}->{ffn} Q4_K, "
-                        f"down {ffn}->{hidden} Q6_K, new routing every token, hipGraph per token",
-            "layers": L, "hidden": hidden, "ffn": ffn, "n_expert": n_expert, "n_sel": n_sel,
-            "shared_expert": shared, "expert_pool_gb": round(res["pool_gb"], 2),
-            "bytes_per_token": res["bytes_per_token"], "parallelism": "single GPU",
-        },
-        "tok_s": round(res["tok_s"], 2),
+        "config": config,
+        **extra,
         "hbm_frac": round(res["value"] / HBM_PEAK_GBS, 4),
         "roofline": {
             "bound": "hbm",
-            "achieved": round(res["kernel_gbs"], 1),
+            "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(res["kernel_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "MoE layer (k_moe_gu + k_moe_down, one graph node pair per layer)",
-            "bytes_per_launch": res["layer_bytes"],
-            "launch_ms_mean": round(res["kernel_ms_mean"], 5),
-            "launch_ms_median": round(res["kernel_ms_median"], 5),
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel": kernel,
+            "bytes_per_unit": unit_bytes,
+            "unit_ms": round(unit_ms, 5),
         },
         "cpu_baseline": cpu,
     }

@@ -155,6 +155,9 @@ class KataliHip:
     def sync(self) -> None:
         self.check(self.lib.katali_hip_sync())
 
+    def memset(self, buf: DeviceBuffer, value: int, nbytes: int) -> None:
+        self.check(self.lib.katali_hip_memset(buf.ptr, value, nbytes))
+
     # -- compute ----------------------------------------------------------
     def quantize_q8_1(self, x: DeviceBuffer, n: int, out: DeviceBuffer) -> None:
         self.check(self.lib.katali_hip_quantize_q8_1(x.ptr, n, out.ptr))

@@ -1,0 +1,171 @@
+"""Profile one bench.py workload with rocprofv3 and write its summary.
+
+    python katali-lab_amd/profile_bench.py --workload moe48 --out DIR [--steps 8]
+    python katali-lab_amd/profile_bench.py --workload moe48 --out DIR --summarize-only
+
+Three runs of bench.py under rocprofv3 (each a child process; rocprofv3
+runs from /tmp with TMPDIR=/tmp):
+  1. --kernel-trace --stats: per-kernel call counts and average durations;
+  2. --pmc FETCH_SIZE and 3. --pmc WRITE_SIZE: HBM KiB per dispatch.
+Every run starts with bench.py --calibrate-copy 256, one plain copy kernel of
+256 MiB read + 256 MiB written; the counter value that copy reports fixes the
+scale factor between counter KiB and bytes. Writes profiles/<name>.md (the
+commands, the kernel table and the traffic per workload unit) and
+profiles/traffic_<workload>.txt (read by bench.py for roofline.traffic).
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import glob
+import os
+import sqlite3
+import subprocess
+import sys
+from collections import defaultdict
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+COPY_MIB = 256
+KERNELS = {
+    "moe48": ("k_moe_gu", "k_moe_down"),
+    "moe40cold": ("k_moe_gu", "k_moe_down"),
+    "gemv6144": ("k_gemv",),
+}
+UNITS_PER_STEP = {"moe48": 48, "moe40cold": 40, "gemv6144": 144}
+
+
+def run(cmd, log):
+    print("[profile] " + " ".join(cmd), flush=True)
+    env = dict(os.environ, TMPDIR="/tmp")
+    with open(log, "w") as f:
+        p = subprocess.run(cmd, cwd="/tmp", env=env, stdout=f, stderr=subprocess.STDOUT, timeout=600)
+    print(f"[profile] exit {p.returncode}", flush=True)
+    return p.returncode
+
+
+def rows_from(outdir, stem):
+    """Rows of a rocprofv3 CSV (any *<stem>.csv under outdir), else None."""
+    files = glob.glob(os.path.join(outdir, "**", f"*{stem}.csv"), recursive=True)
+    if not files:
+        return None
+    with open(files[0]) as f:
+        return list(csv.DictReader(f))
+
+
+def db_rows(outdir, query):
+    files = glob.glob(os.path.join(outdir, "**", "*.db"), recursive=True)
+    if not files:
+        return []
+    return sqlite3.connect(files[0]).execute(query).fetchall()
+
+
+def kernel_stats(outdir):
+    rows = rows_from(outdir, "kernel_stats")
+    out = {}
+    if rows:
+        for r in rows:
+            out[r["Name"]] = (int(r["Calls"]), float(r["AverageNs"]))
+        return out
+    acc = defaultdict(list)
+    for name, dur in db_rows(outdir, "select kernel_name, duration from kernels"):
+        acc[name].append(dur)
+    return {k: (len(v), sum(v) / len(v)) for k, v in acc.items()}
+
+
+def counter_means(outdir, counter):
+    rows = rows_from(outdir, "counter_collection")
+    acc = defaultdict(list)
+    if rows:
+        for r in rows:
+            if r.get("Counter_Name") == counter:
+                acc[r["Kernel_Name"]].append(float(r["Counter_Value"]))
+    else:
+        for name, cname, v in db_rows(outdir, "select kernel_name, counter_name, value from counters_collection"):
+            if cname == counter:
+                acc[name].append(v)
+    return {k: (len(v), sum(v) / len(v)) for k, v in acc.items()}
+
+
+def pick(d, sub):
+    hits = [(k, v) for k, v in d.items() if sub in k]
+    return hits
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--workload", default="moe48", choices=sorted(KERNELS))
+    ap.add_argument("--steps", type=int, default=8)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--out", required=True, help="directory for the raw rocprofv3 output")
+    ap.add_argument("--summarize-only", action="store_true", help="parse an existing --out tree, run nothing")
+    args = ap.parse_args()
+    wl = args.workload
+    out = os.path.join(args.out, wl)
+    os.makedirs(out, exist_ok=True)
+    bench = [sys.executable, os.path.join(REPO, "bench.py"), "--workload", wl, "--steps", str(args.steps),
+             "--warmup", str(args.warmup), "--no-cpu-baseline", "--calibrate-copy", str(COPY_MIB)]
+    cmds = {
+        "trace": ["rocprofv3", "--kernel-trace", "--stats", "--output-format", "csv", "-d", os.path.join(out, "trace"),
+                  "-o", "run", "--"] + bench,
+        "fetch": ["rocprofv3", "--pmc", "FETCH_SIZE", "--output-format", "csv", "-d", os.path.join(out, "fetch"),
+                  "-o", "run", "--"] + bench,
+        "write": ["rocprofv3", "--pmc", "WRITE_SIZE", "--output-format", "csv", "-d", os.path.join(out, "write"),
+                  "-o", "run", "--"] + bench,
+    }
+    for k, c in cmds.items():
+        if args.summarize_only:
+            break
+        if run(c, os.path.join(out, f"{k}.log")) not in (0, 139):   # 139: profiler's own exit after results
+            sys.exit(f"rocprofv3 {k} run failed (see {out}/{k}.log)")
+    stats = kernel_stats(os.path.join(out, "trace"))
+    fetch = counter_means(os.path.join(out, "fetch"), "FETCH_SIZE")
+    write = counter_means(os.path.join(out, "write"), "WRITE_SIZE")
+    copy_bytes = COPY_MIB << 20
+    cf = pick(fetch, "k_copy")
+    cw = pick(write, "k_copy")
+    if not cf or not cw:
+        sys.exit("calibration copy kernel missing from the counter runs")
+    f_scale = copy_bytes / cf[0][1][1]     # bytes per counter unit
+    w_scale = copy_bytes / cw[0][1][1]
+    unit_fetch = unit_write = unit_time = 0.0
+    table = []
+    for sub in KERNELS[wl]:
+        for name, (calls, avg) in pick(stats, sub):
+            fk = pick(fetch, sub)
+            wk = pick(write, sub)
+            fb = fk[0][1][1] * f_scale if fk else float("nan")
+            wb = wk[0][1][1] * w_scale if wk else float("nan")
+            table.append((name, calls, avg / 1e3, fb, wb))
+            unit_fetch += fb
+            unit_write += wb
+            unit_time += avg / 1e3
+    traffic = unit_fetch + unit_write
+    md = os.path.join(REPO, "profiles", f"{'_'.join(KERNELS[wl])}_{wl}.md")
+    os.makedirs(os.path.dirname(md), exist_ok=True)
+    with open(md, "w") as f:
+        f.write(f"# rocprofv3 summary: {wl}\n\n")
+        f.write(f"Made by `python katali-lab_amd/profile_bench.py --workload {wl} --steps {args.steps} "
+                f"--warmup {args.warmup} --out <out>`, which runs (from /tmp, TMPDIR=/tmp; paths relative to the "
+                f"repository root):\n\n")
+        for k, c in cmds.items():
+            txt = " ".join(c).replace(out, "<out>").replace(REPO + "/", "").replace(sys.executable, "python3")
+            f.write(f"- {k}: `{txt}`\n")
+        f.write(f"\nCalibration: one k_copy of {copy_bytes} B read + {copy_bytes} B written reads "
+                f"FETCH_SIZE {cf[0][1][1]:.1f} and WRITE_SIZE {cw[0][1][1]:.1f} (KiB units): "
+                f"{f_scale:.2f} and {w_scale:.2f} bytes per counter unit.\n\n")
+        f.write("| kernel | calls | avg us | HBM fetch B/dispatch | HBM write B/dispatch |\n|---|---|---|---|---|\n")
+        for name, calls, us, fb, wb in table:
+            f.write(f"| {name} | {calls} | {us:.2f} | {fb:,.0f} | {wb:,.0f} |\n")
+        f.write(f"\nPer workload unit ({'layer' if 'moe' in wl else 'GEMV'}): kernel time {unit_time:.2f} us, "
+                f"HBM traffic {traffic:,.0f} B (fetch {unit_fetch:,.0f} + write {unit_write:,.0f}).\n\n")
+        f.write("All kernels in the trace run (calls, avg us):\n\n")
+        for name, (calls, avg) in sorted(stats.items(), key=lambda kv: -kv[1][0] * kv[1][1]):
+            f.write(f"- {name[:110]}: {calls}, {avg / 1e3:.2f}\n")
+    with open(os.path.join(REPO, "profiles", f"traffic_{wl}.txt"), "w") as f:
+        f.write(f"# HBM bytes per {'MoE layer' if 'moe' in wl else 'GEMV'} from {os.path.basename(md)}\n")
+        f.write(f"traffic_bytes_per_unit: {traffic:.0f}\n")
+    print(open(md).read())
+
+
+if __name__ == "__main__":
+    main()
