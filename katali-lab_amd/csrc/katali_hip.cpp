@@ -287,7 +287,7 @@ int katali_hip_sync(void) {
         if (e != hipSuccess) return hip_fail(e, "read error word");
         if (err) {
             (void)hipMemset(g_err_dev, 0, 4);
-            return fail(KATALI_HIP_E_INVALID, "MoE expert id outside [0, n_expert) (bad ids or non-finite logits)");
+            return fail(KATALI_HIP_E_INVALID, "MoE expert id outside [0, n_expert) in the explicit routing");
         }
     }
     return KATALI_HIP_OK;

@@ -672,6 +672,7 @@ bool moe_shape_supported(uint32_t gate_type, uint32_t down_type, uint32_t hidden
 }
 
 hipError_t launch_moe(const MoeArgs &a, hipStream_t s) {
+    if (a.n_expert > MAX_EXPERT || a.n_sel > MAX_SEL) return hipErrorInvalidValue;
     const uint32_t n_slots = (uint32_t)a.n_sel + (a.has_shared ? 1u : 0u);
     hipError_t e;
     switch (a.hidden / 256) {
