@@ -1,6 +1,6 @@
 """Benchmark of the quantized expert-GEMV path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload moe48|moe40cold|gemv6144]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload moe48|moe40cold|gemv6144|qwen8b]
 
 Workloads:
   moe48     (default) one decode token through 48 fused MoE layers,
@@ -15,6 +15,12 @@ in one hipGraph per token; a step is one replay.
   gemv6144  dense Q4_K 6144x2048 GEMV, batch 1, fp32 x quantized to q8_1
             inside the kernel; 144 distinct weight copies (1.02 GB) are cycled
             so every GEMV reads cold weights; a step is one pass over them.
+  qwen8b    dense Qwen3-8B-shaped decode GEMV chain, 36 layers, hidden 4096,
+            q/o 4096x4096 and k 1024x4096 Q4_K, v 1024x4096 Q6_K, SwiGLU
+            12288 (gate/up Q4_K, down Q6_K); per layer q,k,v = W x, o = Wo q
+            (q stands in for the attention output, which is not a GEMV),
+            FFN(o) through the MoE kernels with the shared expert only; every
+            layer reads its own N(0,1) x; a step is one token (one replay).
 
 Printed: ONE JSON line. value = algorithmic HBM GB/s of the whole token
 (selected expert weights + q8_1 activation + fp32 output, per layer) with
@@ -174,6 +180,102 @@ def bench_moe(hip, name, steps, warmup, ring=64):
 
 
 # ---------------------------------------------------------------------------
+# Dense decode chain (Qwen3-8B shapes)
+# ---------------------------------------------------------------------------
+DENSE_WORKLOADS = {
+    # name: layers, hidden, q_rows, kv_rows, ffn
+    "qwen8b": (36, 4096, 4096, 1024, 12288),
+}
+
+
+def dense_layer_bytes(hidden, q_rows, kv_rows, ffn):
+    rb4, rb6 = row_bytes(Q4_K, hidden), row_bytes(Q6_K, hidden)
+    w = (q_rows + kv_rows) * rb4 + kv_rows * rb6 + hidden * row_bytes(Q4_K, q_rows) \
+        + 2 * ffn * rb4 + hidden * row_bytes(Q6_K, ffn)
+    act = 4 * (hidden * 4 + 2 * hidden)   # x, q, o, y reads/writes (fp32) plus k, v outputs
+    return w + act, w
+
+
+def bench_dense(hip, name, steps, warmup):
+    L, hidden, q_rows, kv_rows, ffn = DENSE_WORKLOADS[name]
+    seed = 500
+    layers = []
+
+    def filled(t, rows, cols):
+        nonlocal seed
+        b = hip.alloc(rows * row_bytes(t, cols))
+        hip.synth_fill(t, b, rows * cols // 256, seed)
+        seed += 1
+        return b
+
+    for _ in range(L):
+        wq, wk, wv = filled(Q4_K, q_rows, hidden), filled(Q4_K, kv_rows, hidden), filled(Q6_K, kv_rows, hidden)
+        wo = filled(Q4_K, hidden, q_rows)
+        g, u, d = filled(Q4_K, ffn, hidden), filled(Q4_K, ffn, hidden), filled(Q6_K, hidden, ffn)
+        layers.append((wq, wk, wv, wo, g, u, d))
+    x = hip.alloc(L * hidden * 4)
+    hip.synth_normal(x, L * hidden, 91)
+    q, k, v, o, y = (hip.alloc(L * n * 4) for n in (q_rows, kv_rows, kv_rows, hidden, hidden))
+
+    class View:
+        def __init__(self, ptr):
+            self.ptr = ptr
+
+    def at(buf, li, n):
+        return View(buf.ptr + li * n * 4)
+
+    descs = [hip.moe_desc(hidden, ffn, 0, None, None, None, shared=(g, u, d)) for (_, _, _, _, g, u, d) in layers]
+    route = hip.moe_route(0)
+
+    def token():
+        for li, (wq, wk, wv, wo, g, u, d) in enumerate(layers):
+            xl = at(x, li, hidden)
+            hip.matvec_dp4a(Q4_K, wq, q_rows, hidden, xl, at(q, li, q_rows))
+            hip.matvec_dp4a(Q4_K, wk, kv_rows, hidden, xl, at(k, li, kv_rows))
+            hip.matvec_dp4a(Q6_K, wv, kv_rows, hidden, xl, at(v, li, kv_rows))
+            hip.matvec_dp4a(Q4_K, wo, hidden, q_rows, at(q, li, q_rows), at(o, li, hidden))
+            hip.moe_layer(descs[li], route, at(y, li, hidden), x=at(o, li, hidden))
+
+    token()
+    hip.sync()
+    hip.graph_begin()
+    token()
+    graph = hip.graph_end()
+    for _ in range(warmup):
+        hip.graph_launch(graph)
+    hip.sync()
+    e0, e1 = hip.event(), hip.event()
+    t0 = time.perf_counter()
+    hip.record(e0)
+    for _ in range(steps):
+        hip.graph_launch(graph)
+    hip.record(e1)
+    ms = hip.elapsed_ms(e0, e1)
+    wall = time.perf_counter() - t0
+    hip.sync()
+    for e in (e0, e1):
+        hip.event_destroy(e)
+    hip.graph_destroy(graph)
+    layer_bytes, weight_bytes = dense_layer_bytes(hidden, q_rows, kv_rows, ffn)
+    s_per_tok = ms / 1e3 / steps
+    res = {
+        "ms_per_step": ms / steps,
+        "wall_ms_per_step": wall * 1e3 / steps,
+        "value": L * layer_bytes / s_per_tok / 1e9,
+        "tok_s": 1.0 / s_per_tok,
+        "layer_bytes": layer_bytes,
+        "bytes_per_token": L * layer_bytes,
+        "weights_gb": L * weight_bytes / 1e9,
+    }
+    for bufs in layers:
+        for b in bufs:
+            b.free()
+    for b in (x, q, k, v, o, y):
+        b.free()
+    return res, (L, hidden, q_rows, kv_rows, ffn)
+
+
+# ---------------------------------------------------------------------------
 # Dense GEMV over a cold rotating pool
 # ---------------------------------------------------------------------------
 GEMV_WORKLOADS = {
@@ -287,6 +389,72 @@ def cpu_baseline_gemv(shape, budget_s=12.0):
     }
 
 
+def cpu_baseline_dense(shape, budget_s=12.0):
+    """The reference CPU path on the same per-layer GEMV chain (fused q/k/v,
+    o, fused gate/up, SiLU-GLU, down), distinct weights per layer."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    from oracle import MatvecJob, RefCPU, ref_available
+    if not ref_available():
+        return None
+    L, hidden, q_rows, kv_rows, ffn = shape
+    threads = int(os.environ.get("KATALI_BENCH_CPU_THREADS", min(16, os.cpu_count() or 1)))
+    rng = np.random.default_rng(13)
+    n_layers = 4   # distinct weights for 4 layers (0.49 GB), cycled
+
+    def blocks(t, rows, cols):
+        bb = K.BLOCK_BYTES[t]
+        n = rows * cols // 256
+        b = np.frombuffer(rng.bytes(n * bb), np.uint8).reshape(n, bb).copy()
+        d = np.abs(rng.normal(0, 0.02, (n, 2))).astype(np.float16).view(np.uint8)
+        if t == Q4_K:
+            b[:, 0:4] = d.reshape(n, 4)
+        else:
+            b[:, 208:210] = d[:, :2]
+        return b.reshape(-1)
+
+    ws = [(blocks(Q4_K, q_rows, hidden), blocks(Q4_K, kv_rows, hidden), blocks(Q6_K, kv_rows, hidden),
+           blocks(Q4_K, hidden, q_rows), blocks(Q4_K, ffn, hidden), blocks(Q4_K, ffn, hidden),
+           blocks(Q6_K, hidden, ffn)) for _ in range(n_layers)]
+    ref = RefCPU()
+    x = rng.standard_normal(hidden).astype(np.float32)
+    q, k, v = np.empty(q_rows, np.float32), np.empty(kv_rows, np.float32), np.empty(kv_rows, np.float32)
+    o, y = np.empty(hidden, np.float32), np.empty(hidden, np.float32)
+    g, u = np.empty(ffn, np.float32), np.empty(ffn, np.float32)
+    sums = np.empty(max(hidden, q_rows) // 256 * 64, np.float32)
+
+    def layer(li):
+        wq, wk, wv, wo, wg, wu, wd = ws[li % n_layers]
+        ref.matvec_fused([MatvecJob(Q4_K, wq.ctypes.data, q_rows, q.ctypes.data, 0),
+                          MatvecJob(Q4_K, wk.ctypes.data, kv_rows, k.ctypes.data, 1),
+                          MatvecJob(Q6_K, wv.ctypes.data, kv_rows, v.ctypes.data, 2)], hidden, x, threads, sums)
+        ref.lib.katali_ggml_matvec(Q4_K, wo.ctypes.data, hidden, q_rows, q.ctypes.data, o.ctypes.data, threads,
+                                   None, None, 0)
+        ref.matvec_fused([MatvecJob(Q4_K, wg.ctypes.data, ffn, g.ctypes.data, 6),
+                          MatvecJob(Q4_K, wu.ctypes.data, ffn, u.ctypes.data, 7)], hidden, o, threads, sums)
+        h = ref.silu_mul(g, u)
+        ref.lib.katali_ggml_matvec(Q6_K, wd.ctypes.data, hidden, ffn, h.ctypes.data, y.ctypes.data, threads,
+                                   None, None, 0)
+
+    layer(0)
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < budget_s and n < 50 * L:
+        layer(n)
+        n += 1
+    dt = time.perf_counter() - t0
+    lb, _ = dense_layer_bytes(hidden, q_rows, kv_rows, ffn)
+    return {
+        "value": n * lb / dt / 1e9,
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "reference",
+        "tok_s": (n / L) / dt,
+        "sample": f"{n} layers ({n / L:.2f} tokens) of the same GEMV chain, 4 layers of distinct weights cycled "
+                  f"(0.49 GB, DRAM-cold), reference katali_ggml_matvec_fused + silu_mul_avx2 + katali_ggml_matvec, "
+                  f"{threads} threads, host {os.cpu_count()} logical CPUs",
+    }
+
+
 def read_traffic(workload):
     """HBM bytes per unit from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
     profile of this workload, if there is one."""
@@ -389,7 +557,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--workload", default="moe48", choices=sorted(MOE_WORKLOADS) + sorted(GEMV_WORKLOADS))
+    ap.add_argument("--workload", default="moe48",
+                    choices=sorted(MOE_WORKLOADS) + sorted(GEMV_WORKLOADS) + sorted(DENSE_WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="run one plain copy kernel of MIB MiB before the workload (untimed), as the "
@@ -434,6 +603,22 @@ def main():
         kernel = "MoE layer: k_moe_gu + k_moe_down (two launches per layer)"
         extra = {"tok_s": round(res["tok_s"], 2),
                  "eager_layer_ms_mean": round(res["kernel_ms_mean"], 5)}
+    elif args.workload in DENSE_WORKLOADS:
+        res, shape = bench_dense(hip, args.workload, args.steps, args.warmup)
+        L, hidden, q_rows, kv_rows, ffn = shape
+        unit_ms = res["ms_per_step"] / L
+        unit_bytes = res["layer_bytes"]
+        metric = "dense decode GEMV chain HBM GB/s (% of ~8 TB/s peak) + decode tok/s, batch 1"
+        config = {
+            "workload": f"{args.workload}: {L}-layer Qwen3-8B-shaped decode GEMV chain, hidden {hidden}, "
+                        f"q/o {q_rows}x{hidden} and k {kv_rows}x{hidden} Q4_K, v {kv_rows}x{hidden} Q6_K, "
+                        f"SwiGLU {ffn} (gate/up Q4_K, down Q6_K), q8_1 activations quantized in-kernel, "
+                        f"6 launches per layer, hipGraph per token (attention math not included; LM head not included)",
+            "layers": L, "hidden": hidden, "ffn": ffn, "weights_gb": round(res["weights_gb"], 2),
+            "bytes_per_token": res["bytes_per_token"], "parallelism": "single GPU",
+        }
+        kernel = "decode layer: q, k, v, o GEMVs + k_moe_gu + k_moe_down (shared expert only)"
+        extra = {"tok_s": round(res["tok_s"], 2)}
     else:
         res, shape = bench_gemv(hip, args.workload, args.steps, args.warmup)
         t, rows, cols, copies = shape
@@ -451,7 +636,12 @@ def main():
     print(f"[bench] gpu done: {res['value']:.1f} GB/s", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline_moe(shape) if args.workload in MOE_WORKLOADS else cpu_baseline_gemv(shape)
+        if args.workload in MOE_WORKLOADS:
+            cpu = cpu_baseline_moe(shape)
+        elif args.workload in DENSE_WORKLOADS:
+            cpu = cpu_baseline_dense(shape)
+        else:
+            cpu = cpu_baseline_gemv(shape)
         print(f"[bench] cpu baseline: {cpu['value']:.2f} GB/s ({cpu['kind']}, {cpu['cores']} threads)",
               file=sys.stderr, flush=True)
     achieved = unit_bytes / (unit_ms / 1e3) / 1e9

@@ -114,7 +114,10 @@ typedef struct KataliHipMoe {
 
 typedef struct KataliHipMoeRoute {
     uint32_t struct_size;                  /* sizeof(KataliHipMoeRoute) */
-    int32_t n_sel;                         /* experts per token, 1..16 */
+    int32_t n_sel;                         /* routed experts per token, 0..16;
+                                              0 = the shared expert alone (a
+                                              dense SiLU-GLU FFN; routed experts,
+                                              logits and ids may be NULL) */
     /* Either router logits (the kernel takes the top n_sel, largest first,
      * lower index on ties, and renormalises softmax over them) ... */
     const float *logits;                   /* device [n_expert] or NULL */

@@ -160,15 +160,21 @@ int moe_impl(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, 
                     "hidden in {256,512,1024,2048,4096}, ffn a multiple of 256 (<= 16384)",
                     m->gate_type, m->up_type, m->down_type, m->hidden, m->ffn);
     if (m->ffn > 16384) return fail(KATALI_HIP_E_INVALID, "MoE ffn=%u above 16384", m->ffn);
-    if (!m->n_expert || m->n_expert > 512) return fail(KATALI_HIP_E_INVALID, "n_expert=%u", m->n_expert);
-    if (!m->gate_exps || !m->up_exps || !m->down_exps || !y) return fail(KATALI_HIP_E_INVALID, "null buffer");
+    if (!y) return fail(KATALI_HIP_E_INVALID, "null output");
     if ((x == nullptr) == (xq == nullptr)) return fail(KATALI_HIP_E_INVALID, "give exactly one of x_dev / xq8_dev");
-    if (r->n_sel < 1 || r->n_sel > 16 || (uint32_t)r->n_sel > m->n_expert)
-        return fail(KATALI_HIP_E_INVALID, "n_sel=%d", r->n_sel);
-    if (!r->logits && (!r->ids || !r->weights)) return fail(KATALI_HIP_E_INVALID, "need logits or ids+weights");
     const bool shared = m->gate_shexp || m->up_shexp || m->down_shexp;
     if (shared && !(m->gate_shexp && m->up_shexp && m->down_shexp))
         return fail(KATALI_HIP_E_INVALID, "shared expert needs gate, up and down");
+    if (r->n_sel < 0 || r->n_sel > 16) return fail(KATALI_HIP_E_INVALID, "n_sel=%d", r->n_sel);
+    if (r->n_sel == 0) {
+        // the shared expert alone: a dense SiLU-GLU FFN through the same kernels
+        if (!shared) return fail(KATALI_HIP_E_INVALID, "n_sel=0 needs the shared expert");
+    } else {
+        if (!m->n_expert || m->n_expert > 512) return fail(KATALI_HIP_E_INVALID, "n_expert=%u", m->n_expert);
+        if ((uint32_t)r->n_sel > m->n_expert) return fail(KATALI_HIP_E_INVALID, "n_sel=%d", r->n_sel);
+        if (!m->gate_exps || !m->up_exps || !m->down_exps) return fail(KATALI_HIP_E_INVALID, "null buffer");
+        if (!r->logits && (!r->ids || !r->weights)) return fail(KATALI_HIP_E_INVALID, "need logits or ids+weights");
+    }
     const uint32_t n_slots = (uint32_t)r->n_sel + (shared ? 1 : 0);
     const size_t hq8_bytes = (size_t)n_slots * (m->ffn / 32) * 36;
     if ((rc = moe_scratch(hq8_bytes))) return rc;

@@ -342,12 +342,14 @@ __global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
     float lv[C];
     int32_t eid = -1;
     float ew = 0.0f;
-    if (a.logits) {
-        load_keys<C>(a, lv);
-    } else {
-        const uint32_t r = min(lane, (uint32_t)a.n_sel - 1);
-        eid = a.ids[r];
-        ew = a.wts[r];
+    if (a.n_sel > 0) {
+        if (a.logits) {
+            load_keys<C>(a, lv);
+        } else {
+            const uint32_t r = min(lane, (uint32_t)a.n_sel - 1);
+            eid = a.ids[r];
+            ew = a.wts[r];
+        }
     }
     constexpr int XTASKS = 64 * NB;            // quantizer lane tasks (8 per 32-block)
     constexpr int XPT = (XTASKS + 255) / 256;
@@ -366,7 +368,7 @@ __global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
         }
     }
     float route_l = 0.0f;
-    if (a.logits) {
+    if (a.logits && a.n_sel > 0) {
         const WaveRoute r = wave_topk<C>(a, lv);
         eid = r.id;
         route_l = r.logit;
@@ -414,7 +416,7 @@ __global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
 #pragma unroll
     for (int k = 0; k < LPG; k++) q[k] = ld16(chunk(0, k));
     if (publisher) {
-        if (a.logits) ew = route_weight(route_l, a.n_sel);
+        if (a.logits && a.n_sel > 0) ew = route_weight(route_l, a.n_sel);
         route_publish(a, eid, ew);
     }
 
@@ -524,7 +526,9 @@ __global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
 
 // ---------------------------------------------------------------------------
 // Kernel B: a tile of TR output rows x n_slots down rows per workgroup; one
-// lane-slot (S = QD::IPB lanes) per (row, slot) pair. Order of work: the
+// lane-slot of S = QD::IPB * P lanes per (row, slot) pair: lane s takes item
+// s % IPB of blocks s / IPB + P*i (i < IPL), so long rows (a dense FFN's
+// 12288-wide down projection) spread over up to 64 lanes. Order of work: the
 // routing and the q8_1 h loads (both written by kernel A, so L2/MALL hits),
 // then, once the routing is in, every down-weight load; h is staged into LDS
 // while the weights stream. Loads are clamped rather than guarded so the
@@ -576,7 +580,7 @@ __device__ __forceinline__ void stage_h(uint8_t *hl, uint32_t ffn, uint32_t ntas
     }
 }
 
-template <class QD, int IPL>
+template <class QD, int IPL, int P>
 __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a, uint32_t tr, uint32_t n_slots) {
     extern __shared__ __align__(16) uint8_t lds[];
     const LdsB L = lds_b(a.ffn, n_slots, tr);
@@ -588,13 +592,14 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a, uint32_t tr, uint32
     HLoad hv;
     load_h(a.hq8, ntask, 0, hv);
 
-    const uint32_t S = QD::IPB;
+    constexpr uint32_t S = QD::IPB * P;
     const uint32_t ls = tid / S, s = tid % S;
+    const uint32_t item = s % QD::IPB, sub = s / QD::IPB;
     const uint32_t row0 = blockIdx.x * tr;
     const uint32_t nrows = row0 + tr <= a.hidden ? tr : a.hidden - row0;
     const uint32_t npairs = nrows * n_slots;
     const uint64_t rbd = (uint64_t)(a.ffn / 256) * QD::BB;
-    const uint32_t ipl = a.ffn / 256;
+    const uint32_t nbk = a.ffn / 256;
     const bool active = ls < npairs;
     const uint32_t lc = min(ls, npairs - 1);   // idle lane-slots load a real pair and drop it
     const uint32_t sl = lc % n_slots, r = lc / n_slots;
@@ -604,7 +609,8 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a, uint32_t tr, uint32
     typename QD::Raw raw[IPL > 0 ? IPL : 1];
     if constexpr (IPL > 0) {
 #pragma unroll
-        for (int i = 0; i < IPL; i++) raw[i] = QD::load(rp + i * QD::BB, (int)s);
+        for (int i = 0; i < IPL; i++)   // clamped: a block past the row is loaded and dropped
+            raw[i] = QD::load(rp + min(sub + P * i, nbk - 1) * QD::BB, (int)item);
     }
     stage_h(lds + L.hacts, a.ffn, ntask, 0, hv);
     for (uint32_t first = HT * 256; first < ntask; first += HT * 256) {
@@ -617,12 +623,16 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a, uint32_t tr, uint32
         const Act act = act_carve(lds + L.hacts + sl * act_bytes(a.ffn), a.ffn);
         if constexpr (IPL > 0) {
 #pragma unroll
-            for (int i = 0; i < IPL; i++) x += QD::dot_q8(raw[i], (int)s, act, i);
+            for (int i = 0; i < IPL; i++) {
+                const uint32_t b = sub + P * i;
+                const float v = QD::dot_q8(raw[i], (int)item, act, min(b, nbk - 1));
+                x += b < nbk ? v : 0.0f;
+            }
         } else {
-            for (uint32_t i = 0; i < ipl; i++) x += QD::dot_q8(QD::load(rp + i * QD::BB, (int)s), (int)s, act, i);
+            for (uint32_t b = sub; b < nbk; b += P) x += QD::dot_q8(QD::load(rp + b * QD::BB, (int)item), (int)item, act, b);
         }
     }
-    x = group_sum<QD::IPB>(x);
+    x = group_sum<S>(x);
     float *res = (float *)(lds + L.res);
     if (active && s == 0) res[ls] = x;
     __syncthreads();
@@ -654,14 +664,46 @@ static hipError_t go_a(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <class QD, int IPL>
+template <class QD, int IPL, int P>
 static hipError_t go_b(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
-    const uint32_t lane_slots = 256 / QD::IPB;
+    const uint32_t lane_slots = 256 / (QD::IPB * P);
     uint32_t tr = lane_slots / n_slots;
     if (tr < 1) tr = 1;
     const LdsB L = lds_b(a.ffn, n_slots, tr);
-    hipLaunchKernelGGL((k_moe_down<QD, IPL>), dim3((a.hidden + tr - 1) / tr), dim3(256), L.total, s, a, tr, n_slots);
+    hipLaunchKernelGGL((k_moe_down<QD, IPL, P>), dim3((a.hidden + tr - 1) / tr), dim3(256), L.total, s, a, tr, n_slots);
     return hipGetLastError();
+}
+
+// P = lanes-per-pair multiplier: the smallest power of two that brings a
+// lane's blocks (IPL = ceil(nb / P)) to at most 4 while a workgroup still
+// holds every slot of at least one output row.
+template <class QD>
+static hipError_t go_b_any(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
+    const uint32_t nb = a.ffn / 256;
+    uint32_t p = 1;
+    while ((nb + p - 1) / p > 4 && QD::IPB * 4 * p <= 64 && QD::IPB * 4 * p * n_slots <= 256) p *= 4;
+    const uint32_t ipl = (nb + p - 1) / p;
+    if (QD::IPB * p * n_slots > 256 || ipl > 4) return go_b<QD, 0, 1>(a, n_slots, s);
+    const uint32_t key = p * 8 + ipl;
+    switch (key) {
+        case 1 * 8 + 1: return go_b<QD, 1, 1>(a, n_slots, s);
+        case 1 * 8 + 2: return go_b<QD, 2, 1>(a, n_slots, s);
+        case 1 * 8 + 3: return go_b<QD, 3, 1>(a, n_slots, s);
+        case 1 * 8 + 4: return go_b<QD, 4, 1>(a, n_slots, s);
+        case 4 * 8 + 2: return go_b<QD, 2, 4>(a, n_slots, s);
+        case 4 * 8 + 3: return go_b<QD, 3, 4>(a, n_slots, s);
+        case 4 * 8 + 4: return go_b<QD, 4, 4>(a, n_slots, s);
+        default: break;
+    }
+    if constexpr (QD::IPB * 16 <= 64) {
+        switch (key) {
+            case 16 * 8 + 2: return go_b<QD, 2, 16>(a, n_slots, s);
+            case 16 * 8 + 3: return go_b<QD, 3, 16>(a, n_slots, s);
+            case 16 * 8 + 4: return go_b<QD, 4, 16>(a, n_slots, s);
+            default: break;
+        }
+    }
+    return go_b<QD, 0, 1>(a, n_slots, s);
 }
 
 bool moe_shape_supported(uint32_t gate_type, uint32_t down_type, uint32_t hidden, uint32_t ffn) {
@@ -684,22 +726,7 @@ hipError_t launch_moe(const MoeArgs &a, hipStream_t s) {
         default: return hipErrorInvalidValue;
     }
     if (e != hipSuccess) return e;
-    const uint32_t nbd = a.ffn / 256;
-    if (a.down_type == T_Q6_K) {
-        switch (nbd) {
-            case 1: return go_b<Q6K, 1>(a, n_slots, s);
-            case 2: return go_b<Q6K, 2>(a, n_slots, s);
-            case 3: return go_b<Q6K, 3>(a, n_slots, s);
-            case 4: return go_b<Q6K, 4>(a, n_slots, s);
-            default: return go_b<Q6K, 0>(a, n_slots, s);
-        }
-    }
-    switch (nbd) {
-        case 1: return go_b<Q4K, 1>(a, n_slots, s);
-        case 2: return go_b<Q4K, 2>(a, n_slots, s);
-        case 3: return go_b<Q4K, 3>(a, n_slots, s);
-        default: return go_b<Q4K, 0>(a, n_slots, s);
-    }
+    return a.down_type == T_Q6_K ? go_b_any<Q6K>(a, n_slots, s) : go_b_any<Q4K>(a, n_slots, s);
 }
 
 }  // namespace kq

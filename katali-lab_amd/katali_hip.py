@@ -177,8 +177,9 @@ class KataliHip:
     @staticmethod
     def moe_desc(hidden, ffn, n_expert, gate, up, down, gate_type=Q4_K, down_type=Q6_K,
                  shared=None) -> KataliHipMoe:
+        p = lambda b: None if b is None else b.ptr  # noqa: E731
         d = KataliHipMoe(C.sizeof(KataliHipMoe), gate_type, gate_type, down_type, hidden, ffn, n_expert,
-                         gate.ptr, up.ptr, down.ptr, None, None, None)
+                         p(gate), p(up), p(down), None, None, None)
         if shared is not None:
             d.gate_shexp, d.up_shexp, d.down_shexp = shared[0].ptr, shared[1].ptr, shared[2].ptr
         return d

@@ -258,6 +258,46 @@ def test_moe_graph_replay_matches_eager(hip, oracle, moes):
     assert ctypes is not None
 
 
+DENSE_FFN_CASES = [
+    # hidden, ffn, down_type: kernel B spreads each down row over 4*P lanes
+    (4096, 12288, Q6_K),   # Qwen3-8B FFN: P = 16, 3 blocks per lane
+    (2048, 4096, Q6_K),    # P = 4
+    (1024, 2048, Q4_K),    # Q4_K down, P = 4
+    (2048, 768, Q6_K),     # P = 1
+]
+
+
+@pytest.mark.parametrize("case", DENSE_FFN_CASES, ids=[f"h{c[0]}_f{c[1]}_{'q6' if c[2] == Q6_K else 'q4'}" for c in DENSE_FFN_CASES])
+def test_dense_ffn_shared_expert_only(hip, oracle, case):
+    """n_sel = 0 with a shared expert is a dense SiLU-GLU FFN through the MoE
+    kernels; the same parity bars as a routed layer."""
+    hidden, ffn, down_type = case
+    print(f"[dense-ffn] case={case}", flush=True)
+    rng = np.random.default_rng(hidden * 3 + ffn)
+    g, u = S.matrix(rng, Q4_K, ffn, hidden), S.matrix(rng, Q4_K, ffn, hidden)
+    d = S.matrix(rng, down_type, hidden, ffn)
+    dev = tuple(hip.to_device(a) for a in (g, u, d))
+    desc = hip.moe_desc(hidden, ffn, 0, None, None, None, down_type=down_type, shared=dev)
+    odesc = oracle.moe_desc(hidden, ffn, 0, None, None, None, down_type=down_type, shared=(ffn, g, u, d))
+    x = S.activation(rng, hidden)
+    y = hip.alloc(hidden * 4)
+    gu = hip.alloc(2 * ffn * 4)
+    hq = hip.alloc(ffn // 32 * 36)
+    hip.moe_layer_debug(desc, hip.moe_route(0), y, gu, hq, x=hip.to_device(x))
+    hip.sync()
+    yv = y.download(np.float32)
+    guv = gu.download(np.float32).reshape(2, ffn)
+    hqv = hq.download(np.uint8)
+    none_i, none_w = np.zeros(0, np.int32), np.zeros(0, np.float32)
+    yo, go, uo, hqo = oracle.moe_layer_q8(odesc, x, none_i, none_w, with_stages=True)
+    assert rel_l2(guv[0], go[0]) <= 1e-5 and rel_l2(guv[1], uo[0]) <= 1e-5
+    assert np.array_equal(hqv, oracle.quantize_q8_1(oracle.silu_mul(guv[0], guv[1])))
+    assert rel_l2(yv, oracle.moe_down_q8(odesc, none_i, none_w, hqv[None, :])) <= 1e-5
+    rf = rel_l2(yv, oracle.moe_layer_f32(odesc, x, none_i, none_w))
+    print(f"rel_L2(gpu q8, fp32 CPU path) = {rf:.3e}")
+    assert rf < 3e-2
+
+
 def test_moe_rejects_bad_arguments(hip, moes):
     m = moes(512, 256, 16, False, Q4_K)
     y, x = hip.alloc(512 * 4), hip.alloc(512 * 4)
