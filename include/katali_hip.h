@@ -99,6 +99,12 @@ int katali_hip_matvec_dp4a(uint32_t type, const void *w_dev, uint64_t rows, uint
 int katali_hip_block_isums(uint32_t type, const void *w_dev, uint64_t rows, uint64_t cols,
                            const void *xq8_dev, int32_t *isums_dev);
 
+/* ---- greedy sampling ---------------------------------------------------------- */
+/* *out_dev = the index of the largest of n logits, with the engine's greedy
+ * rule (gguf_sampler.c:62-66: strict '>' from -FLT_MAX, so the first maximum
+ * wins, NaN never wins, 0 when no logit exceeds -FLT_MAX). 1 <= n < 2^31. */
+int katali_hip_argmax(const float *logits_dev, uint64_t n, int32_t *out_dev);
+
 /* ---- fused MoE layer (README.md:13, one GPU call per MoE layer) ----------- */
 typedef struct KataliHipMoe {
     uint32_t struct_size;                  /* sizeof(KataliHipMoe) */

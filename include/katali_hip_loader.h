@@ -55,6 +55,9 @@ int katali_gpu_graph_end(void **graph);
 int katali_gpu_graph_launch(void *graph);
 int katali_gpu_graph_destroy(void *graph);
 int katali_gpu_selftest(char *report, size_t cap);
+/* Greedy token on device (gguf_sampler.c:62-66 rule), for a decode loop that
+ * keeps logits resident. */
+int katali_gpu_argmax(const float *logits_dev, uint64_t n, int32_t *out_dev);
 /* The library's last error for this thread ("" when none / not loaded). */
 const char *katali_gpu_last_error(void);
 
@@ -93,6 +96,7 @@ typedef struct KataliHipApi {
     int (*synth_fill)(uint32_t, void *, uint64_t, uint64_t, float);
     int (*synth_normal)(float *, uint64_t, uint64_t, float);
     int (*copy)(void *, const void *, size_t);
+    int (*argmax)(const float *, uint64_t, int32_t *);
 } KataliHipApi;
 
 /* NULL when the library could not be loaded or an entry point is missing. */

@@ -118,6 +118,8 @@ int check_gemv(uint32_t type, const void *w, uint64_t rows, uint64_t cols, const
 
 int launched(hipError_t e, const char *what) { return e == hipSuccess ? KATALI_HIP_OK : hip_fail(e, what); }
 
+void *g_argmax = nullptr;   // argmax partials (kq::argmax_parts() * 8 bytes)
+
 // MoE scratch: allocated outside any capture; grows only when not capturing.
 int moe_scratch(size_t hq8_bytes) {
     if (!g_route) {
@@ -343,6 +345,22 @@ int katali_hip_block_isums(uint32_t type, const void *w, uint64_t rows, uint64_t
     if (!rows) return KATALI_HIP_OK;
     return launched(kq::launch_isums(type, (const uint8_t *)w, rows, cols, (const uint8_t *)xq8, out, g_stream),
                     "block_isums");
+}
+
+int katali_hip_argmax(const float *x, uint64_t n, int32_t *out) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!x || !out) return fail(KATALI_HIP_E_INVALID, "null buffer");
+    if (n == 0 || n >= (1ull << 31)) return fail(KATALI_HIP_E_INVALID, "argmax n=%llu", (unsigned long long)n);
+    if (!g_argmax) {
+        if (g_capturing) return fail(KATALI_HIP_E_INVALID, "first argmax call must happen outside graph capture");
+        hipError_t e = hipMalloc(&g_argmax, (size_t)kq::argmax_parts() * 8);
+        if (e != hipSuccess) {
+            g_argmax = nullptr;
+            return hip_fail(e, "hipMalloc(argmax scratch)");
+        }
+    }
+    return launched(kq::launch_argmax(x, (uint32_t)n, g_argmax, out, g_stream), "argmax");
 }
 
 int katali_hip_moe_layer(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, const void *xq, float *y) {

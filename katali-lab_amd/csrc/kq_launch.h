@@ -37,6 +37,12 @@ hipError_t launch_step_advance(int32_t *step, int32_t n_steps, hipStream_t s);
 // Plain streaming copy (HBM counter calibration).
 hipError_t launch_copy(const uint8_t *src, uint8_t *dst, uint64_t n, hipStream_t s);
 
+// Greedy sampling: *out = index of the largest of n logits (first maximum
+// wins, NaN never, 0 when nothing exceeds -FLT_MAX). scratch holds
+// argmax_parts() * 8 bytes.
+uint32_t argmax_parts();
+hipError_t launch_argmax(const float *x, uint32_t n, void *scratch, int32_t *out, hipStream_t s);
+
 // MoE layer (two launches). Types: gate/up Q4_K; down Q4_K or Q6_K.
 struct MoeArgs {
     const uint8_t *gate, *up, *down;          // stacked [n_expert][rows][row_bytes]

@@ -55,6 +55,7 @@ SIGNATURES = {
     "katali_hip_synth_fill": (C.c_int, [_u32, _vp, _u64, _u64, _f32]),
     "katali_hip_synth_normal": (C.c_int, [_vp, _u64, _u64, _f32]),
     "katali_hip_copy": (C.c_int, [_vp, _vp, _sz]),
+    "katali_hip_argmax": (C.c_int, [_vp, _u64, _vp]),
 }
 
 
@@ -200,6 +201,9 @@ class KataliHip:
         self.check(self.lib.katali_hip_moe_layer_debug(C.byref(desc), C.byref(route),
                                                        None if x is None else x.ptr,
                                                        None if xq is None else xq.ptr, y.ptr, gu.ptr, hq8.ptr))
+
+    def argmax(self, logits: DeviceBuffer, n: int, out: DeviceBuffer) -> None:
+        self.check(self.lib.katali_hip_argmax(logits.ptr, n, out.ptr))
 
     def step_advance(self, step: DeviceBuffer, n_steps: int) -> None:
         self.check(self.lib.katali_hip_step_advance(step.ptr, n_steps))

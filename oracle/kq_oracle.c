@@ -7,6 +7,7 @@
  */
 #include "kq_oracle.h"
 
+#include <float.h>
 #include <math.h>
 #include <pthread.h>
 #include <stdlib.h>
@@ -530,6 +531,17 @@ int kqo_router_topk(const float *logits_in, int n_expert, int k, int32_t *ids, f
     for (int r = 0; r < k; r++) { e[r] = kqo_expf(logits[ids[r]] - lmax); sum += e[r]; }
     for (int r = 0; r < k; r++) w[r] = e[r] / sum;
     return 0;
+}
+
+/* Greedy sampling (V/src/gguf_sampler.c:62-66): best = 0, bv = -FLT_MAX,
+ * take i when logits[i] > bv, i ascending. */
+int kqo_argmax_greedy(const float *logits, int n) {
+    if (!logits || n <= 0) return -1;
+    int best = 0;
+    float bv = -FLT_MAX;
+    for (int i = 0; i < n; i++)
+        if (logits[i] > bv) { bv = logits[i]; best = i; }
+    return best;
 }
 
 /* ======================================================================== *

@@ -119,6 +119,9 @@ void  kqo_silu_mul_ref(float *gate, const float *up, uint64_t n);
  * renormalisation over the top k. A NaN logit counts as -inf (rank and
  * weight); -0 and +0 are equal logits. */
 int kqo_router_topk(const float *logits, int n_expert, int k, int32_t *ids, float *w);
+/* Greedy argmax: first maximum wins, NaN never, 0 when nothing exceeds
+ * -FLT_MAX (V/src/gguf_sampler.c:62-66). */
+int kqo_argmax_greedy(const float *logits, int n);
 
 /* ---- MoE layer (configs 1, 2, 4) ----------------------------------------- */
 typedef struct KqoMoe {

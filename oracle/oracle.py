@@ -70,6 +70,7 @@ class Oracle:
             "kqo_exp_ref_poly": (_f32, [_f32]),
             "kqo_silu_mul_ref": (None, [_vp, _vp, _u64]),
             "kqo_router_topk": (_i32, [_vp, _i32, _i32, _vp, _vp]),
+            "kqo_argmax_greedy": (_i32, [_vp, _i32]),
             "kqo_moe_layer_q8": (_i32, [C.POINTER(KqoMoe), _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
             "kqo_moe_down_q8": (_i32, [C.POINTER(KqoMoe), _i32, _vp, _vp, _vp, _vp]),
             "kqo_moe_layer_f32": (_i32, [C.POINTER(KqoMoe), _vp, _i32, _vp, _vp, _vp]),
@@ -148,6 +149,10 @@ class Oracle:
         w = np.empty(k, np.float32)
         assert self.lib.kqo_router_topk(_ptr(logits), logits.size, k, _ptr(ids), _ptr(w)) == 0
         return ids, w
+
+    def argmax_greedy(self, logits: np.ndarray) -> int:
+        logits = np.ascontiguousarray(logits, np.float32)
+        return int(self.lib.kqo_argmax_greedy(_ptr(logits), logits.size))
 
     # -- MoE ---------------------------------------------------------------
     @staticmethod
@@ -228,9 +233,16 @@ class RefCPU:
         L.kref_f32_to_f16.argtypes = [_f32]
         L.kref_f16_to_f32.restype = _f32
         L.kref_f16_to_f32.argtypes = [C.c_uint16]
+        L.kref_sample_greedy.restype = _i32
+        L.kref_sample_greedy.argtypes = [_vp, _i32]
 
     def simd(self) -> bool:
         return bool(self.lib.katali_ggml_simd_available())
+
+    def sample_greedy(self, logits: np.ndarray) -> int:
+        """katali_gguf_sample with temperature 0 (gguf_sampler.c:62-66)."""
+        logits = np.ascontiguousarray(logits, np.float32)
+        return int(self.lib.kref_sample_greedy(_ptr(logits), logits.size))
 
     def dequant(self, t, data, n):
         out = np.empty(n, np.float32)

@@ -308,6 +308,30 @@ def test_router_topk_nan_and_signed_zero(oracle):
     assert ids2.tolist() == ids.tolist() and np.array_equal(w2, w)
 
 
+def greedy_cases(rng):
+    yield np.array([1.0], np.float32)
+    yield np.array([np.nan, 2.0, 2.0, 1.0], np.float32)           # NaN skipped, first of the tie
+    yield np.full(7, -np.inf, np.float32)                          # nothing above -FLT_MAX: 0
+    yield np.array([-np.float32(3.4028235e38)] * 3, np.float32)    # exactly -FLT_MAX: 0
+    yield np.array([np.nan, np.nan], np.float32)
+    yield np.array([0.0, -0.0, 0.0], np.float32)                   # -0 == +0: first
+    yield np.array([1.0, np.inf, np.inf, 5.0], np.float32)
+    for n in (2, 63, 64, 65, 2047, 2049, 151936):
+        v = rng.standard_normal(n).astype(np.float32)
+        yield v
+        w = rng.integers(-3, 4, n).astype(np.float32)              # many exact ties
+        w[rng.integers(0, n, max(1, n // 50))] = np.nan
+        yield w
+
+
+def test_argmax_greedy_vs_reference(oracle, refcpu):
+    """The oracle's greedy argmax equals the reference sampler's greedy
+    branch, including ties, NaN, -inf and -FLT_MAX."""
+    rng = np.random.default_rng(21)
+    for v in greedy_cases(rng):
+        assert oracle.argmax_greedy(v) == refcpu.sample_greedy(v)
+
+
 # ---------------------------------------------------------------------------
 # MoE composition: independent float64 composition over reference decoders
 # ---------------------------------------------------------------------------
