@@ -151,6 +151,26 @@ int katali_hip_moe_layer_debug(const KataliHipMoe *moe, const KataliHipMoeRoute 
                                const float *x_dev, const void *xq8_dev, float *y_dev,
                                float *gu_dev, void *hq8_dev);
 
+/* ---- MoE layer over a batch of tokens (batched prefill) ---------- */
+/* The batched counterpart of the reference's CPU matmul (katali_ggml_matmul_role,
+ * V/src/gguf_dtype.c:1059-1105, each weight row decoded once for B tokens):
+ * T tokens with their own experts. Pairs are grouped by expert on the device;
+ * an expert with at least mfma_min_tokens pairs runs as an int8 MFMA grouped
+ * GEMM, the others through the v_dot4 GEMV kernels; results are identical in
+ * definition (q8_1 x and h, rank-order weighted sum). */
+typedef struct KataliHipMoeBatch {
+    uint32_t struct_size;                  /* sizeof(KataliHipMoeBatch) */
+    uint32_t n_tokens;                     /* T, 1..64 */
+    int32_t n_sel;                         /* routed experts per token, 0..16 */
+    uint32_t mfma_min_tokens;              /* grouped-GEMM threshold; 0 = 16 */
+    const int32_t *ids;                    /* device [T][n_sel] */
+    const float *weights;                  /* device [T][n_sel] */
+} KataliHipMoeBatch;
+
+/* y[T][hidden] = the MoE layer of each of the T fp32 rows x[T][hidden]. */
+int katali_hip_moe_batch(const KataliHipMoe *moe, const KataliHipMoeBatch *batch, const float *x_dev,
+                         float *y_dev);
+
 /* Advance a device step index: *step = (*step + 1) % n_steps (one tiny launch). */
 int katali_hip_step_advance(int32_t *step_dev, int32_t n_steps);
 

@@ -221,6 +221,87 @@ int moe_impl(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, 
     return KATALI_HIP_OK;
 }
 
+// Batch scratch: q8_1 x rows, grouping metadata, per-pair down outputs.
+uint8_t *g_bxq = nullptr;
+size_t g_bxq_cap = 0;
+int32_t *g_bmeta = nullptr;
+size_t g_bmeta_cap = 0;
+float *g_byp = nullptr;
+size_t g_byp_cap = 0;
+
+template <class T>
+int grow(T **p, size_t *cap, size_t need, const char *what) {
+    if (need <= *cap) return KATALI_HIP_OK;
+    if (g_capturing) return fail(KATALI_HIP_E_INVALID, "%s must grow outside graph capture", what);
+    if (*p) {
+        hipError_t e = hipStreamSynchronize(g_stream);
+        if (e == hipSuccess) e = hipFree(*p);
+        *p = nullptr;
+        *cap = 0;
+        if (e != hipSuccess) return hip_fail(e, what);
+    }
+    hipError_t e = hipMalloc((void **)p, need);
+    if (e != hipSuccess) {
+        *p = nullptr;
+        return hip_fail(e, what);
+    }
+    *cap = need;
+    return KATALI_HIP_OK;
+}
+
+int moe_batch_impl(const KataliHipMoe *m, const KataliHipMoeBatch *b, const float *x, float *y) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!m || !b || m->struct_size < sizeof(KataliHipMoe) || b->struct_size < sizeof(KataliHipMoeBatch))
+        return fail(KATALI_HIP_E_INVALID, "null or short MoE batch descriptor");
+    if (m->up_type != m->gate_type || !kq::moe_shape_supported(m->gate_type, m->down_type, m->hidden, m->ffn) ||
+        m->ffn > 16384)
+        return fail(KATALI_HIP_E_UNSUPPORTED, "MoE batch shape gate=%u down=%u hidden=%u ffn=%u", m->gate_type,
+                    m->down_type, m->hidden, m->ffn);
+    if (!x || !y) return fail(KATALI_HIP_E_INVALID, "null buffer");
+    if (b->n_tokens < 1 || b->n_tokens > 64) return fail(KATALI_HIP_E_INVALID, "n_tokens=%u (1..64)", b->n_tokens);
+    const bool shared = m->gate_shexp || m->up_shexp || m->down_shexp;
+    if (shared && !(m->gate_shexp && m->up_shexp && m->down_shexp))
+        return fail(KATALI_HIP_E_INVALID, "shared expert needs gate, up and down");
+    if (b->n_sel < 0 || b->n_sel > 16 || (b->n_sel == 0 && !shared)) return fail(KATALI_HIP_E_INVALID, "n_sel=%d", b->n_sel);
+    if (b->n_sel > 0) {
+        if (!m->n_expert || m->n_expert > 512 || (uint32_t)b->n_sel > m->n_expert)
+            return fail(KATALI_HIP_E_INVALID, "n_expert=%u n_sel=%d", m->n_expert, b->n_sel);
+        if (!m->gate_exps || !m->up_exps || !m->down_exps || !b->ids || !b->weights)
+            return fail(KATALI_HIP_E_INVALID, "null expert tensors or routing");
+    }
+    const uint32_t T = b->n_tokens, S = (uint32_t)b->n_sel + (shared ? 1u : 0u), P = T * S;
+    if ((rc = moe_scratch((size_t)P * (m->ffn / 32) * 36))) return rc;
+    if ((rc = grow(&g_bxq, &g_bxq_cap, (size_t)T * (m->hidden / 32) * 36, "MoE batch x scratch"))) return rc;
+    if ((rc = grow(&g_bmeta, &g_bmeta_cap, (size_t)kq::moe_batch_meta_words(P) * 4, "MoE batch metadata"))) return rc;
+    if ((rc = grow(&g_byp, &g_byp_cap, (size_t)P * m->hidden * 4, "MoE batch outputs"))) return rc;
+    kq::MoeArgs a;
+    memset(&a, 0, sizeof a);
+    a.gate = (const uint8_t *)m->gate_exps;
+    a.up = (const uint8_t *)m->up_exps;
+    a.down = (const uint8_t *)m->down_exps;
+    a.gate_sh = (const uint8_t *)m->gate_shexp;
+    a.up_sh = (const uint8_t *)m->up_shexp;
+    a.down_sh = (const uint8_t *)m->down_shexp;
+    a.gate_type = m->gate_type;
+    a.up_type = m->up_type;
+    a.down_type = m->down_type;
+    a.hidden = m->hidden;
+    a.ffn = m->ffn;
+    a.n_expert = m->n_expert;
+    a.n_sel = b->n_sel;
+    a.has_shared = shared ? 1 : 0;
+    a.ids = b->ids;
+    a.wts = b->weights;
+    a.hq8 = g_hq8;
+    a.route_ids = g_route;
+    a.route_w = (float *)(g_route + kq::moe_route_words() / 2);
+    a.err = g_err_dev;
+    a.yp = g_byp;
+    const uint32_t min_big = b->mfma_min_tokens ? b->mfma_min_tokens : 16;
+    return launched(kq::launch_moe_batch(a, T, min_big, x, y, g_bxq, g_bmeta, g_stream), "moe batch launch");
+}
+
 }  // namespace
 
 extern "C" {
@@ -345,6 +426,11 @@ int katali_hip_block_isums(uint32_t type, const void *w, uint64_t rows, uint64_t
     if (!rows) return KATALI_HIP_OK;
     return launched(kq::launch_isums(type, (const uint8_t *)w, rows, cols, (const uint8_t *)xq8, out, g_stream),
                     "block_isums");
+}
+
+int katali_hip_moe_batch(const KataliHipMoe *moe, const KataliHipMoeBatch *batch, const float *x_dev,
+                         float *y_dev) {
+    return moe_batch_impl(moe, batch, x_dev, y_dev);
 }
 
 int katali_hip_argmax(const float *x, uint64_t n, int32_t *out) {

@@ -66,9 +66,31 @@ struct MoeArgs {
     float *route_w;
     float *dbg_gu;           // optional [n_slots][2][ffn] gate/up outputs
     int32_t *err;            // error word (bit 1: expert id out of range)
+    // Batch mode (several tokens): a workgroup's slot is a (token, rank) pair
+    // p = t * bS + r taken from the device list bslot[0 .. *bcount); x comes
+    // from the q8_1 rows xq + t * xq_stride, experts from ids[t * n_sel + r]
+    // (r == n_sel: the shared expert), h goes to hq8 row p, and kernel B
+    // writes the pair's unweighted down output to yp + p * hidden.
+    const int32_t *bslot;    // NULL: single-token layer
+    const int32_t *bcount;
+    uint32_t bS;
+    uint64_t xq_stride;
+    float *yp;
 };
 bool moe_shape_supported(uint32_t gate_type, uint32_t down_type, uint32_t hidden, uint32_t ffn);
 hipError_t launch_moe(const MoeArgs &a, hipStream_t s);
+// Batch mode of the two kernels over up to max_slots listed pairs (grids
+// sized for max_slots; workgroups past *bcount exit at once).
+hipError_t launch_moe_pairs_gu(const MoeArgs &a, uint32_t max_slots, hipStream_t s);
+hipError_t launch_moe_pairs_down(const MoeArgs &a, uint32_t max_slots, hipStream_t s);
+// MoE layer over T <= 64 tokens (a.ids / a.wts: [T][n_sel]; a.hq8: P rows of
+// ffn/32 q8_1 blocks, a.yp: [P][hidden], P = T * (n_sel + shared)). Experts
+// gathering >= min_big pairs use the int8 MFMA grouped GEMM, the rest the
+// per-pair GEMV kernels. xq: T rows of hidden/32 q8_1 blocks; meta:
+// moe_batch_meta_words(P) ints.
+uint64_t moe_batch_meta_words(uint32_t P);
+hipError_t launch_moe_batch(const MoeArgs &a, uint32_t T, uint32_t min_big, const float *x, float *y, uint8_t *xq,
+                            int32_t *meta, hipStream_t s);
 uint64_t moe_route_words();
 
 }  // namespace kq

@@ -334,7 +334,19 @@ __global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t nblk = a.ffn / 32;
     const uint32_t slot = blockIdx.x / nblk, jb = blockIdx.x % nblk;
-    const bool publisher = blockIdx.x == 0 && wave == 0;
+    // batch mode: the slot is a listed (token, rank) pair
+    uint32_t hslot = slot;
+    const uint8_t *xq = a.xq;
+    int32_t bexpert = -1;
+    if (a.bslot) {
+        if (slot >= (uint32_t)*a.bcount) return;   // whole workgroup, before any barrier
+        const uint32_t p = (uint32_t)a.bslot[slot], t = p / a.bS, r = p % a.bS;
+        hslot = p;
+        xq = a.xq + (uint64_t)t * a.xq_stride;
+        bexpert = (int)r < a.n_sel ? a.ids[t * a.n_sel + r] : -1;
+    }
+    const bool batch = a.bslot != nullptr;
+    const bool publisher = blockIdx.x == 0 && wave == 0 && !batch;
 
     // routing inputs, then x (fp32 or q8_1; lane task t covers values
     // 4t..4t+3); their latencies overlap. Loads are clamped, not guarded: no
@@ -342,7 +354,7 @@ __global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
     float lv[C];
     int32_t eid = -1;
     float ew = 0.0f;
-    if (a.n_sel > 0) {
+    if (a.n_sel > 0 && !batch) {
         if (a.logits) {
             load_keys<C>(a, lv);
         } else {
@@ -355,20 +367,20 @@ __global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
     constexpr int XPT = (XTASKS + 255) / 256;
     float4 xv[XPT];
     uint32_t xqv[XPT], xdv[XPT];
-    if (a.xq == nullptr) {
+    if (xq == nullptr) {
 #pragma unroll
         for (int i = 0; i < XPT; i++) xv[i] = *(const float4 *)(a.x + 4 * min(tid + 256 * i, (uint32_t)XTASKS - 1));
     } else {
 #pragma unroll
         for (int i = 0; i < XPT; i++) {
             const uint32_t t = min(tid + 256 * i, (uint32_t)XTASKS - 1);
-            const uint8_t *b = a.xq + (t >> 3) * 36;
+            const uint8_t *b = xq + (t >> 3) * 36;
             xqv[i] = *(const uint32_t *)(b + 4 + 4 * (t & 7));
             xdv[i] = ld_u16(b);
         }
     }
     float route_l = 0.0f;
-    if (a.logits && a.n_sel > 0) {
+    if (a.logits && a.n_sel > 0 && !batch) {
         const WaveRoute r = wave_topk<C>(a, lv);
         eid = r.id;
         route_l = r.logit;
@@ -380,8 +392,8 @@ __global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
 
     const uint64_t rb = NB * 144;
     const uint8_t *gb, *ub;
-    if ((int)slot < a.n_sel) {
-        int32_t id = __builtin_amdgcn_readlane(eid, (int)slot);
+    if (batch ? bexpert >= 0 : (int)slot < a.n_sel) {
+        int32_t id = batch ? bexpert : __builtin_amdgcn_readlane(eid, (int)slot);
         if ((uint32_t)id >= a.n_expert) id = 0;   // bad explicit id: reported by route_publish
         const uint64_t e = (uint64_t)id;
         gb = a.gate + e * a.ffn * rb;
@@ -429,7 +441,7 @@ __global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
         uint32_t qv;
         int lo, hi;
         float dd;
-        if (a.xq) {
+        if (xq) {
             qv = xqv[i];
             q8_part_sums(qv, lo, hi);
             dd = h2f(xdv[i]);
@@ -514,11 +526,11 @@ __global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
         const int qv = (int)roundf(h * id);
         const int total = sum32(qv);
-        uint8_t *blk = a.hq8 + ((uint64_t)slot * nblk + jb) * 36;
+        uint8_t *blk = a.hq8 + ((uint64_t)hslot * nblk + jb) * 36;
         if (lane < 32) blk[4 + lane] = (uint8_t)(qv & 255);
         if (lane == 0) *(uint32_t *)blk = f2h_rne(d) | (f2h_rne((float)total * d) << 16);
     }
-    if (a.dbg_gu && tid < 64) {
+    if (a.dbg_gu && !batch && tid < 64) {
         float *d = a.dbg_gu + (uint64_t)slot * 2 * a.ffn + (tid < 32 ? 0 : a.ffn) + 32 * jb + (tid & 31);
         *d = gu[tid];
     }
@@ -585,12 +597,30 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a, uint32_t tr, uint32
     extern __shared__ __align__(16) uint8_t lds[];
     const LdsB L = lds_b(a.ffn, n_slots, tr);
     const uint32_t tid = threadIdx.x, lane = tid & 63;
+    // batch mode: one listed pair per blockIdx.y, weight 1, output to the
+    // pair's row of yp
+    const bool batch = a.bslot != nullptr;
+    const uint8_t *hsrc = a.hq8;
+    float *yout = a.y;
+    int32_t bexpert = -1;
+    if (batch) {
+        if (blockIdx.y >= (uint32_t)*a.bcount) return;   // whole workgroup, before any barrier
+        const uint32_t p = (uint32_t)a.bslot[blockIdx.y], t = p / a.bS, r = p % a.bS;
+        hsrc = a.hq8 + (uint64_t)p * (a.ffn / 32) * 36;
+        yout = a.yp + (uint64_t)p * a.hidden;
+        bexpert = (int)r < a.n_sel ? a.ids[t * a.n_sel + r] : -1;
+        if (bexpert >= 0 && (uint32_t)bexpert >= a.n_expert) bexpert = 0;   // bad id: reported by the grouping
+    }
     // routing (lane r holds slot r), then the h loads
-    const int32_t rid = a.route_ids[min(lane, (uint32_t)MAX_SLOTS - 1)];
-    const float rw = a.route_w[min(lane, (uint32_t)MAX_SLOTS - 1)];
+    int32_t rid = 0;
+    float rw = batch && lane == 0 ? 1.0f : 0.0f;
+    if (!batch) {
+        rid = a.route_ids[min(lane, (uint32_t)MAX_SLOTS - 1)];
+        rw = a.route_w[min(lane, (uint32_t)MAX_SLOTS - 1)];
+    }
     const uint32_t ntask = n_slots * (a.ffn / 32) * 2;
     HLoad hv;
-    load_h(a.hq8, ntask, 0, hv);
+    load_h(hsrc, ntask, 0, hv);
 
     constexpr uint32_t S = QD::IPB * P;
     const uint32_t ls = tid / S, s = tid % S;
@@ -603,8 +633,9 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a, uint32_t tr, uint32
     const bool active = ls < npairs;
     const uint32_t lc = min(ls, npairs - 1);   // idle lane-slots load a real pair and drop it
     const uint32_t sl = lc % n_slots, r = lc / n_slots;
-    const int32_t sid = __shfl(rid, (int)sl, WAVE);
-    const uint8_t *db = (int)sl < a.n_sel ? a.down + (uint64_t)sid * a.hidden * rbd : a.down_sh;
+    const int32_t sid = batch ? bexpert : __shfl(rid, (int)sl, WAVE);
+    const bool routed = batch ? bexpert >= 0 : (int)sl < a.n_sel;
+    const uint8_t *db = routed ? a.down + (uint64_t)sid * a.hidden * rbd : a.down_sh;
     const uint8_t *rp = db + (uint64_t)(row0 + r) * rbd;
     typename QD::Raw raw[IPL > 0 ? IPL : 1];
     if constexpr (IPL > 0) {
@@ -614,7 +645,7 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a, uint32_t tr, uint32
     }
     stage_h(lds + L.hacts, a.ffn, ntask, 0, hv);
     for (uint32_t first = HT * 256; first < ntask; first += HT * 256) {
-        load_h(a.hq8, ntask, first, hv);   // only when n_slots * ffn / 16 > 512
+        load_h(hsrc, ntask, first, hv);   // only when n_slots * ffn / 16 > 512
         stage_h(lds + L.hacts, a.ffn, ntask, first, hv);
     }
     __syncthreads();
@@ -645,7 +676,7 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a, uint32_t tr, uint32
             const float v = res[tid * n_slots + k];
             y = k < (int)n_slots ? fmaf(w, v, y) : y;
         }
-        a.y[row0 + tid] = y;
+        yout[row0 + tid] = y;
     }
 }
 
@@ -665,12 +696,13 @@ static hipError_t go_a(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
 }
 
 template <class QD, int IPL, int P>
-static hipError_t go_b(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
+static hipError_t go_b(const MoeArgs &a, uint32_t n_slots, uint32_t grid_y, hipStream_t s) {
     const uint32_t lane_slots = 256 / (QD::IPB * P);
     uint32_t tr = lane_slots / n_slots;
     if (tr < 1) tr = 1;
     const LdsB L = lds_b(a.ffn, n_slots, tr);
-    hipLaunchKernelGGL((k_moe_down<QD, IPL, P>), dim3((a.hidden + tr - 1) / tr), dim3(256), L.total, s, a, tr, n_slots);
+    hipLaunchKernelGGL((k_moe_down<QD, IPL, P>), dim3((a.hidden + tr - 1) / tr, grid_y), dim3(256), L.total, s, a, tr,
+                       n_slots);
     return hipGetLastError();
 }
 
@@ -678,32 +710,32 @@ static hipError_t go_b(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
 // lane's blocks (IPL = ceil(nb / P)) to at most 4 while a workgroup still
 // holds every slot of at least one output row.
 template <class QD>
-static hipError_t go_b_any(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
+static hipError_t go_b_any(const MoeArgs &a, uint32_t n_slots, uint32_t grid_y, hipStream_t s) {
     const uint32_t nb = a.ffn / 256;
     uint32_t p = 1;
     while ((nb + p - 1) / p > 4 && QD::IPB * 4 * p <= 64 && QD::IPB * 4 * p * n_slots <= 256) p *= 4;
     const uint32_t ipl = (nb + p - 1) / p;
-    if (QD::IPB * p * n_slots > 256 || ipl > 4) return go_b<QD, 0, 1>(a, n_slots, s);
+    if (QD::IPB * p * n_slots > 256 || ipl > 4) return go_b<QD, 0, 1>(a, n_slots, grid_y, s);
     const uint32_t key = p * 8 + ipl;
     switch (key) {
-        case 1 * 8 + 1: return go_b<QD, 1, 1>(a, n_slots, s);
-        case 1 * 8 + 2: return go_b<QD, 2, 1>(a, n_slots, s);
-        case 1 * 8 + 3: return go_b<QD, 3, 1>(a, n_slots, s);
-        case 1 * 8 + 4: return go_b<QD, 4, 1>(a, n_slots, s);
-        case 4 * 8 + 2: return go_b<QD, 2, 4>(a, n_slots, s);
-        case 4 * 8 + 3: return go_b<QD, 3, 4>(a, n_slots, s);
-        case 4 * 8 + 4: return go_b<QD, 4, 4>(a, n_slots, s);
+        case 1 * 8 + 1: return go_b<QD, 1, 1>(a, n_slots, grid_y, s);
+        case 1 * 8 + 2: return go_b<QD, 2, 1>(a, n_slots, grid_y, s);
+        case 1 * 8 + 3: return go_b<QD, 3, 1>(a, n_slots, grid_y, s);
+        case 1 * 8 + 4: return go_b<QD, 4, 1>(a, n_slots, grid_y, s);
+        case 4 * 8 + 2: return go_b<QD, 2, 4>(a, n_slots, grid_y, s);
+        case 4 * 8 + 3: return go_b<QD, 3, 4>(a, n_slots, grid_y, s);
+        case 4 * 8 + 4: return go_b<QD, 4, 4>(a, n_slots, grid_y, s);
         default: break;
     }
     if constexpr (QD::IPB * 16 <= 64) {
         switch (key) {
-            case 16 * 8 + 2: return go_b<QD, 2, 16>(a, n_slots, s);
-            case 16 * 8 + 3: return go_b<QD, 3, 16>(a, n_slots, s);
-            case 16 * 8 + 4: return go_b<QD, 4, 16>(a, n_slots, s);
+            case 16 * 8 + 2: return go_b<QD, 2, 16>(a, n_slots, grid_y, s);
+            case 16 * 8 + 3: return go_b<QD, 3, 16>(a, n_slots, grid_y, s);
+            case 16 * 8 + 4: return go_b<QD, 4, 16>(a, n_slots, grid_y, s);
             default: break;
         }
     }
-    return go_b<QD, 0, 1>(a, n_slots, s);
+    return go_b<QD, 0, 1>(a, n_slots, grid_y, s);
 }
 
 bool moe_shape_supported(uint32_t gate_type, uint32_t down_type, uint32_t hidden, uint32_t ffn) {
@@ -713,20 +745,35 @@ bool moe_shape_supported(uint32_t gate_type, uint32_t down_type, uint32_t hidden
     return ffn % 256 == 0 && ffn >= 256;
 }
 
+static hipError_t go_a_any(const MoeArgs &a, uint32_t n_slots, hipStream_t s);
+
 hipError_t launch_moe(const MoeArgs &a, hipStream_t s) {
     if (a.n_expert > MAX_EXPERT || a.n_sel > MAX_SEL) return hipErrorInvalidValue;
     const uint32_t n_slots = (uint32_t)a.n_sel + (a.has_shared ? 1u : 0u);
-    hipError_t e;
+    const hipError_t e = go_a_any(a, n_slots, s);
+    if (e != hipSuccess) return e;
+    return a.down_type == T_Q6_K ? go_b_any<Q6K>(a, n_slots, 1, s) : go_b_any<Q4K>(a, n_slots, 1, s);
+}
+
+static hipError_t go_a_any(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
     switch (a.hidden / 256) {
-        case 1: e = go_a<1>(a, n_slots, s); break;
-        case 2: e = go_a<2>(a, n_slots, s); break;
-        case 4: e = go_a<4>(a, n_slots, s); break;
-        case 8: e = go_a<8>(a, n_slots, s); break;
-        case 16: e = go_a<16>(a, n_slots, s); break;
+        case 1: return go_a<1>(a, n_slots, s);
+        case 2: return go_a<2>(a, n_slots, s);
+        case 4: return go_a<4>(a, n_slots, s);
+        case 8: return go_a<8>(a, n_slots, s);
+        case 16: return go_a<16>(a, n_slots, s);
         default: return hipErrorInvalidValue;
     }
-    if (e != hipSuccess) return e;
-    return a.down_type == T_Q6_K ? go_b_any<Q6K>(a, n_slots, s) : go_b_any<Q4K>(a, n_slots, s);
+}
+
+hipError_t launch_moe_pairs_gu(const MoeArgs &a, uint32_t max_slots, hipStream_t s) {
+    if (!a.bslot || !a.bcount || max_slots == 0) return hipErrorInvalidValue;
+    return go_a_any(a, max_slots, s);
+}
+
+hipError_t launch_moe_pairs_down(const MoeArgs &a, uint32_t max_slots, hipStream_t s) {
+    if (!a.bslot || !a.bcount || !a.yp || max_slots == 0 || max_slots > 65535) return hipErrorInvalidValue;
+    return a.down_type == T_Q6_K ? go_b_any<Q6K>(a, 1, max_slots, s) : go_b_any<Q4K>(a, 1, max_slots, s);
 }
 
 }  // namespace kq

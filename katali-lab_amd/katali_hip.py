@@ -56,6 +56,7 @@ SIGNATURES = {
     "katali_hip_synth_normal": (C.c_int, [_vp, _u64, _u64, _f32]),
     "katali_hip_copy": (C.c_int, [_vp, _vp, _sz]),
     "katali_hip_argmax": (C.c_int, [_vp, _u64, _vp]),
+    "katali_hip_moe_batch": (C.c_int, [_vp, _vp, _vp, _vp]),
 }
 
 
@@ -93,6 +94,11 @@ def load_library(path: str | None = None) -> C.CDLL:
         fn.restype = res
         fn.argtypes = args
     return lib
+
+
+class KataliHipMoeBatch(C.Structure):
+    _fields_ = [("struct_size", _u32), ("n_tokens", _u32), ("n_sel", _i32), ("mfma_min_tokens", _u32),
+                ("ids", _vp), ("weights", _vp)]
 
 
 class DeviceBuffer:
@@ -201,6 +207,11 @@ class KataliHip:
         self.check(self.lib.katali_hip_moe_layer_debug(C.byref(desc), C.byref(route),
                                                        None if x is None else x.ptr,
                                                        None if xq is None else xq.ptr, y.ptr, gu.ptr, hq8.ptr))
+
+    def moe_batch(self, desc, n_tokens, n_sel, ids, weights, x, y, mfma_min_tokens=0) -> None:
+        b = KataliHipMoeBatch(C.sizeof(KataliHipMoeBatch), n_tokens, n_sel, mfma_min_tokens,
+                              None if ids is None else ids.ptr, None if weights is None else weights.ptr)
+        self.check(self.lib.katali_hip_moe_batch(C.byref(desc), C.byref(b), x.ptr, y.ptr))
 
     def argmax(self, logits: DeviceBuffer, n: int, out: DeviceBuffer) -> None:
         self.check(self.lib.katali_hip_argmax(logits.ptr, n, out.ptr))

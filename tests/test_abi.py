@@ -51,15 +51,16 @@ def test_loads_and_reports_status():
 
 
 def test_struct_layouts_match_header():
-    # field order and sizes of the two descriptors (checked against a C compile)
+    # field order and sizes of the descriptors (checked against a C compile)
     src = """
 #include <stdio.h>
 #include <stddef.h>
 #include "katali_hip.h"
 int main(void) {
-  printf("%zu %zu %zu %zu %zu %zu\\n", sizeof(KataliHipMoe), offsetof(KataliHipMoe, gate_exps),
+  printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu\\n", sizeof(KataliHipMoe), offsetof(KataliHipMoe, gate_exps),
          offsetof(KataliHipMoe, down_shexp), sizeof(KataliHipMoeRoute),
-         offsetof(KataliHipMoeRoute, logits_stride), offsetof(KataliHipMoeRoute, weights_out));
+         offsetof(KataliHipMoeRoute, logits_stride), offsetof(KataliHipMoeRoute, weights_out),
+         sizeof(KataliHipMoeBatch), offsetof(KataliHipMoeBatch, ids), offsetof(KataliHipMoeBatch, weights));
   return 0;
 }
 """
@@ -70,9 +71,10 @@ int main(void) {
         exe = os.path.join(d, "t")
         subprocess.run(["gcc", "-I" + os.path.join(REPO, "include"), c, "-o", exe], check=True)
         vals = [int(v) for v in subprocess.run([exe], capture_output=True, text=True).stdout.split()]
-    M, R = K.KataliHipMoe, K.KataliHipMoeRoute
+    M, R, B = K.KataliHipMoe, K.KataliHipMoeRoute, K.KataliHipMoeBatch
     assert vals == [ctypes.sizeof(M), M.gate_exps.offset, M.down_shexp.offset, ctypes.sizeof(R),
-                    R.logits_stride.offset, R.weights_out.offset]
+                    R.logits_stride.offset, R.weights_out.offset, ctypes.sizeof(B), B.ids.offset,
+                    B.weights.offset]
 
 
 @pytest.mark.parametrize("t,ok", [(12, 1), (14, 1), (0, 0), (2, 0), (13, 0)])
