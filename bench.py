@@ -1,6 +1,6 @@
 """Benchmark of the quantized expert-GEMV path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload moe48|moe40cold|gemv6144|qwen8b]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload moe48|moe40cold|gemv6144|qwen8b|moebatch]
 
 Workloads:
   moe48     (default) one decode token through 48 fused MoE layers,
@@ -21,6 +21,12 @@ in one hipGraph per token; a step is one replay.
             (q stands in for the attention output, which is not a GEMV),
             FFN(o) through the MoE kernels with the shared expert only; every
             layer reads its own N(0,1) x; a step is one token (one replay).
+  moebatch  the config-1 MoE layer over ragged token batches (1..64 tokens,
+            per-token experts from a Zipf(1.1) popularity), swept over
+            n_sel in {1, 2, 4, 8}; experts that gather >= 16 tokens run as an
+            int8 MFMA grouped GEMM, the rest on the GEMV kernels; 16 layers
+            of distinct weights per pass; the JSON value is the n_sel = 8,
+            64-token point, the whole sweep is in "sweep".
 
 Printed: ONE JSON line. value = algorithmic HBM GB/s of the whole token
 (selected expert weights + q8_1 activation + fp32 output, per layer) with
@@ -273,6 +279,108 @@ def bench_dense(hip, name, steps, warmup):
     for b in (x, q, k, v, o, y):
         b.free()
     return res, (L, hidden, q_rows, kv_rows, ffn)
+
+
+# ---------------------------------------------------------------------------
+# Batched MoE (prefill) sweep
+# ---------------------------------------------------------------------------
+BATCH_SHAPE = (16, 2048, 768, 128)   # layers per pass, hidden, ffn, experts
+BATCH_POINTS = [(n, t) for n in (1, 2, 4, 8) for t in (1, 7, 16, 33, 64)]
+
+
+def zipf_routes(rng, T, n_expert, n_sel, s=1.1):
+    pop = 1.0 / np.arange(1, n_expert + 1) ** s
+    pop /= pop.sum()
+    order = rng.permutation(n_expert)
+    ids = np.empty((T, n_sel), np.int32)
+    w = np.empty((T, n_sel), np.float32)
+    for t in range(T):
+        pick = order[rng.choice(n_expert, n_sel, replace=False, p=pop)]
+        lw = rng.standard_normal(n_sel)
+        ww = np.exp(lw - lw.max())
+        ww /= ww.sum()
+        o = np.argsort(-ww, kind="stable")
+        ids[t], w[t] = pick[o], ww[o].astype(np.float32)
+    return ids, w
+
+
+def bench_moe_batch(hip, steps, warmup):
+    L, hidden, ffn, n_expert = BATCH_SHAPE
+    rb_g, rb_d = row_bytes(Q4_K, hidden), row_bytes(Q6_K, ffn)
+    expert_bytes = 2 * ffn * rb_g + hidden * rb_d
+    seed = 3000
+    layers = []
+    for _ in range(L):
+        bufs = []
+        for t, rows, cols in ((Q4_K, n_expert * ffn, hidden), (Q4_K, n_expert * ffn, hidden),
+                              (Q6_K, n_expert * hidden, ffn)):
+            b = hip.alloc(rows * row_bytes(t, cols))
+            hip.synth_fill(t, b, rows * cols // 256, seed)
+            seed += 1
+            bufs.append(b)
+        layers.append(bufs)
+    descs = [hip.moe_desc(hidden, ffn, n_expert, g, u, d) for g, u, d in layers]
+    rng = np.random.default_rng(2024)
+    x = hip.alloc(64 * hidden * 4)
+    y = hip.alloc(L * 64 * hidden * 4)
+    hip.synth_normal(x, 64 * hidden, 55)
+
+    class View:
+        def __init__(self, ptr):
+            self.ptr = ptr
+
+    points = []
+    for n_sel, T in BATCH_POINTS:
+        routes = [zipf_routes(rng, T, n_expert, n_sel) for _ in range(L)]
+        dev = [(hip.to_device(i), hip.to_device(w)) for i, w in routes]
+        distinct = sum(len(np.unique(i)) for i, _ in routes)
+        big = sum(int((np.bincount(i.reshape(-1), minlength=n_expert) >= 16).sum()) for i, _ in routes)
+
+        def run():
+            for li in range(L):
+                hip.moe_batch(descs[li], T, n_sel, dev[li][0], dev[li][1], x, View(y.ptr + li * 64 * hidden * 4))
+
+        run()
+        hip.sync()
+        hip.graph_begin()
+        run()
+        graph = hip.graph_end()
+        for _ in range(warmup):
+            hip.graph_launch(graph)
+        hip.sync()
+        e0, e1 = hip.event(), hip.event()
+        hip.record(e0)
+        for _ in range(steps):
+            hip.graph_launch(graph)
+        hip.record(e1)
+        ms = hip.elapsed_ms(e0, e1)
+        hip.sync()
+        for e in (e0, e1):
+            hip.event_destroy(e)
+        hip.graph_destroy(graph)
+        for a, b in dev:
+            a.free()
+            b.free()
+        layer_ms = ms / steps / L
+        bytes_per_layer = distinct / L * expert_bytes + T * (hidden // 32 * 36 + hidden * 4)
+        ops = T * n_sel * 2 * (2 * ffn * hidden + hidden * ffn)
+        points.append({
+            "n_sel": n_sel, "tokens": T, "layer_us": round(layer_ms * 1e3, 2),
+            "gbs": round(bytes_per_layer / (layer_ms / 1e3) / 1e9, 1),
+            "tok_s": round(T / (layer_ms / 1e3), 1),
+            "tops": round(ops / (layer_ms / 1e3) / 1e12, 2),
+            "experts_per_layer": round(distinct / L, 1), "grouped_gemm_experts_per_layer": round(big / L, 2),
+        })
+        print(f"[bench] moebatch n_sel={n_sel} T={T}: {points[-1]}", file=sys.stderr, flush=True)
+    for bufs in layers:
+        for b in bufs:
+            b.free()
+    for b in (x, y):
+        b.free()
+    head = next(p for p in points if p["n_sel"] == 8 and p["tokens"] == 64)
+    res = {"points": points, "head": head, "ms_per_step": head["layer_us"] * L / 1e3,
+           "value": head["gbs"], "pool_gb": L * n_expert * expert_bytes / 1e9}
+    return res, BATCH_SHAPE
 
 
 # ---------------------------------------------------------------------------
@@ -558,7 +666,7 @@ def main():
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", default="moe48",
-                    choices=sorted(MOE_WORKLOADS) + sorted(GEMV_WORKLOADS) + sorted(DENSE_WORKLOADS))
+                    choices=sorted(MOE_WORKLOADS) + sorted(GEMV_WORKLOADS) + sorted(DENSE_WORKLOADS) + ["moebatch"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="run one plain copy kernel of MIB MiB before the workload (untimed), as the "
@@ -603,6 +711,23 @@ def main():
         kernel = "MoE layer: k_moe_gu + k_moe_down (two launches per layer)"
         extra = {"tok_s": round(res["tok_s"], 2),
                  "eager_layer_ms_mean": round(res["kernel_ms_mean"], 5)}
+    elif args.workload == "moebatch":
+        res, shape = bench_moe_batch(hip, args.steps, args.warmup)
+        L, hidden, ffn, n_expert = shape
+        head = res["head"]
+        unit_ms = head["layer_us"] / 1e3
+        unit_bytes = head["gbs"] * 1e9 * unit_ms / 1e3
+        metric = "batched MoE layer HBM GB/s (% of ~8 TB/s peak), ragged Zipf-routed token batches"
+        config = {
+            "workload": f"moebatch: MoE layer over ragged token batches (1..64 tokens), hidden {hidden}, {n_expert} "
+                        f"experts, gate/up {hidden}->{ffn} Q4_K, down {ffn}->{hidden} Q6_K, per-token experts from a "
+                        f"Zipf(1.1) popularity, n_sel in {{1,2,4,8}}; experts with >= 16 tokens on the int8 MFMA "
+                        f"grouped GEMM; {L} layers of distinct weights per pass; headline point n_sel 8, 64 tokens",
+            "layers": L, "hidden": hidden, "ffn": ffn, "n_expert": n_expert, "parallelism": "single GPU",
+        }
+        kernel = "batched MoE layer (grouping, GEMV pairs, MFMA grouped GEMM, combine)"
+        extra = {"tok_s": head["tok_s"], "mfma_frac_of_int8_peak": round(head["tops"] / 5000.0, 4),
+                 "sweep": res["points"]}
     elif args.workload in DENSE_WORKLOADS:
         res, shape = bench_dense(hip, args.workload, args.steps, args.warmup)
         L, hidden, q_rows, kv_rows, ffn = shape
@@ -636,14 +761,17 @@ def main():
     print(f"[bench] gpu done: {res['value']:.1f} GB/s", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu_baseline:
-        if args.workload in MOE_WORKLOADS:
+        if args.workload == "moebatch":
+            cpu = None   # the reference has no batched GPU-shaped CPU counterpart timed here
+        elif args.workload in MOE_WORKLOADS:
             cpu = cpu_baseline_moe(shape)
         elif args.workload in DENSE_WORKLOADS:
             cpu = cpu_baseline_dense(shape)
         else:
             cpu = cpu_baseline_gemv(shape)
-        print(f"[bench] cpu baseline: {cpu['value']:.2f} GB/s ({cpu['kind']}, {cpu['cores']} threads)",
-              file=sys.stderr, flush=True)
+        if cpu:
+            print(f"[bench] cpu baseline: {cpu['value']:.2f} GB/s ({cpu['kind']}, {cpu['cores']} threads)",
+                  file=sys.stderr, flush=True)
     achieved = unit_bytes / (unit_ms / 1e3) / 1e9
     line = {
         "metric": metric,
