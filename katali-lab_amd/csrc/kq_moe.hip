@@ -50,11 +50,13 @@ __device__ __forceinline__ const float *route_logits(const MoeArgs &a) {
 // Lane l holds the keys of experts l, l + 64, ... (C chunks of 64 experts).
 // Selection: a binary search over key bits with wave ballots finds T, the
 // n_sel-th largest key; every key > T is selected, and of the keys == T the
-// lowest expert indexes fill the rest. Ranking: for each selected expert in
-// turn (uniform loop over the set bits of the selection ballots), its rank is
-// a ballot count of the selected experts ordered before it (larger key, or
-// equal key and lower index); lane `rank` takes it. Lane r < n_sel ends with
-// the expert and the canonical logit of rank r.
+// lowest expert indexes fill the rest. Ranking: the selected (key, expert)
+// pairs are packed into lanes 0..n_sel-1 (forward permute); a pair's rank is
+// the number of selected pairs ordered before it (larger key, or equal key
+// and lower index), counted against the other lanes of that 16-lane row with
+// DPP rotations; a second permute sends it to lane `rank`. No loop depends on
+// the data. Lane r < n_sel ends with the expert and the canonical logit of
+// rank r.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t logit_key(float v) {
     if (v != v) v = -INFINITY;
@@ -82,6 +84,21 @@ __device__ __forceinline__ void load_keys(const MoeArgs &a, float (&lv)[C]) {
     const float *src = route_logits(a);
 #pragma unroll
     for (int i = 0; i < C; i++) lv[i] = src[min(lane + 64 * i, a.n_expert - 1)];
+}
+
+// The value of lane (l +- S) of the same 16-lane row (DPP row_ror:S), 64 bits.
+template <int S>
+__device__ __forceinline__ uint64_t row_ror64(uint64_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, 0x120 + S, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), 0x120 + S, 0xF, 0xF, false);
+    return ((uint64_t)hi << 32) | lo;
+}
+// Number of the other 15 lanes of this lane's 16-lane row holding a larger v.
+template <int S>
+__device__ __forceinline__ int rank_in_row(uint64_t v) {
+    const int here = row_ror64<S>(v) > v ? 1 : 0;
+    if constexpr (S < 15) return here + rank_in_row<S + 1>(v);
+    else return here;
 }
 
 template <int C>
@@ -115,31 +132,36 @@ __device__ __forceinline__ WaveRoute wave_topk(const MoeArgs &a, const float (&l
         sm[i] = __ballot(sel[i]);
         eq_seen += __popcll(eq);
     }
-    WaveRoute r;
-    r.id = -1;
-    r.logit = 0.0f;
-    uint32_t rkey = 0;
+    // Compact the k selected (key, expert) pairs into lanes 0..k-1 (expert
+    // order) with forward permutes; unselected lanes all aim at lane 63, which
+    // no selected pair uses (k <= 16).
+    uint32_t ck = 0, ce = 0;
+    int base = 0;
 #pragma unroll
-    for (int j = 0; j < C; j++) {
-        uint64_t m = sm[j];
-        while (m) {   // uniform: n_sel iterations in total
-            const int src = __builtin_ctzll(m);
-            m &= m - 1;
-            const uint32_t x = (uint32_t)__builtin_amdgcn_readlane((int)key[j], src);
-            const uint32_t e = (uint32_t)src + 64 * j;
-            int rank = 0;
-#pragma unroll
-            for (int i = 0; i < C; i++) {
-                const uint32_t idx = lane + 64 * i;
-                rank += __popcll(__ballot(sel[i] && (key[i] > x || (key[i] == x && idx < e))));
-            }
-            if ((int)lane == rank) {
-                r.id = (int32_t)e;
-                rkey = x;
-            }
-        }
+    for (int i = 0; i < C; i++) {
+        const int cnt = __popcll(sm[i]);
+        const int dst = sel[i] ? base + popc_below(sm[i]) : 63;
+        const uint32_t pk = (uint32_t)__builtin_amdgcn_ds_permute(4 * dst, (int)key[i]);
+        const uint32_t pe = (uint32_t)__builtin_amdgcn_ds_permute(4 * dst, (int)(lane + 64 * i));
+        const bool mine = (int)lane >= base && (int)lane < base + cnt;
+        ck = mine ? pk : ck;
+        ce = mine ? pe : ce;
+        base += cnt;
     }
-    if ((int)lane < k) r.logit = key_logit(rkey);
+    // Rank inside the first 16-lane row: comp orders like (key desc, expert
+    // asc); lanes >= k carry 0, below every selected pair (a selected key is
+    // never 0 and ~expert is never 0). Each of the 15 row rotations brings one
+    // other lane of the row.
+    const bool valid = (int)lane < k;
+    const uint64_t comp = valid ? (((uint64_t)ck << 32) | (uint32_t)~ce) : 0ull;
+    const int rank = rank_in_row<1>(comp);
+    // lane `rank` takes the pair
+    const int dst = valid ? rank : 63;
+    const uint32_t fe = (uint32_t)__builtin_amdgcn_ds_permute(4 * dst, (int)ce);
+    const uint32_t fk = (uint32_t)__builtin_amdgcn_ds_permute(4 * dst, (int)ck);
+    WaveRoute r;
+    r.id = valid ? (int32_t)fe : -1;
+    r.logit = valid ? key_logit(fk) : 0.0f;
     return r;
 }
 
@@ -243,8 +265,10 @@ __device__ __forceinline__ float reduce_rows(float (&acc)[R]) {
 
 // ---------------------------------------------------------------------------
 // Kernel A: 64 Q4_K rows (32 gate + 32 up) per workgroup, NB blocks per row.
-// Wave w owns rows 16w..16w+15 (waves 0-1 gate, 2-3 up) and runs on its own
-// until the gate/up exchange at the end: no workgroup barrier before that.
+// Eight waves; wave w owns rows 8w..8w+7 (waves 0-3 gate, 4-7 up) and runs on
+// its own apart from the x staging barrier, until the gate/up exchange at the
+// end. (Eight waves of 8 rows rather than four of 16: two waves per SIMD hide
+// each other's routing and decode latency, and each wave's serial work halves.)
 // Lane l always takes the same lane item of every row it touches:
 //   ITEMS = 8*NB >= 64: the k-th chunk is item 64*(k % M) + l of row k / M
 //                       (M = ITEMS/64 items per lane);
@@ -252,7 +276,7 @@ __device__ __forceinline__ float reduce_rows(float (&acc)[R]) {
 //                       chunk is item l % ITEMS of row l / ITEMS + k*64/ITEMS.
 // x is quantized to q8_1 once per workgroup into LDS (8 lanes per 32-value
 // block) while the weights stream in; each lane then reads its items' q8
-// values once. The wave's 16*NB block headers are decoded once into a
+// values once. The wave's 8*NB block headers are decoded once into a
 // wave-private LDS area as {d*sc[2g]*d8[k], d*sc[2g+1]*d8[k+1],
 // dmin*m[2g]*d8[k], dmin*m[2g+1]*d8[k+1]} per group g, where k and k+1 are
 // the q8_1 blocks of x that group meets (a wavefront-scope sync, not a
@@ -264,8 +288,8 @@ struct LdsA {
 __host__ __device__ inline LdsA lds_a(uint32_t hidden, uint32_t nb) {
     LdsA L;
     L.xact = 0;
-    L.scl = L.xact + act_bytes(hidden);   // 4 waves x 16*nb headers x 4 groups x float4
-    L.gu = L.scl + 4 * 16 * nb * 64;
+    L.scl = L.xact + act_bytes(hidden);   // 64 rows x nb headers x 4 groups x float4
+    L.gu = L.scl + 64 * nb * 64;
     L.total = L.gu + 64 * 4;
     return L;
 }
@@ -318,16 +342,21 @@ __device__ __forceinline__ float item_dot(const uint4 &q, const float4 &sc, cons
     return fmaf(sc.x, (float)slo, fmaf(sc.y, (float)shi, -fmaf(sc.z, x.qlo, sc.w * x.qhi)));
 }
 
+constexpr int A_ROWS_PER_WAVE = 8;
+constexpr int A_THREADS = 64 * 64 / A_ROWS_PER_WAVE;
+
 template <int NB, int C>
-__global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
+__global__ void __launch_bounds__(A_THREADS) k_moe_gu(MoeArgs a) {
+    constexpr int RW = A_ROWS_PER_WAVE;
+    constexpr int NT = A_THREADS;
     constexpr int ITEMS = 8 * NB;              // lane items per row
-    constexpr int LPL = 2 * NB;                // 16 rows x ITEMS / 64 lanes
+    constexpr int LPL = RW * ITEMS / 64;       // chunks per lane over the wave's rows
     constexpr int GROUPS = LPL > 16 ? LPL / 16 : 1;
-    constexpr int RPG = 16 / GROUPS;           // rows per group
+    constexpr int RPG = RW / GROUPS;           // rows per group
     constexpr int LPG = RPG * ITEMS / 64;      // chunks per lane per group
     constexpr int M = ITEMS >= 64 ? ITEMS / 64 : 1;   // items per lane
     constexpr int LOG_RPG = RPG == 16 ? 4 : (RPG == 8 ? 3 : (RPG == 4 ? 2 : (RPG == 2 ? 1 : 0)));
-    constexpr int WH = 16 * NB;                // block headers of one wave's rows
+    constexpr int WH = RW * NB;                // block headers of one wave's rows
     constexpr int HPL = (WH + 63) / 64;        // header loads per lane
     extern __shared__ __align__(16) uint8_t lds[];
     const LdsA L = lds_a(a.hidden, NB);
@@ -364,16 +393,16 @@ __global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
         }
     }
     constexpr int XTASKS = 64 * NB;            // quantizer lane tasks (8 per 32-block)
-    constexpr int XPT = (XTASKS + 255) / 256;
+    constexpr int XPT = (XTASKS + NT - 1) / NT;
     float4 xv[XPT];
     uint32_t xqv[XPT], xdv[XPT];
     if (xq == nullptr) {
 #pragma unroll
-        for (int i = 0; i < XPT; i++) xv[i] = *(const float4 *)(a.x + 4 * min(tid + 256 * i, (uint32_t)XTASKS - 1));
+        for (int i = 0; i < XPT; i++) xv[i] = *(const float4 *)(a.x + 4 * min(tid + NT * i, (uint32_t)XTASKS - 1));
     } else {
 #pragma unroll
         for (int i = 0; i < XPT; i++) {
-            const uint32_t t = min(tid + 256 * i, (uint32_t)XTASKS - 1);
+            const uint32_t t = min(tid + NT * i, (uint32_t)XTASKS - 1);
             const uint8_t *b = xq + (t >> 3) * 36;
             xqv[i] = *(const uint32_t *)(b + 4 + 4 * (t & 7));
             xdv[i] = ld_u16(b);
@@ -414,7 +443,7 @@ __global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
             r = lane / ITEMS + k * (64 / ITEMS);
             it = lane % ITEMS;
         }
-        return row_ptr(16 * wave + r) + (it / 8) * 144 + 16 + 16 * (it % 8);
+        return row_ptr(RW * wave + r) + (it / 8) * 144 + 16 + 16 * (it % 8);
     };
 
     // every weight load of the wave: its block headers first, then chunks
@@ -422,7 +451,7 @@ __global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
 #pragma unroll
     for (int i = 0; i < HPL; i++) {
         const uint32_t h = min(lane + 64 * i, (uint32_t)WH - 1);   // duplicates decode the same header
-        hv[i] = ld16(row_ptr(16 * wave + h / NB) + (h % NB) * 144);
+        hv[i] = ld16(row_ptr(RW * wave + h / NB) + (h % NB) * 144);
     }
     uint4 q[LPG];
 #pragma unroll
@@ -436,7 +465,7 @@ __global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
     const Act xa = act_carve(lds + L.xact, a.hidden);
 #pragma unroll
     for (int i = 0; i < XPT; i++) {
-        const uint32_t t = tid + 256 * i, blk = t >> 3, part = t & 7;
+        const uint32_t t = tid + NT * i, blk = t >> 3, part = t & 7;
         if (t >= XTASKS) break;   // whole 8-lane groups leave together
         uint32_t qv;
         int lo, hi;
@@ -502,7 +531,7 @@ __global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
             const float v = reduce_rows<RPG>(acc);
             constexpr int SH = 6 - LOG_RPG;
             const uint32_t r = (lane >> SH) & (RPG - 1);
-            if ((lane & ((1u << SH) - 1)) == 0) gu[16 * wave + grp * RPG + r] = v;
+            if ((lane & ((1u << SH) - 1)) == 0) gu[RW * wave + grp * RPG + r] = v;
         } else {
             const uint32_t it = lane % ITEMS;
 #pragma unroll
@@ -510,7 +539,7 @@ __global__ void __launch_bounds__(256) k_moe_gu(MoeArgs a) {
                 const uint32_t row = lane / ITEMS + k * (64 / ITEMS);   // within the wave
                 const float4 sc = scl[4 * (row * NB + it / 8) + (it % 8) / 2];
                 const float v = group_sum<ITEMS>(item_dot(q[k], sc, xs[0]));
-                if (it == 0) gu[16 * wave + row] = v;
+                if (it == 0) gu[RW * wave + row] = v;
             }
         }
     }
@@ -687,11 +716,11 @@ static hipError_t go_a(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
     const LdsA L = lds_a(a.hidden, NB);
     const dim3 grid(n_slots * (a.ffn / 32));
     if (a.n_expert <= 128)
-        hipLaunchKernelGGL((k_moe_gu<NB, 2>), grid, dim3(256), L.total, s, a);
+        hipLaunchKernelGGL((k_moe_gu<NB, 2>), grid, dim3(A_THREADS), L.total, s, a);
     else if (a.n_expert <= 256)
-        hipLaunchKernelGGL((k_moe_gu<NB, 4>), grid, dim3(256), L.total, s, a);
+        hipLaunchKernelGGL((k_moe_gu<NB, 4>), grid, dim3(A_THREADS), L.total, s, a);
     else
-        hipLaunchKernelGGL((k_moe_gu<NB, 8>), grid, dim3(256), L.total, s, a);
+        hipLaunchKernelGGL((k_moe_gu<NB, 8>), grid, dim3(A_THREADS), L.total, s, a);
     return hipGetLastError();
 }
 
