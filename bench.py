@@ -304,7 +304,7 @@ def zipf_routes(rng, T, n_expert, n_sel, s=1.1):
     return ids, w
 
 
-def bench_moe_batch(hip, steps, warmup):
+def bench_moe_batch(hip, steps, warmup, only=None):
     L, hidden, ffn, n_expert = BATCH_SHAPE
     rb_g, rb_d = row_bytes(Q4_K, hidden), row_bytes(Q6_K, ffn)
     expert_bytes = 2 * ffn * rb_g + hidden * rb_d
@@ -330,7 +330,7 @@ def bench_moe_batch(hip, steps, warmup):
             self.ptr = ptr
 
     points = []
-    for n_sel, T in BATCH_POINTS:
+    for n_sel, T in (only or BATCH_POINTS):
         routes = [zipf_routes(rng, T, n_expert, n_sel) for _ in range(L)]
         dev = [(hip.to_device(i), hip.to_device(w)) for i, w in routes]
         distinct = sum(len(np.unique(i)) for i, _ in routes)
@@ -377,7 +377,7 @@ def bench_moe_batch(hip, steps, warmup):
             b.free()
     for b in (x, y):
         b.free()
-    head = next(p for p in points if p["n_sel"] == 8 and p["tokens"] == 64)
+    head = next((p for p in points if p["n_sel"] == 8 and p["tokens"] == 64), points[-1])
     res = {"points": points, "head": head, "ms_per_step": head["layer_us"] * L / 1e3,
            "value": head["gbs"], "pool_gb": L * n_expert * expert_bytes / 1e9}
     return res, BATCH_SHAPE
@@ -668,6 +668,8 @@ def main():
     ap.add_argument("--workload", default="moe48",
                     choices=sorted(MOE_WORKLOADS) + sorted(GEMV_WORKLOADS) + sorted(DENSE_WORKLOADS) + ["moebatch"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--batch-points", default="", metavar="NxT,...",
+                    help="moebatch: only these (n_sel x tokens) points, e.g. 8x64,2x64 (profiling)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="run one plain copy kernel of MIB MiB before the workload (untimed), as the "
                          "known-size reference for HBM counter profiles")
@@ -712,7 +714,8 @@ def main():
         extra = {"tok_s": round(res["tok_s"], 2),
                  "eager_layer_ms_mean": round(res["kernel_ms_mean"], 5)}
     elif args.workload == "moebatch":
-        res, shape = bench_moe_batch(hip, args.steps, args.warmup)
+        only = [tuple(int(v) for v in pt.split("x")) for pt in args.batch_points.split(",") if pt] or None
+        res, shape = bench_moe_batch(hip, args.steps, args.warmup, only)
         L, hidden, ffn, n_expert = shape
         head = res["head"]
         unit_ms = head["layer_us"] / 1e3

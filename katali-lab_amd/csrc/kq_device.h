@@ -58,6 +58,11 @@ __device__ __forceinline__ uint2 ld8(const uint8_t *p) {
     __builtin_memcpy(&v, p, 8);
     return v;
 }
+__device__ __forceinline__ uint32_t ld4(const uint8_t *p) {
+    uint32_t v;
+    __builtin_memcpy(&v, p, 4);
+    return v;
+}
 __device__ __forceinline__ uint32_t ld_u16(const uint8_t *p) {
     uint16_t v;
     __builtin_memcpy(&v, p, 2);
@@ -323,9 +328,7 @@ struct Q4K {
         dm1 = dmin * (float)((mn >> 8) & 0xFFu);
     }
     // fp32 contribution of the item against a q8_1 activation (block b)
-    __device__ static __forceinline__ float dot_q8(const Raw &r, int c, const Act &a, uint32_t b) {
-        int slo, shi;
-        isums(r, c, a.qs + 256 * b, slo, shi);
+    __device__ static __forceinline__ float finish(const Raw &r, int c, const Act &a, uint32_t b, int slo, int shi) {
         const int g = c >> 1, hh = c & 1;
         float ds0, ds1, dm0, dm1;
         scales(r, g, ds0, ds1, dm0, dm1);
@@ -333,6 +336,38 @@ struct Q4K {
         const float vlo = fmaf(ds0, (float)slo, -(dm0 * (float)a.qs16[2 * k + hh]));
         const float vhi = fmaf(ds1, (float)shi, -(dm1 * (float)a.qs16[2 * k + 2 + hh]));
         return fmaf(a.d8[k], vlo, a.d8[k + 1] * vhi);
+    }
+    __device__ static __forceinline__ float dot_q8(const Raw &r, int c, const Act &a, uint32_t b) {
+        int slo, shi;
+        isums(r, c, a.qs + 256 * b, slo, shi);
+        return finish(r, c, a, b, slo, shi);
+    }
+    // the item's nibbles unpacked once, for dots against several activations
+    struct Unp {
+        uint4 lo, hi;
+    };
+    __device__ static __forceinline__ Unp unpack(const Raw &r) {
+        const uint32_t m = 0x0F0F0F0Fu;
+        Unp u;
+        u.lo = make_uint4(r.q.x & m, r.q.y & m, r.q.z & m, r.q.w & m);
+        u.hi = make_uint4((r.q.x >> 4) & m, (r.q.y >> 4) & m, (r.q.z >> 4) & m, (r.q.w >> 4) & m);
+        return u;
+    }
+    // dot_q8 with the nibbles unpacked beforehand (the same sums and float ops)
+    __device__ static __forceinline__ float dot_q8_u(const Raw &r, const Unp &u, int c, const Act &a, uint32_t b) {
+        const int g = c >> 1, hh = c & 1;
+        const int8_t *al = a.qs + 256 * b + 64 * g + 16 * hh;
+        const int4 xl = *(const int4 *)al;
+        const int4 xh = *(const int4 *)(al + 32);
+        int slo = dot4(u.lo.x, xl.x, 0);
+        slo = dot4(u.lo.y, xl.y, slo);
+        slo = dot4(u.lo.z, xl.z, slo);
+        slo = dot4(u.lo.w, xl.w, slo);
+        int shi = dot4(u.hi.x, xh.x, 0);
+        shi = dot4(u.hi.y, xh.y, shi);
+        shi = dot4(u.hi.z, xh.z, shi);
+        shi = dot4(u.hi.w, xh.w, shi);
+        return finish(r, c, a, b, slo, shi);
     }
     // fp32 contribution of the item against a float activation (block b)
     __device__ static __forceinline__ float dot_f32(const Raw &r, int c, const ActF &a, uint32_t b) {
@@ -418,9 +453,7 @@ struct Q6K {
         const int sh = 8 * (2 * (t & 1) + k);
         return (float)(int)(int8_t)(w >> sh);
     }
-    __device__ static __forceinline__ float dot_q8(const Raw &r, int c, const Act &a, uint32_t b) {
-        int s[4];
-        isums(r, c, a, b, s);
+    __device__ static __forceinline__ float finish(const Raw &r, int c, const Act &a, uint32_t b, const int s[4]) {
         const int n = c >> 1, k = c & 1;
         const float d = h2f(r.d);
         const uint32_t k8 = 8 * b + 4 * n;   // q8 block of quarter 0
@@ -428,6 +461,43 @@ struct Q6K {
 #pragma unroll
         for (int t = 1; t < 4; t++) acc = fmaf(a.d8[k8 + t], (d * scale(r, k, t)) * (float)s[t], acc);
         return acc;
+    }
+    __device__ static __forceinline__ float dot_q8(const Raw &r, int c, const Act &a, uint32_t b) {
+        int s[4];
+        isums(r, c, a, b, s);
+        return finish(r, c, a, b, s);
+    }
+    // the item's 6-bit values unpacked once (quarter t, dword j), for dots
+    // against several activations
+    struct Unp {
+        uint32_t v[4][4];
+    };
+    __device__ static __forceinline__ Unp unpack(const Raw &r) {
+        const uint32_t A[4] = {r.A.x, r.A.y, r.A.z, r.A.w};
+        const uint32_t B[4] = {r.B.x, r.B.y, r.B.z, r.B.w};
+        const uint32_t H[4] = {r.H.x, r.H.y, r.H.z, r.H.w};
+        Unp u;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) u.v[t][j] = q6(A[j], B[j], H[j], t);
+        return u;
+    }
+    // dot_q8 with the values unpacked beforehand (the same sums and float ops)
+    __device__ static __forceinline__ float dot_q8_u(const Raw &r, const Unp &u, int c, const Act &a, uint32_t b) {
+        const int n = c >> 1, k = c & 1;
+        int s[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const uint32_t e0 = 256 * b + 128 * n + 32 * t + 16 * k;
+            const int4 x = *(const int4 *)(a.qs + e0);
+            int acc = dot4(u.v[t][0], x.x, 0);
+            acc = dot4(u.v[t][1], x.y, acc);
+            acc = dot4(u.v[t][2], x.z, acc);
+            acc = dot4(u.v[t][3], x.w, acc);
+            s[t] = acc - 32 * a.qs16[e0 / 16];
+        }
+        return finish(r, c, a, b, s);
     }
     __device__ static __forceinline__ float dot_f32(const Raw &r, int c, const ActF &a, uint32_t b) {
         const int n = c >> 1, k = c & 1;

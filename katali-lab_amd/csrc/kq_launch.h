@@ -76,6 +76,9 @@ struct MoeArgs {
     uint32_t bS;
     uint64_t xq_stride;
     float *yp;
+    // Grouped batch mode: bslot holds {expert, first, count} entries and the
+    // entry's pairs are border[first .. first + count).
+    const int32_t *border;
 };
 bool moe_shape_supported(uint32_t gate_type, uint32_t down_type, uint32_t hidden, uint32_t ffn);
 hipError_t launch_moe(const MoeArgs &a, hipStream_t s);
@@ -83,6 +86,10 @@ hipError_t launch_moe(const MoeArgs &a, hipStream_t s);
 // sized for max_slots; workgroups past *bcount exit at once).
 hipError_t launch_moe_pairs_gu(const MoeArgs &a, uint32_t max_slots, hipStream_t s);
 hipError_t launch_moe_pairs_down(const MoeArgs &a, uint32_t max_slots, hipStream_t s);
+// Grouped batch mode over up to max_entries entries of <= 8 pairs of one
+// expert (the batched layer's GEMV path).
+hipError_t launch_moe_groups_gu(const MoeArgs &a, uint32_t max_entries, hipStream_t s);
+hipError_t launch_moe_groups_down(const MoeArgs &a, uint32_t max_entries, hipStream_t s);
 // MoE layer over T <= 64 tokens (a.ids / a.wts: [T][n_sel]; a.hq8: P rows of
 // ffn/32 q8_1 blocks, a.yp: [P][hidden], P = T * (n_sel + shared)). Experts
 // gathering >= min_big pairs use the int8 MFMA grouped GEMM, the rest the

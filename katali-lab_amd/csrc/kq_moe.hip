@@ -341,6 +341,18 @@ __device__ __forceinline__ float item_dot(const uint4 &q, const float4 &sc, cons
     Q4K::isums_x(q, x.xl, x.xh, slo, shi);
     return fmaf(sc.x, (float)slo, fmaf(sc.y, (float)shi, -fmaf(sc.z, x.qlo, sc.w * x.qhi)));
 }
+// item_dot with the nibbles unpacked beforehand (the same sums and float ops)
+__device__ __forceinline__ float item_dot_u(const Q4K::Unp &u, const float4 &sc, const XSlice &x) {
+    int slo = dot4(u.lo.x, x.xl.x, 0);
+    slo = dot4(u.lo.y, x.xl.y, slo);
+    slo = dot4(u.lo.z, x.xl.z, slo);
+    slo = dot4(u.lo.w, x.xl.w, slo);
+    int shi = dot4(u.hi.x, x.xh.x, 0);
+    shi = dot4(u.hi.y, x.xh.y, shi);
+    shi = dot4(u.hi.z, x.xh.z, shi);
+    shi = dot4(u.hi.w, x.xh.w, shi);
+    return fmaf(sc.x, (float)slo, fmaf(sc.y, (float)shi, -fmaf(sc.z, x.qlo, sc.w * x.qhi)));
+}
 
 constexpr int A_ROWS_PER_WAVE = 8;
 constexpr int A_THREADS = 64 * 64 / A_ROWS_PER_WAVE;
@@ -456,6 +468,7 @@ __global__ void __launch_bounds__(A_THREADS) k_moe_gu(MoeArgs a) {
     uint4 q[LPG];
 #pragma unroll
     for (int k = 0; k < LPG; k++) q[k] = ld16(chunk(0, k));
+
     if (publisher) {
         if (a.logits && a.n_sel > 0) ew = route_weight(route_l, a.n_sel);
         route_publish(a, eid, ew);
@@ -709,6 +722,241 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a, uint32_t tr, uint32
     }
 }
 
+// ---------------------------------------------------------------------------
+// Grouped batch mode: the GEMV path of the batched layer. An entry is up to
+// GRP_MAX (token, rank) pairs routed to one expert, listed as {expert,
+// first, count} (a.bslot, *a.bcount entries) with the pairs at
+// a.border[first ..]. A workgroup reads its weight rows once and dots them
+// with every pair of the entry, whose activations are staged in LDS. The
+// item mapping, scale products, reductions and h quantization are those of
+// kernels A and B, so a pair's h and down output are bit-identical to the
+// single-token layer's.
+// ---------------------------------------------------------------------------
+constexpr uint32_t GRP_MAX = 8;
+
+// Stage n rows of K q8_1 values (row g read from src_of(g)) into LDS
+// activations at base + g * act_bytes(K), one 16-byte half block per task.
+template <class SrcOf>
+__device__ __forceinline__ void stage_rows_q8(uint8_t *base, uint32_t K, uint32_t n, SrcOf src_of) {
+    const uint32_t nblk = K / 32, ab = act_bytes(K), ntask = n * nblk * 2;
+    for (uint32_t t = threadIdx.x; t < ntask; t += blockDim.x) {
+        const uint32_t g = t / (2 * nblk), r = t % (2 * nblk), kb = r >> 1, half = r & 1;
+        const uint8_t *b = src_of(g) + (uint64_t)kb * 36;
+        const uint4 q = ld16(b + 4 + 16 * half);
+        const Act act = act_carve(base + g * ab, K);
+        *(uint4 *)(act.qs + 32 * kb + 16 * half) = q;
+        int sum = dot4(q.x, 0x01010101u, 0);
+        sum = dot4(q.y, 0x01010101u, sum);
+        sum = dot4(q.z, 0x01010101u, sum);
+        sum = dot4(q.w, 0x01010101u, sum);
+        act.qs16[2 * kb + half] = sum;
+        if (half == 0) act.d8[kb] = h2f(ld_u16(b));
+    }
+}
+
+struct LdsG {
+    uint32_t xact, scl, gu, total;
+};
+__host__ __device__ inline LdsG lds_g(uint32_t hidden, uint32_t nb) {
+    LdsG L;
+    L.xact = 0;
+    L.scl = GRP_MAX * act_bytes(hidden);   // 64 rows x nb headers x 4 groups x float4 (scales without x)
+    L.gu = L.scl + 64 * nb * 64;
+    L.total = L.gu + GRP_MAX * 64 * 4;
+    return L;
+}
+
+template <int NB>
+__global__ void __launch_bounds__(A_THREADS) k_moe_gu_grp(MoeArgs a) {
+    constexpr int RW = A_ROWS_PER_WAVE;
+    constexpr int ITEMS = 8 * NB;
+    constexpr int LPG = RW * ITEMS / 64;   // chunks per lane (one row group: RW = 8, NB <= 16)
+    constexpr int M = ITEMS >= 64 ? ITEMS / 64 : 1;
+    constexpr int WH = RW * NB, HPL = (WH + 63) / 64;
+    static_assert(LPG <= 16 && RW == 8, "one row group of 8 rows per wave");
+    extern __shared__ __align__(16) uint8_t lds[];
+    const LdsG L = lds_g(a.hidden, NB);
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t nblk = a.ffn / 32;
+    const uint32_t ei = blockIdx.x / nblk, jb = blockIdx.x % nblk;
+    if (ei >= (uint32_t)*a.bcount) return;   // whole workgroup, before any barrier
+    const int32_t *ent = a.bslot + 3 * ei;
+    const uint32_t ex = (uint32_t)ent[0], cnt = (uint32_t)ent[2];
+    const int32_t *pairs = a.border + ent[1];
+    const uint64_t rb = NB * 144;
+    const bool shared = ex >= a.n_expert;   // the grouping gives the shared expert id n_expert
+    const uint8_t *gb = shared ? a.gate_sh : a.gate + (uint64_t)ex * a.ffn * rb;
+    const uint8_t *ub = shared ? a.up_sh : a.up + (uint64_t)ex * a.ffn * rb;
+    auto row_ptr = [&](uint32_t v) -> const uint8_t * {   // v in [0, 64)
+        return v < 32 ? gb + (uint64_t)(32 * jb + v) * rb : ub + (uint64_t)(32 * jb + v - 32) * rb;
+    };
+    auto chunk = [&](int k) -> const uint8_t * {
+        uint32_t r, it;
+        if constexpr (ITEMS >= 64) {
+            r = k / M;
+            it = 64 * (k % M) + lane;
+        } else {
+            r = lane / ITEMS + k * (64 / ITEMS);
+            it = lane % ITEMS;
+        }
+        return row_ptr(RW * wave + r) + (it / 8) * 144 + 16 + 16 * (it % 8);
+    };
+    // the weights (HBM) first, then the entry's activations (L2)
+    uint4 hv[HPL];
+#pragma unroll
+    for (int i = 0; i < HPL; i++) {
+        const uint32_t h = min(lane + 64 * i, (uint32_t)WH - 1);
+        hv[i] = ld16(row_ptr(RW * wave + h / NB) + (h % NB) * 144);
+    }
+    uint4 q[LPG];
+#pragma unroll
+    for (int k = 0; k < LPG; k++) q[k] = ld16(chunk(k));
+    const uint32_t ab = act_bytes(a.hidden);
+    stage_rows_q8(lds + L.xact, a.hidden, cnt,
+                  [&](uint32_t g) { return a.xq + (uint64_t)((uint32_t)pairs[g] / a.bS) * a.xq_stride; });
+    // the wave's headers -> {d*sc, d*sc', dmin*m, dmin*m'} per group (x's
+    // q8_1 scales are applied per pair below, in kernel A's order)
+    float4 *scl = (float4 *)(lds + L.scl) + 4 * WH * wave;
+#pragma unroll
+    for (int i = 0; i < HPL; i++) {
+        const uint32_t h = lane + 64 * i;
+        if (h < WH) {
+            Q4K::Raw raw;
+            raw.h = hv[i];
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                float ds0, ds1, dm0, dm1;
+                Q4K::scales(raw, g, ds0, ds1, dm0, dm1);
+                scl[4 * h + g] = make_float4(ds0, ds1, dm0, dm1);
+            }
+        }
+    }
+    // nibbles unpacked once for all pairs (when the registers allow)
+    constexpr bool UNP = LPG <= 8;
+    Q4K::Unp qu[UNP ? LPG : 1];
+    if constexpr (UNP) {
+#pragma unroll
+        for (int k = 0; k < LPG; k++) {
+            Q4K::Raw raw;
+            raw.q = q[k];
+            qu[k] = Q4K::unpack(raw);
+        }
+    }
+    __syncthreads();   // activations staged; the scale table is wave-private
+
+    float *gu = (float *)(lds + L.gu);
+    for (uint32_t g = 0; g < cnt; g++) {
+        const Act xa = act_carve(lds + L.xact + g * ab, a.hidden);
+        if constexpr (ITEMS >= 64) {
+            XSlice xs[M];
+            float2 d8[M];
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                const uint32_t it = 64 * m + lane, k8 = 8 * (it / 8) + 2 * ((it % 8) >> 1);
+                xs[m] = x_slice(xa, it);
+                d8[m] = make_float2(xa.d8[k8], xa.d8[k8 + 1]);
+            }
+            float acc[RW];
+#pragma unroll
+            for (int r = 0; r < RW; r++) acc[r] = 0.0f;
+#pragma unroll
+            for (int k = 0; k < LPG; k++) {
+                const uint32_t it = 64 * (k % M) + lane;
+                const uint32_t row = k / M;
+                const float4 s0 = scl[4 * (row * NB + it / 8) + (it % 8) / 2];
+                const float2 dd = d8[k % M];
+                const float4 sc = make_float4(s0.x * dd.x, s0.y * dd.y, s0.z * dd.x, s0.w * dd.y);
+                if constexpr (UNP) acc[row] += item_dot_u(qu[k], sc, xs[k % M]);
+                else acc[row] += item_dot(q[k], sc, xs[k % M]);
+            }
+            const float v = reduce_rows<RW>(acc);
+            const uint32_t r = (lane >> 3) & (RW - 1);
+            if ((lane & 7) == 0) gu[64 * g + RW * wave + r] = v;
+        } else {
+            const uint32_t it = lane % ITEMS, k8 = 8 * (it / 8) + 2 * ((it % 8) >> 1);
+            const XSlice xs = x_slice(xa, it);
+            const float2 dd = make_float2(xa.d8[k8], xa.d8[k8 + 1]);
+#pragma unroll
+            for (int k = 0; k < LPG; k++) {
+                const uint32_t row = lane / ITEMS + k * (64 / ITEMS);
+                const float4 s0 = scl[4 * (row * NB + it / 8) + (it % 8) / 2];
+                const float4 sc = make_float4(s0.x * dd.x, s0.y * dd.y, s0.z * dd.x, s0.w * dd.y);
+                const float v = group_sum<ITEMS>(UNP ? item_dot_u(qu[k], sc, xs) : item_dot(q[k], sc, xs));
+                if (it == 0) gu[64 * g + RW * wave + row] = v;
+            }
+        }
+    }
+    __syncthreads();
+    // h of pair g (wave g % 8): kernel A's q8_1 block
+    for (uint32_t g = wave; g < cnt; g += A_THREADS / 64) {
+        const uint32_t j = lane & 31;
+        const float h = kq_silu_mul(gu[64 * g + j], gu[64 * g + 32 + j]);
+        const float am = max32(fabsf(h));
+        const float d = am / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        const int qv = (int)roundf(h * id);
+        const int total = sum32(qv);
+        uint8_t *blk = a.hq8 + ((uint64_t)pairs[g] * nblk + jb) * 36;
+        if (lane < 32) blk[4 + lane] = (uint8_t)(qv & 255);
+        if (lane == 0) *(uint32_t *)blk = f2h_rne(d) | (f2h_rne((float)total * d) << 16);
+    }
+}
+
+// Down for an entry: kernel B's tile (tr rows, S = IPB * P lanes per row, the
+// same blocks per lane), every pair's h staged in LDS, each pair's unweighted
+// output row to yp.
+template <class QD, int IPL, int P>
+__global__ void __launch_bounds__(256) k_moe_down_grp(MoeArgs a, uint32_t tr) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const uint32_t tid = threadIdx.x;
+    if (blockIdx.y >= (uint32_t)*a.bcount) return;   // whole workgroup, before any barrier
+    const int32_t *ent = a.bslot + 3 * blockIdx.y;
+    const uint32_t ex = (uint32_t)ent[0], cnt = (uint32_t)ent[2];
+    const int32_t *pairs = a.border + ent[1];
+    constexpr uint32_t S = QD::IPB * P;
+    const uint32_t ls = tid / S, s = tid % S;
+    const uint32_t item = s % QD::IPB, sub = s / QD::IPB;
+    const uint32_t row0 = blockIdx.x * tr;
+    const uint32_t nrows = row0 + tr <= a.hidden ? tr : a.hidden - row0;
+    const uint64_t rbd = (uint64_t)(a.ffn / 256) * QD::BB;
+    const uint32_t nbk = a.ffn / 256;
+    const bool active = ls < nrows;
+    const uint32_t r = min(ls, nrows - 1);   // idle lane-slots load a real row and drop it
+    const uint8_t *db = ex >= a.n_expert ? a.down_sh : a.down + (uint64_t)ex * a.hidden * rbd;
+    const uint8_t *rp = db + (uint64_t)(row0 + r) * rbd;
+    typename QD::Raw raw[IPL > 0 ? IPL : 1];
+    if constexpr (IPL > 0) {
+#pragma unroll
+        for (int i = 0; i < IPL; i++) raw[i] = QD::load(rp + min(sub + P * i, nbk - 1) * QD::BB, (int)item);
+    }
+    const uint64_t hstride = (uint64_t)(a.ffn / 32) * 36;
+    stage_rows_q8(lds, a.ffn, cnt, [&](uint32_t g) { return a.hq8 + (uint64_t)pairs[g] * hstride; });
+    // the quants are unpacked once for all pairs
+    typename QD::Unp unp[IPL > 0 ? IPL : 1];
+    if constexpr (IPL > 0) {
+#pragma unroll
+        for (int i = 0; i < IPL; i++) unp[i] = QD::unpack(raw[i]);
+    }
+    __syncthreads();
+    const uint32_t ab = act_bytes(a.ffn);
+    for (uint32_t g = 0; g < cnt; g++) {
+        const Act act = act_carve(lds + g * ab, a.ffn);
+        float x = 0.0f;
+        if constexpr (IPL > 0) {
+#pragma unroll
+            for (int i = 0; i < IPL; i++) {
+                const uint32_t b = sub + P * i;
+                const float v = QD::dot_q8_u(raw[i], unp[i], (int)item, act, min(b, nbk - 1));
+                x += b < nbk ? v : 0.0f;
+            }
+        } else {
+            for (uint32_t b = sub; b < nbk; b += P) x += QD::dot_q8(QD::load(rp + b * QD::BB, (int)item), (int)item, act, b);
+        }
+        x = group_sum<S>(x);
+        if (active && s == 0) a.yp[(uint64_t)pairs[g] * a.hidden + row0 + ls] = x;
+    }
+}
+
 uint64_t moe_route_words() { return 2 * MAX_SLOTS; }
 
 template <int NB>
@@ -724,11 +972,17 @@ static hipError_t go_a(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Kernel B's tile: TR output rows x n_slots pairs per workgroup of 256
+// threads, S = IPB * P lanes per pair.
+template <class QD>
+static uint32_t b_tile_rows(uint32_t P, uint32_t n_slots) {
+    const uint32_t tr = 256 / (QD::IPB * P) / n_slots;
+    return tr < 1 ? 1 : tr;
+}
+
 template <class QD, int IPL, int P>
 static hipError_t go_b(const MoeArgs &a, uint32_t n_slots, uint32_t grid_y, hipStream_t s) {
-    const uint32_t lane_slots = 256 / (QD::IPB * P);
-    uint32_t tr = lane_slots / n_slots;
-    if (tr < 1) tr = 1;
+    const uint32_t tr = b_tile_rows<QD>(P, n_slots);
     const LdsB L = lds_b(a.ffn, n_slots, tr);
     hipLaunchKernelGGL((k_moe_down<QD, IPL, P>), dim3((a.hidden + tr - 1) / tr, grid_y), dim3(256), L.total, s, a, tr,
                        n_slots);
@@ -737,16 +991,23 @@ static hipError_t go_b(const MoeArgs &a, uint32_t n_slots, uint32_t grid_y, hipS
 
 // P = lanes-per-pair multiplier: the smallest power of two that brings a
 // lane's blocks (IPL = ceil(nb / P)) to at most 4 while a workgroup still
-// holds every slot of at least one output row.
+// holds every slot of at least one output row; 1 (a runtime block loop when
+// IPL > 4) where no unrolled variant fits.
 template <class QD>
-static hipError_t go_b_any(const MoeArgs &a, uint32_t n_slots, uint32_t grid_y, hipStream_t s) {
-    const uint32_t nb = a.ffn / 256;
+static uint32_t b_mult(uint32_t nb, uint32_t n_slots) {
     uint32_t p = 1;
     while ((nb + p - 1) / p > 4 && QD::IPB * 4 * p <= 64 && QD::IPB * 4 * p * n_slots <= 256) p *= 4;
     const uint32_t ipl = (nb + p - 1) / p;
-    if (QD::IPB * p * n_slots > 256 || ipl > 4) return go_b<QD, 0, 1>(a, n_slots, grid_y, s);
-    const uint32_t key = p * 8 + ipl;
-    switch (key) {
+    if (QD::IPB * p * n_slots > 256 || ipl > 4 || QD::IPB * p > 64) return 1;
+    return p;
+}
+
+template <class QD>
+static hipError_t go_b_any(const MoeArgs &a, uint32_t n_slots, uint32_t grid_y, hipStream_t s) {
+    const uint32_t nb = a.ffn / 256;
+    const uint32_t p = b_mult<QD>(nb, n_slots);
+    const uint32_t ipl = (nb + p - 1) / p;
+    switch (p * 8 + ipl) {
         case 1 * 8 + 1: return go_b<QD, 1, 1>(a, n_slots, grid_y, s);
         case 1 * 8 + 2: return go_b<QD, 2, 1>(a, n_slots, grid_y, s);
         case 1 * 8 + 3: return go_b<QD, 3, 1>(a, n_slots, grid_y, s);
@@ -757,7 +1018,7 @@ static hipError_t go_b_any(const MoeArgs &a, uint32_t n_slots, uint32_t grid_y, 
         default: break;
     }
     if constexpr (QD::IPB * 16 <= 64) {
-        switch (key) {
+        switch (p * 8 + ipl) {
             case 16 * 8 + 2: return go_b<QD, 2, 16>(a, n_slots, grid_y, s);
             case 16 * 8 + 3: return go_b<QD, 3, 16>(a, n_slots, grid_y, s);
             case 16 * 8 + 4: return go_b<QD, 4, 16>(a, n_slots, grid_y, s);
@@ -793,6 +1054,76 @@ static hipError_t go_a_any(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
         case 16: return go_a<16>(a, n_slots, s);
         default: return hipErrorInvalidValue;
     }
+}
+
+template <int NB>
+static hipError_t go_a_grp(const MoeArgs &a, uint32_t max_entries, hipStream_t s) {
+    const LdsG L = lds_g(a.hidden, NB);
+    if (L.total > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute((const void *)k_moe_gu_grp<NB>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)L.total);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(k_moe_gu_grp<NB>, dim3(max_entries * (a.ffn / 32)), dim3(A_THREADS), L.total, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_groups_gu(const MoeArgs &a, uint32_t max_entries, hipStream_t s) {
+    if (!a.bslot || !a.bcount || !a.border || max_entries == 0) return hipErrorInvalidValue;
+    switch (a.hidden / 256) {
+        case 1: return go_a_grp<1>(a, max_entries, s);
+        case 2: return go_a_grp<2>(a, max_entries, s);
+        case 4: return go_a_grp<4>(a, max_entries, s);
+        case 8: return go_a_grp<8>(a, max_entries, s);
+        case 16: return go_a_grp<16>(a, max_entries, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <class QD, int IPL, int P>
+static hipError_t go_b_grp(const MoeArgs &a, uint32_t max_entries, hipStream_t s) {
+    const uint32_t tr = b_tile_rows<QD>(P, 1);
+    const uint32_t lds = GRP_MAX * act_bytes(a.ffn);
+    if (lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute((const void *)k_moe_down_grp<QD, IPL, P>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL((k_moe_down_grp<QD, IPL, P>), dim3((a.hidden + tr - 1) / tr, max_entries), dim3(256), lds, s, a,
+                       tr);
+    return hipGetLastError();
+}
+
+// the same (P, IPL) choice as kernel B with one slot per row
+template <class QD>
+static hipError_t go_b_grp_any(const MoeArgs &a, uint32_t max_entries, hipStream_t s) {
+    const uint32_t nb = a.ffn / 256;
+    const uint32_t p = b_mult<QD>(nb, 1);
+    const uint32_t ipl = (nb + p - 1) / p;
+    switch (p * 8 + ipl) {
+        case 1 * 8 + 1: return go_b_grp<QD, 1, 1>(a, max_entries, s);
+        case 1 * 8 + 2: return go_b_grp<QD, 2, 1>(a, max_entries, s);
+        case 1 * 8 + 3: return go_b_grp<QD, 3, 1>(a, max_entries, s);
+        case 1 * 8 + 4: return go_b_grp<QD, 4, 1>(a, max_entries, s);
+        case 4 * 8 + 2: return go_b_grp<QD, 2, 4>(a, max_entries, s);
+        case 4 * 8 + 3: return go_b_grp<QD, 3, 4>(a, max_entries, s);
+        case 4 * 8 + 4: return go_b_grp<QD, 4, 4>(a, max_entries, s);
+        default: break;
+    }
+    if constexpr (QD::IPB * 16 <= 64) {
+        switch (p * 8 + ipl) {
+            case 16 * 8 + 2: return go_b_grp<QD, 2, 16>(a, max_entries, s);
+            case 16 * 8 + 3: return go_b_grp<QD, 3, 16>(a, max_entries, s);
+            case 16 * 8 + 4: return go_b_grp<QD, 4, 16>(a, max_entries, s);
+            default: break;
+        }
+    }
+    return go_b_grp<QD, 0, 1>(a, max_entries, s);
+}
+
+hipError_t launch_moe_groups_down(const MoeArgs &a, uint32_t max_entries, hipStream_t s) {
+    if (!a.bslot || !a.bcount || !a.border || !a.yp || max_entries == 0 || max_entries > 65535) return hipErrorInvalidValue;
+    return a.down_type == T_Q6_K ? go_b_grp_any<Q6K>(a, max_entries, s) : go_b_grp_any<Q4K>(a, max_entries, s);
 }
 
 hipError_t launch_moe_pairs_gu(const MoeArgs &a, uint32_t max_slots, hipStream_t s) {
