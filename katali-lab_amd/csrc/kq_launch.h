@@ -66,26 +66,20 @@ struct MoeArgs {
     float *route_w;
     float *dbg_gu;           // optional [n_slots][2][ffn] gate/up outputs
     int32_t *err;            // error word (bit 1: expert id out of range)
-    // Batch mode (several tokens): a workgroup's slot is a (token, rank) pair
-    // p = t * bS + r taken from the device list bslot[0 .. *bcount); x comes
-    // from the q8_1 rows xq + t * xq_stride, experts from ids[t * n_sel + r]
-    // (r == n_sel: the shared expert), h goes to hq8 row p, and kernel B
-    // writes the pair's unweighted down output to yp + p * hidden.
-    const int32_t *bslot;    // NULL: single-token layer
+    // Batched layer (several tokens): a pair p = t * bS + r is token t's rank
+    // r (r == n_sel: the shared expert). bslot holds *bcount {expert, first,
+    // count} entries whose pairs are border[first .. first + count); x comes
+    // from the q8_1 rows xq + t * xq_stride, h goes to hq8 row p and the
+    // pair's unweighted down output to yp + p * hidden.
+    const int32_t *bslot;
     const int32_t *bcount;
+    const int32_t *border;
     uint32_t bS;
     uint64_t xq_stride;
     float *yp;
-    // Grouped batch mode: bslot holds {expert, first, count} entries and the
-    // entry's pairs are border[first .. first + count).
-    const int32_t *border;
 };
 bool moe_shape_supported(uint32_t gate_type, uint32_t down_type, uint32_t hidden, uint32_t ffn);
 hipError_t launch_moe(const MoeArgs &a, hipStream_t s);
-// Batch mode of the two kernels over up to max_slots listed pairs (grids
-// sized for max_slots; workgroups past *bcount exit at once).
-hipError_t launch_moe_pairs_gu(const MoeArgs &a, uint32_t max_slots, hipStream_t s);
-hipError_t launch_moe_pairs_down(const MoeArgs &a, uint32_t max_slots, hipStream_t s);
 // Grouped batch mode over up to max_entries entries of <= 8 pairs of one
 // expert (the batched layer's GEMV path).
 hipError_t launch_moe_groups_gu(const MoeArgs &a, uint32_t max_entries, hipStream_t s);

@@ -375,19 +375,8 @@ __global__ void __launch_bounds__(A_THREADS) k_moe_gu(MoeArgs a) {
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t nblk = a.ffn / 32;
     const uint32_t slot = blockIdx.x / nblk, jb = blockIdx.x % nblk;
-    // batch mode: the slot is a listed (token, rank) pair
-    uint32_t hslot = slot;
     const uint8_t *xq = a.xq;
-    int32_t bexpert = -1;
-    if (a.bslot) {
-        if (slot >= (uint32_t)*a.bcount) return;   // whole workgroup, before any barrier
-        const uint32_t p = (uint32_t)a.bslot[slot], t = p / a.bS, r = p % a.bS;
-        hslot = p;
-        xq = a.xq + (uint64_t)t * a.xq_stride;
-        bexpert = (int)r < a.n_sel ? a.ids[t * a.n_sel + r] : -1;
-    }
-    const bool batch = a.bslot != nullptr;
-    const bool publisher = blockIdx.x == 0 && wave == 0 && !batch;
+    const bool publisher = blockIdx.x == 0 && wave == 0;
 
     // routing inputs, then x (fp32 or q8_1; lane task t covers values
     // 4t..4t+3); their latencies overlap. Loads are clamped, not guarded: no
@@ -395,7 +384,7 @@ __global__ void __launch_bounds__(A_THREADS) k_moe_gu(MoeArgs a) {
     float lv[C];
     int32_t eid = -1;
     float ew = 0.0f;
-    if (a.n_sel > 0 && !batch) {
+    if (a.n_sel > 0) {
         if (a.logits) {
             load_keys<C>(a, lv);
         } else {
@@ -421,7 +410,7 @@ __global__ void __launch_bounds__(A_THREADS) k_moe_gu(MoeArgs a) {
         }
     }
     float route_l = 0.0f;
-    if (a.logits && a.n_sel > 0 && !batch) {
+    if (a.logits && a.n_sel > 0) {
         const WaveRoute r = wave_topk<C>(a, lv);
         eid = r.id;
         route_l = r.logit;
@@ -433,8 +422,8 @@ __global__ void __launch_bounds__(A_THREADS) k_moe_gu(MoeArgs a) {
 
     const uint64_t rb = NB * 144;
     const uint8_t *gb, *ub;
-    if (batch ? bexpert >= 0 : (int)slot < a.n_sel) {
-        int32_t id = batch ? bexpert : __builtin_amdgcn_readlane(eid, (int)slot);
+    if ((int)slot < a.n_sel) {
+        int32_t id = __builtin_amdgcn_readlane(eid, (int)slot);
         if ((uint32_t)id >= a.n_expert) id = 0;   // bad explicit id: reported by route_publish
         const uint64_t e = (uint64_t)id;
         gb = a.gate + e * a.ffn * rb;
@@ -568,11 +557,11 @@ __global__ void __launch_bounds__(A_THREADS) k_moe_gu(MoeArgs a) {
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
         const int qv = (int)roundf(h * id);
         const int total = sum32(qv);
-        uint8_t *blk = a.hq8 + ((uint64_t)hslot * nblk + jb) * 36;
+        uint8_t *blk = a.hq8 + ((uint64_t)slot * nblk + jb) * 36;
         if (lane < 32) blk[4 + lane] = (uint8_t)(qv & 255);
         if (lane == 0) *(uint32_t *)blk = f2h_rne(d) | (f2h_rne((float)total * d) << 16);
     }
-    if (a.dbg_gu && !batch && tid < 64) {
+    if (a.dbg_gu && tid < 64) {
         float *d = a.dbg_gu + (uint64_t)slot * 2 * a.ffn + (tid < 32 ? 0 : a.ffn) + 32 * jb + (tid & 31);
         *d = gu[tid];
     }
@@ -639,30 +628,12 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a, uint32_t tr, uint32
     extern __shared__ __align__(16) uint8_t lds[];
     const LdsB L = lds_b(a.ffn, n_slots, tr);
     const uint32_t tid = threadIdx.x, lane = tid & 63;
-    // batch mode: one listed pair per blockIdx.y, weight 1, output to the
-    // pair's row of yp
-    const bool batch = a.bslot != nullptr;
-    const uint8_t *hsrc = a.hq8;
-    float *yout = a.y;
-    int32_t bexpert = -1;
-    if (batch) {
-        if (blockIdx.y >= (uint32_t)*a.bcount) return;   // whole workgroup, before any barrier
-        const uint32_t p = (uint32_t)a.bslot[blockIdx.y], t = p / a.bS, r = p % a.bS;
-        hsrc = a.hq8 + (uint64_t)p * (a.ffn / 32) * 36;
-        yout = a.yp + (uint64_t)p * a.hidden;
-        bexpert = (int)r < a.n_sel ? a.ids[t * a.n_sel + r] : -1;
-        if (bexpert >= 0 && (uint32_t)bexpert >= a.n_expert) bexpert = 0;   // bad id: reported by the grouping
-    }
     // routing (lane r holds slot r), then the h loads
-    int32_t rid = 0;
-    float rw = batch && lane == 0 ? 1.0f : 0.0f;
-    if (!batch) {
-        rid = a.route_ids[min(lane, (uint32_t)MAX_SLOTS - 1)];
-        rw = a.route_w[min(lane, (uint32_t)MAX_SLOTS - 1)];
-    }
+    const int32_t rid = a.route_ids[min(lane, (uint32_t)MAX_SLOTS - 1)];
+    const float rw = a.route_w[min(lane, (uint32_t)MAX_SLOTS - 1)];
     const uint32_t ntask = n_slots * (a.ffn / 32) * 2;
     HLoad hv;
-    load_h(hsrc, ntask, 0, hv);
+    load_h(a.hq8, ntask, 0, hv);
 
     constexpr uint32_t S = QD::IPB * P;
     const uint32_t ls = tid / S, s = tid % S;
@@ -675,8 +646,8 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a, uint32_t tr, uint32
     const bool active = ls < npairs;
     const uint32_t lc = min(ls, npairs - 1);   // idle lane-slots load a real pair and drop it
     const uint32_t sl = lc % n_slots, r = lc / n_slots;
-    const int32_t sid = batch ? bexpert : __shfl(rid, (int)sl, WAVE);
-    const bool routed = batch ? bexpert >= 0 : (int)sl < a.n_sel;
+    const int32_t sid = __shfl(rid, (int)sl, WAVE);
+    const bool routed = (int)sl < a.n_sel;
     const uint8_t *db = routed ? a.down + (uint64_t)sid * a.hidden * rbd : a.down_sh;
     const uint8_t *rp = db + (uint64_t)(row0 + r) * rbd;
     typename QD::Raw raw[IPL > 0 ? IPL : 1];
@@ -687,7 +658,7 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a, uint32_t tr, uint32
     }
     stage_h(lds + L.hacts, a.ffn, ntask, 0, hv);
     for (uint32_t first = HT * 256; first < ntask; first += HT * 256) {
-        load_h(hsrc, ntask, first, hv);   // only when n_slots * ffn / 16 > 512
+        load_h(a.hq8, ntask, first, hv);   // only when n_slots * ffn / 16 > 512
         stage_h(lds + L.hacts, a.ffn, ntask, first, hv);
     }
     __syncthreads();
@@ -718,7 +689,7 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a, uint32_t tr, uint32
             const float v = res[tid * n_slots + k];
             y = k < (int)n_slots ? fmaf(w, v, y) : y;
         }
-        yout[row0 + tid] = y;
+        a.y[row0 + tid] = y;
     }
 }
 
@@ -981,10 +952,10 @@ static uint32_t b_tile_rows(uint32_t P, uint32_t n_slots) {
 }
 
 template <class QD, int IPL, int P>
-static hipError_t go_b(const MoeArgs &a, uint32_t n_slots, uint32_t grid_y, hipStream_t s) {
+static hipError_t go_b(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
     const uint32_t tr = b_tile_rows<QD>(P, n_slots);
     const LdsB L = lds_b(a.ffn, n_slots, tr);
-    hipLaunchKernelGGL((k_moe_down<QD, IPL, P>), dim3((a.hidden + tr - 1) / tr, grid_y), dim3(256), L.total, s, a, tr,
+    hipLaunchKernelGGL((k_moe_down<QD, IPL, P>), dim3((a.hidden + tr - 1) / tr), dim3(256), L.total, s, a, tr,
                        n_slots);
     return hipGetLastError();
 }
@@ -1003,29 +974,29 @@ static uint32_t b_mult(uint32_t nb, uint32_t n_slots) {
 }
 
 template <class QD>
-static hipError_t go_b_any(const MoeArgs &a, uint32_t n_slots, uint32_t grid_y, hipStream_t s) {
+static hipError_t go_b_any(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
     const uint32_t nb = a.ffn / 256;
     const uint32_t p = b_mult<QD>(nb, n_slots);
     const uint32_t ipl = (nb + p - 1) / p;
     switch (p * 8 + ipl) {
-        case 1 * 8 + 1: return go_b<QD, 1, 1>(a, n_slots, grid_y, s);
-        case 1 * 8 + 2: return go_b<QD, 2, 1>(a, n_slots, grid_y, s);
-        case 1 * 8 + 3: return go_b<QD, 3, 1>(a, n_slots, grid_y, s);
-        case 1 * 8 + 4: return go_b<QD, 4, 1>(a, n_slots, grid_y, s);
-        case 4 * 8 + 2: return go_b<QD, 2, 4>(a, n_slots, grid_y, s);
-        case 4 * 8 + 3: return go_b<QD, 3, 4>(a, n_slots, grid_y, s);
-        case 4 * 8 + 4: return go_b<QD, 4, 4>(a, n_slots, grid_y, s);
+        case 1 * 8 + 1: return go_b<QD, 1, 1>(a, n_slots, s);
+        case 1 * 8 + 2: return go_b<QD, 2, 1>(a, n_slots, s);
+        case 1 * 8 + 3: return go_b<QD, 3, 1>(a, n_slots, s);
+        case 1 * 8 + 4: return go_b<QD, 4, 1>(a, n_slots, s);
+        case 4 * 8 + 2: return go_b<QD, 2, 4>(a, n_slots, s);
+        case 4 * 8 + 3: return go_b<QD, 3, 4>(a, n_slots, s);
+        case 4 * 8 + 4: return go_b<QD, 4, 4>(a, n_slots, s);
         default: break;
     }
     if constexpr (QD::IPB * 16 <= 64) {
         switch (p * 8 + ipl) {
-            case 16 * 8 + 2: return go_b<QD, 2, 16>(a, n_slots, grid_y, s);
-            case 16 * 8 + 3: return go_b<QD, 3, 16>(a, n_slots, grid_y, s);
-            case 16 * 8 + 4: return go_b<QD, 4, 16>(a, n_slots, grid_y, s);
+            case 16 * 8 + 2: return go_b<QD, 2, 16>(a, n_slots, s);
+            case 16 * 8 + 3: return go_b<QD, 3, 16>(a, n_slots, s);
+            case 16 * 8 + 4: return go_b<QD, 4, 16>(a, n_slots, s);
             default: break;
         }
     }
-    return go_b<QD, 0, 1>(a, n_slots, grid_y, s);
+    return go_b<QD, 0, 1>(a, n_slots, s);
 }
 
 bool moe_shape_supported(uint32_t gate_type, uint32_t down_type, uint32_t hidden, uint32_t ffn) {
@@ -1042,7 +1013,7 @@ hipError_t launch_moe(const MoeArgs &a, hipStream_t s) {
     const uint32_t n_slots = (uint32_t)a.n_sel + (a.has_shared ? 1u : 0u);
     const hipError_t e = go_a_any(a, n_slots, s);
     if (e != hipSuccess) return e;
-    return a.down_type == T_Q6_K ? go_b_any<Q6K>(a, n_slots, 1, s) : go_b_any<Q4K>(a, n_slots, 1, s);
+    return a.down_type == T_Q6_K ? go_b_any<Q6K>(a, n_slots, s) : go_b_any<Q4K>(a, n_slots, s);
 }
 
 static hipError_t go_a_any(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
@@ -1124,16 +1095,6 @@ static hipError_t go_b_grp_any(const MoeArgs &a, uint32_t max_entries, hipStream
 hipError_t launch_moe_groups_down(const MoeArgs &a, uint32_t max_entries, hipStream_t s) {
     if (!a.bslot || !a.bcount || !a.border || !a.yp || max_entries == 0 || max_entries > 65535) return hipErrorInvalidValue;
     return a.down_type == T_Q6_K ? go_b_grp_any<Q6K>(a, max_entries, s) : go_b_grp_any<Q4K>(a, max_entries, s);
-}
-
-hipError_t launch_moe_pairs_gu(const MoeArgs &a, uint32_t max_slots, hipStream_t s) {
-    if (!a.bslot || !a.bcount || max_slots == 0) return hipErrorInvalidValue;
-    return go_a_any(a, max_slots, s);
-}
-
-hipError_t launch_moe_pairs_down(const MoeArgs &a, uint32_t max_slots, hipStream_t s) {
-    if (!a.bslot || !a.bcount || !a.yp || max_slots == 0 || max_slots > 65535) return hipErrorInvalidValue;
-    return a.down_type == T_Q6_K ? go_b_any<Q6K>(a, 1, max_slots, s) : go_b_any<Q4K>(a, 1, max_slots, s);
 }
 
 }  // namespace kq
