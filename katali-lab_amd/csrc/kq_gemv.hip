@@ -49,18 +49,100 @@ hipError_t launch_quantize_q8_1(const float *x, uint64_t n, uint8_t *out, hipStr
 // ---------------------------------------------------------------------------
 // GEMV
 // ---------------------------------------------------------------------------
+// The activation of a GEMV workgroup, staged in two halves around the weight
+// loads: load() issues the first XPRE tasks per thread into registers (the
+// whole activation for cols <= 4096), store() writes them to LDS after the
+// weight loads are out and stages any remaining tasks directly. A task is 4
+// values: fp32 copied (MODE 0), q8_1 bytes copied (MODE 1), or fp32
+// quantized to q8_1 with 8 lanes per block (MODE 2).
+constexpr int XPRE = 4;
+template <int MODE>
+struct XStage {
+    float4 v[XPRE];
+    uint32_t q[XPRE], d[XPRE];
+    __device__ static uint32_t tasks(uint32_t cols) { return MODE == 0 ? cols / 4 : cols / 32 * 8; }
+    __device__ __forceinline__ void load(const float *xf, const uint8_t *xq, uint32_t cols) {
+        const uint32_t n = tasks(cols);
+#pragma unroll
+        for (int i = 0; i < XPRE; i++) {
+            const uint32_t t = min(threadIdx.x + 256 * i, n - 1);   // clamped, not skipped
+            if constexpr (MODE == 1) {
+                const uint8_t *b = xq + (t >> 3) * 36;
+                q[i] = *(const uint32_t *)(b + 4 + 4 * (t & 7));
+                d[i] = ld_u16(b);
+                v[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            } else {
+                v[i] = *(const float4 *)(xf + 4 * t);
+                q[i] = d[i] = 0;
+            }
+        }
+    }
+    __device__ __forceinline__ void put(uint32_t t, float4 x4, uint32_t qq, uint32_t dd, const Act &a,
+                                        const ActF &af) const {
+        if constexpr (MODE == 0) {
+            *(float4 *)(af.x + 4 * t) = x4;
+        } else {
+            const uint32_t blk = t >> 3, part = t & 7;
+            uint32_t qv;
+            int lo, hi;
+            float dec;
+            if constexpr (MODE == 1) {
+                qv = qq;
+                q8_part_sums(qv, lo, hi);
+                dec = h2f(dd);
+            } else {
+                uint32_t d16, s16;
+                qv = quant_q8_1_part(x4, d16, s16, lo, hi, dec);
+            }
+            *(uint32_t *)(a.qs + 32 * blk + 4 * part) = qv;
+            if (part == 0) {
+                a.d8[blk] = dec;
+                a.qs16[2 * blk] = lo;
+                a.qs16[2 * blk + 1] = hi;
+            }
+        }
+    }
+    // Tasks past n were loaded clamped and are dropped here (whole 8-lane
+    // groups: n % 8 == 0); the barriers around the weight loads keep the
+    // compiler from sinking the preloads into these branches.
+    __device__ __forceinline__ void store(const float *xf, const uint8_t *xq, uint32_t cols, const Act &a,
+                                          const ActF &af) const {
+        const uint32_t n = tasks(cols);
+#pragma unroll
+        for (int i = 0; i < XPRE; i++) {
+            const uint32_t t = threadIdx.x + 256 * i;
+            if (t < n) put(t, v[i], q[i], d[i], a, af);
+        }
+        for (uint32_t t = threadIdx.x + 256 * XPRE; t < n; t += 256) {   // whole 8-lane groups (n % 8 == 0)
+            float4 x4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            uint32_t qq = 0, dd = 0;
+            if constexpr (MODE == 1) {
+                const uint8_t *b = xq + (t >> 3) * 36;
+                qq = *(const uint32_t *)(b + 4 + 4 * (t & 7));
+                dd = ld_u16(b);
+            } else {
+                x4 = *(const float4 *)(xf + 4 * t);
+            }
+            put(t, x4, qq, dd, a, af);
+        }
+        if constexpr (MODE == 0) {   // half-block sums of the fp32 activation
+            __syncthreads();
+            for (uint32_t t = threadIdx.x; t < cols / 16; t += 256) {
+                float sum = 0.0f;
+                for (int i = 0; i < 16; i++) sum += af.x[16 * t + i];
+                af.xs16[t] = sum;
+            }
+        }
+    }
+};
+
 template <class QT, int IPL_T, int RPS, int MODE>
 __global__ void __launch_bounds__(256)
     k_gemv(const uint8_t *__restrict__ w, uint32_t rows, uint32_t cols, uint64_t rb, uint32_t log2s,
-           const float *__restrict__ xf, const uint8_t *__restrict__ xq, float *__restrict__ y) {
+           const float *xf, const uint8_t *xq, float *__restrict__ y) {
     extern __shared__ __align__(16) uint8_t lds[];
     const Act a = act_carve(lds, cols);
     const ActF af = actf_carve(lds, cols);
-    if constexpr (MODE == 0) actf_stage(xf, cols, af);
-    else if constexpr (MODE == 1) act_stage_from_q8(xq, cols, a);
-    else act_stage_from_f32(xf, cols, a);
-    __syncthreads();
-
     const uint32_t S = 1u << log2s;
     const uint32_t slots = WAVE >> log2s;
     const uint32_t lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
@@ -68,49 +150,67 @@ __global__ void __launch_bounds__(256)
     const uint32_t items = cols / 256 * QT::IPB;
     const int IPL = IPL_T > 0 ? IPL_T : (int)(items >> log2s);
     const uint32_t rows_iter = 4 * slots * RPS;
+    const uint32_t base0 = blockIdx.x * rows_iter;
+    auto row_of = [&](uint32_t base, int r) { return base + r * (4 * slots) + wave * slots + slot; };
 
-    for (uint32_t base = blockIdx.x * rows_iter; base < rows; base += gridDim.x * rows_iter) {
-        float acc[RPS];
+    // Unrolled items: the activation loads, then the first row group's
+    // weight loads, go out before the activation is staged, so the two
+    // latencies overlap. Rows are clamped,
+    // not skipped (a load under a branch makes the compiler wait for all).
+    typename QT::Raw raw[RPS][IPL_T > 0 ? IPL_T : 1];
+    auto load_rows = [&](uint32_t base) {
         if constexpr (IPL_T > 0) {
-            typename QT::Raw raw[RPS][IPL_T];
 #pragma unroll
             for (int r = 0; r < RPS; r++) {
-                const uint32_t row = base + r * (4 * slots) + wave * slots + slot;
-                if (row < rows) {
-                    const uint8_t *rp = w + (uint64_t)row * rb;
+                const uint8_t *rp = w + (uint64_t)min(row_of(base, r), rows - 1) * rb;
 #pragma unroll
-                    for (int i = 0; i < IPL_T; i++) {
-                        const uint32_t item = s + S * i;
-                        raw[r][i] = QT::load(rp + (item / QT::IPB) * QT::BB, item % QT::IPB);
-                    }
+                for (int i = 0; i < IPL_T; i++) {
+                    const uint32_t item = s + S * i;
+                    raw[r][i] = QT::load(rp + (item / QT::IPB) * QT::BB, item % QT::IPB);
                 }
             }
+        }
+    };
+    XStage<MODE> xs;
+    xs.load(xf, xq, cols);   // issued first: waiting for x then waits for nothing else
+    // Neither the compiler nor the scheduler may move work across these two
+    // points (x is deliberately not __restrict__, so its loads are not
+    // treated as invariant and re-issued at their use).
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    load_rows(base0);   // base0 < rows: the grid never exceeds the row groups
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);   // every weight load is out before x is staged
+    xs.store(xf, xq, cols, a, af);
+    __syncthreads();
+
+    for (uint32_t base = base0; base < rows; base += gridDim.x * rows_iter) {
+        float acc[RPS];
+        if constexpr (IPL_T > 0) {
+            if (base != base0) load_rows(base);
 #pragma unroll
             for (int r = 0; r < RPS; r++) {
-                const uint32_t row = base + r * (4 * slots) + wave * slots + slot;
                 float v = 0.0f;
-                if (row < rows) {
 #pragma unroll
-                    for (int i = 0; i < IPL_T; i++) {
-                        const uint32_t item = s + S * i;
-                        if constexpr (MODE == 0) v += QT::dot_f32(raw[r][i], item % QT::IPB, af, item / QT::IPB);
-                        else v += QT::dot_q8(raw[r][i], item % QT::IPB, a, item / QT::IPB);
-                    }
+                for (int i = 0; i < IPL_T; i++) {
+                    const uint32_t item = s + S * i;
+                    if constexpr (MODE == 0) v += QT::dot_f32(raw[r][i], item % QT::IPB, af, item / QT::IPB);
+                    else v += QT::dot_q8(raw[r][i], item % QT::IPB, a, item / QT::IPB);
                 }
                 acc[r] = v;
             }
         } else {
 #pragma unroll
             for (int r = 0; r < RPS; r++) {
-                const uint32_t row = base + r * (4 * slots) + wave * slots + slot;
+                const uint32_t row = row_of(base, r);
                 float v = 0.0f;
                 if (row < rows) {
                     const uint8_t *rp = w + (uint64_t)row * rb;
                     for (int i = 0; i < IPL; i++) {
                         const uint32_t item = s + S * i;
-                        const typename QT::Raw raw = QT::load(rp + (item / QT::IPB) * QT::BB, item % QT::IPB);
-                        if constexpr (MODE == 0) v += QT::dot_f32(raw, item % QT::IPB, af, item / QT::IPB);
-                        else v += QT::dot_q8(raw, item % QT::IPB, a, item / QT::IPB);
+                        const typename QT::Raw rw = QT::load(rp + (item / QT::IPB) * QT::BB, item % QT::IPB);
+                        if constexpr (MODE == 0) v += QT::dot_f32(rw, item % QT::IPB, af, item / QT::IPB);
+                        else v += QT::dot_q8(rw, item % QT::IPB, a, item / QT::IPB);
                     }
                 }
                 acc[r] = v;
@@ -119,7 +219,7 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
         for (int r = 0; r < RPS; r++) {
             const float v = wave_sum_xor(acc[r], (int)S);
-            const uint32_t row = base + r * (4 * slots) + wave * slots + slot;
+            const uint32_t row = row_of(base, r);
             if (s == 0 && row < rows) y[row] = v;
         }
     }
