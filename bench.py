@@ -728,7 +728,7 @@ def main():
                         f"grouped GEMM; {L} layers of distinct weights per pass; headline point n_sel 8, 64 tokens",
             "layers": L, "hidden": hidden, "ffn": ffn, "n_expert": n_expert, "parallelism": "single GPU",
         }
-        kernel = "batched MoE layer (grouping, GEMV pairs, MFMA grouped GEMM, combine)"
+        kernel = "batched MoE layer (grouping, grouped v_dot4 GEMV for experts < 16 tokens, int8 MFMA grouped GEMM, combine)"
         extra = {"tok_s": head["tok_s"], "mfma_frac_of_int8_peak": round(head["tops"] / 5000.0, 4),
                  "sweep": res["points"]}
     elif args.workload in DENSE_WORKLOADS:

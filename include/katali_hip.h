@@ -156,8 +156,10 @@ int katali_hip_moe_layer_debug(const KataliHipMoe *moe, const KataliHipMoeRoute 
  * V/src/gguf_dtype.c:1059-1105, each weight row decoded once for B tokens):
  * T tokens with their own experts. Pairs are grouped by expert on the device;
  * an expert with at least mfma_min_tokens pairs runs as an int8 MFMA grouped
- * GEMM, the others through the v_dot4 GEMV kernels; results are identical in
- * definition (q8_1 x and h, rank-order weighted sum). */
+ * GEMM, the others through the grouped v_dot4 GEMV kernels (one read of the
+ * expert's weights for up to 8 of its tokens); results are identical in
+ * definition (q8_1 x and h, rank-order weighted sum), and a one-token batch
+ * is bit-identical to katali_hip_moe_layer with the same experts. */
 typedef struct KataliHipMoeBatch {
     uint32_t struct_size;                  /* sizeof(KataliHipMoeBatch) */
     uint32_t n_tokens;                     /* T, 1..64 */

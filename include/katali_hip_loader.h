@@ -58,6 +58,9 @@ int katali_gpu_selftest(char *report, size_t cap);
 /* Greedy token on device (gguf_sampler.c:62-66 rule), for a decode loop that
  * keeps logits resident. */
 int katali_gpu_argmax(const float *logits_dev, uint64_t n, int32_t *out_dev);
+/* The MoE layer over a batch of up to 64 tokens (batched prefill). */
+int katali_gpu_moe_batch(const KataliHipMoe *moe, const KataliHipMoeBatch *batch, const float *x_dev,
+                         float *y_dev);
 /* The library's last error for this thread ("" when none / not loaded). */
 const char *katali_gpu_last_error(void);
 
@@ -97,6 +100,7 @@ typedef struct KataliHipApi {
     int (*synth_normal)(float *, uint64_t, uint64_t, float);
     int (*copy)(void *, const void *, size_t);
     int (*argmax)(const float *, uint64_t, int32_t *);
+    int (*moe_batch)(const KataliHipMoe *, const KataliHipMoeBatch *, const float *, float *);
 } KataliHipApi;
 
 /* NULL when the library could not be loaded or an entry point is missing. */

@@ -106,6 +106,7 @@ static int load(void) {
     LOAD(synth_normal, "katali_hip_synth_normal");
     LOAD(copy, "katali_hip_copy");
     LOAD(argmax, "katali_hip_argmax");
+    LOAD(moe_batch, "katali_hip_moe_batch");
     if (g_api.abi_version() != KATALI_HIP_ABI_VERSION) {
         snprintf(g_status, sizeof g_status, "%s: ABI version %d, loader expects %d", tried, g_api.abi_version(),
                  KATALI_HIP_ABI_VERSION);
@@ -172,3 +173,6 @@ int katali_gpu_graph_launch(void *g) { FORWARD(g_api.graph_launch(g)); }
 int katali_gpu_graph_destroy(void *g) { FORWARD(g_api.graph_destroy(g)); }
 int katali_gpu_selftest(char *report, size_t cap) { FORWARD(g_api.selftest(report, cap)); }
 int katali_gpu_argmax(const float *logits, uint64_t n, int32_t *out) { FORWARD(g_api.argmax(logits, n, out)); }
+int katali_gpu_moe_batch(const KataliHipMoe *moe, const KataliHipMoeBatch *batch, const float *x, float *y) {
+    FORWARD(g_api.moe_batch(moe, batch, x, y));
+}

@@ -26,12 +26,19 @@ from collections import defaultdict
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 COPY_MIB = 256
+# kernels summed per workload unit; the first is launched once per unit
 KERNELS = {
     "moe48": ("k_moe_gu", "k_moe_down"),
     "moe40cold": ("k_moe_gu", "k_moe_down"),
     "gemv6144": ("k_gemv",),
+    "qwen8b": ("k_moe_down", "k_moe_gu", "k_gemv"),
+    "moebatch": ("k_mb_group", "k_quantize_q8_1", "k_moe_gu_grp", "k_mb_gu_mfma", "k_moe_down_grp", "k_mb_down_mfma",
+                 "k_mb_combine"),
 }
-UNITS_PER_STEP = {"moe48": 48, "moe40cold": 40, "gemv6144": 144}
+UNIT_NAME = {"moe48": "MoE layer", "moe40cold": "MoE layer", "gemv6144": "GEMV", "qwen8b": "dense layer",
+             "moebatch": "batched MoE layer (n_sel 8, 64 tokens)"}
+EXTRA_ARGS = {"moebatch": ["--batch-points", "8x64"]}
+PROFILE_NAME = {"moebatch": "batched_moe_moebatch_8x64", "qwen8b": "k_gemv_k_moe_gu_k_moe_down_qwen8b"}
 
 
 def run(cmd, log):
@@ -86,9 +93,14 @@ def counter_means(outdir, counter):
     return {k: (len(v), sum(v) / len(v)) for k, v in acc.items()}
 
 
+def kernel_of(name):
+    """The kernel's base name (`void kq::k_moe_gu<8, 2>(...)` -> `k_moe_gu`)."""
+    base = name.split("(")[0].split("<")[0].strip()
+    return base.split("::")[-1].split(" ")[-1]
+
+
 def pick(d, sub):
-    hits = [(k, v) for k, v in d.items() if sub in k]
-    return hits
+    return [(k, v) for k, v in d.items() if kernel_of(k) == sub]
 
 
 def main():
@@ -100,10 +112,11 @@ def main():
     ap.add_argument("--summarize-only", action="store_true", help="parse an existing --out tree, run nothing")
     args = ap.parse_args()
     wl = args.workload
-    out = os.path.join(args.out, wl)
+    out = os.path.join(os.path.abspath(args.out), wl)   # rocprofv3 runs from /tmp
     os.makedirs(out, exist_ok=True)
     bench = [sys.executable, os.path.join(REPO, "bench.py"), "--workload", wl, "--steps", str(args.steps),
-             "--warmup", str(args.warmup), "--no-cpu-baseline", "--calibrate-copy", str(COPY_MIB)]
+             "--warmup", str(args.warmup), "--no-cpu-baseline", "--calibrate-copy", str(COPY_MIB)] + \
+        EXTRA_ARGS.get(wl, [])
     cmds = {
         "trace": ["rocprofv3", "--kernel-trace", "--stats", "--output-format", "csv", "-d", os.path.join(out, "trace"),
                   "-o", "run", "--"] + bench,
@@ -127,20 +140,25 @@ def main():
         sys.exit("calibration copy kernel missing from the counter runs")
     f_scale = copy_bytes / cf[0][1][1]     # bytes per counter unit
     w_scale = copy_bytes / cw[0][1][1]
+    # per workload unit: every kernel's calls relative to the first kernel's
+    # (one launch per unit), times its mean duration and traffic per dispatch
+    ref = pick(stats, KERNELS[wl][0])
+    if not ref:
+        sys.exit(f"{KERNELS[wl][0]} missing from the trace")
+    units = sum(c for _, (c, _) in ref)
     unit_fetch = unit_write = unit_time = 0.0
     table = []
     for sub in KERNELS[wl]:
         for name, (calls, avg) in pick(stats, sub):
-            fk = pick(fetch, sub)
-            wk = pick(write, sub)
-            fb = fk[0][1][1] * f_scale if fk else float("nan")
-            wb = wk[0][1][1] * w_scale if wk else float("nan")
+            fb = fetch[name][1] * f_scale if name in fetch else float("nan")
+            wb = write[name][1] * w_scale if name in write else float("nan")
+            per = calls / units
             table.append((name, calls, avg / 1e3, fb, wb))
-            unit_fetch += fb
-            unit_write += wb
-            unit_time += avg / 1e3
+            unit_fetch += fb * per
+            unit_write += wb * per
+            unit_time += avg / 1e3 * per
     traffic = unit_fetch + unit_write
-    md = os.path.join(REPO, "profiles", f"{'_'.join(KERNELS[wl])}_{wl}.md")
+    md = os.path.join(REPO, "profiles", f"{PROFILE_NAME.get(wl, '_'.join(KERNELS[wl]) + '_' + wl)}.md")
     os.makedirs(os.path.dirname(md), exist_ok=True)
     with open(md, "w") as f:
         f.write(f"# rocprofv3 summary: {wl}\n\n")
@@ -156,13 +174,14 @@ def main():
         f.write("| kernel | calls | avg us | HBM fetch B/dispatch | HBM write B/dispatch |\n|---|---|---|---|---|\n")
         for name, calls, us, fb, wb in table:
             f.write(f"| {name} | {calls} | {us:.2f} | {fb:,.0f} | {wb:,.0f} |\n")
-        f.write(f"\nPer workload unit ({'layer' if 'moe' in wl else 'GEMV'}): kernel time {unit_time:.2f} us, "
-                f"HBM traffic {traffic:,.0f} B (fetch {unit_fetch:,.0f} + write {unit_write:,.0f}).\n\n")
+        f.write(f"\nPer workload unit ({UNIT_NAME[wl]}; {units} units in the trace run, each kernel weighted by "
+                f"its calls per unit): kernel time {unit_time:.2f} us, HBM traffic {traffic:,.0f} B "
+                f"(fetch {unit_fetch:,.0f} + write {unit_write:,.0f}).\n\n")
         f.write("All kernels in the trace run (calls, avg us):\n\n")
         for name, (calls, avg) in sorted(stats.items(), key=lambda kv: -kv[1][0] * kv[1][1]):
             f.write(f"- {name[:110]}: {calls}, {avg / 1e3:.2f}\n")
     with open(os.path.join(REPO, "profiles", f"traffic_{wl}.txt"), "w") as f:
-        f.write(f"# HBM bytes per {'MoE layer' if 'moe' in wl else 'GEMV'} from {os.path.basename(md)}\n")
+        f.write(f"# HBM bytes per {UNIT_NAME[wl]} from {os.path.basename(md)}\n")
         f.write(f"traffic_bytes_per_unit: {traffic:.0f}\n")
     print(open(md).read())
 

@@ -80,3 +80,19 @@ int main(void) {
 @pytest.mark.parametrize("t,ok", [(12, 1), (14, 1), (0, 0), (2, 0), (13, 0)])
 def test_supports_type(t, ok):
     assert K.KataliHip().lib.katali_hip_supports_type(t) == ok
+
+
+def test_loader_exports_its_headers():
+    """libkatali_hip_loader.so (the engine-side loader and dense shim) exports
+    every function include/katali_hip_loader.h and include/katali_dense_hip.h
+    declare."""
+    so = os.path.join(REPO, "katali-lab_amd", "libkatali_hip_loader.so")
+    assert os.path.exists(so), "run python katali-lab_amd/build.py"
+    names = set()
+    for h, prefix in (("katali_hip_loader.h", "katali_gpu_"), ("katali_dense_hip.h", "katali_dense_hip_")):
+        src = re.sub(r"/\*.*?\*/", "", open(os.path.join(REPO, "include", h)).read(), flags=re.S)
+        names |= set(re.findall(r"\b(" + prefix + r"\w+)\s*\(", src))
+    assert "katali_gpu_moe_batch" in names and "katali_dense_hip_matvec" in names
+    out = subprocess.run(["nm", "-D", "--defined-only", so], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\bT (katali_(?:gpu|dense_hip)_\w+)", out))
+    assert names <= exported, names - exported
