@@ -58,6 +58,18 @@ __device__ __forceinline__ uint2 ld8(const uint8_t *p) {
     __builtin_memcpy(&v, p, 8);
     return v;
 }
+// Read kernel arguments into SGPRs at this point. The compiler otherwise
+// loads each argument from the kernarg segment at its first use, which for a
+// weight base pointer is a scalar-memory round trip between a dependent load
+// (the routing) and the weight stream it starts.
+template <class T>
+__device__ __forceinline__ void pin_arg(T v) {
+    asm volatile("" ::"s"(v));
+}
+template <class... T>
+__device__ __forceinline__ void pin_args(T... v) {
+    (pin_arg(v), ...);
+}
 __device__ __forceinline__ uint32_t ld4(const uint8_t *p) {
     uint32_t v;
     __builtin_memcpy(&v, p, 4);

@@ -377,6 +377,7 @@ __global__ void __launch_bounds__(A_THREADS) k_moe_gu(MoeArgs a) {
     const uint32_t slot = blockIdx.x / nblk, jb = blockIdx.x % nblk;
     const uint8_t *xq = a.xq;
     const bool publisher = blockIdx.x == 0 && wave == 0;
+    pin_args(a.gate, a.up, a.gate_sh, a.up_sh, a.hq8);
 
     // routing inputs, then x (fp32 or q8_1; lane task t covers values
     // 4t..4t+3); their latencies overlap. Loads are clamped, not guarded: no
@@ -447,6 +448,40 @@ __global__ void __launch_bounds__(A_THREADS) k_moe_gu(MoeArgs a) {
         return row_ptr(RW * wave + r) + (it / 8) * 144 + 16 + 16 * (it % 8);
     };
 
+    // x -> q8_1 in LDS (the loads are already in): while the weights stream
+    // in when they had to wait for the routing; before they are issued when
+    // nothing routes (the shared expert alone, a dense FFN), so that this
+    // barrier never waits on a sibling wave still issuing into a full memory
+    // pipeline (a dense FFN's 384 workgroups request 58 MB at once)
+    const Act xa = act_carve(lds + L.xact, a.hidden);
+    auto stage_x = [&]() {
+#pragma unroll
+        for (int i = 0; i < XPT; i++) {
+            const uint32_t t = tid + NT * i, blk = t >> 3, part = t & 7;
+            if (t >= XTASKS) break;   // whole 8-lane groups leave together
+            uint32_t qv;
+            int lo, hi;
+            float dd;
+            if (xq) {
+                qv = xqv[i];
+                q8_part_sums(qv, lo, hi);
+                dd = h2f(xdv[i]);
+            } else {
+                uint32_t d16, s16;
+                qv = quant_q8_1_part(xv[i], d16, s16, lo, hi, dd);
+            }
+            *(uint32_t *)(xa.qs + 32 * blk + 4 * part) = qv;
+            if (part == 0) {
+                xa.d8[blk] = dd;
+                xa.qs16[2 * blk] = lo;
+                xa.qs16[2 * blk + 1] = hi;
+            }
+        }
+        __syncthreads();
+    };
+    const bool x_first = a.n_sel == 0;
+    if (x_first) stage_x();
+
     // every weight load of the wave: its block headers first, then chunks
     uint4 hv[HPL];
 #pragma unroll
@@ -462,32 +497,7 @@ __global__ void __launch_bounds__(A_THREADS) k_moe_gu(MoeArgs a) {
         if (a.logits && a.n_sel > 0) ew = route_weight(route_l, a.n_sel);
         route_publish(a, eid, ew);
     }
-
-    // quantize x into LDS while the weights stream in
-    const Act xa = act_carve(lds + L.xact, a.hidden);
-#pragma unroll
-    for (int i = 0; i < XPT; i++) {
-        const uint32_t t = tid + NT * i, blk = t >> 3, part = t & 7;
-        if (t >= XTASKS) break;   // whole 8-lane groups leave together
-        uint32_t qv;
-        int lo, hi;
-        float dd;
-        if (xq) {
-            qv = xqv[i];
-            q8_part_sums(qv, lo, hi);
-            dd = h2f(xdv[i]);
-        } else {
-            uint32_t d16, s16;
-            qv = quant_q8_1_part(xv[i], d16, s16, lo, hi, dd);
-        }
-        *(uint32_t *)(xa.qs + 32 * blk + 4 * part) = qv;
-        if (part == 0) {
-            xa.d8[blk] = dd;
-            xa.qs16[2 * blk] = lo;
-            xa.qs16[2 * blk + 1] = hi;
-        }
-    }
-    __syncthreads();   // x is ready long before the weights: off the critical path
+    if (!x_first) stage_x();   // x is ready long before the weights: off the critical path
     XSlice xs[M];
 #pragma unroll
     for (int m = 0; m < M; m++) xs[m] = x_slice(xa, ITEMS >= 64 ? 64 * m + lane : lane % ITEMS);
@@ -590,12 +600,17 @@ __host__ __device__ inline LdsB lds_b(uint32_t ffn, uint32_t n_slots, uint32_t t
 
 // q8_1 h of every slot: one lane per 16-byte half block (t = 2 * block + half),
 // so each lane's 16 values are exactly one half-block sum.
-constexpr int HT = 2;   // unrolled h tasks per thread (n_slots * ffn/32 * 2 <= 512); more go round a loop
+// HT unrolled h tasks per thread, all issued before the down weights (a task
+// loaded after them could only be waited for together with the whole weight
+// stream): 2 covers n_slots * ffn/16 <= 512 (the MoE shapes), 4 covers a
+// dense FFN's 12288-wide h (768 tasks); more go round a loop.
+template <int HT>
 struct HLoad {
     uint4 q[HT];
     uint32_t d[HT];
 };
-__device__ __forceinline__ void load_h(const uint8_t *hq8, uint32_t ntask, uint32_t first, HLoad &h) {
+template <int HT>
+__device__ __forceinline__ void load_h(const uint8_t *hq8, uint32_t ntask, uint32_t first, HLoad<HT> &h) {
 #pragma unroll
     for (int i = 0; i < HT; i++) {
         const uint32_t t = min(first + threadIdx.x + 256 * i, ntask - 1);
@@ -604,7 +619,8 @@ __device__ __forceinline__ void load_h(const uint8_t *hq8, uint32_t ntask, uint3
         h.d[i] = ld_u16(b);
     }
 }
-__device__ __forceinline__ void stage_h(uint8_t *hl, uint32_t ffn, uint32_t ntask, uint32_t first, const HLoad &h) {
+template <int HT>
+__device__ __forceinline__ void stage_h(uint8_t *hl, uint32_t ffn, uint32_t ntask, uint32_t first, const HLoad<HT> &h) {
     const uint32_t nblk = ffn / 32, ab = act_bytes(ffn);
 #pragma unroll
     for (int i = 0; i < HT; i++) {
@@ -628,11 +644,13 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a, uint32_t tr, uint32
     extern __shared__ __align__(16) uint8_t lds[];
     const LdsB L = lds_b(a.ffn, n_slots, tr);
     const uint32_t tid = threadIdx.x, lane = tid & 63;
+    pin_args(a.down, a.down_sh, a.y);
     // routing (lane r holds slot r), then the h loads
     const int32_t rid = a.route_ids[min(lane, (uint32_t)MAX_SLOTS - 1)];
     const float rw = a.route_w[min(lane, (uint32_t)MAX_SLOTS - 1)];
     const uint32_t ntask = n_slots * (a.ffn / 32) * 2;
-    HLoad hv;
+    constexpr int HT = P >= 16 ? 4 : 2;
+    HLoad<HT> hv;
     load_h(a.hq8, ntask, 0, hv);
 
     constexpr uint32_t S = QD::IPB * P;
@@ -658,7 +676,7 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a, uint32_t tr, uint32
     }
     stage_h(lds + L.hacts, a.ffn, ntask, 0, hv);
     for (uint32_t first = HT * 256; first < ntask; first += HT * 256) {
-        load_h(a.hq8, ntask, first, hv);   // only when n_slots * ffn / 16 > 512
+        load_h(a.hq8, ntask, first, hv);   // only when n_slots * ffn / 16 > 256 * HT
         stage_h(lds + L.hacts, a.ffn, ntask, first, hv);
     }
     __syncthreads();
