@@ -1,0 +1,354 @@
+/* katali-hip — command-line harness over the engine-side loader.
+ *
+ * The GPU harness commands of the reference engine (README.md:13,17,21,99-102,
+ * 149-171,309-312: cuda-info, cuda-check, cuda-check-moe, cuda-dp4a-selftest,
+ * cuda-bench, cuda-bench-cold, gpu-matvec-bench) for libkatali_hip, on
+ * synthetic tensors (no model file):
+ *
+ *   katali-hip info                  device and library status
+ *   katali-hip dp4a-selftest         q8_1 v_dot4 GEMV vs the fp32 GEMV, q8-exact x
+ *   katali-hip check                 the same two GEMV paths on N(0,1) x at the
+ *                                    engine's shapes: rel_L2 and the count outside
+ *                                    1e-3*(1+|ref|)
+ *   katali-hip check-moe             the fused MoE layer vs the same layer composed
+ *                                    from separate library GEMVs (SiLU-GLU and the
+ *                                    weighted sum on the host)
+ *   katali-hip matvec-bench [reps]   dense GEMV: event-timed us per call and GB/s
+ *   katali-hip bench [tokens]        48-layer top-8 MoE decode (hidden 2048, 128
+ *                                    experts, ffn 768), graph-replayed
+ *   katali-hip bench-cold [tokens]   40 layers x 256 experts (ffn 512) + shared
+ *                                    expert, routing rotated every token
+ *
+ * Exit status 0 on success / PASS, 1 on a failed check, 2 when no usable GPU.
+ */
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "katali_hip_loader.h"
+
+#define Q4K KATALI_HIP_TYPE_Q4_K
+#define Q6K KATALI_HIP_TYPE_Q6_K
+
+static const KataliHipApi *api;
+
+static int die(const char *what, int rc) {
+    fprintf(stderr, "katali-hip: %s failed (%d): %s\n", what, rc, katali_gpu_last_error());
+    return 1;
+}
+#define CK(call)                                 \
+    do {                                         \
+        int rc_ = (call);                        \
+        if (rc_) return die(#call, rc_);         \
+    } while (0)
+
+static uint64_t row_bytes(uint32_t type, uint64_t cols) { return cols / 256 * (type == Q4K ? 144 : 210); }
+static const char *tname(uint32_t t) { return t == Q4K ? "Q4_K" : "Q6_K"; }
+
+static double rel_l2(const float *a, const float *b, size_t n, size_t *outside) {
+    double num = 0, den = 0;
+    size_t o = 0;
+    for (size_t i = 0; i < n; i++) {
+        const double d = (double)a[i] - b[i];
+        num += d * d;
+        den += (double)b[i] * b[i];
+        if (fabs(d) > 1e-3 * (1.0 + fabs(b[i]))) o++;
+    }
+    if (outside) *outside = o;
+    return den > 0 ? sqrt(num / den) : sqrt(num);
+}
+
+static float *dalloc_f(size_t n) {
+    void *p = NULL;
+    return api->malloc_(&p, n * 4) ? NULL : (float *)p;
+}
+
+static int cmd_info(void) {
+    printf("library: %s\n", katali_gpu_status());
+    printf("abi version: %d\n", api->abi_version());
+    return 0;
+}
+
+static int cmd_selftest(void) {
+    char rep[1024] = {0};
+    const int rc = api->selftest(rep, sizeof rep);
+    fputs(rep, stdout);
+    if (rc) fprintf(stderr, "%s\n", katali_gpu_last_error());
+    return rc ? 1 : 0;
+}
+
+struct shape {
+    const char *role;
+    uint32_t type;
+    uint64_t rows, cols;
+};
+static const struct shape SHAPES[] = {
+    {"dense 6144x2048", Q4K, 6144, 2048},        {"expert gate/up 768x2048", Q4K, 768, 2048},
+    {"expert down 2048x768", Q6K, 2048, 768},    {"attn q/o 4096x4096", Q4K, 4096, 4096},
+    {"attn v 1024x4096", Q6K, 1024, 4096},       {"ffn down 4096x12288", Q6K, 4096, 12288},
+};
+#define NSHAPES (sizeof SHAPES / sizeof SHAPES[0])
+
+static int cmd_check(void) {
+    int fails = 0;
+    for (size_t s = 0; s < NSHAPES; s++) {
+        const struct shape *sh = &SHAPES[s];
+        void *w = NULL;
+        float *x = dalloc_f(sh->cols), *y0 = dalloc_f(sh->rows), *y1 = dalloc_f(sh->rows);
+        if (!x || !y0 || !y1) return die("malloc", -5);
+        CK(api->malloc_(&w, sh->rows * row_bytes(sh->type, sh->cols)));
+        CK(api->synth_fill(sh->type, w, sh->rows * sh->cols / 256, 100 + s, 0.02f));
+        CK(api->synth_normal(x, sh->cols, 200 + s, 1.0f));
+        CK(api->matvec(sh->type, w, sh->rows, sh->cols, x, y0));   /* fp32 dequantize-and-FMA path */
+        CK(api->matvec_dp4a(sh->type, w, sh->rows, sh->cols, x, y1));
+        float *a = malloc(sh->rows * 4), *b = malloc(sh->rows * 4);
+        CK(api->download(a, y1, sh->rows * 4));
+        CK(api->download(b, y0, sh->rows * 4));
+        size_t outside = 0;
+        const double r = rel_l2(a, b, sh->rows, &outside);
+        /* q8_1 rounding of x alone: ~1e-2 relative on N(0,1) activations */
+        const int ok = r <= 3e-2;
+        fails += !ok;
+        printf("check %-24s %s: rel_L2(dp4a, fp32) = %.3e, %zu of %llu outside 1e-3*(1+|ref|) %s\n", sh->role,
+               tname(sh->type), r, outside, (unsigned long long)sh->rows, ok ? "PASS" : "FAIL");
+        free(a);
+        free(b);
+        api->free_(w);
+        api->free_(x);
+        api->free_(y0);
+        api->free_(y1);
+    }
+    return fails ? 1 : 0;
+}
+
+static float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
+/* The fused layer vs the same layer from separate calls: q8 GEMVs for gate,
+ * up and down of each selected expert, SiLU-GLU and the rank-order weighted
+ * sum on the host. */
+static int cmd_check_moe(void) {
+    const uint32_t H = 2048, F = 768, E = 128, K = 8;
+    const uint64_t rbg = row_bytes(Q4K, H), rbd = row_bytes(Q6K, F);
+    void *g = NULL, *u = NULL, *d = NULL, *xq = NULL, *hq = NULL;
+    CK(api->malloc_(&g, (uint64_t)E * F * rbg));
+    CK(api->malloc_(&u, (uint64_t)E * F * rbg));
+    CK(api->malloc_(&d, (uint64_t)E * H * rbd));
+    CK(api->synth_fill(Q4K, g, (uint64_t)E * F * H / 256, 11, 0.02f));
+    CK(api->synth_fill(Q4K, u, (uint64_t)E * F * H / 256, 12, 0.02f));
+    CK(api->synth_fill(Q6K, d, (uint64_t)E * H * F / 256, 13, 0.02f));
+    float *x = dalloc_f(H), *y = dalloc_f(H), *gv = dalloc_f(F), *uv = dalloc_f(F), *h = dalloc_f(F), *dv = dalloc_f(H);
+    int32_t *ids_d = NULL;
+    float *w_d = dalloc_f(K);
+    CK(api->malloc_((void **)&ids_d, K * 4));
+    CK(api->malloc_(&xq, H / 32 * 36));
+    CK(api->malloc_(&hq, F / 32 * 36));
+    CK(api->synth_normal(x, H, 21, 1.0f));
+    const int32_t ids[8] = {5, 77, 3, 120, 64, 9, 31, 100};
+    const float w[8] = {0.25f, 0.2f, 0.15f, 0.12f, 0.1f, 0.08f, 0.06f, 0.04f};
+    CK(api->upload(ids_d, ids, sizeof ids));
+    CK(api->upload(w_d, w, sizeof w));
+    KataliHipMoe moe = {sizeof moe, Q4K, Q4K, Q6K, H, F, E, g, u, d, NULL, NULL, NULL};
+    KataliHipMoeRoute r;
+    memset(&r, 0, sizeof r);
+    r.struct_size = sizeof r;
+    r.n_sel = K;
+    r.ids = ids_d;
+    r.weights = w_d;
+    CK(api->moe_layer(&moe, &r, x, NULL, y));
+    float fused[2048], ref[2048], gh[768], uh[768], hh[768], dh[2048];
+    CK(api->download(fused, y, sizeof fused));
+    memset(ref, 0, sizeof ref);
+    CK(api->quantize_q8_1(x, H, xq));
+    for (uint32_t k = 0; k < K; k++) {
+        const uint8_t *ge = (const uint8_t *)g + (uint64_t)ids[k] * F * rbg;
+        const uint8_t *ue = (const uint8_t *)u + (uint64_t)ids[k] * F * rbg;
+        const uint8_t *de = (const uint8_t *)d + (uint64_t)ids[k] * H * rbd;
+        CK(api->matvec_q8(Q4K, ge, F, H, xq, gv));
+        CK(api->matvec_q8(Q4K, ue, F, H, xq, uv));
+        CK(api->download(gh, gv, sizeof gh));
+        CK(api->download(uh, uv, sizeof uh));
+        for (uint32_t j = 0; j < F; j++) hh[j] = silu_mul(gh[j], uh[j]);
+        CK(api->upload(h, hh, sizeof hh));
+        CK(api->quantize_q8_1(h, F, hq));
+        CK(api->matvec_q8(Q6K, de, H, F, hq, dv));
+        CK(api->download(dh, dv, sizeof dh));
+        for (uint32_t i = 0; i < H; i++) ref[i] = fmaf(w[k], dh[i], ref[i]);
+    }
+    size_t outside = 0;
+    const double rel = rel_l2(fused, ref, H, &outside);
+    const int ok = rel <= 1e-4;
+    printf("check-moe hidden %u ffn %u top-%u: rel_L2(fused layer, composed GEMVs) = %.3e, %zu of %u outside "
+           "1e-3*(1+|ref|) %s\n", H, F, K, rel, outside, H, ok ? "PASS" : "FAIL");
+    void *bufs[] = {g, u, d, xq, hq, x, y, gv, uv, h, dv, ids_d, w_d};
+    for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) api->free_(bufs[i]);
+    return ok ? 0 : 1;
+}
+
+static int time_ms(void *e0, void *e1, float *ms) { return api->event_elapsed(e0, e1, ms); }
+
+static int cmd_matvec_bench(int reps) {
+    void *e0 = NULL, *e1 = NULL;
+    CK(api->event_create(&e0));
+    CK(api->event_create(&e1));
+    /* raw streaming bandwidth in the same process, for reference */
+    {
+        const size_t n = (size_t)1 << 30;
+        void *a = NULL, *b = NULL;
+        CK(api->malloc_(&a, n));
+        CK(api->malloc_(&b, n));
+        CK(api->copy(b, a, n));
+        CK(api->event_record(e0));
+        for (int i = 0; i < 4; i++) CK(api->copy(b, a, n));
+        CK(api->event_record(e1));
+        CK(api->sync());
+        float ms = 0;
+        CK(time_ms(e0, e1, &ms));
+        printf("device copy 1 GiB: %.1f GB/s (read + write)\n", 4.0 * 2 * n / (ms * 1e-3) / 1e9);
+        api->free_(a);
+        api->free_(b);
+    }
+    for (size_t s = 0; s < NSHAPES; s++) {
+        const struct shape *sh = &SHAPES[s];
+        const uint64_t wb = sh->rows * row_bytes(sh->type, sh->cols);
+        const int copies = (int)((512ull << 20) / wb) + 1;   /* a pool larger than L2 + MALL */
+        void *w = NULL;
+        float *x = dalloc_f(sh->cols), *y = dalloc_f(sh->rows);
+        CK(api->malloc_(&w, wb * copies));
+        CK(api->synth_fill(sh->type, w, sh->rows * sh->cols / 256 * copies, 300 + s, 0.02f));
+        CK(api->synth_normal(x, sh->cols, 7, 1.0f));
+        CK(api->matvec_dp4a(sh->type, w, sh->rows, sh->cols, x, y));
+        CK(api->sync());
+        const int n = reps * copies;
+        CK(api->event_record(e0));
+        for (int i = 0; i < n; i++)
+            CK(api->matvec_dp4a(sh->type, (const uint8_t *)w + (uint64_t)(i % copies) * wb, sh->rows, sh->cols, x, y));
+        CK(api->event_record(e1));
+        CK(api->sync());
+        float ms = 0;
+        CK(time_ms(e0, e1, &ms));
+        const double us = ms * 1e3 / n;
+        printf("matvec-bench %-24s %s: %8.2f us/call, %7.1f GB/s (cold pool of %d copies, %d calls)\n", sh->role,
+               tname(sh->type), us, (double)wb / (us * 1e-6) / 1e9, copies, n);
+        api->free_(w);
+        api->free_(x);
+        api->free_(y);
+    }
+    api->event_destroy(e0);
+    api->event_destroy(e1);
+    return 0;
+}
+
+/* L layers of distinct weights, logits per token and layer (steps tokens,
+ * rotated through a device step index), one graph per token. */
+static int moe_bench(const char *name, uint32_t L, uint32_t H, uint32_t F, uint32_t E, uint32_t K, int shared,
+                     int tokens) {
+    const uint64_t rbg = row_bytes(Q4K, H), rbd = row_bytes(Q6K, F);
+    const uint64_t eb = 2 * F * rbg + H * rbd;
+    const int steps = 64;
+    void **g = calloc(L, sizeof *g), **u = calloc(L, sizeof *u), **d = calloc(L, sizeof *d);
+    void **gs = calloc(L, sizeof *gs), **us_ = calloc(L, sizeof *us_), **ds = calloc(L, sizeof *ds);
+    for (uint32_t l = 0; l < L; l++) {
+        CK(api->malloc_(&g[l], (uint64_t)E * F * rbg));
+        CK(api->malloc_(&u[l], (uint64_t)E * F * rbg));
+        CK(api->malloc_(&d[l], (uint64_t)E * H * rbd));
+        CK(api->synth_fill(Q4K, g[l], (uint64_t)E * F * H / 256, 1000 + 6 * l, 0.02f));
+        CK(api->synth_fill(Q4K, u[l], (uint64_t)E * F * H / 256, 1001 + 6 * l, 0.02f));
+        CK(api->synth_fill(Q6K, d[l], (uint64_t)E * H * F / 256, 1002 + 6 * l, 0.02f));
+        if (shared) {
+            CK(api->malloc_(&gs[l], F * rbg));
+            CK(api->malloc_(&us_[l], F * rbg));
+            CK(api->malloc_(&ds[l], H * rbd));
+            CK(api->synth_fill(Q4K, gs[l], (uint64_t)F * H / 256, 1003 + 6 * l, 0.02f));
+            CK(api->synth_fill(Q4K, us_[l], (uint64_t)F * H / 256, 1004 + 6 * l, 0.02f));
+            CK(api->synth_fill(Q6K, ds[l], (uint64_t)H * F / 256, 1005 + 6 * l, 0.02f));
+        }
+    }
+    float *x = dalloc_f(H), *y = dalloc_f(H), *logits = dalloc_f((size_t)steps * L * E);
+    int32_t *step = NULL;
+    CK(api->malloc_((void **)&step, 4));
+    CK(api->memset_(step, 0, 4));
+    CK(api->synth_normal(x, H, 5, 1.0f));
+    CK(api->synth_normal(logits, (size_t)steps * L * E, 6, 1.0f));
+    KataliHipMoe *m = calloc(L, sizeof *m);
+    KataliHipMoeRoute *r = calloc(L, sizeof *r);
+    for (uint32_t l = 0; l < L; l++) {
+        KataliHipMoe mm = {sizeof mm, Q4K, Q4K, Q6K, H, F, E, g[l], u[l], d[l],
+                           shared ? gs[l] : NULL, shared ? us_[l] : NULL, shared ? ds[l] : NULL};
+        m[l] = mm;
+        r[l].struct_size = sizeof r[l];
+        r[l].n_sel = (int32_t)K;
+        r[l].logits = logits + (size_t)l * E;
+        r[l].step = step;
+        r[l].logits_stride = (uint64_t)L * E;
+    }
+    /* eager once (sizes the scratch), then capture one token */
+    for (uint32_t l = 0; l < L; l++) CK(api->moe_layer(&m[l], &r[l], (l & 1) ? y : x, NULL, (l & 1) ? x : y));
+    CK(api->sync());
+    void *graph = NULL;
+    CK(api->graph_begin());
+    for (uint32_t l = 0; l < L; l++) CK(api->moe_layer(&m[l], &r[l], (l & 1) ? y : x, NULL, (l & 1) ? x : y));
+    CK(api->step_advance(step, steps));
+    CK(api->graph_end(&graph));
+    for (int i = 0; i < 4; i++) CK(api->graph_launch(graph));
+    void *e0 = NULL, *e1 = NULL;
+    CK(api->event_create(&e0));
+    CK(api->event_create(&e1));
+    CK(api->sync());
+    CK(api->event_record(e0));
+    for (int t = 0; t < tokens; t++) CK(api->graph_launch(graph));
+    CK(api->event_record(e1));
+    CK(api->sync());
+    float ms = 0;
+    CK(time_ms(e0, e1, &ms));
+    const double per_tok = ms / tokens, bytes = (double)L * ((K + (shared ? 1 : 0)) * eb + H / 32 * 36 + H * 4);
+    printf("%s: %u layers, %u experts, top-%u%s, hidden %u, ffn %u: %.3f ms/token, %.1f us/layer, %.1f GB/s "
+           "(%.1f %% of 8 TB/s), %.1f tok/s\n", name, L, E, K, shared ? " + shared" : "", H, F, per_tok,
+           per_tok * 1e3 / L, bytes / (per_tok * 1e-3) / 1e9, bytes / (per_tok * 1e-3) / 8e12 * 100, 1e3 / per_tok);
+    api->graph_destroy(graph);
+    api->event_destroy(e0);
+    api->event_destroy(e1);
+    for (uint32_t l = 0; l < L; l++) {
+        api->free_(g[l]);
+        api->free_(u[l]);
+        api->free_(d[l]);
+        if (shared) {
+            api->free_(gs[l]);
+            api->free_(us_[l]);
+            api->free_(ds[l]);
+        }
+    }
+    api->free_(x);
+    api->free_(y);
+    api->free_(logits);
+    api->free_(step);
+    free(g); free(u); free(d); free(gs); free(us_); free(ds); free(m); free(r);
+    return 0;
+}
+
+static void usage(void) {
+    fputs("usage: katali-hip info | dp4a-selftest | check | check-moe | matvec-bench [reps] | bench [tokens] |"
+          " bench-cold [tokens]\n", stderr);
+}
+
+int main(int argc, char **argv) {
+    if (argc < 2) {
+        usage();
+        return 2;
+    }
+    const char *cmd = argv[1];
+    const int n = argc > 2 ? atoi(argv[2]) : 0;
+    if (!katali_gpu_probe() || !(api = katali_gpu_api())) {
+        printf("no usable GPU: %s\n", katali_gpu_status());
+        return 2;
+    }
+    if (!strcmp(cmd, "info")) return cmd_info();
+    if (!strcmp(cmd, "dp4a-selftest")) return cmd_selftest();
+    if (!strcmp(cmd, "check")) return cmd_check();
+    if (!strcmp(cmd, "check-moe")) return cmd_check_moe();
+    if (!strcmp(cmd, "matvec-bench")) return cmd_matvec_bench(n > 0 ? n : 5);
+    if (!strcmp(cmd, "bench")) return moe_bench("bench", 48, 2048, 768, 128, 8, 0, n > 0 ? n : 32);
+    if (!strcmp(cmd, "bench-cold")) return moe_bench("bench-cold", 40, 2048, 512, 256, 8, 1, n > 0 ? n : 64);
+    usage();
+    return 2;
+}
