@@ -265,10 +265,13 @@ __device__ __forceinline__ float reduce_rows(float (&acc)[R]) {
 
 // ---------------------------------------------------------------------------
 // Kernel A: 64 Q4_K rows (32 gate + 32 up) per workgroup, NB blocks per row.
-// Eight waves; wave w owns rows 8w..8w+7 (waves 0-3 gate, 4-7 up) and runs on
-// its own apart from the x staging barrier, until the gate/up exchange at the
-// end. (Eight waves of 8 rows rather than four of 16: two waves per SIMD hide
-// each other's routing and decode latency, and each wave's serial work halves.)
+// Sixteen waves; wave w owns rows 4w..4w+3 (waves 0-7 gate, 8-15 up; eight
+// waves of 8 rows when a row has fewer than 16 lane items) and runs on its
+// own apart from the x staging barrier, until the gate/up exchange at the
+// end. (Measured at config 1: four waves of 16 rows 10.0 us, eight of 8
+// 8.7 us, sixteen of 4 about 8.0 us: with one workgroup per CU, more waves
+// per SIMD hide each other's routing, decode and load latency, and each
+// wave's serial work shrinks.)
 // Lane l always takes the same lane item of every row it touches:
 //   ITEMS = 8*NB >= 64: the k-th chunk is item 64*(k % M) + l of row k / M
 //                       (M = ITEMS/64 items per lane);
@@ -356,11 +359,17 @@ __device__ __forceinline__ float item_dot_u(const Q4K::Unp &u, const float4 &sc,
 
 constexpr int A_ROWS_PER_WAVE = 8;
 constexpr int A_THREADS = 64 * 64 / A_ROWS_PER_WAVE;
+// kernel A (single token): rows per wave (16 waves of 4 rows; 8 rows when a
+// row has fewer than 16 lane items)
+template <int NB>
+constexpr int a1_rw() { return NB >= 2 ? 4 : 8; }
+template <int NB>
+constexpr int a1_threads() { return 64 * 64 / a1_rw<NB>(); }
 
 template <int NB, int C>
-__global__ void __launch_bounds__(A_THREADS) k_moe_gu(MoeArgs a) {
-    constexpr int RW = A_ROWS_PER_WAVE;
-    constexpr int NT = A_THREADS;
+__global__ void __launch_bounds__(a1_threads<NB>()) k_moe_gu(MoeArgs a) {
+    constexpr int RW = a1_rw<NB>();
+    constexpr int NT = a1_threads<NB>();
     constexpr int ITEMS = 8 * NB;              // lane items per row
     constexpr int LPL = RW * ITEMS / 64;       // chunks per lane over the wave's rows
     constexpr int GROUPS = LPL > 16 ? LPL / 16 : 1;
@@ -953,11 +962,11 @@ static hipError_t go_a(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
     const LdsA L = lds_a(a.hidden, NB);
     const dim3 grid(n_slots * (a.ffn / 32));
     if (a.n_expert <= 128)
-        hipLaunchKernelGGL((k_moe_gu<NB, 2>), grid, dim3(A_THREADS), L.total, s, a);
+        hipLaunchKernelGGL((k_moe_gu<NB, 2>), grid, dim3(a1_threads<NB>()), L.total, s, a);
     else if (a.n_expert <= 256)
-        hipLaunchKernelGGL((k_moe_gu<NB, 4>), grid, dim3(A_THREADS), L.total, s, a);
+        hipLaunchKernelGGL((k_moe_gu<NB, 4>), grid, dim3(a1_threads<NB>()), L.total, s, a);
     else
-        hipLaunchKernelGGL((k_moe_gu<NB, 8>), grid, dim3(A_THREADS), L.total, s, a);
+        hipLaunchKernelGGL((k_moe_gu<NB, 8>), grid, dim3(a1_threads<NB>()), L.total, s, a);
     return hipGetLastError();
 }
 
