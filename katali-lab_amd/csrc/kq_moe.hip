@@ -269,7 +269,7 @@ __device__ __forceinline__ float reduce_rows(float (&acc)[R]) {
 // waves of 8 rows when a row has fewer than 16 lane items) and runs on its
 // own apart from the x staging barrier, until the gate/up exchange at the
 // end. (Measured at config 1: four waves of 16 rows 10.0 us, eight of 8
-// 8.7 us, sixteen of 4 about 8.0 us: with one workgroup per CU, more waves
+// 8.7 us, sixteen of 4 8.2 us: with one workgroup per CU, more waves
 // per SIMD hide each other's routing, decode and load latency, and each
 // wave's serial work shrinks.)
 // Lane l always takes the same lane item of every row it touches:
