@@ -266,7 +266,7 @@ __device__ __forceinline__ float reduce_rows(float (&acc)[R]) {
 // ---------------------------------------------------------------------------
 // Kernel A: 64 Q4_K rows (32 gate + 32 up) per workgroup, NB blocks per row.
 // Sixteen waves; wave w owns rows 4w..4w+3 (waves 0-7 gate, 8-15 up; eight
-// waves of 8 rows when a row has fewer than 16 lane items) and runs on its
+// waves of 8 rows for the row widths a1_rw() names) and runs on its
 // own apart from the x staging barrier, until the gate/up exchange at the
 // end. (Measured at config 1: four waves of 16 rows 10.0 us, eight of 8
 // 8.7 us, sixteen of 4 8.2 us: with one workgroup per CU, more waves
@@ -359,10 +359,12 @@ __device__ __forceinline__ float item_dot_u(const Q4K::Unp &u, const float4 &sc,
 
 constexpr int A_ROWS_PER_WAVE = 8;
 constexpr int A_THREADS = 64 * 64 / A_ROWS_PER_WAVE;
-// kernel A (single token): rows per wave (16 waves of 4 rows; 8 rows when a
-// row has fewer than 16 lane items)
+// kernel A (single token): rows per wave. 16 waves of 4 rows; 8 rows when a
+// row has fewer than 16 lane items, and for 4096-wide rows (a dense FFN's
+// 384 workgroups fill the CUs already: 16.8 us with 8 rows per wave against
+// 18.0 us with 4 at the Qwen3-8B shape)
 template <int NB>
-constexpr int a1_rw() { return NB >= 2 ? 4 : 8; }
+constexpr int a1_rw() { return NB >= 2 && NB <= 8 ? 4 : 8; }
 template <int NB>
 constexpr int a1_threads() { return 64 * 64 / a1_rw<NB>(); }
 
