@@ -17,7 +17,7 @@ in one hipGraph per token; a step is one replay.
             so every GEMV reads cold weights; a step is one pass over them.
   qwen8b    dense Qwen3-8B-shaped decode GEMV chain, 36 layers, hidden 4096,
             q/o 4096x4096 and k 1024x4096 Q4_K, v 1024x4096 Q6_K, SwiGLU
-            12288 (gate/up Q4_K, down Q6_K); per layer q,k,v = W x, o = Wo q
+            12288 (gate/up Q4_K, down Q6_K); per layer q,k,v = W x (one launch), o = Wo q
             (q stands in for the attention output, which is not a GEMV),
             FFN(o) through the MoE kernels with the shared expert only; every
             layer reads its own N(0,1) x; a step is one token (one replay).
@@ -236,9 +236,9 @@ def bench_dense(hip, name, steps, warmup):
     def token():
         for li, (wq, wk, wv, wo, g, u, d) in enumerate(layers):
             xl = at(x, li, hidden)
-            hip.matvec_dp4a(Q4_K, wq, q_rows, hidden, xl, at(q, li, q_rows))
-            hip.matvec_dp4a(Q4_K, wk, kv_rows, hidden, xl, at(k, li, kv_rows))
-            hip.matvec_dp4a(Q6_K, wv, kv_rows, hidden, xl, at(v, li, kv_rows))
+            # q, k and v share x: one launch (the engine's matvec_multi)
+            hip.matvec_multi([Q4_K, Q4_K, Q6_K], [wq, wk, wv], [q_rows, kv_rows, kv_rows], hidden, xl,
+                             [at(q, li, q_rows), at(k, li, kv_rows), at(v, li, kv_rows)], dp4a=True)
             hip.matvec_dp4a(Q4_K, wo, hidden, q_rows, at(q, li, q_rows), at(o, li, hidden))
             hip.moe_layer(descs[li], route, at(y, li, hidden), x=at(o, li, hidden))
 
@@ -745,7 +745,7 @@ def main():
             "layers": L, "hidden": hidden, "ffn": ffn, "weights_gb": round(res["weights_gb"], 2),
             "bytes_per_token": res["bytes_per_token"], "parallelism": "single GPU",
         }
-        kernel = "decode layer: q, k, v, o GEMVs + k_moe_gu + k_moe_down (shared expert only)"
+        kernel = "decode layer: k_gemv_multi (q, k, v) + k_gemv (o) + k_moe_gu + k_moe_down (shared expert only)"
         extra = {"tok_s": round(res["tok_s"], 2)}
     else:
         res, shape = bench_gemv(hip, args.workload, args.steps, args.warmup)

@@ -24,7 +24,8 @@ int katali_dense_hip_enabled(void);
  * the device copy is cached by host pointer (katali_dense_cuda.c:46-56). */
 int katali_dense_hip_matvec(uint32_t type, const void *w, uint64_t w_bytes, uint64_t rows, uint64_t cols,
                             const float *x, float *y);
-/* n <= 4 same-input projections (katali_dense_cuda.c:58-73). */
+/* n <= 4 same-input projections (katali_dense_cuda.c:58-73): one upload,
+ * one launch for all n (katali_hip_matvec_multi), n downloads. */
 int katali_dense_hip_matvec_multi(int n, const uint32_t *types, const void *const *ws, const uint64_t *w_bytes,
                                   const uint64_t *rows, uint64_t cols, const float *x, float **ys);
 /* Number of cached device weights (for tests and diagnostics). */

@@ -93,6 +93,19 @@ int katali_hip_matvec_q8(uint32_t type, const void *w_dev, uint64_t rows, uint64
  * launch, bit-identical to quantize_q8_1 followed by matvec_q8). */
 int katali_hip_matvec_dp4a(uint32_t type, const void *w_dev, uint64_t rows, uint64_t cols,
                            const float *x_dev, float *y_dev);
+/* Up to four GEMVs over one activation in one launch: ys[i][rows[i]] =
+ * W_i . x, W_i of types[i] (Q4_K or Q6_K, mixed allowed), all with `cols`
+ * columns. Replaces the per-tensor katali_cuda_matvec loop of
+ * katali_dense_cuda_matvec_multi (V/src/katali_dense_cuda.c:58-72; called at
+ * V/src/gguf_model.c:533 for q, k, v (:614) and gate, up (:680)): each
+ * ys[i] is bit-identical to katali_hip_matvec on W_i. Activation
+ * mode as katali_hip_matvec (fp32, or v_dot4 with KATALI_HIP_DP4A=1). */
+int katali_hip_matvec_multi(int n, const uint32_t *types, const void *const *w_devs, const uint64_t *rows,
+                            uint64_t cols, const float *x_dev, float *const *y_devs);
+/* The same with x quantized to q8_1 in every workgroup (v_dot4), each output
+ * bit-identical to katali_hip_matvec_dp4a. */
+int katali_hip_matvec_multi_dp4a(int n, const uint32_t *types, const void *const *w_devs, const uint64_t *rows,
+                                 uint64_t cols, const float *x_dev, float *const *y_devs);
 /* Exact per-block int32 sums of the q8 GEMV, from the same device routines:
  * Q4_K -> isums[rows][cols/32], Q6_K -> isums[rows][cols/16] (sum of
  * (q6-32)*q8 per 16 values). For self-tests. */

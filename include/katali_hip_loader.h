@@ -41,6 +41,11 @@ int katali_gpu_download(void *host, const void *dev, size_t bytes);
 int katali_gpu_supports_type(uint32_t ggml_type);
 int katali_gpu_matvec(uint32_t type, const void *w_dev, uint64_t rows, uint64_t cols,
                       const float *x_dev, float *y_dev);
+/* Up to four GEMVs over one x in one launch, in place of the per-tensor
+ * katali_cuda_matvec loop of katali_dense_cuda_matvec_multi
+ * (V/src/katali_dense_cuda.c:58-72). */
+int katali_gpu_matvec_multi(int n, const uint32_t *types, const void *const *w_devs, const uint64_t *rows,
+                            uint64_t cols, const float *x_dev, float *const *y_devs);
 
 /* The MoE-engine entry points of the closed backend (README.md:13,17,21):
  * one call per MoE layer, q8_1 activations, graphs, self-test. */
@@ -101,6 +106,10 @@ typedef struct KataliHipApi {
     int (*copy)(void *, const void *, size_t);
     int (*argmax)(const float *, uint64_t, int32_t *);
     int (*moe_batch)(const KataliHipMoe *, const KataliHipMoeBatch *, const float *, float *);
+    int (*matvec_multi)(int, const uint32_t *, const void *const *, const uint64_t *, uint64_t, const float *,
+                        float *const *);
+    int (*matvec_multi_dp4a)(int, const uint32_t *, const void *const *, const uint64_t *, uint64_t,
+                             const float *, float *const *);
 } KataliHipApi;
 
 /* NULL when the library could not be loaded or an entry point is missing. */

@@ -420,6 +420,29 @@ int katali_hip_matvec_dp4a(uint32_t type, const void *w, uint64_t rows, uint64_t
     return launched(kq::launch_gemv(type, (const uint8_t *)w, rows, cols, x, nullptr, y, 2, g_stream), "matvec_dp4a");
 }
 
+static int matvec_multi(int n, const uint32_t *types, const void *const *ws, const uint64_t *rows, uint64_t cols,
+                        const float *x, float *const *ys, int mode, const char *what) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (n < 1 || n > kq::GEMV_MULTI_MAX) return fail(KATALI_HIP_E_INVALID, "n=%d not in 1..%d", n, kq::GEMV_MULTI_MAX);
+    if (!types || !ws || !rows || !ys) return fail(KATALI_HIP_E_INVALID, "null array");
+    for (int i = 0; i < n; i++)
+        if ((rc = check_gemv(types[i], ws[i], rows[i], cols, x, ys[i]))) return rc;
+    return launched(kq::launch_gemv_multi(n, types, (const uint8_t *const *)ws, rows, cols, x, ys, mode, g_stream),
+                    what);
+}
+
+int katali_hip_matvec_multi(int n, const uint32_t *types, const void *const *ws, const uint64_t *rows, uint64_t cols,
+                            const float *x, float *const *ys) {
+    const int mode = (env_on("KATALI_CUDA_DP4A") || env_on("KATALI_HIP_DP4A")) ? 2 : 0;
+    return matvec_multi(n, types, ws, rows, cols, x, ys, mode, "matvec_multi");
+}
+
+int katali_hip_matvec_multi_dp4a(int n, const uint32_t *types, const void *const *ws, const uint64_t *rows,
+                                 uint64_t cols, const float *x, float *const *ys) {
+    return matvec_multi(n, types, ws, rows, cols, x, ys, 2, "matvec_multi_dp4a");
+}
+
 int katali_hip_block_isums(uint32_t type, const void *w, uint64_t rows, uint64_t cols, const void *xq8, int32_t *out) {
     int rc = ensure();
     if (rc || (rc = check_gemv(type, w, rows, cols, xq8, out))) return rc;

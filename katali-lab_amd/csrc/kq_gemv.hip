@@ -136,11 +136,12 @@ struct XStage {
     }
 };
 
+// The row groups of one matrix that workgroup `block` of `nblocks` takes
+// (the workgroups' shares of the matrix interleave: a grid-stride loop).
 template <class QT, int IPL_T, int RPS, int MODE>
-__global__ void __launch_bounds__(256)
-    k_gemv(const uint8_t *__restrict__ w, uint32_t rows, uint32_t cols, uint64_t rb, uint32_t log2s,
-           const float *xf, const uint8_t *xq, float *__restrict__ y) {
-    extern __shared__ __align__(16) uint8_t lds[];
+__device__ __forceinline__ void gemv_rows(const uint8_t *__restrict__ w, uint32_t rows, uint32_t cols, uint64_t rb,
+                                          uint32_t log2s, const float *xf, const uint8_t *xq, float *__restrict__ y,
+                                          uint32_t block, uint32_t nblocks, uint8_t *lds) {
     const Act a = act_carve(lds, cols);
     const ActF af = actf_carve(lds, cols);
     const uint32_t S = 1u << log2s;
@@ -150,7 +151,7 @@ __global__ void __launch_bounds__(256)
     const uint32_t items = cols / 256 * QT::IPB;
     const int IPL = IPL_T > 0 ? IPL_T : (int)(items >> log2s);
     const uint32_t rows_iter = 4 * slots * RPS;
-    const uint32_t base0 = blockIdx.x * rows_iter;
+    const uint32_t base0 = block * rows_iter;
     auto row_of = [&](uint32_t base, int r) { return base + r * (4 * slots) + wave * slots + slot; };
 
     // Unrolled items: the activation loads, then the first row group's
@@ -184,7 +185,7 @@ __global__ void __launch_bounds__(256)
     xs.store(xf, xq, cols, a, af);
     __syncthreads();
 
-    for (uint32_t base = base0; base < rows; base += gridDim.x * rows_iter) {
+    for (uint32_t base = base0; base < rows; base += nblocks * rows_iter) {
         float acc[RPS];
         if constexpr (IPL_T > 0) {
             if (base != base0) load_rows(base);
@@ -223,6 +224,35 @@ __global__ void __launch_bounds__(256)
             if (s == 0 && row < rows) y[row] = v;
         }
     }
+}
+
+template <class QT, int IPL_T, int RPS, int MODE>
+__global__ void __launch_bounds__(256)
+    k_gemv(const uint8_t *__restrict__ w, uint32_t rows, uint32_t cols, uint64_t rb, uint32_t log2s,
+           const float *xf, const uint8_t *xq, float *__restrict__ y) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    gemv_rows<QT, IPL_T, RPS, MODE>(w, rows, cols, rb, log2s, xf, xq, y, blockIdx.x, gridDim.x, lds);
+}
+
+// Up to four GEMVs over one activation in one launch (the engine's
+// matvec_multi: q, k and v of a layer). Matrix m owns workgroups
+// [end[m-1], end[m]) and runs the single-matrix body on them, so each row's
+// arithmetic, and its bits, are those of k_gemv.
+template <int IPL4, int RPS4, int IPL6, int RPS6, int MODE>
+__global__ void __launch_bounds__(256) k_gemv_multi(GemvMultiArgs g) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < GEMV_MULTI_MAX - 1; i++)
+        if (blockIdx.x >= g.end[i]) m = i + 1;   // end[] is non-decreasing, padded with the total
+    const uint32_t start = m ? g.end[m - 1] : 0;
+    const uint32_t blk = blockIdx.x - start, nblk = g.end[m] - start;
+    if (g.type[m] == T_Q4_K)
+        gemv_rows<Q4K, IPL4, RPS4, MODE>(g.w[m], g.rows[m], g.cols, (uint64_t)(g.cols / 256) * Q4K::BB, g.log2s4,
+                                         g.x, nullptr, g.y[m], blk, nblk, lds);
+    else
+        gemv_rows<Q6K, IPL6, RPS6, MODE>(g.w[m], g.rows[m], g.cols, (uint64_t)(g.cols / 256) * Q6K::BB, g.log2s6,
+                                         g.x, nullptr, g.y[m], blk, nblk, lds);
 }
 
 static int ilog2(uint32_t v) {
@@ -267,6 +297,80 @@ static hipError_t gemv_dispatch(const uint8_t *w, uint64_t rows, uint64_t cols, 
         case 2: return Q4 ? go(k_gemv<QT, 2, 2, MODE>, 2) : go(k_gemv<QT, 2, 1, MODE>, 1);
         case 3: return go(k_gemv<QT, 3, 1, MODE>, 1);
         default: return go(k_gemv<QT, 0, 1, MODE>, 1);
+    }
+}
+
+// Rows per workgroup pass of the unrolled instantiations (the same choice
+// gemv_dispatch makes; the generic path takes one row per lane slot).
+static int gemv_rps(uint32_t type, uint32_t ipl) {
+    if (type == T_Q4_K) return ipl == 1 ? 4 : (ipl == 2 ? 2 : 1);
+    return ipl == 1 ? 2 : 1;
+}
+
+hipError_t launch_gemv_multi(int n, const uint32_t *types, const uint8_t *const *ws, const uint64_t *rows,
+                             uint64_t cols, const float *x, float *const *ys, int mode, hipStream_t st) {
+    GemvMultiArgs g{};
+    const uint32_t items4 = (uint32_t)(cols / 256) * Q4K::IPB, items6 = (uint32_t)(cols / 256) * Q6K::IPB;
+    const uint32_t s4 = lanes_per_row(items4), s6 = lanes_per_row(items6);
+    const uint32_t ipl4 = items4 / s4, ipl6 = items6 / s6;
+    // The unrolled pairs that one column count gives (cols 256..2048, 4096,
+    // 6144); any other pair runs the generic item loop for both types.
+    int sel = 0;   // 0 generic, 1 (1,1), 2 (2,1), 3 (3,3)
+    if (ipl4 == 1 && ipl6 == 1) sel = 1;
+    else if (ipl4 == 2 && ipl6 == 1) sel = 2;
+    else if (ipl4 == 3 && ipl6 == 3) sel = 3;
+    uint64_t iters[GEMV_MULTI_MAX] = {0}, total = 0;
+    for (int i = 0; i < n; i++) {
+        const uint32_t ipl = types[i] == T_Q4_K ? ipl4 : ipl6;
+        const uint32_t S = types[i] == T_Q4_K ? s4 : s6;
+        const uint64_t rows_iter = 4ull * (64 / S) * (sel ? gemv_rps(types[i], ipl) : 1);
+        iters[i] = (rows[i] + rows_iter - 1) / rows_iter;
+        total += iters[i];
+    }
+    if (!total) return hipSuccess;
+    const uint64_t cap = 8ull * device_cu_count();
+    uint32_t end = 0;
+    for (int i = 0; i < GEMV_MULTI_MAX; i++) {
+        if (i < n) {
+            uint64_t wg = iters[i];
+            if (total > cap && wg) {   // share the capped grid in proportion, at least one each
+                wg = wg * cap / total;
+                if (!wg) wg = 1;
+            }
+            end += (uint32_t)wg;
+            g.w[i] = ws[i];
+            g.y[i] = ys[i];
+            g.rows[i] = (uint32_t)rows[i];
+            g.type[i] = types[i];
+        }
+        g.end[i] = end;   // past n: the total, so no workgroup maps there
+    }
+    g.cols = (uint32_t)cols;
+    g.log2s4 = (uint32_t)ilog2(s4);
+    g.log2s6 = (uint32_t)ilog2(s6);
+    g.x = x;
+    const uint32_t lds = mode == 0 ? actf_bytes((uint32_t)cols) : act_bytes((uint32_t)cols);
+    auto go = [&](auto kern) -> hipError_t {
+        if (lds > 64 * 1024) {
+            hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+        }
+        hipLaunchKernelGGL(kern, dim3(end), dim3(256), lds, st, g);
+        return hipGetLastError();
+    };
+    if (mode == 0) {
+        switch (sel) {
+            case 1: return go(k_gemv_multi<1, 4, 1, 2, 0>);
+            case 2: return go(k_gemv_multi<2, 2, 1, 2, 0>);
+            case 3: return go(k_gemv_multi<3, 1, 3, 1, 0>);
+            default: return go(k_gemv_multi<0, 1, 0, 1, 0>);
+        }
+    }
+    switch (sel) {
+        case 1: return go(k_gemv_multi<1, 4, 1, 2, 2>);
+        case 2: return go(k_gemv_multi<2, 2, 1, 2, 2>);
+        case 3: return go(k_gemv_multi<3, 1, 3, 1, 2>);
+        default: return go(k_gemv_multi<0, 1, 0, 1, 2>);
     }
 }
 

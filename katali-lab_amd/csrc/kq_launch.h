@@ -21,6 +21,21 @@ hipError_t launch_quantize_q8_1(const float *x, uint64_t n, uint8_t *out, hipStr
 hipError_t launch_gemv(uint32_t type, const uint8_t *w, uint64_t rows, uint64_t cols, const float *xf,
                        const uint8_t *xq, float *y, int mode, hipStream_t s);
 
+// Up to GEMV_MULTI_MAX GEMVs sharing one fp32 activation in one launch
+// (mode 0 or 2 as above); every output is bit-identical to launch_gemv's.
+constexpr int GEMV_MULTI_MAX = 4;
+struct GemvMultiArgs {
+    const uint8_t *w[GEMV_MULTI_MAX];
+    float *y[GEMV_MULTI_MAX];
+    uint32_t rows[GEMV_MULTI_MAX];
+    uint32_t type[GEMV_MULTI_MAX];
+    uint32_t end[GEMV_MULTI_MAX];   // cumulative workgroup counts
+    uint32_t cols, log2s4, log2s6;
+    const float *x;
+};
+hipError_t launch_gemv_multi(int n, const uint32_t *types, const uint8_t *const *ws, const uint64_t *rows,
+                             uint64_t cols, const float *x, float *const *ys, int mode, hipStream_t s);
+
 // Per-block exact integer sums of a GEMV against a q8_1 activation:
 // Q4_K -> out[rows][cols/32], Q6_K -> out[rows][cols/16].
 hipError_t launch_isums(uint32_t type, const uint8_t *w, uint64_t rows, uint64_t cols, const uint8_t *xq,

@@ -99,19 +99,24 @@ int katali_dense_hip_matvec(uint32_t type, const void *w, uint64_t w_bytes, uint
 int katali_dense_hip_matvec_multi(int n, const uint32_t *types, const void *const *ws, const uint64_t *w_bytes,
                                   const uint64_t *rows, uint64_t cols, const float *x, float **ys) {
     if (n <= 0 || n > 4 || !types || !ws || !w_bytes || !rows || !ys || !x || !katali_dense_hip_enabled()) return -1;
-    uint64_t maxrows = 0;
+    /* One launch for all n tensors: their outputs sit back to back in g_y. */
+    uint64_t total = 0, off[4];
     for (int i = 0; i < n; i++) {
-        if (!ws[i] || !ys[i]) return -1;
-        if (rows[i] > maxrows) maxrows = rows[i];
+        if (!ws[i] || !ys[i] || !katali_gpu_supports_type(types[i])) return -1;
+        off[i] = total;
+        total += rows[i];
     }
-    if (ensure_buffers(cols, maxrows) != 0) return -1;
+    if (ensure_buffers(cols, total) != 0) return -1;
+    const void *dw[4];
+    float *dy[4];
+    for (int i = 0; i < n; i++) {
+        if (!(dw[i] = device_weight(ws[i], w_bytes[i]))) return -1;
+        dy[i] = g_y + off[i];
+    }
     if (katali_gpu_upload(g_x, x, (size_t)cols * sizeof(float)) != KATALI_GPU_OK) return -1;
-    for (int i = 0; i < n; i++) {
-        if (!katali_gpu_supports_type(types[i])) return -1;
-        void *dw = device_weight(ws[i], w_bytes[i]);
-        if (!dw || katali_gpu_matvec(types[i], dw, rows[i], cols, g_x, g_y) != KATALI_GPU_OK) return -1;
-        if (katali_gpu_download(ys[i], g_y, (size_t)rows[i] * sizeof(float)) != KATALI_GPU_OK) return -1;
-    }
+    if (katali_gpu_matvec_multi(n, types, dw, rows, cols, g_x, dy) != KATALI_GPU_OK) return -1;
+    for (int i = 0; i < n; i++)
+        if (katali_gpu_download(ys[i], dy[i], (size_t)rows[i] * sizeof(float)) != KATALI_GPU_OK) return -1;
     return 0;
 }
 

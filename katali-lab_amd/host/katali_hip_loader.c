@@ -107,6 +107,8 @@ static int load(void) {
     LOAD(copy, "katali_hip_copy");
     LOAD(argmax, "katali_hip_argmax");
     LOAD(moe_batch, "katali_hip_moe_batch");
+    LOAD(matvec_multi, "katali_hip_matvec_multi");
+    LOAD(matvec_multi_dp4a, "katali_hip_matvec_multi_dp4a");
     if (g_api.abi_version() != KATALI_HIP_ABI_VERSION) {
         snprintf(g_status, sizeof g_status, "%s: ABI version %d, loader expects %d", tried, g_api.abi_version(),
                  KATALI_HIP_ABI_VERSION);
@@ -157,6 +159,10 @@ int katali_gpu_download(void *host, const void *dev, size_t n) { FORWARD(g_api.d
 int katali_gpu_supports_type(uint32_t t) { return katali_gpu_probe() ? g_api.supports_type(t) : 0; }
 int katali_gpu_matvec(uint32_t type, const void *w, uint64_t rows, uint64_t cols, const float *x, float *y) {
     FORWARD(g_api.matvec(type, w, rows, cols, x, y));
+}
+int katali_gpu_matvec_multi(int n, const uint32_t *types, const void *const *w, const uint64_t *rows, uint64_t cols,
+                            const float *x, float *const *y) {
+    FORWARD(g_api.matvec_multi(n, types, w, rows, cols, x, y));
 }
 int katali_gpu_quantize_q8_1(const float *x, uint64_t n, void *q8) { FORWARD(g_api.quantize_q8_1(x, n, q8)); }
 int katali_gpu_matvec_q8(uint32_t type, const void *w, uint64_t rows, uint64_t cols, const void *xq, float *y) {

@@ -57,6 +57,8 @@ SIGNATURES = {
     "katali_hip_copy": (C.c_int, [_vp, _vp, _sz]),
     "katali_hip_argmax": (C.c_int, [_vp, _u64, _vp]),
     "katali_hip_moe_batch": (C.c_int, [_vp, _vp, _vp, _vp]),
+    "katali_hip_matvec_multi": (C.c_int, [C.c_int, _vp, _vp, _vp, _u64, _vp, _vp]),
+    "katali_hip_matvec_multi_dp4a": (C.c_int, [C.c_int, _vp, _vp, _vp, _u64, _vp, _vp]),
 }
 
 
@@ -177,6 +179,14 @@ class KataliHip:
 
     def matvec_dp4a(self, t, w, rows, cols, x, y) -> None:
         self.check(self.lib.katali_hip_matvec_dp4a(t, w.ptr, rows, cols, x.ptr, y.ptr))
+
+    def matvec_multi(self, types, ws, rows, cols, x, ys, dp4a: bool = False) -> None:
+        """ys[i] = W_i . x for up to four matrices in one launch."""
+        n = len(types)
+        args = ((_u32 * n)(*types), (_vp * n)(*[w.ptr for w in ws]), (_u64 * n)(*rows), cols, x.ptr,
+                (_vp * n)(*[y.ptr for y in ys]))
+        fn = self.lib.katali_hip_matvec_multi_dp4a if dp4a else self.lib.katali_hip_matvec_multi
+        self.check(fn(n, *args))
 
     def block_isums(self, t, w, rows, cols, xq, out) -> None:
         self.check(self.lib.katali_hip_block_isums(t, w.ptr, rows, cols, xq.ptr, out.ptr))

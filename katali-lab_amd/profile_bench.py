@@ -31,7 +31,7 @@ KERNELS = {
     "moe48": ("k_moe_gu", "k_moe_down"),
     "moe40cold": ("k_moe_gu", "k_moe_down"),
     "gemv6144": ("k_gemv",),
-    "qwen8b": ("k_moe_down", "k_moe_gu", "k_gemv"),
+    "qwen8b": ("k_moe_down", "k_moe_gu", "k_gemv_multi", "k_gemv"),
     "moebatch": ("k_mb_group", "k_quantize_q8_1", "k_moe_gu_grp", "k_mb_gu_mfma", "k_moe_down_grp", "k_mb_down_mfma",
                  "k_mb_combine"),
 }

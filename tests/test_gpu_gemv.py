@@ -182,3 +182,77 @@ def test_gemv_rejects_bad_arguments(hip):
     with pytest.raises(HipError) as e:
         hip.matvec_dp4a(13, w, 1, 256, x, y)            # Q5_K not supported
     assert e.value.rc == -4
+
+
+# (cols, [(type, rows), ...]): the engine's q/k/v and gate/up groups plus
+# geometries that take each unrolled type pair, the generic item loop, a
+# matrix with no rows and ragged row counts.
+MULTI_CASES = [
+    (4096, [(Q4_K, 4096), (Q4_K, 1024), (Q6_K, 1024)]),
+    (2048, [(Q4_K, 768), (Q4_K, 768)]),
+    (256, [(Q6_K, 5), (Q4_K, 0), (Q4_K, 130), (Q6_K, 64)]),
+    (6144, [(Q4_K, 100), (Q6_K, 33)]),
+    (1280, [(Q6_K, 9), (Q4_K, 17), (Q6_K, 1)]),
+    (12288, [(Q4_K, 40), (Q6_K, 24)]),
+    (2048, [(Q6_K, 300)]),
+]
+
+
+@pytest.mark.parametrize("dp4a", [False, True], ids=["f32", "dp4a"])
+@pytest.mark.parametrize("cols,mats", MULTI_CASES, ids=[f"c{c}_n{len(m)}" for c, m in MULTI_CASES])
+def test_gemv_multi_bit_identical(hip, oracle, cols, mats, dp4a):
+    """One launch over several matrices gives each output the single GEMV's bits."""
+    print(f"[gemv_multi] cols={cols} mats={mats} dp4a={dp4a}", flush=True)
+    rng = np.random.default_rng(cols + 13 * len(mats) + dp4a)
+    ws = [S.matrix(rng, t, r, cols) for t, r in mats]
+    x = S.activation(rng, cols)
+    xd = hip.to_device(x)
+    wds = [hip.to_device(w) for w in ws]
+    ys = [hip.alloc(max(r, 1) * 4) for _, r in mats]
+    hip.matvec_multi([t for t, _ in mats], wds, [r for _, r in mats], cols, xd, ys, dp4a=dp4a)
+    xq = oracle.quantize_q8_1(x)
+    for (t, r), w, wd, y in zip(mats, ws, wds, ys):
+        if not r:
+            continue
+        one = hip.alloc(r * 4)
+        (hip.matvec_dp4a if dp4a else hip.matvec)(t, wd, r, cols, xd, one)
+        got = y.download(np.float32, r)
+        assert np.array_equal(got.view(np.uint32), one.download(np.float32, r).view(np.uint32))
+        if dp4a:
+            assert rel_l2(got, oracle.matvec_q8(t, w, r, cols, xq)) <= 1e-5
+        else:
+            want = oracle.matvec_f32x(t, w, r, cols, x)
+            assert np.all(np.abs(got - want) <= 1e-4 + 1e-3 * np.abs(want))
+
+
+def test_gemv_multi_capped_grid(hip):
+    """More row groups than the capped grid: each matrix's share loops over its rows."""
+    cols, mats = 4096, [(Q4_K, 20000), (Q6_K, 9000)]
+    print(f"[gemv_multi_cap] cols={cols} mats={mats}", flush=True)
+    wds = []
+    for i, (t, r) in enumerate(mats):
+        b = hip.alloc(r * cols // 256 * (144 if t == Q4_K else 210))
+        hip.synth_fill(t, b, r * cols // 256, 700 + i)
+        wds.append(b)
+    xd = hip.alloc(cols * 4)
+    hip.synth_normal(xd, cols, 77)
+    for dp4a in (False, True):
+        ys = [hip.alloc(r * 4) for _, r in mats]
+        hip.matvec_multi([t for t, _ in mats], wds, [r for _, r in mats], cols, xd, ys, dp4a=dp4a)
+        for (t, r), wd, y in zip(mats, wds, ys):
+            one = hip.alloc(r * 4)
+            (hip.matvec_dp4a if dp4a else hip.matvec)(t, wd, r, cols, xd, one)
+            assert np.array_equal(y.download(np.uint32), one.download(np.uint32))
+
+
+def test_gemv_multi_rejects_bad_arguments(hip):
+    from katali_hip import HipError
+    w, x, y = hip.alloc(144 * 8), hip.alloc(1024 * 4), hip.alloc(64)
+    for types, n in (([Q4_K] * 5, 5), ([13], 1)):
+        with pytest.raises(HipError) as e:
+            hip.matvec_multi(types, [w] * n, [1] * n, 256, x, [y] * n)
+        assert e.value.rc == (-1 if n == 5 else -4)
+    with pytest.raises(HipError) as e:
+        hip.matvec_multi([Q4_K, Q6_K], [w, w], [1, 1], 1000, x, [y, y])   # cols not a multiple of 256
+    assert e.value.rc == -1
+    assert hip.lib.katali_hip_matvec_multi(0, None, None, None, 256, x.ptr, None) == -1

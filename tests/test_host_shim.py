@@ -79,8 +79,10 @@ def test_shim_matvec_on_gpu(oracle):
     ws = [S.matrix(rng, t, r, cols) for t, r in mats]
     x = S.activation(rng, cols)
     n0 = lib.katali_dense_hip_cached()
+    singles = []
     for (t, r), w in zip(mats, ws):
         y = np.empty(r, np.float32)
+        singles.append(y)
         for _ in range(2):   # second call reuses the cached device copy
             assert lib.katali_dense_hip_matvec(t, w.ctypes.data, w.nbytes, r, cols, x.ctypes.data, y.ctypes.data) == 0
         want = oracle.matvec_f32x(t, w, r, cols, x, 1)
@@ -93,9 +95,10 @@ def test_shim_matvec_on_gpu(oracle):
     rows = (C.c_uint64 * 3)(*[r for _, r in mats])
     outs = (C.c_void_p * 3)(*[y.ctypes.data for y in ys])
     assert lib.katali_dense_hip_matvec_multi(3, types, ptrs, sizes, rows, cols, x.ctypes.data, outs) == 0
-    for (t, r), w, y in zip(mats, ws, ys):
+    for (t, r), w, y, y1 in zip(mats, ws, ys, singles):
         want = oracle.matvec_f32x(t, w, r, cols, x, 1)
         assert np.all(np.abs(y - want) <= 1e-4 + 1e-3 * np.abs(want))
+        assert np.array_equal(y.view(np.uint32), y1.view(np.uint32))   # one launch, same bits
     assert lib.katali_dense_hip_cached() == n0 + len(mats)
     lib.katali_dense_hip_shutdown()
     assert lib.katali_dense_hip_cached() == 0
