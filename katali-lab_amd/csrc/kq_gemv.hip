@@ -217,11 +217,31 @@ __device__ __forceinline__ void gemv_rows(const uint8_t *__restrict__ w, uint32_
                 acc[r] = v;
             }
         }
+        if (log2s == 6) {
+            // one row per wave instruction: the RPS rows reduce together
+            // (halving exchanges, no LDS); lane groups of 64 / RPS then hold
+            // row (lane >> SH) & (RPS - 1)
+            constexpr int LOGR = RPS >= 4 ? 2 : (RPS >= 2 ? 1 : 0);
+            constexpr int SH = 6 - LOGR;
+            const float v = reduce_rows<RPS>(acc);
+            const uint32_t r = (lane >> SH) & (RPS - 1);
+            const uint32_t row = row_of(base, (int)r);
+            if ((lane & ((1u << SH) - 1)) == 0 && row < rows) y[row] = v;
+        } else {
 #pragma unroll
-        for (int r = 0; r < RPS; r++) {
-            const float v = wave_sum_xor(acc[r], (int)S);
-            const uint32_t row = row_of(base, r);
-            if (s == 0 && row < rows) y[row] = v;
+            for (int r = 0; r < RPS; r++) {
+                float v;
+                switch (log2s) {   // uniform: the lanes of a row slot sum on the VALU
+                    case 5: v = group_sum<32>(acc[r]); break;
+                    case 4: v = group_sum<16>(acc[r]); break;
+                    case 3: v = group_sum<8>(acc[r]); break;
+                    case 2: v = group_sum<4>(acc[r]); break;
+                    case 1: v = group_sum<2>(acc[r]); break;
+                    default: v = acc[r]; break;
+                }
+                const uint32_t row = row_of(base, r);
+                if (s == 0 && row < rows) y[row] = v;
+            }
         }
     }
 }

@@ -198,71 +198,6 @@ __device__ __forceinline__ void route_publish(const MoeArgs &a, int32_t id, floa
     if (__ballot(bad) != 0 && lane == 0) atomicOr(a.err, 2);
 }
 
-// Sum R per-lane values over the 64 lanes of a wave for R rows at once: each
-// halving step sends the half of the rows the partner keeps, then the
-// remaining offsets finish a plain butterfly. Partners differ in lane bit 5
-// (v_permlane32_swap), bit 4 (v_permlane16_swap), then inside 16-lane rows
-// by DPP: lane ^ 15, lane ^ 7, lane ^ 2, lane ^ 1 (these masks span the low
-// 4 bits, so every lane's value is counted once). Afterwards every lane holds
-// the full sum of row (lane >> (6 - log2 R)) & (R - 1).
-//
-// v_permlane32_swap(X, Y) gives r0 = {X[0..31], Y[0..31]} and
-// r1 = {X[32..63], Y[32..63]} (lane halves), so r0 + r1 is X[l] + X[l+32] in
-// the lower half and Y[l-32] + Y[l] in the upper half; v_permlane16_swap does
-// the same for odd/even 16-lane rows.
-template <int OFF>
-__device__ __forceinline__ float swap_sum(float x, float y) {
-    static_assert(OFF == 32 || OFF == 16, "swap_sum crosses 32 or 16 lanes");
-    if constexpr (OFF == 32) {
-        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
-        return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    } else {
-        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false, false);
-        return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    }
-}
-template <int OFF>
-__device__ __forceinline__ float row_partner(float v) {   // OFF in {8, 4, 2, 1}
-    if constexpr (OFF == 8) return dpp_f<DPP_MIRROR>(v);
-    else if constexpr (OFF == 4) return dpp_f<DPP_HALF_MIRROR>(v);
-    else if constexpr (OFF == 2) return dpp_f<DPP_XOR2>(v);
-    else return dpp_f<DPP_XOR1>(v);
-}
-template <int N, int OFF, int R>
-__device__ __forceinline__ void reduce_halve(float (&acc)[R], int lane) {
-    if constexpr (N > 1) {
-        constexpr int HALF = N / 2;
-        if constexpr (OFF >= 16) {
-#pragma unroll
-            for (int i = 0; i < HALF; i++) acc[i] = swap_sum<OFF>(acc[i], acc[i + HALF]);
-        } else {
-            const bool upper = lane & OFF;
-#pragma unroll
-            for (int i = 0; i < HALF; i++) {
-                const float send = upper ? acc[i] : acc[i + HALF];
-                const float keep = upper ? acc[i + HALF] : acc[i];
-                acc[i] = keep + row_partner<OFF>(send);
-            }
-        }
-        reduce_halve<HALF, OFF / 2, R>(acc, lane);
-    }
-}
-template <int OFF>
-__device__ __forceinline__ float butterfly_from(float v) {
-    if constexpr (OFF >= 16) v = swap_sum<OFF>(v, v);
-    else if constexpr (OFF >= 1) v += row_partner<OFF>(v);
-    if constexpr (OFF > 1) return butterfly_from<OFF / 2>(v);
-    else return v;
-}
-template <int R>
-__device__ __forceinline__ float reduce_rows(float (&acc)[R]) {
-    const int lane = threadIdx.x & 63;
-    reduce_halve<R, 32, R>(acc, lane);
-    constexpr int LOG = R >= 16 ? 4 : (R >= 8 ? 3 : (R >= 4 ? 2 : (R >= 2 ? 1 : 0)));
-    if constexpr (LOG < 6) return butterfly_from<(32 >> LOG)>(acc[0]);
-    else return acc[0];
-}
-
 // ---------------------------------------------------------------------------
 // Kernel A: 64 Q4_K rows (32 gate + 32 up) per workgroup, NB blocks per row.
 // Sixteen waves; wave w owns rows 4w..4w+3 (waves 0-7 gate, 8-15 up; eight
