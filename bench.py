@@ -6,12 +6,14 @@ Workloads:
   moe48     (default) one decode token through 48 fused MoE layers,
 hidden 2048, 128 experts, top-8, gate/up 2048->768 Q4_K, down 768->2048 Q6_K,
 random weights (independent seed per layer), N(0,1) activations and router
-logits. Every token draws new router logits (a ring of 64 steps), so each token
-touches a different 1.17 GB of the 18.8 GB expert pool: a cold working set far
-beyond L2 and the 256 MB MALL. The 48 layers and a step advance are captured
-in one hipGraph per token; a step is one replay.
+logits. Every token draws new router logits (a ring of 64 positions), so each
+token touches a different 1.17 GB of the 18.8 GB expert pool: a cold working
+set far beyond L2 and the 256 MB MALL. Each ring position's 48 layers are
+captured in one hipGraph, reading that position's logits from fixed addresses
+(as a decode loop reads its router's output buffer); a step is one token, one
+replay, and consecutive steps replay consecutive positions.
   moe40cold 40 MoE layers x 256 experts, gate/up 2048->512 Q4_K, down 512->2048
-            Q6_K, top-8 plus an always-on shared expert, 64-step logit ring.
+            Q6_K, top-8 plus an always-on shared expert, 64-position logit ring.
   gemv6144  dense Q4_K 6144x2048 GEMV, batch 1, fp32 x quantized to q8_1
             inside the kernel; 144 distinct weight copies (1.02 GB) are cycled
             so every GEMV reads cold weights; a step is one pass over them.
@@ -101,15 +103,20 @@ def bench_moe(hip, name, steps, warmup, ring=64):
     x = hip.alloc(L * hidden * 4)
     hip.synth_normal(x, L * hidden, 77)
     y = hip.alloc(L * hidden * 4)
+    # router logits of ring position t, layer l at (t * L + l) * n_expert: each
+    # token reads its own logits from a fixed address, as a decode loop reads
+    # the router's output buffer
     logits = hip.alloc(ring * L * n_expert * 4)
     hip.synth_normal(logits, ring * L * n_expert, 78)
-    step = hip.to_device(np.zeros(1, np.int32))
-    descs, routes = [], []
-    for li, (g, u, d, sh) in enumerate(layers):
-        descs.append(hip.moe_desc(hidden, ffn, n_expert, g, u, d, shared=sh))
-        r = hip.moe_route(n_sel, step=step, logits_stride=L * n_expert)
-        r.logits = logits.ptr + li * n_expert * 4
-        routes.append(r)
+    descs = [hip.moe_desc(hidden, ffn, n_expert, g, u, d, shared=sh) for (g, u, d, sh) in layers]
+    routes = []
+    for t in range(ring):
+        rt = []
+        for li in range(L):
+            r = hip.moe_route(n_sel)
+            r.logits = logits.ptr + (t * L + li) * n_expert * 4
+            rt.append(r)
+        routes.append(rt)
 
     class View:  # a device pointer inside a larger buffer
         def __init__(self, ptr):
@@ -118,28 +125,28 @@ def bench_moe(hip, name, steps, warmup, ring=64):
     xs = [View(x.ptr + li * hidden * 4) for li in range(L)]
     ys = [View(y.ptr + li * hidden * 4) for li in range(L)]
 
-    def token():
+    def token(t):
         for li in range(L):
-            hip.moe_layer(descs[li], routes[li], ys[li], x=xs[li])
+            hip.moe_layer(descs[li], routes[t][li], ys[li], x=xs[li])
 
-    # eager pass sizes the scratch, then capture one token
-    token()
-    hip.step_advance(step, ring)
+    # eager pass sizes the scratch, then one graph per ring position
+    token(0)
     hip.sync()
-    hip.graph_begin()
-    token()
-    hip.step_advance(step, ring)
-    graph = hip.graph_end()
+    graphs = []
+    for t in range(ring):
+        hip.graph_begin()
+        token(t)
+        graphs.append(hip.graph_end())
 
-    for _ in range(warmup):
-        hip.graph_launch(graph)
+    for i in range(warmup):
+        hip.graph_launch(graphs[i % ring])
     hip.sync()
     e0, e1 = hip.event(), hip.event()
     hip.sync()
     t0 = time.perf_counter()
     hip.record(e0)
-    for _ in range(steps):
-        hip.graph_launch(graph)
+    for i in range(steps):
+        hip.graph_launch(graphs[(warmup + i) % ring])
     hip.record(e1)
     ms = hip.elapsed_ms(e0, e1)
     wall = time.perf_counter() - t0
@@ -148,17 +155,17 @@ def bench_moe(hip, name, steps, warmup, ring=64):
     # per-launch kernel time: an event pair around each layer, eager
     ev = [hip.event() for _ in range(2 * L)]
     per = []
-    for _ in range(3):
+    for t in range(3):
         for li in range(L):
             hip.record(ev[2 * li])
-            hip.moe_layer(descs[li], routes[li], ys[li], x=xs[li])
+            hip.moe_layer(descs[li], routes[t][li], ys[li], x=xs[li])
             hip.record(ev[2 * li + 1])
-        hip.step_advance(step, ring)
         hip.sync()
         per += [hip.elapsed_ms(ev[2 * li], ev[2 * li + 1]) for li in range(L)]
     for e in ev + [e0, e1]:
         hip.event_destroy(e)
-    hip.graph_destroy(graph)
+    for gr in graphs:
+        hip.graph_destroy(gr)
 
     layer_bytes, weight_bytes = moe_bytes_per_layer(hidden, ffn, n_sel, shared)
     tok_bytes = L * layer_bytes
@@ -705,7 +712,7 @@ def main():
             "workload": f"{args.workload}: {L}-layer MoE decode, 1 token, hidden {hidden}, {n_expert} experts, "
                         f"top-{n_sel}{' + shared expert' if shared else ''}, gate/up {hidden}->{ffn} Q4_K, "
                         f"down {ffn}->{hidden} Q6_K, fp32 x quantized to q8_1 in the layer, new routing every "
-                        f"token from a 64-step logit ring, hipGraph per token",
+                        f"token from a 64-position logit ring (fixed logits addresses per position), hipGraph per token",
             "layers": L, "hidden": hidden, "ffn": ffn, "n_expert": n_expert, "n_sel": n_sel,
             "shared_expert": shared, "expert_pool_gb": round(res["pool_gb"], 2),
             "bytes_per_token": res["bytes_per_token"], "parallelism": "single GPU",
