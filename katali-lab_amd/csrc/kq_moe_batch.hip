@@ -5,7 +5,7 @@
 //
 // 1. x_t -> q8_1 (one quantize launch over all tokens).
 // 2. k_mb_group (one workgroup): the T*S (token, slot) pairs, S = n_sel +
-//    shared, are sorted by expert (stable in pair order). An expert that
+//    shared, are grouped by expert (counting sort). An expert that
 //    gathers at least min_big pairs goes to the grouped-GEMM list (in entries
 //    of at most 64 pairs), every other expert to the small list (entries of
 //    at most 8 pairs).
@@ -35,35 +35,39 @@ constexpr uint32_t MB_MAX_E = 513;   // routed experts + the shared expert's vir
 // meta layout (int32): [0] small entries, [1] grouped-GEMM entries, [2]
 // error bits, [16 ..) small entries (3 ints each: expert, first, count <= 8;
 // at most P), then grouped-GEMM entries (3 ints each: count <= 64; at most
-// P), then order (the P pairs sorted by expert, stable in pair order); an
-// entry's pairs are order[first .. first + count).
+// P), then order (the P pairs grouped by expert, experts ascending; the order
+// inside one expert's run is arbitrary); an entry's pairs are
+// order[first .. first + count).
 constexpr uint32_t MB_GRP = 8;   // pairs per small entry (the grouped GEMV kernels' GRP_MAX)
 __host__ __device__ inline uint32_t mb_small_off() { return 16; }
 __host__ __device__ inline uint32_t mb_big_off(uint32_t P) { return 16 + 3 * P; }
 __host__ __device__ inline uint32_t mb_order_off(uint32_t P) { return 16 + 6 * P; }
 uint64_t moe_batch_meta_words(uint32_t P) { return mb_order_off(P) + P; }
 
-// Inclusive prefix sum over the 64 lanes of a wave.
+// Inclusive prefix sum over the 64 lanes of a wave on the VALU: row_shr 1, 2,
+// 4, 8 inside each 16-lane row (lanes without a source add 0), then
+// row_bcast:15 adds row 0's total to row 1 and row 2's to row 3, and
+// row_bcast:31 adds lane 31's running total to rows 2 and 3.
 __device__ __forceinline__ int wave_incl_scan(int v) {
-    const int lane = (int)(threadIdx.x & 63);
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int t = __shfl_up(v, (unsigned)o, 64);
-        if (lane >= o) v += t;
-    }
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);
     return v;
 }
 
 __global__ void __launch_bounds__(1024) k_mb_group(const int32_t *__restrict__ ids, uint32_t T, uint32_t n_sel,
                                                    uint32_t S, uint32_t n_expert, uint32_t min_big,
                                                    int32_t *__restrict__ meta, int32_t *__restrict__ err) {
-    __shared__ int32_t cnt[MB_MAX_E], off_all[MB_MAX_E], small_idx[MB_MAX_E], big_idx[MB_MAX_E];
+    __shared__ int32_t cnt[MB_MAX_E], off_all[MB_MAX_E], small_idx[MB_MAX_E], big_idx[MB_MAX_E], cur[MB_MAX_E];
     __shared__ int32_t exp_of[MB_MAX_P];
     __shared__ int32_t wsum[3][16];
     __shared__ int32_t bad;
     const uint32_t P = T * S, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t NE = n_expert + 1;   // id n_expert = the shared expert
-    for (uint32_t e = tid; e < NE; e += blockDim.x) cnt[e] = 0;
+    for (uint32_t e = tid; e < NE; e += blockDim.x) cnt[e] = cur[e] = 0;
     if (tid == 0) bad = 0;
     __syncthreads();
     for (uint32_t p = tid; p < P; p += blockDim.x) {
@@ -114,11 +118,12 @@ __global__ void __launch_bounds__(1024) k_mb_group(const int32_t *__restrict__ i
     }
     __syncthreads();
     int32_t *small = meta + mb_small_off(), *bigl = meta + mb_big_off(P), *order = meta + mb_order_off(P);
+    // a pair's place among its expert's pairs comes from an LDS cursor: the
+    // order inside an expert's run may differ from call to call, which no
+    // result depends on (every pair's sums are formed on their own)
     for (uint32_t p = tid; p < P; p += blockDim.x) {
         const int32_t e = exp_of[p];
-        int32_t rank = 0;
-        for (uint32_t q = 0; q < p; q++) rank += exp_of[q] == e;
-        order[off_all[e] + rank] = (int32_t)p;
+        order[off_all[e] + atomicAdd(&cur[e], 1)] = (int32_t)p;
     }
     for (uint32_t e = tid; e < NE; e += blockDim.x) {
         const int32_t c = cnt[e];
