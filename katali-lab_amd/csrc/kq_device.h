@@ -168,6 +168,15 @@ __device__ __forceinline__ float reduce_rows(float (&acc)[R]) {
     else return acc[0];
 }
 
+// LDS writes of this wave become visible to its own other lanes (a
+// wavefront-scope release/acquire pair around a wave barrier; no workgroup
+// barrier)
+__device__ __forceinline__ void wave_sync_lds() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // sum over aligned groups of W lanes (W a power of 2 up to 64), all lanes get
 // it: DPP inside 16-lane rows, then v_permlane16_swap / v_permlane32_swap
 // across rows (each partner pair adds the same two values, so every lane of

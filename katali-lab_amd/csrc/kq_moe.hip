@@ -250,12 +250,6 @@ __device__ __forceinline__ int sum32(int v) {
     return (int)r[0] + (int)r[1];
 }
 
-__device__ __forceinline__ void wave_sync_lds() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // the activation side of one lane item (constant over rows)
 struct XSlice {
     int4 xl, xh;

@@ -7,7 +7,7 @@
 // 2. k_mb_group (one workgroup): the T*S (token, slot) pairs, S = n_sel +
 //    shared, are grouped by expert (counting sort). An expert that
 //    gathers at least min_big pairs goes to the grouped-GEMM list (in entries
-//    of at most 64 pairs), every other expert to the small list (entries of
+//    of at most 16 pairs), every other expert to the small list (entries of
 //    at most 8 pairs).
 // 3. Small list: the grouped v_dot4 GEMV kernels k_moe_gu_grp and
 //    k_moe_down_grp (kq_moe.hip): one read of a weight tile per entry,
@@ -27,6 +27,15 @@ namespace kq {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
+// f(integral_constant<int, I>) for I = B .. E-1, unrolled at compile time
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
 constexpr uint32_t MB_MAX_T = 64;
 constexpr uint32_t MB_MAX_S = 17;
 constexpr uint32_t MB_MAX_P = MB_MAX_T * MB_MAX_S;
@@ -34,11 +43,13 @@ constexpr uint32_t MB_MAX_E = 513;   // routed experts + the shared expert's vir
 
 // meta layout (int32): [0] small entries, [1] grouped-GEMM entries, [2]
 // error bits, [16 ..) small entries (3 ints each: expert, first, count <= 8;
-// at most P), then grouped-GEMM entries (3 ints each: count <= 64; at most
-// P), then order (the P pairs grouped by expert, experts ascending; the order
+// at most P), then grouped-GEMM entries (3 ints each: count <= 16; at most
+// P; an expert's entries are consecutive), then order (the P pairs grouped by expert, experts ascending; the order
 // inside one expert's run is arbitrary); an entry's pairs are
 // order[first .. first + count).
 constexpr uint32_t MB_GRP = 8;   // pairs per small entry (the grouped GEMV kernels' GRP_MAX)
+constexpr uint32_t MB_BIG = 16;  // pairs per grouped-GEMM entry (the MFMA's 16 B columns)
+constexpr uint32_t MB_DN_CHUNK = 8;   // h blocks staged at once by the down kernel beyond 3 blocks
 __host__ __device__ inline uint32_t mb_small_off() { return 16; }
 __host__ __device__ inline uint32_t mb_big_off(uint32_t P) { return 16 + 3 * P; }
 __host__ __device__ inline uint32_t mb_order_off(uint32_t P) { return 16 + 6 * P; }
@@ -90,7 +101,7 @@ __global__ void __launch_bounds__(1024) k_mb_group(const int32_t *__restrict__ i
     {
         const int c = tid < NE ? cnt[tid] : 0;
         const bool big = c >= (int)min_big && c > 0;
-        const int va = c, vs = big ? 0 : (c + (int)MB_GRP - 1) / (int)MB_GRP, vb = big ? (c + 63) / 64 : 0;
+        const int va = c, vs = big ? 0 : (c + (int)MB_GRP - 1) / (int)MB_GRP, vb = big ? (c + (int)MB_BIG - 1) / (int)MB_BIG : 0;
         const int ia = wave_incl_scan(va), is = wave_incl_scan(vs), ib = wave_incl_scan(vb);
         if (lane == 63) {
             wsum[0][wave] = ia;
@@ -128,11 +139,11 @@ __global__ void __launch_bounds__(1024) k_mb_group(const int32_t *__restrict__ i
     for (uint32_t e = tid; e < NE; e += blockDim.x) {
         const int32_t c = cnt[e];
         if (big_idx[e] >= 0) {
-            for (int32_t k = 0; 64 * k < c; k++) {
+            for (int32_t k = 0; (int32_t)MB_BIG * k < c; k++) {
                 const int32_t i = big_idx[e] + k;
                 bigl[3 * i + 0] = (int32_t)e;
-                bigl[3 * i + 1] = off_all[e] + 64 * k;
-                bigl[3 * i + 2] = min(64, c - 64 * k);
+                bigl[3 * i + 1] = off_all[e] + (int32_t)MB_BIG * k;
+                bigl[3 * i + 2] = min((int32_t)MB_BIG, c - (int32_t)MB_BIG * k);
             }
         } else if (small_idx[e] >= 0) {
             for (int32_t k = 0; (int32_t)MB_GRP * k < c; k++) {
@@ -167,12 +178,10 @@ __device__ __forceinline__ MbX mbx_carve(uint8_t *base) {
     return x;
 }
 constexpr uint32_t MBX_BYTES = 16 * MBX_ROW + 2 * 16 * 8 * 4;
-constexpr uint32_t MB_CG = 4;   // column groups of 16 pairs per grouped-GEMM entry (<= 64 pairs)
 
 // Staging split (16 pairs per workgroup): thread t takes local pair t / 16,
 // q8_1 block 8b + (t / 2) % 8 of that pair's row and half t % 2 of its
-// values. The loads go to registers first, so block b+1 is in flight while
-// block b is multiplied.
+// values.
 struct XPart {
     uint4 q;
     uint32_t h;
@@ -286,188 +295,219 @@ struct MbW<Q6K> {
 };
 
 // ---------------------------------------------------------------------------
-// Gate/up for one grouped expert: 32 gate + 32 up rows (jb) x one column
-// group of 16 of its pairs (a workgroup per group keeps the fp32 scale
-// epilogue, which costs more than the MFMAs, spread over the chip; the
-// groups of one row tile are a multiple of 8 workgroups apart, so they share
-// an XCD and its L2 copy of the weights)
+// Gate/up of the grouped-GEMM entries: a tile is 32 gate + 32 up rows (jb) x
+// one entry's <= 16 pairs, workgroup t = entry * nblk + jb, so the tiles of
+// the entries the grouping made come first and the workgroups past them
+// (the grid covers the worst-case entry count) leave after one scalar load.
+// The entries of one expert are consecutive, so the tiles that share a
+// weight tile are nblk workgroups apart: with nblk a multiple of 8 they run
+// on one XCD and share its L2 copy of the weights. Per tile: the entry,
+// then its pair list with every weight load behind it, then the pairs'
+// activation blocks, each loaded two blocks ahead of its multiplication (a
+// ring of three in registers, two LDS buffers).
 // ---------------------------------------------------------------------------
 template <int NB>
 __global__ void __launch_bounds__(256) k_mb_gu_mfma(MoeArgs a, const int32_t *__restrict__ meta, uint32_t P) {
     extern __shared__ __align__(16) uint8_t lds[];
-    const uint32_t nblk = a.ffn / 32, g0 = gridDim.x / MB_CG;
-    const uint32_t cg = blockIdx.x / g0, bi = (blockIdx.x % g0) / nblk, jb = blockIdx.x % nblk;
-    if (bi >= (uint32_t)meta[1]) return;   // whole workgroup, before any barrier
-    const int32_t *big = meta + mb_big_off(P) + 3 * bi;
-    const int32_t e = big[0];
-    if (big[2] <= (int32_t)(16 * cg)) return;
-    const uint32_t cnt = min(16u, (uint32_t)big[2] - 16 * cg);
-    const int32_t *pairs = meta + mb_order_off(P) + big[1] + 16 * cg;
+    const uint32_t nblk = a.ffn / 32;
+    const uint32_t ntiles = (uint32_t)meta[1] * nblk;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint64_t rb = NB * 144;
-    const bool shared = (uint32_t)e == a.n_expert;
-    const uint8_t *gb = shared ? a.gate_sh : a.gate + (uint64_t)e * a.ffn * rb;
-    const uint8_t *ub = shared ? a.up_sh : a.up + (uint64_t)e * a.ffn * rb;
-    // wave w: rows 16w..16w+15 of the 64 (waves 0-1 gate, 2-3 up)
-    const uint8_t *wbase = wave < 2 ? gb + (uint64_t)(32 * jb + 16 * wave) * rb : ub + (uint64_t)(32 * jb + 16 * (wave - 2)) * rb;
     const uint32_t arow = lane % 16, kc = lane / 16;   // A: row, k chunk
     const uint32_t dcol = lane % 16, drow0 = 4 * (lane / 16);   // D: pair column, first row
-    const uint8_t *ap = wbase + (uint64_t)arow * rb, *hp = wbase + (uint64_t)(lane >> 2) * rb;
-    // this thread's staging pair (clamped; pairs past cnt stage zeros)
-    const uint32_t si = tid >> 4;
-    const bool sval = si < cnt;
-    const uint32_t sp = (uint32_t)pairs[min(si, cnt - 1)];
-    const uint8_t *xrow = a.xq + (uint64_t)(sp / a.bS) * a.xq_stride;
-
-    const MbX x = mbx_carve(lds);
-    float2 *scl = (float2 *)(lds + MBX_BYTES) + 16 * 8 * wave;   // this wave's [16 rows][8 sub-blocks] {d*sc, dmin*m}
-    float *gu = (float *)(lds + MBX_BYTES + 4 * 16 * 8 * 8);        // [64 rows][16 pairs]
-    float acc[4];
+    const uint32_t si = tid >> 4;   // this thread's staging pair
+    constexpr bool UP = NB <= 8;   // every block's weights in registers at once
+    {
+        const uint32_t t = blockIdx.x;
+        if (t >= ntiles) return;   // whole workgroup, before any barrier
+        uint8_t *const lt = lds;
+        float2 *scl = (float2 *)(lt + 2 * MBX_BYTES) + 16 * 8 * wave;   // this wave's [16 rows][8 sub-blocks] {d*sc, dmin*m}
+        float *gu = (float *)(lt + 2 * MBX_BYTES + 4 * 16 * 8 * 8);      // [64 rows][16 pairs]
+        const uint32_t bi = t / nblk, jb = t % nblk;
+        const int32_t *big = meta + mb_big_off(P) + 3 * bi;
+        const int32_t e = big[0];
+        const uint32_t cnt = (uint32_t)big[2];
+        const int32_t *pairs = meta + mb_order_off(P) + big[1];
+        const bool shared = (uint32_t)e == a.n_expert;
+        const uint8_t *gb = shared ? a.gate_sh : a.gate + (uint64_t)e * a.ffn * rb;
+        const uint8_t *ub = shared ? a.up_sh : a.up + (uint64_t)e * a.ffn * rb;
+        // wave w: rows 16w..16w+15 of the 64 (waves 0-1 gate, 2-3 up)
+        const uint8_t *wbase = wave < 2 ? gb + (uint64_t)(32 * jb + 16 * wave) * rb
+                                        : ub + (uint64_t)(32 * jb + 16 * (wave - 2)) * rb;
+        const uint8_t *ap = wbase + (uint64_t)arow * rb, *hp = wbase + (uint64_t)(lane >> 2) * rb;
+        // the pair (clamped; pairs past cnt stage zeros), then the weights:
+        // waiting for the pair waits for nothing else
+        const uint32_t sp = (uint32_t)pairs[min(si, cnt - 1)];
+        MbW<Q4K> w[UP ? NB : 1];
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < 4; i++) acc[i] = 0.0f;
-
-    // x block 0, then the weights: every block's at once when they fit in
-    // registers (NB <= 8), else one block ahead
-    constexpr bool UP = NB <= 8;
-    XPart xv = mbx_load(xrow, 0);
-    MbW<Q4K> w[UP ? NB : 1];
+        for (int b = 0; b < (UP ? NB : 1); b++) w[b].load(ap + b * 144, hp + b * 144, kc);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        // activation blocks two ahead of the one being multiplied (a ring of
+        // three in registers), each staged into its own LDS buffer
+        const uint8_t *xrow = a.xq + (uint64_t)(sp / a.bS) * a.xq_stride;
+        XPart xv[3];
+        xv[0] = mbx_load(xrow, 0);
+        xv[1] = mbx_load(xrow, NB > 1 ? 1 : 0);
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        static_for<0, NB>([&](auto bc) {   // unrolled: the register ring is indexed by constants
+            constexpr uint32_t b = decltype(bc)::value;
+            __builtin_amdgcn_sched_barrier(0);   // one block's operands live at a time
+            if constexpr (b % 2 == 0) __syncthreads();   // the buffers written next are free (previous tile / blocks b-2, b-1)
+            mbx_put(mbx_carve(lt + (b % 2) * MBX_BYTES), xv[b % 3], si < cnt);
+            xv[(b + 2) % 3] = mbx_load(xrow, b + 2 < (uint32_t)NB ? b + 2 : NB - 1);   // clamped, not skipped
+            if constexpr (!UP) w[0].load(ap + b * 144, hp + b * 144, kc);
+            __syncthreads();
+            const MbW<Q4K> &wc = w[UP ? b : 0];
+            const MbX x = mbx_carve(lt + (b % 2) * MBX_BYTES);
+            wc.put_scales(scl);   // wave-private table
+            wave_sync_lds();
 #pragma unroll
-    for (int b = 0; b < (UP ? NB : 1); b++) w[b].load(ap + b * 144, hp + b * 144, kc);
-#pragma unroll(UP ? NB : 1)
-    for (uint32_t b = 0; b < NB; b++) {
-        __syncthreads();   // the previous block's LDS is consumed
-        mbx_put(x, xv, sval);
-        const MbW<Q4K> wc = w[UP ? b : 0];
-        wc.put_scales(scl);
-        // block b+1's loads fly during block b's MFMAs (the last block loads
-        // itself again: clamped, not skipped)
-        const uint32_t bn = b + 1 < NB ? b + 1 : NB - 1;
-        xv = mbx_load(xrow, bn);
-        if constexpr (!UP) w[0].load(ap + bn * 144, hp + bn * 144, kc);
-        __syncthreads();
+            for (uint32_t j = 0; j < 8; j++) {
+                const long av = wc.a_op(j);
+                const v4i d = mfma16(av, mbx_b(x, arow, j, kc));
+                const float d8 = x.d8[8 * dcol + j], qs = (float)x.qs[8 * dcol + j];
 #pragma unroll
-        for (uint32_t j = 0; j < 8; j++) {
-            const long av = wc.a_op(j);
-            const v4i d = mfma16(av, mbx_b(x, arow, j, kc));
-            const float d8 = x.d8[8 * dcol + j], qs = (float)x.qs[8 * dcol + j];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float2 sc = scl[8 * (drow0 + i) + j];
-                acc[i] = fmaf(d8, fmaf(sc.x, (float)d[i], -(sc.y * qs)), acc[i]);
+                for (int i = 0; i < 4; i++) {
+                    const float2 sc = scl[8 * (drow0 + i) + j];
+                    acc[i] = fmaf(d8, fmaf(sc.x, (float)d[i], -(sc.y * qs)), acc[i]);
+                }
             }
-        }
-    }
-    // gate/up of (row, pair) -> LDS, then SiLU-GLU and one q8_1 block per pair
+            wave_sync_lds();   // the table is rewritten for the next block
+        });
+        // gate/up of (row, pair) -> LDS, then SiLU-GLU and one q8_1 block per pair
 #pragma unroll
-    for (int i = 0; i < 4; i++) gu[16 * (16 * wave + drow0 + i) + dcol] = acc[i];
-    __syncthreads();
-    if (tid < 16 * 8) {
-        const uint32_t i = tid / 8, part = tid % 8;
-        if (i < cnt) {   // whole 8-lane groups take this branch together
-            float4 h;
-            h.x = kq_silu_mul(gu[16 * (4 * part + 0) + i], gu[16 * (32 + 4 * part + 0) + i]);
-            h.y = kq_silu_mul(gu[16 * (4 * part + 1) + i], gu[16 * (32 + 4 * part + 1) + i]);
-            h.z = kq_silu_mul(gu[16 * (4 * part + 2) + i], gu[16 * (32 + 4 * part + 2) + i]);
-            h.w = kq_silu_mul(gu[16 * (4 * part + 3) + i], gu[16 * (32 + 4 * part + 3) + i]);
-            uint32_t d16, s16;
-            int lo, hi;
-            float dd;
-            const uint32_t qv = quant_q8_1_part(h, d16, s16, lo, hi, dd);
-            uint8_t *blk = a.hq8 + ((uint64_t)pairs[i] * nblk + jb) * 36;
-            *(uint32_t *)(blk + 4 + 4 * part) = qv;
-            if (part == 0) *(uint32_t *)blk = d16 | (s16 << 16);
+        for (int i = 0; i < 4; i++) gu[16 * (16 * wave + drow0 + i) + dcol] = acc[i];
+        __syncthreads();
+        if (tid < 16 * 8) {
+            const uint32_t i = tid / 8, part = tid % 8;
+            if (i < cnt) {   // whole 8-lane groups take this branch together
+                float4 h;
+                h.x = kq_silu_mul(gu[16 * (4 * part + 0) + i], gu[16 * (32 + 4 * part + 0) + i]);
+                h.y = kq_silu_mul(gu[16 * (4 * part + 1) + i], gu[16 * (32 + 4 * part + 1) + i]);
+                h.z = kq_silu_mul(gu[16 * (4 * part + 2) + i], gu[16 * (32 + 4 * part + 2) + i]);
+                h.w = kq_silu_mul(gu[16 * (4 * part + 3) + i], gu[16 * (32 + 4 * part + 3) + i]);
+                uint32_t d16, s16;
+                int lo, hi;
+                float dd;
+                const uint32_t qv = quant_q8_1_part(h, d16, s16, lo, hi, dd);
+                uint8_t *blk = a.hq8 + ((uint64_t)pairs[i] * nblk + jb) * 36;
+                *(uint32_t *)(blk + 4 + 4 * part) = qv;
+                if (part == 0) *(uint32_t *)blk = d16 | (s16 << 16);
+            }
         }
     }
 }
 
 // ---------------------------------------------------------------------------
-// Down for one grouped expert: 64 output rows x one column group of 16 of
-// its pairs -> yp
+// Down of the grouped-GEMM entries: a tile is 64 output rows (rt) x one
+// entry's <= 16 pairs -> yp, workgroup t = entry * ntile + rt as in the
+// gate/up kernel; the pairs' h rows staged once per tile.
 // ---------------------------------------------------------------------------
 template <class QD, int NBD>
 __global__ void __launch_bounds__(256) k_mb_down_mfma(MoeArgs a, const int32_t *__restrict__ meta, uint32_t P) {
     extern __shared__ __align__(16) uint8_t lds[];
-    const uint32_t ntile = (a.hidden + 63) / 64, g0 = gridDim.x / MB_CG;
-    const uint32_t cg = blockIdx.x / g0, bi = (blockIdx.x % g0) / ntile, rt = blockIdx.x % ntile;
-    if (bi >= (uint32_t)meta[1]) return;
-    const int32_t *big = meta + mb_big_off(P) + 3 * bi;
-    const int32_t e = big[0];
-    if (big[2] <= (int32_t)(16 * cg)) return;
-    const uint32_t cnt = min(16u, (uint32_t)big[2] - 16 * cg);
-    const int32_t *pairs = meta + mb_order_off(P) + big[1] + 16 * cg;
+    const uint32_t ntile = (a.hidden + 63) / 64;
+    const uint32_t ntiles = (uint32_t)meta[1] * ntile;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t nb = NBD > 0 ? (uint32_t)NBD : a.ffn / 256;
     const uint64_t rb = (uint64_t)nb * QD::BB;
-    const bool shared = (uint32_t)e == a.n_expert;
-    const uint8_t *db = shared ? a.down_sh : a.down + (uint64_t)e * a.hidden * rb;
-    const uint32_t row0 = 64 * rt + 16 * wave;   // this wave's 16 rows
     const uint32_t arow = lane % 16, kc = lane / 16;
     const uint32_t dcol = lane % 16, drow0 = 4 * (lane / 16);
-    // rows past hidden read the last row and are not written
-    const uint8_t *ap = db + (uint64_t)min(row0 + arow, a.hidden - 1) * rb;
-    const uint8_t *hp = db + (uint64_t)min(row0 + (lane >> 2), a.hidden - 1) * rb;
     const uint32_t si = tid >> 4;
-    const bool sval = si < cnt;
     const uint64_t hstride = (uint64_t)(a.ffn / 32) * 36;
-    const uint8_t *xrow = a.hq8 + (uint64_t)pairs[min(si, cnt - 1)] * hstride;
-
     using W = MbW<QD>;
     constexpr uint32_t NS = W::NS;
-    const MbX x = mbx_carve(lds);
-    float2 *scl = (float2 *)(lds + MBX_BYTES) + 16 * 16 * wave;   // [16 rows][NS] {scale, min}
-    float acc[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) acc[i] = 0.0f;
-
-    // as in the gate/up kernel: every block's weights at once for a
-    // compile-time block count (up to 3 blocks: more spills), else one block
-    // ahead
     constexpr bool UP = NBD > 0;
-    XPart xv = mbx_load(xrow, 0);
-    W w[UP ? NBD : 1];
+    // every block's weights and activations at once for a compile-time block
+    // count (up to 3 blocks: more spills); else one block at a time
+    {
+        const uint32_t t = blockIdx.x;
+        if (t >= ntiles) return;   // whole workgroup, before any barrier
+        uint8_t *const lt = lds;
+        float2 *scl = (float2 *)(lt + (UP ? nb : MB_DN_CHUNK) * MBX_BYTES) + 16 * 16 * wave;   // [16 rows][NS] {scale, min}
+        const uint32_t bi = t / ntile, rt = t % ntile;
+        const int32_t *big = meta + mb_big_off(P) + 3 * bi;
+        const int32_t e = big[0];
+        const uint32_t cnt = (uint32_t)big[2];
+        const int32_t *pairs = meta + mb_order_off(P) + big[1];
+        const bool shared = (uint32_t)e == a.n_expert;
+        const uint8_t *db = shared ? a.down_sh : a.down + (uint64_t)e * a.hidden * rb;
+        const uint32_t row0 = 64 * rt + 16 * wave;   // this wave's 16 rows
+        // rows past hidden read the last row and are not written
+        const uint8_t *ap = db + (uint64_t)min(row0 + arow, a.hidden - 1) * rb;
+        const uint8_t *hp = db + (uint64_t)min(row0 + (lane >> 2), a.hidden - 1) * rb;
+        const uint32_t sp = (uint32_t)pairs[min(si, cnt - 1)];
+        W w[UP ? NBD : 1];
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int b = 0; b < (UP ? NBD : 1); b++) w[b].load(ap + b * QD::BB, hp + b * QD::BB, kc);
+        for (int b = 0; b < (UP ? NBD : 1); b++) w[b].load(ap + b * QD::BB, hp + b * QD::BB, kc);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t *xrow = a.hq8 + (uint64_t)sp * hstride;
+        if constexpr (UP) {
+            XPart xv[NBD];
+#pragma unroll
+            for (int b = 0; b < NBD; b++) xv[b] = mbx_load(xrow, b);
+            __syncthreads();   // the previous tile is done with the LDS
+#pragma unroll
+            for (int b = 0; b < NBD; b++) mbx_put(mbx_carve(lt + b * MBX_BYTES), xv[b], si < cnt);
+            __syncthreads();
+        }
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll(UP ? NBD : 1)
-    for (uint32_t b = 0; b < nb; b++) {
-        __syncthreads();
-        mbx_put(x, xv, sval);
-        const W wc = w[UP ? b : 0];
-        wc.put_scales(scl);
-        const uint32_t bn = b + 1 < nb ? b + 1 : nb - 1;
-        xv = mbx_load(xrow, bn);
-        if constexpr (!UP) w[0].load(ap + bn * QD::BB, hp + bn * QD::BB, kc);
-        __syncthreads();
-#pragma unroll
-        for (uint32_t j = 0; j < 8; j++) {   // 32-value sub-blocks
-            const long av = wc.a_op(j);
-            const long bv = mbx_b(x, arow, j, kc);
-            const float d8 = x.d8[8 * dcol + j];
-            if constexpr (QD::TYPE == T_Q6_K) {
-                // two 16-value scale groups: A halves zeroed in turn
-                const long a_lo = kc < 2 ? av : 0, a_hi = kc < 2 ? 0 : av;
-                const v4i d1 = mfma16(a_lo, bv), d2 = mfma16(a_hi, bv);
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float s_lo = scl[NS * (drow0 + i) + 2 * j].x, s_hi = scl[NS * (drow0 + i) + 2 * j + 1].x;
-                    acc[i] = fmaf(d8, fmaf(s_lo, (float)d1[i], s_hi * (float)d2[i]), acc[i]);
+        for (uint32_t b = 0; b < nb; b++) {
+            if constexpr (!UP) {
+                // long rows: the h blocks go through LDS MB_DN_CHUNK at a time
+                if (b % MB_DN_CHUNK == 0) {
+                    const uint32_t n = min(MB_DN_CHUNK, nb - b);
+                    __syncthreads();   // the previous chunk (or tile) is done with the LDS
+                    for (uint32_t c = 0; c < n; c++)
+                        mbx_put(mbx_carve(lt + c * MBX_BYTES), mbx_load(xrow, b + c), si < cnt);
+                    __syncthreads();
                 }
-            } else {
-                const v4i d = mfma16(av, bv);
-                const float qs = (float)x.qs[8 * dcol + j];
+                w[0].load(ap + b * QD::BB, hp + b * QD::BB, kc);
+            }
+            const W &wc = w[UP ? b : 0];
+            const MbX x = mbx_carve(lt + (UP ? b : b % MB_DN_CHUNK) * MBX_BYTES);
+            wc.put_scales(scl);   // wave-private table
+            wave_sync_lds();
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float2 sc = scl[NS * (drow0 + i) + j];
-                    acc[i] = fmaf(d8, fmaf(sc.x, (float)d[i], -(sc.y * qs)), acc[i]);
+            for (uint32_t j = 0; j < 8; j++) {   // 32-value sub-blocks
+                const long av = wc.a_op(j);
+                const long bv = mbx_b(x, arow, j, kc);
+                const float d8 = x.d8[8 * dcol + j];
+                if constexpr (QD::TYPE == T_Q6_K) {
+                    // two 16-value scale groups: A halves zeroed in turn
+                    const long a_lo = kc < 2 ? av : 0, a_hi = kc < 2 ? 0 : av;
+                    const v4i d1 = mfma16(a_lo, bv), d2 = mfma16(a_hi, bv);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const float s_lo = scl[NS * (drow0 + i) + 2 * j].x, s_hi = scl[NS * (drow0 + i) + 2 * j + 1].x;
+                        acc[i] = fmaf(d8, fmaf(s_lo, (float)d1[i], s_hi * (float)d2[i]), acc[i]);
+                    }
+                } else {
+                    const v4i d = mfma16(av, bv);
+                    const float qs = (float)x.qs[8 * dcol + j];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const float2 sc = scl[NS * (drow0 + i) + j];
+                        acc[i] = fmaf(d8, fmaf(sc.x, (float)d[i], -(sc.y * qs)), acc[i]);
+                    }
                 }
             }
+            wave_sync_lds();   // the table is rewritten for the next block
         }
-    }
-    if (dcol < cnt) {
-        float *yrow = a.yp + (uint64_t)pairs[dcol] * a.hidden;
+        if (dcol < cnt) {
+            float *yrow = a.yp + (uint64_t)pairs[dcol] * a.hidden;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t row = row0 + drow0 + i;
-            if (row < a.hidden) yrow[row] = acc[i];
+            for (int i = 0; i < 4; i++) {
+                const uint32_t row = row0 + drow0 + i;
+                if (row < a.hidden) yrow[row] = acc[i];
+            }
         }
     }
 }
@@ -509,39 +549,60 @@ hipError_t launch_moe_batch(const MoeArgs &base, uint32_t T, uint32_t min_big, c
     const uint32_t ne = base.n_expert + 1;
     const uint32_t max_small = P / MB_GRP + (ne < P ? ne : P);
     if ((e = launch_moe_groups_gu(a, max_small, s)) != hipSuccess) return e;
-    // grouped entries: each holds 1..64 pairs of one expert with >= min_big
-    // pairs, so there are at most P / 64 + P / min_big + 1 of them
-    const uint32_t max_big = P / 64 + P / (min_big > 0 ? min_big : 1) + 1;
+    // grouped entries: each holds 1..16 pairs of one expert with >= min_big
+    // pairs, so there are at most P / 16 + P / min_big + 1 of them
+    const uint32_t max_big = P / MB_BIG + P / (min_big > 0 ? min_big : 1) + 1;
+    auto grid_for = [&](uint32_t tiles_per_entry) { return dim3(max_big * tiles_per_entry); };
     const uint32_t nblk = base.ffn / 32;
-    const uint32_t lds_gu = MBX_BYTES + 4 * 16 * 8 * 8 + 64 * 16 * 4;
-    switch (base.hidden / 256) {
-        case 1: hipLaunchKernelGGL(k_mb_gu_mfma<1>, dim3(MB_CG * max_big * nblk), dim3(256), lds_gu, s, a, meta, P); break;
-        case 2: hipLaunchKernelGGL(k_mb_gu_mfma<2>, dim3(MB_CG * max_big * nblk), dim3(256), lds_gu, s, a, meta, P); break;
-        case 4: hipLaunchKernelGGL(k_mb_gu_mfma<4>, dim3(MB_CG * max_big * nblk), dim3(256), lds_gu, s, a, meta, P); break;
-        case 8: hipLaunchKernelGGL(k_mb_gu_mfma<8>, dim3(MB_CG * max_big * nblk), dim3(256), lds_gu, s, a, meta, P); break;
-        case 16: hipLaunchKernelGGL(k_mb_gu_mfma<16>, dim3(MB_CG * max_big * nblk), dim3(256), lds_gu, s, a, meta, P); break;
+    const uint32_t nb_gu = base.hidden / 256;
+    const uint32_t lds_gu = 2 * MBX_BYTES + 4 * 16 * 8 * 8 + 64 * 16 * 4;
+    auto go_gu = [&](auto kern) -> hipError_t {
+        if (lds_gu > 64 * 1024) {
+            const hipError_t r = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     (int)lds_gu);
+            if (r != hipSuccess) return r;
+        }
+        hipLaunchKernelGGL(kern, grid_for(nblk), dim3(256), lds_gu, s, a, meta, P);
+        return hipGetLastError();
+    };
+    switch (nb_gu) {
+        case 1: e = go_gu(k_mb_gu_mfma<1>); break;
+        case 2: e = go_gu(k_mb_gu_mfma<2>); break;
+        case 4: e = go_gu(k_mb_gu_mfma<4>); break;
+        case 8: e = go_gu(k_mb_gu_mfma<8>); break;
+        case 16: e = go_gu(k_mb_gu_mfma<16>); break;
         default: return hipErrorInvalidValue;
     }
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (e != hipSuccess) return e;
     if ((e = launch_moe_groups_down(a, max_small, s)) != hipSuccess) return e;
     const uint32_t ntile = (base.hidden + 63) / 64;
-    const uint32_t lds_dn = MBX_BYTES + 4 * 16 * 16 * 8;
-    const dim3 gdn(MB_CG * max_big * ntile);
+    const uint32_t nb_dn = base.ffn / 256;
+    const uint32_t lds_dn = (nb_dn <= 3 ? nb_dn : MB_DN_CHUNK) * MBX_BYTES + 4 * 16 * 16 * 8;
+    auto go_dn = [&](auto kern) -> hipError_t {
+        if (lds_dn > 64 * 1024) {
+            const hipError_t r = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     (int)lds_dn);
+            if (r != hipSuccess) return r;
+        }
+        hipLaunchKernelGGL(kern, grid_for(ntile), dim3(256), lds_dn, s, a, meta, P);
+        return hipGetLastError();
+    };
     if (base.down_type == T_Q6_K) {
-        switch (base.ffn / 256) {
-            case 1: hipLaunchKernelGGL((k_mb_down_mfma<Q6K, 1>), gdn, dim3(256), lds_dn, s, a, meta, P); break;
-            case 2: hipLaunchKernelGGL((k_mb_down_mfma<Q6K, 2>), gdn, dim3(256), lds_dn, s, a, meta, P); break;
-            case 3: hipLaunchKernelGGL((k_mb_down_mfma<Q6K, 3>), gdn, dim3(256), lds_dn, s, a, meta, P); break;
-            default: hipLaunchKernelGGL((k_mb_down_mfma<Q6K, 0>), gdn, dim3(256), lds_dn, s, a, meta, P); break;
+        switch (nb_dn) {
+            case 1: e = go_dn(k_mb_down_mfma<Q6K, 1>); break;
+            case 2: e = go_dn(k_mb_down_mfma<Q6K, 2>); break;
+            case 3: e = go_dn(k_mb_down_mfma<Q6K, 3>); break;
+            default: e = go_dn(k_mb_down_mfma<Q6K, 0>); break;
         }
     } else {
-        switch (base.ffn / 256) {
-            case 1: hipLaunchKernelGGL((k_mb_down_mfma<Q4K, 1>), gdn, dim3(256), lds_dn, s, a, meta, P); break;
-            case 2: hipLaunchKernelGGL((k_mb_down_mfma<Q4K, 2>), gdn, dim3(256), lds_dn, s, a, meta, P); break;
-            case 3: hipLaunchKernelGGL((k_mb_down_mfma<Q4K, 3>), gdn, dim3(256), lds_dn, s, a, meta, P); break;
-            default: hipLaunchKernelGGL((k_mb_down_mfma<Q4K, 0>), gdn, dim3(256), lds_dn, s, a, meta, P); break;
+        switch (nb_dn) {
+            case 1: e = go_dn(k_mb_down_mfma<Q4K, 1>); break;
+            case 2: e = go_dn(k_mb_down_mfma<Q4K, 2>); break;
+            case 3: e = go_dn(k_mb_down_mfma<Q4K, 3>); break;
+            default: e = go_dn(k_mb_down_mfma<Q4K, 0>); break;
         }
     }
+    if (e != hipSuccess) return e;
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const uint64_t n = (uint64_t)T * base.hidden;
     hipLaunchKernelGGL(k_mb_combine, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, s, a.yp, base.wts, T,
