@@ -30,6 +30,10 @@ std::string g_status = "not probed";
 int g_device = 0;
 hipStream_t g_own_stream = nullptr;
 hipStream_t g_stream = nullptr;
+// the batched layer's second path (forked from g_stream and joined back
+// inside one call; default priority like every stream here)
+hipStream_t g_aux_stream = nullptr;
+hipEvent_t g_ev_fork = nullptr, g_ev_join = nullptr;
 bool g_capturing = false;
 
 // MoE scratch
@@ -83,7 +87,10 @@ int init_locked() {
         return KATALI_HIP_E_NODEVICE;
     }
     if ((e = hipSetDevice(g_device)) != hipSuccess ||
-        (e = hipStreamCreateWithFlags(&g_own_stream, hipStreamNonBlocking)) != hipSuccess) {
+        (e = hipStreamCreateWithFlags(&g_own_stream, hipStreamNonBlocking)) != hipSuccess ||
+        (e = hipStreamCreateWithFlags(&g_aux_stream, hipStreamNonBlocking)) != hipSuccess ||
+        (e = hipEventCreateWithFlags(&g_ev_fork, hipEventDisableTiming)) != hipSuccess ||
+        (e = hipEventCreateWithFlags(&g_ev_join, hipEventDisableTiming)) != hipSuccess) {
         g_status = std::string("device init: ") + hipGetErrorString(e);
         return KATALI_HIP_E_NODEVICE;
     }
@@ -299,7 +306,9 @@ int moe_batch_impl(const KataliHipMoe *m, const KataliHipMoeBatch *b, const floa
     a.err = g_err_dev;
     a.yp = g_byp;
     const uint32_t min_big = b->mfma_min_tokens ? b->mfma_min_tokens : 16;
-    return launched(kq::launch_moe_batch(a, T, min_big, x, y, g_bxq, g_bmeta, g_stream), "moe batch launch");
+    return launched(kq::launch_moe_batch(a, T, min_big, x, y, g_bxq, g_bmeta, g_stream, g_aux_stream, g_ev_fork,
+                                         g_ev_join),
+                    "moe batch launch");
 }
 
 }  // namespace

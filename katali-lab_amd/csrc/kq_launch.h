@@ -103,10 +103,12 @@ hipError_t launch_moe_groups_down(const MoeArgs &a, uint32_t max_entries, hipStr
 // ffn/32 q8_1 blocks, a.yp: [P][hidden], P = T * (n_sel + shared)). Experts
 // gathering >= min_big pairs use the int8 MFMA grouped GEMM, the rest the
 // per-pair GEMV kernels. xq: T rows of hidden/32 q8_1 blocks; meta:
-// moe_batch_meta_words(P) ints.
+// moe_batch_meta_words(P) ints. The two paths touch disjoint pairs and run
+// side by side: the MFMA kernels on `aux`, forked from `s` after the
+// grouping (event `fork`) and joined back before the combine (`join`).
 uint64_t moe_batch_meta_words(uint32_t P);
 hipError_t launch_moe_batch(const MoeArgs &a, uint32_t T, uint32_t min_big, const float *x, float *y, uint8_t *xq,
-                            int32_t *meta, hipStream_t s);
+                            int32_t *meta, hipStream_t s, hipStream_t aux, hipEvent_t fork, hipEvent_t join);
 uint64_t moe_route_words();
 
 }  // namespace kq

@@ -49,6 +49,7 @@ constexpr uint32_t MB_MAX_E = 513;   // routed experts + the shared expert's vir
 // order[first .. first + count).
 constexpr uint32_t MB_GRP = 8;   // pairs per small entry (the grouped GEMV kernels' GRP_MAX)
 constexpr uint32_t MB_BIG = 16;  // pairs per grouped-GEMM entry (the MFMA's 16 B columns)
+constexpr uint32_t MB_FORK_PAIRS = 96;   // batches from this many pairs run the two paths side by side
 constexpr uint32_t MB_DN_CHUNK = 8;   // h blocks staged at once by the down kernel beyond 3 blocks
 __host__ __device__ inline uint32_t mb_small_off() { return 16; }
 __host__ __device__ inline uint32_t mb_big_off(uint32_t P) { return 16 + 3 * P; }
@@ -528,7 +529,7 @@ __global__ void __launch_bounds__(256) k_mb_combine(const float *__restrict__ yp
 }
 
 hipError_t launch_moe_batch(const MoeArgs &base, uint32_t T, uint32_t min_big, const float *x, float *y, uint8_t *xq,
-                            int32_t *meta, hipStream_t s) {
+                            int32_t *meta, hipStream_t s, hipStream_t aux, hipEvent_t fork, hipEvent_t join) {
     const uint32_t S = (uint32_t)base.n_sel + (base.has_shared ? 1u : 0u);
     const uint32_t P = T * S;
     if (T == 0 || T > MB_MAX_T || S == 0 || S > MB_MAX_S || base.n_expert > MB_MAX_E - 1) return hipErrorInvalidValue;
@@ -548,7 +549,17 @@ hipError_t launch_moe_batch(const MoeArgs &base, uint32_t T, uint32_t min_big, c
     // small entries: at most P / 8 + one per expert (each has >= 1 pair)
     const uint32_t ne = base.n_expert + 1;
     const uint32_t max_small = P / MB_GRP + (ne < P ? ne : P);
+    // No expert can reach min_big pairs below min_big pairs in all: then the
+    // grouped-GEMM kernels are not launched. From MB_FORK_PAIRS pairs they
+    // run on the side stream, beside the small-entry kernels (a fork and a
+    // join cost ~3-4 us, more than the overlap gains on smaller batches).
+    const bool any_big = P >= min_big;
+    const bool side = any_big && P >= MB_FORK_PAIRS;
+    hipStream_t sb = side ? aux : s;
+    if (side && ((e = hipEventRecord(fork, s)) != hipSuccess || (e = hipStreamWaitEvent(aux, fork, 0)) != hipSuccess))
+        return e;
     if ((e = launch_moe_groups_gu(a, max_small, s)) != hipSuccess) return e;
+    if ((e = launch_moe_groups_down(a, max_small, s)) != hipSuccess) return e;
     // grouped entries: each holds 1..16 pairs of one expert with >= min_big
     // pairs, so there are at most P / 16 + P / min_big + 1 of them
     const uint32_t max_big = P / MB_BIG + P / (min_big > 0 ? min_big : 1) + 1;
@@ -557,12 +568,13 @@ hipError_t launch_moe_batch(const MoeArgs &base, uint32_t T, uint32_t min_big, c
     const uint32_t nb_gu = base.hidden / 256;
     const uint32_t lds_gu = 2 * MBX_BYTES + 4 * 16 * 8 * 8 + 64 * 16 * 4;
     auto go_gu = [&](auto kern) -> hipError_t {
+        if (!any_big) return hipSuccess;
         if (lds_gu > 64 * 1024) {
             const hipError_t r = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                      (int)lds_gu);
             if (r != hipSuccess) return r;
         }
-        hipLaunchKernelGGL(kern, grid_for(nblk), dim3(256), lds_gu, s, a, meta, P);
+        hipLaunchKernelGGL(kern, grid_for(nblk), dim3(256), lds_gu, sb, a, meta, P);
         return hipGetLastError();
     };
     switch (nb_gu) {
@@ -574,17 +586,17 @@ hipError_t launch_moe_batch(const MoeArgs &base, uint32_t T, uint32_t min_big, c
         default: return hipErrorInvalidValue;
     }
     if (e != hipSuccess) return e;
-    if ((e = launch_moe_groups_down(a, max_small, s)) != hipSuccess) return e;
     const uint32_t ntile = (base.hidden + 63) / 64;
     const uint32_t nb_dn = base.ffn / 256;
     const uint32_t lds_dn = (nb_dn <= 3 ? nb_dn : MB_DN_CHUNK) * MBX_BYTES + 4 * 16 * 16 * 8;
     auto go_dn = [&](auto kern) -> hipError_t {
+        if (!any_big) return hipSuccess;
         if (lds_dn > 64 * 1024) {
             const hipError_t r = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                      (int)lds_dn);
             if (r != hipSuccess) return r;
         }
-        hipLaunchKernelGGL(kern, grid_for(ntile), dim3(256), lds_dn, s, a, meta, P);
+        hipLaunchKernelGGL(kern, grid_for(ntile), dim3(256), lds_dn, sb, a, meta, P);
         return hipGetLastError();
     };
     if (base.down_type == T_Q6_K) {
@@ -604,6 +616,8 @@ hipError_t launch_moe_batch(const MoeArgs &base, uint32_t T, uint32_t min_big, c
     }
     if (e != hipSuccess) return e;
     if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (side && ((e = hipEventRecord(join, aux)) != hipSuccess || (e = hipStreamWaitEvent(s, join, 0)) != hipSuccess))
+        return e;
     const uint64_t n = (uint64_t)T * base.hidden;
     hipLaunchKernelGGL(k_mb_combine, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, s, a.yp, base.wts, T,
                        (uint32_t)base.n_sel, S, base.hidden, y);
