@@ -142,3 +142,38 @@ def test_moe_batch_rejects_bad_arguments(hip, built):
             hip.moe_batch(desc, T, 2, ids, w, x, y)
     with pytest.raises(HipError):
         hip.moe_batch(desc, 4, 17, ids, w, x, y)
+
+
+@pytest.mark.parametrize("T,thr", [(64, 0), (64, 1), (5, 0)], ids=["fork", "fork_all_mfma", "one_stream"])
+def test_moe_batch_graph_replays_match_eager(hip, oracle, built, T, thr):
+    """One batched layer captured in a graph (two stream branches from 96
+    pairs on) replays to the eager call's bits, with eager work between the
+    replays."""
+    case = CASES[0]
+    hidden, ffn, n_expert, n_sel = case[:4]
+    print(f"[moe-batch-graph] T={T} thr={thr}", flush=True)
+    desc = built(case)[0]
+    rng = np.random.default_rng(900 + T + thr)
+    ids, w = zipf_routes(rng, T, n_expert, n_sel)
+    x = rng.standard_normal((T, hidden)).astype(np.float32)
+    dids, dw, dx = hip.to_device(ids), hip.to_device(w), hip.to_device(x)
+    want, got = hip.alloc(T * hidden * 4), hip.alloc(T * hidden * 4)
+    hip.moe_batch(desc, T, n_sel, dids, dw, dx, want, mfma_min_tokens=thr)
+    hip.sync()
+    ref = want.download(np.uint32)
+    hip.graph_begin()
+    hip.moe_batch(desc, T, n_sel, dids, dw, dx, got, mfma_min_tokens=thr)
+    g = hip.graph_end()
+    other = hip.alloc(T * hidden * 4)
+    try:
+        for i in range(3):
+            hip.memset(got, 0, T * hidden * 4)
+            hip.graph_launch(g)
+            hip.sync()
+            assert np.array_equal(got.download(np.uint32), ref), i
+            # eager work between replays, on the same scratch
+            hip.moe_batch(desc, T, n_sel, dids, dw, dx, other, mfma_min_tokens=thr)
+            hip.sync()
+            assert np.array_equal(other.download(np.uint32), ref), i
+    finally:
+        hip.graph_destroy(g)
