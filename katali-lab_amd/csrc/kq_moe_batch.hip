@@ -3,12 +3,12 @@
 // y_t = sum_r w_{t,r} Down_e(q8(SiLU(Gate_e x_t) * Up_e x_t)), e = ids[t][r],
 // plus the shared expert (weight 1) when present, for T <= 64 tokens.
 //
-// 1. x_t -> q8_1 (one quantize launch over all tokens).
-// 2. k_mb_group (one workgroup): the T*S (token, slot) pairs, S = n_sel +
-//    shared, are grouped by expert (counting sort). An expert that
-//    gathers at least min_big pairs goes to the grouped-GEMM list (in entries
-//    of at most 16 pairs), every other expert to the small list (entries of
-//    at most 8 pairs).
+// 1. k_mb_group, one launch: its first workgroup groups the T*S (token,
+//    slot) pairs, S = n_sel + shared, by expert (counting sort) while the
+//    others quantize every x_t to q8_1. An expert that gathers at least
+//    min_big pairs goes to the grouped-GEMM list (in entries of at most 16
+//    pairs), every other expert to the small list (entries of at most 8
+//    pairs).
 // 3. Small list: the grouped v_dot4 GEMV kernels k_moe_gu_grp and
 //    k_moe_down_grp (kq_moe.hip): one read of a weight tile per entry,
 //    dotted with each pair's activation exactly as kernels A and B of the
@@ -70,9 +70,27 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
     return v;
 }
 
+// Workgroup 0 groups the pairs; workgroups 1.. quantize the T activation
+// rows to q8_1 meanwhile (k_quantize_q8_1's split: 8 lanes per 32-value
+// block, the same bits), so the two take one launch.
 __global__ void __launch_bounds__(1024) k_mb_group(const int32_t *__restrict__ ids, uint32_t T, uint32_t n_sel,
                                                    uint32_t S, uint32_t n_expert, uint32_t min_big,
-                                                   int32_t *__restrict__ meta, int32_t *__restrict__ err) {
+                                                   int32_t *__restrict__ meta, int32_t *__restrict__ err,
+                                                   const float *__restrict__ x, uint32_t nq, uint8_t *__restrict__ xq) {
+    if (blockIdx.x > 0) {   // whole workgroup
+        for (uint32_t t = (blockIdx.x - 1) * 1024 + threadIdx.x; t < nq; t += (gridDim.x - 1) * 1024) {
+            const uint32_t blk = t >> 3, part = t & 7;   // whole 8-lane groups (nq % 8 == 0)
+            const float4 v = *(const float4 *)(x + 32 * blk + 4 * part);
+            uint32_t d16, s16;
+            int lo, hi;
+            float dd;
+            const uint32_t q = quant_q8_1_part(v, d16, s16, lo, hi, dd);
+            uint8_t *b = xq + 36 * blk;
+            *(uint32_t *)(b + 4 + 4 * part) = q;
+            if (part == 0) *(uint32_t *)b = d16 | (s16 << 16);
+        }
+        return;
+    }
     __shared__ int32_t cnt[MB_MAX_E], off_all[MB_MAX_E], small_idx[MB_MAX_E], big_idx[MB_MAX_E], cur[MB_MAX_E];
     __shared__ int32_t exp_of[MB_MAX_P];
     __shared__ int32_t wsum[3][16];
@@ -533,11 +551,12 @@ hipError_t launch_moe_batch(const MoeArgs &base, uint32_t T, uint32_t min_big, c
     const uint32_t S = (uint32_t)base.n_sel + (base.has_shared ? 1u : 0u);
     const uint32_t P = T * S;
     if (T == 0 || T > MB_MAX_T || S == 0 || S > MB_MAX_S || base.n_expert > MB_MAX_E - 1) return hipErrorInvalidValue;
-    hipError_t e = launch_quantize_q8_1(x, (uint64_t)T * base.hidden, xq, s);
+    const uint32_t nq = T * base.hidden / 4;   // quantizer tasks: 8 per 32-value block
+    const uint32_t qwg = (nq + 1023) / 1024;
+    hipLaunchKernelGGL(k_mb_group, dim3(1 + qwg), dim3(1024), 0, s, base.ids, T, (uint32_t)base.n_sel, S,
+                       base.n_expert, min_big, meta, base.err, x, nq, xq);
+    hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_mb_group, dim3(1), dim3(1024), 0, s, base.ids, T, (uint32_t)base.n_sel, S, base.n_expert,
-                       min_big, meta, base.err);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
     MoeArgs a = base;
     a.x = nullptr;
     a.xq = xq;
