@@ -48,15 +48,8 @@ __device__ __forceinline__ const float *route_logits(const MoeArgs &a) {
 // Keys: a logit maps to an unsigned key that orders like the float, with NaN
 // ranked as -inf and -0 as +0; experts past n_expert get key 0 (below -inf).
 // Lane l holds the keys of experts l, l + 64, ... (C chunks of 64 experts).
-// Selection: a binary search over key bits with wave ballots finds T, the
-// n_sel-th largest key; every key > T is selected, and of the keys == T the
-// lowest expert indexes fill the rest. Ranking: the selected (key, expert)
-// pairs are packed into lanes 0..n_sel-1 (forward permute); a pair's rank is
-// the number of selected pairs ordered before it (larger key, or equal key
-// and lower index), counted against the other lanes of that 16-lane row with
-// DPP rotations; a second permute sends it to lane `rank`. No loop depends on
-// the data. Lane r < n_sel ends with the expert and the canonical logit of
-// rank r.
+// Selection and ranking at once: n_sel rounds of a wave-wide max (wave_topk).
+// Lane r < n_sel ends with the expert and the canonical logit of rank r.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t logit_key(float v) {
     if (v != v) v = -INFINITY;
@@ -65,9 +58,6 @@ __device__ __forceinline__ uint32_t logit_key(float v) {
 }
 __device__ __forceinline__ float key_logit(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
-}
-__device__ __forceinline__ int popc_below(uint64_t m) {
-    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
 struct WaveRoute {
@@ -86,21 +76,28 @@ __device__ __forceinline__ void load_keys(const MoeArgs &a, float (&lv)[C]) {
     for (int i = 0; i < C; i++) lv[i] = src[min(lane + 64 * i, a.n_expert - 1)];
 }
 
-// The value of lane (l +- S) of the same 16-lane row (DPP row_ror:S), 64 bits.
-template <int S>
-__device__ __forceinline__ uint64_t row_ror64(uint64_t v) {
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, 0x120 + S, 0xF, 0xF, false);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), 0x120 + S, 0xF, 0xF, false);
-    return ((uint64_t)hi << 32) | lo;
+// max over the 64 lanes, every lane gets it (DPP inside 16-lane rows, then
+// the two row swaps)
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)dpp_i<DPP_XOR1>((int)v));
+    v = max(v, (uint32_t)dpp_i<DPP_XOR2>((int)v));
+    v = max(v, (uint32_t)dpp_i<DPP_HALF_MIRROR>((int)v));
+    v = max(v, (uint32_t)dpp_i<DPP_MIRROR>((int)v));
+    const auto r16 = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = max((uint32_t)r16[0], (uint32_t)r16[1]);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return max((uint32_t)r32[0], (uint32_t)r32[1]);
 }
-// Number of the other 15 lanes of this lane's 16-lane row holding a larger v.
-template <int S>
-__device__ __forceinline__ int rank_in_row(uint64_t v) {
-    const int here = row_ror64<S>(v) > v ? 1 : 0;
-    if constexpr (S < 15) return here + rank_in_row<S + 1>(v);
-    else return here;
-}
-
+// Top n_sel of the logits, every wave on its own (no LDS, no barrier): n_sel
+// rounds of (largest remaining key over the wave; the lowest expert index
+// holding it; that key retired). Round j's expert and logit land in lane j,
+// so lanes 0..n_sel-1 hold the selection in rank order: larger logit first,
+// lower index on ties, NaN as -inf, -0 as +0. Keys of valid experts are
+// never 0 (the largest NaN-free order key of -inf is 0x007FFFFF), so the
+// retired and the padding lanes (key 0) are never chosen while n_sel <=
+// n_expert. (A 32-step binary search for the n_sel-th key plus a ranking
+// pass took ~2.5x the instructions: ~1.7 us of every wave's time at 256
+// experts.)
 template <int C>
 __device__ __forceinline__ WaveRoute wave_topk(const MoeArgs &a, const float (&lv)[C]) {
     const uint32_t lane = threadIdx.x & 63;
@@ -108,60 +105,29 @@ __device__ __forceinline__ WaveRoute wave_topk(const MoeArgs &a, const float (&l
     uint32_t key[C];
 #pragma unroll
     for (int i = 0; i < C; i++) key[i] = (lane + 64 * i < a.n_expert) ? logit_key(lv[i]) : 0u;
-    // T = largest t with #{key >= t} >= k (then T is the k-th largest key)
-    uint32_t T = 0;
+    int32_t id = -1;
+    uint32_t mk = 0;
 #pragma unroll
-    for (int b = 31; b >= 0; b--) {
-        const uint32_t c = T | (1u << b);
-        int cnt = 0;
+    for (int j = 0; j < MAX_SEL; j++) {
+        if (j >= k) break;   // uniform
+        uint32_t m = key[0];
 #pragma unroll
-        for (int i = 0; i < C; i++) cnt += __popcll(__ballot(key[i] >= c));
-        T = cnt >= k ? c : T;
+        for (int i = 1; i < C; i++) m = max(m, key[i]);
+        const uint32_t M = wave_max_u32(m);
+        int e = 0;
+#pragma unroll
+        for (int i = C - 1; i >= 0; i--) {   // the lowest chunk holding M wins, then the lowest lane
+            const uint64_t b = __ballot(key[i] == M);
+            e = b ? 64 * i + (int)__builtin_ctzll(b) : e;
+        }
+#pragma unroll
+        for (int i = 0; i < C; i++) key[i] = (int)(lane + 64 * i) == e ? 0u : key[i];
+        id = (int)lane == j ? e : id;
+        mk = (int)lane == j ? M : mk;
     }
-    int gt = 0;
-#pragma unroll
-    for (int i = 0; i < C; i++) gt += __popcll(__ballot(key[i] > T));
-    const int need = k - gt;   // ties at T to take, lowest index first
-    uint64_t sm[C];
-    bool sel[C];
-    int eq_seen = 0;
-#pragma unroll
-    for (int i = 0; i < C; i++) {
-        const uint64_t eq = __ballot(key[i] == T);
-        sel[i] = key[i] > T || (key[i] == T && eq_seen + popc_below(eq) < need);
-        sm[i] = __ballot(sel[i]);
-        eq_seen += __popcll(eq);
-    }
-    // Compact the k selected (key, expert) pairs into lanes 0..k-1 (expert
-    // order) with forward permutes; unselected lanes all aim at lane 63, which
-    // no selected pair uses (k <= 16).
-    uint32_t ck = 0, ce = 0;
-    int base = 0;
-#pragma unroll
-    for (int i = 0; i < C; i++) {
-        const int cnt = __popcll(sm[i]);
-        const int dst = sel[i] ? base + popc_below(sm[i]) : 63;
-        const uint32_t pk = (uint32_t)__builtin_amdgcn_ds_permute(4 * dst, (int)key[i]);
-        const uint32_t pe = (uint32_t)__builtin_amdgcn_ds_permute(4 * dst, (int)(lane + 64 * i));
-        const bool mine = (int)lane >= base && (int)lane < base + cnt;
-        ck = mine ? pk : ck;
-        ce = mine ? pe : ce;
-        base += cnt;
-    }
-    // Rank inside the first 16-lane row: comp orders like (key desc, expert
-    // asc); lanes >= k carry 0, below every selected pair (a selected key is
-    // never 0 and ~expert is never 0). Each of the 15 row rotations brings one
-    // other lane of the row.
-    const bool valid = (int)lane < k;
-    const uint64_t comp = valid ? (((uint64_t)ck << 32) | (uint32_t)~ce) : 0ull;
-    const int rank = rank_in_row<1>(comp);
-    // lane `rank` takes the pair
-    const int dst = valid ? rank : 63;
-    const uint32_t fe = (uint32_t)__builtin_amdgcn_ds_permute(4 * dst, (int)ce);
-    const uint32_t fk = (uint32_t)__builtin_amdgcn_ds_permute(4 * dst, (int)ck);
     WaveRoute r;
-    r.id = valid ? (int32_t)fe : -1;
-    r.logit = valid ? key_logit(fk) : 0.0f;
+    r.id = (int)lane < k ? id : -1;
+    r.logit = (int)lane < k ? key_logit(mk) : 0.0f;
     return r;
 }
 
