@@ -32,6 +32,7 @@
 namespace kq {
 
 constexpr int MAX_SEL = 16;
+constexpr uint32_t B_MAX_THREADS = 512;   // kernel B's largest workgroup
 constexpr int MAX_SLOTS = MAX_SEL + 1;
 constexpr uint32_t MAX_EXPERT = 512;
 
@@ -516,21 +517,22 @@ struct HLoad {
     uint32_t d[HT];
 };
 template <int HT>
-__device__ __forceinline__ void load_h(const uint8_t *hq8, uint32_t ntask, uint32_t first, HLoad<HT> &h) {
+__device__ __forceinline__ void load_h(const uint8_t *hq8, uint32_t ntask, uint32_t first, uint32_t nt, HLoad<HT> &h) {
 #pragma unroll
     for (int i = 0; i < HT; i++) {
-        const uint32_t t = min(first + threadIdx.x + 256 * i, ntask - 1);
+        const uint32_t t = min(first + threadIdx.x + nt * i, ntask - 1);
         const uint8_t *b = hq8 + (t >> 1) * 36;
         h.q[i] = ld16(b + 4 + 16 * (t & 1));
         h.d[i] = ld_u16(b);
     }
 }
 template <int HT>
-__device__ __forceinline__ void stage_h(uint8_t *hl, uint32_t ffn, uint32_t ntask, uint32_t first, const HLoad<HT> &h) {
+__device__ __forceinline__ void stage_h(uint8_t *hl, uint32_t ffn, uint32_t ntask, uint32_t first, uint32_t nt,
+                                        const HLoad<HT> &h) {
     const uint32_t nblk = ffn / 32, ab = act_bytes(ffn);
 #pragma unroll
     for (int i = 0; i < HT; i++) {
-        const uint32_t t = first + threadIdx.x + 256 * i;
+        const uint32_t t = first + threadIdx.x + nt * i;
         if (t < ntask) {
             const uint32_t blk = t >> 1, half = t & 1, slot = blk / nblk, kb = blk % nblk;
             const Act act = act_carve(hl + slot * ab, ffn);
@@ -545,8 +547,10 @@ __device__ __forceinline__ void stage_h(uint8_t *hl, uint32_t ffn, uint32_t ntas
     }
 }
 
-template <class QD, int IPL, int P>
-__global__ void __launch_bounds__(256) k_moe_down(MoeArgs a, uint32_t tr, uint32_t n_slots) {
+// NT: the workgroup size, or 0 for blockDim.x (up to B_MAX_THREADS)
+template <class QD, int IPL, int P, int NT>
+__global__ void __launch_bounds__(NT > 0 ? NT : B_MAX_THREADS) k_moe_down(MoeArgs a, uint32_t tr, uint32_t n_slots) {
+    const uint32_t nt = NT > 0 ? (uint32_t)NT : blockDim.x;
     extern __shared__ __align__(16) uint8_t lds[];
     const LdsB L = lds_b(a.ffn, n_slots, tr);
     const uint32_t tid = threadIdx.x, lane = tid & 63;
@@ -557,7 +561,7 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a, uint32_t tr, uint32
     const uint32_t ntask = n_slots * (a.ffn / 32) * 2;
     constexpr int HT = P >= 16 ? 4 : 2;
     HLoad<HT> hv;
-    load_h(a.hq8, ntask, 0, hv);
+    load_h(a.hq8, ntask, 0, nt, hv);
 
     constexpr uint32_t S = QD::IPB * P;
     const uint32_t ls = tid / S, s = tid % S;
@@ -580,10 +584,10 @@ __global__ void __launch_bounds__(256) k_moe_down(MoeArgs a, uint32_t tr, uint32
         for (int i = 0; i < IPL; i++)   // clamped: a block past the row is loaded and dropped
             raw[i] = QD::load(rp + min(sub + P * i, nbk - 1) * QD::BB, (int)item);
     }
-    stage_h(lds + L.hacts, a.ffn, ntask, 0, hv);
-    for (uint32_t first = HT * 256; first < ntask; first += HT * 256) {
-        load_h(a.hq8, ntask, first, hv);   // only when n_slots * ffn / 16 > 256 * HT
-        stage_h(lds + L.hacts, a.ffn, ntask, first, hv);
+    stage_h(lds + L.hacts, a.ffn, ntask, 0, nt, hv);
+    for (uint32_t first = HT * nt; first < ntask; first += HT * nt) {
+        load_h(a.hq8, ntask, first, nt, hv);   // only when n_slots * ffn / 16 > nt * HT
+        stage_h(lds + L.hacts, a.ffn, ntask, first, nt, hv);
     }
     __syncthreads();
     float x = 0.0f;
@@ -875,15 +879,31 @@ static uint32_t b_tile_rows(uint32_t P, uint32_t n_slots) {
     return tr < 1 ? 1 : tr;
 }
 
+// Kernel B's launch: 256-thread tiles, unless those give between one and
+// two workgroups per CU (some CUs would take two tiles while the rest idle):
+// then the fewest rows per tile that keep one tile per CU, in up to
+// B_MAX_THREADS threads (nine slots at 2048 rows: 293 tiles of 7 rows ->
+// 256 tiles of 8 rows in 320 threads).
 template <class QD, int IPL, int P>
 static hipError_t go_b(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
-    const uint32_t tr = b_tile_rows<QD>(P, n_slots);
+    const uint32_t S = QD::IPB * P;
+    uint32_t tr = b_tile_rows<QD>(P, n_slots), nt = 256;
+    const uint32_t cus = (uint32_t)device_cu_count();
+    const uint32_t ntile = (a.hidden + tr - 1) / tr;
+    if (ntile > cus && ntile < 2 * cus) {
+        const uint32_t tr1 = (a.hidden + cus - 1) / cus, lanes = tr1 * n_slots * S;
+        if (lanes <= B_MAX_THREADS) {
+            tr = tr1;
+            nt = (lanes + 63) / 64 * 64;
+        }
+    }
     const LdsB L = lds_b(a.ffn, n_slots, tr);
-    hipLaunchKernelGGL((k_moe_down<QD, IPL, P>), dim3((a.hidden + tr - 1) / tr), dim3(256), L.total, s, a, tr,
-                       n_slots);
+    const dim3 grid((a.hidden + tr - 1) / tr);
+    // the 256-thread tiles keep their own build (a constant workgroup size)
+    if (nt == 256) hipLaunchKernelGGL((k_moe_down<QD, IPL, P, 256>), grid, dim3(nt), L.total, s, a, tr, n_slots);
+    else hipLaunchKernelGGL((k_moe_down<QD, IPL, P, 0>), grid, dim3(nt), L.total, s, a, tr, n_slots);
     return hipGetLastError();
 }
-
 // P = lanes-per-pair multiplier: the smallest power of two that brings a
 // lane's blocks (IPL = ceil(nb / P)) to at most 4 while a workgroup still
 // holds every slot of at least one output row; 1 (a runtime block loop when
