@@ -182,7 +182,11 @@ typedef struct KataliHipMoeBatch {
     const float *weights;                  /* device [T][n_sel] */
 } KataliHipMoeBatch;
 
-/* y[T][hidden] = the MoE layer of each of the T fp32 rows x[T][hidden]. */
+/* y[T][hidden] = the MoE layer of each of the T fp32 rows x[T][hidden].
+ * From 96 (token, slot) pairs on, the grouped-GEMM part runs on a second,
+ * library-owned stream forked from the library stream and joined back
+ * before the call's last kernel, so work queued after the call (or a graph
+ * captured around it) still sees the whole layer finished in order. */
 int katali_hip_moe_batch(const KataliHipMoe *moe, const KataliHipMoeBatch *batch, const float *x_dev,
                          float *y_dev);
 
