@@ -118,6 +118,21 @@ int katali_hip_block_isums(uint32_t type, const void *w_dev, uint64_t rows, uint
  * wins, NaN never wins, 0 when no logit exceeds -FLT_MAX). 1 <= n < 2^31. */
 int katali_hip_argmax(const float *logits_dev, uint64_t n, int32_t *out_dev);
 
+/* ---- the decode chain's norm and residual (RMSNorm, residual add) -------- */
+/* out[n] = RMSNorm(x) * w with the engine's arithmetic, replacing
+ * katali_gguf_rmsnorm (V/src/gguf_kernels.c:13-18; called at
+ * V/src/gguf_model.c:604,683,698): the sum of squares in double, inv =
+ * 1/sqrtf((float)(sumsq/n) + eps), out[i] = x[i]*inv*w[i]. Bit-identical to
+ * it unless the double sum, formed in another order, straddles a float
+ * rounding boundary. out may be x (katali_gguf_rmsnorm_inplace, :20-25).
+ * 1 <= n <= 2^20. */
+int katali_hip_rmsnorm(const float *x_dev, const float *w_dev, uint64_t n, float eps, float *out_dev);
+/* The residual step and the next norm in one launch: x += delta (scale ==
+ * 1, katali_gguf_add_inplace at V/src/gguf_model.c:677,692) or x += scale *
+ * delta (:678,693), in place, then out = RMSNorm(x) * w as above. */
+int katali_hip_add_rmsnorm(float *x_dev, const float *delta_dev, float scale, const float *w_dev, uint64_t n,
+                           float eps, float *out_dev);
+
 /* ---- fused MoE layer (README.md:13, one GPU call per MoE layer) ----------- */
 typedef struct KataliHipMoe {
     uint32_t struct_size;                  /* sizeof(KataliHipMoe) */

@@ -63,6 +63,11 @@ int katali_gpu_selftest(char *report, size_t cap);
 /* Greedy token on device (gguf_sampler.c:62-66 rule), for a decode loop that
  * keeps logits resident. */
 int katali_gpu_argmax(const float *logits_dev, uint64_t n, int32_t *out_dev);
+/* RMSNorm and the residual add before it (V/src/gguf_kernels.c:13-18,
+ * V/src/gguf_model.c:677-683). */
+int katali_gpu_rmsnorm(const float *x_dev, const float *w_dev, uint64_t n, float eps, float *out_dev);
+int katali_gpu_add_rmsnorm(float *x_dev, const float *delta_dev, float scale, const float *w_dev, uint64_t n,
+                           float eps, float *out_dev);
 /* The MoE layer over a batch of up to 64 tokens (batched prefill). */
 int katali_gpu_moe_batch(const KataliHipMoe *moe, const KataliHipMoeBatch *batch, const float *x_dev,
                          float *y_dev);
@@ -110,6 +115,8 @@ typedef struct KataliHipApi {
                         float *const *);
     int (*matvec_multi_dp4a)(int, const uint32_t *, const void *const *, const uint64_t *, uint64_t,
                              const float *, float *const *);
+    int (*rmsnorm)(const float *, const float *, uint64_t, float, float *);
+    int (*add_rmsnorm)(float *, const float *, float, const float *, uint64_t, float, float *);
 } KataliHipApi;
 
 /* NULL when the library could not be loaded or an entry point is missing. */

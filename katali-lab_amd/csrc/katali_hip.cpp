@@ -465,6 +465,26 @@ int katali_hip_moe_batch(const KataliHipMoe *moe, const KataliHipMoeBatch *batch
     return moe_batch_impl(moe, batch, x_dev, y_dev);
 }
 
+static int check_norm(const void *x, const void *w, uint64_t n, const void *out) {
+    if (!x || !w || !out) return fail(KATALI_HIP_E_INVALID, "null buffer");
+    if (n == 0 || n > (1u << 20)) return fail(KATALI_HIP_E_INVALID, "rmsnorm n=%llu (1..2^20)", (unsigned long long)n);
+    return KATALI_HIP_OK;
+}
+
+int katali_hip_rmsnorm(const float *x, const float *w, uint64_t n, float eps, float *out) {
+    int rc = ensure();
+    if (rc || (rc = check_norm(x, w, n, out))) return rc;
+    return launched(kq::launch_rmsnorm(x, w, (uint32_t)n, eps, out, g_stream), "rmsnorm");
+}
+
+int katali_hip_add_rmsnorm(float *x, const float *delta, float scale, const float *w, uint64_t n, float eps,
+                           float *out) {
+    int rc = ensure();
+    if (rc || (rc = check_norm(x, w, n, out))) return rc;
+    if (!delta) return fail(KATALI_HIP_E_INVALID, "null buffer");
+    return launched(kq::launch_add_rmsnorm(x, delta, scale, w, (uint32_t)n, eps, out, g_stream), "add_rmsnorm");
+}
+
 int katali_hip_argmax(const float *x, uint64_t n, int32_t *out) {
     int rc = ensure();
     if (rc) return rc;

@@ -56,6 +56,12 @@ hipError_t launch_copy(const uint8_t *src, uint8_t *dst, uint64_t n, hipStream_t
 // wins, NaN never, 0 when nothing exceeds -FLT_MAX). scratch holds
 // argmax_parts() * 8 bytes.
 uint32_t argmax_parts();
+// out = RMSNorm(x) * w with the engine's arithmetic; the add variant first
+// does x += delta (scale 1) or x += scale * delta in place. One workgroup;
+// out may be x.
+hipError_t launch_rmsnorm(const float *x, const float *w, uint32_t n, float eps, float *out, hipStream_t s);
+hipError_t launch_add_rmsnorm(float *x, const float *delta, float scale, const float *w, uint32_t n, float eps,
+                              float *out, hipStream_t s);
 hipError_t launch_argmax(const float *x, uint32_t n, void *scratch, int32_t *out, hipStream_t s);
 
 // MoE layer (two launches). Types: gate/up Q4_K; down Q4_K or Q6_K.

@@ -109,6 +109,8 @@ static int load(void) {
     LOAD(moe_batch, "katali_hip_moe_batch");
     LOAD(matvec_multi, "katali_hip_matvec_multi");
     LOAD(matvec_multi_dp4a, "katali_hip_matvec_multi_dp4a");
+    LOAD(rmsnorm, "katali_hip_rmsnorm");
+    LOAD(add_rmsnorm, "katali_hip_add_rmsnorm");
     if (g_api.abi_version() != KATALI_HIP_ABI_VERSION) {
         snprintf(g_status, sizeof g_status, "%s: ABI version %d, loader expects %d", tried, g_api.abi_version(),
                  KATALI_HIP_ABI_VERSION);
@@ -179,6 +181,13 @@ int katali_gpu_graph_launch(void *g) { FORWARD(g_api.graph_launch(g)); }
 int katali_gpu_graph_destroy(void *g) { FORWARD(g_api.graph_destroy(g)); }
 int katali_gpu_selftest(char *report, size_t cap) { FORWARD(g_api.selftest(report, cap)); }
 int katali_gpu_argmax(const float *logits, uint64_t n, int32_t *out) { FORWARD(g_api.argmax(logits, n, out)); }
+int katali_gpu_rmsnorm(const float *x, const float *w, uint64_t n, float eps, float *out) {
+    FORWARD(g_api.rmsnorm(x, w, n, eps, out));
+}
+int katali_gpu_add_rmsnorm(float *x, const float *delta, float scale, const float *w, uint64_t n, float eps,
+                           float *out) {
+    FORWARD(g_api.add_rmsnorm(x, delta, scale, w, n, eps, out));
+}
 int katali_gpu_moe_batch(const KataliHipMoe *moe, const KataliHipMoeBatch *batch, const float *x, float *y) {
     FORWARD(g_api.moe_batch(moe, batch, x, y));
 }

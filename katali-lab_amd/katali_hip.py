@@ -59,6 +59,8 @@ SIGNATURES = {
     "katali_hip_moe_batch": (C.c_int, [_vp, _vp, _vp, _vp]),
     "katali_hip_matvec_multi": (C.c_int, [C.c_int, _vp, _vp, _vp, _u64, _vp, _vp]),
     "katali_hip_matvec_multi_dp4a": (C.c_int, [C.c_int, _vp, _vp, _vp, _u64, _vp, _vp]),
+    "katali_hip_rmsnorm": (C.c_int, [_vp, _vp, _u64, _f32, _vp]),
+    "katali_hip_add_rmsnorm": (C.c_int, [_vp, _vp, _f32, _vp, _u64, _f32, _vp]),
 }
 
 
@@ -187,6 +189,12 @@ class KataliHip:
                 (_vp * n)(*[y.ptr for y in ys]))
         fn = self.lib.katali_hip_matvec_multi_dp4a if dp4a else self.lib.katali_hip_matvec_multi
         self.check(fn(n, *args))
+
+    def rmsnorm(self, x, w, n, eps, out) -> None:
+        self.check(self.lib.katali_hip_rmsnorm(x.ptr, w.ptr, n, eps, out.ptr))
+
+    def add_rmsnorm(self, x, delta, scale, w, n, eps, out) -> None:
+        self.check(self.lib.katali_hip_add_rmsnorm(x.ptr, delta.ptr, scale, w.ptr, n, eps, out.ptr))
 
     def block_isums(self, t, w, rows, cols, xq, out) -> None:
         self.check(self.lib.katali_hip_block_isums(t, w.ptr, rows, cols, xq.ptr, out.ptr))

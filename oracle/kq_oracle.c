@@ -544,6 +544,18 @@ int kqo_argmax_greedy(const float *logits, int n) {
     return best;
 }
 
+void kqo_rmsnorm(const float *x, const float *w, uint64_t n, float eps, float *out) {
+    double sumsq = 0.0;
+    for (uint64_t i = 0; i < n; i++) sumsq += (double)x[i] * (double)x[i];
+    const float inv = 1.0f / sqrtf((float)(sumsq / (double)n) + eps);
+    for (uint64_t i = 0; i < n; i++) out[i] = x[i] * inv * w[i];
+}
+
+void kqo_add_rmsnorm(float *x, const float *delta, float scale, const float *w, uint64_t n, float eps, float *out) {
+    for (uint64_t i = 0; i < n; i++) x[i] = scale == 1.0f ? x[i] + delta[i] : x[i] + scale * delta[i];
+    kqo_rmsnorm(x, w, n, eps, out);
+}
+
 /* ======================================================================== *
  * MoE layer                                                                 *
  * ======================================================================== */

@@ -122,6 +122,13 @@ int kqo_router_topk(const float *logits, int n_expert, int k, int32_t *ids, floa
 /* Greedy argmax: first maximum wins, NaN never, 0 when nothing exceeds
  * -FLT_MAX (V/src/gguf_sampler.c:62-66). */
 int kqo_argmax_greedy(const float *logits, int n);
+/* RMSNorm (V/src/gguf_kernels.c:13-18): sumsq = sum x[i]^2 in double, in
+ * index order; inv = 1/sqrtf((float)(sumsq/n) + eps); out[i] = x[i]*inv*w[i].
+ * out may be x. */
+void kqo_rmsnorm(const float *x, const float *w, uint64_t n, float eps, float *out);
+/* The residual step before a norm (V/src/gguf_model.c:677-678): x[i] +=
+ * delta[i] when scale == 1, else x[i] += scale*delta[i]; then kqo_rmsnorm. */
+void kqo_add_rmsnorm(float *x, const float *delta, float scale, const float *w, uint64_t n, float eps, float *out);
 
 /* ---- MoE layer (configs 1, 2, 4) ----------------------------------------- */
 typedef struct KqoMoe {

@@ -71,6 +71,8 @@ class Oracle:
             "kqo_silu_mul_ref": (None, [_vp, _vp, _u64]),
             "kqo_router_topk": (_i32, [_vp, _i32, _i32, _vp, _vp]),
             "kqo_argmax_greedy": (_i32, [_vp, _i32]),
+            "kqo_rmsnorm": (None, [_vp, _vp, _u64, _f32, _vp]),
+            "kqo_add_rmsnorm": (None, [_vp, _vp, _f32, _vp, _u64, _f32, _vp]),
             "kqo_moe_layer_q8": (_i32, [C.POINTER(KqoMoe), _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
             "kqo_moe_down_q8": (_i32, [C.POINTER(KqoMoe), _i32, _vp, _vp, _vp, _vp]),
             "kqo_moe_layer_f32": (_i32, [C.POINTER(KqoMoe), _vp, _i32, _vp, _vp, _vp]),
@@ -150,6 +152,22 @@ class Oracle:
         assert self.lib.kqo_router_topk(_ptr(logits), logits.size, k, _ptr(ids), _ptr(w)) == 0
         return ids, w
 
+    def rmsnorm(self, x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        w = np.ascontiguousarray(w, np.float32)
+        out = np.empty_like(x)
+        self.lib.kqo_rmsnorm(_ptr(x), _ptr(w), x.size, eps, _ptr(out))
+        return out
+
+    def add_rmsnorm(self, x: np.ndarray, delta: np.ndarray, scale: float, w: np.ndarray, eps: float):
+        """(x + scale*delta, its RMSNorm * w); x is not modified."""
+        x = np.array(x, np.float32, copy=True)
+        delta = np.ascontiguousarray(delta, np.float32)
+        w = np.ascontiguousarray(w, np.float32)
+        out = np.empty_like(x)
+        self.lib.kqo_add_rmsnorm(_ptr(x), _ptr(delta), scale, _ptr(w), x.size, eps, _ptr(out))
+        return x, out
+
     def argmax_greedy(self, logits: np.ndarray) -> int:
         logits = np.ascontiguousarray(logits, np.float32)
         return int(self.lib.kqo_argmax_greedy(_ptr(logits), logits.size))
@@ -226,6 +244,10 @@ class RefCPU:
         L.katali_ggml_silu_mul_avx2.argtypes = [_vp, _vp, C.c_size_t]
         L.katali_gguf_softmax.restype = None
         L.katali_gguf_softmax.argtypes = [_vp, C.c_size_t]
+        L.katali_gguf_rmsnorm.restype = None
+        L.katali_gguf_rmsnorm.argtypes = [_vp, _vp, C.c_size_t, _f32, _vp]
+        L.katali_gguf_add_inplace.restype = None
+        L.katali_gguf_add_inplace.argtypes = [_vp, _vp, C.c_size_t]
         L.katali_ggml_simd_available.restype = _i32
         L.katali_gguf_set_threads.argtypes = [_i32]
         L.katali_gguf_threads_shutdown.restype = None
@@ -280,6 +302,18 @@ class RefCPU:
         x = np.array(x, np.float32, copy=True)
         self.lib.katali_gguf_softmax(_ptr(x), x.size)
         return x
+
+    def rmsnorm(self, x, w, eps):
+        x = np.ascontiguousarray(x, np.float32)
+        w = np.ascontiguousarray(w, np.float32)
+        out = np.empty_like(x)
+        self.lib.katali_gguf_rmsnorm(_ptr(x), _ptr(w), x.size, eps, _ptr(out))
+        return out
+
+    def add_inplace(self, a, b):
+        a = np.array(a, np.float32, copy=True)
+        self.lib.katali_gguf_add_inplace(_ptr(a), _ptr(np.ascontiguousarray(b, np.float32)), a.size)
+        return a
 
 
 def ref_available() -> bool:
