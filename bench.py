@@ -73,13 +73,26 @@ MOE_WORKLOADS = {
 }
 
 
+# Whole decode tokens of a MoE workload, attention aside: the token's
+# residual stream, per layer RMSNorm (residual add from the second layer on),
+# F32 router logits and the MoE layer routed from them on the device, then the
+# output norm, the Q6_K LM head and the greedy argmax, all in one hipGraph.
+TOKEN_WORKLOADS = {
+    # name: MoE workload, vocabulary
+    "moe48tok": ("moe48", 151936),
+}
+
+
 def moe_bytes_per_layer(hidden, ffn, n_sel, shared):
     per_expert = 2 * ffn * row_bytes(Q4_K, hidden) + hidden * row_bytes(Q6_K, ffn)
     slots = n_sel + (1 if shared else 0)
     return slots * per_expert + hidden // 32 * 36 + hidden * 4, slots * per_expert
 
 
-def bench_moe(hip, name, steps, warmup, ring=64):
+def bench_moe(hip, name, steps, warmup, ring=64, vocab=0):
+    """One hipGraph per ring position, replayed per token. vocab == 0: the
+    MoE layers only (router logits from a ring). vocab > 0: the whole token
+    chain (TOKEN_WORKLOADS), routing from the device router's logits."""
     L, hidden, ffn, n_expert, n_sel, shared = MOE_WORKLOADS[name]
     rb_g, rb_d = row_bytes(Q4_K, hidden), row_bytes(Q6_K, ffn)
     layers = []
@@ -129,6 +142,44 @@ def bench_moe(hip, name, steps, warmup, ring=64):
         for li in range(L):
             hip.moe_layer(descs[li], routes[t][li], ys[li], x=xs[li])
 
+    chain_bufs = []
+    if vocab:
+        rb_h = row_bytes(Q6_K, hidden)
+        router = hip.alloc(L * n_expert * hidden * 4)
+        hip.synth_normal(router, L * n_expert * hidden, 79, 0.05)
+        norm_w = hip.alloc((L + 1) * hidden * 4)
+        hip.synth_normal(norm_w, (L + 1) * hidden, 80, 1.0)
+        x0 = hip.alloc(ring * hidden * 4)          # the ring's token inputs
+        hip.synth_normal(x0, ring * hidden, 81, 1.0)
+        xpp, xn_out = [hip.alloc(hidden * 4), hip.alloc(hidden * 4)], hip.alloc(hidden * 4)
+        clog = hip.alloc(L * n_expert * 4)
+        head = hip.alloc(vocab * rb_h)
+        hip.synth_fill(Q6_K, head, vocab * hidden // 256, seed)
+        head_logits, tok = hip.alloc(vocab * 4), hip.alloc(256)
+        chain_bufs = [router, norm_w, x0, *xpp, xn_out, clog, head, head_logits, tok]
+        routers = [View(router.ptr + li * n_expert * hidden * 4) for li in range(L + 1)]
+        nws = [View(norm_w.ptr + li * hidden * 4) for li in range(L + 1)]
+        cls = [View(clog.ptr + li * n_expert * 4) for li in range(L)]
+        croutes = [hip.moe_route(n_sel, logits=cls[li]) for li in range(L)]
+
+        def token(t):  # noqa: F811
+            # residual step + norm + router logits in one launch per layer; the
+            # residual stream alternates between two buffers after the input
+            cur = View(x0.ptr + t * hidden * 4)
+            for li in range(L):
+                if li == 0:
+                    hip.rmsnorm_matvec_f32(cur, None, 1.0, None, nws[0], hidden, 1e-6, xs[0], routers[0],
+                                           n_expert, cls[0])
+                else:
+                    nxt = xpp[li % 2]
+                    hip.rmsnorm_matvec_f32(cur, ys[li - 1], 1.0, nxt, nws[li], hidden, 1e-6, xs[li], routers[li],
+                                           n_expert, cls[li])
+                    cur = nxt
+                hip.moe_layer(descs[li], croutes[li], ys[li], x=xs[li])
+            hip.add_rmsnorm(cur, ys[L - 1], 1.0, nws[L], hidden, 1e-6, xn_out)
+            hip.matvec_dp4a(Q6_K, head, vocab, hidden, xn_out, head_logits)
+            hip.argmax(head_logits, vocab, tok)
+
     # eager pass sizes the scratch, then one graph per ring position
     token(0)
     hip.sync()
@@ -155,10 +206,10 @@ def bench_moe(hip, name, steps, warmup, ring=64):
     # per-launch kernel time: an event pair around each layer, eager
     ev = [hip.event() for _ in range(2 * L)]
     per = []
-    for t in range(3):
+    for t in range(0 if vocab else 3):   # (the token chain reports the graph only)
         for li in range(L):
             hip.record(ev[2 * li])
-            hip.moe_layer(descs[li], routes[t][li], ys[li], x=xs[li])
+            hip.moe_layer(descs[li], croutes[li] if vocab else routes[t][li], ys[li], x=xs[li])
             hip.record(ev[2 * li + 1])
         hip.sync()
         per += [hip.elapsed_ms(ev[2 * li], ev[2 * li + 1]) for li in range(L)]
@@ -169,8 +220,16 @@ def bench_moe(hip, name, steps, warmup, ring=64):
 
     layer_bytes, weight_bytes = moe_bytes_per_layer(hidden, ffn, n_sel, shared)
     tok_bytes = L * layer_bytes
+    if vocab:
+        # + per layer: router weights and logits out; the norm's x, delta, w
+        # in and x_out, xn written (20 B per element); + the output norm, the
+        # LM head (weights, logits out) and the argmax read
+        tok_bytes += L * (n_expert * hidden * 4 + n_expert * 4 + 20 * hidden)
+        tok_bytes += 16 * hidden + vocab * row_bytes(Q6_K, hidden) + vocab * 4 + vocab * 4
+        for b in chain_bufs:
+            b.free()
     s_per_tok = ms / 1e3 / steps
-    kernel_ms = float(np.mean(per))
+    kernel_ms = float(np.mean(per)) if per else float("nan")
     res = {
         "ms_per_step": ms / steps,
         "wall_ms_per_step": wall * 1e3 / steps,
@@ -178,7 +237,7 @@ def bench_moe(hip, name, steps, warmup, ring=64):
         "tok_s": 1.0 / s_per_tok,
         "bytes_per_token": tok_bytes,
         "kernel_ms_mean": kernel_ms,
-        "kernel_ms_median": float(np.median(per)),
+        "kernel_ms_median": float(np.median(per)) if per else float("nan"),
         "kernel_gbs": layer_bytes / (kernel_ms / 1e3) / 1e9,
         "layer_bytes": layer_bytes,
         "pool_gb": L * (n_expert * (2 * ffn * rb_g + hidden * rb_d)) / 1e9,
@@ -673,7 +732,7 @@ def main():
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", default="moe48",
-                    choices=sorted(MOE_WORKLOADS) + sorted(GEMV_WORKLOADS) + sorted(DENSE_WORKLOADS) + ["moebatch"])
+                    choices=sorted(MOE_WORKLOADS) + sorted(TOKEN_WORKLOADS) + sorted(GEMV_WORKLOADS) + sorted(DENSE_WORKLOADS) + ["moebatch"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--batch-points", default="", metavar="NxT,...",
                     help="moebatch: only these (n_sel x tokens) points, e.g. 8x64,2x64 (profiling)")
@@ -720,6 +779,24 @@ def main():
         kernel = "MoE layer: k_moe_gu + k_moe_down (two launches per layer)"
         extra = {"tok_s": round(res["tok_s"], 2),
                  "eager_layer_ms_mean": round(res["kernel_ms_mean"], 5)}
+    elif args.workload in TOKEN_WORKLOADS:
+        base, vocab = TOKEN_WORKLOADS[args.workload]
+        res, shape = bench_moe(hip, base, args.steps, args.warmup, vocab=vocab)
+        L, hidden, ffn, n_expert, n_sel, shared = shape
+        unit_ms = res["ms_per_step"]
+        unit_bytes = res["bytes_per_token"]
+        metric = "decode token HBM GB/s (% of ~8 TB/s peak) + tok/s: MoE FFN chain, LM head and argmax on device"
+        config = {
+            "workload": f"{args.workload}: whole decode tokens of {base} with attention aside: per layer one launch "
+                        f"for residual add + RMSNorm + F32 router {n_expert}x{hidden}, the MoE layer routed on the "
+                        f"device from those logits (top-{n_sel}, gate/up {hidden}->{ffn} Q4_K, down Q6_K); output "
+                        f"RMSNorm, Q6_K LM head {vocab}x{hidden} (v_dot4), greedy argmax; one hipGraph per token "
+                        f"(64 input vectors in a ring)",
+            "layers": L, "hidden": hidden, "ffn": ffn, "n_expert": n_expert, "n_sel": n_sel, "vocab": vocab,
+            "bytes_per_token": res["bytes_per_token"], "parallelism": "single GPU",
+        }
+        kernel = "whole token graph (3 per layer + 4 launches: k_norm_router, k_moe_gu, k_moe_down; output norm, head, argmax)"
+        extra = {"tok_s": round(res["tok_s"], 2)}
     elif args.workload == "moebatch":
         only = [tuple(int(v) for v in pt.split("x")) for pt in args.batch_points.split(",") if pt] or None
         res, shape = bench_moe_batch(hip, args.steps, args.warmup, only)
@@ -771,8 +848,8 @@ def main():
     print(f"[bench] gpu done: {res['value']:.1f} GB/s", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu_baseline:
-        if args.workload == "moebatch":
-            cpu = None   # the reference has no batched GPU-shaped CPU counterpart timed here
+        if args.workload == "moebatch" or args.workload in TOKEN_WORKLOADS:
+            cpu = None   # no CPU counterpart of this exact workload is timed here
         elif args.workload in MOE_WORKLOADS:
             cpu = cpu_baseline_moe(shape)
         elif args.workload in DENSE_WORKLOADS:

@@ -45,6 +45,7 @@ extern "C" {
 #define KATALI_HIP_E_NOMEM (-5)       /* device allocation failed */
 #define KATALI_HIP_E_TIMEOUT (-6)     /* in-kernel dependency wait expired */
 
+#define KATALI_HIP_TYPE_F32 0u
 #define KATALI_HIP_TYPE_Q4_K 12u
 #define KATALI_HIP_TYPE_Q6_K 14u
 
@@ -67,12 +68,17 @@ int katali_hip_free(void *dev);
 int katali_hip_upload(void *dev, const void *host, size_t bytes);
 /* Waits for queued work, then device->host. Replaces katali_cuda_download (:54,70). */
 int katali_hip_download(void *host, const void *dev, size_t bytes);
-/* 1 for Q4_K and Q6_K. Replaces katali_cuda_supports_type (:48,67). */
+/* 1 for Q4_K, Q6_K and F32 (F32: katali_hip_matvec only). Replaces
+ * katali_cuda_supports_type (:48,67). */
 int katali_hip_supports_type(uint32_t ggml_type);
 /* y[rows] = W[rows x cols] . x with fp32 x and y, W in GGUF layout on the
  * device. With KATALI_CUDA_DP4A=1 (or KATALI_HIP_DP4A=1) in the environment x
  * is quantized to q8_1 inside the kernel and dotted with v_dot4; otherwise
  * weights are dequantized and dotted in fp32. cols % 256 == 0.
+ * F32 weights (type 0: the MoE router matrices) take their own kernel,
+ * bit-identical to the engine's AVX2 F32 dot (V/src/gguf_simd_x86.c:111-122,
+ * the path katali_ggml_matvec takes for F32 rows, gguf_simd_x86.c:875-877):
+ * cols % 4 == 0, w and x 16-byte aligned, the DP4A switch does not apply.
  * Replaces katali_cuda_matvec (V/src/katali_dense_cuda.c:53,69). */
 int katali_hip_matvec(uint32_t type, const void *w_dev, uint64_t rows, uint64_t cols,
                       const float *x_dev, float *y_dev);
@@ -132,6 +138,18 @@ int katali_hip_rmsnorm(const float *x_dev, const float *w_dev, uint64_t n, float
  * delta (:678,693), in place, then out = RMSNorm(x) * w as above. */
 int katali_hip_add_rmsnorm(float *x_dev, const float *delta_dev, float scale, const float *w_dev, uint64_t n,
                            float eps, float *out_dev);
+/* The steps before a MoE layer in one launch: the residual step (when
+ * delta_dev is not NULL: x_out = x + delta, or x + scale * delta), the norm
+ * xn = RMSNorm(x_out or x) * norm_w as katali_hip_rmsnorm, and the router
+ * logits y[rows] = W_router[rows x n] . xn as katali_hip_matvec on F32
+ * (bit-identical to both: V/src/gguf_model.c:677-683 followed by the F32
+ * router product, V/src/gguf_simd_x86.c:111-122). The new residual goes to
+ * x_out, a buffer apart from x (x is read by every workgroup); with delta
+ * NULL, x_out is unused and may be NULL. 4 <= n <= 8192, n % 4 == 0, rows >= 1,
+ * all vectors and W 16-byte aligned; outputs must not overlap inputs. */
+int katali_hip_rmsnorm_matvec_f32(const float *x_dev, const float *delta_dev, float scale, float *x_out_dev,
+                                  const float *norm_w_dev, uint64_t n, float eps, float *xn_dev,
+                                  const float *w_dev, uint64_t rows, float *y_dev);
 
 /* ---- fused MoE layer (README.md:13, one GPU call per MoE layer) ----------- */
 typedef struct KataliHipMoe {

@@ -68,6 +68,10 @@ int katali_gpu_argmax(const float *logits_dev, uint64_t n, int32_t *out_dev);
 int katali_gpu_rmsnorm(const float *x_dev, const float *w_dev, uint64_t n, float eps, float *out_dev);
 int katali_gpu_add_rmsnorm(float *x_dev, const float *delta_dev, float scale, const float *w_dev, uint64_t n,
                            float eps, float *out_dev);
+/* Residual step, norm and F32 router logits in one launch. */
+int katali_gpu_rmsnorm_matvec_f32(const float *x_dev, const float *delta_dev, float scale, float *x_out_dev,
+                                  const float *norm_w_dev, uint64_t n, float eps, float *xn_dev,
+                                  const float *w_dev, uint64_t rows, float *y_dev);
 /* The MoE layer over a batch of up to 64 tokens (batched prefill). */
 int katali_gpu_moe_batch(const KataliHipMoe *moe, const KataliHipMoeBatch *batch, const float *x_dev,
                          float *y_dev);
@@ -117,6 +121,8 @@ typedef struct KataliHipApi {
                              const float *, float *const *);
     int (*rmsnorm)(const float *, const float *, uint64_t, float, float *);
     int (*add_rmsnorm)(float *, const float *, float, const float *, uint64_t, float, float *);
+    int (*rmsnorm_matvec_f32)(const float *, const float *, float, float *, const float *, uint64_t, float, float *,
+                              const float *, uint64_t, float *);
 } KataliHipApi;
 
 /* NULL when the library could not be loaded or an entry point is missing. */

@@ -364,11 +364,25 @@ int katali_hip_download(void *host, const void *dev, size_t bytes) {
     return e == hipSuccess ? KATALI_HIP_OK : hip_fail(e, "download");
 }
 
-int katali_hip_supports_type(uint32_t t) { return type_ok(t) ? 1 : 0; }
+int katali_hip_supports_type(uint32_t t) { return type_ok(t) || t == KATALI_HIP_TYPE_F32 ? 1 : 0; }
+
+static int check_gemv_f32(const void *w, uint64_t rows, uint64_t cols, const void *x, const void *y) {
+    if (!w || !x || !y) return fail(KATALI_HIP_E_INVALID, "null buffer");
+    if (cols == 0 || cols % 4 || cols > 32768)
+        return fail(KATALI_HIP_E_INVALID, "F32 cols=%llu (a multiple of 4, at most 32768)", (unsigned long long)cols);
+    if (((uintptr_t)w | (uintptr_t)x) % 16) return fail(KATALI_HIP_E_INVALID, "F32 w and x must be 16-byte aligned");
+    if (rows > 0xFFFFFFFFull) return fail(KATALI_HIP_E_INVALID, "rows above 2^32");
+    return KATALI_HIP_OK;
+}
 
 int katali_hip_matvec(uint32_t type, const void *w, uint64_t rows, uint64_t cols, const float *x, float *y) {
     int rc = ensure();
-    if (rc || (rc = check_gemv(type, w, rows, cols, x, y))) return rc;
+    if (rc) return rc;
+    if (type == KATALI_HIP_TYPE_F32) {
+        if ((rc = check_gemv_f32(w, rows, cols, x, y)) || !rows) return rc;
+        return launched(kq::launch_gemv_f32((const float *)w, rows, cols, x, y, g_stream), "matvec F32");
+    }
+    if ((rc = check_gemv(type, w, rows, cols, x, y))) return rc;
     if (!rows) return KATALI_HIP_OK;
     const int mode = (env_on("KATALI_CUDA_DP4A") || env_on("KATALI_HIP_DP4A")) ? 2 : 0;
     return launched(kq::launch_gemv(type, (const uint8_t *)w, rows, cols, x, nullptr, y, mode, g_stream), "matvec");
@@ -483,6 +497,37 @@ int katali_hip_add_rmsnorm(float *x, const float *delta, float scale, const floa
     if (rc || (rc = check_norm(x, w, n, out))) return rc;
     if (!delta) return fail(KATALI_HIP_E_INVALID, "null buffer");
     return launched(kq::launch_add_rmsnorm(x, delta, scale, w, (uint32_t)n, eps, out, g_stream), "add_rmsnorm");
+}
+
+static bool overlap(const void *a, uint64_t an, const void *b, uint64_t bn) {
+    if (!a || !b) return false;
+    const uintptr_t pa = (uintptr_t)a, pb = (uintptr_t)b;
+    return pa < pb + bn && pb < pa + an;
+}
+
+int katali_hip_rmsnorm_matvec_f32(const float *x, const float *delta, float scale, float *x_out, const float *nw,
+                                  uint64_t n, float eps, float *xn, const float *w, uint64_t rows, float *y) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!x || !nw || !xn || !w || !y || (delta && !x_out)) return fail(KATALI_HIP_E_INVALID, "null buffer");
+    if (n < 4 || n > 8192 || n % 4) return fail(KATALI_HIP_E_INVALID, "n=%llu (a multiple of 4 in 4..8192)",
+                                                (unsigned long long)n);
+    if (rows == 0 || rows > 0xFFFFFFFFull) return fail(KATALI_HIP_E_INVALID, "rows=%llu", (unsigned long long)rows);
+    if (((uintptr_t)x | (uintptr_t)delta | (uintptr_t)x_out | (uintptr_t)nw | (uintptr_t)xn | (uintptr_t)w) % 16)
+        return fail(KATALI_HIP_E_INVALID, "vectors and W must be 16-byte aligned");
+    const uint64_t vb = n * 4, wb = rows * n * 4, yb = rows * 4;
+    const void *ins[4] = {x, delta, nw, w};
+    const uint64_t inb[4] = {vb, vb, vb, wb};
+    const void *outs[3] = {delta ? x_out : nullptr, xn, y};
+    const uint64_t outb[3] = {vb, vb, yb};
+    for (int o = 0; o < 3; o++) {
+        for (int i = 0; i < 4; i++)
+            if (overlap(outs[o], outb[o], ins[i], inb[i])) return fail(KATALI_HIP_E_INVALID, "an output overlaps an input");
+        for (int p = o + 1; p < 3; p++)
+            if (overlap(outs[o], outb[o], outs[p], outb[p])) return fail(KATALI_HIP_E_INVALID, "outputs overlap");
+    }
+    return launched(kq::launch_norm_router(x, delta, scale, x_out, nw, n, eps, xn, w, rows, y, g_stream),
+                    "rmsnorm_matvec_f32");
 }
 
 int katali_hip_argmax(const float *x, uint64_t n, int32_t *out) {

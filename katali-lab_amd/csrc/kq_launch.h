@@ -20,6 +20,14 @@ hipError_t launch_quantize_q8_1(const float *x, uint64_t n, uint8_t *out, hipStr
 //  mode 2: fp32 activation quantized to q8_1 inside every workgroup
 hipError_t launch_gemv(uint32_t type, const uint8_t *w, uint64_t rows, uint64_t cols, const float *xf,
                        const uint8_t *xq, float *y, int mode, hipStream_t s);
+// y = W . x for fp32 W [rows][cols] (cols % 4 == 0, w and x 16-byte aligned),
+// bit-identical to the engine's AVX2 F32 dot.
+hipError_t launch_gemv_f32(const float *w, uint64_t rows, uint64_t cols, const float *x, float *y, hipStream_t s);
+// Residual step (delta != nullptr), RMSNorm and F32 GEMV in one launch
+// (n <= 8192, n % 4 == 0, rows >= 1, x_out apart from x).
+hipError_t launch_norm_router(const float *x, const float *delta, float scale, float *x_out, const float *nw,
+                              uint64_t n, float eps, float *xn, const float *w, uint64_t rows, float *y,
+                              hipStream_t s);
 
 // Up to GEMV_MULTI_MAX GEMVs sharing one fp32 activation in one launch
 // (mode 0 or 2 as above); every output is bit-identical to launch_gemv's.

@@ -102,7 +102,8 @@ int katali_dense_hip_matvec_multi(int n, const uint32_t *types, const void *cons
     /* One launch for all n tensors: their outputs sit back to back in g_y. */
     uint64_t total = 0, off[4];
     for (int i = 0; i < n; i++) {
-        if (!ws[i] || !ys[i] || !katali_gpu_supports_type(types[i])) return -1;
+        if (!ws[i] || !ys[i] || types[i] == 0 /* F32: single matvec only */ || !katali_gpu_supports_type(types[i]))
+            return -1;
         off[i] = total;
         total += rows[i];
     }

@@ -111,6 +111,7 @@ static int load(void) {
     LOAD(matvec_multi_dp4a, "katali_hip_matvec_multi_dp4a");
     LOAD(rmsnorm, "katali_hip_rmsnorm");
     LOAD(add_rmsnorm, "katali_hip_add_rmsnorm");
+    LOAD(rmsnorm_matvec_f32, "katali_hip_rmsnorm_matvec_f32");
     if (g_api.abi_version() != KATALI_HIP_ABI_VERSION) {
         snprintf(g_status, sizeof g_status, "%s: ABI version %d, loader expects %d", tried, g_api.abi_version(),
                  KATALI_HIP_ABI_VERSION);
@@ -187,6 +188,10 @@ int katali_gpu_rmsnorm(const float *x, const float *w, uint64_t n, float eps, fl
 int katali_gpu_add_rmsnorm(float *x, const float *delta, float scale, const float *w, uint64_t n, float eps,
                            float *out) {
     FORWARD(g_api.add_rmsnorm(x, delta, scale, w, n, eps, out));
+}
+int katali_gpu_rmsnorm_matvec_f32(const float *x, const float *delta, float scale, float *x_out, const float *nw,
+                                  uint64_t n, float eps, float *xn, const float *w, uint64_t rows, float *y) {
+    FORWARD(g_api.rmsnorm_matvec_f32(x, delta, scale, x_out, nw, n, eps, xn, w, rows, y));
 }
 int katali_gpu_moe_batch(const KataliHipMoe *moe, const KataliHipMoeBatch *batch, const float *x, float *y) {
     FORWARD(g_api.moe_batch(moe, batch, x, y));

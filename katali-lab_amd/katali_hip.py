@@ -61,6 +61,7 @@ SIGNATURES = {
     "katali_hip_matvec_multi_dp4a": (C.c_int, [C.c_int, _vp, _vp, _vp, _u64, _vp, _vp]),
     "katali_hip_rmsnorm": (C.c_int, [_vp, _vp, _u64, _f32, _vp]),
     "katali_hip_add_rmsnorm": (C.c_int, [_vp, _vp, _f32, _vp, _u64, _f32, _vp]),
+    "katali_hip_rmsnorm_matvec_f32": (C.c_int, [_vp, _vp, _f32, _vp, _vp, _u64, _f32, _vp, _vp, _u64, _vp]),
 }
 
 
@@ -195,6 +196,12 @@ class KataliHip:
 
     def add_rmsnorm(self, x, delta, scale, w, n, eps, out) -> None:
         self.check(self.lib.katali_hip_add_rmsnorm(x.ptr, delta.ptr, scale, w.ptr, n, eps, out.ptr))
+
+    def rmsnorm_matvec_f32(self, x, delta, scale, x_out, norm_w, n, eps, xn, w, rows, y) -> None:
+        """x_out = x + scale*delta (delta not None); xn = RMSNorm(.)*norm_w; y = W . xn."""
+        p = lambda b: None if b is None else b.ptr  # noqa: E731
+        self.check(self.lib.katali_hip_rmsnorm_matvec_f32(x.ptr, p(delta), scale, p(x_out), norm_w.ptr, n, eps,
+                                                          xn.ptr, w.ptr, rows, y.ptr))
 
     def block_isums(self, t, w, rows, cols, xq, out) -> None:
         self.check(self.lib.katali_hip_block_isums(t, w.ptr, rows, cols, xq.ptr, out.ptr))

@@ -32,13 +32,15 @@ KERNELS = {
     "moe40cold": ("k_moe_gu", "k_moe_down"),
     "gemv6144": ("k_gemv",),
     "qwen8b": ("k_moe_down", "k_moe_gu", "k_gemv_multi", "k_gemv"),
+    "moe48tok": ("k_argmax_final", "k_norm_router", "k_moe_gu", "k_moe_down", "k_rmsnorm", "k_gemv",
+                 "k_argmax_part"),
     "moebatch": ("k_mb_group", "k_quantize_q8_1", "k_moe_gu_grp", "k_mb_gu_mfma", "k_moe_down_grp", "k_mb_down_mfma",
                  "k_mb_combine"),
 }
 UNIT_NAME = {"moe48": "MoE layer", "moe40cold": "MoE layer", "gemv6144": "GEMV", "qwen8b": "dense layer",
-             "moebatch": "batched MoE layer (n_sel 8, 64 tokens)"}
+             "moebatch": "batched MoE layer (n_sel 8, 64 tokens)", "moe48tok": "decode token"}
 EXTRA_ARGS = {"moebatch": ["--batch-points", "8x64"]}
-PROFILE_NAME = {"moebatch": "batched_moe_moebatch_8x64", "qwen8b": "k_gemv_k_moe_gu_k_moe_down_qwen8b"}
+PROFILE_NAME = {"moebatch": "batched_moe_moebatch_8x64", "moe48tok": "decode_token_moe48tok", "qwen8b": "k_gemv_k_moe_gu_k_moe_down_qwen8b"}
 
 
 def run(cmd, log):

@@ -297,8 +297,26 @@ float kqo_dot_q6_K_avx2order(const uint8_t *row, const float *x, uint64_t nb) {
     return (float)acc;
 }
 
+float kqo_dot_f32_avx2order(const float *w, const float *x, uint64_t n) {
+    float a[16] = {0};
+    uint64_t i = 0;
+    for (; i + 16 <= n; i += 16)
+        for (int j = 0; j < 16; j++) a[j] = fmaf(w[i + j], x[i + j], a[j]);
+    float v[8], l[4];
+    for (int k = 0; k < 8; k++) v[k] = a[k] + a[k + 8];
+    for (int k = 0; k < 4; k++) l[k] = v[k] + v[k + 4];
+    const float acc = (l[0] + l[1]) + (l[2] + l[3]);
+    double tail = 0.0;
+    for (; i < n; i++) tail += (double)w[i] * (double)x[i];
+    return acc + (float)tail;
+}
+
 int kqo_matvec_f32x(uint32_t type, const void *w, uint64_t rows, uint64_t cols,
                     const float *x, float *y) {
+    if (type == KQO_F32) {
+        for (uint64_t r = 0; r < rows; r++) y[r] = kqo_dot_f32_avx2order((const float *)w + r * cols, x, cols);
+        return 0;
+    }
     const uint64_t rb = kqo_row_bytes(type, cols);
     if (!rb || (type != KQO_Q4_K && type != KQO_Q6_K)) return -1;
     const uint8_t *wb = (const uint8_t *)w;

@@ -74,9 +74,15 @@ float kqo_dot_q4_K_scalar(const uint8_t *row, const float *x, uint64_t nb);
 float kqo_dot_q4_K_avx2order(const uint8_t *row, const float *x, uint64_t nb);
 /* gguf_simd_x86.c:566-629 */
 float kqo_dot_q6_K_avx2order(const uint8_t *row, const float *x, uint64_t nb);
+/* gguf_simd_x86.c:111-122 with hsum256_ps (:80-89): 16 fp32 fma chains
+ * (chain j over columns j, j+16, ... of the first n & ~15), chains j and j+8
+ * added, then ((v0+v4)+(v1+v5)) + ((v2+v6)+(v3+v7)); the columns past that
+ * summed in double and added as float. The F32 row loop (rows_f32, :674-682). */
+float kqo_dot_f32_avx2order(const float *w, const float *x, uint64_t n);
 /* The reference fp32 matvec row loop (gguf_dtype.c:731-856 ->
  * gguf_simd_x86.c:699-736, 865-893): y[r] = fast dot of row r. Rows are
- * independent, so the result does not depend on the thread partition. */
+ * independent, so the result does not depend on the thread partition.
+ * Types Q4_K, Q6_K and F32 (row stride 4·cols). */
 int kqo_matvec_f32x(uint32_t type, const void *w, uint64_t rows, uint64_t cols,
                     const float *x, float *y);
 /* Same result, rows split over n_threads pthreads (contiguous ranges). */

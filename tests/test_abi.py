@@ -77,7 +77,7 @@ int main(void) {
                     B.weights.offset]
 
 
-@pytest.mark.parametrize("t,ok", [(12, 1), (14, 1), (0, 0), (2, 0), (13, 0)])
+@pytest.mark.parametrize("t,ok", [(12, 1), (14, 1), (0, 1), (2, 0), (13, 0)])
 def test_supports_type(t, ok):
     assert K.KataliHip().lib.katali_hip_supports_type(t) == ok
 

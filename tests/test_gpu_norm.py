@@ -65,3 +65,51 @@ def test_norm_rejects_bad_arguments(hip):
         with pytest.raises(HipError):
             hip.rmsnorm(x, x, n, 1e-6, x)
     assert hip.lib.katali_hip_add_rmsnorm(x.ptr, None, 1.0, x.ptr, 4, 1e-6, x.ptr) == -1
+
+
+NR_CASES = [
+    # n, rows, residual scale (None: no residual step)
+    (2048, 128, 1.0), (2048, 128, None), (4096, 256, 0.5), (7168, 300, 1.0), (8192, 1030, None),
+    (1000, 64, 1.0), (12, 1, 1.0), (3072, 513, 0.25),
+]
+
+
+@pytest.mark.parametrize("n,rows,scale", NR_CASES)
+def test_norm_router_bit_identical(hip, oracle, n, rows, scale):
+    """Residual step + RMSNorm + F32 router logits in one launch: each output
+    bit-identical to the oracle's separate steps."""
+    print(f"[norm-router] n={n} rows={rows} scale={scale}", flush=True)
+    rng = np.random.default_rng(n + rows)
+    x, d, nw = (rng.standard_normal(n).astype(np.float32) for _ in range(3))
+    w = (rng.standard_normal((rows, n)) * 0.05).astype(np.float32)
+    xd, dd, nwd, wd = hip.to_device(x), hip.to_device(d), hip.to_device(nw), hip.to_device(w)
+    xo, xn, y = hip.alloc(n * 4), hip.alloc(n * 4), hip.alloc(rows * 4)
+    if scale is None:
+        hip.rmsnorm_matvec_f32(xd, None, 1.0, None, nwd, n, 1e-6, xn, wd, rows, y)
+        want_x, want_xn = x, oracle.rmsnorm(x, nw, 1e-6)
+    else:
+        hip.rmsnorm_matvec_f32(xd, dd, scale, xo, nwd, n, 1e-6, xn, wd, rows, y)
+        want_x, want_xn = oracle.add_rmsnorm(x, d, scale, nw, 1e-6)
+        assert np.array_equal(xo.download(np.uint32, n), want_x.view(np.uint32))
+    assert np.array_equal(xd.download(np.uint32, n), x.view(np.uint32))          # x untouched
+    assert np.array_equal(xn.download(np.uint32, n), want_xn.view(np.uint32))
+    want_y = oracle.matvec_f32x(0, w, rows, n, want_xn)
+    assert np.array_equal(y.download(np.uint32, rows), want_y.view(np.uint32))
+
+
+def test_norm_router_rejects_bad_arguments(hip):
+    from katali_hip import HipError
+    n, rows = 256, 8
+    a, b, c, xn, w, y = (hip.alloc(n * rows * 4) for _ in range(6))
+    bad = [
+        (a, b, 1.0, None, c, n, 1e-6, xn, w, rows, y),      # residual without x_out
+        (a, b, 1.0, a, c, n, 1e-6, xn, w, rows, y),         # x_out is x
+        (a, None, 1.0, None, c, n, 1e-6, a, w, rows, y),    # xn is x
+        (a, None, 1.0, None, c, n, 1e-6, xn, w, rows, w),   # y inside W
+        (a, None, 1.0, None, c, 8196, 1e-6, xn, w, 1, y),   # n above 8192
+        (a, None, 1.0, None, c, 6, 1e-6, xn, w, rows, y),   # n % 4
+        (a, None, 1.0, None, c, n, 1e-6, xn, w, 0, y),      # no rows
+    ]
+    for args in bad:
+        with pytest.raises(HipError):
+            hip.rmsnorm_matvec_f32(*args)
