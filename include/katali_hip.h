@@ -145,7 +145,7 @@ int katali_hip_add_rmsnorm(float *x_dev, const float *delta_dev, float scale, co
  * (bit-identical to both: V/src/gguf_model.c:677-683 followed by the F32
  * router product, V/src/gguf_simd_x86.c:111-122). The new residual goes to
  * x_out, a buffer apart from x (x is read by every workgroup); with delta
- * NULL, x_out is unused and may be NULL. 4 <= n <= 8192, n % 4 == 0, rows >= 1,
+ * NULL, x_out is unused and may be NULL. 4 <= n <= 8192, n % 4 == 0, 1 <= rows < 2^31,
  * all vectors and W 16-byte aligned; outputs must not overlap inputs. */
 int katali_hip_rmsnorm_matvec_f32(const float *x_dev, const float *delta_dev, float scale, float *x_out_dev,
                                   const float *norm_w_dev, uint64_t n, float eps, float *xn_dev,

@@ -512,7 +512,7 @@ int katali_hip_rmsnorm_matvec_f32(const float *x, const float *delta, float scal
     if (!x || !nw || !xn || !w || !y || (delta && !x_out)) return fail(KATALI_HIP_E_INVALID, "null buffer");
     if (n < 4 || n > 8192 || n % 4) return fail(KATALI_HIP_E_INVALID, "n=%llu (a multiple of 4 in 4..8192)",
                                                 (unsigned long long)n);
-    if (rows == 0 || rows > 0xFFFFFFFFull) return fail(KATALI_HIP_E_INVALID, "rows=%llu", (unsigned long long)rows);
+    if (rows == 0 || rows > 0x7FFFFFFFull) return fail(KATALI_HIP_E_INVALID, "rows=%llu", (unsigned long long)rows);
     if (((uintptr_t)x | (uintptr_t)delta | (uintptr_t)x_out | (uintptr_t)nw | (uintptr_t)xn | (uintptr_t)w) % 16)
         return fail(KATALI_HIP_E_INVALID, "vectors and W must be 16-byte aligned");
     const uint64_t vb = n * 4, wb = rows * n * 4, yb = rows * 4;

@@ -193,6 +193,56 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// sum of a double over the 64 lanes of a wave, every lane gets it: the same
+// DPP and permlane-swap butterfly as group_sum<64>, on both 32-bit halves
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+    const uint64_t u = (uint64_t)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)dpp_i<CTRL>((int)(uint32_t)u);
+    const uint32_t hi = (uint32_t)dpp_i<CTRL>((int)(uint32_t)(u >> 32));
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+template <int OFF>
+__device__ __forceinline__ double swap_sum_f64(double v) {
+    const uint64_t u = (uint64_t)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)u, hi = (uint32_t)(u >> 32);
+    uint32_t l0, l1, h0, h1;
+    if constexpr (OFF == 32) {
+        const auto rl = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+        const auto rh = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+        l0 = rl[0]; l1 = rl[1]; h0 = rh[0]; h1 = rh[1];
+    } else {
+        const auto rl = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+        const auto rh = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+        l0 = rl[0]; l1 = rl[1]; h0 = rh[0]; h1 = rh[1];
+    }
+    return __longlong_as_double((long long)(((uint64_t)h0 << 32) | l0)) +
+           __longlong_as_double((long long)(((uint64_t)h1 << 32) | l1));
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+    v += dpp_d<DPP_XOR1>(v);
+    v += dpp_d<DPP_XOR2>(v);
+    v += dpp_d<DPP_HALF_MIRROR>(v);
+    v += dpp_d<DPP_MIRROR>(v);
+    v = swap_sum_f64<16>(v);
+    return swap_sum_f64<32>(v);
+}
+
+// The engine's AVX2 horizontal sum of 16 fp32 accumulators
+// (vendor/katali_gguf_dense/src/gguf_simd_x86.c:80-89, 118: a0 + a1, then
+// hsum256_ps) over the 16 lanes of a DPP row, lane k holding accumulator k:
+// v_k = a_k + a_{k+8} (row_ror 8 is lane ^ 8), l_k = v_k + v_{k+4} (row_ror 4;
+// v is 8-periodic after the first step), then (l0 + l1) + (l2 + l3) (lane ^ 1,
+// lane ^ 2). Every add is commutative, so each lane of the row ends with the
+// same bits.
+constexpr int DPP_ROR8 = 0x128, DPP_ROR4 = 0x124;
+__device__ __forceinline__ float hsum16_avx2_order(float a) {
+    float v = a + dpp_f<DPP_ROR8>(a);
+    v = v + dpp_f<DPP_ROR4>(v);
+    v = v + dpp_f<DPP_XOR1>(v);
+    return v + dpp_f<DPP_XOR2>(v);
+}
+
 // exp by Cody-Waite reduction x = n*ln2 + r (ln2 split into a 15-bit high part,
 // exact for |n| <= 256, and a low correction) and a degree-7 Taylor polynomial
 // for e^r, |r| <= ln2/2, evaluated by Horner with fused multiply-adds. Every

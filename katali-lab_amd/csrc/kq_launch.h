@@ -24,7 +24,8 @@ hipError_t launch_gemv(uint32_t type, const uint8_t *w, uint64_t rows, uint64_t 
 // bit-identical to the engine's AVX2 F32 dot.
 hipError_t launch_gemv_f32(const float *w, uint64_t rows, uint64_t cols, const float *x, float *y, hipStream_t s);
 // Residual step (delta != nullptr), RMSNorm and F32 GEMV in one launch
-// (n <= 8192, n % 4 == 0, rows >= 1, x_out apart from x).
+// (n <= 8192, n % 4 == 0, 1 <= rows < 2^31, x_out apart from x; one
+// workgroup per row).
 hipError_t launch_norm_router(const float *x, const float *delta, float scale, float *x_out, const float *nw,
                               uint64_t n, float eps, float *xn, const float *w, uint64_t rows, float *y,
                               hipStream_t s);

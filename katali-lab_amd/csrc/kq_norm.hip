@@ -7,9 +7,9 @@
 // delta[i], or x[i] += scale * delta[i] when the model scales its residual.
 //
 // One workgroup of 1024 threads: each thread adds and squares its elements
-// (t, t + 1024, ...), the double partial sums meet in a fixed tree (wave,
-// then the 16 wave sums in order), every thread forms the same inv and
-// writes its outputs. The double sum is in a different order than the
+// (t, t + 1024, ...), the double partial sums meet in a fixed tree (a DPP
+// and permlane butterfly in each wave, then the 16 wave sums in order), every
+// thread forms the same inv and writes its outputs. The double sum is in a different order than the
 // engine's loop; its rounding to float is the same unless the two doubles
 // straddle a float rounding boundary (relative distance ~2^-29).
 #include "kq_device.h"
@@ -18,13 +18,6 @@
 namespace kq {
 
 constexpr uint32_t NORM_THREADS = 1024;
-
-__device__ __forceinline__ double shfl_xor_f64(double v, int o) {
-    const uint64_t u = (uint64_t)__double_as_longlong(v);
-    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)u, o, WAVE);
-    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(u >> 32), o, WAVE);
-    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
-}
 
 template <bool ADD>
 __global__ void __launch_bounds__(NORM_THREADS)
@@ -41,8 +34,7 @@ __global__ void __launch_bounds__(NORM_THREADS)
         }
         s += (double)v * (double)v;
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) s += shfl_xor_f64(s, o);
+    s = wave_sum_f64(s);
     if (lane == 0) part[wave] = s;
     __syncthreads();
     double sumsq = part[0];
