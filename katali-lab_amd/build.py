@@ -75,10 +75,11 @@ def build_host() -> list[str]:
         return outs
     loader = os.path.join(HOST, "katali_hip_loader.c")
     dense = os.path.join(HOST, "katali_dense_hip.c")
+    gguf = os.path.join(HOST, "katali_hip_gguf.c")
     cli = os.path.join(HOST, "katali_hip_cli.c")
     if os.path.exists(loader):
         so = os.path.join(PKG, "libkatali_hip_loader.so")
-        srcs = [loader] + ([dense] if os.path.exists(dense) else [])
+        srcs = [loader] + [p for p in (dense, gguf) if os.path.exists(p)]
         _run([CC, *C_FLAGS, "-shared", *srcs, "-o", so, "-ldl"])
         outs.append(so)
         if os.path.exists(cli):

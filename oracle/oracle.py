@@ -258,6 +258,32 @@ class RefCPU:
         L.kref_sample_greedy.restype = _i32
         L.kref_sample_greedy.argtypes = [_vp, _i32]
 
+    def gguf_table(self, path: str, cap: int = 64):
+        """The reference reader's verdict on a GGUF file: None when it refuses
+        it, else (header (version, alignment, data_offset), tensor table)."""
+        L = self.lib
+        if not hasattr(self, "_gguf_sig"):
+            L.kref_gguf_table.restype = C.c_int64
+            L.kref_gguf_table.argtypes = [C.c_char_p, C.c_int64] + [_vp] * 8
+            self._gguf_sig = True
+        names = C.create_string_buffer(64 * cap)
+        nd = np.zeros(cap, np.uint32)
+        dims = np.zeros((cap, 4), np.uint64)
+        types = np.zeros(cap, np.uint32)
+        offs = np.zeros(cap, np.uint64)
+        nbytes = np.zeros(cap, np.uint64)
+        pos = np.zeros(cap, np.int64)
+        hdr = np.zeros(3, np.uint64)
+        n = L.kref_gguf_table(path.encode(), cap, names, _ptr(nd), _ptr(dims), _ptr(types), _ptr(offs), _ptr(nbytes),
+                              _ptr(pos), _ptr(hdr))
+        if n < 0:
+            return None
+        raw = names.raw
+        table = [{"name": raw[64 * i:64 * i + 64].split(b"\0")[0].decode(), "n_dims": int(nd[i]),
+                  "dims": [int(v) for v in dims[i]], "type": int(types[i]), "offset": int(offs[i]),
+                  "nbytes": int(nbytes[i]), "data_pos": int(pos[i])} for i in range(min(n, cap))]
+        return (int(hdr[0]), int(hdr[1]), int(hdr[2])), table
+
     def simd(self) -> bool:
         return bool(self.lib.katali_ggml_simd_available())
 

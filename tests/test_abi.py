@@ -83,16 +83,17 @@ def test_supports_type(t, ok):
 
 
 def test_loader_exports_its_headers():
-    """libkatali_hip_loader.so (the engine-side loader and dense shim) exports
-    every function include/katali_hip_loader.h and include/katali_dense_hip.h
-    declare."""
+    """libkatali_hip_loader.so (the engine-side loader, dense shim and GGUF
+    module) exports every function include/katali_hip_loader.h,
+    include/katali_dense_hip.h and include/katali_hip_gguf.h declare."""
     so = os.path.join(REPO, "katali-lab_amd", "libkatali_hip_loader.so")
     assert os.path.exists(so), "run python katali-lab_amd/build.py"
     names = set()
-    for h, prefix in (("katali_hip_loader.h", "katali_gpu_"), ("katali_dense_hip.h", "katali_dense_hip_")):
+    for h, prefix in (("katali_hip_loader.h", "katali_gpu_"), ("katali_dense_hip.h", "katali_dense_hip_"),
+                      ("katali_hip_gguf.h", "katali_hip_(?:gguf|weights|tier|ggml)_")):
         src = re.sub(r"/\*.*?\*/", "", open(os.path.join(REPO, "include", h)).read(), flags=re.S)
         names |= set(re.findall(r"\b(" + prefix + r"\w+)\s*\(", src))
-    assert "katali_gpu_moe_batch" in names and "katali_dense_hip_matvec" in names
+    assert "katali_gpu_moe_batch" in names and "katali_dense_hip_matvec" in names and "katali_hip_tier_layer" in names
     out = subprocess.run(["nm", "-D", "--defined-only", so], capture_output=True, text=True).stdout
-    exported = set(re.findall(r"\bT (katali_(?:gpu|dense_hip)_\w+)", out))
+    exported = set(re.findall(r"\bT (katali_(?:gpu|dense_hip|hip_gguf|hip_weights|hip_tier|hip_ggml)_\w+)", out))
     assert names <= exported, names - exported
