@@ -214,14 +214,19 @@ class KataliHip:
                          p(gate), p(up), p(down), None, None, None)
         if shared is not None:
             d.gate_shexp, d.up_shexp, d.down_shexp = shared[0].ptr, shared[1].ptr, shared[2].ptr
+        # the struct holds raw device pointers: keep their buffers alive with it
+        # (a temporary DeviceBuffer would otherwise be freed before a layer runs)
+        d._keep = (gate, up, down, shared)
         return d
 
     @staticmethod
     def moe_route(n_sel, logits=None, ids=None, weights=None, step=None, logits_stride=0,
                   ids_out=None, weights_out=None) -> KataliHipMoeRoute:
         p = lambda b: None if b is None else b.ptr  # noqa: E731
-        return KataliHipMoeRoute(C.sizeof(KataliHipMoeRoute), n_sel, p(logits), p(step), logits_stride,
-                                 p(ids), p(weights), p(ids_out), p(weights_out))
+        r = KataliHipMoeRoute(C.sizeof(KataliHipMoeRoute), n_sel, p(logits), p(step), logits_stride,
+                              p(ids), p(weights), p(ids_out), p(weights_out))
+        r._keep = (logits, ids, weights, step, ids_out, weights_out)   # as in moe_desc
+        return r
 
     def moe_layer(self, desc, route, y, x=None, xq=None) -> None:
         self.check(self.lib.katali_hip_moe_layer(C.byref(desc), C.byref(route),

@@ -21,13 +21,7 @@ import pytest
 import kq_synth as S
 from oracle import Q4_K, Q6_K
 
-pytestmark = [
-    pytest.mark.gpu,
-    pytest.mark.skip(reason="a full GPU-suite run faulted the GPU while this file's first tests ran (an illegal "
-                            "memory access reported at its first sync); the same code passed here three times "
-                            "before and no cause has been found by reading, so it stays off the GPU until one is "
-                            "shown. tests/test_gpu_gguf.py covers the same fused chain stage by stage."),
-]
+pytestmark = pytest.mark.gpu
 
 EPS = 1e-6
 
