@@ -102,3 +102,32 @@ def test_shim_matvec_on_gpu(oracle):
     assert lib.katali_dense_hip_cached() == n0 + len(mats)
     lib.katali_dense_hip_shutdown()
     assert lib.katali_dense_hip_cached() == 0
+
+
+def test_moe_structs_keep_their_buffers_alive():
+    """The MoE descriptor and route hold raw device pointers; the structs
+    must keep the buffers behind them alive, or a temporary buffer passed
+    straight into moe_desc / moe_route is freed before the layer runs."""
+    import gc
+    import weakref
+    from katali_hip import KataliHip
+
+    class Buf:   # stands in for DeviceBuffer (no device needed)
+        def __init__(self, ptr):
+            self.ptr = ptr
+
+    refs = []
+
+    def buf(p):
+        b = Buf(p)
+        refs.append(weakref.ref(b))
+        return b
+
+    d = KataliHip.moe_desc(256, 256, 4, buf(0x1000), buf(0x2000), buf(0x3000), shared=(buf(1), buf(2), buf(3)))
+    r = KataliHip.moe_route(2, logits=buf(0x4000), ids_out=buf(0x5000))
+    gc.collect()
+    assert all(ref() is not None for ref in refs)
+    assert d.gate_exps == 0x1000 and d.down_shexp == 3 and r.logits == 0x4000
+    del d, r
+    gc.collect()
+    assert all(ref() is None for ref in refs)
