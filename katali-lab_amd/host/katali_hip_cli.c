@@ -18,6 +18,12 @@
  *                                    experts, ffn 768), graph-replayed
  *   katali-hip bench-cold [tokens]   40 layers x 256 experts (ffn 512) + shared
  *                                    expert, routing rotated every token
+ *   katali-hip gguf-info FILE        a GGUF file's header, metadata and tensor
+ *                                    table (no GPU needed)
+ *   katali-hip gguf-check FILE       every MoE layer of FILE on the device: routed
+ *                                    by the file's own F32 router on N(0,1) x,
+ *                                    the fused layer vs the same layer composed
+ *                                    from separate library GEMVs
  *
  * Exit status 0 on success / PASS, 1 on a failed check, 2 when no usable GPU.
  */
@@ -26,6 +32,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "katali_hip_gguf.h"
 #include "katali_hip_loader.h"
 
 #define Q4K KATALI_HIP_TYPE_Q4_K
@@ -326,9 +333,134 @@ static int moe_bench(const char *name, uint32_t L, uint32_t H, uint32_t F, uint3
     return 0;
 }
 
+static int cmd_gguf_info(const char *path) {
+    KataliHipGguf *g = NULL;
+    char err[256];
+    if (katali_hip_gguf_open(path, &g, err, sizeof err)) {
+        printf("gguf-info: %s\n", err);
+        return 1;
+    }
+    size_t al = 0;
+    const char *arch = katali_hip_gguf_get_str(g, "general.architecture", &al);
+    printf("GGUF v%u, alignment %llu, data at %llu, architecture %.*s, %llu tensors\n", katali_hip_gguf_version(g),
+           (unsigned long long)katali_hip_gguf_alignment(g), (unsigned long long)katali_hip_gguf_data_offset(g),
+           arch ? (int)al : 1, arch ? arch : "?", (unsigned long long)katali_hip_gguf_tensor_count(g));
+    for (uint64_t i = 0; i < katali_hip_gguf_tensor_count(g); i++) {
+        KataliHipGgufTensor t;
+        katali_hip_gguf_tensor(g, i, &t);
+        printf("  %-40s type %2u dims", t.name, t.type);
+        for (uint32_t d = 0; d < t.n_dims; d++) printf(" %llu", (unsigned long long)t.dims[d]);
+        printf("  %llu bytes%s\n", (unsigned long long)t.nbytes, t.data ? "" : " (no data: unknown type)");
+    }
+    katali_hip_gguf_close(g);
+    return 0;
+}
+
+/* One layer of the file: the fused layer routed by the file's router on
+ * N(0,1) x, against the same layer composed from separate library GEMVs
+ * (q8 gate/up GEMVs, SiLU-GLU on the host, q8 down GEMV, the weighted sum in
+ * rank order with the shared expert last, as the fused layer forms it). */
+static int gguf_check_layer(KataliHipWeights *w, uint32_t l, int n_sel) {
+    KataliHipMoe m;
+    const float *router = NULL;
+    if (katali_hip_gguf_moe_layer(w, l, &m, &router, NULL)) {
+        printf("gguf-check layer %u: %s\n", l, katali_hip_gguf_last_error());
+        return 1;
+    }
+    const uint32_t H = m.hidden, F = m.ffn, E = m.n_expert, K = (uint32_t)n_sel;
+    const uint64_t rbg = row_bytes(m.gate_type, H), rbd = row_bytes(m.down_type, F);
+    float *x = dalloc_f(H), *y = dalloc_f(H), *logits = dalloc_f(E), *gv = dalloc_f(F), *uv = dalloc_f(F),
+          *h = dalloc_f(F), *dv = dalloc_f(H), *wo = dalloc_f(16);
+    void *xq = NULL, *hq = NULL, *ido = NULL;
+    CK(api->malloc_(&xq, H / 32 * 36));
+    CK(api->malloc_(&hq, F / 32 * 36));
+    CK(api->malloc_(&ido, 64));
+    CK(api->synth_normal(x, H, 31 + l, 1.0f));
+    CK(api->matvec(0, router, E, H, x, logits));
+    KataliHipMoeRoute r;
+    memset(&r, 0, sizeof r);
+    r.struct_size = sizeof r;
+    r.n_sel = (int32_t)K;
+    r.logits = logits;
+    r.ids_out = (int32_t *)ido;
+    r.weights_out = wo;
+    CK(api->moe_layer(&m, &r, x, NULL, y));
+    float *fused = malloc(H * 4), *ref = calloc(H, 4), *gh = malloc(F * 4), *uh = malloc(F * 4),
+          *hh = malloc(F * 4), *dh = malloc(H * 4), wts[16];
+    int32_t ids[16];
+    CK(api->download(fused, y, H * 4));
+    CK(api->download(ids, ido, K * 4));
+    CK(api->download(wts, wo, K * 4));
+    CK(api->quantize_q8_1(x, H, xq));
+    const int shared = m.gate_shexp != NULL;
+    for (uint32_t k = 0; k < K + (shared ? 1 : 0); k++) {
+        const int sh = k == K;
+        const uint8_t *ge = sh ? m.gate_shexp : (const uint8_t *)m.gate_exps + (uint64_t)ids[k] * F * rbg;
+        const uint8_t *ue = sh ? m.up_shexp : (const uint8_t *)m.up_exps + (uint64_t)ids[k] * F * rbg;
+        const uint8_t *de = sh ? m.down_shexp : (const uint8_t *)m.down_exps + (uint64_t)ids[k] * H * rbd;
+        CK(api->matvec_q8(m.gate_type, ge, F, H, xq, gv));
+        CK(api->matvec_q8(m.up_type, ue, F, H, xq, uv));
+        CK(api->download(gh, gv, F * 4));
+        CK(api->download(uh, uv, F * 4));
+        for (uint32_t j = 0; j < F; j++) hh[j] = silu_mul(gh[j], uh[j]);
+        CK(api->upload(h, hh, F * 4));
+        CK(api->quantize_q8_1(h, F, hq));
+        CK(api->matvec_q8(m.down_type, de, H, F, hq, dv));
+        CK(api->download(dh, dv, H * 4));
+        const float wk = sh ? 1.0f : wts[k];
+        for (uint32_t i = 0; i < H; i++) ref[i] = fmaf(wk, dh[i], ref[i]);
+    }
+    size_t outside = 0;
+    const double rel = rel_l2(fused, ref, H, &outside);
+    const int ok = rel <= 1e-4;
+    printf("gguf-check layer %u: hidden %u ffn %u top-%u of %u%s, experts", l, H, F, K, E, shared ? " + shared" : "");
+    for (uint32_t k = 0; k < K; k++) printf(" %d", ids[k]);
+    printf(": rel_L2(fused, composed) = %.3e %s\n", rel, ok ? "PASS" : "FAIL");
+    void *bufs[] = {x, y, logits, gv, uv, h, dv, wo, xq, hq, ido};
+    for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) api->free_(bufs[i]);
+    free(fused); free(ref); free(gh); free(uh); free(hh); free(dh);
+    return ok ? 0 : 1;
+}
+
+static int cmd_gguf_check(const char *path) {
+    KataliHipGguf *g = NULL;
+    char err[256];
+    if (katali_hip_gguf_open(path, &g, err, sizeof err)) {
+        printf("gguf-check: %s\n", err);
+        return 1;
+    }
+    size_t al = 0;
+    const char *arch = katali_hip_gguf_get_str(g, "general.architecture", &al);
+    char key[96];
+    snprintf(key, sizeof key, "%.*s.expert_used_count", arch ? (int)al : 0, arch ? arch : "");
+    const int n_sel = (int)katali_hip_gguf_get_int(g, key, 8);
+    snprintf(key, sizeof key, "%.*s.block_count", arch ? (int)al : 0, arch ? arch : "");
+    const int64_t L = katali_hip_gguf_get_int(g, key, 0);
+    KataliHipWeights *w = NULL;
+    int fails = 0, layers = 0;
+    if (katali_hip_weights_create(g, 0, &w)) {
+        printf("gguf-check: %s\n", katali_hip_gguf_last_error());
+        katali_hip_gguf_close(g);
+        return 1;
+    }
+    for (int64_t l = 0; l < L; l++) {
+        char name[64];
+        snprintf(name, sizeof name, "blk.%lld.ffn_gate_exps.weight", (long long)l);
+        KataliHipGgufTensor t;
+        if (katali_hip_gguf_find(g, name, &t)) continue;   /* a dense layer */
+        fails += gguf_check_layer(w, (uint32_t)l, n_sel);
+        layers++;
+    }
+    printf("gguf-check: %d MoE layer(s), %d failed, %.2f GB resident\n", layers, fails,
+           katali_hip_weights_resident_bytes(w) / 1e9);
+    katali_hip_weights_destroy(w);
+    katali_hip_gguf_close(g);
+    return (fails || !layers) ? 1 : 0;
+}
+
 static void usage(void) {
     fputs("usage: katali-hip info | dp4a-selftest | check | check-moe | matvec-bench [reps] | bench [tokens] |"
-          " bench-cold [tokens]\n", stderr);
+          " bench-cold [tokens] | gguf-info FILE | gguf-check FILE\n", stderr);
 }
 
 int main(int argc, char **argv) {
@@ -338,6 +470,7 @@ int main(int argc, char **argv) {
     }
     const char *cmd = argv[1];
     const int n = argc > 2 ? atoi(argv[2]) : 0;
+    if (!strcmp(cmd, "gguf-info") && argc > 2) return cmd_gguf_info(argv[2]);
     if (!katali_gpu_probe() || !(api = katali_gpu_api())) {
         printf("no usable GPU: %s\n", katali_gpu_status());
         return 2;
@@ -349,6 +482,7 @@ int main(int argc, char **argv) {
     if (!strcmp(cmd, "matvec-bench")) return cmd_matvec_bench(n > 0 ? n : 5);
     if (!strcmp(cmd, "bench")) return moe_bench("bench", 48, 2048, 768, 128, 8, 0, n > 0 ? n : 32);
     if (!strcmp(cmd, "bench-cold")) return moe_bench("bench-cold", 40, 2048, 512, 256, 8, 1, n > 0 ? n : 64);
+    if (!strcmp(cmd, "gguf-check") && argc > 2) return cmd_gguf_check(argv[2]);
     usage();
     return 2;
 }
