@@ -4,9 +4,9 @@
  * (katali_dense_cuda_enabled / _matvec / _matvec_multi / _shutdown). The
  * engine's functions take a KataliGgufTensor; these take the fields the shim
  * reads from it (type, data, nbytes, dims[1] = rows, dims[0] = cols;
- * katali_gguf.h:67) so this header needs nothing from the engine. The
- * engine-side forwarding (three lines per function) is shown in
- * INTEGRATION.md. Returns 0 on success and -1 on any failure: the caller then
+ * katali_gguf.h:67) so this header needs nothing from the engine; the
+ * engine's katali_dense_cuda_* functions forward to these in three lines
+ * each. Returns 0 on success and -1 on any failure: the caller then
  * computes on the CPU, exactly as with the CUDA shim. */
 #ifndef KATALI_DENSE_HIP_H
 #define KATALI_DENSE_HIP_H

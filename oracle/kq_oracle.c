@@ -1,6 +1,6 @@
 /* kq_oracle — CPU restatement of katali-lab's quantized expert-GEMV numerics.
  *
- * TEST INFRASTRUCTURE ONLY (the checker, never the product). See kq_oracle.h
+ * TEST INFRASTRUCTURE ONLY (the oracle, never the product). See kq_oracle.h
  * for what each function restates or defines. Build with -ffp-contract=off: the
  * only fused multiply-adds are the explicit fmaf() calls, placed exactly where
  * the reference uses _mm256_fmadd_ps.

@@ -1,6 +1,6 @@
 /* kq_oracle — CPU restatement of katali-lab's quantized expert-GEMV numerics.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker for libkatali_hip: only
+ * TEST INFRASTRUCTURE ONLY. This library is the oracle for libkatali_hip: only
  * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.
  * The product path (libkatali_hip, the host loader, the CLI) never links it and
  * never falls back to it.
