@@ -220,6 +220,16 @@ typedef struct KataliHipMoeBatch {
  * library-owned stream forked from the library stream and joined back
  * before the call's last kernel, so work queued after the call (or a graph
  * captured around it) still sees the whole layer finished in order. */
+/* Device routing for a batch (prefill): ids/weights [n_tokens][n_sel] from
+ * router logits [n_tokens][n_expert], each row routed exactly as
+ * katali_hip_moe_layer routes one token from its logits (top n_sel, larger
+ * logit first, lower index on ties, NaN as -inf; softmax over the selected,
+ * renormalised), ready for KataliHipMoeBatch.ids / .weights. No reference
+ * signature: the engine's router for a prompt is its CPU softmax and top-k
+ * per token (V/src/gguf_kernels.c:63-80). 1 <= n_tokens <= 65535,
+ * n_expert <= 512, 1 <= n_sel <= min(16, n_expert). */
+int katali_hip_moe_route_batch(const float *logits_dev, uint32_t n_tokens, uint32_t n_expert, int32_t n_sel,
+                               int32_t *ids_dev, float *weights_dev);
 int katali_hip_moe_batch(const KataliHipMoe *moe, const KataliHipMoeBatch *batch, const float *x_dev,
                          float *y_dev);
 

@@ -72,6 +72,9 @@ int katali_gpu_add_rmsnorm(float *x_dev, const float *delta_dev, float scale, co
 int katali_gpu_rmsnorm_matvec_f32(const float *x_dev, const float *delta_dev, float scale, float *x_out_dev,
                                   const float *norm_w_dev, uint64_t n, float eps, float *xn_dev,
                                   const float *w_dev, uint64_t rows, float *y_dev);
+/* Device routing for a batch: ids/weights [T][n_sel] from logits [T][n_expert]. */
+int katali_gpu_moe_route_batch(const float *logits_dev, uint32_t n_tokens, uint32_t n_expert, int32_t n_sel,
+                               int32_t *ids_dev, float *weights_dev);
 /* The MoE layer over a batch of up to 64 tokens (batched prefill). */
 int katali_gpu_moe_batch(const KataliHipMoe *moe, const KataliHipMoeBatch *batch, const float *x_dev,
                          float *y_dev);
@@ -123,6 +126,7 @@ typedef struct KataliHipApi {
     int (*add_rmsnorm)(float *, const float *, float, const float *, uint64_t, float, float *);
     int (*rmsnorm_matvec_f32)(const float *, const float *, float, float *, const float *, uint64_t, float, float *,
                               const float *, uint64_t, float *);
+    int (*moe_route_batch)(const float *, uint32_t, uint32_t, int32_t, int32_t *, float *);
 } KataliHipApi;
 
 /* NULL when the library could not be loaded or an entry point is missing. */

@@ -530,6 +530,17 @@ int katali_hip_rmsnorm_matvec_f32(const float *x, const float *delta, float scal
                     "rmsnorm_matvec_f32");
 }
 
+int katali_hip_moe_route_batch(const float *logits, uint32_t n_tokens, uint32_t n_expert, int32_t n_sel,
+                               int32_t *ids, float *wts) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!logits || !ids || !wts) return fail(KATALI_HIP_E_INVALID, "null buffer");
+    if (n_tokens < 1 || n_tokens > 65535 || n_expert < 1 || n_expert > 512 || n_sel < 1 || n_sel > 16 ||
+        (uint32_t)n_sel > n_expert)
+        return fail(KATALI_HIP_E_INVALID, "route_batch T=%u E=%u n_sel=%d", n_tokens, n_expert, n_sel);
+    return launched(kq::launch_route_batch(logits, n_tokens, n_expert, n_sel, ids, wts, g_stream), "route_batch");
+}
+
 int katali_hip_argmax(const float *x, uint64_t n, int32_t *out) {
     int rc = ensure();
     if (rc) return rc;

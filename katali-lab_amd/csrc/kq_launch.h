@@ -110,6 +110,11 @@ struct MoeArgs {
 };
 bool moe_shape_supported(uint32_t gate_type, uint32_t down_type, uint32_t hidden, uint32_t ffn);
 hipError_t launch_moe(const MoeArgs &a, hipStream_t s);
+// Top-n_sel routing of n_tokens rows of logits [n_tokens][n_expert] (<= 512
+// experts, 1 <= n_sel <= min(16, n_expert)): ids / weights [n_tokens][n_sel],
+// each row as the single-token layer routes it.
+hipError_t launch_route_batch(const float *logits, uint32_t n_tokens, uint32_t n_expert, int n_sel, int32_t *ids,
+                              float *wts, hipStream_t s);
 // Grouped batch mode over up to max_entries entries of <= 8 pairs of one
 // expert (the batched layer's GEMV path).
 hipError_t launch_moe_groups_gu(const MoeArgs &a, uint32_t max_entries, hipStream_t s);

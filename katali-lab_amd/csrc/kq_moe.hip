@@ -952,6 +952,39 @@ bool moe_shape_supported(uint32_t gate_type, uint32_t down_type, uint32_t hidden
 
 static hipError_t go_a_any(const MoeArgs &a, uint32_t n_slots, hipStream_t s);
 
+// Routing of T tokens at once (batched prefill): one wave per token runs
+// kernel A's own routing (load_keys, wave_topk, route_weight) on its row of
+// logits, so every token gets the experts and weights the single-token layer
+// would route it to, bit for bit. Lanes r < n_sel write rank r.
+template <int C>
+__global__ void __launch_bounds__(64) k_route_batch(const float *logits, uint32_t n_expert, int n_sel,
+                                                    int32_t *ids, float *wts) {
+    MoeArgs a{};
+    a.logits = logits + (uint64_t)blockIdx.x * n_expert;
+    a.n_expert = n_expert;
+    a.n_sel = n_sel;
+    float lv[C];
+    load_keys<C>(a, lv);
+    const WaveRoute r = wave_topk<C>(a, lv);
+    const float w = route_weight(r.logit, n_sel);
+    const uint32_t lane = threadIdx.x;
+    if ((int)lane < n_sel) {
+        ids[(uint64_t)blockIdx.x * n_sel + lane] = r.id;
+        wts[(uint64_t)blockIdx.x * n_sel + lane] = w;
+    }
+}
+
+hipError_t launch_route_batch(const float *logits, uint32_t n_tokens, uint32_t n_expert, int n_sel, int32_t *ids,
+                              float *wts, hipStream_t s) {
+    if (n_expert <= 128)
+        hipLaunchKernelGGL(k_route_batch<2>, dim3(n_tokens), dim3(64), 0, s, logits, n_expert, n_sel, ids, wts);
+    else if (n_expert <= 256)
+        hipLaunchKernelGGL(k_route_batch<4>, dim3(n_tokens), dim3(64), 0, s, logits, n_expert, n_sel, ids, wts);
+    else
+        hipLaunchKernelGGL(k_route_batch<8>, dim3(n_tokens), dim3(64), 0, s, logits, n_expert, n_sel, ids, wts);
+    return hipGetLastError();
+}
+
 hipError_t launch_moe(const MoeArgs &a, hipStream_t s) {
     if (a.n_expert > MAX_EXPERT || a.n_sel > MAX_SEL) return hipErrorInvalidValue;
     const uint32_t n_slots = (uint32_t)a.n_sel + (a.has_shared ? 1u : 0u);

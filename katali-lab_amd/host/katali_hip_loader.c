@@ -112,6 +112,7 @@ static int load(void) {
     LOAD(rmsnorm, "katali_hip_rmsnorm");
     LOAD(add_rmsnorm, "katali_hip_add_rmsnorm");
     LOAD(rmsnorm_matvec_f32, "katali_hip_rmsnorm_matvec_f32");
+    LOAD(moe_route_batch, "katali_hip_moe_route_batch");
     if (g_api.abi_version() != KATALI_HIP_ABI_VERSION) {
         snprintf(g_status, sizeof g_status, "%s: ABI version %d, loader expects %d", tried, g_api.abi_version(),
                  KATALI_HIP_ABI_VERSION);
@@ -188,6 +189,10 @@ int katali_gpu_rmsnorm(const float *x, const float *w, uint64_t n, float eps, fl
 int katali_gpu_add_rmsnorm(float *x, const float *delta, float scale, const float *w, uint64_t n, float eps,
                            float *out) {
     FORWARD(g_api.add_rmsnorm(x, delta, scale, w, n, eps, out));
+}
+int katali_gpu_moe_route_batch(const float *logits, uint32_t n_tokens, uint32_t n_expert, int32_t n_sel, int32_t *ids,
+                               float *w) {
+    FORWARD(g_api.moe_route_batch(logits, n_tokens, n_expert, n_sel, ids, w));
 }
 int katali_gpu_rmsnorm_matvec_f32(const float *x, const float *delta, float scale, float *x_out, const float *nw,
                                   uint64_t n, float eps, float *xn, const float *w, uint64_t rows, float *y) {

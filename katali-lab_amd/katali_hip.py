@@ -61,6 +61,7 @@ SIGNATURES = {
     "katali_hip_matvec_multi_dp4a": (C.c_int, [C.c_int, _vp, _vp, _vp, _u64, _vp, _vp]),
     "katali_hip_rmsnorm": (C.c_int, [_vp, _vp, _u64, _f32, _vp]),
     "katali_hip_add_rmsnorm": (C.c_int, [_vp, _vp, _f32, _vp, _u64, _f32, _vp]),
+    "katali_hip_moe_route_batch": (C.c_int, [_vp, _u32, _u32, _i32, _vp, _vp]),
     "katali_hip_rmsnorm_matvec_f32": (C.c_int, [_vp, _vp, _f32, _vp, _vp, _u64, _f32, _vp, _vp, _u64, _vp]),
 }
 
@@ -202,6 +203,9 @@ class KataliHip:
         p = lambda b: None if b is None else b.ptr  # noqa: E731
         self.check(self.lib.katali_hip_rmsnorm_matvec_f32(x.ptr, p(delta), scale, p(x_out), norm_w.ptr, n, eps,
                                                           xn.ptr, w.ptr, rows, y.ptr))
+
+    def moe_route_batch(self, logits, n_tokens, n_expert, n_sel, ids, weights) -> None:
+        self.check(self.lib.katali_hip_moe_route_batch(logits.ptr, n_tokens, n_expert, n_sel, ids.ptr, weights.ptr))
 
     def block_isums(self, t, w, rows, cols, xq, out) -> None:
         self.check(self.lib.katali_hip_block_isums(t, w.ptr, rows, cols, xq.ptr, out.ptr))

@@ -177,3 +177,68 @@ def test_moe_batch_graph_replays_match_eager(hip, oracle, built, T, thr):
             assert np.array_equal(other.download(np.uint32), ref), i
     finally:
         hip.graph_destroy(g)
+
+
+def batch_logits(rng, T, E, kind):
+    if kind == "ties":
+        return rng.integers(-2, 3, (T, E)).astype(np.float32)
+    v = rng.standard_normal((T, E)).astype(np.float32)
+    if kind == "special":   # NaN ranks as -inf, -0 equals +0
+        v[:, ::7] = np.nan
+        v[:, 1::11] = -np.inf
+        v[:, 2::13] = -0.0
+        v[:, 3::13] = 0.0
+    return v
+
+
+ROUTE_BATCH = [(37, 128, 8, "normal"), (64, 256, 8, "ties"), (5, 512, 16, "normal"), (20, 200, 5, "special"),
+               (9, 16, 16, "normal"), (3, 64, 1, "special")]
+
+
+@pytest.mark.parametrize("T,E,k,kind", ROUTE_BATCH, ids=[f"t{c[0]}_e{c[1]}_k{c[2]}_{c[3]}" for c in ROUTE_BATCH])
+def test_route_batch_matches_oracle(hip, oracle, T, E, k, kind):
+    """Device routing of a prompt's logits: every token's experts and weights
+    bit-identical to the oracle router (the single-token layer's routing)."""
+    print(f"[route-batch] T={T} E={E} k={k} {kind}", flush=True)
+    rng = np.random.default_rng(T * 1000 + E + k)
+    logits = batch_logits(rng, T, E, kind)
+    ids, w = hip.alloc(T * k * 4), hip.alloc(T * k * 4)
+    hip.moe_route_batch(hip.to_device(logits), T, E, k, ids, w)
+    got_i = ids.download(np.int32).reshape(T, k)
+    got_w = w.download(np.float32).reshape(T, k)
+    for t in range(T):
+        oi, ow = oracle.router_topk(logits[t], k)
+        assert got_i[t].tolist() == oi.tolist(), t
+        assert np.array_equal(got_w[t].view(np.uint32), ow.view(np.uint32)), t
+
+
+def test_prefill_with_device_routing(hip, oracle, built):
+    """Prefill on the device end to end: logits -> katali_hip_moe_route_batch
+    -> katali_hip_moe_batch gives the bits of the same batch with the
+    oracle's routing uploaded."""
+    case = CASES[2]
+    hidden, ffn, n_expert, n_sel, T = case[:5]
+    desc = built(case)[0]
+    rng = np.random.default_rng(5)
+    logits = rng.standard_normal((T, n_expert)).astype(np.float32)
+    x = rng.standard_normal((T, hidden)).astype(np.float32)
+    dx = hip.to_device(x)
+    ids, w = hip.alloc(T * n_sel * 4), hip.alloc(T * n_sel * 4)
+    hip.moe_route_batch(hip.to_device(logits), T, n_expert, n_sel, ids, w)
+    y1, y2 = hip.alloc(T * hidden * 4), hip.alloc(T * hidden * 4)
+    hip.moe_batch(desc, T, n_sel, ids, w, dx, y1)
+    routes = [oracle.router_topk(logits[t], n_sel) for t in range(T)]
+    oi = np.stack([r[0] for r in routes]).astype(np.int32)
+    ow = np.stack([r[1] for r in routes]).astype(np.float32)
+    di, dw = hip.to_device(oi), hip.to_device(ow)
+    hip.moe_batch(desc, T, n_sel, di, dw, dx, y2)
+    hip.sync()
+    assert np.array_equal(y1.download(np.uint32), y2.download(np.uint32))
+
+
+def test_route_batch_rejects_bad_arguments(hip):
+    from katali_hip import HipError
+    b = hip.alloc(4096)
+    for T, E, k in ((0, 8, 2), (4, 513, 2), (4, 8, 0), (4, 8, 17), (4, 8, 9)):
+        with pytest.raises(HipError):
+            hip.moe_route_batch(b, T, E, k, b, b)
