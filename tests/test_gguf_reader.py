@@ -147,3 +147,30 @@ def test_reader_metadata_and_table(lib, tmp_path):
                                       (12, 100, 0), (200, 256, 0), (30, 5, 10)])
 def test_row_bytes(lib, t, n, want):
     assert lib.katali_hip_ggml_row_bytes(t, n) == want
+
+
+def test_reader_matches_reference_at_every_truncation(lib, refcpu, tmp_path):
+    """The minimal file cut at every length (and the multi-tensor file at
+    every 7th): same verdict and table as the reference reader."""
+    for name, raw, step in (("minimal", minimal().build(), 1), ("moe", moe_file().build(), 7)):
+        for n in range(0, len(raw) + 1, step):
+            p = tmp_path / f"{name}_{n}.gguf"
+            p.write_bytes(raw[:n])
+            assert ours(lib, p) == refcpu.gguf_table(str(p)), (name, n)
+            p.unlink()
+
+
+def test_reader_matches_reference_on_corrupted_bytes(lib, refcpu, tmp_path):
+    """Random single-byte corruptions of the header and directory: same
+    verdict and table as the reference reader."""
+    raw = bytearray(minimal().build())
+    head = len(raw) - 32          # header, metadata and tensor directory
+    rng = np.random.default_rng(11)
+    for i in range(300):
+        b = bytearray(raw)
+        pos = int(rng.integers(0, head))
+        b[pos] = int(rng.integers(0, 256))
+        p = tmp_path / f"c{i}.gguf"
+        p.write_bytes(bytes(b))
+        assert ours(lib, p) == refcpu.gguf_table(str(p)), (pos, b[pos])
+        p.unlink()
