@@ -102,6 +102,8 @@ __device__ __forceinline__ float dpp_f(float v) {
     return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
 }
 constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+// row_ror 8 / 4: lane k of a 16-lane row takes lane (k + 8) % 16 / (k + 4) % 16
+constexpr int DPP_ROR8 = 0x128, DPP_ROR4 = 0x124;
 
 // Sum R per-lane values over the 64 lanes of a wave for R rows at once: each
 // halving step sends the half of the rows the partner keeps, then the
@@ -166,6 +168,80 @@ __device__ __forceinline__ float reduce_rows(float (&acc)[R]) {
     constexpr int LOG = R >= 16 ? 4 : (R >= 8 ? 3 : (R >= 4 ? 2 : (R >= 2 ? 1 : 0)));
     if constexpr (LOG < 6) return butterfly_from<(32 >> LOG)>(acc[0]);
     else return acc[0];
+}
+
+// ---------------------------------------------------------------------------
+// Pairwise sums over lanes (lane bit 0 first): the q8_1 path's row dot sums
+// its per-sub-block terms t_0 .. t_{n-1} pairwise, sum(t[0..n)) =
+// sum(t[0..n/2)) + sum(t[n/2..n)), and lane l holds t_l, so combining the
+// lane bits from the lowest up forms exactly that tree. Every partner below
+// is lane ^ OFF; fp32 addition commutes, so both partners of a pair hold the
+// same bits afterwards.
+// ---------------------------------------------------------------------------
+constexpr int DPP_ROW_SHL4 = 0x104, DPP_ROW_SHR4 = 0x114;
+template <int OFF>
+__device__ __forceinline__ float xor_lane(float v) {   // OFF in {1, 2, 4, 8}
+    if constexpr (OFF == 1) return dpp_f<DPP_XOR1>(v);
+    else if constexpr (OFF == 2) return dpp_f<DPP_XOR2>(v);
+    else if constexpr (OFF == 8) return dpp_f<DPP_ROR8>(v);   // row_ror 8 inside 16 lanes is lane ^ 8
+    else {
+        // lane ^ 4: banks 0 and 2 of a row (lanes 0-3, 8-11) take lane + 4
+        // (row_shl 4), banks 1 and 3 take lane - 4 (row_shr 4)
+        const int x = __float_as_int(v);
+        int t = __builtin_amdgcn_update_dpp(0, x, DPP_ROW_SHL4, 0xF, 0x5, false);
+        t = __builtin_amdgcn_update_dpp(t, x, DPP_ROW_SHR4, 0xF, 0xA, false);
+        return __int_as_float(t);
+    }
+}
+// N values per lane (virtual rows) summed over the 64 lanes at once: the
+// step at lane bit s sends half of the remaining rows to the partner (lanes
+// with bit s set keep the upper half), so after log2(N) steps each lane
+// holds one row, whose remaining lane bits then sum by a plain butterfly.
+// Lane l ends with the whole sum of virtual row pw_row<N>(l).
+template <int N, int OFF, int R>
+__device__ __forceinline__ void pw_halve(float (&acc)[R], int lane) {
+    if constexpr (N > 1) {
+        constexpr int HALF = N / 2;
+        if constexpr (OFF >= 16) {
+#pragma unroll
+            for (int i = 0; i < HALF; i++) acc[i] = swap_sum<OFF>(acc[i], acc[i + HALF]);
+        } else {
+            const bool upper = lane & OFF;
+#pragma unroll
+            for (int i = 0; i < HALF; i++) {
+                const float send = upper ? acc[i] : acc[i + HALF];
+                const float keep = upper ? acc[i + HALF] : acc[i];
+                acc[i] = keep + xor_lane<OFF>(send);
+            }
+        }
+        pw_halve<HALF, OFF * 2, R>(acc, lane);
+    }
+}
+template <int OFF>
+__device__ __forceinline__ float pw_butterfly(float v) {
+    if constexpr (OFF <= 32) {
+        if constexpr (OFF >= 16) v = swap_sum<OFF>(v, v);
+        else v += xor_lane<OFF>(v);
+        return pw_butterfly<OFF * 2>(v);
+    } else {
+        return v;
+    }
+}
+template <int N>
+constexpr int log2c() { return N <= 1 ? 0 : 1 + log2c<N / 2>(); }
+template <int N>
+__device__ __forceinline__ float pw_reduce(float (&acc)[N]) {
+    static_assert(N >= 1 && N <= 64 && (N & (N - 1)) == 0, "pw_reduce: N a power of 2 <= 64");
+    pw_halve<N, 1, N>(acc, (int)(threadIdx.x & 63));
+    return pw_butterfly<N>(acc[0]);
+}
+// The virtual row lane l holds after pw_reduce<N>: lane bit s carries row
+// bit log2(N) - 1 - s (the row index bit-reversed into the low lane bits).
+template <int N>
+__device__ __forceinline__ uint32_t pw_row(uint32_t lane) {
+    constexpr int L = log2c<N>();
+    if constexpr (L == 0) return 0;
+    else return __builtin_bitreverse32(lane) >> (32 - L);
 }
 
 // LDS writes of this wave become visible to its own other lanes (a
@@ -235,7 +311,6 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 // v is 8-periodic after the first step), then (l0 + l1) + (l2 + l3) (lane ^ 1,
 // lane ^ 2). Every add is commutative, so each lane of the row ends with the
 // same bits.
-constexpr int DPP_ROR8 = 0x128, DPP_ROR4 = 0x124;
 __device__ __forceinline__ float hsum16_avx2_order(float a) {
     float v = a + dpp_f<DPP_ROR8>(a);
     v = v + dpp_f<DPP_ROR4>(v);

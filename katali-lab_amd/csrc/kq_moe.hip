@@ -220,7 +220,7 @@ __device__ __forceinline__ int sum32(int v) {
 // the activation side of one lane item (constant over rows)
 struct XSlice {
     int4 xl, xh;
-    float qlo, qhi;   // integer sums of the lane's 16 low / 16 high x values
+    float xsum;   // exact sum of the 32 int8 values of x's q8_1 block it (the lane's sub-block)
 };
 __device__ __forceinline__ XSlice x_slice(const Act &xa, uint32_t it) {
     const uint32_t b = it / 8, c = it % 8, g = c >> 1, hh = c & 1;
@@ -228,20 +228,33 @@ __device__ __forceinline__ XSlice x_slice(const Act &xa, uint32_t it) {
     XSlice x;
     x.xl = *(const int4 *)al;
     x.xh = *(const int4 *)(al + 32);
-    const uint32_t k = 8 * b + 2 * g;
-    x.qlo = (float)xa.qs16[2 * k + hh];
-    x.qhi = (float)xa.qs16[2 * k + 2 + hh];
+    x.xsum = (float)(xa.qs16[2 * it] + xa.qs16[2 * it + 1]);
     return x;
 }
-// d8lo*(ds0*slo - dm0*qlo) + d8hi*(ds1*shi - dm1*qhi) with the x scales
-// folded into the decoded header (sc = {ds0*d8lo, ds1*d8hi, dm0*d8lo, dm1*d8hi})
-__device__ __forceinline__ float item_dot(const uint4 &q, const float4 &sc, const XSlice &x) {
+
+// The q8_1 path's Q4_K row dot is the pairwise sum of one fp32 term per
+// 32-value sub-block j:
+//   t_j = fmaf(A_j, isum_j, -(B_j * xsum_j)),  A_j = (d*sc_j)*d8_j,  B_j = (dmin*m_j)*d8_j,
+// isum_j the exact integer sum over the sub-block. Lane item it (16 nibble
+// bytes: values 16hh..16hh+15 of sub-blocks 2g and 2g+1, hh = it & 1) forms
+// half sums of both; lanes it and it ^ 1 (partners by DPP) swap the halves
+// the other needs, after which lane it holds sub-block it's term (hh = 0:
+// sub-block 2g, the low nibbles; hh = 1: 2g+1). The decoded header gives
+// sc = {A_2g, A_2g+1, B_2g, B_2g+1}. The lane bit hh equals lane bit 0 in
+// every item mapping here (items of a row sit on consecutive lanes).
+__device__ __forceinline__ float q4k_term_from(int slo, int shi, const float4 &sc, float xsum) {
+    const bool hh = threadIdx.x & 1;
+    const int isum = (hh ? shi : slo) + dpp_i<DPP_XOR1>(hh ? slo : shi);
+    const float A = hh ? sc.y : sc.x, B = hh ? sc.w : sc.z;
+    return fmaf(A, (float)isum, -(B * xsum));
+}
+__device__ __forceinline__ float q4k_term(const uint4 &q, const float4 &sc, const XSlice &x) {
     int slo, shi;
     Q4K::isums_x(q, x.xl, x.xh, slo, shi);
-    return fmaf(sc.x, (float)slo, fmaf(sc.y, (float)shi, -fmaf(sc.z, x.qlo, sc.w * x.qhi)));
+    return q4k_term_from(slo, shi, sc, x.xsum);
 }
-// item_dot with the nibbles unpacked beforehand (the same sums and float ops)
-__device__ __forceinline__ float item_dot_u(const Q4K::Unp &u, const float4 &sc, const XSlice &x) {
+// q4k_term with the nibbles unpacked beforehand (the same sums and float ops)
+__device__ __forceinline__ float q4k_term_u(const Q4K::Unp &u, const float4 &sc, const XSlice &x) {
     int slo = dot4(u.lo.x, x.xl.x, 0);
     slo = dot4(u.lo.y, x.xl.y, slo);
     slo = dot4(u.lo.z, x.xl.z, slo);
@@ -250,7 +263,28 @@ __device__ __forceinline__ float item_dot_u(const Q4K::Unp &u, const float4 &sc,
     shi = dot4(u.hi.y, x.xh.y, shi);
     shi = dot4(u.hi.z, x.xh.z, shi);
     shi = dot4(u.hi.w, x.xh.w, shi);
-    return fmaf(sc.x, (float)slo, fmaf(sc.y, (float)shi, -fmaf(sc.z, x.qlo, sc.w * x.qhi)));
+    return q4k_term_from(slo, shi, sc, x.xsum);
+}
+
+// Rows of sub-block terms summed pairwise over the lanes. Chunk k of a lane
+// is its item 64*(k % M) + lane of row k / M (M items per lane per row), so
+// the chunk index is the virtual row of pw_reduce: row sub-block j = 64m +
+// lane. With M = 2 the lanes hold the two halves of the row (j < 64, j >= 64)
+// as separate virtual rows, whose sums (partners at lane bit log2(V) - 1)
+// make the tree's top level. Lanes 0 .. V/M - 1 end with whole rows:
+// pw_rows_row(lane) of them.
+template <int V, int M>
+__device__ __forceinline__ float pw_rows(float (&acc)[V]) {
+    float v = pw_reduce<V>(acc);
+    if constexpr (M == 2) {
+        if constexpr (V / 2 >= 16) v = swap_sum<V / 2>(v, v);
+        else v += xor_lane<V / 2>(v);
+    }
+    return v;
+}
+template <int V, int M>
+__device__ __forceinline__ uint32_t pw_rows_row(uint32_t lane) {
+    return pw_row<V>(lane) / M;
 }
 
 constexpr int A_ROWS_PER_WAVE = 8;
@@ -274,7 +308,6 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_gu(MoeArgs a) {
     constexpr int RPG = RW / GROUPS;           // rows per group
     constexpr int LPG = RPG * ITEMS / 64;      // chunks per lane per group
     constexpr int M = ITEMS >= 64 ? ITEMS / 64 : 1;   // items per lane
-    constexpr int LOG_RPG = RPG == 16 ? 4 : (RPG == 8 ? 3 : (RPG == 4 ? 2 : (RPG == 2 ? 1 : 0)));
     constexpr int WH = RW * NB;                // block headers of one wave's rows
     constexpr int HPL = (WH + 63) / 64;        // header loads per lane
     extern __shared__ __align__(16) uint8_t lds[];
@@ -437,27 +470,24 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_gu(MoeArgs a) {
             for (int k = 0; k < LPG; k++) q[k] = ld16(chunk(grp, k));
         }
         if constexpr (ITEMS >= 64) {
-            float acc[RPG];
-#pragma unroll
-            for (int r = 0; r < RPG; r++) acc[r] = 0.0f;
+            float acc[LPG];   // virtual row k: sub-block 64 * (k % M) + lane of row k / M
 #pragma unroll
             for (int k = 0; k < LPG; k++) {
                 const uint32_t it = 64 * (k % M) + lane;
                 const uint32_t row = grp * RPG + k / M;   // within the wave
                 const float4 sc = scl[4 * (row * NB + it / 8) + (it % 8) / 2];
-                acc[k / M] += item_dot(q[k], sc, xs[k % M]);
+                acc[k] = q4k_term(q[k], sc, xs[k % M]);
             }
-            const float v = reduce_rows<RPG>(acc);
-            constexpr int SH = 6 - LOG_RPG;
-            const uint32_t r = (lane >> SH) & (RPG - 1);
-            if ((lane & ((1u << SH) - 1)) == 0) gu[RW * wave + grp * RPG + r] = v;
+            const float v = pw_rows<LPG, M>(acc);
+            if (lane < (uint32_t)RPG) gu[RW * wave + grp * RPG + pw_rows_row<LPG, M>(lane)] = v;
         } else {
             const uint32_t it = lane % ITEMS;
 #pragma unroll
             for (int k = 0; k < LPG; k++) {
                 const uint32_t row = lane / ITEMS + k * (64 / ITEMS);   // within the wave
                 const float4 sc = scl[4 * (row * NB + it / 8) + (it % 8) / 2];
-                const float v = group_sum<ITEMS>(item_dot(q[k], sc, xs[0]));
+                // group_sum adds lane bit 0 first: the pairwise tree over the row's sub-blocks
+                const float v = group_sum<ITEMS>(q4k_term(q[k], sc, xs[0]));
                 if (it == 0) gu[RW * wave + row] = v;
             }
         }
@@ -755,9 +785,7 @@ __global__ void __launch_bounds__(A_THREADS) k_moe_gu_grp(MoeArgs a) {
                 xs[m] = x_slice(xa, it);
                 d8[m] = make_float2(xa.d8[k8], xa.d8[k8 + 1]);
             }
-            float acc[RW];
-#pragma unroll
-            for (int r = 0; r < RW; r++) acc[r] = 0.0f;
+            float acc[LPG];   // virtual row k: sub-block 64 * (k % M) + lane of row k / M
 #pragma unroll
             for (int k = 0; k < LPG; k++) {
                 const uint32_t it = 64 * (k % M) + lane;
@@ -765,12 +793,11 @@ __global__ void __launch_bounds__(A_THREADS) k_moe_gu_grp(MoeArgs a) {
                 const float4 s0 = scl[4 * (row * NB + it / 8) + (it % 8) / 2];
                 const float2 dd = d8[k % M];
                 const float4 sc = make_float4(s0.x * dd.x, s0.y * dd.y, s0.z * dd.x, s0.w * dd.y);
-                if constexpr (UNP) acc[row] += item_dot_u(qu[k], sc, xs[k % M]);
-                else acc[row] += item_dot(q[k], sc, xs[k % M]);
+                if constexpr (UNP) acc[k] = q4k_term_u(qu[k], sc, xs[k % M]);
+                else acc[k] = q4k_term(q[k], sc, xs[k % M]);
             }
-            const float v = reduce_rows<RW>(acc);
-            const uint32_t r = (lane >> 3) & (RW - 1);
-            if ((lane & 7) == 0) gu[64 * g + RW * wave + r] = v;
+            const float v = pw_rows<LPG, M>(acc);
+            if (lane < (uint32_t)RW) gu[64 * g + RW * wave + pw_rows_row<LPG, M>(lane)] = v;
         } else {
             const uint32_t it = lane % ITEMS, k8 = 8 * (it / 8) + 2 * ((it % 8) >> 1);
             const XSlice xs = x_slice(xa, it);
@@ -780,7 +807,7 @@ __global__ void __launch_bounds__(A_THREADS) k_moe_gu_grp(MoeArgs a) {
                 const uint32_t row = lane / ITEMS + k * (64 / ITEMS);
                 const float4 s0 = scl[4 * (row * NB + it / 8) + (it % 8) / 2];
                 const float4 sc = make_float4(s0.x * dd.x, s0.y * dd.y, s0.z * dd.x, s0.w * dd.y);
-                const float v = group_sum<ITEMS>(UNP ? item_dot_u(qu[k], sc, xs) : item_dot(q[k], sc, xs));
+                const float v = group_sum<ITEMS>(UNP ? q4k_term_u(qu[k], sc, xs) : q4k_term(q[k], sc, xs));
                 if (it == 0) gu[64 * g + RW * wave + row] = v;
             }
         }

@@ -242,6 +242,20 @@ __device__ __forceinline__ uint32_t q6_minus_32(uint32_t q) {
     return x | (m << 1) | (m << 2);
 }
 
+// Pairwise sum of a stream of terms t_0, t_1, ... pushed in index order (J
+// known at compile time): stk[l] holds the sum of the last complete group of
+// 2^l terms not yet combined. Pushing t_J adds it to the pending groups while
+// bit l of J is set (each such group is the left half of the next level's
+// group), then parks the result at the first clear bit. After t_{2^K - 1},
+// stk[K] holds sum(t[0 .. 2^K)) in the pairwise tree:
+// sum(t[0..n)) = sum(t[0..n/2)) + sum(t[n/2..n)).
+template <int J, int L, int LV>
+__device__ __forceinline__ void pw_push(float (&stk)[LV], float c) {
+    static_assert(L < LV, "pw_push: stack too shallow");
+    if constexpr ((J >> L) & 1) pw_push<J, L + 1, LV>(stk, stk[L] + c);
+    else stk[L] = c;
+}
+
 __device__ __forceinline__ v4i mfma16(long a, long b) {
     const v4i z = {0, 0, 0, 0};
     return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, z, 0, 0, 0);
@@ -370,7 +384,10 @@ __global__ void __launch_bounds__(256) k_mb_gu_mfma(MoeArgs a, const int32_t *__
         XPart xv[3];
         xv[0] = mbx_load(xrow, 0);
         xv[1] = mbx_load(xrow, NB > 1 ? 1 : 0);
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        // each (row, pair) value is the pairwise sum of its sub-block terms,
+        // pushed in sub-block order (kernel A's q8_1-path dot, bit for bit)
+        constexpr int LV = log2c<NB>() + 1;
+        float stk[4][LV];
         static_for<0, NB>([&](auto bc) {   // unrolled: the register ring is indexed by constants
             constexpr uint32_t b = decltype(bc)::value;
             __builtin_amdgcn_sched_barrier(0);   // one block's operands live at a time
@@ -383,22 +400,32 @@ __global__ void __launch_bounds__(256) k_mb_gu_mfma(MoeArgs a, const int32_t *__
             const MbX x = mbx_carve(lt + (b % 2) * MBX_BYTES);
             wc.put_scales(scl);   // wave-private table
             wave_sync_lds();
+            float t[4][8];   // the block's 8 sub-block terms per (row, pair)
 #pragma unroll
             for (uint32_t j = 0; j < 8; j++) {
                 const long av = wc.a_op(j);
-                const v4i d = mfma16(av, mbx_b(x, arow, j, kc));
+                const v4i d = mfma16(av, mbx_b(x, arow, j, kc));   // exact isum of sub-block 8b + j
                 const float d8 = x.d8[8 * dcol + j], qs = (float)x.qs[8 * dcol + j];
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const float2 sc = scl[8 * (drow0 + i) + j];
-                    acc[i] = fmaf(d8, fmaf(sc.x, (float)d[i], -(sc.y * qs)), acc[i]);
+                    const float A = sc.x * d8, B = sc.y * d8;
+                    t[i][j] = fmaf(A, (float)d[i], -(B * qs));
                 }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float s = ((t[i][0] + t[i][1]) + (t[i][2] + t[i][3])) + ((t[i][4] + t[i][5]) + (t[i][6] + t[i][7]));
+                float sb = s;
+                asm volatile("" : "+v"(sb));   // formed here: sinking the block's arithmetic past the
+                                               // next barriers would keep its LDS reads live and spill
+                pw_push<b, 0>(stk[i], sb);   // blocks: the tree's levels above 8 sub-blocks
             }
             wave_sync_lds();   // the table is rewritten for the next block
         });
         // gate/up of (row, pair) -> LDS, then SiLU-GLU and one q8_1 block per pair
 #pragma unroll
-        for (int i = 0; i < 4; i++) gu[16 * (16 * wave + drow0 + i) + dcol] = acc[i];
+        for (int i = 0; i < 4; i++) gu[16 * (16 * wave + drow0 + i) + dcol] = stk[i][LV - 1];   // after block NB - 1: the whole row
         __syncthreads();
         if (tid < 16 * 8) {
             const uint32_t i = tid / 8, part = tid % 8;

@@ -430,7 +430,7 @@ int kqo_q6K_q8_isums(const uint8_t *row, const uint8_t *q8, uint64_t nb, int32_t
     return 0;
 }
 
-float kqo_dot_q4K_q8(const uint8_t *row, const uint8_t *q8, uint64_t nb) {
+float kqo_dot_q4K_q8_f64(const uint8_t *row, const uint8_t *q8, uint64_t nb) {
     double acc = 0.0;
     int32_t is[8];
     for (uint64_t b = 0; b < nb; b++) {
@@ -446,6 +446,38 @@ float kqo_dot_q4K_q8(const uint8_t *row, const uint8_t *q8, uint64_t nb) {
         }
     }
     return (float)acc;
+}
+
+float kqo_q4K_q8_term(const uint8_t *blk, int j, const uint8_t *q8blk) {
+    int32_t isum = 0;
+    for (int i = 0; i < 32; i++) isum += q4k_val(blk, 32 * j + i) * (int8_t)q8blk[4 + i];
+    uint8_t sc, m;
+    kqo_q4k_scale_min(j, blk + 4, &sc, &m);
+    const float d = kqo_f16_to_f32(rd16(blk)), dmin = kqo_f16_to_f32(rd16(blk + 2));
+    const float d8 = kqo_f16_to_f32(rd16(q8blk));
+    const float A = (d * (float)sc) * d8;
+    const float B = (dmin * (float)m) * d8;
+    const float X = (float)q8_qsum(q8blk, 0);
+    return fmaf(A, (float)isum, -(B * X));
+}
+
+/* Pairwise sum of t[0..n): halves split at the largest power of two below n
+ * (the exact halves when n is a power of two), each half summed the same
+ * way, then left + right. */
+static float pairwise_sum(const float *t, uint64_t n) {
+    if (n == 1) return t[0];
+    uint64_t h = 1;
+    while (2 * h < n) h *= 2;
+    return pairwise_sum(t, h) + pairwise_sum(t + h, n - h);
+}
+
+float kqo_dot_q4K_q8(const uint8_t *row, const uint8_t *q8, uint64_t nb) {
+    float t[8 * 128];
+    if (nb == 0 || nb > 128) return NAN;
+    for (uint64_t b = 0; b < nb; b++)
+        for (int j = 0; j < 8; j++)
+            t[8 * b + j] = kqo_q4K_q8_term(row + b * KQO_Q4K_BYTES, j, q8 + (8 * b + j) * KQO_Q81_BYTES);
+    return pairwise_sum(t, 8 * nb);
 }
 
 float kqo_dot_q6K_q8(const uint8_t *row, const uint8_t *q8, uint64_t nb) {

@@ -100,11 +100,26 @@ int kqo_quantize_q8_1(const float *x, uint64_t n, uint8_t *out);
 int kqo_q4K_q8_isums(const uint8_t *row, const uint8_t *q8, uint64_t nb, int32_t *isums);
 /* isums[16*b + t] = sum_{i<16} (q6(b, 16t+i) - 32) * q8[256b + 16t + i]. */
 int kqo_q6K_q8_isums(const uint8_t *row, const uint8_t *q8, uint64_t nb, int32_t *isums);
-/* Float compositions of those sums, accumulated in double:
- *   Q4_K: sum_j (d*sc_j)*d8*isum_j - (dmin*m_j)*d8*qsum_j
- *   Q6_K: sum_t (d*sc_t)*d8*isum_t
- * (d*sc and dmin*m are float products, as the GPU forms them). */
+/* The q8_1 path's Q4_K row dot (own definition, bit-identical on the GPU):
+ * for each 32-value sub-block j (block b = j/8, sub-block j%8, with
+ * (sc_j, m_j) from get_scale_min_k4 and d8_j the f16 scale of x's q8_1 block
+ * j), in fp32 with one rounding per operation:
+ *   A_j = (d * sc_j) * d8_j,  B_j = (dmin * m_j) * d8_j,
+ *   t_j = fmaf(A_j, isum_j, -(B_j * xsum_j)),
+ * isum_j the exact integer block sum above and xsum_j the exact sum of the 32
+ * int8 values of x's block j; then the pairwise sum of t_0 .. t_{n-1}
+ * (n = 8*nb): sum(t[0..n)) = sum(t[0..h)) + sum(t[h..n)), h the largest
+ * power of two below n (n/2 for the row widths the GPU kernels take, all
+ * powers of two). nb <= 128. */
 float kqo_dot_q4K_q8(const uint8_t *row, const uint8_t *q8, uint64_t nb);
+/* t_j of one block for sub-block j, with q8blk pointing at x's block j. */
+float kqo_q4K_q8_term(const uint8_t *blk, int j, const uint8_t *q8blk);
+/* The same terms' closed form in double (d*sc and dmin*m as fp32 products,
+ * the rest exact-ish in double), for bounding kqo_dot_q4K_q8:
+ *   sum_j (d*sc_j)*d8_j*isum_j - (dmin*m_j)*d8_j*xsum_j. */
+float kqo_dot_q4K_q8_f64(const uint8_t *row, const uint8_t *q8, uint64_t nb);
+/* Q6_K: sum_t (d*sc_t)*d8*isum_t accumulated in double (the down projection,
+ * whose output is not quantized again). */
 float kqo_dot_q6K_q8(const uint8_t *row, const uint8_t *q8, uint64_t nb);
 int   kqo_matvec_q8(uint32_t type, const void *w, uint64_t rows, uint64_t cols,
                     const uint8_t *q8, float *y);

@@ -63,6 +63,8 @@ class Oracle:
             "kqo_q4K_q8_isums": (_i32, [_vp, _vp, _u64, _vp]),
             "kqo_q6K_q8_isums": (_i32, [_vp, _vp, _u64, _vp]),
             "kqo_dot_q4K_q8": (_f32, [_vp, _vp, _u64]),
+            "kqo_dot_q4K_q8_f64": (_f32, [_vp, _vp, _u64]),
+            "kqo_q4K_q8_term": (_f32, [_vp, _i32, _vp]),
             "kqo_dot_q6K_q8": (_f32, [_vp, _vp, _u64]),
             "kqo_matvec_q8": (_i32, [_u32, _vp, _u64, _u64, _vp, _vp]),
             "kqo_expf": (_f32, [_f32]),
@@ -113,6 +115,16 @@ class Oracle:
         y = np.empty(rows, np.float32)
         assert self.lib.kqo_matvec_q8(t, _ptr(w), rows, cols, _ptr(q8), _ptr(y)) == 0
         return y
+
+    def dot_q4K_q8(self, row: np.ndarray, q8: np.ndarray, f64: bool = False) -> float:
+        """One Q4_K row against q8_1 blocks: the q8 path's pairwise fp32 dot,
+        or (f64=True) the same terms' closed form in double."""
+        nb = row.size // 144
+        fn = self.lib.kqo_dot_q4K_q8_f64 if f64 else self.lib.kqo_dot_q4K_q8
+        return float(np.float32(fn(_ptr(row), _ptr(q8), nb)))
+
+    def q4K_q8_term(self, blk: np.ndarray, j: int, q8blk: np.ndarray) -> float:
+        return float(np.float32(self.lib.kqo_q4K_q8_term(_ptr(blk), j, _ptr(q8blk))))
 
     def vec_dot_ref_rows(self, t: int, w: np.ndarray, rows: int, cols: int, x: np.ndarray) -> np.ndarray:
         rb = row_bytes(t, cols)

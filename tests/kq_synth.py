@@ -26,10 +26,24 @@ def q6k_blocks(rng: np.random.Generator, nblocks: int, dscale: float = 0.02) -> 
     return b.reshape(-1)
 
 
-def matrix(rng: np.random.Generator, t: int, rows: int, cols: int) -> np.ndarray:
+def matrix(rng: np.random.Generator, t: int, rows: int, cols: int, dscale: float = 0.02) -> np.ndarray:
     assert cols % 256 == 0
     nb = rows * cols // 256
-    return q4k_blocks(rng, nb) if t == Q4_K else q6k_blocks(rng, nb)
+    return q4k_blocks(rng, nb, dscale) if t == Q4_K else q6k_blocks(rng, nb, dscale)
+
+
+def representable_activation(rng: np.random.Generator, n: int) -> np.ndarray:
+    """fp32 values that q8_1 holds exactly: per 32-value block an f16 scale d
+    and x = d * q with integer q in [-127, 127], |q| = 127 somewhere (so the
+    quantizer picks the same d back)."""
+    assert n % 32 == 0
+    x = np.empty(n, np.float32)
+    for b in range(n // 32):
+        d = np.float32(np.float16(abs(rng.normal(0.0, 1.0)) / 127.0 + 1e-3))
+        q = rng.integers(-127, 128, 32)
+        q[rng.integers(0, 32)] = 127 if rng.random() < 0.5 else -127
+        x[32 * b:32 * b + 32] = d * q.astype(np.float32)
+    return x
 
 
 def activation(rng: np.random.Generator, n: int) -> np.ndarray:

@@ -2,13 +2,16 @@
 
 Stage by stage against the oracle on the same inputs:
   routing (ids exact, weights bit-exact: same fp32 operations);
-  gate/up outputs: rel_L2 <= 1e-5;
-  q8_1 SiLU-GLU blocks: bit-exact to the oracle's quantization of the GPU's
-    own gate/up (the SiLU and the quantizer are exact fp32 restatements);
-  layer output: rel_L2 <= 1e-5 against the oracle's down stage on the GPU's
-    h, and against the oracle's end-to-end q8 path whenever no h block
-    quantized differently (a 1-ulp gate/up difference can move one q8 value
-    across a rounding boundary; the test counts such blocks).
+  gate/up outputs: bit-exact (the q8_1 path's Q4_K dot is defined as
+    per-sub-block fp32 terms summed pairwise, which the kernels reproduce);
+  q8_1 SiLU-GLU blocks: bit-exact to the oracle's;
+  layer output: rel_L2 <= 1e-5 against the oracle's end-to-end q8 path (the
+    down projection is summed in another fp32 order than the oracle's double);
+  against the fp32 CPU path (the reference's AVX2 dots and SiLU): on
+    q8-representable activations every element within the bound the h
+    quantization step allows (half a q8_1 step of h, times |down| and the
+    routing weight), and, at a real layer's magnitudes, within
+    1e-3*(1+|ref|) (the reference's bar, README.md:17).
 Also: repeat launches bit-identical, graph replays equal to eager runs, bad
 arguments refused.
 """
@@ -29,17 +32,18 @@ def rel_l2(a, b):
 
 
 class Moe:
-    def __init__(self, hip, oracle, hidden, ffn, n_expert, shared, seed, down_type=Q6_K):
+    def __init__(self, hip, oracle, hidden, ffn, n_expert, shared, seed, down_type=Q6_K, dscale=(0.02, 0.02)):
         rng = np.random.default_rng(seed)
         self.hidden, self.ffn, self.n_expert = hidden, ffn, n_expert
-        self.gate = S.matrix(rng, Q4_K, n_expert * ffn, hidden)
-        self.up = S.matrix(rng, Q4_K, n_expert * ffn, hidden)
-        self.down = S.matrix(rng, down_type, n_expert * hidden, ffn)
+        self.down_type = down_type
+        self.gate = S.matrix(rng, Q4_K, n_expert * ffn, hidden, dscale[0])
+        self.up = S.matrix(rng, Q4_K, n_expert * ffn, hidden, dscale[0])
+        self.down = S.matrix(rng, down_type, n_expert * hidden, ffn, dscale[1])
         self.sh = None
         dsh = None
         if shared:
-            self.sh = (ffn, S.matrix(rng, Q4_K, ffn, hidden), S.matrix(rng, Q4_K, ffn, hidden),
-                       S.matrix(rng, down_type, hidden, ffn))
+            self.sh = (ffn, S.matrix(rng, Q4_K, ffn, hidden, dscale[0]), S.matrix(rng, Q4_K, ffn, hidden, dscale[0]),
+                       S.matrix(rng, down_type, hidden, ffn, dscale[1]))
             dsh = tuple(hip.to_device(a) for a in self.sh[1:])
         self.dev = [hip.to_device(self.gate), hip.to_device(self.up), hip.to_device(self.down)]
         self.dsh = dsh
@@ -66,11 +70,12 @@ CASES = [
 def moes(hip, oracle):
     cache = {}
 
-    def get(hidden, ffn, n_expert, shared, down_type):
-        key = (hidden, ffn, n_expert, shared, down_type)
+    def get(hidden, ffn, n_expert, shared, down_type, dscale=(0.02, 0.02)):
+        key = (hidden, ffn, n_expert, shared, down_type, dscale)
         if key not in cache:
+            cache.clear()   # one problem at a time keeps host and device memory small
             cache[key] = Moe(hip, oracle, hidden, ffn, n_expert, shared, seed=hash(key) & 0xFFFF,
-                             down_type=down_type)
+                             down_type=down_type, dscale=dscale)
         return cache[key]
     return get
 
@@ -108,18 +113,13 @@ def test_moe_layer_parity(hip, oracle, moes, case):
     assert np.array_equal(wo.view(np.uint32), w.view(np.uint32))
 
     yo, go, uo, hqo = oracle.moe_layer_q8(m.odesc, x, ids, w, with_stages=True)
-    assert rel_l2(gu[:, 0], go) <= 1e-5
-    assert rel_l2(gu[:, 1], uo) <= 1e-5
-    # SiLU-GLU + q8_1 of the GPU's own gate/up: bit-exact
-    for s in range(gu.shape[0]):
-        assert np.array_equal(hq[s], oracle.quantize_q8_1(oracle.silu_mul(gu[s, 0], gu[s, 1]))), s
-    # down + weighted sum on the GPU's h
-    assert rel_l2(y, oracle.moe_down_q8(m.odesc, ids, w, hq)) <= 1e-5
-    # end to end
-    flips = int(np.sum(np.any(hq.reshape(hq.shape[0], -1, 36) != hqo.reshape(hq.shape[0], -1, 36), axis=2)))
+    ns = gu.shape[0]
+    assert np.array_equal(gu[:, 0].view(np.uint32), go[:ns].view(np.uint32))
+    assert np.array_equal(gu[:, 1].view(np.uint32), uo[:ns].view(np.uint32))
+    assert np.array_equal(hq, hqo.reshape(hq.shape))
     r = rel_l2(y, yo)
-    print(f"rel_L2(gpu, oracle q8) = {r:.3e}  h blocks with a rounding flip: {flips}")
-    assert r <= (1e-5 if flips == 0 else 1e-3)
+    print(f"rel_L2(gpu, oracle q8) = {r:.3e}")
+    assert r <= 1e-5
     # against the fp32 CPU path (reference AVX2 dots + reference SiLU): q8 noise only
     rf = rel_l2(y, oracle.moe_layer_f32(m.odesc, x, ids, w))
     print(f"rel_L2(gpu q8, fp32 CPU path) = {rf:.3e}")
@@ -128,6 +128,77 @@ def test_moe_layer_parity(hip, oracle, moes, case):
     # explicit ids/weights give the same bits as in-kernel routing
     y2, *_ = run_layer(hip, m, x, n_sel, ids=ids, w=w)
     assert np.array_equal(y2.view(np.uint32), y.view(np.uint32))
+
+
+# the layer shapes of the decode workloads: top-8 of 128 (2048 -> 768 -> 2048)
+# and top-8 of 256 plus a shared expert (2048 -> 512 -> 2048)
+FP32_CASES = [(2048, 768, 128, 8, False), (2048, 512, 256, 8, True)]
+FP32_IDS = ["h2048_f768_e128_k8", "h2048_f512_e256_k8_sh"]
+
+
+def _fp32_path_bound(oracle, m, ids, w, hq):
+    """Per element of y, what the q8_1 path may differ from the fp32 path by
+    when x is q8-representable: h is rounded to q8_1 (at most half a step
+    d_h/2 per value), everything else differs by fp32 rounding. Returns
+    sum_s w_s * sum_k |D_s[i,k]| * (d_h(s,k)/2 + 1e-4 |h(s,k)|) +
+    1e-5 * sum_s w_s * sum_k |D_s[i,k] h(s,k)|."""
+    from oracle import Q8_1
+    rbd = m.ffn // 256 * 210
+    slots = [(m.down[int(e) * m.hidden * rbd:(int(e) + 1) * m.hidden * rbd], float(wt)) for e, wt in zip(ids, w)]
+    if m.sh is not None:
+        slots.append((m.sh[3], 1.0))
+    bound = np.zeros(m.hidden)
+    for s, (dw, wt) in enumerate(slots):
+        D = np.abs(oracle.dequant(Q6_K, dw, m.hidden * m.ffn).astype(np.float64)).reshape(m.hidden, m.ffn)
+        blocks = hq[s].reshape(-1, 36)
+        h = np.abs(oracle.dequant(Q8_1, hq[s], m.ffn).astype(np.float64))
+        dh = np.repeat(blocks[:, 0:2].copy().view(np.float16).astype(np.float64).reshape(-1), 32)
+        bound += wt * (D @ (0.5 * dh + 1e-4 * h) + 1e-5 * (D @ h))
+    return bound
+
+
+@pytest.mark.parametrize("case", FP32_CASES, ids=FP32_IDS)
+def test_moe_layer_vs_fp32_path_elementwise(hip, oracle, moes, case):
+    """Every output element against the fp32 CPU path within the h
+    quantization bound (BASELINE weight statistics, q8-representable x)."""
+    hidden, ffn, n_expert, n_sel, shared = case
+    print(f"[moe fp32 bound] case={case}", flush=True)
+    m = moes(hidden, ffn, n_expert, shared, Q6_K)
+    rng = np.random.default_rng(7 + ffn)
+    x = S.representable_activation(rng, hidden)
+    logits = rng.standard_normal(n_expert).astype(np.float32)
+    ids, w = oracle.router_topk(logits, n_sel)
+    y, _, hq, _, _ = run_layer(hip, m, x, n_sel, logits=logits)
+    yf = oracle.moe_layer_f32(m.odesc, x, ids, w).astype(np.float64)
+    err = np.abs(y.astype(np.float64) - yf)
+    bound = _fp32_path_bound(oracle, m, ids, w, hq)
+    print(f"max err/bound {np.max(err / bound):.3f}, rel_L2 {rel_l2(y, yf):.3e}")
+    assert np.all(err <= bound)
+
+
+@pytest.mark.parametrize("case", FP32_CASES, ids=FP32_IDS)
+def test_moe_layer_vs_fp32_path_reference_bar(hip, oracle, moes, case):
+    """The reference's bar (README.md:17: 0 elements outside 1e-3*(1+|ref|)
+    on real weights). The q8_1 rounding of h moves y by ~1% of |y|
+    (README.md:17 reports rel_L2 7.2e-3), so this bar, absolute for |y| << 1,
+    holds for outputs of a few 1e-3 like a real layer's residual update and
+    not at the unit-free BASELINE statistics (|y| ~ 1e7, where the
+    h-quantization bound above is the element-wise check). Here: gate/up
+    scales |N(0, 1e-4)| (pre-activations of order 1), down scales
+    |N(0, 5e-7)| (y RMS a few 1e-3), q8-representable x."""
+    hidden, ffn, n_expert, n_sel, shared = case
+    print(f"[moe fp32 1e-3 bar] case={case}", flush=True)
+    m = moes(hidden, ffn, n_expert, shared, Q6_K, dscale=(1e-4, 5e-7))
+    rng = np.random.default_rng(11 + ffn)
+    x = S.representable_activation(rng, hidden)
+    logits = rng.standard_normal(n_expert).astype(np.float32)
+    ids, w = oracle.router_topk(logits, n_sel)
+    y, _, _, _, _ = run_layer(hip, m, x, n_sel, logits=logits)
+    yf = oracle.moe_layer_f32(m.odesc, x, ids, w).astype(np.float64)
+    err = np.abs(y.astype(np.float64) - yf) / (1.0 + np.abs(yf))
+    print(f"|y| rms {np.sqrt(np.mean(yf ** 2)):.3g}, max err/(1+|ref|) {err.max():.3e}, "
+          f"outside {int(np.sum(err > 1e-3))}, rel_L2 {rel_l2(y, yf):.3e}")
+    assert int(np.sum(err > 1e-3)) == 0
 
 
 ROUTE_CASES = [
@@ -209,7 +280,7 @@ def test_moe_back_to_back_layers(hip, oracle, moes):
     for i in (0, 7, L - 1):
         ids, w = oracle.router_topk(lg[i], n_sel)
         want = oracle.moe_layer_q8(m.odesc, xs[i], ids, w)
-        assert rel_l2(ys[i].download(np.float32), want) <= 1e-3
+        assert rel_l2(ys[i].download(np.float32), want) <= 1e-5
         y1, *_ = run_layer(hip, m, xs[i], n_sel, logits=lg[i])
         assert np.array_equal(y1.view(np.uint32), ys[i].download(np.uint32))
 

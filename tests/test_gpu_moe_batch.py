@@ -3,13 +3,16 @@
 Every token's output is checked against the oracle's single-token q8_1 layer
 with that token's experts and weights. Each case runs three ways: the
 default grouped-GEMM threshold (experts with >= 16 pairs on int8 MFMA), every
-expert on MFMA, and every expert on the v_dot4 GEMV kernels. The q8_1 of h
-can round one value differently when gate/up differ by an ulp (the float sums
-run in another order than the oracle's), and one such value moves its token's
-output by up to ~1e-4 (most with n_sel = 1), so the bar is: median token
-rel_L2 <= 1e-5 (most tokens have no such value), batch <= 1e-4, any token
-<= 1e-3; the MFMA and GEMV paths agree with each other to the batch bar.
+expert on MFMA, and every expert on the v_dot4 GEMV kernels. All three form
+gate/up in the q8_1 path's order (per-sub-block terms, pairwise), so every
+pair's h is bit-identical to the oracle's and every token's output is within
+rel_L2 1e-5 of it (the down projections sum in fp32 in their own orders);
+the MFMA and GEMV paths agree token by token to the same bar. The cases
+include the sweep's own points: 128 experts of the 2048 -> 768 -> 2048 shape
+at n_sel 2, 4, 8 and 16, 33, 64 tokens.
 """
+import concurrent.futures as cf
+
 import numpy as np
 import pytest
 
@@ -54,7 +57,7 @@ CASES = [
     (4096, 256, 8, 2, 20, False, Q6_K),      # wide hidden
     (1024, 2304, 8, 2, 12, True, Q6_K),      # 9 down blocks: h staged 8 blocks at a time
     (512, 2304, 4, 2, 9, False, Q4_K),       # the same with a Q4_K down
-]
+] + [(2048, 768, 128, k, t, False, Q6_K) for k in (2, 4, 8) for t in (16, 33, 64)]   # the sweep's points
 
 
 @pytest.fixture(scope="module")
@@ -94,7 +97,8 @@ def test_moe_batch_parity(hip, oracle, built, case):
     x = rng.standard_normal((T, hidden)).astype(np.float32)
     counts = np.bincount(ids.reshape(-1), minlength=n_expert)
     print(f"pairs per expert: max {counts.max()}, experts with >= 16: {int((counts >= 16).sum())}")
-    want = np.stack([oracle.moe_layer_q8(odesc, x[t], ids[t], w[t]) for t in range(T)])
+    with cf.ThreadPoolExecutor(8) as ex:   # the oracle's C calls release the GIL
+        want = np.stack(list(ex.map(lambda t: oracle.moe_layer_q8(odesc, x[t], ids[t], w[t]), range(T))))
     dids, dw, dx = hip.to_device(ids), hip.to_device(w), hip.to_device(x)
     outs = {}
     for name, thr in (("default", 0), ("all-mfma", 1), ("all-gemv", 1000)):
@@ -105,11 +109,9 @@ def test_moe_batch_parity(hip, oracle, built, case):
         tok = [rel_l2(got[t], want[t]) for t in range(T)]
         print(f"{name}: batch rel_L2 {rel_l2(got, want):.2e}, median token {np.median(tok):.2e}, "
               f"worst token {max(tok):.2e}")
-        assert np.median(tok) <= 1e-5
-        assert rel_l2(got, want) <= 1e-4
-        assert max(tok) <= 1e-3
+        assert max(tok) <= 1e-5
         outs[name] = got
-    assert rel_l2(outs["all-mfma"], outs["all-gemv"]) <= 1e-4
+    assert max(rel_l2(outs["all-mfma"][t], outs["all-gemv"][t]) for t in range(T)) <= 1e-5
 
 
 def test_moe_batch_single_token_matches_layer(hip, oracle, built):
