@@ -41,6 +41,7 @@ uint8_t *g_hq8 = nullptr;
 size_t g_hq8_cap = 0;
 int32_t *g_route = nullptr;   // [ids | weights] from kernel A to kernel B
 int32_t *g_err_dev = nullptr;
+uint32_t *g_fsync = nullptr;  // the fused layer's generation word and flags (zeroed once)
 
 int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 int fail(int code, const char *fmt, ...) {
@@ -135,6 +136,9 @@ int moe_scratch(size_t hq8_bytes) {
         if (e != hipSuccess) return hip_fail(e, "hipMalloc(moe routing scratch)");
         if ((e = hipMalloc((void **)&g_err_dev, 64)) != hipSuccess) return hip_fail(e, "hipMalloc(moe err)");
         if ((e = hipMemset(g_err_dev, 0, 64)) != hipSuccess) return hip_fail(e, "hipMemset");
+        if ((e = hipMalloc((void **)&g_fsync, kq::fsync_words() * 4)) != hipSuccess)
+            return hip_fail(e, "hipMalloc(fused-layer flags)");
+        if ((e = hipMemset(g_fsync, 0, kq::fsync_words() * 4)) != hipSuccess) return hip_fail(e, "hipMemset");
     }
     if (hq8_bytes > g_hq8_cap) {
         if (g_capturing) return fail(KATALI_HIP_E_INVALID, "MoE scratch must grow outside graph capture");
@@ -219,7 +223,11 @@ int moe_impl(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, 
     a.route_w = (float *)(g_route + kq::moe_route_words() / 2);
     a.dbg_gu = gu_dbg;
     a.err = g_err_dev;
-    rc = launched(kq::launch_moe(a, g_stream), "moe launch");
+    a.fsync = g_fsync;
+    // the one-launch layer is opt-in: measured slower than kernels A and B
+    // on MI355X (its in-kernel h exchange costs more than the launch it saves)
+    const bool allow_fused = env_on("KATALI_HIP_FUSED");
+    rc = launched(kq::launch_moe(a, g_stream, allow_fused), "moe launch");
     if (rc) return rc;
     if (hq8_dbg) {
         hipError_t e = hipMemcpyAsync(hq8_dbg, g_hq8, hq8_bytes, hipMemcpyDeviceToDevice, g_stream);
@@ -399,6 +407,12 @@ int katali_hip_sync(void) {
         if (e != hipSuccess) return hip_fail(e, "read error word");
         if (err) {
             (void)hipMemset(g_err_dev, 0, 4);
+            if (err & 4) {
+                // a fused layer gave up waiting (the device was shared with
+                // other work): its output and the flags are void; start over
+                if (g_fsync) (void)hipMemset(g_fsync, 0, kq::fsync_words() * 4);
+                return fail(KATALI_HIP_E_TIMEOUT, "fused MoE layer: in-kernel wait expired (output invalid)");
+            }
             return fail(KATALI_HIP_E_INVALID, "MoE expert id outside [0, n_expert) in the explicit routing");
         }
     }

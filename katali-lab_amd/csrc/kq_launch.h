@@ -95,7 +95,8 @@ struct MoeArgs {
     int32_t *route_ids;      // scratch [moe_route_words()/2]: routing from kernel A to kernel B
     float *route_w;
     float *dbg_gu;           // optional [n_slots][2][ffn] gate/up outputs
-    int32_t *err;            // error word (bit 1: expert id out of range)
+    int32_t *err;            // error word (bit 1: expert id out of range, bit 2: fused-layer wait expired)
+    uint32_t *fsync;         // fused layer's exchange (layout at fsync_words())
     // Batched layer (several tokens): a pair p = t * bS + r is token t's rank
     // r (r == n_sel: the shared expert). bslot holds *bcount {expert, first,
     // count} entries whose pairs are border[first .. first + count); x comes
@@ -109,7 +110,15 @@ struct MoeArgs {
     float *yp;
 };
 bool moe_shape_supported(uint32_t gate_type, uint32_t down_type, uint32_t hidden, uint32_t ffn);
-hipError_t launch_moe(const MoeArgs &a, hipStream_t s);
+// The layer in one launch when the shape fits the fused kernel and a.fsync is
+// set (and `allow_fused`), else kernels A and B. *fused tells which ran.
+hipError_t launch_moe(const MoeArgs &a, hipStream_t s, bool allow_fused = false, bool *fused = nullptr);
+// The fused layer's exchange (zeroed once, before first use): [0] the
+// generation, from FSYNC_H one block per workgroup of 9 8-byte words
+// {dword, generation} (its q8_1 h block, or zeros).
+constexpr uint32_t FSYNC_H = 64;
+constexpr uint32_t FUSED_MAX_G = 256;   // workgroups of the fused layer
+constexpr uint32_t fsync_words() { return FSYNC_H + 2 * 9 * FUSED_MAX_G; }
 // Top-n_sel routing of n_tokens rows of logits [n_tokens][n_expert] (<= 512
 // experts, 1 <= n_sel <= min(16, n_expert)): ids / weights [n_tokens][n_sel],
 // each row as the single-token layer routes it.

@@ -36,6 +36,26 @@ constexpr uint32_t B_MAX_THREADS = 512;   // kernel B's largest workgroup
 constexpr int MAX_SLOTS = MAX_SEL + 1;
 constexpr uint32_t MAX_EXPERT = 512;
 
+// Device-coherent 32-bit accesses (relaxed, agent scope): the store reaches
+// the point every XCD's L2 reads through and the load does not answer from a
+// stale line of its own XCD's L2, with no cache-wide write-back or
+// invalidate. The fused layer's h blocks and flags travel this way only.
+__device__ __forceinline__ void st_dev(uint32_t *p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_dev(uint32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_dev2(uint32_t *p) {   // p 8-byte aligned
+    return __hip_atomic_load((uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev2(uint32_t *p, uint64_t v) {   // p 8-byte aligned
+    __hip_atomic_store((uint64_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// polls of the fused layer's wait before it gives up (each at least one
+// device round trip: ~1 s in all); expiry sets error bit 4
+constexpr uint32_t FSYNC_SPIN_LIMIT = 1u << 20;
+
 
 __device__ __forceinline__ const float *route_logits(const MoeArgs &a) {
     const float *l = a.logits;
@@ -298,8 +318,51 @@ constexpr int a1_rw() { return NB >= 2 && NB <= 8 ? 4 : 8; }
 template <int NB>
 constexpr int a1_threads() { return 64 * 64 / a1_rw<NB>(); }
 
-template <int NB, int C>
-__global__ void __launch_bounds__(a1_threads<NB>()) k_moe_gu(MoeArgs a) {
+// The routing of one wave: lane r < n_sel ends with the expert of rank r
+// (rt.eid) and, when logits route, its canonical logit (rt.logit); with an
+// explicit selection, its weight (rt.w). Issue and finish are split so the
+// caller can put other loads between them.
+struct GuRoute {
+    int32_t eid;
+    float logit;
+    float w;
+};
+template <int C>
+__device__ __forceinline__ void route_issue(const MoeArgs &a, float (&lv)[C], GuRoute &rt) {
+    const uint32_t lane = threadIdx.x & 63;
+    rt.eid = -1;
+    rt.logit = 0.0f;
+    rt.w = 0.0f;
+    if (a.n_sel > 0) {
+        if (a.logits) {
+            load_keys<C>(a, lv);
+        } else {
+            const uint32_t r = min(lane, (uint32_t)a.n_sel - 1);
+            rt.eid = a.ids[r];
+            rt.w = a.wts[r];
+        }
+    }
+}
+template <int C>
+__device__ __forceinline__ void route_finish(const MoeArgs &a, const float (&lv)[C], GuRoute &rt) {
+    if (a.logits && a.n_sel > 0) {
+        const WaveRoute r = wave_topk<C>(a, lv);
+        rt.eid = r.id;
+        rt.logit = r.logit;
+    }
+}
+
+// One gate/up unit (32 gate + 32 up rows of one slot, one q8_1 block of h)
+// for the workgroup: kernel A's whole body, and the first phase of the fused
+// layer (FUSED: h also goes out as generation-tagged device-coherent words,
+// then every wave runs `after`, the down tile's loads).
+struct NoMore {
+    __device__ void operator()(const GuRoute &) const {}
+};
+template <int NB, int C, bool FUSED, class After = NoMore>
+__device__ __forceinline__ void gu_unit(const MoeArgs &a, uint32_t unit, uint8_t *lds, GuRoute &rt, uint32_t flag,
+                                        After after = After()) {
+    // FUSED: flag is this call's generation; h's words are tagged flag + 1
     constexpr int RW = a1_rw<NB>();
     constexpr int NT = a1_threads<NB>();
     constexpr int ITEMS = 8 * NB;              // lane items per row
@@ -310,30 +373,19 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_gu(MoeArgs a) {
     constexpr int M = ITEMS >= 64 ? ITEMS / 64 : 1;   // items per lane
     constexpr int WH = RW * NB;                // block headers of one wave's rows
     constexpr int HPL = (WH + 63) / 64;        // header loads per lane
-    extern __shared__ __align__(16) uint8_t lds[];
     const LdsA L = lds_a(a.hidden, NB);
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t nblk = a.ffn / 32;
-    const uint32_t slot = blockIdx.x / nblk, jb = blockIdx.x % nblk;
+    const uint32_t slot = unit / nblk, jb = unit % nblk;
     const uint8_t *xq = a.xq;
-    const bool publisher = blockIdx.x == 0 && wave == 0;
+    const bool publisher = unit == 0 && wave == 0;
     pin_args(a.gate, a.up, a.gate_sh, a.up_sh, a.hq8);
 
     // routing inputs, then x (fp32 or q8_1; lane task t covers values
     // 4t..4t+3); their latencies overlap. Loads are clamped, not guarded: no
     // branch sits around a load.
     float lv[C];
-    int32_t eid = -1;
-    float ew = 0.0f;
-    if (a.n_sel > 0) {
-        if (a.logits) {
-            load_keys<C>(a, lv);
-        } else {
-            const uint32_t r = min(lane, (uint32_t)a.n_sel - 1);
-            eid = a.ids[r];
-            ew = a.wts[r];
-        }
-    }
+    route_issue<C>(a, lv, rt);
     constexpr int XTASKS = 64 * NB;            // quantizer lane tasks (8 per 32-block)
     constexpr int XPT = (XTASKS + NT - 1) / NT;
     float4 xv[XPT];
@@ -350,12 +402,7 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_gu(MoeArgs a) {
             xdv[i] = ld_u16(b);
         }
     }
-    float route_l = 0.0f;
-    if (a.logits && a.n_sel > 0) {
-        const WaveRoute r = wave_topk<C>(a, lv);
-        eid = r.id;
-        route_l = r.logit;
-    }
+    route_finish<C>(a, lv, rt);
     // Drain the routing and x loads here, in one place: with loads issued
     // under branches the compiler cannot tell which registers are still
     // pending and would otherwise wait for the weight loads one by one.
@@ -364,7 +411,7 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_gu(MoeArgs a) {
     const uint64_t rb = NB * 144;
     const uint8_t *gb, *ub;
     if ((int)slot < a.n_sel) {
-        int32_t id = __builtin_amdgcn_readlane(eid, (int)slot);
+        int32_t id = __builtin_amdgcn_readlane(rt.eid, (int)slot);
         if ((uint32_t)id >= a.n_expert) id = 0;   // bad explicit id: reported by route_publish
         const uint64_t e = (uint64_t)id;
         gb = a.gate + e * a.ffn * rb;
@@ -433,10 +480,7 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_gu(MoeArgs a) {
 #pragma unroll
     for (int k = 0; k < LPG; k++) q[k] = ld16(chunk(0, k));
 
-    if (publisher) {
-        if (a.logits && a.n_sel > 0) ew = route_weight(route_l, a.n_sel);
-        route_publish(a, eid, ew);
-    }
+    if (publisher) route_publish(a, rt.eid, a.logits && a.n_sel > 0 ? route_weight(rt.logit, a.n_sel) : rt.w);
     if (!x_first) stage_x();   // x is ready long before the weights: off the critical path
     XSlice xs[M];
 #pragma unroll
@@ -507,11 +551,40 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_gu(MoeArgs a) {
         uint8_t *blk = a.hq8 + ((uint64_t)slot * nblk + jb) * 36;
         if (lane < 32) blk[4 + lane] = (uint8_t)(qv & 255);
         if (lane == 0) *(uint32_t *)blk = f2h_rne(d) | (f2h_rne((float)total * d) << 16);
+        if constexpr (FUSED) {
+            // the block's 9 dwords again, each as one 8-byte device-coherent
+            // word {dword, generation + 1}: a reader that sees the tag sees
+            // the dword with it, so nothing here waits for the stores
+            uint8_t *stage = lds + L.xact;   // the x area is free by now
+            if (lane < 32) stage[4 + lane] = (uint8_t)(qv & 255);
+            if (lane == 0) *(uint32_t *)stage = f2h_rne(d) | (f2h_rne((float)total * d) << 16);
+            wave_sync_lds();
+            uint32_t g = flag;   // the generation: made opaque here so no earlier use waits for its load
+            asm volatile("" : "+v"(g));
+            if (lane < 9)
+                st_dev2(a.fsync + FSYNC_H + 2 * (9 * blockIdx.x + lane),
+                        ((uint64_t)(g + 1) << 32) | ((const uint32_t *)stage)[lane]);
+        }
     }
     if (a.dbg_gu && tid < 64) {
         float *d = a.dbg_gu + (uint64_t)slot * 2 * a.ffn + (tid < 32 ? 0 : a.ffn) + 32 * jb + (tid & 31);
         *d = gu[tid];
     }
+    if constexpr (FUSED) {
+        // h is out: now the fused layer's down-tile loads (a barrier that
+        // orders LDS alone, so nobody waits for h's stores to be acknowledged)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        after(rt);
+    }
+}
+
+template <int NB, int C>
+__global__ void __launch_bounds__(a1_threads<NB>()) k_moe_gu(MoeArgs a) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    GuRoute rt;
+    gu_unit<NB, C, false>(a, blockIdx.x, lds, rt, 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -587,7 +660,7 @@ __global__ void __launch_bounds__(NT > 0 ? NT : B_MAX_THREADS) k_moe_down(MoeArg
     pin_args(a.down, a.down_sh, a.y);
     // routing (lane r holds slot r), then the h loads
     const int32_t rid = a.route_ids[min(lane, (uint32_t)MAX_SLOTS - 1)];
-    const float rw = a.route_w[min(lane, (uint32_t)MAX_SLOTS - 1)];
+    float rw = a.route_w[min(lane, (uint32_t)MAX_SLOTS - 1)];
     const uint32_t ntask = n_slots * (a.ffn / 32) * 2;
     constexpr int HT = P >= 16 ? 4 : 2;
     HLoad<HT> hv;
@@ -637,6 +710,9 @@ __global__ void __launch_bounds__(NT > 0 ? NT : B_MAX_THREADS) k_moe_down(MoeArg
     x = group_sum<S>(x);
     float *res = (float *)(lds + L.res);
     if (active && s == 0) res[ls] = x;
+    // every lane's weight in place before the row branch reads it by lane
+    // (the compiler could otherwise sink the load into the branch)
+    asm volatile("" : "+v"(rw));
     __syncthreads();
     if (tid < nrows) {
         // rank order, one fmaf per slot: y = w_{n-1} r_{n-1} + (... + (w_0 r_0 + 0))
@@ -883,6 +959,267 @@ __global__ void __launch_bounds__(256) k_moe_down_grp(MoeArgs a, uint32_t tr) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// The fused layer: one launch per layer. The grid never exceeds the CU count
+// and a workgroup fits an empty CU, so every workgroup is resident at once
+// and the wait below ends. Workgroup w:
+//   1. w < U = n_slots * ffn/32: gate/up unit w exactly as kernel A;
+//   2. publishes its exchange block: 9 device-coherent 8-byte words
+//      {dword, gen + 1} (its q8_1 h block, or zeros without a unit). A
+//      reader that sees a word's tag sees its dword, so nothing waits for
+//      these stores;
+//   3. loads its down tile (output rows w*tr .., every slot of each row, S
+//      lanes per pair) once its own gate/up is done: issued earlier, behind
+//      the gate/up loads, they stall the CU's issue (its outstanding-request
+//      capacity) and the unit's dots wait (measured: 2 us later);
+//   4. reads every workgroup's block until all words carry gen + 1 (that
+//      read is h), stages h into LDS, dots, and sums each row's slots in
+//      rank order.
+// gen: every workgroup reads it before it publishes, so once workgroup 0
+// has seen every block, every read is done and it advances gen for the next
+// call. Nothing is cleared between calls (graph replays included): stale
+// words carry an older generation.
+// ---------------------------------------------------------------------------
+struct LdsF {
+    uint32_t hacts, res, wts, vote, total;
+};
+__host__ __device__ inline LdsF lds_f(uint32_t hidden, uint32_t nb, uint32_t ffn, uint32_t n_slots, uint32_t tr) {
+    LdsF L;
+    L.hacts = lds_a(hidden, nb).total;
+    L.res = L.hacts + n_slots * act_bytes(ffn);
+    L.wts = L.res + (tr * n_slots + MAX_SLOTS) * 4;   // padding: the unrolled slot sum reads past the tile
+    L.vote = L.wts + MAX_SLOTS * 4;
+    L.total = L.vote + 2 * 16 * 4;
+    return L;
+}
+// AND of a predicate over the workgroup, exchanged through LDS with fences
+// that order LDS alone: unlike __syncthreads it does not wait for this
+// workgroup's global stores to be acknowledged. Alternate `parity` between
+// consecutive calls (two vote buffers of 16 waves).
+__device__ __forceinline__ bool wg_and_lds(bool ok, int *vote, uint32_t parity) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
+    int *v = vote + 16 * (parity & 1);
+    const bool w = __all(ok);
+    if (lane == 0) v[wave] = w;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    bool all = true;
+    for (uint32_t i = 0; i < nwave; i++) all = all && v[i] != 0;
+    return all;
+}
+// Waves 0 .. 7 hold the down tile (its weights and dots), waves 8 .. 15 read
+// the exchange: a wave's loads complete in issue order, so a poll issued
+// behind a wave's down-weight loads could not be seen before those arrive
+// (measured: h seen 3.1 us after its last store with one wave doing both).
+constexpr uint32_t FUSED_DOWN_THREADS = 512;
+constexpr int FUSED_HW = 5;   // exchange words per polling thread: 9 * G <= 5 * 512
+
+template <int NB, int C, class QD, int S, int IPL>
+__global__ void __launch_bounds__(a1_threads<NB>()) k_moe_fused(MoeArgs a, uint32_t tr, uint32_t n_slots) {
+    constexpr uint32_t NP = a1_threads<NB>() - FUSED_DOWN_THREADS;   // polling threads
+    constexpr uint32_t P = S / QD::IPB;   // block slots per pair: lane s takes blocks s / IPB + P * i
+    extern __shared__ __align__(16) uint8_t lds[];
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t w = blockIdx.x, G = gridDim.x;
+    const uint32_t nblk = a.ffn / 32, U = n_slots * nblk;
+    const LdsF L = lds_f(a.hidden, NB, a.ffn, n_slots, tr);
+    const bool poller = tid >= FUSED_DOWN_THREADS;
+    pin_args(a.down, a.down_sh, a.y, a.fsync, a.hq8);
+    // this call's generation: issued first, used last (any arithmetic on it
+    // here would wait for the load before the routing loads go out)
+    const uint32_t gen = ld_dev(a.fsync);
+
+    // the down tile's pair ls = (row r, slot sl) on S lanes of waves 0 .. 7;
+    // lane s of it takes item s % IPB of blocks s / IPB + P * i
+    const uint32_t s = tid % S, ls = tid / S;
+    const uint32_t item = s % QD::IPB, bs = s / QD::IPB;
+    const uint32_t nbk = a.ffn / 256;
+    const uint32_t row0 = w * tr;
+    const uint32_t nrows = min(tr, a.hidden - row0);   // the host keeps row0 < hidden
+    const uint32_t npairs = nrows * n_slots;
+    const uint32_t lc = min(ls, npairs - 1);   // idle lane-slots (and the pollers) address a real pair
+    const uint32_t sl = lc % n_slots, r = lc / n_slots;
+    const uint64_t rbd = (uint64_t)nbk * QD::BB;
+    typename QD::Raw raw[IPL];
+    auto load_down = [&](const GuRoute &rt) {
+        int32_t sid = __shfl(rt.eid, (int)sl, WAVE);
+        if ((uint32_t)sid >= a.n_expert) sid = 0;   // bad explicit id: reported by route_publish
+        const uint8_t *rp = ((int)sl < a.n_sel ? a.down + (uint64_t)sid * a.hidden * rbd : a.down_sh) +
+                            (uint64_t)(row0 + r) * rbd;
+        if (!poller) {   // whole waves
+#pragma unroll
+            for (int i = 0; i < IPL; i++) raw[i] = QD::load(rp + min(bs + P * i, nbk - 1) * QD::BB, (int)item);
+        }
+    };
+    GuRoute rt;
+    if (w < U) {
+        gu_unit<NB, C, true>(a, w, lds, rt, gen, load_down);
+    } else {
+        float lv[C];
+        route_issue<C>(a, lv, rt);
+        route_finish<C>(a, lv, rt);
+        uint32_t g = gen;
+        asm volatile("" : "+v"(g));
+        if (tid < 9) st_dev2(a.fsync + FSYNC_H + 2 * (9 * w + tid), (uint64_t)(g + 1) << 32);
+        load_down(rt);
+    }
+    // routing weights: lane k = slot k (the shared expert weighs 1)
+    float rw = a.logits && a.n_sel > 0 ? route_weight(rt.logit, a.n_sel) : rt.w;
+    rw = (int)lane < a.n_sel ? rw : ((int)lane == a.n_sel && a.has_shared ? 1.0f : 0.0f);
+
+    // every workgroup's block, until all carry gen + 1 (the pollers read;
+    // everyone votes)
+    uint32_t tag = gen;
+    asm volatile("" : "+v"(tag));
+    tag += 1;
+    const uint32_t nw = 9 * G, pt = tid - FUSED_DOWN_THREADS;
+    uint32_t *xw = a.fsync + FSYNC_H;
+    uint32_t spins = 0;
+    uint64_t v[FUSED_HW];
+    for (;;) {
+        bool ok = true;
+        if (poller) {   // whole waves
+#pragma unroll
+            for (int i = 0; i < FUSED_HW; i++) v[i] = ld_dev2(xw + 2 * min(pt + NP * i, nw - 1));
+#pragma unroll
+            for (int i = 0; i < FUSED_HW; i++) ok &= (uint32_t)(v[i] >> 32) == tag;
+        }
+        if (wg_and_lds(ok, (int *)(lds + L.vote), spins)) break;
+        if (++spins >= FSYNC_SPIN_LIMIT) {
+            if (tid == 0) atomicOr(a.err, 4);
+            break;
+        }
+        if (poller) __builtin_amdgcn_s_sleep(1);
+    }
+    if (w == 0 && tid == 0) st_dev(a.fsync, tag);   // every workgroup has read gen: the next call's
+
+    // h into LDS: word t = dword t % 9 of block t / 9 (dword 0: d and s;
+    // blocks past U are the other workgroups' empty ones)
+    const uint32_t ab = act_bytes(a.ffn);
+    if (poller) {
+#pragma unroll
+        for (int i = 0; i < FUSED_HW; i++) {
+            const uint32_t t = pt + NP * i;
+            if (t < 9 * U) {
+                const uint32_t b = t / 9, k = t % 9, kb = b % nblk;
+                const Act act = act_carve(lds + L.hacts + (b / nblk) * ab, a.ffn);
+                const uint32_t dw = (uint32_t)v[i];
+                if (k == 0) act.d8[kb] = h2f(dw & 0xFFFFu);
+                else *(uint32_t *)(act.qs + 32 * kb + 4 * (k - 1)) = dw;
+            }
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    // exact sums of each 16-value half block
+    for (uint32_t t = tid; t < 2 * U; t += blockDim.x) {
+        const uint32_t b = t >> 1, half = t & 1, kb = b % nblk;
+        const Act act = act_carve(lds + L.hacts + (b / nblk) * ab, a.ffn);
+        const uint4 q = *(const uint4 *)(act.qs + 32 * kb + 16 * half);
+        int sum = dot4(q.x, 0x01010101u, 0);
+        sum = dot4(q.y, 0x01010101u, sum);
+        sum = dot4(q.z, 0x01010101u, sum);
+        sum = dot4(q.w, 0x01010101u, sum);
+        act.qs16[2 * kb + half] = sum;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+
+    float *res = (float *)(lds + L.res), *wts = (float *)(lds + L.wts);
+    if (!poller) {   // whole waves
+        float x = 0.0f;
+        const Act act = act_carve(lds + L.hacts + sl * ab, a.ffn);
+#pragma unroll
+        for (int i = 0; i < IPL; i++) {
+            const uint32_t b = bs + P * i;
+            const float d = QD::dot_q8(raw[i], (int)item, act, min(b, nbk - 1));
+            x += b < nbk ? d : 0.0f;
+        }
+        x = group_sum<S>(x);
+        if (ls < npairs && s == 0) res[ls] = x;
+    }
+    // the slot weights through LDS: read back by lane from inside the row
+    // branch below, a register's other lanes may never have been computed
+    // (the compiler sinks the weight arithmetic into the branch)
+    if (tid < MAX_SLOTS) wts[tid] = rw;
+    __syncthreads();
+    if (tid < nrows) {
+        // rank order, one fmaf per slot: y = w_{n-1} r_{n-1} + (... + (w_0 r_0 + 0))
+        float y = 0.0f;
+#pragma unroll
+        for (int k = 0; k < MAX_SLOTS; k++) {
+            const float v2 = res[tid * n_slots + k];
+            y = k < (int)n_slots ? fmaf(wts[k], v2, y) : y;
+        }
+        a.y[row0 + tid] = y;
+    }
+}
+
+template <int NB, int C, class QD, int S, int IPL>
+static hipError_t go_fused(const MoeArgs &a, uint32_t n_slots, uint32_t tr, uint32_t G, hipStream_t s) {
+    const LdsF L = lds_f(a.hidden, NB, a.ffn, n_slots, tr);
+    if (L.total > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute((const void *)k_moe_fused<NB, C, QD, S, IPL>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)L.total);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL((k_moe_fused<NB, C, QD, S, IPL>), dim3(G), dim3(a1_threads<NB>()), L.total, s, a, tr, n_slots);
+    return hipGetLastError();
+}
+// S lanes per pair (QD::IPB items of P = S / IPB block slots), IPL blocks per lane
+template <int NB, int C, class QD>
+static hipError_t go_fused_s(const MoeArgs &a, uint32_t n_slots, uint32_t tr, uint32_t G, uint32_t S, uint32_t ipl,
+                             hipStream_t s) {
+    constexpr uint32_t B = QD::IPB;
+    switch (S / B * 8 + ipl) {
+        case 1 * 8 + 1: return go_fused<NB, C, QD, B, 1>(a, n_slots, tr, G, s);
+        case 1 * 8 + 2: return go_fused<NB, C, QD, B, 2>(a, n_slots, tr, G, s);
+        case 1 * 8 + 3: return go_fused<NB, C, QD, B, 3>(a, n_slots, tr, G, s);
+        case 1 * 8 + 4: return go_fused<NB, C, QD, B, 4>(a, n_slots, tr, G, s);
+        case 2 * 8 + 1: return go_fused<NB, C, QD, 2 * B, 1>(a, n_slots, tr, G, s);
+        case 2 * 8 + 2: return go_fused<NB, C, QD, 2 * B, 2>(a, n_slots, tr, G, s);
+        case 4 * 8 + 1: return go_fused<NB, C, QD, 4 * B, 1>(a, n_slots, tr, G, s);
+        default: return hipErrorNotSupported;
+    }
+}
+template <int NB, int C>
+static hipError_t go_fused_q(const MoeArgs &a, uint32_t n_slots, uint32_t tr, uint32_t G, uint32_t S, uint32_t ipl,
+                             hipStream_t s) {
+    return a.down_type == T_Q6_K ? go_fused_s<NB, C, Q6K>(a, n_slots, tr, G, S, ipl, s)
+                                 : go_fused_s<NB, C, Q4K>(a, n_slots, tr, G, S, ipl, s);
+}
+template <int NB>
+static hipError_t go_fused_c(const MoeArgs &a, uint32_t n_slots, uint32_t tr, uint32_t G, uint32_t S, uint32_t ipl,
+                             hipStream_t s) {
+    if (a.n_expert <= 128) return go_fused_q<NB, 2>(a, n_slots, tr, G, S, ipl, s);
+    if (a.n_expert <= 256) return go_fused_q<NB, 4>(a, n_slots, tr, G, S, ipl, s);
+    return hipErrorNotSupported;
+}
+
+// The fused layer's shape: tr rows per workgroup so that the grid (one
+// workgroup per tr rows) fits the CUs and every gate/up unit has a
+// workgroup; the widest S (lanes per pair) whose tile fits the down waves,
+// IPL = the row's blocks over S / IPB; hipErrorNotSupported when not.
+static hipError_t launch_moe_fused(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
+    const uint32_t nb = a.hidden / 256;
+    if (!a.fsync || !(nb == 4 || nb == 8) || a.n_expert > 256) return hipErrorNotSupported;
+    const uint32_t cus = min((uint32_t)device_cu_count(), FUSED_MAX_G);
+    const uint32_t tr = (a.hidden + cus - 1) / cus;
+    const uint32_t G = (a.hidden + tr - 1) / tr;
+    const uint32_t U = n_slots * (a.ffn / 32);
+    const uint32_t ipb = a.down_type == T_Q6_K ? 4 : 8, nbk = a.ffn / 256, pairs = tr * n_slots;
+    if (U > G || 9 * G > (uint32_t)FUSED_HW * (1024 - FUSED_DOWN_THREADS) || pairs * ipb > FUSED_DOWN_THREADS)
+        return hipErrorNotSupported;
+    uint32_t S = ipb;
+    while (2 * S <= 4 * ipb && S * ipb / ipb < ipb * nbk && pairs * 2 * S <= FUSED_DOWN_THREADS) S *= 2;
+    const uint32_t P = S / ipb, ipl = (nbk + P - 1) / P;
+    if (ipl > 4 || (P > 1 && ipl > (P == 2 ? 2u : 1u))) return hipErrorNotSupported;
+    return nb == 8 ? go_fused_c<8>(a, n_slots, tr, G, S, ipl, s) : go_fused_c<4>(a, n_slots, tr, G, S, ipl, s);
+}
+
 uint64_t moe_route_words() { return 2 * MAX_SLOTS; }
 
 template <int NB>
@@ -1012,9 +1349,17 @@ hipError_t launch_route_batch(const float *logits, uint32_t n_tokens, uint32_t n
     return hipGetLastError();
 }
 
-hipError_t launch_moe(const MoeArgs &a, hipStream_t s) {
+hipError_t launch_moe(const MoeArgs &a, hipStream_t s, bool allow_fused, bool *fused) {
     if (a.n_expert > MAX_EXPERT || a.n_sel > MAX_SEL) return hipErrorInvalidValue;
     const uint32_t n_slots = (uint32_t)a.n_sel + (a.has_shared ? 1u : 0u);
+    if (fused) *fused = false;
+    if (allow_fused && a.n_sel > 0) {
+        const hipError_t f = launch_moe_fused(a, n_slots, s);
+        if (f != hipErrorNotSupported) {
+            if (fused) *fused = f == hipSuccess;
+            return f;
+        }
+    }
     const hipError_t e = go_a_any(a, n_slots, s);
     if (e != hipSuccess) return e;
     return a.down_type == T_Q6_K ? go_b_any<Q6K>(a, n_slots, s) : go_b_any<Q4K>(a, n_slots, s);

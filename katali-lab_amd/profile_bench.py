@@ -43,9 +43,9 @@ EXTRA_ARGS = {"moebatch": ["--batch-points", "8x64"]}
 PROFILE_NAME = {"moebatch": "batched_moe_moebatch_8x64", "moe48tok": "decode_token_moe48tok", "qwen8b": "k_gemv_k_moe_gu_k_moe_down_qwen8b"}
 
 
-def run(cmd, log):
+def run(cmd, log, extra_env=None):
     print("[profile] " + " ".join(cmd), flush=True)
-    env = dict(os.environ, TMPDIR="/tmp")
+    env = dict(os.environ, TMPDIR="/tmp", **(extra_env or {}))
     with open(log, "w") as f:
         p = subprocess.run(cmd, cwd="/tmp", env=env, stdout=f, stderr=subprocess.STDOUT, timeout=600)
     print(f"[profile] exit {p.returncode}", flush=True)
@@ -112,9 +112,18 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--out", required=True, help="directory for the raw rocprofv3 output")
     ap.add_argument("--summarize-only", action="store_true", help="parse an existing --out tree, run nothing")
+    ap.add_argument("--fused", action="store_true",
+                    help="the one-launch MoE layer (KATALI_HIP_FUSED=1; moe48 and moe40cold)")
     args = ap.parse_args()
     wl = args.workload
-    out = os.path.join(os.path.abspath(args.out), wl)   # rocprofv3 runs from /tmp
+    extra_env = {}
+    kernels, profile_name, traffic_name = KERNELS[wl], PROFILE_NAME.get(wl, "_".join(KERNELS[wl]) + "_" + wl), wl
+    if args.fused:
+        if wl not in ("moe48", "moe40cold"):
+            sys.exit("--fused applies to moe48 and moe40cold")
+        extra_env = {"KATALI_HIP_FUSED": "1"}
+        kernels, profile_name, traffic_name = ("k_moe_fused",), "k_moe_fused_" + wl, "fused_" + wl
+    out = os.path.join(os.path.abspath(args.out), traffic_name)   # rocprofv3 runs from /tmp
     os.makedirs(out, exist_ok=True)
     bench = [sys.executable, os.path.join(REPO, "bench.py"), "--workload", wl, "--steps", str(args.steps),
              "--warmup", str(args.warmup), "--no-cpu-baseline", "--calibrate-copy", str(COPY_MIB)] + \
@@ -130,7 +139,7 @@ def main():
     for k, c in cmds.items():
         if args.summarize_only:
             break
-        if run(c, os.path.join(out, f"{k}.log")) not in (0, 139):   # 139: profiler's own exit after results
+        if run(c, os.path.join(out, f"{k}.log"), extra_env) not in (0, 139):   # 139: profiler's own exit after results
             sys.exit(f"rocprofv3 {k} run failed (see {out}/{k}.log)")
     stats = kernel_stats(os.path.join(out, "trace"))
     fetch = counter_means(os.path.join(out, "fetch"), "FETCH_SIZE")
@@ -144,13 +153,13 @@ def main():
     w_scale = copy_bytes / cw[0][1][1]
     # per workload unit: every kernel's calls relative to the first kernel's
     # (one launch per unit), times its mean duration and traffic per dispatch
-    ref = pick(stats, KERNELS[wl][0])
+    ref = pick(stats, kernels[0])
     if not ref:
-        sys.exit(f"{KERNELS[wl][0]} missing from the trace")
+        sys.exit(f"{kernels[0]} missing from the trace")
     units = sum(c for _, (c, _) in ref)
     unit_fetch = unit_write = unit_time = 0.0
     table = []
-    for sub in KERNELS[wl]:
+    for sub in kernels:
         for name, (calls, avg) in pick(stats, sub):
             fb = fetch[name][1] * f_scale if name in fetch else float("nan")
             wb = write[name][1] * w_scale if name in write else float("nan")
@@ -160,12 +169,13 @@ def main():
             unit_write += wb * per
             unit_time += avg / 1e3 * per
     traffic = unit_fetch + unit_write
-    md = os.path.join(REPO, "profiles", f"{PROFILE_NAME.get(wl, '_'.join(KERNELS[wl]) + '_' + wl)}.md")
+    md = os.path.join(REPO, "profiles", f"{profile_name}.md")
     os.makedirs(os.path.dirname(md), exist_ok=True)
     with open(md, "w") as f:
         f.write(f"# rocprofv3 summary: {wl}\n\n")
         f.write(f"Made by `python katali-lab_amd/profile_bench.py --workload {wl} --steps {args.steps} "
-                f"--warmup {args.warmup} --out <out>`, which runs (from /tmp, TMPDIR=/tmp; paths relative to the "
+                f"--warmup {args.warmup} --out <out>{' --fused' if args.fused else ''}`, which runs (from /tmp, "
+                f"TMPDIR=/tmp{', KATALI_HIP_FUSED=1' if args.fused else ''}; paths relative to the "
                 f"repository root):\n\n")
         for k, c in cmds.items():
             txt = " ".join(c).replace(out, "<out>").replace(REPO + "/", "").replace(sys.executable, "python3")
@@ -182,7 +192,7 @@ def main():
         f.write("All kernels in the trace run (calls, avg us):\n\n")
         for name, (calls, avg) in sorted(stats.items(), key=lambda kv: -kv[1][0] * kv[1][1]):
             f.write(f"- {name[:110]}: {calls}, {avg / 1e3:.2f}\n")
-    with open(os.path.join(REPO, "profiles", f"traffic_{wl}.txt"), "w") as f:
+    with open(os.path.join(REPO, "profiles", f"traffic_{traffic_name}.txt"), "w") as f:
         f.write(f"# HBM bytes per {UNIT_NAME[wl]} from {os.path.basename(md)}\n")
         f.write(f"traffic_bytes_per_unit: {traffic:.0f}\n")
     print(open(md).read())

@@ -97,10 +97,13 @@ def run_layer(hip, m, x, n_sel, logits=None, ids=None, w=None):
             wo.download(np.float32)[:n_sel])
 
 
+@pytest.mark.parametrize("fused", [False, True], ids=["two_launch", "one_launch"])
 @pytest.mark.parametrize("case", CASES, ids=[f"h{c[0]}_f{c[1]}_e{c[2]}_k{c[3]}{'_sh' if c[4] else ''}{'_q4down' if c[5] == Q4_K else ''}" for c in CASES])
-def test_moe_layer_parity(hip, oracle, moes, case):
+def test_moe_layer_parity(hip, oracle, moes, case, fused, monkeypatch):
     hidden, ffn, n_expert, n_sel, shared, down_type = case
-    print(f"[moe] case={case}", flush=True)
+    print(f"[moe] case={case} fused={fused}", flush=True)
+    if fused:
+        monkeypatch.setenv("KATALI_HIP_FUSED", "1")   # where the shape fits the one-launch kernel
     m = moes(hidden, ffn, n_expert, shared, down_type)
     rng = np.random.default_rng(hidden + ffn + n_sel)
     x = S.activation(rng, hidden)
@@ -201,6 +204,29 @@ def test_moe_layer_vs_fp32_path_reference_bar(hip, oracle, moes, case):
     assert int(np.sum(err > 1e-3)) == 0
 
 
+@pytest.mark.parametrize("case", CASES[:6], ids=[f"h{c[0]}_f{c[1]}_e{c[2]}_k{c[3]}{'_sh' if c[4] else ''}" for c in CASES[:6]])
+def test_fused_layer_matches_two_launches(hip, oracle, moes, case, monkeypatch):
+    """The one-launch layer (KATALI_HIP_FUSED=1, where the shape fits)
+    against kernels A and B: the same gate/up bits and h blocks; y within
+    fp32 reordering of the down sums."""
+    hidden, ffn, n_expert, n_sel, shared, down_type = case
+    print(f"[moe fused vs two launches] case={case}", flush=True)
+    m = moes(hidden, ffn, n_expert, shared, down_type)
+    rng = np.random.default_rng(5 + hidden + n_sel)
+    x = S.activation(rng, hidden)
+    logits = rng.standard_normal(n_expert).astype(np.float32)
+    monkeypatch.setenv("KATALI_HIP_FUSED", "1")
+    y1, gu1, hq1, ido1, wo1 = run_layer(hip, m, x, n_sel, logits=logits)
+    monkeypatch.delenv("KATALI_HIP_FUSED")
+    y0, gu0, hq0, ido0, wo0 = run_layer(hip, m, x, n_sel, logits=logits)
+    assert np.array_equal(gu1.view(np.uint32), gu0.view(np.uint32))
+    assert np.array_equal(hq1, hq0)
+    assert ido1.tolist() == ido0.tolist() and np.array_equal(wo1.view(np.uint32), wo0.view(np.uint32))
+    r = rel_l2(y1, y0)
+    print(f"rel_L2(fused, two launches) = {r:.3e}")
+    assert r <= 1e-6
+
+
 ROUTE_CASES = [
     # n_expert, n_sel, logits
     (128, 8, "ties"),      # integer logits: many equal values across the cut
@@ -285,10 +311,14 @@ def test_moe_back_to_back_layers(hip, oracle, moes):
         assert np.array_equal(y1.view(np.uint32), ys[i].download(np.uint32))
 
 
-def test_moe_graph_replay_matches_eager(hip, oracle, moes):
+@pytest.mark.parametrize("fused", [False, True], ids=["two_launch", "one_launch"])
+def test_moe_graph_replay_matches_eager(hip, oracle, moes, fused, monkeypatch):
     """A captured per-token sequence (two layers and a step advance) replayed
     over a ring of router logits; every replay is checked against an eager
-    run, with eager work and syncs between replays."""
+    run, with eager work and syncs between replays. One launch: the layer's
+    generation-tagged exchange across replays of the same nodes."""
+    if fused:
+        monkeypatch.setenv("KATALI_HIP_FUSED", "1")
     hidden, ffn, n_expert, n_sel = 2048, 512, 256, 8
     m = moes(hidden, ffn, n_expert, True, Q6_K)
     rng = np.random.default_rng(7)
