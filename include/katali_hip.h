@@ -190,6 +190,19 @@ typedef struct KataliHipMoeRoute {
 int katali_hip_moe_layer(const KataliHipMoe *moe, const KataliHipMoeRoute *route,
                          const float *x_dev, const void *xq8_dev, float *y_dev);
 
+/* katali_hip_moe_layer without any allocation, for callers that cannot
+ * allocate device memory (code under hipGraph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. Same
+ * arguments, results bit-identical to katali_hip_moe_layer (the same
+ * kernels); its routing hand-off and q8_1 h blocks live in a fixed static
+ * device array of the library (one per GPU, held until the process ends):
+ * n_slots * ffn/32 * 36 bytes of h must fit 262144 (n_slots = n_sel + 1 with
+ * a shared expert), else KATALI_HIP_E_INVALID. The library must be
+ * initialised first (katali_hip_probe); calls that overlap on one GPU share
+ * the array and race. */
+int katali_hip_moe_layer_noalloc(const KataliHipMoe *moe, const KataliHipMoeRoute *route,
+                                 const float *x_dev, const void *xq8_dev, float *y_dev);
+
 /* Debug variant: also writes gate/up outputs gu_dev[n_slots][2][ffn] (fp32) and
  * the quantized SiLU-GLU output hq8_dev[n_slots][ffn/32][36] (slot n_sel is the
  * shared expert). */

@@ -43,6 +43,16 @@ int32_t *g_route = nullptr;   // [ids | weights] from kernel A to kernel B
 int32_t *g_err_dev = nullptr;
 uint32_t *g_fsync = nullptr;  // the fused layer's generation word and flags (zeroed once)
 
+// Scratch of katali_hip_moe_layer_noalloc: a static device array, resolved
+// to a device address once per device at init (the array's name is a host
+// stand-in, not a device address). [0, 256) the routing words kernel A hands
+// to kernel B, [256, 260) the error word (zero from load, reset by
+// katali_hip_sync after it reports), [512, ..) the q8_1 h blocks.
+constexpr size_t NOALLOC_HQ8_MAX = 256 * 1024;
+constexpr size_t NOALLOC_ERR = 256, NOALLOC_HQ8 = 512;
+__device__ __align__(256) uint8_t scratch[NOALLOC_HQ8 + NOALLOC_HQ8_MAX];
+uint8_t *g_scratch = nullptr;   // scratch's device address on g_device
+
 int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 int fail(int code, const char *fmt, ...) {
     char buf[512];
@@ -96,6 +106,10 @@ int init_locked() {
         return KATALI_HIP_E_NODEVICE;
     }
     g_stream = g_own_stream;
+    if ((e = hipGetSymbolAddress((void **)&g_scratch, HIP_SYMBOL(scratch))) != hipSuccess || !g_scratch) {
+        g_status = std::string("device init: allocation-free scratch: ") + hipGetErrorString(e);
+        return KATALI_HIP_E_NODEVICE;
+    }
     char buf[256];
     snprintf(buf, sizeof buf, "%s (%s, %d CUs, %.0f GiB)", p.name, p.gcnArchName, p.multiProcessorCount,
              (double)p.totalGlobalMem / (1024.0 * 1024.0 * 1024.0));
@@ -161,10 +175,9 @@ int moe_scratch(size_t hq8_bytes) {
     return KATALI_HIP_OK;
 }
 
-int moe_impl(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, const void *xq, float *y,
-             float *gu_dbg, void *hq8_dbg) {
-    int rc = ensure();
-    if (rc) return rc;
+// Validates a MoE call and fills everything but the scratch pointers.
+int moe_args(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, const void *xq, float *y,
+             kq::MoeArgs &a, uint32_t &n_slots) {
     if (!m || !r || m->struct_size < sizeof(KataliHipMoe) || r->struct_size < sizeof(KataliHipMoeRoute))
         return fail(KATALI_HIP_E_INVALID, "null or short MoE descriptor");
     if (m->up_type != m->gate_type || !kq::moe_shape_supported(m->gate_type, m->down_type, m->hidden, m->ffn))
@@ -188,11 +201,7 @@ int moe_impl(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, 
         if (!m->gate_exps || !m->up_exps || !m->down_exps) return fail(KATALI_HIP_E_INVALID, "null buffer");
         if (!r->logits && (!r->ids || !r->weights)) return fail(KATALI_HIP_E_INVALID, "need logits or ids+weights");
     }
-    const uint32_t n_slots = (uint32_t)r->n_sel + (shared ? 1 : 0);
-    const size_t hq8_bytes = (size_t)n_slots * (m->ffn / 32) * 36;
-    if ((rc = moe_scratch(hq8_bytes))) return rc;
-
-    kq::MoeArgs a;
+    n_slots = (uint32_t)r->n_sel + (shared ? 1 : 0);
     memset(&a, 0, sizeof a);
     a.gate = (const uint8_t *)m->gate_exps;
     a.up = (const uint8_t *)m->up_exps;
@@ -218,6 +227,18 @@ int moe_impl(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, 
     a.ids_out = r->ids_out;
     a.wts_out = r->weights_out;
     a.y = y;
+    return KATALI_HIP_OK;
+}
+
+int moe_impl(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, const void *xq, float *y,
+             float *gu_dbg, void *hq8_dbg) {
+    int rc = ensure();
+    if (rc) return rc;
+    kq::MoeArgs a;
+    uint32_t n_slots = 0;
+    if ((rc = moe_args(m, r, x, xq, y, a, n_slots))) return rc;
+    const size_t hq8_bytes = (size_t)n_slots * (m->ffn / 32) * 36;
+    if ((rc = moe_scratch(hq8_bytes))) return rc;
     a.hq8 = g_hq8;
     a.route_ids = g_route;
     a.route_w = (float *)(g_route + kq::moe_route_words() / 2);
@@ -401,6 +422,15 @@ int katali_hip_sync(void) {
     if (rc) return rc;
     hipError_t e = hipStreamSynchronize(g_stream);
     if (e != hipSuccess) return hip_fail(e, "sync");
+    {
+        int32_t err = 0;
+        e = hipMemcpy(&err, g_scratch + NOALLOC_ERR, 4, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) return hip_fail(e, "read error word");
+        if (err) {
+            (void)hipMemset(g_scratch + NOALLOC_ERR, 0, 4);
+            return fail(KATALI_HIP_E_INVALID, "MoE expert id outside [0, n_expert) in the explicit routing");
+        }
+    }
     if (g_err_dev) {
         int32_t err = 0;
         e = hipMemcpy(&err, g_err_dev, 4, hipMemcpyDeviceToHost);
@@ -569,6 +599,30 @@ int katali_hip_argmax(const float *x, uint64_t n, int32_t *out) {
         }
     }
     return launched(kq::launch_argmax(x, (uint32_t)n, g_argmax, out, g_stream), "argmax");
+}
+
+int katali_hip_moe_layer_noalloc(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, const void *xq,
+                                 float *y) {
+    // no init here (init creates streams): the library must be up already
+    if (!g_inited || !g_usable || !g_scratch)
+        return fail(KATALI_HIP_E_INVALID, "katali_hip_moe_layer_noalloc: call katali_hip_probe() first");
+    hipError_t e = hipSetDevice(g_device);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    kq::MoeArgs a;
+    uint32_t n_slots = 0;
+    int rc = moe_args(m, r, x, xq, y, a, n_slots);
+    if (rc) return rc;
+    const size_t hq8_bytes = (size_t)n_slots * (m->ffn / 32) * 36;
+    if (hq8_bytes > NOALLOC_HQ8_MAX)
+        return fail(KATALI_HIP_E_INVALID,
+                    "katali_hip_moe_layer_noalloc: %zu bytes of h scratch (n_slots %u x ffn %u / 32 x 36) above its "
+                    "%zu-byte maximum",
+                    hq8_bytes, n_slots, m->ffn, NOALLOC_HQ8_MAX);
+    a.hq8 = g_scratch + NOALLOC_HQ8;
+    a.route_ids = (int32_t *)g_scratch;
+    a.route_w = (float *)(g_scratch + 4 * kq::moe_route_words() / 2);
+    a.err = (int32_t *)(g_scratch + NOALLOC_ERR);
+    return launched(kq::launch_moe(a, g_stream), "moe launch");
 }
 
 int katali_hip_moe_layer(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, const void *xq, float *y) {

@@ -42,6 +42,7 @@ SIGNATURES = {
     "katali_hip_block_isums": (C.c_int, [_u32, _vp, _u64, _u64, _vp, _vp]),
     "katali_hip_moe_layer": (C.c_int, [_vp, _vp, _vp, _vp, _vp]),
     "katali_hip_moe_layer_debug": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "katali_hip_moe_layer_noalloc": (C.c_int, [_vp, _vp, _vp, _vp, _vp]),
     "katali_hip_step_advance": (C.c_int, [_vp, _i32]),
     "katali_hip_graph_begin": (C.c_int, []),
     "katali_hip_graph_end": (C.c_int, [C.POINTER(_vp)]),
@@ -236,6 +237,11 @@ class KataliHip:
         self.check(self.lib.katali_hip_moe_layer(C.byref(desc), C.byref(route),
                                                  None if x is None else x.ptr,
                                                  None if xq is None else xq.ptr, y.ptr))
+
+    def moe_layer_noalloc(self, desc, route, y, x=None, xq=None) -> None:
+        self.check(self.lib.katali_hip_moe_layer_noalloc(C.byref(desc), C.byref(route),
+                                                         None if x is None else x.ptr,
+                                                         None if xq is None else xq.ptr, y.ptr))
 
     def moe_layer_debug(self, desc, route, y, gu, hq8, x=None, xq=None) -> None:
         self.check(self.lib.katali_hip_moe_layer_debug(C.byref(desc), C.byref(route),

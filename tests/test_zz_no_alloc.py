@@ -1,0 +1,58 @@
+"""katali_hip_moe_layer_noalloc against katali_hip_moe_layer through the C ABI.
+
+The allocation-free entry point runs the same kernels on a static device
+scratch, so its output must be bit-identical to the allocating entry point's.
+Two calls in a row, the second with a smaller problem (fewer slots, narrower
+rows), then a shape whose h would not fit the scratch is refused before any
+launch.
+"""
+import numpy as np
+import pytest
+
+import kq_synth as S
+from katali_hip import HipError
+from oracle import Q4_K, Q6_K
+
+pytestmark = pytest.mark.gpu
+
+
+def _problem(hip, rng, hidden, ffn, n_expert, shared):
+    g = S.matrix(rng, Q4_K, n_expert * ffn, hidden)
+    u = S.matrix(rng, Q4_K, n_expert * ffn, hidden)
+    d = S.matrix(rng, Q6_K, n_expert * hidden, ffn)
+    dev = [hip.to_device(a) for a in (g, u, d)]
+    dsh = None
+    if shared:
+        dsh = tuple(hip.to_device(S.matrix(rng, t, r, c)) for t, r, c in
+                    ((Q4_K, ffn, hidden), (Q4_K, ffn, hidden), (Q6_K, hidden, ffn)))
+    return hip.moe_desc(hidden, ffn, n_expert, *dev, shared=dsh), dev, dsh
+
+
+def test_noalloc_layer_matches_allocating_layer(hip):
+    rng = np.random.default_rng(2024)
+    # the larger call first (top-8 of 128, 2048 -> 768), then a smaller one
+    for hidden, ffn, n_expert, n_sel, shared in ((2048, 768, 128, 8, False), (1024, 512, 32, 3, True)):
+        print(f"[noalloc] hidden={hidden} ffn={ffn} n_expert={n_expert} n_sel={n_sel} shared={shared}", flush=True)
+        desc, keep, keep_sh = _problem(hip, rng, hidden, ffn, n_expert, shared)
+        x = hip.to_device(S.activation(rng, hidden))
+        logits = hip.to_device(rng.standard_normal(n_expert).astype(np.float32))
+        route = hip.moe_route(n_sel, logits=logits)
+        y_ref, y_na = hip.alloc(hidden * 4), hip.alloc(hidden * 4)
+        hip.moe_layer(desc, route, y_ref, x=x)
+        hip.moe_layer_noalloc(desc, route, y_na, x=x)
+        hip.sync()
+        a, b = y_ref.download(np.uint32), y_na.download(np.uint32)
+        assert np.array_equal(a, b), int(np.sum(a != b))
+        assert np.any(a != 0)
+
+
+def test_noalloc_layer_refuses_oversized_scratch(hip):
+    # 16 routed experts + a shared expert at ffn 16384: 17 * 512 * 36 bytes of h
+    # (313,344) exceed the 262,144-byte scratch; refused before any launch
+    hidden, ffn, n_expert = 2048, 16384, 16
+    tiny = hip.alloc(256)
+    desc = hip.moe_desc(hidden, ffn, n_expert, tiny, tiny, tiny, shared=(tiny, tiny, tiny))
+    route = hip.moe_route(16, logits=tiny)
+    y = hip.alloc(hidden * 4)
+    with pytest.raises(HipError, match="maximum"):
+        hip.moe_layer_noalloc(desc, route, y, x=tiny)
