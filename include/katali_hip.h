@@ -186,9 +186,27 @@ typedef struct KataliHipMoeRoute {
 /* y[hidden] = sum_r w_r * Down_e(SiLU(Gate_e x) * Up_e x) (+ shared expert).
  * x is fp32 (x_dev) or already q8_1 (xq8_dev); exactly one is non-NULL. The
  * activation and the SiLU-GLU output are quantized to q8_1 inside the kernel;
- * dots use int8 v_dot4 with fp32 scales; the expert sum is in rank order. */
+ * dots use int8 v_dot4 with fp32 scales; the expert sum is in rank order.
+ * Shapes beyond what katali_hip_moe_check admits return an error before
+ * anything is enqueued. */
 int katali_hip_moe_layer(const KataliHipMoe *moe, const KataliHipMoeRoute *route,
                          const float *x_dev, const void *xq8_dev, float *y_dev);
+
+/* KATALI_HIP_OK when katali_hip_moe_layer (n_tokens 0) or katali_hip_moe_batch
+ * (n_tokens 1..64 tokens) runs a layer of this descriptor's shape with n_sel
+ * routed experts; else the code and last-error message the call would give.
+ * Reads only the descriptor's types, sizes and which shared-expert pointers
+ * are set; needs no device. Beyond the type and size rules (Q4_K gate/up, Q4_K
+ * or Q6_K down, hidden in {256, 512, 1024, 2048, 4096}, ffn % 256 == 0 and
+ * <= 16384, n_sel <= min(16, n_expert)), every workgroup must fit gfx950's
+ * 160 KiB of LDS (KATALI_HIP_E_UNSUPPORTED otherwise):
+ *   layer: n_slots * ffn * 11/8 + 2116 <= 163840, n_slots = n_sel + (shared
+ *          expert), i.e. n_slots * ffn <= 117617 (17 slots: ffn <= 6912;
+ *          9 slots: ffn <= 13056; up to 7 slots: every ffn);
+ *   batch: 8 * ffn * 11/8 <= 163840, i.e. ffn <= 14848.
+ * No counterpart in the reference (its CPU engine has no such limit): for a
+ * caller that decides before offloading a layer. */
+int katali_hip_moe_check(const KataliHipMoe *moe, int32_t n_sel, uint32_t n_tokens);
 
 /* katali_hip_moe_layer without any allocation, for callers that cannot
  * allocate device memory (code under hipGraph capture, tight serving loops,
@@ -196,8 +214,9 @@ int katali_hip_moe_layer(const KataliHipMoe *moe, const KataliHipMoeRoute *route
  * arguments, results bit-identical to katali_hip_moe_layer (the same
  * kernels); its routing hand-off and q8_1 h blocks live in a fixed static
  * device array of the library (one per GPU, held until the process ends):
- * n_slots * ffn/32 * 36 bytes of h must fit 262144 (n_slots = n_sel + 1 with
- * a shared expert), else KATALI_HIP_E_INVALID. The library must be
+ * n_slots * ffn/32 * 36 bytes of h must fit 135168 (n_slots = n_sel + 1 with
+ * a shared expert), else KATALI_HIP_E_INVALID; every shape that passes
+ * katali_hip_moe_check's LDS rule needs at most 132192. The library must be
  * initialised first (katali_hip_probe); calls that overlap on one GPU share
  * the array and race. */
 int katali_hip_moe_layer_noalloc(const KataliHipMoe *moe, const KataliHipMoeRoute *route,
@@ -250,6 +269,16 @@ int katali_hip_moe_batch(const KataliHipMoe *moe, const KataliHipMoeBatch *batch
 int katali_hip_step_advance(int32_t *step_dev, int32_t n_steps);
 
 /* ---- per-token graphs (hipGraph capture of the library stream) ------------ */
+/* Library scratch (the MoE layer's routing hand-off and h, the batched
+ * layer's rows, about 39 MB, argmax partials) is allocated once at its largest
+ * size by the first call that needs it, outside any capture (that first call
+ * inside a capture returns KATALI_HIP_E_INVALID), and never moves or is freed,
+ * so a captured graph stays valid whatever calls follow it. Graphs replay on
+ * the library stream and share that scratch: replays and eager calls run in
+ * stream order, never side by side. During a capture, katali_hip_malloc,
+ * upload, download, sync, memset and set_stream return KATALI_HIP_E_INVALID
+ * (each would end or corrupt the capture), and katali_hip_free is deferred to
+ * katali_hip_graph_end. */
 int katali_hip_graph_begin(void);
 int katali_hip_graph_end(void **graph);
 int katali_hip_graph_launch(void *graph);

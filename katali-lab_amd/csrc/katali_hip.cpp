@@ -35,10 +35,13 @@ hipStream_t g_stream = nullptr;
 hipStream_t g_aux_stream = nullptr;
 hipEvent_t g_ev_fork = nullptr, g_ev_join = nullptr;
 bool g_capturing = false;
+std::vector<void *> g_deferred_free;   // katali_hip_free calls made during a capture
 
-// MoE scratch
-uint8_t *g_hq8 = nullptr;
-size_t g_hq8_cap = 0;
+// MoE scratch. Every buffer is allocated once, at its largest size, on the
+// first call that needs it, and never freed or moved: a graph captured around
+// any call stays valid whatever later calls ask for.
+constexpr size_t HQ8_LAYER = 1u << 20;   // >= 17 slots x ffn/32 x 36 of every layer shape that fits LDS
+uint8_t *g_hq8 = nullptr;     // single-token layer: q8_1 h [n_slots][ffn/32]
 int32_t *g_route = nullptr;   // [ids | weights] from kernel A to kernel B
 int32_t *g_err_dev = nullptr;
 uint32_t *g_fsync = nullptr;  // the fused layer's generation word and flags (zeroed once)
@@ -47,8 +50,11 @@ uint32_t *g_fsync = nullptr;  // the fused layer's generation word and flags (ze
 // to a device address once per device at init (the array's name is a host
 // stand-in, not a device address). [0, 256) the routing words kernel A hands
 // to kernel B, [256, 260) the error word (zero from load, reset by
-// katali_hip_sync after it reports), [512, ..) the q8_1 h blocks.
-constexpr size_t NOALLOC_HQ8_MAX = 256 * 1024;
+// katali_hip_sync after it reports), [512, ..) the q8_1 h blocks. Kernel B
+// stages every slot's h in LDS, n_slots * ffn * 11/8 + 2116 <= 163840 bytes,
+// so n_slots * ffn / 256 <= 459 and h takes at most 459 * 288 = 132192
+// bytes: every layer shape the LDS admits fits the maximum below.
+constexpr size_t NOALLOC_HQ8_MAX = 132 * 1024;
 constexpr size_t NOALLOC_ERR = 256, NOALLOC_HQ8 = 512;
 __device__ __align__(256) uint8_t scratch[NOALLOC_HQ8 + NOALLOC_HQ8_MAX];
 uint8_t *g_scratch = nullptr;   // scratch's device address on g_device
@@ -140,68 +146,92 @@ int check_gemv(uint32_t type, const void *w, uint64_t rows, uint64_t cols, const
 
 int launched(hipError_t e, const char *what) { return e == hipSuccess ? KATALI_HIP_OK : hip_fail(e, what); }
 
+// Frees that katali_hip_free deferred while a capture was open.
+int release_deferred() {
+    if (g_deferred_free.empty()) return KATALI_HIP_OK;
+    hipError_t e = hipStreamSynchronize(g_stream);
+    for (void *p : g_deferred_free) {
+        const hipError_t f = hipFree(p);
+        if (e == hipSuccess) e = f;
+    }
+    g_deferred_free.clear();
+    return e == hipSuccess ? KATALI_HIP_OK : hip_fail(e, "deferred hipFree");
+}
+
 void *g_argmax = nullptr;   // argmax partials (kq::argmax_parts() * 8 bytes)
 
-// MoE scratch: allocated outside any capture; grows only when not capturing.
-int moe_scratch(size_t hq8_bytes) {
-    if (!g_route) {
-        if (g_capturing) return fail(KATALI_HIP_E_INVALID, "first MoE call must happen outside graph capture");
-        hipError_t e = hipMalloc((void **)&g_route, kq::moe_route_words() * 4);
-        if (e != hipSuccess) return hip_fail(e, "hipMalloc(moe routing scratch)");
-        if ((e = hipMalloc((void **)&g_err_dev, 64)) != hipSuccess) return hip_fail(e, "hipMalloc(moe err)");
-        if ((e = hipMemset(g_err_dev, 0, 64)) != hipSuccess) return hip_fail(e, "hipMemset");
-        if ((e = hipMalloc((void **)&g_fsync, kq::fsync_words() * 4)) != hipSuccess)
-            return hip_fail(e, "hipMalloc(fused-layer flags)");
-        if ((e = hipMemset(g_fsync, 0, kq::fsync_words() * 4)) != hipSuccess) return hip_fail(e, "hipMemset");
+// The single-token layer's scratch (routing hand-off, error word, fused-layer
+// flags, h), allocated and zeroed on the first MoE call, outside any capture.
+int moe_scratch() {
+    if (g_hq8) return KATALI_HIP_OK;
+    if (g_capturing) return fail(KATALI_HIP_E_INVALID, "first MoE call must happen outside graph capture");
+    hipError_t e = hipMalloc((void **)&g_route, kq::moe_route_words() * 4);
+    if (e == hipSuccess) e = hipMalloc((void **)&g_err_dev, 64);
+    if (e == hipSuccess) e = hipMemset(g_err_dev, 0, 64);
+    if (e == hipSuccess) e = hipMalloc((void **)&g_fsync, kq::fsync_words() * 4);
+    if (e == hipSuccess) e = hipMemset(g_fsync, 0, kq::fsync_words() * 4);
+    if (e == hipSuccess) e = hipMalloc((void **)&g_hq8, HQ8_LAYER);
+    if (e != hipSuccess) {
+        // nothing half-made stays: the next call starts over
+        for (void *p : {(void *)g_route, (void *)g_err_dev, (void *)g_fsync, (void *)g_hq8})
+            if (p) (void)hipFree(p);
+        g_route = g_err_dev = nullptr;
+        g_fsync = nullptr;
+        g_hq8 = nullptr;
+        return fail(KATALI_HIP_E_NOMEM, "MoE scratch: %s", hipGetErrorString(e));
     }
-    if (hq8_bytes > g_hq8_cap) {
-        if (g_capturing) return fail(KATALI_HIP_E_INVALID, "MoE scratch must grow outside graph capture");
-        if (g_hq8) {
-            hipError_t e = hipStreamSynchronize(g_stream);
-            if (e == hipSuccess) e = hipFree(g_hq8);
-            g_hq8 = nullptr;
-            g_hq8_cap = 0;
-            if (e != hipSuccess) return hip_fail(e, "release moe scratch");
-        }
-        size_t cap = hq8_bytes < (1u << 20) ? (1u << 20) : hq8_bytes;
-        hipError_t e = hipMalloc((void **)&g_hq8, cap);
-        if (e != hipSuccess) {
-            g_hq8 = nullptr;
-            g_hq8_cap = 0;
-            return hip_fail(e, "hipMalloc(moe scratch)");
-        }
-        g_hq8_cap = cap;
-    }
+    return KATALI_HIP_OK;
+}
+
+const char *type_name(uint32_t t) {
+    return t == KATALI_HIP_TYPE_Q4_K ? "Q4_K" : t == KATALI_HIP_TYPE_Q6_K ? "Q6_K" : "?";
+}
+
+// The shape rules of every MoE entry point (and of katali_hip_moe_check,
+// which needs no device): types and sizes, the selection, and the LDS the
+// largest workgroup takes. n_tokens 0 is the single-token layer, 1..64 the
+// batched layer.
+int moe_shape(const KataliHipMoe *m, int32_t n_sel, uint32_t n_tokens, uint32_t &n_slots) {
+    if (!m || m->struct_size < sizeof(KataliHipMoe)) return fail(KATALI_HIP_E_INVALID, "null or short MoE descriptor");
+    if (m->up_type != m->gate_type || m->ffn > 16384 ||
+        !kq::moe_shape_supported(m->gate_type, m->down_type, m->hidden, m->ffn))
+        return fail(KATALI_HIP_E_UNSUPPORTED,
+                    "MoE gate=%u up=%u down=%u hidden=%u ffn=%u: need Q4_K gate/up, Q4_K or Q6_K down, "
+                    "hidden in {256,512,1024,2048,4096}, ffn a multiple of 256 (<= 16384)",
+                    m->gate_type, m->up_type, m->down_type, m->hidden, m->ffn);
+    const bool shared = m->gate_shexp || m->up_shexp || m->down_shexp;
+    if (shared && !(m->gate_shexp && m->up_shexp && m->down_shexp))
+        return fail(KATALI_HIP_E_INVALID, "shared expert needs gate, up and down");
+    if (n_sel < 0 || n_sel > 16) return fail(KATALI_HIP_E_INVALID, "n_sel=%d (0..16)", n_sel);
+    // n_sel 0: the shared expert alone, a dense SiLU-GLU FFN through the same kernels
+    if (n_sel == 0 && !shared) return fail(KATALI_HIP_E_INVALID, "n_sel=0 needs the shared expert");
+    if (n_sel > 0 && (!m->n_expert || m->n_expert > 512 || (uint32_t)n_sel > m->n_expert))
+        return fail(KATALI_HIP_E_INVALID, "n_expert=%u n_sel=%d", m->n_expert, n_sel);
+    if (n_tokens > 64) return fail(KATALI_HIP_E_INVALID, "n_tokens=%u (1..64)", n_tokens);
+    n_slots = (uint32_t)n_sel + (shared ? 1u : 0u);
+    const uint32_t lds = n_tokens ? kq::moe_batch_lds(m->hidden, m->ffn) : kq::moe_layer_lds(m->hidden, m->ffn, n_slots);
+    if (lds > kq::LDS_PER_WG)
+        return fail(KATALI_HIP_E_UNSUPPORTED,
+                    "MoE %s hidden=%u ffn=%u, %u slot(s), down %s: a workgroup would need %u bytes of LDS, above "
+                    "the %u a gfx950 workgroup has",
+                    n_tokens ? "batch" : "layer", m->hidden, m->ffn, n_slots, type_name(m->down_type), lds,
+                    kq::LDS_PER_WG);
     return KATALI_HIP_OK;
 }
 
 // Validates a MoE call and fills everything but the scratch pointers.
 int moe_args(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, const void *xq, float *y,
              kq::MoeArgs &a, uint32_t &n_slots) {
-    if (!m || !r || m->struct_size < sizeof(KataliHipMoe) || r->struct_size < sizeof(KataliHipMoeRoute))
-        return fail(KATALI_HIP_E_INVALID, "null or short MoE descriptor");
-    if (m->up_type != m->gate_type || !kq::moe_shape_supported(m->gate_type, m->down_type, m->hidden, m->ffn))
-        return fail(KATALI_HIP_E_UNSUPPORTED,
-                    "MoE gate=%u up=%u down=%u hidden=%u ffn=%u: need Q4_K gate/up, Q4_K or Q6_K down, "
-                    "hidden in {256,512,1024,2048,4096}, ffn a multiple of 256 (<= 16384)",
-                    m->gate_type, m->up_type, m->down_type, m->hidden, m->ffn);
-    if (m->ffn > 16384) return fail(KATALI_HIP_E_INVALID, "MoE ffn=%u above 16384", m->ffn);
+    if (!r || r->struct_size < sizeof(KataliHipMoeRoute)) return fail(KATALI_HIP_E_INVALID, "null or short MoE route");
+    int rc = moe_shape(m, r->n_sel, 0, n_slots);
+    if (rc) return rc;
     if (!y) return fail(KATALI_HIP_E_INVALID, "null output");
     if ((x == nullptr) == (xq == nullptr)) return fail(KATALI_HIP_E_INVALID, "give exactly one of x_dev / xq8_dev");
-    const bool shared = m->gate_shexp || m->up_shexp || m->down_shexp;
-    if (shared && !(m->gate_shexp && m->up_shexp && m->down_shexp))
-        return fail(KATALI_HIP_E_INVALID, "shared expert needs gate, up and down");
-    if (r->n_sel < 0 || r->n_sel > 16) return fail(KATALI_HIP_E_INVALID, "n_sel=%d", r->n_sel);
-    if (r->n_sel == 0) {
-        // the shared expert alone: a dense SiLU-GLU FFN through the same kernels
-        if (!shared) return fail(KATALI_HIP_E_INVALID, "n_sel=0 needs the shared expert");
-    } else {
-        if (!m->n_expert || m->n_expert > 512) return fail(KATALI_HIP_E_INVALID, "n_expert=%u", m->n_expert);
-        if ((uint32_t)r->n_sel > m->n_expert) return fail(KATALI_HIP_E_INVALID, "n_sel=%d", r->n_sel);
+    const bool shared = n_slots > (uint32_t)r->n_sel;
+    if (r->n_sel > 0) {
         if (!m->gate_exps || !m->up_exps || !m->down_exps) return fail(KATALI_HIP_E_INVALID, "null buffer");
         if (!r->logits && (!r->ids || !r->weights)) return fail(KATALI_HIP_E_INVALID, "need logits or ids+weights");
     }
-    n_slots = (uint32_t)r->n_sel + (shared ? 1 : 0);
     memset(&a, 0, sizeof a);
     a.gate = (const uint8_t *)m->gate_exps;
     a.up = (const uint8_t *)m->up_exps;
@@ -238,7 +268,8 @@ int moe_impl(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, 
     uint32_t n_slots = 0;
     if ((rc = moe_args(m, r, x, xq, y, a, n_slots))) return rc;
     const size_t hq8_bytes = (size_t)n_slots * (m->ffn / 32) * 36;
-    if ((rc = moe_scratch(hq8_bytes))) return rc;
+    if (hq8_bytes > HQ8_LAYER) return fail(KATALI_HIP_E_UNSUPPORTED, "MoE h scratch %zu bytes", hq8_bytes);
+    if ((rc = moe_scratch())) return rc;
     a.hq8 = g_hq8;
     a.route_ids = g_route;
     a.route_w = (float *)(g_route + kq::moe_route_words() / 2);
@@ -257,60 +288,50 @@ int moe_impl(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, 
     return KATALI_HIP_OK;
 }
 
-// Batch scratch: q8_1 x rows, grouping metadata, per-pair down outputs.
+// The batched layer's scratch at its largest (64 tokens x 17 slots = 1088
+// pairs, hidden 4096, ffn 16384): q8_1 x rows, q8_1 h rows, the grouping
+// metadata and the per-pair down outputs, about 39 MB in all, allocated once
+// on the first batched call.
+constexpr uint32_t BATCH_MAX_P = 64 * 17;
+constexpr size_t BATCH_XQ = (size_t)64 * (4096 / 32) * 36;
+constexpr size_t BATCH_HQ8 = (size_t)BATCH_MAX_P * (16384 / 32) * 36;
+constexpr size_t BATCH_YP = (size_t)BATCH_MAX_P * 4096 * 4;
 uint8_t *g_bxq = nullptr;
-size_t g_bxq_cap = 0;
+uint8_t *g_bhq8 = nullptr;
 int32_t *g_bmeta = nullptr;
-size_t g_bmeta_cap = 0;
 float *g_byp = nullptr;
-size_t g_byp_cap = 0;
 
-template <class T>
-int grow(T **p, size_t *cap, size_t need, const char *what) {
-    if (need <= *cap) return KATALI_HIP_OK;
-    if (g_capturing) return fail(KATALI_HIP_E_INVALID, "%s must grow outside graph capture", what);
-    if (*p) {
-        hipError_t e = hipStreamSynchronize(g_stream);
-        if (e == hipSuccess) e = hipFree(*p);
-        *p = nullptr;
-        *cap = 0;
-        if (e != hipSuccess) return hip_fail(e, what);
-    }
-    hipError_t e = hipMalloc((void **)p, need);
+int batch_scratch() {
+    if (g_byp) return KATALI_HIP_OK;
+    if (g_capturing) return fail(KATALI_HIP_E_INVALID, "first batched MoE call must happen outside graph capture");
+    hipError_t e = hipMalloc((void **)&g_bxq, BATCH_XQ);
+    if (e == hipSuccess) e = hipMalloc((void **)&g_bhq8, BATCH_HQ8);
+    if (e == hipSuccess) e = hipMalloc((void **)&g_bmeta, (size_t)kq::moe_batch_meta_words(BATCH_MAX_P) * 4);
+    if (e == hipSuccess) e = hipMalloc((void **)&g_byp, BATCH_YP);
     if (e != hipSuccess) {
-        *p = nullptr;
-        return hip_fail(e, what);
+        for (void *p : {(void *)g_bxq, (void *)g_bhq8, (void *)g_bmeta, (void *)g_byp})
+            if (p) (void)hipFree(p);
+        g_bxq = g_bhq8 = nullptr;
+        g_bmeta = nullptr;
+        g_byp = nullptr;
+        return fail(KATALI_HIP_E_NOMEM, "MoE batch scratch: %s", hipGetErrorString(e));
     }
-    *cap = need;
     return KATALI_HIP_OK;
 }
 
 int moe_batch_impl(const KataliHipMoe *m, const KataliHipMoeBatch *b, const float *x, float *y) {
     int rc = ensure();
     if (rc) return rc;
-    if (!m || !b || m->struct_size < sizeof(KataliHipMoe) || b->struct_size < sizeof(KataliHipMoeBatch))
-        return fail(KATALI_HIP_E_INVALID, "null or short MoE batch descriptor");
-    if (m->up_type != m->gate_type || !kq::moe_shape_supported(m->gate_type, m->down_type, m->hidden, m->ffn) ||
-        m->ffn > 16384)
-        return fail(KATALI_HIP_E_UNSUPPORTED, "MoE batch shape gate=%u down=%u hidden=%u ffn=%u", m->gate_type,
-                    m->down_type, m->hidden, m->ffn);
-    if (!x || !y) return fail(KATALI_HIP_E_INVALID, "null buffer");
+    if (!b || b->struct_size < sizeof(KataliHipMoeBatch)) return fail(KATALI_HIP_E_INVALID, "null or short MoE batch");
     if (b->n_tokens < 1 || b->n_tokens > 64) return fail(KATALI_HIP_E_INVALID, "n_tokens=%u (1..64)", b->n_tokens);
-    const bool shared = m->gate_shexp || m->up_shexp || m->down_shexp;
-    if (shared && !(m->gate_shexp && m->up_shexp && m->down_shexp))
-        return fail(KATALI_HIP_E_INVALID, "shared expert needs gate, up and down");
-    if (b->n_sel < 0 || b->n_sel > 16 || (b->n_sel == 0 && !shared)) return fail(KATALI_HIP_E_INVALID, "n_sel=%d", b->n_sel);
-    if (b->n_sel > 0) {
-        if (!m->n_expert || m->n_expert > 512 || (uint32_t)b->n_sel > m->n_expert)
-            return fail(KATALI_HIP_E_INVALID, "n_expert=%u n_sel=%d", m->n_expert, b->n_sel);
-        if (!m->gate_exps || !m->up_exps || !m->down_exps || !b->ids || !b->weights)
-            return fail(KATALI_HIP_E_INVALID, "null expert tensors or routing");
-    }
-    const uint32_t T = b->n_tokens, S = (uint32_t)b->n_sel + (shared ? 1u : 0u), P = T * S;
-    if ((rc = moe_scratch((size_t)P * (m->ffn / 32) * 36))) return rc;
-    if ((rc = grow(&g_bxq, &g_bxq_cap, (size_t)T * (m->hidden / 32) * 36, "MoE batch x scratch"))) return rc;
-    if ((rc = grow(&g_bmeta, &g_bmeta_cap, (size_t)kq::moe_batch_meta_words(P) * 4, "MoE batch metadata"))) return rc;
-    if ((rc = grow(&g_byp, &g_byp_cap, (size_t)P * m->hidden * 4, "MoE batch outputs"))) return rc;
+    uint32_t S = 0;
+    if ((rc = moe_shape(m, b->n_sel, b->n_tokens, S))) return rc;
+    if (!x || !y) return fail(KATALI_HIP_E_INVALID, "null buffer");
+    if (b->n_sel > 0 && (!m->gate_exps || !m->up_exps || !m->down_exps || !b->ids || !b->weights))
+        return fail(KATALI_HIP_E_INVALID, "null expert tensors or routing");
+    const bool shared = S > (uint32_t)b->n_sel;
+    const uint32_t T = b->n_tokens;
+    if ((rc = moe_scratch()) || (rc = batch_scratch())) return rc;
     kq::MoeArgs a;
     memset(&a, 0, sizeof a);
     a.gate = (const uint8_t *)m->gate_exps;
@@ -329,7 +350,7 @@ int moe_batch_impl(const KataliHipMoe *m, const KataliHipMoeBatch *b, const floa
     a.has_shared = shared ? 1 : 0;
     a.ids = b->ids;
     a.wts = b->weights;
-    a.hq8 = g_hq8;
+    a.hq8 = g_bhq8;
     a.route_ids = g_route;
     a.route_w = (float *)(g_route + kq::moe_route_words() / 2);
     a.err = g_err_dev;
@@ -358,6 +379,7 @@ int katali_hip_malloc(void **dev, size_t bytes) {
     int rc = ensure();
     if (rc) return rc;
     if (!dev) return fail(KATALI_HIP_E_INVALID, "null out pointer");
+    if (g_capturing) return fail(KATALI_HIP_E_INVALID, "katali_hip_malloc during graph capture");
     *dev = nullptr;
     hipError_t e = hipMalloc(dev, bytes ? bytes : 1);
     if (e != hipSuccess) return fail(KATALI_HIP_E_NOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
@@ -368,6 +390,11 @@ int katali_hip_free(void *dev) {
     if (!dev) return KATALI_HIP_OK;
     int rc = ensure();
     if (rc) return rc;
+    if (g_capturing) {
+        // a synchronisation would end the capture: released after graph_end
+        g_deferred_free.push_back(dev);
+        return KATALI_HIP_OK;
+    }
     hipError_t e = hipStreamSynchronize(g_stream);
     if (e == hipSuccess) e = hipFree(dev);
     return e == hipSuccess ? KATALI_HIP_OK : hip_fail(e, "hipFree");
@@ -376,6 +403,7 @@ int katali_hip_free(void *dev) {
 int katali_hip_upload(void *dev, const void *host, size_t bytes) {
     int rc = ensure();
     if (rc) return rc;
+    if (g_capturing) return fail(KATALI_HIP_E_INVALID, "katali_hip_upload during graph capture");
     if (!bytes) return KATALI_HIP_OK;
     if (!dev || !host) return fail(KATALI_HIP_E_INVALID, "null buffer");
     hipError_t e = hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, g_stream);
@@ -386,6 +414,7 @@ int katali_hip_upload(void *dev, const void *host, size_t bytes) {
 int katali_hip_download(void *host, const void *dev, size_t bytes) {
     int rc = ensure();
     if (rc) return rc;
+    if (g_capturing) return fail(KATALI_HIP_E_INVALID, "katali_hip_download during graph capture");
     if (!bytes) return katali_hip_sync();
     if (!dev || !host) return fail(KATALI_HIP_E_INVALID, "null buffer");
     hipError_t e = hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, g_stream);
@@ -420,6 +449,7 @@ int katali_hip_matvec(uint32_t type, const void *w, uint64_t rows, uint64_t cols
 int katali_hip_sync(void) {
     int rc = ensure();
     if (rc) return rc;
+    if (g_capturing) return fail(KATALI_HIP_E_INVALID, "katali_hip_sync during graph capture");
     hipError_t e = hipStreamSynchronize(g_stream);
     if (e != hipSuccess) return hip_fail(e, "sync");
     {
@@ -453,12 +483,15 @@ int katali_hip_memset(void *dev, int value, size_t bytes) {
     int rc = ensure();
     if (rc) return rc;
     if (!dev) return fail(KATALI_HIP_E_INVALID, "null buffer");
+    // a captured memset node has given wrong results on replays after the first
+    if (g_capturing) return fail(KATALI_HIP_E_INVALID, "katali_hip_memset during graph capture");
     return launched(hipMemsetAsync(dev, value, bytes, g_stream), "memset");
 }
 
 int katali_hip_set_stream(void *s) {
     int rc = ensure();
     if (rc) return rc;
+    if (g_capturing) return fail(KATALI_HIP_E_INVALID, "katali_hip_set_stream during graph capture");
     g_stream = s ? (hipStream_t)s : g_own_stream;
     return KATALI_HIP_OK;
 }
@@ -625,6 +658,11 @@ int katali_hip_moe_layer_noalloc(const KataliHipMoe *m, const KataliHipMoeRoute 
     return launched(kq::launch_moe(a, g_stream), "moe launch");
 }
 
+int katali_hip_moe_check(const KataliHipMoe *m, int32_t n_sel, uint32_t n_tokens) {
+    uint32_t n_slots = 0;
+    return moe_shape(m, n_sel, n_tokens, n_slots);
+}
+
 int katali_hip_moe_layer(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, const void *xq, float *y) {
     return moe_impl(m, r, x, xq, y, nullptr, nullptr);
 }
@@ -658,6 +696,10 @@ int katali_hip_graph_end(void **graph) {
     g_capturing = false;
     hipGraph_t gr = nullptr;
     hipError_t e = hipStreamEndCapture(g_stream, &gr);
+    if ((rc = release_deferred())) {
+        if (gr) (void)hipGraphDestroy(gr);
+        return rc;
+    }
     if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
     hipGraphExec_t ex = nullptr;
     e = hipGraphInstantiate(&ex, gr, nullptr, nullptr, 0);

@@ -110,6 +110,16 @@ struct MoeArgs {
     float *yp;
 };
 bool moe_shape_supported(uint32_t gate_type, uint32_t down_type, uint32_t hidden, uint32_t ffn);
+// Dynamic LDS (bytes) of the largest workgroup a layer of this shape launches:
+// kernel A, kernel B (n_slots * (ffn + ffn/8 + ffn/4) for the staged h, plus
+// at most (B_MAX_THREADS + n_slots) partial sums), or for the batched layer
+// the grouped GEMV kernels (8 pairs' h) and the MFMA kernels. The host checks
+// these against the device's per-workgroup LDS before it launches anything.
+uint32_t moe_layer_lds(uint32_t hidden, uint32_t ffn, uint32_t n_slots);
+uint32_t moe_groups_lds(uint32_t hidden, uint32_t ffn);
+uint32_t moe_batch_lds(uint32_t hidden, uint32_t ffn);
+// gfx950's LDS per workgroup
+constexpr uint32_t LDS_PER_WG = 160 * 1024;
 // The layer in one launch when the shape fits the fused kernel and a.fsync is
 // set (and `allow_fused`), else kernels A and B. *fused tells which ran.
 hipError_t launch_moe(const MoeArgs &a, hipStream_t s, bool allow_fused = false, bool *fused = nullptr);

@@ -1262,6 +1262,7 @@ static hipError_t go_b(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
         }
     }
     const LdsB L = lds_b(a.ffn, n_slots, tr);
+    if (L.total > moe_layer_lds(a.hidden, a.ffn, n_slots)) return hipErrorInvalidValue;   // the host's bound
     const dim3 grid((a.hidden + tr - 1) / tr);
     // the 256-thread tiles keep their own build (a constant workgroup size)
     if (nt == 256) hipLaunchKernelGGL((k_moe_down<QD, IPL, P, 256>), grid, dim3(nt), L.total, s, a, tr, n_slots);
@@ -1305,6 +1306,20 @@ static hipError_t go_b_any(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
         }
     }
     return go_b<QD, 0, 1>(a, n_slots, s);
+}
+
+// Kernel B's tile holds tr * n_slots <= B_MAX_THREADS partial sums: tr =
+// 256 / (IPB * P) / n_slots (or 1 when that is 0, then n_slots <= MAX_SLOTS
+// sums), or tr1 with tr1 * n_slots * S <= B_MAX_THREADS lanes.
+uint32_t moe_layer_lds(uint32_t hidden, uint32_t ffn, uint32_t n_slots) {
+    const uint32_t a = lds_a(hidden, hidden / 256).total;
+    const uint32_t b = n_slots * act_bytes(ffn) + (B_MAX_THREADS + MAX_SLOTS) * 4;
+    return a > b ? a : b;
+}
+
+uint32_t moe_groups_lds(uint32_t hidden, uint32_t ffn) {
+    const uint32_t g = lds_g(hidden, hidden / 256).total, d = GRP_MAX * act_bytes(ffn);
+    return g > d ? g : d;
 }
 
 bool moe_shape_supported(uint32_t gate_type, uint32_t down_type, uint32_t hidden, uint32_t ffn) {

@@ -573,6 +573,21 @@ __global__ void __launch_bounds__(256) k_mb_combine(const float *__restrict__ yp
     y[i] = acc;
 }
 
+// dynamic LDS of the MFMA gate/up kernel (two x tiles, the block scales, the
+// epilogue's sums) and of the MFMA down kernel (up to MB_DN_CHUNK staged h
+// blocks and the scale table)
+static uint32_t mb_lds_gu() { return 2 * MBX_BYTES + 4 * 16 * 8 * 8 + 64 * 16 * 4; }
+static uint32_t mb_lds_dn(uint32_t ffn) {
+    const uint32_t nb = ffn / 256;
+    return (nb <= 3 ? nb : MB_DN_CHUNK) * MBX_BYTES + 4 * 16 * 16 * 8;
+}
+
+uint32_t moe_batch_lds(uint32_t hidden, uint32_t ffn) {
+    uint32_t m = moe_groups_lds(hidden, ffn);
+    m = m > mb_lds_gu() ? m : mb_lds_gu();
+    return m > mb_lds_dn(ffn) ? m : mb_lds_dn(ffn);
+}
+
 hipError_t launch_moe_batch(const MoeArgs &base, uint32_t T, uint32_t min_big, const float *x, float *y, uint8_t *xq,
                             int32_t *meta, hipStream_t s, hipStream_t aux, hipEvent_t fork, hipEvent_t join) {
     const uint32_t S = (uint32_t)base.n_sel + (base.has_shared ? 1u : 0u);
@@ -604,15 +619,23 @@ hipError_t launch_moe_batch(const MoeArgs &base, uint32_t T, uint32_t min_big, c
     hipStream_t sb = side ? aux : s;
     if (side && ((e = hipEventRecord(fork, s)) != hipSuccess || (e = hipStreamWaitEvent(aux, fork, 0)) != hipSuccess))
         return e;
-    if ((e = launch_moe_groups_gu(a, max_small, s)) != hipSuccess) return e;
-    if ((e = launch_moe_groups_down(a, max_small, s)) != hipSuccess) return e;
+    // after the fork every exit joins aux back into s (an unjoined side
+    // stream would leave a capture of s unable to end); the first error wins
+    auto joined = [&](hipError_t err) -> hipError_t {
+        if (!side) return err;
+        hipError_t j = hipEventRecord(join, aux);
+        if (j == hipSuccess) j = hipStreamWaitEvent(s, join, 0);
+        return err != hipSuccess ? err : j;
+    };
+    if ((e = launch_moe_groups_gu(a, max_small, s)) != hipSuccess) return joined(e);
+    if ((e = launch_moe_groups_down(a, max_small, s)) != hipSuccess) return joined(e);
     // grouped entries: each holds 1..16 pairs of one expert with >= min_big
     // pairs, so there are at most P / 16 + P / min_big + 1 of them
     const uint32_t max_big = P / MB_BIG + P / (min_big > 0 ? min_big : 1) + 1;
     auto grid_for = [&](uint32_t tiles_per_entry) { return dim3(max_big * tiles_per_entry); };
     const uint32_t nblk = base.ffn / 32;
     const uint32_t nb_gu = base.hidden / 256;
-    const uint32_t lds_gu = 2 * MBX_BYTES + 4 * 16 * 8 * 8 + 64 * 16 * 4;
+    const uint32_t lds_gu = mb_lds_gu();
     auto go_gu = [&](auto kern) -> hipError_t {
         if (!any_big) return hipSuccess;
         if (lds_gu > 64 * 1024) {
@@ -629,12 +652,12 @@ hipError_t launch_moe_batch(const MoeArgs &base, uint32_t T, uint32_t min_big, c
         case 4: e = go_gu(k_mb_gu_mfma<4>); break;
         case 8: e = go_gu(k_mb_gu_mfma<8>); break;
         case 16: e = go_gu(k_mb_gu_mfma<16>); break;
-        default: return hipErrorInvalidValue;
+        default: return joined(hipErrorInvalidValue);
     }
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess) return joined(e);
     const uint32_t ntile = (base.hidden + 63) / 64;
     const uint32_t nb_dn = base.ffn / 256;
-    const uint32_t lds_dn = (nb_dn <= 3 ? nb_dn : MB_DN_CHUNK) * MBX_BYTES + 4 * 16 * 16 * 8;
+    const uint32_t lds_dn = mb_lds_dn(base.ffn);
     auto go_dn = [&](auto kern) -> hipError_t {
         if (!any_big) return hipSuccess;
         if (lds_dn > 64 * 1024) {
@@ -660,10 +683,8 @@ hipError_t launch_moe_batch(const MoeArgs &base, uint32_t T, uint32_t min_big, c
             default: e = go_dn(k_mb_down_mfma<Q4K, 0>); break;
         }
     }
-    if (e != hipSuccess) return e;
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    if (side && ((e = hipEventRecord(join, aux)) != hipSuccess || (e = hipStreamWaitEvent(s, join, 0)) != hipSuccess))
-        return e;
+    if (e == hipSuccess) e = hipGetLastError();
+    if ((e = joined(e)) != hipSuccess) return e;
     const uint64_t n = (uint64_t)T * base.hidden;
     hipLaunchKernelGGL(k_mb_combine, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, s, a.yp, base.wts, T,
                        (uint32_t)base.n_sel, S, base.hidden, y);

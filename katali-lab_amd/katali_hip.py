@@ -43,6 +43,7 @@ SIGNATURES = {
     "katali_hip_moe_layer": (C.c_int, [_vp, _vp, _vp, _vp, _vp]),
     "katali_hip_moe_layer_debug": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "katali_hip_moe_layer_noalloc": (C.c_int, [_vp, _vp, _vp, _vp, _vp]),
+    "katali_hip_moe_check": (C.c_int, [_vp, _i32, _u32]),
     "katali_hip_step_advance": (C.c_int, [_vp, _i32]),
     "katali_hip_graph_begin": (C.c_int, []),
     "katali_hip_graph_end": (C.c_int, [C.POINTER(_vp)]),
@@ -237,6 +238,11 @@ class KataliHip:
         self.check(self.lib.katali_hip_moe_layer(C.byref(desc), C.byref(route),
                                                  None if x is None else x.ptr,
                                                  None if xq is None else xq.ptr, y.ptr))
+
+    def moe_check(self, desc, n_sel, n_tokens=0) -> None:
+        """Raises HipError when a layer (n_tokens 0) or a batch of n_tokens of
+        this shape would be refused; needs no device."""
+        self.check(self.lib.katali_hip_moe_check(C.byref(desc), n_sel, n_tokens))
 
     def moe_layer_noalloc(self, desc, route, y, x=None, xq=None) -> None:
         self.check(self.lib.katali_hip_moe_layer_noalloc(C.byref(desc), C.byref(route),

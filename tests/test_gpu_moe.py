@@ -63,6 +63,8 @@ CASES = [
     (1024, 512, 32, 3, True, Q6_K),
     (512, 256, 16, 4, False, Q4_K),      # Q4_K down projection
     (4096, 256, 8, 2, False, Q6_K),      # wide hidden: 2 items per lane in gate/up
+    (256, 2048, 16, 16, True, Q6_K),     # 17 slots, 8 blocks per down row: kernel B's block loop
+    (512, 1536, 32, 8, True, Q4_K),      # 9 slots of Q4_K down, 6 blocks per row: the block loop
 ]
 
 
