@@ -45,6 +45,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -518,11 +519,10 @@ def bench_gemv(hip, name, steps, warmup):
     return res, (t, rows, cols, copies)
 
 
-def cpu_baseline_gemv(shape, budget_s=12.0):
+def cpu_baseline_gemv(shape, threads, budget_s=8.0):
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     from oracle import RefCPU, ref_available, Oracle
     t, rows, cols, _ = shape
-    threads = int(os.environ.get("KATALI_BENCH_CPU_THREADS", min(16, os.cpu_count() or 1)))
     rng = np.random.default_rng(9)
     bb = K.BLOCK_BYTES[t]
     n = rows * cols // 256
@@ -559,11 +559,11 @@ def cpu_baseline_gemv(shape, budget_s=12.0):
         "sample": f"{calls} calls of the {rows}x{cols} {'Q4_K' if t == Q4_K else 'Q6_K'} GEMV (one weight matrix, "
                   f"cache-resident as in the reference's own probe), "
                   f"{'reference katali_ggml_matvec' if kind == 'reference' else 'oracle port of the reference AVX2 row loop'}, "
-                  f"{threads} threads, host {os.cpu_count()} logical CPUs",
+                  f"{threads} threads",
     }
 
 
-def cpu_baseline_dense(shape, budget_s=12.0):
+def cpu_baseline_dense(shape, threads, budget_s=8.0):
     """The reference CPU path on the same per-layer GEMV chain (fused q/k/v,
     o, fused gate/up, SiLU-GLU, down), distinct weights per layer."""
     sys.path.insert(0, os.path.join(REPO, "oracle"))
@@ -571,7 +571,6 @@ def cpu_baseline_dense(shape, budget_s=12.0):
     if not ref_available():
         return None
     L, hidden, q_rows, kv_rows, ffn = shape
-    threads = int(os.environ.get("KATALI_BENCH_CPU_THREADS", min(16, os.cpu_count() or 1)))
     rng = np.random.default_rng(13)
     n_layers = 4   # distinct weights for 4 layers (0.49 GB), cycled
 
@@ -625,7 +624,7 @@ def cpu_baseline_dense(shape, budget_s=12.0):
         "tok_s": (n / L) / dt,
         "sample": f"{n} layers ({n / L:.2f} tokens) of the same GEMV chain, 4 layers of distinct weights cycled "
                   f"(0.49 GB, DRAM-cold), reference katali_ggml_matvec_fused + silu_mul_avx2 + katali_ggml_matvec, "
-                  f"{threads} threads, host {os.cpu_count()} logical CPUs",
+                  f"{threads} threads",
     }
 
 
@@ -645,11 +644,10 @@ def read_traffic(workload):
 # ---------------------------------------------------------------------------
 # CPU baseline: the reference's own CPU path on a bounded sample
 # ---------------------------------------------------------------------------
-def cpu_baseline_moe(shape, budget_s=12.0):
+def cpu_baseline_moe(shape, threads, budget_s=8.0):
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     from oracle import MatvecJob, RefCPU, ref_available, Oracle
     L, hidden, ffn, n_expert, n_sel, shared = shape
-    threads = int(os.environ.get("KATALI_BENCH_CPU_THREADS", min(16, os.cpu_count() or 1)))
     rng = np.random.default_rng(5)
     slots = n_sel + (1 if shared else 0)
     rb_g, rb_d = row_bytes(Q4_K, hidden), row_bytes(Q6_K, ffn)
@@ -722,11 +720,98 @@ def cpu_baseline_moe(shape, budget_s=12.0):
         "sample": f"{tokens} token(s) x {L} layers x {slots} experts, distinct expert weights per (layer, slot) "
                   f"({L * slots * 2 * (ffn * rb_g) / 1e9 + L * slots * hidden * rb_d / 1e9:.2f} GB), "
                   f"{'reference katali_ggml_matvec_fused + silu_mul_avx2 + katali_ggml_matvec' if kind == 'reference' else 'oracle port of the reference AVX2 row loop'}, "
-                  f"{threads} threads, host {os.cpu_count()} logical CPUs",
+                  f"{threads} threads",
     }
 
 
+# The box a GPU job runs on grants it a share of the host's cores; the CPU
+# baseline uses at most this many threads whatever the host has.
+CPU_SHARE = 16
+
+
+def host_cpu():
+    """The host CPU as lscpu reports it, and the CPUs this process may run on
+    (with the socket of each)."""
+    info = {"nproc": os.cpu_count()}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        kv = {}
+        for ln in out.splitlines():
+            if ":" in ln:
+                k, v = ln.split(":", 1)
+                kv[k.strip()] = v.strip()
+        info["model"] = kv.get("Model name")
+        for key, name in (("Socket(s)", "sockets"), ("Core(s) per socket", "cores_per_socket"),
+                          ("Thread(s) per core", "threads_per_core"), ("NUMA node(s)", "numa_nodes")):
+            if kv.get(key, "").isdigit():
+                info[name] = int(kv[key])
+        if "sockets" in info and "cores_per_socket" in info:
+            info["physical_cores"] = info["sockets"] * info["cores_per_socket"]
+        info["numa"] = {k.split()[1]: v for k, v in kv.items() if k.startswith("NUMA node") and "CPU(s)" in k}
+    except (OSError, subprocess.SubprocessError):
+        info["model"] = None
+    allowed = sorted(os.sched_getaffinity(0))
+    sockets = {}
+    for c in allowed:
+        try:
+            with open(f"/sys/devices/system/cpu/cpu{c}/topology/physical_package_id") as f:
+                sockets.setdefault(int(f.read()), []).append(c)
+        except OSError:
+            sockets.setdefault(0, []).append(c)
+    info["allowed_cpus"] = len(allowed)
+    info["allowed_by_socket"] = {str(k): len(v) for k, v in sorted(sockets.items())}
+    return info, sockets
+
+
+def cpu_sample(kind, shape, threads, pin=None):
+    """One CPU baseline sample in a child process (so a pinned run starts its
+    thread pool under the pinning); it never touches the GPU."""
+    spec = json.dumps({"kind": kind, "shape": list(shape), "threads": threads, "pin": pin})
+    out = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-sample", spec], capture_output=True,
+                         text=True, timeout=600)
+    if out.returncode != 0:
+        print(f"[bench] cpu sample failed: {out.stderr[-2000:]}", file=sys.stderr, flush=True)
+        return None
+    return json.loads(out.stdout.strip().splitlines()[-1])
+
+
+def run_cpu_sample(spec):
+    s = json.loads(spec)
+    if s["pin"]:
+        os.sched_setaffinity(0, s["pin"])
+    fn = {"moe": cpu_baseline_moe, "dense": cpu_baseline_dense, "gemv": cpu_baseline_gemv}[s["kind"]]
+    print(json.dumps(fn(tuple(s["shape"]), s["threads"])), flush=True)
+
+
+def cpu_baseline(kind, shape):
+    """The reference CPU path timed twice: on every CPU this job may use (at
+    most CPU_SHARE threads) and pinned to one socket's share of them."""
+    info, sockets = host_cpu()
+    threads = int(os.environ.get("KATALI_BENCH_CPU_THREADS", min(CPU_SHARE, info["allowed_cpus"])))
+    res = cpu_sample(kind, shape, threads)
+    if res is None:
+        return None
+    sock, cpus = max(sockets.items(), key=lambda kv: len(kv[1]))
+    pinned_cpus = cpus[:threads]
+    pinned = cpu_sample(kind, shape, len(pinned_cpus), pin=pinned_cpus)
+    res["host"] = info
+    phys = info.get("physical_cores")
+    if phys is not None and threads >= phys:
+        res["threads_note"] = f"{threads} threads: all {phys} physical cores"
+    else:
+        res["threads_note"] = (f"{threads} threads: the CPUs this job may use ({info['allowed_cpus']}), capped at the "
+                               f"{CPU_SHARE}-thread share a one-GPU job gets on this host, of its {phys} physical "
+                               f"cores")
+    if pinned is not None:
+        res["pinned_one_socket"] = {"value": pinned["value"], "unit": pinned["unit"], "threads": len(pinned_cpus),
+                                    "socket": sock, "cpus": pinned_cpus}
+    return res
+
+
 def main():
+    if len(sys.argv) > 2 and sys.argv[1] == "--cpu-sample":
+        run_cpu_sample(sys.argv[2])
+        return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=64)
@@ -744,6 +829,22 @@ def main():
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the expert-parallel "
               "layout for several GPUs is a design note, not a measured path).", file=sys.stderr)
         sys.exit(2)
+
+    # the CPU baseline first, in child processes started before this process
+    # initialises the GPU
+    cpu = None
+    if not args.no_cpu_baseline:
+        if args.workload in MOE_WORKLOADS:
+            cpu = cpu_baseline("moe", MOE_WORKLOADS[args.workload])
+        elif args.workload in DENSE_WORKLOADS:
+            cpu = cpu_baseline("dense", DENSE_WORKLOADS[args.workload])
+        elif args.workload in GEMV_WORKLOADS:
+            cpu = cpu_baseline("gemv", GEMV_WORKLOADS[args.workload])
+        # moebatch and the whole-token workloads: no CPU counterpart of that
+        # exact workload is timed here
+        if cpu:
+            print(f"[bench] cpu baseline: {cpu['value']:.2f} GB/s ({cpu['kind']}, {cpu['cores']} threads)",
+                  file=sys.stderr, flush=True)
 
     hip = K.KataliHip()
     if not hip.probe():
@@ -846,19 +947,6 @@ def main():
         kernel = "k_gemv (q8_1 activation quantized in the workgroup)"
         extra = {}
     print(f"[bench] gpu done: {res['value']:.1f} GB/s", file=sys.stderr, flush=True)
-    cpu = None
-    if not args.no_cpu_baseline:
-        if args.workload == "moebatch" or args.workload in TOKEN_WORKLOADS:
-            cpu = None   # no CPU counterpart of this exact workload is timed here
-        elif args.workload in MOE_WORKLOADS:
-            cpu = cpu_baseline_moe(shape)
-        elif args.workload in DENSE_WORKLOADS:
-            cpu = cpu_baseline_dense(shape)
-        else:
-            cpu = cpu_baseline_gemv(shape)
-        if cpu:
-            print(f"[bench] cpu baseline: {cpu['value']:.2f} GB/s ({cpu['kind']}, {cpu['cores']} threads)",
-                  file=sys.stderr, flush=True)
     achieved = unit_bytes / (unit_ms / 1e3) / 1e9
     line = {
         "metric": metric,

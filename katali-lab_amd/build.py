@@ -84,7 +84,8 @@ def build_host() -> list[str]:
         outs.append(so)
         if os.path.exists(cli):
             exe = os.path.join(PKG, "katali-hip")
-            _run([CC, *C_FLAGS, cli, *srcs, "-o", exe, "-ldl", "-lm"])
+            # the harness's CPU side (GPU-versus-CPU checks) links into the CLI only
+            _run([CC, *C_FLAGS, cli, os.path.join(HOST, "katali_hip_cpu.c"), *srcs, "-o", exe, "-ldl", "-lm"])
             outs.append(exe)
     return outs
 

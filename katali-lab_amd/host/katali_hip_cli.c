@@ -7,12 +7,10 @@
  *
  *   katali-hip info                  device and library status
  *   katali-hip dp4a-selftest         q8_1 v_dot4 GEMV vs the fp32 GEMV, q8-exact x
- *   katali-hip check                 the same two GEMV paths on N(0,1) x at the
- *                                    engine's shapes: rel_L2 and the count outside
- *                                    1e-3*(1+|ref|)
- *   katali-hip check-moe             the fused MoE layer vs the same layer composed
- *                                    from separate library GEMVs (SiLU-GLU and the
- *                                    weighted sum on the host)
+ *   katali-hip check                 both GEMV paths against the CPU on N(0,1) x
+ *                                    at the engine's shapes (criteria printed)
+ *   katali-hip check-moe             the fused MoE layer against the CPU's q8_1
+ *                                    path (and, for information, its fp32 path)
  *   katali-hip matvec-bench [reps]   dense GEMV: event-timed us per call and GB/s
  *   katali-hip bench [tokens]        48-layer top-8 MoE decode (hidden 2048, 128
  *                                    experts, ffn 768), graph-replayed
@@ -32,6 +30,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "katali_hip_cpu.h"
 #include "katali_hip_gguf.h"
 #include "katali_hip_loader.h"
 
@@ -97,31 +96,66 @@ static const struct shape SHAPES[] = {
 };
 #define NSHAPES (sizeof SHAPES / sizeof SHAPES[0])
 
+/* GPU against CPU (katali_hip_cpu.c) at each shape, on N(0,1) x. PASS needs
+ * all three of:
+ *   the fp32 GEMV: every element within 1e-3*(1+|cpu|) (the engine's bar,
+ *     README.md:17) of the CPU's double-precision dot over the dequantized
+ *     rows with the same fp32 x (the largest error over that bar is printed);
+ *   the v_dot4 GEMV: rel_L2 <= 1e-5 against the CPU dot with the same q8_1 x;
+ *   the device quantizer: q8_1 blocks of x identical to the CPU's.
+ * The v_dot4 GEMV against the CPU with fp32 x (the q8_1 rounding of x, about
+ * 1e-2 on N(0,1) activations) is printed for information only. */
 static int cmd_check(void) {
     int fails = 0;
     for (size_t s = 0; s < NSHAPES; s++) {
         const struct shape *sh = &SHAPES[s];
-        void *w = NULL;
-        float *x = dalloc_f(sh->cols), *y0 = dalloc_f(sh->rows), *y1 = dalloc_f(sh->rows);
+        const uint64_t R = sh->rows, C = sh->cols, wb = R * row_bytes(sh->type, C);
+        void *w = NULL, *xq = NULL;
+        float *x = dalloc_f(C), *y0 = dalloc_f(R), *y1 = dalloc_f(R);
         if (!x || !y0 || !y1) return die("malloc", -5);
-        CK(api->malloc_(&w, sh->rows * row_bytes(sh->type, sh->cols)));
-        CK(api->synth_fill(sh->type, w, sh->rows * sh->cols / 256, 100 + s, 0.02f));
-        CK(api->synth_normal(x, sh->cols, 200 + s, 1.0f));
-        CK(api->matvec(sh->type, w, sh->rows, sh->cols, x, y0));   /* fp32 dequantize-and-FMA path */
-        CK(api->matvec_dp4a(sh->type, w, sh->rows, sh->cols, x, y1));
-        float *a = malloc(sh->rows * 4), *b = malloc(sh->rows * 4);
-        CK(api->download(a, y1, sh->rows * 4));
-        CK(api->download(b, y0, sh->rows * 4));
-        size_t outside = 0;
-        const double r = rel_l2(a, b, sh->rows, &outside);
-        /* q8_1 rounding of x alone: ~1e-2 relative on N(0,1) activations */
-        const int ok = r <= 3e-2;
+        CK(api->malloc_(&w, wb));
+        CK(api->malloc_(&xq, C / 32 * 36));
+        CK(api->synth_fill(sh->type, w, R * C / 256, 100 + s, 0.02f));
+        CK(api->synth_normal(x, C, 200 + s, 1.0f));
+        CK(api->matvec(sh->type, w, R, C, x, y0));   /* fp32 dequantize-and-FMA path */
+        CK(api->matvec_dp4a(sh->type, w, R, C, x, y1));
+        CK(api->quantize_q8_1(x, C, xq));
+        uint8_t *wh = malloc(wb), *xq_gpu = malloc(C / 32 * 36), *xq_cpu = malloc(C / 32 * 36);
+        float *xh = malloc(C * 4), *x8 = malloc(C * 4), *g0 = malloc(R * 4), *g1 = malloc(R * 4);
+        double *cf = malloc(R * 8), *cq = malloc(R * 8);
+        float *cff = malloc(R * 4), *cqf = malloc(R * 4);
+        if (!wh || !xq_gpu || !xq_cpu || !xh || !x8 || !g0 || !g1 || !cf || !cq || !cff || !cqf)
+            return die("host malloc", -5);
+        CK(api->download(wh, w, wb));
+        CK(api->download(xh, x, C * 4));
+        CK(api->download(g0, y0, R * 4));
+        CK(api->download(g1, y1, R * 4));
+        CK(api->download(xq_gpu, xq, C / 32 * 36));
+        kh_cpu_quantize_q8_1(xh, C, xq_cpu);
+        kh_cpu_dequant(9, xq_cpu, C, x8);
+        if (kh_cpu_matvec(sh->type, wh, R, C, xh, cf) || kh_cpu_matvec(sh->type, wh, R, C, x8, cq))
+            return die("cpu matvec", -1);
+        size_t outside = 0, xq_diff = 0;
+        double worst = 0.0;
+        for (uint64_t i = 0; i < R; i++) {
+            cff[i] = (float)cf[i];
+            cqf[i] = (float)cq[i];
+            const double e = fabs((double)g0[i] - cf[i]) / (1e-3 * (1.0 + fabs(cf[i])));
+            worst = e > worst ? e : worst;
+            outside += e > 1.0;
+        }
+        for (uint64_t k = 0; k < C / 32; k++) xq_diff += memcmp(xq_gpu + 36 * k, xq_cpu + 36 * k, 36) != 0;
+        const double rq = rel_l2(g1, cqf, R, NULL), rx = rel_l2(g1, cff, R, NULL);
+        const int ok = outside == 0 && rq <= 1e-5 && xq_diff == 0;
         fails += !ok;
-        printf("check %-24s %s: rel_L2(dp4a, fp32) = %.3e, %zu of %llu outside 1e-3*(1+|ref|) %s\n", sh->role,
-               tname(sh->type), r, outside, (unsigned long long)sh->rows, ok ? "PASS" : "FAIL");
-        free(a);
-        free(b);
+        printf("check %-24s %s: fp32 GEMV %zu of %llu outside 1e-3*(1+|cpu|) (worst %.3f of it); v_dot4 GEMV "
+               "rel_L2 %.2e vs cpu on the same q8_1 x (<= 1e-5); q8_1 x blocks differing %zu; [v_dot4 vs cpu "
+               "fp32 x: %.2e] %s\n",
+               sh->role, tname(sh->type), outside, (unsigned long long)R, worst, rq, xq_diff, rx, ok ? "PASS" : "FAIL");
+        void *hb[] = {wh, xq_gpu, xq_cpu, xh, x8, g0, g1, cf, cq, cff, cqf};
+        for (size_t i = 0; i < sizeof hb / sizeof hb[0]; i++) free(hb[i]);
         api->free_(w);
+        api->free_(xq);
         api->free_(x);
         api->free_(y0);
         api->free_(y1);
@@ -129,30 +163,28 @@ static int cmd_check(void) {
     return fails ? 1 : 0;
 }
 
-static float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
-
-/* The fused layer vs the same layer from separate calls: q8 GEMVs for gate,
- * up and down of each selected expert, SiLU-GLU and the rank-order weighted
- * sum on the host. */
+/* The fused MoE layer on the GPU against the CPU. PASS: rel_L2 <= 1e-5 to
+ * the CPU's q8_1 path (x quantized to q8_1; gate/up with the library's q8_1
+ * Q4_K dot and SiLU; h quantized to q8_1; down in double; the rank-order
+ * weighted sum). The CPU's fp32 path (fp32 x and h, no quantization) is
+ * printed for information: it differs by the q8_1 rounding of x and h. */
 static int cmd_check_moe(void) {
-    const uint32_t H = 2048, F = 768, E = 128, K = 8;
+    enum { H = 2048, F = 768, E = 128, K = 8 };
     const uint64_t rbg = row_bytes(Q4K, H), rbd = row_bytes(Q6K, F);
-    void *g = NULL, *u = NULL, *d = NULL, *xq = NULL, *hq = NULL;
-    CK(api->malloc_(&g, (uint64_t)E * F * rbg));
-    CK(api->malloc_(&u, (uint64_t)E * F * rbg));
-    CK(api->malloc_(&d, (uint64_t)E * H * rbd));
+    const uint64_t gb = (uint64_t)E * F * rbg, db = (uint64_t)E * H * rbd;
+    void *g = NULL, *u = NULL, *d = NULL;
+    CK(api->malloc_(&g, gb));
+    CK(api->malloc_(&u, gb));
+    CK(api->malloc_(&d, db));
     CK(api->synth_fill(Q4K, g, (uint64_t)E * F * H / 256, 11, 0.02f));
     CK(api->synth_fill(Q4K, u, (uint64_t)E * F * H / 256, 12, 0.02f));
     CK(api->synth_fill(Q6K, d, (uint64_t)E * H * F / 256, 13, 0.02f));
-    float *x = dalloc_f(H), *y = dalloc_f(H), *gv = dalloc_f(F), *uv = dalloc_f(F), *h = dalloc_f(F), *dv = dalloc_f(H);
+    float *x = dalloc_f(H), *y = dalloc_f(H), *w_d = dalloc_f(K);
     int32_t *ids_d = NULL;
-    float *w_d = dalloc_f(K);
     CK(api->malloc_((void **)&ids_d, K * 4));
-    CK(api->malloc_(&xq, H / 32 * 36));
-    CK(api->malloc_(&hq, F / 32 * 36));
     CK(api->synth_normal(x, H, 21, 1.0f));
-    const int32_t ids[8] = {5, 77, 3, 120, 64, 9, 31, 100};
-    const float w[8] = {0.25f, 0.2f, 0.15f, 0.12f, 0.1f, 0.08f, 0.06f, 0.04f};
+    const int32_t ids[K] = {5, 77, 3, 120, 64, 9, 31, 100};
+    const float w[K] = {0.25f, 0.2f, 0.15f, 0.12f, 0.1f, 0.08f, 0.06f, 0.04f};
     CK(api->upload(ids_d, ids, sizeof ids));
     CK(api->upload(w_d, w, sizeof w));
     KataliHipMoe moe = {sizeof moe, Q4K, Q4K, Q6K, H, F, E, g, u, d, NULL, NULL, NULL};
@@ -163,31 +195,56 @@ static int cmd_check_moe(void) {
     r.ids = ids_d;
     r.weights = w_d;
     CK(api->moe_layer(&moe, &r, x, NULL, y));
-    float fused[2048], ref[2048], gh[768], uh[768], hh[768], dh[2048];
+    static float fused[H], xh[H], ref_q[H], ref_f[H], hq_f[F], h_f[F];
+    static uint8_t xq[H / 32 * 36], hq[F / 32 * 36];
+    static double acc[H];
     CK(api->download(fused, y, sizeof fused));
-    memset(ref, 0, sizeof ref);
-    CK(api->quantize_q8_1(x, H, xq));
-    for (uint32_t k = 0; k < K; k++) {
-        const uint8_t *ge = (const uint8_t *)g + (uint64_t)ids[k] * F * rbg;
-        const uint8_t *ue = (const uint8_t *)u + (uint64_t)ids[k] * F * rbg;
-        const uint8_t *de = (const uint8_t *)d + (uint64_t)ids[k] * H * rbd;
-        CK(api->matvec_q8(Q4K, ge, F, H, xq, gv));
-        CK(api->matvec_q8(Q4K, ue, F, H, xq, uv));
-        CK(api->download(gh, gv, sizeof gh));
-        CK(api->download(uh, uv, sizeof uh));
-        for (uint32_t j = 0; j < F; j++) hh[j] = silu_mul(gh[j], uh[j]);
-        CK(api->upload(h, hh, sizeof hh));
-        CK(api->quantize_q8_1(h, F, hq));
-        CK(api->matvec_q8(Q6K, de, H, F, hq, dv));
-        CK(api->download(dh, dv, sizeof dh));
-        for (uint32_t i = 0; i < H; i++) ref[i] = fmaf(w[k], dh[i], ref[i]);
+    CK(api->download(xh, x, sizeof xh));
+    uint8_t *gh = malloc(gb), *uh = malloc(gb), *dh = malloc(db);
+    if (!gh || !uh || !dh) return die("host malloc", -5);
+    CK(api->download(gh, g, gb));
+    CK(api->download(uh, u, gb));
+    CK(api->download(dh, d, db));
+    kh_cpu_quantize_q8_1(xh, H, xq);
+    memset(ref_q, 0, sizeof ref_q);
+    memset(ref_f, 0, sizeof ref_f);
+    for (int k = 0; k < K; k++) {
+        const uint8_t *ge = gh + (uint64_t)ids[k] * F * rbg, *ue = uh + (uint64_t)ids[k] * F * rbg;
+        const uint8_t *de = dh + (uint64_t)ids[k] * H * rbd;
+        for (int j = 0; j < F; j++) {
+            /* q8_1 path as the library defines it */
+            hq_f[j] = kh_cpu_silu_mul(kh_cpu_dot_q4k_q8(ge + j * rbg, xq, H / 256),
+                                      kh_cpu_dot_q4k_q8(ue + j * rbg, xq, H / 256));
+            /* fp32 path: dequantized rows against fp32 x, exact exp */
+            double gd = 0, ud = 0;
+            float grow[H], urow[H];
+            kh_cpu_dequant(Q4K, ge + j * rbg, H, grow);
+            kh_cpu_dequant(Q4K, ue + j * rbg, H, urow);
+            for (int c = 0; c < H; c++) {
+                gd += (double)grow[c] * xh[c];
+                ud += (double)urow[c] * xh[c];
+            }
+            h_f[j] = (float)(gd / (1.0 + exp(-gd)) * ud);
+        }
+        kh_cpu_quantize_q8_1(hq_f, F, hq);
+        float h8[F];
+        kh_cpu_dequant(9, hq, F, h8);
+        kh_cpu_matvec(Q6K, de, H, F, h8, acc);
+        for (int i = 0; i < H; i++) ref_q[i] = fmaf(w[k], (float)acc[i], ref_q[i]);
+        kh_cpu_matvec(Q6K, de, H, F, h_f, acc);
+        for (int i = 0; i < H; i++) ref_f[i] = fmaf(w[k], (float)acc[i], ref_f[i]);
     }
+    const double rel_q = rel_l2(fused, ref_q, H, NULL);
     size_t outside = 0;
-    const double rel = rel_l2(fused, ref, H, &outside);
-    const int ok = rel <= 1e-4;
-    printf("check-moe hidden %u ffn %u top-%u: rel_L2(fused layer, composed GEMVs) = %.3e, %zu of %u outside "
-           "1e-3*(1+|ref|) %s\n", H, F, K, rel, outside, H, ok ? "PASS" : "FAIL");
-    void *bufs[] = {g, u, d, xq, hq, x, y, gv, uv, h, dv, ids_d, w_d};
+    const double rel_f = rel_l2(fused, ref_f, H, &outside);
+    const int ok = rel_q <= 1e-5;
+    printf("check-moe hidden %u ffn %u top-%u: rel_L2 %.2e vs the cpu q8_1 path (<= 1e-5); [cpu fp32 path: "
+           "rel_L2 %.2e, %zu of %u outside 1e-3*(1+|ref|)] %s\n",
+           H, F, K, rel_q, rel_f, outside, H, ok ? "PASS" : "FAIL");
+    free(gh);
+    free(uh);
+    free(dh);
+    void *bufs[] = {g, u, d, x, y, ids_d, w_d};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) api->free_(bufs[i]);
     return ok ? 0 : 1;
 }
@@ -402,7 +459,7 @@ static int gguf_check_layer(KataliHipWeights *w, uint32_t l, int n_sel) {
         CK(api->matvec_q8(m.up_type, ue, F, H, xq, uv));
         CK(api->download(gh, gv, F * 4));
         CK(api->download(uh, uv, F * 4));
-        for (uint32_t j = 0; j < F; j++) hh[j] = silu_mul(gh[j], uh[j]);
+        for (uint32_t j = 0; j < F; j++) hh[j] = kh_cpu_silu_mul(gh[j], uh[j]);
         CK(api->upload(h, hh, F * 4));
         CK(api->quantize_q8_1(h, F, hq));
         CK(api->matvec_q8(m.down_type, de, H, F, hq, dv));

@@ -1,10 +1,12 @@
 /* katali_hip_gguf.c — GGUF reader, device weight cache, MoE layer assembly
  * and expert VRAM tier (declarations and contracts in katali_hip_gguf.h).
  *
- * The reader maps the file read-only and walks it with a bounds-checked
- * cursor; every length and offset from the file is checked against the bytes
- * left before it is used. Its acceptance rules are the engine reader's
- * (V/src/gguf_reader.c:351-543) so that both open and refuse the same files.
+ * The reader maps the file read-only and parses it from the public GGUF
+ * layout in four passes (header, metadata, tensor directory, data layout);
+ * every count, length and offset read from the file is checked against the
+ * bytes left before it is used, and the first refusal is reported with its
+ * byte position. It accepts and refuses the same files as the engine's reader
+ * (V/src/gguf_reader.c:351-543), so a file the engine opens opens here too.
  * Little-endian host (x86-64, as the engine).
  */
 #ifndef _POSIX_C_SOURCE
@@ -56,197 +58,252 @@ uint64_t katali_hip_ggml_row_bytes(uint32_t type, uint64_t n) {
 }
 
 /* ---- the file ------------------------------------------------------------ */
-enum { GV_U8, GV_I8, GV_U16, GV_I16, GV_U32, GV_I32, GV_F32, GV_BOOL, GV_STR, GV_ARR, GV_U64, GV_I64, GV_F64 };
+/* GGUF metadata value types (the public GGUF format) */
+enum {
+    VT_U8 = 0, VT_I8, VT_U16, VT_I16, VT_U32, VT_I32, VT_F32, VT_BOOL, VT_STRING, VT_ARRAY, VT_U64, VT_I64, VT_F64,
+    VT_COUNT
+};
 
-typedef struct Kv {
+/* bytes of one fixed-size value, 0 for strings, arrays and unknown types */
+static unsigned value_width(uint32_t vt) {
+    static const uint8_t w[VT_COUNT] = {1, 1, 2, 2, 4, 4, 4, 1, 0, 0, 8, 8, 8};
+    return vt < VT_COUNT ? w[vt] : 0;
+}
+static int value_signed(uint32_t vt) { return vt == VT_I8 || vt == VT_I16 || vt == VT_I32 || vt == VT_I64; }
+static int value_float(uint32_t vt) { return vt == VT_F32 || vt == VT_F64; }
+
+/* A metadata entry as kept: a number as int64 and double, a string as bytes
+ * in the map; arrays are validated and skipped (nothing here reads them). */
+typedef struct Meta {
     char *key;
-    uint32_t type;
-    uint64_t u;          /* unsigned view (0 for floats and strings) */
-    int64_t i;           /* signed view */
-    double f;            /* float view */
-    const uint8_t *s;    /* string bytes in the map */
-    uint64_t s_len;
-} Kv;
+    uint32_t vt;
+    int64_t num;       /* integers and bools (unsigned 64-bit kept as its bits) */
+    double real;       /* F32 / F64 */
+    const uint8_t *str;
+    uint64_t str_len;
+} Meta;
 
 struct KataliHipGguf {
     const uint8_t *map;
     uint64_t size;
     uint32_t version;
-    uint64_t n_kv, n_tensors, alignment, data_offset;
-    Kv *kv;
+    uint64_t n_meta, n_tensors, alignment, data_offset;
+    Meta *meta;
     KataliHipGgufTensor *t;
 };
 
-typedef struct Cur {
-    const uint8_t *m;
-    uint64_t size, pos;
-    const char *bad;     /* first failure, NULL while fine */
-} Cur;
+/* The parser: a read position over the mapped file and the first refusal. */
+typedef struct Reader {
+    const uint8_t *base;
+    uint64_t size, at;
+    char *why;
+    size_t why_cap;
+    int refused;
+} Reader;
 
-static const uint8_t *take(Cur *c, uint64_t n) {
-    if (c->bad) return NULL;
-    if (n > c->size - c->pos) { c->bad = "truncated file"; return NULL; }
-    const uint8_t *p = c->m + c->pos;
-    c->pos += n;
-    return p;
-}
-static uint64_t rd(Cur *c, unsigned n) {   /* little-endian n-byte unsigned */
-    const uint8_t *p = take(c, n);
-    uint64_t v = 0;
-    if (p) memcpy(&v, p, n);
-    return v;
-}
-static const uint8_t *rd_str(Cur *c, uint64_t *len) {
-    const uint64_t n = rd(c, 8);
-    const uint8_t *p = take(c, n);
-    *len = p ? n : 0;
-    return p;
-}
-static unsigned scalar_bytes(uint32_t t) {
-    switch (t) {
-        case GV_U8: case GV_I8: case GV_BOOL: return 1;
-        case GV_U16: case GV_I16: return 2;
-        case GV_U32: case GV_I32: case GV_F32: return 4;
-        case GV_U64: case GV_I64: case GV_F64: return 8;
-        default: return 0;
+static int refuse(Reader *r, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+static int refuse(Reader *r, const char *fmt, ...) {
+    if (!r->refused && r->why && r->why_cap) {
+        va_list ap;
+        va_start(ap, fmt);
+        const int n = vsnprintf(r->why, r->why_cap, fmt, ap);
+        va_end(ap);
+        if (n >= 0 && (size_t)n < r->why_cap)
+            snprintf(r->why + n, r->why_cap - (size_t)n, " [byte %llu of %llu]", (unsigned long long)r->at,
+                     (unsigned long long)r->size);
     }
+    r->refused = 1;
+    return -1;
 }
 
-/* One scalar of type t: numbers into u/i/f as the engine's reader keeps
- * them (gguf_reader.c:246-274), strings as a pointer into the map. */
-static void scalar(Cur *c, uint32_t t, Kv *kv) {
-    uint64_t v;
-    float f32;
-    double f64;
-    switch (t) {
-        case GV_U8: case GV_U16: case GV_U32: case GV_U64:
-            kv->u = rd(c, scalar_bytes(t)); kv->i = (int64_t)kv->u; break;
-        case GV_I8: kv->i = (int8_t)rd(c, 1); kv->u = (uint64_t)kv->i; break;
-        case GV_I16: kv->i = (int16_t)rd(c, 2); kv->u = (uint64_t)kv->i; break;
-        case GV_I32: kv->i = (int32_t)rd(c, 4); kv->u = (uint64_t)kv->i; break;
-        case GV_I64: kv->i = (int64_t)rd(c, 8); kv->u = (uint64_t)kv->i; break;
-        case GV_BOOL: kv->u = rd(c, 1) ? 1u : 0u; kv->i = (int64_t)kv->u; break;
-        case GV_F32: v = rd(c, 4); memcpy(&f32, &v, 4); kv->f = f32; break;
-        case GV_F64: v = rd(c, 8); memcpy(&f64, &v, 8); kv->f = f64; break;
-        case GV_STR: kv->s = rd_str(c, &kv->s_len); break;
-        default: if (!c->bad) c->bad = "unsupported metadata value type"; break;
-    }
+static uint64_t left(const Reader *r) { return r->size - r->at; }
+
+/* n little-endian bytes (n <= 8) as an unsigned number */
+static int fixed(Reader *r, unsigned n, uint64_t *v, const char *what) {
+    *v = 0;
+    if (left(r) < n) return refuse(r, "file ends inside %s", what);
+    uint64_t x = 0;
+    for (unsigned k = 0; k < n; k++) x |= (uint64_t)r->base[r->at + k] << (8 * k);
+    r->at += n;
+    *v = x;
+    return 0;
+}
+static int u32_at(Reader *r, uint32_t *v, const char *what) {
+    uint64_t x;
+    if (fixed(r, 4, &x, what)) return -1;
+    *v = (uint32_t)x;
+    return 0;
 }
 
-/* An array is checked, not kept (the fused path reads no array metadata):
- * nested arrays refused, the count and a fixed-size payload bounded by the
- * bytes left, strings walked one by one (gguf_reader.c:277-330). */
-static void array(Cur *c) {
-    const uint32_t et = (uint32_t)rd(c, 4);
-    const uint64_t n = rd(c, 8);
-    if (c->bad) return;
-    if (et == GV_ARR) { c->bad = "nested metadata arrays are unsupported"; return; }
-    if (n > c->size - c->pos) { c->bad = "array count exceeds file size"; return; }
-    const unsigned es = scalar_bytes(et);
-    if (es) {
-        if (n > (c->size - c->pos) / es) { c->bad = "array payload exceeds file size"; return; }
-        take(c, n * es);
-        return;
-    }
-    if (et != GV_STR) { c->bad = "unsupported metadata array element type"; return; }
-    for (uint64_t k = 0; k < n && !c->bad; k++) {
-        uint64_t len;
-        rd_str(c, &len);
-    }
+/* a GGUF string: u64 length, then that many bytes, all inside the file */
+static int string_at(Reader *r, const uint8_t **p, uint64_t *len, const char *what) {
+    uint64_t n;
+    if (fixed(r, 8, &n, what)) return -1;
+    if (n > left(r)) return refuse(r, "%s claims %llu bytes, %llu remain", what, (unsigned long long)n,
+                                   (unsigned long long)left(r));
+    *p = r->base + r->at;
+    *len = n;
+    r->at += n;
+    return 0;
 }
 
-static const Kv *kv_find(const KataliHipGguf *g, const char *key) {
-    for (uint64_t k = 0; k < g->n_kv; k++)
-        if (g->kv[k].key && strcmp(g->kv[k].key, key) == 0) return &g->kv[k];
-    return NULL;
-}
-
-void katali_hip_gguf_close(KataliHipGguf *g) {
-    if (!g) return;
-    for (uint64_t k = 0; g->kv && k < g->n_kv; k++) free(g->kv[k].key);
-    for (uint64_t k = 0; g->t && k < g->n_tensors; k++) free((char *)g->t[k].name);
-    free(g->kv);
-    free(g->t);
-    if (g->map) munmap((void *)g->map, g->size);
-    free(g);
-}
-
-static char *dup_bytes(const uint8_t *p, uint64_t n) {
+static char *c_string(const uint8_t *p, uint64_t n) {
     char *s = (char *)malloc(n + 1);
     if (s) {
-        if (n) memcpy(s, p, n);
+        memcpy(s, p, n);
         s[n] = 0;
     }
     return s;
 }
 
-static int parse(KataliHipGguf *g, char *err, size_t cap) {
-    Cur c = {g->map, g->size, 0, NULL};
-#define BAD(...) do { if (err && cap) snprintf(err, cap, __VA_ARGS__); return -1; } while (0)
-    if (rd(&c, 4) != 0x46554747u || c.bad) BAD("not a GGUF file (bad magic)");
-    g->version = (uint32_t)rd(&c, 4);
-    if (c.bad || g->version < 1 || g->version > 3) BAD("unsupported GGUF version %u", g->version);
-    g->n_tensors = rd(&c, 8);
-    g->n_kv = rd(&c, 8);
-    if (c.bad) BAD("truncated GGUF header");
-    if (g->n_tensors > g->size || g->n_kv > g->size) BAD("implausible header counts");
-    g->kv = (Kv *)calloc(g->n_kv ? g->n_kv : 1, sizeof(Kv));
+/* An array value: element type, count, then the elements. Arrays of arrays
+ * are refused; the count may not exceed the bytes left (a cheap bound before
+ * any element is read), fixed-size payloads must fit, and strings are walked
+ * one by one. */
+static int skip_array(Reader *r, const char *key) {
+    uint32_t et;
+    uint64_t count;
+    if (u32_at(r, &et, "an array's element type") || fixed(r, 8, &count, "an array's length")) return -1;
+    if (et == VT_ARRAY) return refuse(r, "metadata '%s': arrays of arrays are not read", key);
+    if (count > left(r)) return refuse(r, "metadata '%s': array of %llu elements in %llu bytes", key,
+                                       (unsigned long long)count, (unsigned long long)left(r));
+    const unsigned w = value_width(et);
+    if (w) {
+        if (count > left(r) / w)
+            return refuse(r, "metadata '%s': %llu elements of %u bytes overrun the file", key,
+                          (unsigned long long)count, w);
+        r->at += count * w;
+        return 0;
+    }
+    if (et != VT_STRING) return refuse(r, "metadata '%s': array element type %u is not a GGUF type", key, et);
+    for (uint64_t k = 0; k < count; k++) {
+        const uint8_t *p;
+        uint64_t n;
+        if (string_at(r, &p, &n, "a string element")) return -1;
+    }
+    return 0;
+}
+
+static int read_meta(Reader *r, Meta *m) {
+    const uint8_t *kp;
+    uint64_t kn;
+    if (string_at(r, &kp, &kn, "a metadata key")) return -1;
+    if (!(m->key = c_string(kp, kn))) return refuse(r, "out of memory");
+    if (u32_at(r, &m->vt, "a metadata value type")) return -1;
+    if (m->vt == VT_ARRAY) return skip_array(r, m->key);
+    if (m->vt == VT_STRING) return string_at(r, &m->str, &m->str_len, "a metadata string");
+    const unsigned w = value_width(m->vt);
+    if (!w) return refuse(r, "metadata '%s': value type %u is not a GGUF type", m->key, m->vt);
+    uint64_t bits;
+    if (fixed(r, w, &bits, "a metadata value")) return -1;
+    if (m->vt == VT_F32) {
+        float f;
+        const uint32_t b32 = (uint32_t)bits;
+        memcpy(&f, &b32, 4);
+        m->real = f;
+    } else if (m->vt == VT_F64) {
+        memcpy(&m->real, &bits, 8);
+    } else if (m->vt == VT_BOOL) {
+        m->num = bits != 0;
+    } else if (value_signed(m->vt)) {
+        const unsigned sh = 64 - 8 * w;   /* sign-extend from w bytes */
+        m->num = (int64_t)(bits << sh) >> sh;
+    } else {
+        m->num = (int64_t)bits;
+    }
+    return 0;
+}
+
+/* One tensor directory record: name, rank 1..4, dims (none zero, product
+ * in 64 bits), ggml type, offset into the data section. */
+static int read_tensor(Reader *r, KataliHipGgufTensor *t) {
+    const uint8_t *np;
+    uint64_t nn;
+    if (string_at(r, &np, &nn, "a tensor name")) return -1;
+    if (!(t->name = c_string(np, nn))) return refuse(r, "out of memory");
+    if (u32_at(r, &t->n_dims, "a tensor rank")) return -1;
+    if (t->n_dims == 0 || t->n_dims > 4) return refuse(r, "tensor '%s': rank %u (1 to 4)", t->name, t->n_dims);
+    for (uint32_t d = 0; d < t->n_dims; d++)
+        if (fixed(r, 8, &t->dims[d], "a tensor dimension")) return -1;
+    uint64_t elems = 1;
+    for (uint32_t d = 0; d < t->n_dims; d++) {
+        if (t->dims[d] == 0) return refuse(r, "tensor '%s': dimension %u is 0", t->name, d);
+        if (elems > UINT64_MAX / t->dims[d]) return refuse(r, "tensor '%s': more than 2^64 elements", t->name);
+        elems *= t->dims[d];
+    }
+    if (u32_at(r, &t->type, "a tensor type") || fixed(r, 8, &t->offset, "a tensor offset")) return -1;
+    t->nbytes = elems;   /* elements until the layout is resolved */
+    return 0;
+}
+
+static const Meta *meta_find(const KataliHipGguf *g, const char *key) {
+    for (uint64_t k = 0; k < g->n_meta; k++)
+        if (g->meta[k].key && strcmp(g->meta[k].key, key) == 0) return &g->meta[k];
+    return NULL;
+}
+
+void katali_hip_gguf_close(KataliHipGguf *g) {
+    if (!g) return;
+    for (uint64_t k = 0; g->meta && k < g->n_meta; k++) free(g->meta[k].key);
+    for (uint64_t k = 0; g->t && k < g->n_tensors; k++) free((char *)g->t[k].name);
+    free(g->meta);
+    free(g->t);
+    if (g->map) munmap((void *)g->map, g->size);
+    free(g);
+}
+
+/* The file in four passes: header, metadata, tensor directory, layout. */
+static int parse(KataliHipGguf *g, char *why, size_t why_cap) {
+    Reader r = {g->map, g->size, 0, why, why_cap, 0};
+    uint32_t magic = 0;
+    if (left(&r) < 4) return refuse(&r, "too short for a GGUF header");
+    u32_at(&r, &magic, "the magic");
+    if (magic != 0x46554747u) return refuse(&r, "no GGUF magic at the start of the file");
+    if (u32_at(&r, &g->version, "the version")) return -1;
+    if (g->version < 1 || g->version > 3) return refuse(&r, "GGUF version %u (versions 1 to 3 are read)", g->version);
+    if (fixed(&r, 8, &g->n_tensors, "the tensor count") || fixed(&r, 8, &g->n_meta, "the metadata count"))
+        return -1;
+    /* every entry takes at least one byte: larger counts cannot be real */
+    if (g->n_tensors > g->size || g->n_meta > g->size)
+        return refuse(&r, "%llu tensors / %llu metadata entries in a %llu-byte file",
+                      (unsigned long long)g->n_tensors, (unsigned long long)g->n_meta, (unsigned long long)g->size);
+    g->meta = (Meta *)calloc(g->n_meta ? g->n_meta : 1, sizeof(Meta));
     g->t = (KataliHipGgufTensor *)calloc(g->n_tensors ? g->n_tensors : 1, sizeof(KataliHipGgufTensor));
-    if (!g->kv || !g->t) BAD("out of memory");
-    for (uint64_t k = 0; k < g->n_kv && !c.bad; k++) {
-        Kv *kv = &g->kv[k];
-        uint64_t klen;
-        const uint8_t *kp = rd_str(&c, &klen);
-        if (c.bad) break;
-        if (!(kv->key = dup_bytes(kp, klen))) BAD("out of memory");
-        kv->type = (uint32_t)rd(&c, 4);
-        if (c.bad) break;
-        if (kv->type == GV_ARR) array(&c);
-        else scalar(&c, kv->type, kv);
-    }
-    if (c.bad) BAD("%s (at offset %llu)", c.bad, (unsigned long long)c.pos);
+    if (!g->meta || !g->t) return refuse(&r, "out of memory");
+
+    for (uint64_t k = 0; k < g->n_meta; k++)
+        if (read_meta(&r, &g->meta[k])) return -1;
+    /* general.alignment, when an integer in [8, 2^20]; 32 otherwise */
     g->alignment = 32;
-    const Kv *a = kv_find(g, "general.alignment");
-    if (a && a->type != GV_ARR && a->u >= 8 && a->u <= (1u << 20)) g->alignment = a->u;
+    const Meta *al = meta_find(g, "general.alignment");
+    if (al && !value_float(al->vt) && value_width(al->vt) && (uint64_t)al->num >= 8 &&
+        (uint64_t)al->num <= (1u << 20))
+        g->alignment = (uint64_t)al->num;
 
-    for (uint64_t k = 0; k < g->n_tensors && !c.bad; k++) {
-        KataliHipGgufTensor *t = &g->t[k];
-        uint64_t nlen;
-        const uint8_t *np = rd_str(&c, &nlen);
-        if (c.bad) break;
-        if (!(t->name = dup_bytes(np, nlen))) BAD("out of memory");
-        t->n_dims = (uint32_t)rd(&c, 4);
-        if (c.bad) break;
-        if (t->n_dims < 1 || t->n_dims > 4) { c.bad = "tensor rank out of range"; break; }
-        int over = 0;
-        for (uint32_t d = 0; d < t->n_dims; d++) t->dims[d] = rd(&c, 8);
-        if (c.bad) break;
-        uint64_t n = 1;
-        for (uint32_t d = 0; d < t->n_dims; d++) {
-            if (!t->dims[d] || n > UINT64_MAX / t->dims[d]) over = 1;
-            else n *= t->dims[d];
-        }
-        if (over) { c.bad = "tensor element count overflows"; break; }
-        t->type = (uint32_t)rd(&c, 4);
-        t->offset = rd(&c, 8);
-        t->nbytes = n;   /* element count until resolved below */
-    }
-    if (c.bad) BAD("%s (at offset %llu)", c.bad, (unsigned long long)c.pos);
+    for (uint64_t k = 0; k < g->n_tensors; k++)
+        if (read_tensor(&r, &g->t[k])) return -1;
 
-    const uint64_t rem = c.pos % g->alignment;
-    g->data_offset = rem ? c.pos + (g->alignment - rem) : c.pos;
-    if (g->data_offset > g->size) BAD("tensor data offset past end of file");
+    /* data section: the directory's end rounded up to the alignment */
+    g->data_offset = (r.at + g->alignment - 1) / g->alignment * g->alignment;
+    if (g->data_offset > g->size) return refuse(&r, "the data section would start past the end of the file");
     const uint64_t data = g->size - g->data_offset;
     for (uint64_t k = 0; k < g->n_tensors; k++) {
         KataliHipGgufTensor *t = &g->t[k];
-        const uint64_t nb = katali_hip_ggml_row_bytes(t->type, t->nbytes);
-        if (t->offset > data) BAD("tensor '%s' offset past end of file", t->name);
-        if (!nb) { t->nbytes = 0; t->data = NULL; continue; }
-        if (nb > data - t->offset) BAD("tensor '%s' (%llu bytes) is truncated", t->name, (unsigned long long)nb);
-        t->nbytes = nb;
+        if (t->offset > data)
+            return refuse(&r, "tensor '%s' starts %llu bytes into a %llu-byte data section", t->name,
+                          (unsigned long long)t->offset, (unsigned long long)data);
+        const uint64_t bytes = katali_hip_ggml_row_bytes(t->type, t->nbytes);
+        if (bytes == 0) {          /* a type this library has no block size for: listed, no data */
+            t->nbytes = 0;
+            t->data = NULL;
+            continue;
+        }
+        if (bytes > data - t->offset)
+            return refuse(&r, "tensor '%s' needs %llu bytes, %llu remain after its offset", t->name,
+                          (unsigned long long)bytes, (unsigned long long)(data - t->offset));
+        t->nbytes = bytes;
         t->data = g->map + g->data_offset + t->offset;
     }
-#undef BAD
     return 0;
 }
 
@@ -255,15 +312,16 @@ int katali_hip_gguf_open(const char *path, KataliHipGguf **out, char *err, size_
     *out = NULL;
     const int fd = open(path, O_RDONLY);
     struct stat st;
-    if (fd < 0 || fstat(fd, &st) != 0 || st.st_size <= 0) {
+    const char *why = fd < 0 ? "open failed" : fstat(fd, &st) != 0 ? "stat failed" : st.st_size <= 0 ? "empty file" : NULL;
+    if (why) {
         if (fd >= 0) close(fd);
-        if (err && cap) snprintf(err, cap, "cannot open file: %s", path);
+        if (err && cap) snprintf(err, cap, "%s: %s", path, why);
         return -1;
     }
     void *m = mmap(NULL, (size_t)st.st_size, PROT_READ, MAP_PRIVATE, fd, 0);
     close(fd);
     if (m == MAP_FAILED) {
-        if (err && cap) snprintf(err, cap, "cannot map file: %s", path);
+        if (err && cap) snprintf(err, cap, "%s: mmap failed", path);
         return -1;
     }
     KataliHipGguf *g = (KataliHipGguf *)calloc(1, sizeof *g);
@@ -307,24 +365,22 @@ int katali_hip_gguf_find(const KataliHipGguf *g, const char *name, KataliHipGguf
 }
 
 int64_t katali_hip_gguf_get_int(const KataliHipGguf *g, const char *key, int64_t def) {
-    const Kv *kv = g ? kv_find(g, key) : NULL;
-    if (!kv || kv->type == GV_ARR || kv->type == GV_STR) return def;
-    if (kv->type == GV_F32 || kv->type == GV_F64) return (int64_t)kv->f;
-    return kv->i;
+    const Meta *m = g ? meta_find(g, key) : NULL;
+    if (!m || m->vt == VT_ARRAY || m->vt == VT_STRING) return def;
+    return value_float(m->vt) ? (int64_t)m->real : m->num;
 }
 
 double katali_hip_gguf_get_float(const KataliHipGguf *g, const char *key, double def) {
-    const Kv *kv = g ? kv_find(g, key) : NULL;
-    if (!kv || kv->type == GV_ARR || kv->type == GV_STR) return def;
-    if (kv->type == GV_F32 || kv->type == GV_F64) return kv->f;
-    return (double)kv->i;
+    const Meta *m = g ? meta_find(g, key) : NULL;
+    if (!m || m->vt == VT_ARRAY || m->vt == VT_STRING) return def;
+    return value_float(m->vt) ? m->real : (double)m->num;
 }
 
 const char *katali_hip_gguf_get_str(const KataliHipGguf *g, const char *key, size_t *len_out) {
-    const Kv *kv = g ? kv_find(g, key) : NULL;
-    if (!kv || kv->type != GV_STR) return NULL;
-    if (len_out) *len_out = (size_t)kv->s_len;
-    return (const char *)kv->s;
+    const Meta *m = g ? meta_find(g, key) : NULL;
+    if (!m || m->vt != VT_STRING) return NULL;
+    if (len_out) *len_out = (size_t)m->str_len;
+    return (const char *)m->str;
 }
 
 /* ---- device weight cache --------------------------------------------------- */
