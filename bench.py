@@ -23,6 +23,12 @@ replay, and consecutive steps replay consecutive positions.
             (q stands in for the attention output, which is not a GEMV),
             FFN(o) through the MoE kernels with the shared expert only; every
             layer reads its own N(0,1) x; a step is one token (one replay).
+  moe48duty the moe48 layers submitted one by one with a host busy interval
+            (0, 20, 200, 1000 us) before each, as an engine running attention
+            on the CPU between GPU layers: GPU time per layer at each duty
+            cycle (event-timed, synchronous submission) against back to back,
+            and tok/s of synchronous vs asynchronous submission; the JSON
+            value is the layer's GB/s at 200 us per layer.
   moebatch  the config-1 MoE layer over ragged token batches (1..64 tokens,
             per-token experts from a Zipf(1.1) popularity), swept over
             n_sel in {1, 2, 4, 8}; experts that gather >= 16 tokens run as an
@@ -90,10 +96,16 @@ def moe_bytes_per_layer(hidden, ffn, n_sel, shared):
     return slots * per_expert + hidden // 32 * 36 + hidden * 4, slots * per_expert
 
 
-def bench_moe(hip, name, steps, warmup, ring=64, vocab=0):
-    """One hipGraph per ring position, replayed per token. vocab == 0: the
-    MoE layers only (router logits from a ring). vocab > 0: the whole token
-    chain (TOKEN_WORKLOADS), routing from the device router's logits."""
+class View:  # a device pointer inside a larger buffer
+    def __init__(self, ptr):
+        self.ptr = ptr
+
+
+def moe_setup(hip, name, ring=64):
+    """A MoE workload's device state: per layer distinct random expert stacks
+    (and shared expert), one x and one y slot per layer, and a ring of router
+    logits (position t, layer l at (t * L + l) * n_expert) with a route per
+    (position, layer) reading its logits from a fixed address."""
     L, hidden, ffn, n_expert, n_sel, shared = MOE_WORKLOADS[name]
     rb_g, rb_d = row_bytes(Q4_K, hidden), row_bytes(Q6_K, ffn)
     layers = []
@@ -132,12 +144,26 @@ def bench_moe(hip, name, steps, warmup, ring=64, vocab=0):
             rt.append(r)
         routes.append(rt)
 
-    class View:  # a device pointer inside a larger buffer
-        def __init__(self, ptr):
-            self.ptr = ptr
-
     xs = [View(x.ptr + li * hidden * 4) for li in range(L)]
     ys = [View(y.ptr + li * hidden * 4) for li in range(L)]
+    return layers, descs, routes, (x, y, logits), xs, ys, seed
+
+
+def moe_free(layers, bufs):
+    for g, u, d, sh in layers:
+        for b in (g, u, d) + tuple(sh or ()):
+            b.free()
+    for b in bufs:
+        b.free()
+
+
+def bench_moe(hip, name, steps, warmup, ring=64, vocab=0, normed=False):
+    """One hipGraph per ring position, replayed per token. vocab == 0: the
+    MoE layers only (router logits from a ring). vocab > 0: the whole token
+    chain (TOKEN_WORKLOADS), routing from the device router's logits."""
+    L, hidden, ffn, n_expert, n_sel, shared = MOE_WORKLOADS[name]
+    rb_g, rb_d = row_bytes(Q4_K, hidden), row_bytes(Q6_K, ffn)
+    layers, descs, routes, bufs, xs, ys, seed = moe_setup(hip, name, ring)
 
     def token(t):
         for li in range(L):
@@ -164,19 +190,23 @@ def bench_moe(hip, name, steps, warmup, ring=64, vocab=0):
         croutes = [hip.moe_route(n_sel, logits=cls[li]) for li in range(L)]
 
         def token(t):  # noqa: F811
-            # residual step + norm + router logits in one launch per layer; the
-            # residual stream alternates between two buffers after the input
+            # per layer the residual step, the norm, the router logits and the
+            # MoE layer: three launches (katali_hip_rmsnorm_matvec_f32, then
+            # the layer), or two with normed (katali_hip_moe_layer_normed);
+            # the residual stream alternates between two buffers
             cur = View(x0.ptr + t * hidden * 4)
             for li in range(L):
-                if li == 0:
-                    hip.rmsnorm_matvec_f32(cur, None, 1.0, None, nws[0], hidden, 1e-6, xs[0], routers[0],
-                                           n_expert, cls[0])
+                delta = ys[li - 1] if li else None
+                nxt = xpp[li % 2] if li else None
+                if normed:
+                    hip.moe_layer_normed(descs[li], n_sel, cur, nws[li], routers[li], ys[li], delta=delta,
+                                         scale=1.0, x_out=nxt)
                 else:
-                    nxt = xpp[li % 2]
-                    hip.rmsnorm_matvec_f32(cur, ys[li - 1], 1.0, nxt, nws[li], hidden, 1e-6, xs[li], routers[li],
+                    hip.rmsnorm_matvec_f32(cur, delta, 1.0, nxt, nws[li], hidden, 1e-6, xs[li], routers[li],
                                            n_expert, cls[li])
+                    hip.moe_layer(descs[li], croutes[li], ys[li], x=xs[li])
+                if li:
                     cur = nxt
-                hip.moe_layer(descs[li], croutes[li], ys[li], x=xs[li])
             hip.add_rmsnorm(cur, ys[L - 1], 1.0, nws[L], hidden, 1e-6, xn_out)
             hip.matvec_dp4a(Q6_K, head, vocab, hidden, xn_out, head_logits)
             hip.argmax(head_logits, vocab, tok)
@@ -243,12 +273,90 @@ def bench_moe(hip, name, steps, warmup, ring=64, vocab=0):
         "layer_bytes": layer_bytes,
         "pool_gb": L * (n_expert * (2 * ffn * rb_g + hidden * rb_d)) / 1e9,
     }
-    for bufs in layers:
-        for b in bufs[:3]:
-            b.free()
-        if bufs[3]:
-            for b in bufs[3]:
-                b.free()
+    moe_free(layers, bufs)
+    return res, (L, hidden, ffn, n_expert, n_sel, shared)
+
+
+# ---------------------------------------------------------------------------
+# Duty cycle: host work between MoE layer submissions
+# ---------------------------------------------------------------------------
+DUTY_INTERVALS_US = (0, 20, 200, 1000)   # host time per layer (200: the engine's ~6 % GPU duty cycle)
+
+
+def spin_us(us):
+    """Busy the calling host thread for `us` microseconds (it stands in for
+    the engine's CPU attention of one layer)."""
+    if us <= 0:
+        return
+    end = time.perf_counter() + us * 1e-6
+    while time.perf_counter() < end:
+        pass
+
+
+def bench_duty(hip, name, steps, warmup, intervals=DUTY_INTERVALS_US):
+    """The moe48 layers submitted one by one (no graph) with a host busy
+    interval before each layer, as an engine that runs attention on the CPU
+    between GPU MoE layers does. Per interval:
+      sync:  interval, submit the layer, wait for it (the synchronous engine);
+             HIP events around each layer give its GPU time at this duty cycle;
+      async: interval, submit, no wait; one wait per token (the host work of
+             the next layer overlaps the GPU's layer).
+    Reported per interval: GPU us per layer (event-timed, sync mode), tok/s of
+    both modes and the GPU duty cycle of the sync mode. Interval 0 is the
+    back-to-back case."""
+    L, hidden, ffn, n_expert, n_sel, shared = MOE_WORKLOADS[name]
+    layers, descs, routes, bufs, xs, ys, _ = moe_setup(hip, name)
+    ring = len(routes)
+    ev = [hip.event() for _ in range(2 * L)]
+    points = []
+    tok = 0
+    for us in intervals:
+        for mode in ("sync", "async"):
+            per, walls = [], []
+            for i in range(warmup + steps):
+                t = routes[tok % ring]
+                tok += 1
+                t0 = time.perf_counter()
+                for li in range(L):
+                    spin_us(us)
+                    if mode == "sync":
+                        hip.record(ev[2 * li])
+                    hip.moe_layer(descs[li], t[li], ys[li], x=xs[li])
+                    if mode == "sync":
+                        hip.record(ev[2 * li + 1])
+                        hip.sync()
+                hip.sync()
+                if i >= warmup:
+                    walls.append(time.perf_counter() - t0)
+                    if mode == "sync":
+                        per += [hip.elapsed_ms(ev[2 * li], ev[2 * li + 1]) for li in range(L)]
+            wall = float(np.mean(walls))
+            pt = {"host_us_per_layer": us, "mode": mode, "tok_s": round(1.0 / wall, 2),
+                  "ms_per_token": round(wall * 1e3, 4)}
+            if mode == "sync":
+                pt["gpu_us_per_layer"] = round(float(np.mean(per)) * 1e3, 3)
+                pt["gpu_us_per_layer_median"] = round(float(np.median(per)) * 1e3, 3)
+                pt["duty_cycle"] = round(float(np.sum(per)) / 1e3 / steps / wall, 4)
+            points.append(pt)
+            print(f"[bench] duty {us:5d} us/layer {mode:5s}: {pt['tok_s']:8.2f} tok/s"
+                  + (f", GPU {pt['gpu_us_per_layer']:.2f} us/layer, duty {pt['duty_cycle']:.3f}" if mode == "sync" else ""),
+                  file=sys.stderr, flush=True)
+    for e in ev:
+        hip.event_destroy(e)
+    moe_free(layers, bufs)
+    layer_bytes, _ = moe_bytes_per_layer(hidden, ffn, n_sel, shared)
+    base = next(p for p in points if p["mode"] == "sync" and p["host_us_per_layer"] == 0)
+    head = next(p for p in points if p["mode"] == "sync" and p["host_us_per_layer"] == 200)
+    res = {
+        "points": points,
+        "layer_bytes": layer_bytes,
+        # the headline: GPU GB/s of a layer at the engine's duty cycle (host
+        # 200 us per layer, synchronous), from its event-timed GPU time
+        "value": layer_bytes / (head["gpu_us_per_layer"] * 1e-6) / 1e9,
+        "ms_per_step": head["ms_per_token"],
+        "unit_ms": head["gpu_us_per_layer"] / 1e3,
+        "back_to_back_unit_ms": base["gpu_us_per_layer"] / 1e3,
+    }
     return res, (L, hidden, ffn, n_expert, n_sel, shared)
 
 
@@ -817,8 +925,11 @@ def main():
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", default="moe48",
-                    choices=sorted(MOE_WORKLOADS) + sorted(TOKEN_WORKLOADS) + sorted(GEMV_WORKLOADS) + sorted(DENSE_WORKLOADS) + ["moebatch"])
+                    choices=sorted(MOE_WORKLOADS) + sorted(TOKEN_WORKLOADS) + sorted(GEMV_WORKLOADS) + sorted(DENSE_WORKLOADS) + ["moebatch", "moe48duty"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--normed-layer", action="store_true",
+                    help="moe48tok: katali_hip_moe_layer_normed (norm, router and layer in two launches per layer) "
+                         "instead of the norm/router launch and the layer (three)")
     ap.add_argument("--batch-points", default="", metavar="NxT,...",
                     help="moebatch: only these (n_sel x tokens) points, e.g. 8x64,2x64 (profiling)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -882,22 +993,47 @@ def main():
                  "eager_layer_ms_mean": round(res["kernel_ms_mean"], 5)}
     elif args.workload in TOKEN_WORKLOADS:
         base, vocab = TOKEN_WORKLOADS[args.workload]
-        res, shape = bench_moe(hip, base, args.steps, args.warmup, vocab=vocab)
+        res, shape = bench_moe(hip, base, args.steps, args.warmup, vocab=vocab, normed=args.normed_layer)
         L, hidden, ffn, n_expert, n_sel, shared = shape
         unit_ms = res["ms_per_step"]
         unit_bytes = res["bytes_per_token"]
         metric = "decode token HBM GB/s (% of ~8 TB/s peak) + tok/s: MoE FFN chain, LM head and argmax on device"
+        steps_desc = ("one launch for residual add + RMSNorm + F32 router, then the MoE layer's two"
+                      if not args.normed_layer else
+                      "two launches (katali_hip_moe_layer_normed: kernel A forms the residual add, RMSNorm and "
+                      "F32 router rows itself and exchanges the logits on the device, then kernel B)")
         config = {
-            "workload": f"{args.workload}: whole decode tokens of {base} with attention aside: per layer one launch "
-                        f"for residual add + RMSNorm + F32 router {n_expert}x{hidden}, the MoE layer routed on the "
+            "workload": f"{args.workload}: whole decode tokens of {base} with attention aside: per layer "
+                        f"{steps_desc}; router {n_expert}x{hidden} F32, the MoE layer routed on the "
                         f"device from those logits (top-{n_sel}, gate/up {hidden}->{ffn} Q4_K, down Q6_K); output "
                         f"RMSNorm, Q6_K LM head {vocab}x{hidden} (v_dot4), greedy argmax; one hipGraph per token "
                         f"(64 input vectors in a ring)",
             "layers": L, "hidden": hidden, "ffn": ffn, "n_expert": n_expert, "n_sel": n_sel, "vocab": vocab,
             "bytes_per_token": res["bytes_per_token"], "parallelism": "single GPU",
         }
-        kernel = "whole token graph (3 per layer + 4 launches: k_norm_router, k_moe_gu, k_moe_down; output norm, head, argmax)"
+        kernel = ("whole token graph (3 per layer + 4 launches: k_norm_router, k_moe_gu, k_moe_down; output norm, "
+                  "head, argmax)" if not args.normed_layer else
+                  "whole token graph (2 per layer + 4 launches: k_moe_gu with the norm and router, k_moe_down; "
+                  "output norm, head, argmax)")
         extra = {"tok_s": round(res["tok_s"], 2)}
+    elif args.workload == "moe48duty":
+        res, shape = bench_duty(hip, "moe48", args.steps, args.warmup)
+        L, hidden, ffn, n_expert, n_sel, shared = shape
+        unit_ms = res["unit_ms"]
+        unit_bytes = res["layer_bytes"]
+        metric = ("fused MoE layer HBM GB/s at the engine's duty cycle (200 us of host work before each layer, "
+                  "synchronous submission) + tok/s synchronous vs asynchronous")
+        config = {
+            "workload": f"moe48duty: the moe48 layers (hidden {hidden}, {n_expert} experts, top-{n_sel}, gate/up "
+                        f"{hidden}->{ffn} Q4_K, down Q6_K) submitted one by one without a graph, with a host busy "
+                        f"interval before each layer standing in for the engine's CPU attention; intervals "
+                        f"{list(DUTY_INTERVALS_US)} us; sync = wait after every layer, async = one wait per token",
+            "layers": L, "hidden": hidden, "ffn": ffn, "n_expert": n_expert, "n_sel": n_sel,
+            "parallelism": "single GPU",
+        }
+        kernel = "MoE layer at the duty cycle: k_moe_gu + k_moe_down, event-timed per layer"
+        extra = {"duty_points": res["points"],
+                 "back_to_back_gpu_us_per_layer": round(res["back_to_back_unit_ms"] * 1e3, 3)}
     elif args.workload == "moebatch":
         only = [tuple(int(v) for v in pt.split("x")) for pt in args.batch_points.split(",") if pt] or None
         res, shape = bench_moe_batch(hip, args.steps, args.warmup, only)

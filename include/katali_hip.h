@@ -192,6 +192,39 @@ typedef struct KataliHipMoeRoute {
 int katali_hip_moe_layer(const KataliHipMoe *moe, const KataliHipMoeRoute *route,
                          const float *x_dev, const void *xq8_dev, float *y_dev);
 
+/* The steps before a MoE layer and the layer, in two launches where the
+ * separate calls take three: katali_hip_rmsnorm_matvec_f32(x, delta, scale,
+ * x_out, norm_w, hidden, eps, xn_out, router, n_expert, logits_out)
+ * followed by katali_hip_moe_layer routed from those logits (n_sel experts,
+ * ids_out / weights_out optional) on xn, with every output bit-identical to
+ * that pair's (V/src/gguf_model.c:677-683, the F32 router product, the MoE
+ * layer). Kernel A forms the residual step, the norm and the router rows in
+ * its own workgroups and exchanges the logits between them on the device
+ * (its workgroups wait for each other: on a device busy with other work the
+ * wait can expire, reported as KATALI_HIP_E_TIMEOUT by the next
+ * katali_hip_sync, the outputs then invalid). When kernel A has more
+ * workgroups (n_slots * ffn / 32) than the device has CUs, or n_expert is
+ * more than 4 router rows per workgroup, the call runs the norm/router
+ * launch and the layer instead, with the same results. Rules of
+ * katali_hip_rmsnorm_matvec_f32
+ * (16-byte alignment, outputs apart from inputs) and of katali_hip_moe_layer;
+ * n_sel >= 1; xn_out and logits_out may be NULL. No counterpart in the
+ * reference: for an engine that keeps the residual stream on the device. */
+typedef struct KataliHipMoeNorm {
+    uint32_t struct_size;                  /* sizeof(KataliHipMoeNorm) */
+    const float *x;                        /* residual stream [hidden] */
+    const float *delta;                    /* optional: x_out = x + scale * delta */
+    float scale;
+    float *x_out;                          /* the new residual (with delta), apart from x */
+    const float *norm_w;                   /* RMSNorm weights [hidden] */
+    float eps;
+    float *xn_out;                         /* optional: RMSNorm(x_out or x) * norm_w */
+    const float *router;                   /* F32 router [n_expert][hidden] */
+    float *logits_out;                     /* optional [n_expert] */
+} KataliHipMoeNorm;
+int katali_hip_moe_layer_normed(const KataliHipMoe *moe, const KataliHipMoeNorm *norm, int32_t n_sel,
+                                int32_t *ids_out, float *weights_out, float *y_dev);
+
 /* KATALI_HIP_OK when katali_hip_moe_layer (n_tokens 0) or katali_hip_moe_batch
  * (n_tokens 1..64 tokens) runs a layer of this descriptor's shape with n_sel
  * routed experts; else the code and last-error message the call would give.

@@ -44,7 +44,8 @@ constexpr size_t HQ8_LAYER = 1u << 20;   // >= 17 slots x ffn/32 x 36 of every l
 uint8_t *g_hq8 = nullptr;     // single-token layer: q8_1 h [n_slots][ffn/32]
 int32_t *g_route = nullptr;   // [ids | weights] from kernel A to kernel B
 int32_t *g_err_dev = nullptr;
-uint32_t *g_fsync = nullptr;  // the fused layer's generation word and flags (zeroed once)
+uint32_t *g_fsync = nullptr;  // the in-kernel exchanges' generation words and flags (zeroed once)
+float *g_nbuf = nullptr;      // the normed layer's xn [4096] and logits [512] when it runs as two steps
 
 // Scratch of katali_hip_moe_layer_noalloc: a static device array, resolved
 // to a device address once per device at init (the array's name is a host
@@ -170,13 +171,15 @@ int moe_scratch() {
     if (e == hipSuccess) e = hipMemset(g_err_dev, 0, 64);
     if (e == hipSuccess) e = hipMalloc((void **)&g_fsync, kq::fsync_words() * 4);
     if (e == hipSuccess) e = hipMemset(g_fsync, 0, kq::fsync_words() * 4);
+    if (e == hipSuccess) e = hipMalloc((void **)&g_nbuf, (4096 + 512) * 4);
     if (e == hipSuccess) e = hipMalloc((void **)&g_hq8, HQ8_LAYER);
     if (e != hipSuccess) {
         // nothing half-made stays: the next call starts over
-        for (void *p : {(void *)g_route, (void *)g_err_dev, (void *)g_fsync, (void *)g_hq8})
+        for (void *p : {(void *)g_route, (void *)g_err_dev, (void *)g_fsync, (void *)g_nbuf, (void *)g_hq8})
             if (p) (void)hipFree(p);
         g_route = g_err_dev = nullptr;
         g_fsync = nullptr;
+        g_nbuf = nullptr;
         g_hq8 = nullptr;
         return fail(KATALI_HIP_E_NOMEM, "MoE scratch: %s", hipGetErrorString(e));
     }
@@ -468,10 +471,11 @@ int katali_hip_sync(void) {
         if (err) {
             (void)hipMemset(g_err_dev, 0, 4);
             if (err & 4) {
-                // a fused layer gave up waiting (the device was shared with
-                // other work): its output and the flags are void; start over
+                // a fused or normed layer gave up waiting for its own
+                // workgroups (the device was shared with other work): its
+                // outputs and the exchange words are void; start over
                 if (g_fsync) (void)hipMemset(g_fsync, 0, kq::fsync_words() * 4);
-                return fail(KATALI_HIP_E_TIMEOUT, "fused MoE layer: in-kernel wait expired (output invalid)");
+                return fail(KATALI_HIP_E_TIMEOUT, "MoE layer: in-kernel wait expired (outputs invalid)");
             }
             return fail(KATALI_HIP_E_INVALID, "MoE expert id outside [0, n_expert) in the explicit routing");
         }
@@ -665,6 +669,60 @@ int katali_hip_moe_check(const KataliHipMoe *m, int32_t n_sel, uint32_t n_tokens
 
 int katali_hip_moe_layer(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, const void *xq, float *y) {
     return moe_impl(m, r, x, xq, y, nullptr, nullptr);
+}
+
+int katali_hip_moe_layer_normed(const KataliHipMoe *m, const KataliHipMoeNorm *nrm, int32_t n_sel, int32_t *ids_out,
+                                float *weights_out, float *y) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!nrm || nrm->struct_size < sizeof(KataliHipMoeNorm)) return fail(KATALI_HIP_E_INVALID, "null or short norm descriptor");
+    if (n_sel < 1) return fail(KATALI_HIP_E_INVALID, "n_sel=%d: the normed layer routes (1..16)", n_sel);
+    KataliHipMoeRoute r;
+    memset(&r, 0, sizeof r);
+    r.struct_size = sizeof r;
+    r.n_sel = n_sel;
+    r.logits = nrm->router;   // stands for "routed from logits" in the checks below
+    r.ids_out = ids_out;
+    r.weights_out = weights_out;
+    kq::MoeArgs a;
+    uint32_t n_slots = 0;
+    if ((rc = moe_args(m, &r, nrm->x, nullptr, y, a, n_slots))) return rc;
+    // the steps before the layer: katali_hip_rmsnorm_matvec_f32's rules
+    const uint64_t n = m->hidden, rows = m->n_expert;
+    const float *x = nrm->x, *delta = nrm->delta, *nw = nrm->norm_w, *w = nrm->router;
+    float *x_out = nrm->x_out, *xn = nrm->xn_out, *lg = nrm->logits_out;
+    if (!x || !nw || !w || (delta && !x_out)) return fail(KATALI_HIP_E_INVALID, "null buffer");
+    if (((uintptr_t)x | (uintptr_t)delta | (uintptr_t)x_out | (uintptr_t)nw | (uintptr_t)xn | (uintptr_t)w) % 16)
+        return fail(KATALI_HIP_E_INVALID, "vectors and the router must be 16-byte aligned");
+    const uint64_t vb = n * 4, wb = rows * n * 4;
+    const void *ins[4] = {x, delta, nw, w};
+    const uint64_t inb[4] = {vb, vb, vb, wb};
+    const void *outs[4] = {delta ? x_out : nullptr, xn, lg, y};
+    const uint64_t outb[4] = {vb, vb, rows * 4, vb};
+    for (int o = 0; o < 4; o++) {
+        for (int i = 0; i < 4; i++)
+            if (overlap(outs[o], outb[o], ins[i], inb[i])) return fail(KATALI_HIP_E_INVALID, "an output overlaps an input");
+        for (int p = o + 1; p < 4; p++)
+            if (overlap(outs[o], outb[o], outs[p], outb[p])) return fail(KATALI_HIP_E_INVALID, "outputs overlap");
+    }
+    if ((rc = moe_scratch())) return rc;
+    a.x = nullptr;
+    a.logits = nullptr;
+    a.hq8 = g_hq8;
+    a.route_ids = g_route;
+    a.route_w = (float *)(g_route + kq::moe_route_words() / 2);
+    a.err = g_err_dev;
+    a.fsync = g_fsync;
+    a.nx = x;
+    a.ndelta = delta;
+    a.nscale = nrm->scale;
+    a.nx_out = x_out;
+    a.nw = nw;
+    a.neps = nrm->eps;
+    a.nxn_out = xn;
+    a.router = w;
+    a.logits_out = lg;
+    return launched(kq::launch_moe_normed(a, g_nbuf, g_nbuf + 4096, g_stream), "moe normed launch");
 }
 
 int katali_hip_moe_layer_debug(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, const void *xq,

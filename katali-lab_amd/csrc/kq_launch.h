@@ -108,6 +108,16 @@ struct MoeArgs {
     uint32_t bS;
     uint64_t xq_stride;
     float *yp;
+    // The steps before the layer, in kernel A (launch_moe_normed; router !=
+    // NULL): x_out = nx + nscale * ndelta (with ndelta), xn = RMSNorm(x_out or
+    // nx) * nw, logits = router . xn, routed from those logits.
+    const float *nx, *ndelta;
+    float nscale, neps;
+    float *nx_out;
+    const float *nw;
+    float *nxn_out;
+    const float *router;   // F32 [n_expert][hidden]
+    float *logits_out;
 };
 bool moe_shape_supported(uint32_t gate_type, uint32_t down_type, uint32_t hidden, uint32_t ffn);
 // Dynamic LDS (bytes) of the largest workgroup a layer of this shape launches:
@@ -123,12 +133,28 @@ constexpr uint32_t LDS_PER_WG = 160 * 1024;
 // The layer in one launch when the shape fits the fused kernel and a.fsync is
 // set (and `allow_fused`), else kernels A and B. *fused tells which ran.
 hipError_t launch_moe(const MoeArgs &a, hipStream_t s, bool allow_fused = false, bool *fused = nullptr);
-// The fused layer's exchange (zeroed once, before first use): [0] the
-// generation, from FSYNC_H one block per workgroup of 9 8-byte words
-// {dword, generation} (its q8_1 h block, or zeros).
+// The in-kernel exchanges (zeroed once, before first use): [0] the fused
+// layer's generation, [1] the normed layer's; from FSYNC_H one block per
+// workgroup of the fused layer of 9 8-byte words {dword, generation} (its
+// q8_1 h block, or zeros); from FSYNC_R, FSYNC_REP copies 4 KiB apart of one
+// 8-byte word {logit, generation} per router row of the normed layer (its
+// workgroups read the copy of their index mod FSYNC_REP, so no few cache
+// lines take every poll).
 constexpr uint32_t FSYNC_H = 64;
 constexpr uint32_t FUSED_MAX_G = 256;   // workgroups of the fused layer
-constexpr uint32_t fsync_words() { return FSYNC_H + 2 * 9 * FUSED_MAX_G; }
+constexpr uint32_t FSYNC_R = 8192;      // 32 KiB in, past the fused layer's words
+constexpr uint32_t FSYNC_REP = 16;
+constexpr uint32_t fsync_words() { return FSYNC_R + FSYNC_REP * 2 * 512; }
+static_assert(FSYNC_H + 2 * 9 * FUSED_MAX_G <= FSYNC_R, "exchange areas overlap");
+// The steps before the layer and the layer in two launches (MoeArgs' n*
+// fields and router set, n_sel >= 1, hidden <= 4096): kernel A forms the
+// residual step, the RMSNorm and its router rows itself (bit-identical to
+// launch_norm_router), exchanges the logits between its workgroups through
+// a.fsync, routes and runs the gate/up units; kernel B as launch_moe's.
+// When the router rows do not spread over kernel A's workgroups (more than
+// 4 rows each), launch_norm_router into xn_buf / logits_buf first, then
+// launch_moe. *merged tells which ran.
+hipError_t launch_moe_normed(MoeArgs a, float *xn_buf, float *logits_buf, hipStream_t s, bool *merged = nullptr);
 // Top-n_sel routing of n_tokens rows of logits [n_tokens][n_expert] (<= 512
 // experts, 1 <= n_sel <= min(16, n_expert)): ids / weights [n_tokens][n_sel],
 // each row as the single-token layer routes it.

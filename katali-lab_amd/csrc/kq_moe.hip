@@ -352,6 +352,220 @@ __device__ __forceinline__ void route_finish(const MoeArgs &a, const float (&lv)
     }
 }
 
+// ---------------------------------------------------------------------------
+// The normed layer's prologue (kernel A of launch_moe_normed): the steps
+// before the layer, formed by every workgroup of kernel A itself.
+//   Residual step and RMSNorm as k_norm_router forms them: threads 0..255
+//   take float4 q = t + 256 k (k < KN), each its double sum of squares in
+//   that order, the wave sums, then waves 0..3 in order; inv = 1 / sqrtf(
+//   (float)(sumsq / H) + eps), xn = v * inv * w; workgroup 0 writes xn and
+//   the new residual.
+//   Router rows w + U v on wave v < R (U workgroups): the engine's AVX2 F32
+//   dot, accumulator j's FMA chain over columns j, j + 16, ... on lane j < 16,
+//   then its horizontal sum (bit-identical to k_norm_router's rows), each
+//   published as one 8-byte device-coherent word {logit, generation + 1} in
+//   FSYNC_REP copies (lane k < 16 writes copy k). The rows and xn sit in LDS
+//   transposed by accumulator (column c at [c % 16][c / 16], row stride
+//   H / 16 + 4 floats: 16-byte chain reads, no bank conflicts).
+//   Wave 0 then waits for every row's word (two rounds of loads in flight),
+//   routes from those logits and hands the routing to the other waves in
+//   LDS.
+// LDS at `area`: xn and NORMED_MAX_R rows (16 (H/16 + 4) floats each),
+// 4 doubles, the routing (16 ids, 16 logits). Returns this thread's xn
+// float4s for the q8_1 staging. (Ranking the experts over the whole
+// workgroup instead of wave 0's wave_topk measured slower: 1.65 us against
+// 1.2 us, bound by the LDS reads of 1024 threads.)
+// ---------------------------------------------------------------------------
+constexpr uint32_t NORMED_MAX_R = 4;
+__host__ __device__ constexpr uint32_t normed_area_bytes(uint32_t H) {
+    return 4 * (H + 64) * (1 + NORMED_MAX_R) + 32 + 128;
+}
+
+template <int NB, int C, int NT, int XPT>
+__device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area, uint32_t U, GuRoute &rt,
+                                                float4 (&xv)[XPT]) {
+    constexpr uint32_t H = 256 * NB;
+    constexpr uint32_t KN = H <= 2048 ? 2 : 4;   // k_norm_router's float4 per thread
+    constexpr uint32_t Q4 = H / 4;
+    constexpr uint32_t M = H / 16, TS = M + 4;   // chain length, transposed row stride
+    constexpr uint32_t VT = 16 * TS;             // floats of one transposed vector
+    constexpr uint32_t RF = NORMED_MAX_R * Q4;   // router float4s of a full workgroup share
+    constexpr uint32_t RPT = (RF + NT - 1) / NT;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t w = blockIdx.x;
+    float *xnT = (float *)area;
+    float *rowsT = xnT + VT;
+    double *part = (double *)(rowsT + NORMED_MAX_R * VT);
+    int32_t *rte = (int32_t *)(part + 4);
+    float *rtl = (float *)(rte + 16);
+    auto at = [](uint32_t c) { return (c & 15) * TS + (c >> 4); };
+    const uint32_t R = (a.n_expert + U - 1) / U;   // the host keeps R <= NORMED_MAX_R
+    const uint32_t gen = ld_dev(a.fsync + 1);        // issued first, used last
+
+    // 1. every load: x, delta and the norm weights (threads < 256, whole
+    //    waves), the router rows (all threads; clamped)
+    float4 vx[KN], vd[KN], vn[KN];
+    if (tid < 256) {
+#pragma unroll
+        for (uint32_t k = 0; k < KN; k++) {
+            const uint32_t q = min(tid + k * 256, Q4 - 1);
+            vx[k] = *(const float4 *)&a.nx[4 * q];
+            vd[k] = a.ndelta ? *(const float4 *)&a.ndelta[4 * q] : make_float4(0.f, 0.f, 0.f, 0.f);
+            vn[k] = *(const float4 *)&a.nw[4 * q];
+        }
+    }
+    float4 rv[RPT];
+#pragma unroll
+    for (uint32_t i = 0; i < RPT; i++) {
+        const uint32_t f = min(tid + NT * i, RF - 1), v = f / Q4, q = f % Q4;
+        const uint32_t r = min(w + U * v, a.n_expert - 1);
+        rv[i] = *(const float4 *)&a.router[(uint64_t)r * H + 4 * q];
+    }
+    // all NORMED_MAX_R row slots, transposed (those past R hold a copy of the
+    // last row; a clamped thread writes what its twin writes)
+#pragma unroll
+    for (uint32_t i = 0; i < RPT; i++) {
+        const uint32_t f = min(tid + NT * i, RF - 1), c = 4 * (f % Q4);
+        float *rt_ = rowsT + (f / Q4) * VT;
+        rt_[at(c)] = rv[i].x;
+        rt_[at(c + 1)] = rv[i].y;
+        rt_[at(c + 2)] = rv[i].z;
+        rt_[at(c + 3)] = rv[i].w;
+    }
+    // 2. residual step and the sum of squares
+    if (tid < 256) {
+        double sq = 0.0;
+        const bool unit = a.nscale == 1.0f;
+#pragma unroll
+        for (uint32_t k = 0; k < KN; k++) {
+            if (a.ndelta) {
+                if (unit) {
+                    vx[k].x = vx[k].x + vd[k].x; vx[k].y = vx[k].y + vd[k].y;
+                    vx[k].z = vx[k].z + vd[k].z; vx[k].w = vx[k].w + vd[k].w;
+                } else {
+                    vx[k].x = vx[k].x + a.nscale * vd[k].x; vx[k].y = vx[k].y + a.nscale * vd[k].y;
+                    vx[k].z = vx[k].z + a.nscale * vd[k].z; vx[k].w = vx[k].w + a.nscale * vd[k].w;
+                }
+            }
+            const bool own = tid + k * 256 < Q4;
+            sq += own ? (double)vx[k].x * (double)vx[k].x : 0.0;
+            sq += own ? (double)vx[k].y * (double)vx[k].y : 0.0;
+            sq += own ? (double)vx[k].z * (double)vx[k].z : 0.0;
+            sq += own ? (double)vx[k].w * (double)vx[k].w : 0.0;
+        }
+        sq = wave_sum_f64(sq);
+        if (lane == 0) part[wave] = sq;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    // 3. xn into LDS, transposed (and from workgroup 0 to memory, with the
+    //    new residual)
+    if (tid < 256) {
+        double sumsq = part[0];
+#pragma unroll
+        for (uint32_t k = 1; k < 4; k++) sumsq += part[k];
+        const float inv = 1.0f / sqrtf((float)(sumsq / (double)H) + a.neps);
+#pragma unroll
+        for (uint32_t k = 0; k < KN; k++) {
+            const uint32_t q = min(tid + k * 256, Q4 - 1), c = 4 * q;
+            float4 o;
+            o.x = vx[k].x * inv * vn[k].x; o.y = vx[k].y * inv * vn[k].y;
+            o.z = vx[k].z * inv * vn[k].z; o.w = vx[k].w * inv * vn[k].w;
+            xnT[at(c)] = o.x;
+            xnT[at(c + 1)] = o.y;
+            xnT[at(c + 2)] = o.z;
+            xnT[at(c + 3)] = o.w;
+            if (w == 0) {
+                if (a.nxn_out) *(float4 *)&a.nxn_out[c] = o;
+                if (a.ndelta) *(float4 *)&a.nx_out[c] = vx[k];
+            }
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    // 4. this workgroup's router rows: wave v, lanes 0..15
+    uint32_t tag = gen;
+    asm volatile("" : "+v"(tag));
+    tag += 1;
+    const uint32_t r = w + U * wave;
+    if (wave < R && r < a.n_expert && lane < 16) {
+        const float *pw = rowsT + wave * VT + lane * TS, *px = xnT + lane * TS;
+        float acc = 0.0f;
+#pragma unroll 8
+        for (uint32_t i = 0; i < M; i += 4) {
+            const float4 wv = *(const float4 *)&pw[i], xq = *(const float4 *)&px[i];
+            acc = fmaf(wv.x, xq.x, acc);
+            acc = fmaf(wv.y, xq.y, acc);
+            acc = fmaf(wv.z, xq.z, acc);
+            acc = fmaf(wv.w, xq.w, acc);
+        }
+        // + 0.0f: a zero sum's sign as k_norm_router leaves it
+        const float logit = hsum16_avx2_order(acc) + 0.0f;   // every lane of the row holds it
+        if (lane == 0 && a.logits_out) a.logits_out[r] = logit;
+        st_dev2(a.fsync + FSYNC_R + 2 * (512 * lane + r), ((uint64_t)tag << 32) | __float_as_uint(logit));
+    }
+    // 5. wave 0: every row's word (from this workgroup's copy), the routing
+    //    from those logits, into LDS for the other waves
+    if (wave == 0) {
+        const uint32_t *rep = a.fsync + FSYNC_R + 2 * 512 * (w % FSYNC_REP);
+        uint64_t va[C], vb[C];
+        auto issue = [&](uint64_t *o) {
+#pragma unroll
+            for (int i = 0; i < C; i++) o[i] = ld_dev2((uint32_t *)rep + 2 * min(lane + 64 * i, a.n_expert - 1));
+        };
+        auto seen = [&](const uint64_t *o) {
+            bool ok = true;
+#pragma unroll
+            for (int i = 0; i < C; i++) ok &= (uint32_t)(o[i] >> 32) == tag;
+            return __all(ok);
+        };
+        float lv[C];
+        auto take = [&](const uint64_t *o) {
+#pragma unroll
+            for (int i = 0; i < C; i++) lv[i] = __uint_as_float((uint32_t)o[i]);
+        };
+        issue(va);
+        uint32_t spins = 0;
+        for (;;) {
+            issue(vb);
+            if (seen(va)) {
+                take(va);
+                break;
+            }
+            issue(va);
+            if (seen(vb)) {
+                take(vb);
+                break;
+            }
+            if (++spins >= FSYNC_SPIN_LIMIT / 2) {
+                if (lane == 0) atomicOr(a.err, 4);
+                take(vb);
+                break;
+            }
+        }
+        const WaveRoute wr = wave_topk<C>(a, lv);
+        if (lane < 16) {
+            rte[lane] = wr.id;
+            rtl[lane] = wr.logit;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    // 6. every wave's routing (lane r < n_sel: rank r); 7. xn for the staging
+    const bool ranked = lane < 16 && (int)lane < a.n_sel;
+    rt.eid = ranked ? rte[min(lane, 15u)] : -1;
+    rt.logit = ranked ? rtl[min(lane, 15u)] : 0.0f;
+    rt.w = 0.0f;
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+        const uint32_t c = 4 * min(tid + NT * i, (uint32_t)(64 * NB) - 1);
+        xv[i] = make_float4(xnT[at(c)], xnT[at(c + 1)], xnT[at(c + 2)], xnT[at(c + 3)]);
+    }
+}
+
 // One gate/up unit (32 gate + 32 up rows of one slot, one q8_1 block of h)
 // for the workgroup: kernel A's whole body, and the first phase of the fused
 // layer (FUSED: h also goes out as generation-tagged device-coherent words,
@@ -359,7 +573,7 @@ __device__ __forceinline__ void route_finish(const MoeArgs &a, const float (&lv)
 struct NoMore {
     __device__ void operator()(const GuRoute &) const {}
 };
-template <int NB, int C, bool FUSED, class After = NoMore>
+template <int NB, int C, bool FUSED, class After = NoMore, bool NORMED = false>
 __device__ __forceinline__ void gu_unit(const MoeArgs &a, uint32_t unit, uint8_t *lds, GuRoute &rt, uint32_t flag,
                                         After after = After()) {
     // FUSED: flag is this call's generation; h's words are tagged flag + 1
@@ -384,25 +598,33 @@ __device__ __forceinline__ void gu_unit(const MoeArgs &a, uint32_t unit, uint8_t
     // routing inputs, then x (fp32 or q8_1; lane task t covers values
     // 4t..4t+3); their latencies overlap. Loads are clamped, not guarded: no
     // branch sits around a load.
-    float lv[C];
-    route_issue<C>(a, lv, rt);
     constexpr int XTASKS = 64 * NB;            // quantizer lane tasks (8 per 32-block)
     constexpr int XPT = (XTASKS + NT - 1) / NT;
     float4 xv[XPT];
     uint32_t xqv[XPT], xdv[XPT];
-    if (xq == nullptr) {
-#pragma unroll
-        for (int i = 0; i < XPT; i++) xv[i] = *(const float4 *)(a.x + 4 * min(tid + NT * i, (uint32_t)XTASKS - 1));
+    if constexpr (NORMED) {
+        // the steps before the layer, here: xn and the routing from its logits
+        normed_prologue<NB, C, NT, XPT>(a, lds + L.scl, gridDim.x, rt, xv);
     } else {
+        // every wave routes on its own: no barrier before its weight loads
+        // (routing by rank over the workgroup, 8 threads per expert, measured
+        // slower: 14.3-14.6 us against 13.6-13.9 us per layer)
+        float lv[C];
+        route_issue<C>(a, lv, rt);
+        if (xq == nullptr) {
 #pragma unroll
-        for (int i = 0; i < XPT; i++) {
-            const uint32_t t = min(tid + NT * i, (uint32_t)XTASKS - 1);
-            const uint8_t *b = xq + (t >> 3) * 36;
-            xqv[i] = *(const uint32_t *)(b + 4 + 4 * (t & 7));
-            xdv[i] = ld_u16(b);
+            for (int i = 0; i < XPT; i++) xv[i] = *(const float4 *)(a.x + 4 * min(tid + NT * i, (uint32_t)XTASKS - 1));
+        } else {
+#pragma unroll
+            for (int i = 0; i < XPT; i++) {
+                const uint32_t t = min(tid + NT * i, (uint32_t)XTASKS - 1);
+                const uint8_t *b = xq + (t >> 3) * 36;
+                xqv[i] = *(const uint32_t *)(b + 4 + 4 * (t & 7));
+                xdv[i] = ld_u16(b);
+            }
         }
+        route_finish<C>(a, lv, rt);
     }
-    route_finish<C>(a, lv, rt);
     // Drain the routing and x loads here, in one place: with loads issued
     // under branches the compiler cannot tell which registers are still
     // pending and would otherwise wait for the weight loads one by one.
@@ -480,7 +702,8 @@ __device__ __forceinline__ void gu_unit(const MoeArgs &a, uint32_t unit, uint8_t
 #pragma unroll
     for (int k = 0; k < LPG; k++) q[k] = ld16(chunk(0, k));
 
-    if (publisher) route_publish(a, rt.eid, a.logits && a.n_sel > 0 ? route_weight(rt.logit, a.n_sel) : rt.w);
+    if (publisher)
+        route_publish(a, rt.eid, (NORMED || a.logits) && a.n_sel > 0 ? route_weight(rt.logit, a.n_sel) : rt.w);
     if (!x_first) stage_x();   // x is ready long before the weights: off the critical path
     XSlice xs[M];
 #pragma unroll
@@ -580,11 +803,11 @@ __device__ __forceinline__ void gu_unit(const MoeArgs &a, uint32_t unit, uint8_t
     }
 }
 
-template <int NB, int C>
+template <int NB, int C, bool NORMED = false>
 __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_gu(MoeArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
     GuRoute rt;
-    gu_unit<NB, C, false>(a, blockIdx.x, lds, rt, 0);
+    gu_unit<NB, C, false, NoMore, NORMED>(a, blockIdx.x, lds, rt, 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -658,6 +881,10 @@ __global__ void __launch_bounds__(NT > 0 ? NT : B_MAX_THREADS) k_moe_down(MoeArg
     const LdsB L = lds_b(a.ffn, n_slots, tr);
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     pin_args(a.down, a.down_sh, a.y);
+    // the normed layer's exchange generation, read now and advanced at the
+    // end: kernel A is over, so every one of its workgroups has read it (the
+    // load is unconditional; without a router it reads the routing words)
+    uint32_t gen = ld_dev(a.router ? a.fsync + 1 : (uint32_t *)a.route_ids);
     // routing (lane r holds slot r), then the h loads
     const int32_t rid = a.route_ids[min(lane, (uint32_t)MAX_SLOTS - 1)];
     float rw = a.route_w[min(lane, (uint32_t)MAX_SLOTS - 1)];
@@ -725,6 +952,8 @@ __global__ void __launch_bounds__(NT > 0 ? NT : B_MAX_THREADS) k_moe_down(MoeArg
         }
         a.y[row0 + tid] = y;
     }
+    asm volatile("" : "+v"(gen));
+    if (a.router && blockIdx.x == 0 && tid == 0) st_dev(a.fsync + 1, gen + 1);
 }
 
 // ---------------------------------------------------------------------------
@@ -992,22 +1221,6 @@ __host__ __device__ inline LdsF lds_f(uint32_t hidden, uint32_t nb, uint32_t ffn
     L.total = L.vote + 2 * 16 * 4;
     return L;
 }
-// AND of a predicate over the workgroup, exchanged through LDS with fences
-// that order LDS alone: unlike __syncthreads it does not wait for this
-// workgroup's global stores to be acknowledged. Alternate `parity` between
-// consecutive calls (two vote buffers of 16 waves).
-__device__ __forceinline__ bool wg_and_lds(bool ok, int *vote, uint32_t parity) {
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
-    int *v = vote + 16 * (parity & 1);
-    const bool w = __all(ok);
-    if (lane == 0) v[wave] = w;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-    bool all = true;
-    for (uint32_t i = 0; i < nwave; i++) all = all && v[i] != 0;
-    return all;
-}
 // Waves 0 .. 7 hold the down tile (its weights and dots), waves 8 .. 15 read
 // the exchange: a wave's loads complete in issue order, so a poll issued
 // behind a wave's down-weight loads could not be seen before those arrive
@@ -1068,31 +1281,51 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_fused(MoeArgs a, uint3
     float rw = a.logits && a.n_sel > 0 ? route_weight(rt.logit, a.n_sel) : rt.w;
     rw = (int)lane < a.n_sel ? rw : ((int)lane == a.n_sel && a.has_shared ? 1.0f : 0.0f);
 
-    // every workgroup's block, until all carry gen + 1 (the pollers read;
-    // everyone votes)
+    // every workgroup's block, until all carry gen + 1: each polling wave
+    // waits for its own words with two rounds of loads in flight (the next
+    // round goes out before the previous one is checked, so a word is sampled
+    // twice per round trip); the down waves go straight to the barrier below
     uint32_t tag = gen;
     asm volatile("" : "+v"(tag));
     tag += 1;
     const uint32_t nw = 9 * G, pt = tid - FUSED_DOWN_THREADS;
     uint32_t *xw = a.fsync + FSYNC_H;
-    uint32_t spins = 0;
     uint64_t v[FUSED_HW];
-    for (;;) {
-        bool ok = true;
-        if (poller) {   // whole waves
+    if (poller) {   // whole waves
+        uint64_t va[FUSED_HW], vb[FUSED_HW];
+        auto issue = [&](uint64_t *o) {
 #pragma unroll
-            for (int i = 0; i < FUSED_HW; i++) v[i] = ld_dev2(xw + 2 * min(pt + NP * i, nw - 1));
+            for (int i = 0; i < FUSED_HW; i++) o[i] = ld_dev2(xw + 2 * min(pt + NP * i, nw - 1));
+        };
+        auto seen = [&](const uint64_t *o) {
+            bool ok = true;
 #pragma unroll
-            for (int i = 0; i < FUSED_HW; i++) ok &= (uint32_t)(v[i] >> 32) == tag;
+            for (int i = 0; i < FUSED_HW; i++) ok &= (uint32_t)(o[i] >> 32) == tag;
+            return __all(ok);
+        };
+        issue(va);
+        uint32_t spins = 0;
+        for (;;) {
+            issue(vb);
+            if (seen(va)) {
+#pragma unroll
+                for (int i = 0; i < FUSED_HW; i++) v[i] = va[i];
+                break;
+            }
+            issue(va);
+            if (seen(vb)) {
+#pragma unroll
+                for (int i = 0; i < FUSED_HW; i++) v[i] = vb[i];
+                break;
+            }
+            if (++spins >= FSYNC_SPIN_LIMIT / 2) {
+                if (lane == 0) atomicOr(a.err, 4);
+#pragma unroll
+                for (int i = 0; i < FUSED_HW; i++) v[i] = vb[i];
+                break;
+            }
         }
-        if (wg_and_lds(ok, (int *)(lds + L.vote), spins)) break;
-        if (++spins >= FSYNC_SPIN_LIMIT) {
-            if (tid == 0) atomicOr(a.err, 4);
-            break;
-        }
-        if (poller) __builtin_amdgcn_s_sleep(1);
     }
-    if (w == 0 && tid == 0) st_dev(a.fsync, tag);   // every workgroup has read gen: the next call's
 
     // h into LDS: word t = dword t % 9 of block t / 9 (dword 0: d and s;
     // blocks past U are the other workgroups' empty ones)
@@ -1113,6 +1346,10 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_fused(MoeArgs a, uint3
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    // past the barrier every polling wave of this workgroup has seen all
+    // blocks, so every workgroup has read gen: workgroup 0 publishes the next
+    // call's
+    if (w == 0 && tid == 0) st_dev(a.fsync, tag);
     // exact sums of each 16-value half block
     for (uint32_t t = tid; t < 2 * U; t += blockDim.x) {
         const uint32_t b = t >> 1, half = t & 1, kb = b % nblk;
@@ -1222,16 +1459,18 @@ static hipError_t launch_moe_fused(const MoeArgs &a, uint32_t n_slots, hipStream
 
 uint64_t moe_route_words() { return 2 * MAX_SLOTS; }
 
-template <int NB>
+template <int NB, bool NORMED = false>
 static hipError_t go_a(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
     const LdsA L = lds_a(a.hidden, NB);
     const dim3 grid(n_slots * (a.ffn / 32));
+    uint32_t lds = L.total;
+    if (NORMED && L.scl + normed_area_bytes(a.hidden) > lds) lds = L.scl + normed_area_bytes(a.hidden);
     if (a.n_expert <= 128)
-        hipLaunchKernelGGL((k_moe_gu<NB, 2>), grid, dim3(a1_threads<NB>()), L.total, s, a);
+        hipLaunchKernelGGL((k_moe_gu<NB, 2, NORMED>), grid, dim3(a1_threads<NB>()), lds, s, a);
     else if (a.n_expert <= 256)
-        hipLaunchKernelGGL((k_moe_gu<NB, 4>), grid, dim3(a1_threads<NB>()), L.total, s, a);
+        hipLaunchKernelGGL((k_moe_gu<NB, 4, NORMED>), grid, dim3(a1_threads<NB>()), lds, s, a);
     else
-        hipLaunchKernelGGL((k_moe_gu<NB, 8>), grid, dim3(a1_threads<NB>()), L.total, s, a);
+        hipLaunchKernelGGL((k_moe_gu<NB, 8, NORMED>), grid, dim3(a1_threads<NB>()), lds, s, a);
     return hipGetLastError();
 }
 
@@ -1389,6 +1628,49 @@ static hipError_t go_a_any(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
         case 16: return go_a<16>(a, n_slots, s);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_moe_normed(MoeArgs a, float *xn_buf, float *logits_buf, hipStream_t s, bool *merged) {
+    if (merged) *merged = false;
+    if (!a.router || a.n_sel < 1 || a.n_expert > MAX_EXPERT || a.n_sel > MAX_SEL || a.hidden > 4096)
+        return hipErrorInvalidValue;
+    const uint32_t n_slots = (uint32_t)a.n_sel + (a.has_shared ? 1u : 0u);
+    const uint32_t U = n_slots * (a.ffn / 32);
+    // kernel A's workgroups wait for each other's router rows: all of them
+    // must be resident at once (one per CU at most), each with <= 4 rows
+    if (a.fsync && U <= (uint32_t)device_cu_count() && (a.n_expert + U - 1) / U <= NORMED_MAX_R) {
+        a.x = nullptr;
+        a.xq = nullptr;
+        a.logits = nullptr;
+        a.step = nullptr;
+        hipError_t e;
+        switch (a.hidden / 256) {
+            case 1: e = go_a<1, true>(a, n_slots, s); break;
+            case 2: e = go_a<2, true>(a, n_slots, s); break;
+            case 4: e = go_a<4, true>(a, n_slots, s); break;
+            case 8: e = go_a<8, true>(a, n_slots, s); break;
+            case 16: e = go_a<16, true>(a, n_slots, s); break;
+            default: return hipErrorInvalidValue;
+        }
+        if (e != hipSuccess) return e;
+        if (merged) *merged = true;
+        // kernel B advances the exchange generation (a.router set)
+        return a.down_type == T_Q6_K ? go_b_any<Q6K>(a, n_slots, s) : go_b_any<Q4K>(a, n_slots, s);
+    }
+    // the router rows do not spread over kernel A: the steps before the
+    // layer in their own launch, then the layer from their outputs
+    float *xn = a.nxn_out ? a.nxn_out : xn_buf;
+    float *lg = a.logits_out ? a.logits_out : logits_buf;
+    hipError_t e = launch_norm_router(a.nx, a.ndelta, a.nscale, a.nx_out, a.nw, a.hidden, a.neps, xn, a.router,
+                                      a.n_expert, lg, s);
+    if (e != hipSuccess) return e;
+    MoeArgs b = a;
+    b.router = nullptr;
+    b.x = xn;
+    b.xq = nullptr;
+    b.logits = lg;
+    b.step = nullptr;
+    return launch_moe(b, s);
 }
 
 template <int NB>

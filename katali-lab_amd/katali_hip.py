@@ -44,6 +44,7 @@ SIGNATURES = {
     "katali_hip_moe_layer_debug": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "katali_hip_moe_layer_noalloc": (C.c_int, [_vp, _vp, _vp, _vp, _vp]),
     "katali_hip_moe_check": (C.c_int, [_vp, _i32, _u32]),
+    "katali_hip_moe_layer_normed": (C.c_int, [_vp, _vp, _i32, _vp, _vp, _vp]),
     "katali_hip_step_advance": (C.c_int, [_vp, _i32]),
     "katali_hip_graph_begin": (C.c_int, []),
     "katali_hip_graph_end": (C.c_int, [C.POINTER(_vp)]),
@@ -79,6 +80,11 @@ class KataliHipMoeRoute(C.Structure):
     _fields_ = [("struct_size", _u32), ("n_sel", _i32), ("logits", _vp), ("step", _vp),
                 ("logits_stride", _u64), ("ids", _vp), ("weights", _vp),
                 ("ids_out", _vp), ("weights_out", _vp)]
+
+
+class KataliHipMoeNorm(C.Structure):
+    _fields_ = [("struct_size", _u32), ("x", _vp), ("delta", _vp), ("scale", _f32), ("x_out", _vp),
+                ("norm_w", _vp), ("eps", _f32), ("xn_out", _vp), ("router", _vp), ("logits_out", _vp)]
 
 
 class HipError(RuntimeError):
@@ -238,6 +244,14 @@ class KataliHip:
         self.check(self.lib.katali_hip_moe_layer(C.byref(desc), C.byref(route),
                                                  None if x is None else x.ptr,
                                                  None if xq is None else xq.ptr, y.ptr))
+
+    def moe_layer_normed(self, desc, n_sel, x, norm_w, router, y, delta=None, scale=1.0, x_out=None, eps=1e-6,
+                         xn_out=None, logits_out=None, ids_out=None, weights_out=None) -> None:
+        p = lambda b: None if b is None else b.ptr  # noqa: E731
+        nrm = KataliHipMoeNorm(C.sizeof(KataliHipMoeNorm), p(x), p(delta), scale, p(x_out), p(norm_w), eps,
+                               p(xn_out), p(router), p(logits_out))
+        self.check(self.lib.katali_hip_moe_layer_normed(C.byref(desc), C.byref(nrm), n_sel, p(ids_out),
+                                                        p(weights_out), y.ptr))
 
     def moe_check(self, desc, n_sel, n_tokens=0) -> None:
         """Raises HipError when a layer (n_tokens 0) or a batch of n_tokens of
