@@ -359,7 +359,10 @@ int moe_batch_impl(const KataliHipMoe *m, const KataliHipMoeBatch *b, const floa
     a.err = g_err_dev;
     a.yp = g_byp;
     const uint32_t min_big = b->mfma_min_tokens ? b->mfma_min_tokens : 16;
-    return launched(kq::launch_moe_batch(a, T, min_big, x, y, g_bxq, g_bmeta, g_stream, g_aux_stream, g_ev_fork,
+    // KATALI_HIP_ONE_STREAM=1 keeps the grouped GEMM on the library stream
+    // (per-kernel profiles attribute time only without the side stream)
+    hipStream_t aux = env_on("KATALI_HIP_ONE_STREAM") ? g_stream : g_aux_stream;
+    return launched(kq::launch_moe_batch(a, T, min_big, x, y, g_bxq, g_bmeta, g_stream, aux, g_ev_fork,
                                          g_ev_join),
                     "moe batch launch");
 }

@@ -615,7 +615,7 @@ hipError_t launch_moe_batch(const MoeArgs &base, uint32_t T, uint32_t min_big, c
     // run on the side stream, beside the small-entry kernels (a fork and a
     // join cost ~3-4 us, more than the overlap gains on smaller batches).
     const bool any_big = P >= min_big;
-    const bool side = any_big && P >= MB_FORK_PAIRS;
+    const bool side = any_big && P >= MB_FORK_PAIRS && aux != s;   // aux == s: one stream
     hipStream_t sb = side ? aux : s;
     if (side && ((e = hipEventRecord(fork, s)) != hipSuccess || (e = hipStreamWaitEvent(aux, fork, 0)) != hipSuccess))
         return e;

@@ -114,6 +114,9 @@ def main():
     ap.add_argument("--summarize-only", action="store_true", help="parse an existing --out tree, run nothing")
     ap.add_argument("--fused", action="store_true",
                     help="the one-launch MoE layer (KATALI_HIP_FUSED=1; moe48 and moe40cold)")
+    ap.add_argument("--one-stream", action="store_true",
+                    help="moebatch: the grouped GEMM on the library stream (KATALI_HIP_ONE_STREAM=1), so "
+                         "per-kernel times add up to the layer")
     args = ap.parse_args()
     wl = args.workload
     extra_env = {}
@@ -123,6 +126,11 @@ def main():
             sys.exit("--fused applies to moe48 and moe40cold")
         extra_env = {"KATALI_HIP_FUSED": "1"}
         kernels, profile_name, traffic_name = ("k_moe_fused",), "k_moe_fused_" + wl, "fused_" + wl
+    if args.one_stream:
+        if wl != "moebatch":
+            sys.exit("--one-stream applies to moebatch")
+        extra_env = {"KATALI_HIP_ONE_STREAM": "1"}
+        profile_name, traffic_name = profile_name + "_one_stream", wl + "_one_stream"
     out = os.path.join(os.path.abspath(args.out), traffic_name)   # rocprofv3 runs from /tmp
     os.makedirs(out, exist_ok=True)
     bench = [sys.executable, os.path.join(REPO, "bench.py"), "--workload", wl, "--steps", str(args.steps),
@@ -136,6 +144,9 @@ def main():
         "write": ["rocprofv3", "--pmc", "WRITE_SIZE", "--output-format", "csv", "-d", os.path.join(out, "write"),
                   "-o", "run", "--"] + bench,
     }
+    if wl == "moebatch":   # the int8 MFMA kernels: MFMA busy share and int8 MFMA ops, from counters
+        cmds["mfma"] = ["rocprofv3", "--pmc", "MfmaUtil", "SQ_INSTS_VALU_MFMA_MOPS_I8", "--output-format", "csv",
+                        "-d", os.path.join(out, "mfma"), "-o", "run", "--"] + bench
     for k, c in cmds.items():
         if args.summarize_only:
             break
@@ -144,6 +155,8 @@ def main():
     stats = kernel_stats(os.path.join(out, "trace"))
     fetch = counter_means(os.path.join(out, "fetch"), "FETCH_SIZE")
     write = counter_means(os.path.join(out, "write"), "WRITE_SIZE")
+    mfma = counter_means(os.path.join(out, "mfma"), "MfmaUtil") if "mfma" in cmds else {}
+    mops = counter_means(os.path.join(out, "mfma"), "SQ_INSTS_VALU_MFMA_MOPS_I8") if "mfma" in cmds else {}
     copy_bytes = COPY_MIB << 20
     cf = pick(fetch, "k_copy")
     cw = pick(write, "k_copy")
@@ -183,6 +196,16 @@ def main():
         f.write(f"\nCalibration: one k_copy of {copy_bytes} B read + {copy_bytes} B written reads "
                 f"FETCH_SIZE {cf[0][1][1]:.1f} and WRITE_SIZE {cw[0][1][1]:.1f} (KiB units): "
                 f"{f_scale:.2f} and {w_scale:.2f} bytes per counter unit.\n\n")
+        if mfma:
+            f.write("MFMA counters (mfma run): MfmaUtil = SQ_VALU_MFMA_BUSY_CYCLES summed over SIMDs / "
+                    "(GRBM_GUI_ACTIVE x SIMDs) in percent, over each dispatch; SQ_INSTS_VALU_MFMA_MOPS_I8 "
+                    "per dispatch (units of 512 int8 ops).\n\n")
+            f.write("| kernel | MfmaUtil % | MOPS_I8 per dispatch |\n|---|---|---|\n")
+            for sub in kernels:
+                for name, _ in pick(stats, sub):
+                    if name in mfma:
+                        f.write(f"| {name} | {mfma[name][1]:.2f} | {mops.get(name, (0, float('nan')))[1]:,.0f} |\n")
+            f.write("\n")
         f.write("| kernel | calls | avg us | HBM fetch B/dispatch | HBM write B/dispatch |\n|---|---|---|---|---|\n")
         for name, calls, us, fb, wb in table:
             f.write(f"| {name} | {calls} | {us:.2f} | {fb:,.0f} | {wb:,.0f} |\n")
