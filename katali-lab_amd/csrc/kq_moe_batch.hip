@@ -43,17 +43,21 @@ constexpr uint32_t MB_MAX_E = 513;   // routed experts + the shared expert's vir
 
 // meta layout (int32): [0] small entries, [1] grouped-GEMM entries, [2]
 // error bits, [16 ..) small entries (3 ints each: expert, first, count <= 8;
-// at most P), then grouped-GEMM entries (3 ints each: count <= 16; at most
-// P; an expert's entries are consecutive), then order (the P pairs grouped by expert, experts ascending; the order
-// inside one expert's run is arbitrary); an entry's pairs are
-// order[first .. first + count).
+// at most P), then grouped-GEMM entries (MB_REC ints each: expert, first,
+// count <= 16, 0, then the entry's 16 pairs inline, slots past count
+// holding pair 0; at most P; an expert's entries are consecutive), then
+// order (the P pairs grouped by expert, experts ascending; the order inside
+// one expert's run is arbitrary); a small entry's pairs are
+// order[first .. first + count). A grouped-GEMM tile reads its entry count
+// and its whole record at once: no load waits on another.
 constexpr uint32_t MB_GRP = 8;   // pairs per small entry (the grouped GEMV kernels' GRP_MAX)
 constexpr uint32_t MB_BIG = 16;  // pairs per grouped-GEMM entry (the MFMA's 16 B columns)
 constexpr uint32_t MB_FORK_PAIRS = 96;   // batches from this many pairs run the two paths side by side
 constexpr uint32_t MB_DN_CHUNK = 8;   // h blocks staged at once by the down kernel beyond 3 blocks
+constexpr uint32_t MB_REC = 20;      // ints per grouped-GEMM entry: 4 + MB_BIG pairs
 __host__ __device__ inline uint32_t mb_small_off() { return 16; }
 __host__ __device__ inline uint32_t mb_big_off(uint32_t P) { return 16 + 3 * P; }
-__host__ __device__ inline uint32_t mb_order_off(uint32_t P) { return 16 + 6 * P; }
+__host__ __device__ inline uint32_t mb_order_off(uint32_t P) { return 16 + 3 * P + MB_REC * P; }
 uint64_t moe_batch_meta_words(uint32_t P) { return mb_order_off(P) + P; }
 
 // Inclusive prefix sum over the 64 lanes of a wave on the VALU: row_shr 1, 2,
@@ -148,21 +152,16 @@ __global__ void __launch_bounds__(1024) k_mb_group(const int32_t *__restrict__ i
     }
     __syncthreads();
     int32_t *small = meta + mb_small_off(), *bigl = meta + mb_big_off(P), *order = meta + mb_order_off(P);
-    // a pair's place among its expert's pairs comes from an LDS cursor: the
-    // order inside an expert's run may differ from call to call, which no
-    // result depends on (every pair's sums are formed on their own)
-    for (uint32_t p = tid; p < P; p += blockDim.x) {
-        const int32_t e = exp_of[p];
-        order[off_all[e] + atomicAdd(&cur[e], 1)] = (int32_t)p;
-    }
     for (uint32_t e = tid; e < NE; e += blockDim.x) {
         const int32_t c = cnt[e];
         if (big_idx[e] >= 0) {
             for (int32_t k = 0; (int32_t)MB_BIG * k < c; k++) {
-                const int32_t i = big_idx[e] + k;
-                bigl[3 * i + 0] = (int32_t)e;
-                bigl[3 * i + 1] = off_all[e] + (int32_t)MB_BIG * k;
-                bigl[3 * i + 2] = min((int32_t)MB_BIG, c - (int32_t)MB_BIG * k);
+                int32_t *rec = bigl + MB_REC * (big_idx[e] + k);
+                rec[0] = (int32_t)e;
+                rec[1] = off_all[e] + (int32_t)MB_BIG * k;
+                rec[2] = min((int32_t)MB_BIG, c - (int32_t)MB_BIG * k);
+                rec[3] = 0;
+                for (uint32_t j = 0; j < MB_BIG; j++) rec[4 + j] = 0;   // pair 0: a valid row to address
             }
         } else if (small_idx[e] >= 0) {
             for (int32_t k = 0; (int32_t)MB_GRP * k < c; k++) {
@@ -172,6 +171,16 @@ __global__ void __launch_bounds__(1024) k_mb_group(const int32_t *__restrict__ i
                 small[3 * i + 2] = min((int32_t)MB_GRP, c - (int32_t)MB_GRP * k);
             }
         }
+    }
+    __syncthreads();   // the records' pair slots are prefilled before the pairs land in them
+    // a pair's place among its expert's pairs comes from an LDS cursor: the
+    // order inside an expert's run may differ from call to call, which no
+    // result depends on (every pair's sums are formed on their own)
+    for (uint32_t p = tid; p < P; p += blockDim.x) {
+        const int32_t e = exp_of[p];
+        const int32_t k = atomicAdd(&cur[e], 1);
+        order[off_all[e] + k] = (int32_t)p;
+        if (big_idx[e] >= 0) bigl[MB_REC * (big_idx[e] + k / (int32_t)MB_BIG) + 4 + k % (int32_t)MB_BIG] = (int32_t)p;
     }
 }
 
@@ -331,36 +340,42 @@ struct MbW<Q6K> {
 // Gate/up of the grouped-GEMM entries: a tile is 32 gate + 32 up rows (jb) x
 // one entry's <= 16 pairs, workgroup t = entry * nblk + jb, so the tiles of
 // the entries the grouping made come first and the workgroups past them
-// (the grid covers the worst-case entry count) leave after one scalar load.
-// The entries of one expert are consecutive, so the tiles that share a
+// (the grid covers the worst-case entry count) leave after their first
+// loads. The entries of one expert are consecutive, so the tiles that share a
 // weight tile are nblk workgroups apart: with nblk a multiple of 8 they run
-// on one XCD and share its L2 copy of the weights. Per tile: the entry,
-// then its pair list with every weight load behind it, then the pairs'
-// activation blocks, each loaded two blocks ahead of its multiplication (a
-// ring of three in registers, two LDS buffers).
+// on one XCD and share its L2 copy of the weights. Per tile: the entry count
+// and the entry's record (pairs inline) at once, every weight load behind
+// them, then the pairs' activation blocks: up to 8 blocks all staged in LDS
+// at once behind one barrier (one LDS buffer per block), else a ring of
+// three in registers two blocks ahead over two LDS buffers.
 // ---------------------------------------------------------------------------
 template <int NB>
 __global__ void __launch_bounds__(256) k_mb_gu_mfma(MoeArgs a, const int32_t *__restrict__ meta, uint32_t P) {
     extern __shared__ __align__(16) uint8_t lds[];
     const uint32_t nblk = a.ffn / 32;
-    const uint32_t ntiles = (uint32_t)meta[1] * nblk;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint64_t rb = NB * 144;
     const uint32_t arow = lane % 16, kc = lane / 16;   // A: row, k chunk
     const uint32_t dcol = lane % 16, drow0 = 4 * (lane / 16);   // D: pair column, first row
     const uint32_t si = tid >> 4;   // this thread's staging pair
-    constexpr bool UP = NB <= 8;   // every block's weights in registers at once
+    constexpr bool UP = NB <= 8;   // every block's weights in registers, every x block in LDS, at once
+    constexpr uint32_t NBUF = UP ? NB : 2;
     {
         const uint32_t t = blockIdx.x;
-        if (t >= ntiles) return;   // whole workgroup, before any barrier
-        uint8_t *const lt = lds;
-        float2 *scl = (float2 *)(lt + 2 * MBX_BYTES) + 16 * 8 * wave;   // this wave's [16 rows][8 sub-blocks] {d*sc, dmin*m}
-        float *gu = (float *)(lt + 2 * MBX_BYTES + 4 * 16 * 8 * 8);      // [64 rows][16 pairs]
         const uint32_t bi = t / nblk, jb = t % nblk;
-        const int32_t *big = meta + mb_big_off(P) + 3 * bi;
-        const int32_t e = big[0];
-        const uint32_t cnt = (uint32_t)big[2];
-        const int32_t *pairs = meta + mb_order_off(P) + big[1];
+        const int32_t *rec = meta + mb_big_off(P) + MB_REC * bi;
+        // independent loads: the entry count, the record, this thread's pair
+        // (slots past the count hold pair 0)
+        const uint32_t nent = (uint32_t)meta[1];
+        const int4 hd = *(const int4 *)rec;
+        const uint32_t sp = (uint32_t)rec[4 + si];
+        if (bi >= nent) return;   // whole workgroup, before any barrier
+        uint8_t *const lt = lds;
+        float2 *scl = (float2 *)(lt + NBUF * MBX_BYTES) + 16 * 8 * wave;   // this wave's [16 rows][8 sub-blocks] {d*sc, dmin*m}
+        float *gu = (float *)(lt + NBUF * MBX_BYTES + 4 * 16 * 8 * 8);      // [64 rows][16 pairs]
+        const int32_t e = hd.x;
+        const uint32_t cnt = (uint32_t)hd.z;
+        const int32_t *pairs = rec + 4;
         const bool shared = (uint32_t)e == a.n_expert;
         const uint8_t *gb = shared ? a.gate_sh : a.gate + (uint64_t)e * a.ffn * rb;
         const uint8_t *ub = shared ? a.up_sh : a.up + (uint64_t)e * a.ffn * rb;
@@ -368,36 +383,45 @@ __global__ void __launch_bounds__(256) k_mb_gu_mfma(MoeArgs a, const int32_t *__
         const uint8_t *wbase = wave < 2 ? gb + (uint64_t)(32 * jb + 16 * wave) * rb
                                         : ub + (uint64_t)(32 * jb + 16 * (wave - 2)) * rb;
         const uint8_t *ap = wbase + (uint64_t)arow * rb, *hp = wbase + (uint64_t)(lane >> 2) * rb;
-        // the pair (clamped; pairs past cnt stage zeros), then the weights:
-        // waiting for the pair waits for nothing else
-        const uint32_t sp = (uint32_t)pairs[min(si, cnt - 1)];
-        MbW<Q4K> w[UP ? NB : 1];
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int b = 0; b < (UP ? NB : 1); b++) w[b].load(ap + b * 144, hp + b * 144, kc);
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
-        // activation blocks two ahead of the one being multiplied (a ring of
-        // three in registers), each staged into its own LDS buffer
         const uint8_t *xrow = a.xq + (uint64_t)(sp / a.bS) * a.xq_stride;
-        XPart xv[3];
-        xv[0] = mbx_load(xrow, 0);
-        xv[1] = mbx_load(xrow, NB > 1 ? 1 : 0);
+        MbW<Q4K> w[UP ? NB : 1];
+        XPart xv[UP ? NB : 3];
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (UP) {
+            // x first: its wait (in issue order) then waits for no weight
+#pragma unroll
+            for (int b = 0; b < NB; b++) xv[b] = mbx_load(xrow, b);
+#pragma unroll
+            for (int b = 0; b < NB; b++) w[b].load(ap + b * 144, hp + b * 144, kc);
+        } else {
+            w[0].load(ap, hp, kc);
+            xv[0] = mbx_load(xrow, 0);
+            xv[1] = mbx_load(xrow, NB > 1 ? 1 : 0);
+        }
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (UP) {
+#pragma unroll
+            for (int b = 0; b < NB; b++) mbx_put(mbx_carve(lt + b * MBX_BYTES), xv[b], si < cnt);
+            __syncthreads();
+        }
         // each (row, pair) value is the pairwise sum of its sub-block terms,
         // pushed in sub-block order (kernel A's q8_1-path dot, bit for bit)
         constexpr int LV = log2c<NB>() + 1;
         float stk[4][LV];
-        static_for<0, NB>([&](auto bc) {   // unrolled: the register ring is indexed by constants
+        static_for<0, NB>([&](auto bc) {   // unrolled: registers indexed by constants
             constexpr uint32_t b = decltype(bc)::value;
             __builtin_amdgcn_sched_barrier(0);   // one block's operands live at a time
-            if constexpr (b % 2 == 0) __syncthreads();   // the buffers written next are free (previous tile / blocks b-2, b-1)
-            mbx_put(mbx_carve(lt + (b % 2) * MBX_BYTES), xv[b % 3], si < cnt);
-            xv[(b + 2) % 3] = mbx_load(xrow, b + 2 < (uint32_t)NB ? b + 2 : NB - 1);   // clamped, not skipped
-            if constexpr (!UP) w[0].load(ap + b * 144, hp + b * 144, kc);
-            __syncthreads();
+            if constexpr (!UP) {
+                if constexpr (b % 2 == 0) __syncthreads();   // the buffers written next are free (blocks b-2, b-1)
+                mbx_put(mbx_carve(lt + (b % 2) * MBX_BYTES), xv[b % 3], si < cnt);
+                xv[(b + 2) % 3] = mbx_load(xrow, b + 2 < (uint32_t)NB ? b + 2 : NB - 1);   // clamped, not skipped
+                if constexpr (b > 0) w[0].load(ap + b * 144, hp + b * 144, kc);
+                __syncthreads();
+            }
             const MbW<Q4K> &wc = w[UP ? b : 0];
-            const MbX x = mbx_carve(lt + (b % 2) * MBX_BYTES);
+            const MbX x = mbx_carve(lt + (UP ? b : b % 2) * MBX_BYTES);
             wc.put_scales(scl);   // wave-private table
             wave_sync_lds();
             float t[4][8];   // the block's 8 sub-block terms per (row, pair)
@@ -456,7 +480,6 @@ template <class QD, int NBD>
 __global__ void __launch_bounds__(256) k_mb_down_mfma(MoeArgs a, const int32_t *__restrict__ meta, uint32_t P) {
     extern __shared__ __align__(16) uint8_t lds[];
     const uint32_t ntile = (a.hidden + 63) / 64;
-    const uint32_t ntiles = (uint32_t)meta[1] * ntile;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t nb = NBD > 0 ? (uint32_t)NBD : a.ffn / 256;
     const uint64_t rb = (uint64_t)nb * QD::BB;
@@ -471,21 +494,25 @@ __global__ void __launch_bounds__(256) k_mb_down_mfma(MoeArgs a, const int32_t *
     // count (up to 3 blocks: more spills); else one block at a time
     {
         const uint32_t t = blockIdx.x;
-        if (t >= ntiles) return;   // whole workgroup, before any barrier
+        const uint32_t bi = t / ntile, rt = t % ntile;
+        const int32_t *rec = meta + mb_big_off(P) + MB_REC * bi;
+        // independent loads: the entry count, the record, this thread's pair
+        // (slots past the count hold pair 0)
+        const uint32_t nent = (uint32_t)meta[1];
+        const int4 hd = *(const int4 *)rec;
+        const uint32_t sp = (uint32_t)rec[4 + si];
+        if (bi >= nent) return;   // whole workgroup, before any barrier
         uint8_t *const lt = lds;
         float2 *scl = (float2 *)(lt + (UP ? nb : MB_DN_CHUNK) * MBX_BYTES) + 16 * 16 * wave;   // [16 rows][NS] {scale, min}
-        const uint32_t bi = t / ntile, rt = t % ntile;
-        const int32_t *big = meta + mb_big_off(P) + 3 * bi;
-        const int32_t e = big[0];
-        const uint32_t cnt = (uint32_t)big[2];
-        const int32_t *pairs = meta + mb_order_off(P) + big[1];
+        const int32_t e = hd.x;
+        const uint32_t cnt = (uint32_t)hd.z;
+        const int32_t *pairs = rec + 4;
         const bool shared = (uint32_t)e == a.n_expert;
         const uint8_t *db = shared ? a.down_sh : a.down + (uint64_t)e * a.hidden * rb;
         const uint32_t row0 = 64 * rt + 16 * wave;   // this wave's 16 rows
         // rows past hidden read the last row and are not written
         const uint8_t *ap = db + (uint64_t)min(row0 + arow, a.hidden - 1) * rb;
         const uint8_t *hp = db + (uint64_t)min(row0 + (lane >> 2), a.hidden - 1) * rb;
-        const uint32_t sp = (uint32_t)pairs[min(si, cnt - 1)];
         W w[UP ? NBD : 1];
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
@@ -544,6 +571,9 @@ __global__ void __launch_bounds__(256) k_mb_down_mfma(MoeArgs a, const int32_t *
                         acc[i] = fmaf(d8, fmaf(sc.x, (float)d[i], -(sc.y * qs)), acc[i]);
                     }
                 }
+                // the sums formed here: sunk into the store branch below, the
+                // arithmetic kept every block's MFMA results live at once
+                asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
             }
             wave_sync_lds();   // the table is rewritten for the next block
         }
@@ -576,7 +606,7 @@ __global__ void __launch_bounds__(256) k_mb_combine(const float *__restrict__ yp
 // dynamic LDS of the MFMA gate/up kernel (two x tiles, the block scales, the
 // epilogue's sums) and of the MFMA down kernel (up to MB_DN_CHUNK staged h
 // blocks and the scale table)
-static uint32_t mb_lds_gu() { return 2 * MBX_BYTES + 4 * 16 * 8 * 8 + 64 * 16 * 4; }
+static uint32_t mb_lds_gu(uint32_t nb) { return (nb <= 8 ? nb : 2) * MBX_BYTES + 4 * 16 * 8 * 8 + 64 * 16 * 4; }
 static uint32_t mb_lds_dn(uint32_t ffn) {
     const uint32_t nb = ffn / 256;
     return (nb <= 3 ? nb : MB_DN_CHUNK) * MBX_BYTES + 4 * 16 * 16 * 8;
@@ -584,7 +614,7 @@ static uint32_t mb_lds_dn(uint32_t ffn) {
 
 uint32_t moe_batch_lds(uint32_t hidden, uint32_t ffn) {
     uint32_t m = moe_groups_lds(hidden, ffn);
-    m = m > mb_lds_gu() ? m : mb_lds_gu();
+    m = m > mb_lds_gu(hidden / 256) ? m : mb_lds_gu(hidden / 256);
     return m > mb_lds_dn(ffn) ? m : mb_lds_dn(ffn);
 }
 
@@ -635,7 +665,7 @@ hipError_t launch_moe_batch(const MoeArgs &base, uint32_t T, uint32_t min_big, c
     auto grid_for = [&](uint32_t tiles_per_entry) { return dim3(max_big * tiles_per_entry); };
     const uint32_t nblk = base.ffn / 32;
     const uint32_t nb_gu = base.hidden / 256;
-    const uint32_t lds_gu = mb_lds_gu();
+    const uint32_t lds_gu = mb_lds_gu(base.hidden / 256);
     auto go_gu = [&](auto kern) -> hipError_t {
         if (!any_big) return hipSuccess;
         if (lds_gu > 64 * 1024) {
