@@ -1500,6 +1500,9 @@ static hipError_t go_b(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
             nt = (lanes + 63) / 64 * 64;
         }
     }
+    // every pair of a tile has its S lanes (a pair without them would leave
+    // its partial sum unwritten)
+    if (tr * n_slots * S > nt) return hipErrorInvalidValue;
     const LdsB L = lds_b(a.ffn, n_slots, tr);
     if (L.total > moe_layer_lds(a.hidden, a.ffn, n_slots)) return hipErrorInvalidValue;   // the host's bound
     const dim3 grid((a.hidden + tr - 1) / tr);
@@ -1520,13 +1523,17 @@ static uint32_t b_mult(uint32_t nb, uint32_t n_slots) {
     if (QD::IPB * p * n_slots > 256 || ipl > 4 || QD::IPB * p > 64) return 1;
     return p;
 }
+// The switch key of kernel B's unrolled variants, P * 8 + IPL, unique only
+// for IPL <= 4 (P = 1 with 26 blocks would otherwise read as P = 4, IPL = 2);
+// 0 (the runtime block loop) for every other choice.
+static uint32_t b_variant(uint32_t p, uint32_t ipl) { return ipl >= 1 && ipl <= 4 ? p * 8 + ipl : 0; }
 
 template <class QD>
 static hipError_t go_b_any(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
     const uint32_t nb = a.ffn / 256;
     const uint32_t p = b_mult<QD>(nb, n_slots);
-    const uint32_t ipl = (nb + p - 1) / p;
-    switch (p * 8 + ipl) {
+    const uint32_t key = b_variant(p, (nb + p - 1) / p);
+    switch (key) {
         case 1 * 8 + 1: return go_b<QD, 1, 1>(a, n_slots, s);
         case 1 * 8 + 2: return go_b<QD, 2, 1>(a, n_slots, s);
         case 1 * 8 + 3: return go_b<QD, 3, 1>(a, n_slots, s);
@@ -1537,7 +1544,7 @@ static hipError_t go_b_any(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
         default: break;
     }
     if constexpr (QD::IPB * 16 <= 64) {
-        switch (p * 8 + ipl) {
+        switch (key) {
             case 16 * 8 + 2: return go_b<QD, 2, 16>(a, n_slots, s);
             case 16 * 8 + 3: return go_b<QD, 3, 16>(a, n_slots, s);
             case 16 * 8 + 4: return go_b<QD, 4, 16>(a, n_slots, s);
@@ -1700,6 +1707,7 @@ hipError_t launch_moe_groups_gu(const MoeArgs &a, uint32_t max_entries, hipStrea
 template <class QD, int IPL, int P>
 static hipError_t go_b_grp(const MoeArgs &a, uint32_t max_entries, hipStream_t s) {
     const uint32_t tr = b_tile_rows<QD>(P, 1);
+    if (tr * QD::IPB * P > 256) return hipErrorInvalidValue;   // a row's lanes in one workgroup
     const uint32_t lds = GRP_MAX * act_bytes(a.ffn);
     if (lds > 64 * 1024) {
         const hipError_t e = hipFuncSetAttribute((const void *)k_moe_down_grp<QD, IPL, P>,
@@ -1716,8 +1724,8 @@ template <class QD>
 static hipError_t go_b_grp_any(const MoeArgs &a, uint32_t max_entries, hipStream_t s) {
     const uint32_t nb = a.ffn / 256;
     const uint32_t p = b_mult<QD>(nb, 1);
-    const uint32_t ipl = (nb + p - 1) / p;
-    switch (p * 8 + ipl) {
+    const uint32_t key = b_variant(p, (nb + p - 1) / p);
+    switch (key) {
         case 1 * 8 + 1: return go_b_grp<QD, 1, 1>(a, max_entries, s);
         case 1 * 8 + 2: return go_b_grp<QD, 2, 1>(a, max_entries, s);
         case 1 * 8 + 3: return go_b_grp<QD, 3, 1>(a, max_entries, s);
@@ -1728,7 +1736,7 @@ static hipError_t go_b_grp_any(const MoeArgs &a, uint32_t max_entries, hipStream
         default: break;
     }
     if constexpr (QD::IPB * 16 <= 64) {
-        switch (p * 8 + ipl) {
+        switch (key) {
             case 16 * 8 + 2: return go_b_grp<QD, 2, 16>(a, max_entries, s);
             case 16 * 8 + 3: return go_b_grp<QD, 3, 16>(a, max_entries, s);
             case 16 * 8 + 4: return go_b_grp<QD, 4, 16>(a, max_entries, s);

@@ -363,7 +363,9 @@ __global__ void __launch_bounds__(256) k_mb_gu_mfma(MoeArgs a, const int32_t *__
     {
         const uint32_t t = blockIdx.x;
         const uint32_t bi = t / nblk, jb = t % nblk;
-        const int32_t *rec = meta + mb_big_off(P) + MB_REC * bi;
+        // (a grid sized for the most entries a batch could hold has tiles past
+        // the P records: they read the last record and leave)
+        const int32_t *rec = meta + mb_big_off(P) + MB_REC * min(bi, P - 1);
         // independent loads: the entry count, the record, this thread's pair
         // (slots past the count hold pair 0)
         const uint32_t nent = (uint32_t)meta[1];
@@ -495,7 +497,9 @@ __global__ void __launch_bounds__(256) k_mb_down_mfma(MoeArgs a, const int32_t *
     {
         const uint32_t t = blockIdx.x;
         const uint32_t bi = t / ntile, rt = t % ntile;
-        const int32_t *rec = meta + mb_big_off(P) + MB_REC * bi;
+        // (a grid sized for the most entries a batch could hold has tiles past
+        // the P records: they read the last record and leave)
+        const int32_t *rec = meta + mb_big_off(P) + MB_REC * min(bi, P - 1);
         // independent loads: the entry count, the record, this thread's pair
         // (slots past the count hold pair 0)
         const uint32_t nent = (uint32_t)meta[1];

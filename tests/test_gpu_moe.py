@@ -65,6 +65,11 @@ CASES = [
     (4096, 256, 8, 2, False, Q6_K),      # wide hidden: 2 items per lane in gate/up
     (256, 2048, 16, 16, True, Q6_K),     # 17 slots, 8 blocks per down row: kernel B's block loop
     (512, 1536, 32, 8, True, Q4_K),      # 9 slots of Q4_K down, 6 blocks per row: the block loop
+    # the block loop past 25 blocks per row (P = 1 with 26..28 blocks must not
+    # select an unrolled P = 4 variant): the largest layer shape, 17 slots of
+    # 27 blocks, and a Q4_K down of 26 blocks
+    (1024, 6912, 16, 16, True, Q6_K),
+    (512, 6656, 8, 8, False, Q4_K),
 ]
 
 

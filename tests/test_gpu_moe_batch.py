@@ -57,6 +57,7 @@ CASES = [
     (4096, 256, 8, 2, 20, False, Q6_K),      # wide hidden
     (1024, 2304, 8, 2, 12, True, Q6_K),      # 9 down blocks: h staged 8 blocks at a time
     (512, 2304, 4, 2, 9, False, Q4_K),       # the same with a Q4_K down
+    (512, 6656, 8, 2, 12, False, Q4_K),      # Q4_K down of 26 blocks: the grouped down's block loop
 ] + [(2048, 768, 128, k, t, False, Q6_K) for k in (2, 4, 8) for t in (16, 33, 64)]   # the sweep's points
 
 
