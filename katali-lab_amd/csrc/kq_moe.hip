@@ -1482,24 +1482,15 @@ static uint32_t b_tile_rows(uint32_t P, uint32_t n_slots) {
     return tr < 1 ? 1 : tr;
 }
 
-// Kernel B's launch: 256-thread tiles, unless those give between one and
-// two workgroups per CU (some CUs would take two tiles while the rest idle):
-// then the fewest rows per tile that keep one tile per CU, in up to
-// B_MAX_THREADS threads (nine slots at 2048 rows: 293 tiles of 7 rows ->
-// 256 tiles of 8 rows in 320 threads).
+// Kernel B's variant (b_variant's key), tile rows and workgroup size.
+struct BPlan {
+    uint32_t key, tr, nt;
+};
+
+// Kernel B's launch as planned by b_plan (tile rows, workgroup size).
 template <class QD, int IPL, int P>
-static hipError_t go_b(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
-    const uint32_t S = QD::IPB * P;
-    uint32_t tr = b_tile_rows<QD>(P, n_slots), nt = 256;
-    const uint32_t cus = (uint32_t)device_cu_count();
-    const uint32_t ntile = (a.hidden + tr - 1) / tr;
-    if (ntile > cus && ntile < 2 * cus) {
-        const uint32_t tr1 = (a.hidden + cus - 1) / cus, lanes = tr1 * n_slots * S;
-        if (lanes <= B_MAX_THREADS) {
-            tr = tr1;
-            nt = (lanes + 63) / 64 * 64;
-        }
-    }
+static hipError_t go_b(const MoeArgs &a, uint32_t n_slots, const BPlan &pl, hipStream_t s) {
+    const uint32_t S = QD::IPB * P, tr = pl.tr, nt = pl.nt;
     // every pair of a tile has its S lanes (a pair without them would leave
     // its partial sum unwritten)
     if (tr * n_slots * S > nt) return hipErrorInvalidValue;
@@ -1528,30 +1519,59 @@ static uint32_t b_mult(uint32_t nb, uint32_t n_slots) {
 // 0 (the runtime block loop) for every other choice.
 static uint32_t b_variant(uint32_t p, uint32_t ipl) { return ipl >= 1 && ipl <= 4 ? p * 8 + ipl : 0; }
 
+// Kernel B's variant and tiles: 256-thread tiles, unless those give between
+// one and two workgroups per CU (some CUs would take two tiles while the rest
+// idle): then the fewest rows per tile that keep one tile per CU, in up to
+// B_MAX_THREADS threads (nine slots at 2048 rows: 293 tiles of 7 rows -> 256
+// tiles of 8 rows in 320 threads).
 template <class QD>
-static hipError_t go_b_any(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
+static BPlan b_plan(const MoeArgs &a, uint32_t n_slots) {
     const uint32_t nb = a.ffn / 256;
     const uint32_t p = b_mult<QD>(nb, n_slots);
-    const uint32_t key = b_variant(p, (nb + p - 1) / p);
-    switch (key) {
-        case 1 * 8 + 1: return go_b<QD, 1, 1>(a, n_slots, s);
-        case 1 * 8 + 2: return go_b<QD, 2, 1>(a, n_slots, s);
-        case 1 * 8 + 3: return go_b<QD, 3, 1>(a, n_slots, s);
-        case 1 * 8 + 4: return go_b<QD, 4, 1>(a, n_slots, s);
-        case 4 * 8 + 2: return go_b<QD, 2, 4>(a, n_slots, s);
-        case 4 * 8 + 3: return go_b<QD, 3, 4>(a, n_slots, s);
-        case 4 * 8 + 4: return go_b<QD, 4, 4>(a, n_slots, s);
+    BPlan pl;
+    pl.key = b_variant(p, (nb + p - 1) / p);
+    const uint32_t P = pl.key ? p : 1u, S = QD::IPB * P;
+    pl.tr = b_tile_rows<QD>(P, n_slots);
+    pl.nt = 256;
+    const uint32_t cus = (uint32_t)device_cu_count();
+    const uint32_t ntile = (a.hidden + pl.tr - 1) / pl.tr;
+    if (ntile > cus && ntile < 2 * cus) {
+        const uint32_t tr1 = (a.hidden + cus - 1) / cus, lanes = tr1 * n_slots * S;
+        if (lanes <= B_MAX_THREADS) {
+            pl.tr = tr1;
+            pl.nt = (lanes + 63) / 64 * 64;
+        }
+    }
+    return pl;
+}
+static BPlan b_plan_any(const MoeArgs &a, uint32_t n_slots) {
+    return a.down_type == T_Q6_K ? b_plan<Q6K>(a, n_slots) : b_plan<Q4K>(a, n_slots);
+}
+
+template <class QD>
+static hipError_t go_b_any(const MoeArgs &a, uint32_t n_slots, const BPlan &pl, hipStream_t s) {
+    switch (pl.key) {
+        case 1 * 8 + 1: return go_b<QD, 1, 1>(a, n_slots, pl, s);
+        case 1 * 8 + 2: return go_b<QD, 2, 1>(a, n_slots, pl, s);
+        case 1 * 8 + 3: return go_b<QD, 3, 1>(a, n_slots, pl, s);
+        case 1 * 8 + 4: return go_b<QD, 4, 1>(a, n_slots, pl, s);
+        case 4 * 8 + 2: return go_b<QD, 2, 4>(a, n_slots, pl, s);
+        case 4 * 8 + 3: return go_b<QD, 3, 4>(a, n_slots, pl, s);
+        case 4 * 8 + 4: return go_b<QD, 4, 4>(a, n_slots, pl, s);
         default: break;
     }
     if constexpr (QD::IPB * 16 <= 64) {
-        switch (key) {
-            case 16 * 8 + 2: return go_b<QD, 2, 16>(a, n_slots, s);
-            case 16 * 8 + 3: return go_b<QD, 3, 16>(a, n_slots, s);
-            case 16 * 8 + 4: return go_b<QD, 4, 16>(a, n_slots, s);
+        switch (pl.key) {
+            case 16 * 8 + 2: return go_b<QD, 2, 16>(a, n_slots, pl, s);
+            case 16 * 8 + 3: return go_b<QD, 3, 16>(a, n_slots, pl, s);
+            case 16 * 8 + 4: return go_b<QD, 4, 16>(a, n_slots, pl, s);
             default: break;
         }
     }
-    return go_b<QD, 0, 1>(a, n_slots, s);
+    return go_b<QD, 0, 1>(a, n_slots, pl, s);
+}
+static hipError_t go_b_run(const MoeArgs &a, uint32_t n_slots, const BPlan &pl, hipStream_t s) {
+    return a.down_type == T_Q6_K ? go_b_any<Q6K>(a, n_slots, pl, s) : go_b_any<Q4K>(a, n_slots, pl, s);
 }
 
 // Kernel B's tile holds tr * n_slots <= B_MAX_THREADS partial sums: tr =
@@ -1623,7 +1643,7 @@ hipError_t launch_moe(const MoeArgs &a, hipStream_t s, bool allow_fused, bool *f
     }
     const hipError_t e = go_a_any(a, n_slots, s);
     if (e != hipSuccess) return e;
-    return a.down_type == T_Q6_K ? go_b_any<Q6K>(a, n_slots, s) : go_b_any<Q4K>(a, n_slots, s);
+    return go_b_run(a, n_slots, b_plan_any(a, n_slots), s);
 }
 
 static hipError_t go_a_any(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
@@ -1662,7 +1682,7 @@ hipError_t launch_moe_normed(MoeArgs a, float *xn_buf, float *logits_buf, hipStr
         if (e != hipSuccess) return e;
         if (merged) *merged = true;
         // kernel B advances the exchange generation (a.router set)
-        return a.down_type == T_Q6_K ? go_b_any<Q6K>(a, n_slots, s) : go_b_any<Q4K>(a, n_slots, s);
+        return go_b_run(a, n_slots, b_plan_any(a, n_slots), s);
     }
     // the router rows do not spread over kernel A: the steps before the
     // layer in their own launch, then the layer from their outputs

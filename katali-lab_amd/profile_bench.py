@@ -186,10 +186,11 @@ def main():
     os.makedirs(os.path.dirname(md), exist_ok=True)
     with open(md, "w") as f:
         f.write(f"# rocprofv3 summary: {wl}\n\n")
+        flags = (" --fused" if args.fused else "") + (" --one-stream" if args.one_stream else "")
+        env = "".join(f", {k}={v}" for k, v in extra_env.items())
         f.write(f"Made by `python katali-lab_amd/profile_bench.py --workload {wl} --steps {args.steps} "
-                f"--warmup {args.warmup} --out <out>{' --fused' if args.fused else ''}`, which runs (from /tmp, "
-                f"TMPDIR=/tmp{', KATALI_HIP_FUSED=1' if args.fused else ''}; paths relative to the "
-                f"repository root):\n\n")
+                f"--warmup {args.warmup} --out <out>{flags}`, which runs (from /tmp, "
+                f"TMPDIR=/tmp{env}; paths relative to the repository root):\n\n")
         for k, c in cmds.items():
             txt = " ".join(c).replace(out, "<out>").replace(REPO + "/", "").replace(sys.executable, "python3")
             f.write(f"- {k}: `{txt}`\n")
