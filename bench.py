@@ -90,6 +90,22 @@ TOKEN_WORKLOADS = {
 }
 
 
+def xcd_layer(hip, hidden, ffn, n_expert, n_slots):
+    """Whether the library runs this layer shape as the XCD-sliced one-launch
+    layer (k_moe_xcd) rather than kernels A and B: the rule launch_moe
+    applies (eight slots, hidden 1024 or 2048, ffn <= 1024, <= 256 experts,
+    a 256-CU device, KATALI_HIP_XCD not 0)."""
+    if os.environ.get("KATALI_HIP_XCD", "1")[:1] in ("0", "n", "N"):
+        return False
+    return (n_slots == 8 and hidden in (1024, 2048) and ffn <= 1024 and n_expert <= 256
+            and " 256 CUs" in hip.status())
+
+
+def layer_kernels(hip, hidden, ffn, n_expert, n_slots):
+    return ("k_moe_xcd (one launch per layer)" if xcd_layer(hip, hidden, ffn, n_expert, n_slots)
+            else "k_moe_gu + k_moe_down (two launches per layer)")
+
+
 def moe_bytes_per_layer(hidden, ffn, n_sel, shared):
     per_expert = 2 * ffn * row_bytes(Q4_K, hidden) + hidden * row_bytes(Q6_K, ffn)
     slots = n_sel + (1 if shared else 0)
@@ -988,7 +1004,7 @@ def main():
             "shared_expert": shared, "expert_pool_gb": round(res["pool_gb"], 2),
             "bytes_per_token": res["bytes_per_token"], "parallelism": "single GPU",
         }
-        kernel = "MoE layer: k_moe_gu + k_moe_down (two launches per layer)"
+        kernel = "MoE layer: " + layer_kernels(hip, hidden, ffn, n_expert, n_sel + (1 if shared else 0))
         extra = {"tok_s": round(res["tok_s"], 2),
                  "eager_layer_ms_mean": round(res["kernel_ms_mean"], 5)}
     elif args.workload in TOKEN_WORKLOADS:
@@ -1031,7 +1047,8 @@ def main():
             "layers": L, "hidden": hidden, "ffn": ffn, "n_expert": n_expert, "n_sel": n_sel,
             "parallelism": "single GPU",
         }
-        kernel = "MoE layer at the duty cycle: k_moe_gu + k_moe_down, event-timed per layer"
+        kernel = "MoE layer at the duty cycle: " + layer_kernels(hip, hidden, ffn, n_expert, n_sel) + \
+            ", event-timed per layer"
         extra = {"duty_points": res["points"],
                  "back_to_back_gpu_us_per_layer": round(res["back_to_back_unit_ms"] * 1e3, 3)}
     elif args.workload == "moebatch":

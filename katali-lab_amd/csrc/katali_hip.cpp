@@ -79,6 +79,10 @@ bool env_on(const char *name) {
     const char *e = getenv(name);
     return e && (e[0] == '1' || e[0] == 'y' || e[0] == 'Y');
 }
+bool env_off(const char *name) {
+    const char *e = getenv(name);
+    return e && (e[0] == '0' || e[0] == 'n' || e[0] == 'N');
+}
 
 int init_locked() {
     if (g_inited) return g_usable ? KATALI_HIP_OK : KATALI_HIP_E_NODEVICE;
@@ -279,10 +283,15 @@ int moe_impl(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, 
     a.dbg_gu = gu_dbg;
     a.err = g_err_dev;
     a.fsync = g_fsync;
-    // the one-launch layer is opt-in: measured slower than kernels A and B
-    // on MI355X (its in-kernel h exchange costs more than the launch it saves)
+    // Eight slots take the XCD-sliced layer (one launch, every CU streaming
+    // both phases; 12.0 us per layer at the 2048/768 top-8 shape against
+    // 13.7 for kernels A and B); KATALI_HIP_XCD=0 keeps kernels A and B. The
+    // other one-launch layer is opt-in (KATALI_HIP_FUSED=1): measured slower
+    // than kernels A and B (its all-slots h exchange costs more than the
+    // launch it saves).
     const bool allow_fused = env_on("KATALI_HIP_FUSED");
-    rc = launched(kq::launch_moe(a, g_stream, allow_fused), "moe launch");
+    const bool allow_xcd = !env_off("KATALI_HIP_XCD");
+    rc = launched(kq::launch_moe(a, g_stream, allow_fused, nullptr, allow_xcd), "moe launch");
     if (rc) return rc;
     if (hq8_dbg) {
         hipError_t e = hipMemcpyAsync(hq8_dbg, g_hq8, hq8_bytes, hipMemcpyDeviceToDevice, g_stream);

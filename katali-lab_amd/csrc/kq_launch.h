@@ -132,7 +132,11 @@ uint32_t moe_batch_lds(uint32_t hidden, uint32_t ffn);
 constexpr uint32_t LDS_PER_WG = 160 * 1024;
 // The layer in one launch when the shape fits the fused kernel and a.fsync is
 // set (and `allow_fused`), else kernels A and B. *fused tells which ran.
-hipError_t launch_moe(const MoeArgs &a, hipStream_t s, bool allow_fused = false, bool *fused = nullptr);
+// allow_xcd: the XCD-sliced one-launch layer where the shape fits it
+// (eight slots, hidden 1024 or 2048, ffn <= 1024, a 256-CU device), tried
+// before the fused one.
+hipError_t launch_moe(const MoeArgs &a, hipStream_t s, bool allow_fused = false, bool *fused = nullptr,
+                      bool allow_xcd = false);
 // The in-kernel exchanges (zeroed once, before first use): [0] the fused
 // layer's generation, [1] the normed layer's; from FSYNC_H one block per
 // workgroup of the fused layer of 9 8-byte words {dword, generation} (its
@@ -140,11 +144,23 @@ hipError_t launch_moe(const MoeArgs &a, hipStream_t s, bool allow_fused = false,
 // 8-byte word {logit, generation} per router row of the normed layer (its
 // workgroups read the copy of their index mod FSYNC_REP, so no few cache
 // lines take every poll).
+// From FSYNC_X, the XCD-sliced layer's (launch_moe with allow_xcd): one
+// generation word per workgroup (XCD_G of them), then from FSYNC_XH its h
+// values [slot][ffn <= 1024], then from FSYNC_XP its unweighted down
+// partials [slot][hidden], each value one 8-byte word {float, generation}. Each exchange has its own generations, so no
+// word one of them writes can pass for another's.
 constexpr uint32_t FSYNC_H = 64;
 constexpr uint32_t FUSED_MAX_G = 256;   // workgroups of the fused layer
 constexpr uint32_t FSYNC_R = 8192;      // 32 KiB in, past the fused layer's words
 constexpr uint32_t FSYNC_REP = 16;
-constexpr uint32_t fsync_words() { return FSYNC_R + FSYNC_REP * 2 * 512; }
+constexpr uint32_t XCD_SLOTS = 8;       // the XCD-sliced layer: slot x on XCD x
+constexpr uint32_t XCD_G = 256;         // its workgroups: one per CU, 32 per XCD
+constexpr uint32_t XCD_MAX_HIDDEN = 2048;
+constexpr uint32_t FSYNC_X = FSYNC_R + FSYNC_REP * 2 * 512;
+constexpr uint32_t FSYNC_XH = FSYNC_X + XCD_G;
+constexpr uint32_t XCD_MAX_FFN = 1024;
+constexpr uint32_t FSYNC_XP = FSYNC_XH + 2 * XCD_SLOTS * XCD_MAX_FFN;
+constexpr uint32_t fsync_words() { return FSYNC_XP + 2 * XCD_SLOTS * XCD_MAX_HIDDEN; }
 static_assert(FSYNC_H + 2 * 9 * FUSED_MAX_G <= FSYNC_R, "exchange areas overlap");
 // The steps before the layer and the layer in two launches (MoeArgs' n*
 // fields and router set, n_sel >= 1, hidden <= 4096): kernel A forms the

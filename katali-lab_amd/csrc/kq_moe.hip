@@ -575,8 +575,9 @@ struct NoMore {
 };
 template <int NB, int C, bool FUSED, class After = NoMore, bool NORMED = false>
 __device__ __forceinline__ void gu_unit(const MoeArgs &a, uint32_t unit, uint8_t *lds, GuRoute &rt, uint32_t flag,
-                                        After after = After()) {
+                                        uint32_t *hx = nullptr, After after = After()) {
     // FUSED: flag is this call's generation; h's words are tagged flag + 1
+    // and go to hx + 2 * (9 * unit + k), k < 9.
     constexpr int RW = a1_rw<NB>();
     constexpr int NT = a1_threads<NB>();
     constexpr int ITEMS = 8 * NB;              // lane items per row
@@ -785,8 +786,7 @@ __device__ __forceinline__ void gu_unit(const MoeArgs &a, uint32_t unit, uint8_t
             uint32_t g = flag;   // the generation: made opaque here so no earlier use waits for its load
             asm volatile("" : "+v"(g));
             if (lane < 9)
-                st_dev2(a.fsync + FSYNC_H + 2 * (9 * blockIdx.x + lane),
-                        ((uint64_t)(g + 1) << 32) | ((const uint32_t *)stage)[lane]);
+                st_dev2(hx + 2 * (9 * unit + lane), ((uint64_t)(g + 1) << 32) | ((const uint32_t *)stage)[lane]);
         }
     }
     if (a.dbg_gu && tid < 64) {
@@ -1267,7 +1267,7 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_fused(MoeArgs a, uint3
     };
     GuRoute rt;
     if (w < U) {
-        gu_unit<NB, C, true>(a, w, lds, rt, gen, load_down);
+        gu_unit<NB, C, true>(a, w, lds, rt, gen, a.fsync + FSYNC_H, load_down);
     } else {
         float lv[C];
         route_issue<C>(a, lv, rt);
@@ -1457,6 +1457,419 @@ static hipError_t launch_moe_fused(const MoeArgs &a, uint32_t n_slots, hipStream
     return nb == 8 ? go_fused_c<8>(a, n_slots, tr, G, S, ipl, s) : go_fused_c<4>(a, n_slots, tr, G, S, ipl, s);
 }
 
+// ---------------------------------------------------------------------------
+// The XCD-sliced one-launch layer (k_moe_xcd): eight slots, XCD_G = 256
+// workgroups, one per CU. Workgroup b serves slot x = b % 8 only; the
+// dispatcher deals workgroups to the eight XCDs round robin, so slot x's
+// workgroups run on XCD x (only the exchange's latency depends on that; the
+// words are device-coherent either way). A CU streams at most ~25 GB/s, so
+// every CU takes an equal share of both phases. With li = b / 8:
+//   1. every wave routes; waves 0 .. R/4 - 1 issue the loads of the slot's
+//      gate and up rows IW * li .. IW * li + IW - 1 (IW = ffn / 32, R = 2 IW
+//      rows, 4 per wave) and decode, stage x and dot them as kernel A does;
+//      then every wave issues its share of the slot's down rows [li * TRX,
+//      (li + 1) * TRX), TRX = hidden / 32 (behind the gate/up loads in the
+//      CU's queue, so the gate/up data comes first);
+//   2. wave 0 forms the IW values of h = SiLU(g) * u (fp32, kernel A's
+//      arithmetic) and publishes each as one tagged word;
+//   3. the last four waves poll slot x's ffn words, quantize them to q8_1
+//      in LDS (kernel A's quantizer, so the blocks are kernel A's bits;
+//      workgroup li = 0 also writes them to a.hq8), and the down rows are
+//      dotted: 16 lanes per row, lane s takes item s % IPB of blocks s / IPB
+//      + P * i; each row's unweighted partial goes out as one tagged word;
+//   4. wave 0 polls the eight slots' partials of rows li * TRX + x * TRC +
+//      [0, TRC), TRC = TRX / 8, and writes y there: one fmaf per slot in
+//      rank order, kernel B's sum.
+// Generations: each workgroup reads its own word at its start (issued
+// first, used last) and advances it at its end. Every workgroup runs every
+// call, so the words stay equal and a call's tag is that value + 1; every
+// word a call reads is written in that call, and stale words carry older
+// tags. Nothing is cleared between calls or graph replays. Every wait is
+// bounded (FSYNC_SPIN_LIMIT polls, then error bit 4 and the call's outputs
+// are void).
+// ---------------------------------------------------------------------------
+constexpr uint32_t XCD_POLL_WAVES = 4;   // waves that poll the slot's h
+constexpr int XCD_HW = 4;                // h words per polling thread: ffn <= 4 * 256
+
+// One workgroup's gate/up part: rows v < R of slot `slot` (v < IW: gate row
+// IW * li + v, else up row IW * li + v - IW), kernel A's item mapping, scale
+// records, term order and reductions (so every value is kernel A's), on
+// waves 0 .. R/4 - 1; the others stage x with them. `down` issues the
+// caller's down loads (after the wave's dots, or once x is staged on waves
+// without rows). Leaves gate/up values in LDS at lds + lds_a(..).gu.
+template <int NB, int C, int IW, class Down>
+__device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_t li, uint8_t *lds, GuRoute &rt,
+                                        Down down) {
+    constexpr int RW = 4;                      // rows per wave (kernel A's at these widths)
+    static_assert(a1_rw<NB>() == RW, "gu_part: kernel A's 4-row waves");
+    constexpr int R = 2 * IW, GW = R / RW;     // rows, waves with rows
+    constexpr int NT = a1_threads<NB>();
+    constexpr int ITEMS = 8 * NB;
+    constexpr int LPG = RW * ITEMS / 64;       // chunks per lane (one group: LPG <= 16)
+    constexpr int M = ITEMS >= 64 ? ITEMS / 64 : 1;
+    constexpr int WH = RW * NB;
+    constexpr int HPL = (WH + 63) / 64;
+    static_assert(R % RW == 0 && GW <= NT / 64 && LPG <= 16, "gu_part shape");
+    const LdsA L = lds_a(a.hidden, NB);
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool rows = wave < (uint32_t)GW;
+    pin_args(a.gate, a.up, a.gate_sh, a.up_sh);
+
+    constexpr int XTASKS = 64 * NB;
+    constexpr int XPT = (XTASKS + NT - 1) / NT;
+    float4 xv[XPT];
+    uint32_t xqv[XPT], xdv[XPT];
+    {
+        float lv[C];
+        route_issue<C>(a, lv, rt);
+        if (a.xq == nullptr) {
+#pragma unroll
+            for (int i = 0; i < XPT; i++) xv[i] = *(const float4 *)(a.x + 4 * min(tid + NT * i, (uint32_t)XTASKS - 1));
+        } else {
+#pragma unroll
+            for (int i = 0; i < XPT; i++) {
+                const uint32_t t = min(tid + NT * i, (uint32_t)XTASKS - 1);
+                const uint8_t *b = a.xq + (t >> 3) * 36;
+                xqv[i] = *(const uint32_t *)(b + 4 + 4 * (t & 7));
+                xdv[i] = ld_u16(b);
+            }
+        }
+        route_finish<C>(a, lv, rt);
+    }
+    __builtin_amdgcn_s_waitcnt(VMCNT0);
+
+    const uint64_t rb = NB * 144;
+    const uint8_t *gb, *ub;
+    if ((int)slot < a.n_sel) {
+        int32_t id = __builtin_amdgcn_readlane(rt.eid, (int)slot);
+        if ((uint32_t)id >= a.n_expert) id = 0;   // bad explicit id: reported by route_publish
+        gb = a.gate + (uint64_t)id * a.ffn * rb;
+        ub = a.up + (uint64_t)id * a.ffn * rb;
+    } else {
+        gb = a.gate_sh;
+        ub = a.up_sh;
+    }
+    auto row_ptr = [&](uint32_t v) -> const uint8_t * {   // v < R (clamped for waves without rows)
+        v = min(v, (uint32_t)R - 1);
+        return v < (uint32_t)IW ? gb + (uint64_t)(IW * li + v) * rb : ub + (uint64_t)(IW * li + v - IW) * rb;
+    };
+    auto chunk = [&](int k) -> const uint8_t * {
+        uint32_t r, it;
+        if constexpr (ITEMS >= 64) {
+            r = k / M;
+            it = 64 * (k % M) + lane;
+        } else {
+            r = lane / ITEMS + k * (64 / ITEMS);
+            it = lane % ITEMS;
+        }
+        return row_ptr(RW * wave + r) + (it / 8) * 144 + 16 + 16 * (it % 8);
+    };
+
+    uint4 hv[HPL];
+    uint4 q[LPG];
+    if (rows) {   // whole waves
+#pragma unroll
+        for (int i = 0; i < HPL; i++) {
+            const uint32_t h = min(lane + 64 * i, (uint32_t)WH - 1);
+            hv[i] = ld16(row_ptr(RW * wave + h / NB) + (h % NB) * 144);
+        }
+#pragma unroll
+        for (int k = 0; k < LPG; k++) q[k] = ld16(chunk(k));
+    }
+    if (slot == 0 && li == 0 && wave == 0)
+        route_publish(a, rt.eid, a.logits && a.n_sel > 0 ? route_weight(rt.logit, a.n_sel) : rt.w);
+
+    // x -> q8_1 in LDS while the weights stream in
+    const Act xa = act_carve(lds + L.xact, a.hidden);
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+        const uint32_t t = tid + NT * i, blk = t >> 3, part = t & 7;
+        if (t >= (uint32_t)XTASKS) break;   // whole 8-lane groups leave together
+        uint32_t qv;
+        int lo, hi;
+        float dd;
+        if (a.xq) {
+            qv = xqv[i];
+            q8_part_sums(qv, lo, hi);
+            dd = h2f(xdv[i]);
+        } else {
+            uint32_t d16, s16;
+            qv = quant_q8_1_part(xv[i], d16, s16, lo, hi, dd);
+        }
+        *(uint32_t *)(xa.qs + 32 * blk + 4 * part) = qv;
+        if (part == 0) {
+            xa.d8[blk] = dd;
+            xa.qs16[2 * blk] = lo;
+            xa.qs16[2 * blk + 1] = hi;
+        }
+    }
+    __syncthreads();
+
+    float *gu = (float *)(lds + L.gu);
+    if (rows) {
+        XSlice xs[M];
+#pragma unroll
+        for (int m = 0; m < M; m++) xs[m] = x_slice(xa, ITEMS >= 64 ? 64 * m + lane : lane % ITEMS);
+        float4 *scl = (float4 *)(lds + L.scl) + 4 * WH * wave;
+#pragma unroll
+        for (int i = 0; i < HPL; i++) {
+            const uint32_t h = lane + 64 * i;
+            if (h < WH) {
+                Q4K::Raw raw;
+                raw.h = hv[i];
+                const uint32_t b = h % NB;
+                const float4 dA = *(const float4 *)(xa.d8 + 8 * b), dB = *(const float4 *)(xa.d8 + 8 * b + 4);
+                const float d8[8] = {dA.x, dA.y, dA.z, dA.w, dB.x, dB.y, dB.z, dB.w};
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    float ds0, ds1, dm0, dm1;
+                    Q4K::scales(raw, g, ds0, ds1, dm0, dm1);
+                    scl[4 * h + g] = make_float4(ds0 * d8[2 * g], ds1 * d8[2 * g + 1], dm0 * d8[2 * g], dm1 * d8[2 * g + 1]);
+                }
+            }
+        }
+        wave_sync_lds();
+        if constexpr (ITEMS >= 64) {
+            float acc[LPG];
+#pragma unroll
+            for (int k = 0; k < LPG; k++) {
+                const uint32_t it = 64 * (k % M) + lane;
+                const uint32_t row = k / M;
+                const float4 sc = scl[4 * (row * NB + it / 8) + (it % 8) / 2];
+                acc[k] = q4k_term(q[k], sc, xs[k % M]);
+            }
+            const float v = pw_rows<LPG, M>(acc);
+            if (lane < (uint32_t)RW) gu[RW * wave + pw_rows_row<LPG, M>(lane)] = v;
+        } else {
+            const uint32_t it = lane % ITEMS;
+#pragma unroll
+            for (int k = 0; k < LPG; k++) {
+                const uint32_t row = lane / ITEMS + k * (64 / ITEMS);
+                const float4 sc = scl[4 * (row * NB + it / 8) + (it % 8) / 2];
+                const float v = group_sum<ITEMS>(q4k_term(q[k], sc, xs[0]));
+                if (it == 0) gu[RW * wave + row] = v;
+            }
+        }
+    }
+    down();   // behind this wave's gate/up loads in the CU's queue
+    __syncthreads();
+    if (a.dbg_gu && tid < (uint32_t)R) {
+        float *d = a.dbg_gu + (uint64_t)slot * 2 * a.ffn + (tid < (uint32_t)IW ? 0 : a.ffn) + IW * li + tid % IW;
+        *d = gu[tid];
+    }
+}
+
+template <int NB, int C, class QD, int S, int IPL, int IW>
+__global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
+    constexpr uint32_t NT = a1_threads<NB>();
+    constexpr uint32_t P = S / QD::IPB;
+    constexpr uint32_t H = 256 * NB;
+    constexpr uint32_t F = 32 * IW;               // ffn
+    constexpr uint32_t PER = XCD_G / XCD_SLOTS;   // workgroups per slot
+    constexpr uint32_t TRX = H / PER;             // down rows per workgroup
+    constexpr uint32_t TRC = TRX / XCD_SLOTS;     // rows each workgroup sums
+    constexpr uint32_t NBK = F / 256;             // blocks per down row
+    static_assert(S * TRX <= NT && TRC >= 1 && XCD_SLOTS * TRC <= 64, "XCD layer tile");
+    static_assert(F <= XCD_HW * 64 * XCD_POLL_WAVES && F % 256 == 0, "XCD layer ffn");
+    extern __shared__ __align__(16) uint8_t lds[];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t b = blockIdx.x, xs = b % XCD_SLOTS, li = b / XCD_SLOTS;
+    pin_args(a.down, a.down_sh, a.y, a.fsync, a.hq8);
+    uint32_t *gw = a.fsync + FSYNC_X + b;
+    const uint32_t gen = ld_dev(gw);   // issued first, used last
+
+    // the down share: row r = tid / S of the tile, lane s = tid % S
+    const uint32_t s = tid % S, r = tid / S;
+    const uint32_t item = s % QD::IPB, bs = s / QD::IPB;
+    const uint32_t row0 = li * TRX, rr = min(r, TRX - 1);   // idle threads load a real row and drop it
+    constexpr uint64_t rbd = (uint64_t)NBK * QD::BB;
+    typename QD::Raw raw[IPL];
+    GuRoute rt;
+    auto load_down = [&]() {
+        int32_t sid = __builtin_amdgcn_readlane(rt.eid, (int)xs);
+        if ((uint32_t)sid >= a.n_expert) sid = 0;   // bad explicit id: reported by route_publish
+        const uint8_t *rp = ((int)xs < a.n_sel ? a.down + (uint64_t)sid * H * rbd : a.down_sh) +
+                            (uint64_t)(row0 + rr) * rbd;
+#pragma unroll
+        for (int i = 0; i < IPL; i++) raw[i] = QD::load(rp + min(bs + P * i, NBK - 1) * QD::BB, (int)item);
+    };
+    gu_part<NB, C, IW>(a, xs, li, lds, rt, load_down);
+
+    uint32_t tag = gen;
+    asm volatile("" : "+v"(tag));
+    tag += 1;
+    uint32_t *hx = a.fsync + FSYNC_XH + 2 * F * xs;   // slot xs's h words
+    if (wave == 0 && lane < IW) {
+        const float *gu = (const float *)(lds + lds_a(a.hidden, NB).gu);
+        const float h = kq_silu_mul(gu[lane], gu[IW + lane]);
+        st_dev2(hx + 2 * (IW * li + lane), ((uint64_t)tag << 32) | __float_as_uint(h));
+    }
+
+    // 3. slot xs's h: word t of thread pt is h[pt + 256 t]; quantized where
+    //    32 lanes hold one 32-value block (kernel A's quantizer)
+    uint32_t spins = 0;
+    const uint32_t first_poller = NT - 64 * XCD_POLL_WAVES;
+    const bool poller = tid >= first_poller;   // whole waves
+    const Act act = act_carve(lds + lds_a(a.hidden, NB).total, F);
+    if (poller) {
+        const uint32_t pt = tid - first_poller;
+        constexpr int NW = (F + 64 * XCD_POLL_WAVES - 1) / (64 * XCD_POLL_WAVES);
+        // two rounds in flight: the next round goes out before the previous
+        // one is checked, so a word is sampled twice per round trip
+        uint64_t hv[NW], va[NW], vb[NW];
+        auto issue = [&](uint64_t *o) {
+#pragma unroll
+            for (int i = 0; i < NW; i++) o[i] = ld_dev2(hx + 2 * min(pt + 64 * XCD_POLL_WAVES * i, F - 1));
+        };
+        auto seen = [&](const uint64_t *o) {
+            bool ok = true;
+#pragma unroll
+            for (int i = 0; i < NW; i++) ok &= (uint32_t)(o[i] >> 32) == tag;
+            return __all(ok);
+        };
+        auto take = [&](const uint64_t *o) {
+#pragma unroll
+            for (int i = 0; i < NW; i++) hv[i] = o[i];
+        };
+        issue(va);
+        for (;;) {
+            issue(vb);
+            if (seen(va)) {
+                take(va);
+                break;
+            }
+            issue(va);
+            if (seen(vb)) {
+                take(vb);
+                break;
+            }
+            if (++spins >= FSYNC_SPIN_LIMIT / 2) {
+                if (lane == 0) atomicOr(a.err, 4);
+                take(vb);
+                break;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NW; i++) {
+            const uint32_t e = pt + 64 * XCD_POLL_WAVES * i;   // h index; its 32-lane half is one block
+            if (e < F) {   // whole 32-lane halves (F % 256 == 0)
+                const float h = __uint_as_float((uint32_t)hv[i]);
+                const float am = max32(fabsf(h));
+                const float d = am / 127.0f;
+                const float id = d != 0.0f ? 1.0f / d : 0.0f;
+                const int qv = (int)roundf(h * id);
+                const int total = sum32(qv);
+                int s16 = qv;   // the 16-value half-block sum: a 16-lane row of DPP
+                s16 += dpp_i<DPP_XOR1>(s16);
+                s16 += dpp_i<DPP_XOR2>(s16);
+                s16 += dpp_i<DPP_HALF_MIRROR>(s16);
+                s16 += dpp_i<DPP_MIRROR>(s16);
+                const uint32_t kb = e / 32, j = e % 32;
+                const uint32_t d16 = f2h_rne(d);
+                act.qs[e] = (int8_t)qv;
+                if (j == 0) act.d8[kb] = h2f(d16);
+                if ((j & 15) == 0) act.qs16[2 * kb + j / 16] = s16;
+                if (li == 0) {   // the q8_1 blocks of h, as kernel A writes them
+                    uint8_t *blk = a.hq8 + ((uint64_t)xs * (F / 32) + kb) * 36;
+                    blk[4 + j] = (uint8_t)(qv & 255);
+                    if (j == 0) *(uint32_t *)blk = d16 | (f2h_rne((float)total * d) << 16);
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // the tile's unweighted down partials
+    float x = 0.0f;
+#pragma unroll
+    for (int i = 0; i < IPL; i++) {
+        const uint32_t blk = bs + P * i;
+        const float d = QD::dot_q8(raw[i], (int)item, act, min(blk, NBK - 1));
+        x += blk < NBK ? d : 0.0f;
+    }
+    x = group_sum<S>(x);
+    if (r < TRX && s == 0)
+        st_dev2(a.fsync + FSYNC_XP + 2 * (xs * H + row0 + r), ((uint64_t)tag << 32) | __float_as_uint(x));
+
+    // 4. wave 0: rows row0 + xs * TRC + c (c < TRC) over the eight slots
+    if (wave == 0) {
+        float rw = a.logits && a.n_sel > 0 ? route_weight(rt.logit, a.n_sel) : rt.w;
+        rw = (int)lane < a.n_sel ? rw : ((int)lane == a.n_sel && a.has_shared ? 1.0f : 0.0f);
+        if (lane == 0) st_dev(gw, tag);   // gen was read at the start: advance it now
+        const uint32_t q = lane / TRC, c = lane % TRC;   // lane: slot q, row c
+        uint32_t *pw = a.fsync + FSYNC_XP + 2 * (min(q, XCD_SLOTS - 1) * H + row0 + xs * TRC + c);
+        auto ok = [&](uint64_t v) { return __all(lane >= XCD_SLOTS * TRC || (uint32_t)(v >> 32) == tag); };
+        uint64_t pv, pa = ld_dev2(pw), pb;
+        for (;;) {   // two rounds in flight, as above
+            pb = ld_dev2(pw);
+            if (ok(pa)) {
+                pv = pa;
+                break;
+            }
+            pa = ld_dev2(pw);
+            if (ok(pb)) {
+                pv = pb;
+                break;
+            }
+            if (++spins >= FSYNC_SPIN_LIMIT / 2) {
+                if (lane == 0) atomicOr(a.err, 4);
+                pv = pb;
+                break;
+            }
+        }
+        const float v = __uint_as_float((uint32_t)pv);
+        float y = 0.0f;
+#pragma unroll
+        for (uint32_t k = 0; k < XCD_SLOTS; k++) {   // rank order, one fmaf per slot
+            const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rw), (int)k));
+            y = fmaf(w, __shfl(v, (int)(k * TRC + c), WAVE), y);
+        }
+        if (lane < TRC) a.y[row0 + xs * TRC + lane] = y;
+    }
+}
+
+template <int NB, int C, class QD, int S, int IPL, int IW>
+static hipError_t go_xcd(const MoeArgs &a, hipStream_t s) {
+    const uint32_t lds = lds_a(a.hidden, NB).total + act_bytes(32 * IW);
+    if (lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute((const void *)k_moe_xcd<NB, C, QD, S, IPL, IW>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL((k_moe_xcd<NB, C, QD, S, IPL, IW>), dim3(XCD_G), dim3(a1_threads<NB>()), lds, s, a);
+    return hipGetLastError();
+}
+// 16 lanes per down row: Q6_K 4 items x 4 block slots (ffn <= 1024: one
+// block per lane), Q4_K 8 items x 2 block slots (up to two)
+template <int NB, int C, int IW>
+static hipError_t go_xcd_q(const MoeArgs &a, hipStream_t s) {
+    if (a.down_type == T_Q6_K) return go_xcd<NB, C, Q6K, 16, 1, IW>(a, s);
+    if constexpr (IW <= 16) return go_xcd<NB, C, Q4K, 16, 1, IW>(a, s);
+    else return go_xcd<NB, C, Q4K, 16, 2, IW>(a, s);
+}
+template <int NB, int C>
+static hipError_t go_xcd_f(const MoeArgs &a, hipStream_t s) {
+    switch (a.ffn) {
+        case 256: return go_xcd_q<NB, C, 8>(a, s);
+        case 512: return go_xcd_q<NB, C, 16>(a, s);
+        case 768: return go_xcd_q<NB, C, 24>(a, s);
+        case 1024: return go_xcd_q<NB, C, 32>(a, s);
+        default: return hipErrorNotSupported;
+    }
+}
+template <int NB>
+static hipError_t go_xcd_c(const MoeArgs &a, hipStream_t s) {
+    return a.n_expert <= 128 ? go_xcd_f<NB, 2>(a, s) : go_xcd_f<NB, 4>(a, s);
+}
+// hipErrorNotSupported when the shape does not fit the XCD-sliced layer
+static hipError_t launch_moe_xcd(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
+    const uint32_t nb = a.hidden / 256;
+    if (!a.fsync || n_slots != XCD_SLOTS || a.n_sel < 1 || !(nb == 4 || nb == 8) || a.n_expert > 256 ||
+        a.ffn > 1024 || device_cu_count() != (int)XCD_G)
+        return hipErrorNotSupported;
+    return nb == 8 ? go_xcd_c<8>(a, s) : go_xcd_c<4>(a, s);
+}
+
 uint64_t moe_route_words() { return 2 * MAX_SLOTS; }
 
 template <int NB, bool NORMED = false>
@@ -1630,10 +2043,17 @@ hipError_t launch_route_batch(const float *logits, uint32_t n_tokens, uint32_t n
     return hipGetLastError();
 }
 
-hipError_t launch_moe(const MoeArgs &a, hipStream_t s, bool allow_fused, bool *fused) {
+hipError_t launch_moe(const MoeArgs &a, hipStream_t s, bool allow_fused, bool *fused, bool allow_xcd) {
     if (a.n_expert > MAX_EXPERT || a.n_sel > MAX_SEL) return hipErrorInvalidValue;
     const uint32_t n_slots = (uint32_t)a.n_sel + (a.has_shared ? 1u : 0u);
     if (fused) *fused = false;
+    if (allow_xcd) {
+        const hipError_t f = launch_moe_xcd(a, n_slots, s);
+        if (f != hipErrorNotSupported) {
+            if (fused) *fused = f == hipSuccess;
+            return f;
+        }
+    }
     if (allow_fused && a.n_sel > 0) {
         const hipError_t f = launch_moe_fused(a, n_slots, s);
         if (f != hipErrorNotSupported) {

@@ -28,12 +28,11 @@ REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 COPY_MIB = 256
 # kernels summed per workload unit; the first is launched once per unit
 KERNELS = {
-    "moe48": ("k_moe_gu", "k_moe_down"),
+    "moe48": ("k_moe_xcd",),
     "moe40cold": ("k_moe_gu", "k_moe_down"),
     "gemv6144": ("k_gemv",),
     "qwen8b": ("k_moe_down", "k_moe_gu", "k_gemv_multi", "k_gemv"),
-    "moe48tok": ("k_argmax_final", "k_norm_router", "k_moe_gu", "k_moe_down", "k_rmsnorm", "k_gemv",
-                 "k_argmax_part"),
+    "moe48tok": ("k_argmax_final", "k_norm_router", "k_moe_xcd", "k_rmsnorm", "k_gemv", "k_argmax_part"),
     "moebatch": ("k_mb_group", "k_quantize_q8_1", "k_moe_gu_grp", "k_mb_gu_mfma", "k_moe_down_grp", "k_mb_down_mfma",
                  "k_mb_combine"),
 }
@@ -41,6 +40,7 @@ UNIT_NAME = {"moe48": "MoE layer", "moe40cold": "MoE layer", "gemv6144": "GEMV",
              "moebatch": "batched MoE layer (n_sel 8, 64 tokens)", "moe48tok": "decode token"}
 EXTRA_ARGS = {"moebatch": ["--batch-points", "8x64"]}
 PROFILE_NAME = {"moebatch": "batched_moe_moebatch_8x64", "moe48tok": "decode_token_moe48tok", "qwen8b": "k_gemv_k_moe_gu_k_moe_down_qwen8b"}
+# eight-slot layers run as k_moe_xcd unless KATALI_HIP_XCD=0 (--two-launch)
 
 
 def run(cmd, log, extra_env=None):
@@ -113,7 +113,10 @@ def main():
     ap.add_argument("--out", required=True, help="directory for the raw rocprofv3 output")
     ap.add_argument("--summarize-only", action="store_true", help="parse an existing --out tree, run nothing")
     ap.add_argument("--fused", action="store_true",
-                    help="the one-launch MoE layer (KATALI_HIP_FUSED=1; moe48 and moe40cold)")
+                    help="the all-slots one-launch MoE layer (KATALI_HIP_FUSED=1, KATALI_HIP_XCD=0; moe48 and "
+                         "moe40cold)")
+    ap.add_argument("--two-launch", action="store_true",
+                    help="moe48: kernels A and B instead of the XCD-sliced layer (KATALI_HIP_XCD=0)")
     ap.add_argument("--one-stream", action="store_true",
                     help="moebatch: the grouped GEMM on the library stream (KATALI_HIP_ONE_STREAM=1), so "
                          "per-kernel times add up to the layer")
@@ -124,8 +127,13 @@ def main():
     if args.fused:
         if wl not in ("moe48", "moe40cold"):
             sys.exit("--fused applies to moe48 and moe40cold")
-        extra_env = {"KATALI_HIP_FUSED": "1"}
+        extra_env = {"KATALI_HIP_FUSED": "1", "KATALI_HIP_XCD": "0"}
         kernels, profile_name, traffic_name = ("k_moe_fused",), "k_moe_fused_" + wl, "fused_" + wl
+    if args.two_launch:
+        if wl != "moe48":
+            sys.exit("--two-launch applies to moe48")
+        extra_env = {"KATALI_HIP_XCD": "0"}
+        kernels, profile_name, traffic_name = ("k_moe_gu", "k_moe_down"), "k_moe_gu_k_moe_down_moe48", "two_launch_moe48"
     if args.one_stream:
         if wl != "moebatch":
             sys.exit("--one-stream applies to moebatch")

@@ -37,3 +37,13 @@ def hip():
     assert h.probe(), f"no usable gfx950 device: {h.status()}"
     print(f"[katali_hip] {h.status()}", flush=True)
     return h
+
+
+@pytest.fixture
+def two_launch_layer(monkeypatch):
+    """The single-token layer as kernels A and B (KATALI_HIP_XCD=0): for tests
+    whose other path (batched, normed, allocation-free) must match those two
+    kernels bit for bit. The XCD-sliced layer that eight-slot shapes take by
+    default sums each down row over its own lane split and is tested against
+    kernels A and B and the oracle on its own."""
+    monkeypatch.setenv("KATALI_HIP_XCD", "0")

@@ -70,7 +70,33 @@ CASES = [
     # 27 blocks, and a Q4_K down of 26 blocks
     (1024, 6912, 16, 16, True, Q6_K),
     (512, 6656, 8, 8, False, Q4_K),
+    # eight slots, the XCD-sliced layer's shapes: seven routed plus the
+    # shared expert; hidden 1024 with a Q4_K down of 4 blocks (two per
+    # lane) and every workgroup a gate/up unit (ffn 1024); ffn 256
+    (2048, 512, 256, 7, True, Q6_K),
+    (1024, 1024, 64, 8, False, Q4_K),
+    (2048, 256, 32, 8, False, Q6_K),
 ]
+# the cases whose shape the XCD-sliced layer takes (eight slots, hidden 1024
+# or 2048, ffn <= 1024, <= 256 experts); every other shape runs kernels A and B
+XCD_CASES = [c for c in CASES if c[3] + (1 if c[4] else 0) == 8 and c[0] in (1024, 2048) and c[1] <= 1024
+             and c[2] <= 256]
+# two_launch: kernels A and B; one_launch: k_moe_fused; xcd: the default,
+# the XCD-sliced layer where the shape fits it
+MODES = {"two_launch": {"KATALI_HIP_XCD": "0"}, "one_launch": {"KATALI_HIP_FUSED": "1", "KATALI_HIP_XCD": "0"},
+         "xcd": {}}
+
+
+def set_mode(monkeypatch, mode):
+    for k in ("KATALI_HIP_FUSED", "KATALI_HIP_XCD"):
+        monkeypatch.delenv(k, raising=False)
+    for k, v in MODES[mode].items():
+        monkeypatch.setenv(k, v)
+
+
+def case_id(c):
+    return f"h{c[0]}_f{c[1]}_e{c[2]}_k{c[3]}{'_sh' if c[4] else ''}{'_q4down' if c[5] == Q4_K else ''}"
+
 
 
 @pytest.fixture(scope="module")
@@ -104,13 +130,12 @@ def run_layer(hip, m, x, n_sel, logits=None, ids=None, w=None):
             wo.download(np.float32)[:n_sel])
 
 
-@pytest.mark.parametrize("fused", [False, True], ids=["two_launch", "one_launch"])
-@pytest.mark.parametrize("case", CASES, ids=[f"h{c[0]}_f{c[1]}_e{c[2]}_k{c[3]}{'_sh' if c[4] else ''}{'_q4down' if c[5] == Q4_K else ''}" for c in CASES])
-def test_moe_layer_parity(hip, oracle, moes, case, fused, monkeypatch):
+@pytest.mark.parametrize("mode", list(MODES))
+@pytest.mark.parametrize("case", CASES, ids=[case_id(c) for c in CASES])
+def test_moe_layer_parity(hip, oracle, moes, case, mode, monkeypatch):
     hidden, ffn, n_expert, n_sel, shared, down_type = case
-    print(f"[moe] case={case} fused={fused}", flush=True)
-    if fused:
-        monkeypatch.setenv("KATALI_HIP_FUSED", "1")   # where the shape fits the one-launch kernel
+    print(f"[moe] case={case} mode={mode}", flush=True)
+    set_mode(monkeypatch, mode)   # where the shape fits that layer; kernels A and B elsewhere
     m = moes(hidden, ffn, n_expert, shared, down_type)
     rng = np.random.default_rng(hidden + ffn + n_sel)
     x = S.activation(rng, hidden)
@@ -222,9 +247,9 @@ def test_fused_layer_matches_two_launches(hip, oracle, moes, case, monkeypatch):
     rng = np.random.default_rng(5 + hidden + n_sel)
     x = S.activation(rng, hidden)
     logits = rng.standard_normal(n_expert).astype(np.float32)
-    monkeypatch.setenv("KATALI_HIP_FUSED", "1")
+    set_mode(monkeypatch, "one_launch")
     y1, gu1, hq1, ido1, wo1 = run_layer(hip, m, x, n_sel, logits=logits)
-    monkeypatch.delenv("KATALI_HIP_FUSED")
+    set_mode(monkeypatch, "two_launch")
     y0, gu0, hq0, ido0, wo0 = run_layer(hip, m, x, n_sel, logits=logits)
     assert np.array_equal(gu1.view(np.uint32), gu0.view(np.uint32))
     assert np.array_equal(hq1, hq0)
@@ -232,6 +257,32 @@ def test_fused_layer_matches_two_launches(hip, oracle, moes, case, monkeypatch):
     r = rel_l2(y1, y0)
     print(f"rel_L2(fused, two launches) = {r:.3e}")
     assert r <= 1e-6
+
+
+@pytest.mark.parametrize("case", XCD_CASES, ids=[case_id(c) for c in XCD_CASES])
+def test_xcd_layer_matches_two_launches(hip, oracle, moes, case, monkeypatch):
+    """The XCD-sliced one-launch layer (the default here) against kernels A
+    and B, twice in a row with new inputs (the exchange's generations
+    advance between calls): the same routing, gate/up bits and h blocks; y
+    within fp32 reordering of the down sums (16 lanes per row here, kernel
+    B's own lane split there)."""
+    hidden, ffn, n_expert, n_sel, shared, down_type = case
+    print(f"[moe xcd vs two launches] case={case}", flush=True)
+    m = moes(hidden, ffn, n_expert, shared, down_type)
+    rng = np.random.default_rng(11 + hidden + ffn)
+    for call in range(2):
+        x = S.activation(rng, hidden)
+        logits = rng.standard_normal(n_expert).astype(np.float32)
+        set_mode(monkeypatch, "xcd")
+        y1, gu1, hq1, ido1, wo1 = run_layer(hip, m, x, n_sel, logits=logits)
+        set_mode(monkeypatch, "two_launch")
+        y0, gu0, hq0, ido0, wo0 = run_layer(hip, m, x, n_sel, logits=logits)
+        assert np.array_equal(gu1.view(np.uint32), gu0.view(np.uint32))
+        assert np.array_equal(hq1, hq0)
+        assert ido1.tolist() == ido0.tolist() and np.array_equal(wo1.view(np.uint32), wo0.view(np.uint32))
+        r = rel_l2(y1, y0)
+        print(f"call {call}: rel_L2(xcd, two launches) = {r:.3e}", flush=True)
+        assert r <= 1e-6
 
 
 ROUTE_CASES = [
@@ -318,15 +369,15 @@ def test_moe_back_to_back_layers(hip, oracle, moes):
         assert np.array_equal(y1.view(np.uint32), ys[i].download(np.uint32))
 
 
-@pytest.mark.parametrize("fused", [False, True], ids=["two_launch", "one_launch"])
-def test_moe_graph_replay_matches_eager(hip, oracle, moes, fused, monkeypatch):
+@pytest.mark.parametrize("mode", list(MODES))
+def test_moe_graph_replay_matches_eager(hip, oracle, moes, mode, monkeypatch):
     """A captured per-token sequence (two layers and a step advance) replayed
     over a ring of router logits; every replay is checked against an eager
     run, with eager work and syncs between replays. One launch: the layer's
-    generation-tagged exchange across replays of the same nodes."""
-    if fused:
-        monkeypatch.setenv("KATALI_HIP_FUSED", "1")
-    hidden, ffn, n_expert, n_sel = 2048, 512, 256, 8
+    generation-tagged exchange across replays of the same nodes (xcd: seven
+    routed experts and the shared one, the eight slots that layer takes)."""
+    set_mode(monkeypatch, mode)
+    hidden, ffn, n_expert, n_sel = 2048, 512, 256, 7 if mode == "xcd" else 8
     m = moes(hidden, ffn, n_expert, True, Q6_K)
     rng = np.random.default_rng(7)
     steps, layers = 4, 2

@@ -19,7 +19,7 @@ import pytest
 import kq_synth as S
 from oracle import Q4_K, Q6_K
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("two_launch_layer")]
 
 
 def rel_l2(a, b):

@@ -13,7 +13,7 @@ import pytest
 from katali_hip import HipError
 from oracle import Q4_K, Q6_K
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("two_launch_layer")]
 
 CASES = [
     # hidden, ffn, n_expert, n_sel, shared, down, residual scale (None: no residual step)

@@ -13,7 +13,7 @@ import kq_synth as S
 from katali_hip import HipError
 from oracle import Q4_K, Q6_K
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("two_launch_layer")]
 
 
 def _problem(hip, rng, hidden, ffn, n_expert, shared):
