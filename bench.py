@@ -90,19 +90,22 @@ TOKEN_WORKLOADS = {
 }
 
 
-def xcd_layer(hip, hidden, ffn, n_expert, n_slots):
+def xcd_layer(hip, hidden, ffn, n_expert, n_slots, shared=False):
     """Whether the library runs this layer shape as the XCD-sliced one-launch
     layer (k_moe_xcd) rather than kernels A and B: the rule launch_moe
-    applies (eight slots, hidden 1024 or 2048, ffn <= 1024, <= 256 experts,
-    a 256-CU device, KATALI_HIP_XCD not 0)."""
+    applies (eight slots, or with KATALI_HIP_XCD_SHARED=1 eight routed
+    experts plus the shared expert with ffn 256 or 512; hidden 1024 or 2048,
+    ffn <= 1024, <= 256 experts, a 256-CU device, KATALI_HIP_XCD not 0)."""
     if os.environ.get("KATALI_HIP_XCD", "1")[:1] in ("0", "n", "N"):
         return False
-    return (n_slots == 8 and hidden in (1024, 2048) and ffn <= 1024 and n_expert <= 256
+    spread = (n_slots == 9 and shared and ffn in (256, 512)
+              and os.environ.get("KATALI_HIP_XCD_SHARED", "")[:1] in ("1", "y", "Y"))
+    return ((n_slots == 8 or spread) and hidden in (1024, 2048) and ffn <= 1024 and n_expert <= 256
             and " 256 CUs" in hip.status())
 
 
-def layer_kernels(hip, hidden, ffn, n_expert, n_slots):
-    return ("k_moe_xcd (one launch per layer)" if xcd_layer(hip, hidden, ffn, n_expert, n_slots)
+def layer_kernels(hip, hidden, ffn, n_expert, n_slots, shared=False):
+    return ("k_moe_xcd (one launch per layer)" if xcd_layer(hip, hidden, ffn, n_expert, n_slots, shared)
             else "k_moe_gu + k_moe_down (two launches per layer)")
 
 
@@ -1004,7 +1007,7 @@ def main():
             "shared_expert": shared, "expert_pool_gb": round(res["pool_gb"], 2),
             "bytes_per_token": res["bytes_per_token"], "parallelism": "single GPU",
         }
-        kernel = "MoE layer: " + layer_kernels(hip, hidden, ffn, n_expert, n_sel + (1 if shared else 0))
+        kernel = "MoE layer: " + layer_kernels(hip, hidden, ffn, n_expert, n_sel + (1 if shared else 0), shared)
         extra = {"tok_s": round(res["tok_s"], 2),
                  "eager_layer_ms_mean": round(res["kernel_ms_mean"], 5)}
     elif args.workload in TOKEN_WORKLOADS:

@@ -289,9 +289,13 @@ int moe_impl(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, 
     // other one-launch layer is opt-in (KATALI_HIP_FUSED=1): measured slower
     // than kernels A and B (its all-slots h exchange costs more than the
     // launch it saves).
+    // Eight routed experts plus the shared expert can take it too, the shared
+    // expert in 128-value units (KATALI_HIP_XCD_SHARED=1): measured slower
+    // than kernels A and B at the 2048/512 top-8-of-256 shape.
     const bool allow_fused = env_on("KATALI_HIP_FUSED");
     const bool allow_xcd = !env_off("KATALI_HIP_XCD");
-    rc = launched(kq::launch_moe(a, g_stream, allow_fused, nullptr, allow_xcd), "moe launch");
+    const bool xcd_units = env_on("KATALI_HIP_XCD_SHARED");
+    rc = launched(kq::launch_moe(a, g_stream, allow_fused, nullptr, allow_xcd, xcd_units), "moe launch");
     if (rc) return rc;
     if (hq8_dbg) {
         hipError_t e = hipMemcpyAsync(hq8_dbg, g_hq8, hq8_bytes, hipMemcpyDeviceToDevice, g_stream);

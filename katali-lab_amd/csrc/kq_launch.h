@@ -133,10 +133,11 @@ constexpr uint32_t LDS_PER_WG = 160 * 1024;
 // The layer in one launch when the shape fits the fused kernel and a.fsync is
 // set (and `allow_fused`), else kernels A and B. *fused tells which ran.
 // allow_xcd: the XCD-sliced one-launch layer where the shape fits it
-// (eight slots, hidden 1024 or 2048, ffn <= 1024, a 256-CU device), tried
-// before the fused one.
+// (eight slots, or with xcd_shared_units eight routed experts and the
+// shared expert with ffn 256 or 512; hidden 1024 or 2048, ffn <= 1024,
+// <= 256 experts, a 256-CU device), tried before the fused one.
 hipError_t launch_moe(const MoeArgs &a, hipStream_t s, bool allow_fused = false, bool *fused = nullptr,
-                      bool allow_xcd = false);
+                      bool allow_xcd = false, bool xcd_shared_units = false);
 // The in-kernel exchanges (zeroed once, before first use): [0] the fused
 // layer's generation, [1] the normed layer's; from FSYNC_H one block per
 // workgroup of the fused layer of 9 8-byte words {dword, generation} (its
@@ -147,7 +148,10 @@ hipError_t launch_moe(const MoeArgs &a, hipStream_t s, bool allow_fused = false,
 // From FSYNC_X, the XCD-sliced layer's (launch_moe with allow_xcd): one
 // generation word per workgroup (XCD_G of them), then from FSYNC_XH its h
 // values [slot][ffn <= 1024], then from FSYNC_XP its unweighted down
-// partials [slot][hidden], each value one 8-byte word {float, generation}. Each exchange has its own generations, so no
+// partials [slot][hidden], then with the shared expert in 128-value units
+// from FSYNC_XS each XCD's copy of its unit's h [xcd][128] and from
+// FSYNC_XSP the units' unweighted down partials [unit][hidden]; each value
+// one 8-byte word {float, generation}. Each exchange has its own generations, so no
 // word one of them writes can pass for another's.
 constexpr uint32_t FSYNC_H = 64;
 constexpr uint32_t FUSED_MAX_G = 256;   // workgroups of the fused layer
@@ -160,7 +164,10 @@ constexpr uint32_t FSYNC_X = FSYNC_R + FSYNC_REP * 2 * 512;
 constexpr uint32_t FSYNC_XH = FSYNC_X + XCD_G;
 constexpr uint32_t XCD_MAX_FFN = 1024;
 constexpr uint32_t FSYNC_XP = FSYNC_XH + 2 * XCD_SLOTS * XCD_MAX_FFN;
-constexpr uint32_t fsync_words() { return FSYNC_XP + 2 * XCD_SLOTS * XCD_MAX_HIDDEN; }
+constexpr uint32_t XCD_MAX_UNITS = 4;   // the shared expert's 128-value units (ffn <= 512)
+constexpr uint32_t FSYNC_XS = FSYNC_XP + 2 * XCD_SLOTS * XCD_MAX_HIDDEN;
+constexpr uint32_t FSYNC_XSP = FSYNC_XS + 2 * XCD_SLOTS * 128;
+constexpr uint32_t fsync_words() { return FSYNC_XSP + 2 * XCD_MAX_UNITS * XCD_MAX_HIDDEN; }
 static_assert(FSYNC_H + 2 * 9 * FUSED_MAX_G <= FSYNC_R, "exchange areas overlap");
 // The steps before the layer and the layer in two launches (MoeArgs' n*
 // fields and router set, n_sel >= 1, hidden <= 4096): kernel A forms the

@@ -1489,27 +1489,30 @@ static hipError_t launch_moe_fused(const MoeArgs &a, uint32_t n_slots, hipStream
 // are void).
 // ---------------------------------------------------------------------------
 constexpr uint32_t XCD_POLL_WAVES = 4;   // waves that poll the slot's h
-constexpr int XCD_HW = 4;                // h words per polling thread: ffn <= 4 * 256
+constexpr int XCD_HW = 4;                // h words per polling thread at most: 1024 <= 4 * 256
 
 // One workgroup's gate/up part: rows v < R of slot `slot` (v < IW: gate row
-// IW * li + v, else up row IW * li + v - IW), kernel A's item mapping, scale
-// records, term order and reductions (so every value is kernel A's), on
-// waves 0 .. R/4 - 1; the others stage x with them. `down` issues the
-// caller's down loads (after the wave's dots, or once x is staged on waves
-// without rows). Leaves gate/up values in LDS at lds + lds_a(..).gu.
-template <int NB, int C, int IW, class Down>
+// IW * li + v, v < 2 IW: up row IW * li + v - IW) and, with IWS > 0, of the
+// shared expert (v < 2 IW + IWS: gate row shb + v - 2 IW; then the up rows;
+// written to dbg_gu only when sh_dbg), kernel A's item mapping, scale records, term
+// order and reductions (so every value is kernel A's), on waves 0 .. R/4 - 1
+// (rows past R in the last of them are loaded and dropped); the others stage
+// x with them. `down` issues the caller's down loads (after the wave's dots,
+// or once x is staged on waves without rows). Leaves the R gate/up values in
+// LDS at lds + lds_a(..).gu.
+template <int NB, int C, int IW, int IWS, class Down>
 __device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_t li, uint8_t *lds, GuRoute &rt,
-                                        Down down) {
+                                        Down down, uint32_t shb = 0, bool sh_dbg = false) {
     constexpr int RW = 4;                      // rows per wave (kernel A's at these widths)
     static_assert(a1_rw<NB>() == RW, "gu_part: kernel A's 4-row waves");
-    constexpr int R = 2 * IW, GW = R / RW;     // rows, waves with rows
+    constexpr int R = 2 * IW + 2 * IWS, GW = (R + RW - 1) / RW;   // rows, waves with rows
     constexpr int NT = a1_threads<NB>();
     constexpr int ITEMS = 8 * NB;
     constexpr int LPG = RW * ITEMS / 64;       // chunks per lane (one group: LPG <= 16)
     constexpr int M = ITEMS >= 64 ? ITEMS / 64 : 1;
     constexpr int WH = RW * NB;
     constexpr int HPL = (WH + 63) / 64;
-    static_assert(R % RW == 0 && GW <= NT / 64 && LPG <= 16, "gu_part shape");
+    static_assert(R <= 64 && GW <= NT / 64 && LPG <= 16, "gu_part shape");
     const LdsA L = lds_a(a.hidden, NB);
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const bool rows = wave < (uint32_t)GW;
@@ -1549,9 +1552,12 @@ __device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_
         gb = a.gate_sh;
         ub = a.up_sh;
     }
-    auto row_ptr = [&](uint32_t v) -> const uint8_t * {   // v < R (clamped for waves without rows)
+    auto row_ptr = [&](uint32_t v) -> const uint8_t * {   // v < R (clamped past it)
         v = min(v, (uint32_t)R - 1);
-        return v < (uint32_t)IW ? gb + (uint64_t)(IW * li + v) * rb : ub + (uint64_t)(IW * li + v - IW) * rb;
+        if (v < (uint32_t)IW) return gb + (uint64_t)(IW * li + v) * rb;
+        if (v < (uint32_t)(2 * IW)) return ub + (uint64_t)(IW * li + v - IW) * rb;
+        if (v < (uint32_t)(2 * IW + IWS)) return a.gate_sh + (uint64_t)(shb + v - 2 * IW) * rb;
+        return a.up_sh + (uint64_t)(shb + v - 2 * IW - IWS) * rb;
     };
     auto chunk = [&](int k) -> const uint8_t * {
         uint32_t r, it;
@@ -1639,7 +1645,8 @@ __device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_
                 acc[k] = q4k_term(q[k], sc, xs[k % M]);
             }
             const float v = pw_rows<LPG, M>(acc);
-            if (lane < (uint32_t)RW) gu[RW * wave + pw_rows_row<LPG, M>(lane)] = v;
+            const uint32_t row = RW * wave + pw_rows_row<LPG, M>(lane);
+            if (lane < (uint32_t)RW && row < (uint32_t)R) gu[row] = v;
         } else {
             const uint32_t it = lane % ITEMS;
 #pragma unroll
@@ -1647,7 +1654,7 @@ __device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_
                 const uint32_t row = lane / ITEMS + k * (64 / ITEMS);
                 const float4 sc = scl[4 * (row * NB + it / 8) + (it % 8) / 2];
                 const float v = group_sum<ITEMS>(q4k_term(q[k], sc, xs[0]));
-                if (it == 0) gu[RW * wave + row] = v;
+                if (it == 0 && RW * wave + row < (uint32_t)R) gu[RW * wave + row] = v;
             }
         }
     }
@@ -1655,11 +1662,28 @@ __device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_
     __syncthreads();
     if (a.dbg_gu && tid < (uint32_t)R) {
         float *d = a.dbg_gu + (uint64_t)slot * 2 * a.ffn + (tid < (uint32_t)IW ? 0 : a.ffn) + IW * li + tid % IW;
+        if constexpr (IWS > 0) {
+            if (tid >= (uint32_t)(2 * IW) && !sh_dbg) return;
+            if (tid >= (uint32_t)(2 * IW))   // the shared expert is slot n_sel
+                d = a.dbg_gu + (uint64_t)a.n_sel * 2 * a.ffn + (tid < (uint32_t)(2 * IW + IWS) ? 0 : a.ffn) + shb +
+                    (tid - 2 * IW) % IWS;
+        }
         *d = gu[tid];
     }
 }
 
-template <int NB, int C, class QD, int S, int IPL, int IW>
+// SH: eight routed slots plus the shared expert. The shared expert's ffn is
+// cut into U = ffn / 128 units of 128 intermediate values (one half n of
+// down block bk: 2 bk + n = u), so every q8_1 block of its h lies in one
+// unit. XCD x takes unit u = x % U: its 32 workgroups compute the unit's
+// 128 h values (4 each: gate and up rows 128 u + 4 li + [0, 4), the same
+// values on each of the Q = 8 / U XCDs of a unit), exchange them inside
+// the XCD, and dot the unit's down items (half n of block bk: IPB / 2 items
+// per row) over the XCD's part x / U of the output rows, one unweighted
+// partial per row and unit. Wave 0 sums, per row, the eight slots in rank
+// order and then the U shared partials in unit order, weight 1 (the shared
+// expert enters last, as in kernel B).
+template <int NB, int C, class QD, int S, int IPL, int IW, bool SH>
 __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
     constexpr uint32_t NT = a1_threads<NB>();
     constexpr uint32_t P = S / QD::IPB;
@@ -1669,21 +1693,35 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
     constexpr uint32_t TRX = H / PER;             // down rows per workgroup
     constexpr uint32_t TRC = TRX / XCD_SLOTS;     // rows each workgroup sums
     constexpr uint32_t NBK = F / 256;             // blocks per down row
-    static_assert(S * TRX <= NT && TRC >= 1 && XCD_SLOTS * TRC <= 64, "XCD layer tile");
-    static_assert(F <= XCD_HW * 64 * XCD_POLL_WAVES && F % 256 == 0, "XCD layer ffn");
+    constexpr uint32_t U = SH ? F / 128 : 1;      // shared units
+    constexpr uint32_t Q = XCD_SLOTS / U;         // XCDs per unit
+    constexpr int IWS = SH ? 4 : 0;               // shared h values per workgroup (128 / 32)
+    constexpr uint32_t HW = F + (SH ? 128 : 0);   // h words polled: the slot's, then the unit's
+    constexpr uint32_t IH = QD::IPB / 2;          // down items of one half block
+    constexpr uint32_t RS = H / Q / PER;          // shared down rows per workgroup
+    static_assert(S * TRX <= NT && TRC >= 1 && XCD_SLOTS * TRC <= 64 && (!SH || U * TRC <= 64), "XCD layer tile");
+    static_assert(!SH || (XCD_SLOTS % U == 0 && RS * IH <= 128), "XCD layer shared units");
+    static_assert(HW <= XCD_HW * 64 * XCD_POLL_WAVES && F % 256 == 0, "XCD layer ffn");
     extern __shared__ __align__(16) uint8_t lds[];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t b = blockIdx.x, xs = b % XCD_SLOTS, li = b / XCD_SLOTS;
+    const uint32_t u = xs % U, part = xs / U;   // SH: this XCD's unit and its part of the output rows
     pin_args(a.down, a.down_sh, a.y, a.fsync, a.hq8);
     uint32_t *gw = a.fsync + FSYNC_X + b;
     const uint32_t gen = ld_dev(gw);   // issued first, used last
 
-    // the down share: row r = tid / S of the tile, lane s = tid % S
+    // the down share: row r = tid / S of the tile, lane s = tid % S; with SH,
+    // threads t < RS * IH also take item IH * (u % 2) + t % IH of block u / 2
+    // of shared row part * H / Q + li * RS + t / IH
     const uint32_t s = tid % S, r = tid / S;
     const uint32_t item = s % QD::IPB, bs = s / QD::IPB;
     const uint32_t row0 = li * TRX, rr = min(r, TRX - 1);   // idle threads load a real row and drop it
+    const bool sdown = SH && tid < RS * IH;                   // whole waves up to RS * IH (a multiple of 32)
+    const uint32_t itemS = IH * (u % 2) + tid % IH, bkS = u / 2;
+    const uint32_t rowS = part * (H / Q) + li * RS + min(tid / IH, RS - 1);
     constexpr uint64_t rbd = (uint64_t)NBK * QD::BB;
     typename QD::Raw raw[IPL];
+    typename QD::Raw rawS;
     GuRoute rt;
     auto load_down = [&]() {
         int32_t sid = __builtin_amdgcn_readlane(rt.eid, (int)xs);
@@ -1692,34 +1730,52 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
                             (uint64_t)(row0 + rr) * rbd;
 #pragma unroll
         for (int i = 0; i < IPL; i++) raw[i] = QD::load(rp + min(bs + P * i, NBK - 1) * QD::BB, (int)item);
+        if constexpr (SH) {
+            if (tid < ((RS * IH + 63) & ~63u))   // whole waves; threads past RS * IH load a real row and drop it
+                rawS = QD::load(a.down_sh + (uint64_t)rowS * rbd + bkS * QD::BB, (int)itemS);
+        }
     };
-    gu_part<NB, C, IW>(a, xs, li, lds, rt, load_down);
+    gu_part<NB, C, IW, IWS>(a, xs, li, lds, rt, load_down, 128 * u + IWS * li, part == 0);
 
     uint32_t tag = gen;
     asm volatile("" : "+v"(tag));
     tag += 1;
-    uint32_t *hx = a.fsync + FSYNC_XH + 2 * F * xs;   // slot xs's h words
-    if (wave == 0 && lane < IW) {
+    uint32_t *hx = a.fsync + FSYNC_XH + 2 * F * xs;    // slot xs's h words
+    uint32_t *hxs = a.fsync + FSYNC_XS + 2 * 128 * xs;   // this XCD's copy of its unit's
+    if (wave == 0) {
         const float *gu = (const float *)(lds + lds_a(a.hidden, NB).gu);
-        const float h = kq_silu_mul(gu[lane], gu[IW + lane]);
-        st_dev2(hx + 2 * (IW * li + lane), ((uint64_t)tag << 32) | __float_as_uint(h));
+        if (lane < (uint32_t)IW) {
+            const float h = kq_silu_mul(gu[lane], gu[IW + lane]);
+            st_dev2(hx + 2 * (IW * li + lane), ((uint64_t)tag << 32) | __float_as_uint(h));
+        }
+        if constexpr (SH) {
+            if (lane >= (uint32_t)IW && lane < (uint32_t)(IW + IWS)) {
+                const uint32_t j = lane - IW;
+                const float h = kq_silu_mul(gu[2 * IW + j], gu[2 * IW + IWS + j]);
+                st_dev2(hxs + 2 * (IWS * li + j), ((uint64_t)tag << 32) | __float_as_uint(h));
+            }
+        }
     }
 
-    // 3. slot xs's h: word t of thread pt is h[pt + 256 t]; quantized where
-    //    32 lanes hold one 32-value block (kernel A's quantizer)
+    // 3. the h words: word t of thread pt is word pt + 256 t (the slot's h
+    //    first, then the unit's), quantized where 32 lanes hold one 32-value
+    //    block (kernel A's quantizer)
     uint32_t spins = 0;
     const uint32_t first_poller = NT - 64 * XCD_POLL_WAVES;
     const bool poller = tid >= first_poller;   // whole waves
-    const Act act = act_carve(lds + lds_a(a.hidden, NB).total, F);
+    const uint32_t LT = lds_a(a.hidden, NB).total;
+    const Act act = act_carve(lds + LT, F);
+    const Act actS = act_carve(lds + LT + act_bytes(F), F);   // SH only: the unit's blocks
     if (poller) {
         const uint32_t pt = tid - first_poller;
-        constexpr int NW = (F + 64 * XCD_POLL_WAVES - 1) / (64 * XCD_POLL_WAVES);
+        constexpr int NW = (HW + 64 * XCD_POLL_WAVES - 1) / (64 * XCD_POLL_WAVES);
+        auto word = [&](uint32_t e) { return e < F ? hx + 2 * e : hxs + 2 * (e - F); };
         // two rounds in flight: the next round goes out before the previous
         // one is checked, so a word is sampled twice per round trip
         uint64_t hv[NW], va[NW], vb[NW];
         auto issue = [&](uint64_t *o) {
 #pragma unroll
-            for (int i = 0; i < NW; i++) o[i] = ld_dev2(hx + 2 * min(pt + 64 * XCD_POLL_WAVES * i, F - 1));
+            for (int i = 0; i < NW; i++) o[i] = ld_dev2(word(min(pt + 64 * XCD_POLL_WAVES * i, HW - 1)));
         };
         auto seen = [&](const uint64_t *o) {
             bool ok = true;
@@ -1751,8 +1807,11 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
         }
 #pragma unroll
         for (int i = 0; i < NW; i++) {
-            const uint32_t e = pt + 64 * XCD_POLL_WAVES * i;   // h index; its 32-lane half is one block
-            if (e < F) {   // whole 32-lane halves (F % 256 == 0)
+            const uint32_t w = pt + 64 * XCD_POLL_WAVES * i;   // its 32-lane half is one block of one expert
+            if (w < HW) {   // whole 32-lane halves (F and 128 multiples of 32)
+                const bool shared = SH && w >= F;
+                const uint32_t e = shared ? 128 * u + (w - F) : w;   // the value's index in its expert's h
+                const Act &dst = shared ? actS : act;
                 const float h = __uint_as_float((uint32_t)hv[i]);
                 const float am = max32(fabsf(h));
                 const float d = am / 127.0f;
@@ -1766,11 +1825,12 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
                 s16 += dpp_i<DPP_MIRROR>(s16);
                 const uint32_t kb = e / 32, j = e % 32;
                 const uint32_t d16 = f2h_rne(d);
-                act.qs[e] = (int8_t)qv;
-                if (j == 0) act.d8[kb] = h2f(d16);
-                if ((j & 15) == 0) act.qs16[2 * kb + j / 16] = s16;
-                if (li == 0) {   // the q8_1 blocks of h, as kernel A writes them
-                    uint8_t *blk = a.hq8 + ((uint64_t)xs * (F / 32) + kb) * 36;
+                dst.qs[e] = (int8_t)qv;
+                if (j == 0) dst.d8[kb] = h2f(d16);
+                if ((j & 15) == 0) dst.qs16[2 * kb + j / 16] = s16;
+                if (li == 0 && (!shared || part == 0)) {   // the q8_1 blocks of h, as kernel A writes them
+                    const uint32_t hs = shared ? (uint32_t)a.n_sel : xs;   // the shared expert is slot n_sel
+                    uint8_t *blk = a.hq8 + ((uint64_t)hs * (F / 32) + kb) * 36;
                     blk[4 + j] = (uint8_t)(qv & 255);
                     if (j == 0) *(uint32_t *)blk = d16 | (f2h_rne((float)total * d) << 16);
                 }
@@ -1779,7 +1839,7 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
     }
     __syncthreads();
 
-    // the tile's unweighted down partials
+    // the tile's unweighted down partials (and, with SH, the unit's shared ones)
     float x = 0.0f;
 #pragma unroll
     for (int i = 0; i < IPL; i++) {
@@ -1790,30 +1850,49 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
     x = group_sum<S>(x);
     if (r < TRX && s == 0)
         st_dev2(a.fsync + FSYNC_XP + 2 * (xs * H + row0 + r), ((uint64_t)tag << 32) | __float_as_uint(x));
+    if constexpr (SH) {
+        if (tid < ((RS * IH + 63) & ~63u)) {   // whole waves
+            const float xsh = group_sum<IH>(QD::dot_q8(rawS, (int)itemS, actS, bkS));
+            if (sdown && tid % IH == 0)
+                st_dev2(a.fsync + FSYNC_XSP + 2 * (u * H + rowS), ((uint64_t)tag << 32) | __float_as_uint(xsh));
+        }
+    }
 
-    // 4. wave 0: rows row0 + xs * TRC + c (c < TRC) over the eight slots
+    // 4. wave 0: rows row0 + xs * TRC + c (c < TRC) over the eight slots, then
+    //    the shared expert's U partials
     if (wave == 0) {
         float rw = a.logits && a.n_sel > 0 ? route_weight(rt.logit, a.n_sel) : rt.w;
         rw = (int)lane < a.n_sel ? rw : ((int)lane == a.n_sel && a.has_shared ? 1.0f : 0.0f);
         if (lane == 0) st_dev(gw, tag);   // gen was read at the start: advance it now
-        const uint32_t q = lane / TRC, c = lane % TRC;   // lane: slot q, row c
-        uint32_t *pw = a.fsync + FSYNC_XP + 2 * (min(q, XCD_SLOTS - 1) * H + row0 + xs * TRC + c);
-        auto ok = [&](uint64_t v) { return __all(lane >= XCD_SLOTS * TRC || (uint32_t)(v >> 32) == tag); };
-        uint64_t pv, pa = ld_dev2(pw), pb;
+        const uint32_t q = lane / TRC, c = lane % TRC;   // lane: slot (or unit) q, row c
+        const uint32_t yr = row0 + xs * TRC + c;
+        uint32_t *pw = a.fsync + FSYNC_XP + 2 * (min(q, XCD_SLOTS - 1) * H + yr);
+        uint32_t *pws = a.fsync + FSYNC_XSP + 2 * (min(q, U - 1) * H + yr);
+        auto ok = [&](uint64_t v, uint64_t vs) {
+            return __all((lane >= XCD_SLOTS * TRC || (uint32_t)(v >> 32) == tag) &&
+                         (!SH || lane >= U * TRC || (uint32_t)(vs >> 32) == tag));
+        };
+        uint64_t pv, pa = ld_dev2(pw), pb, sv = 0, sa = 0, sb = 0;
+        if constexpr (SH) sa = ld_dev2(pws);
         for (;;) {   // two rounds in flight, as above
             pb = ld_dev2(pw);
-            if (ok(pa)) {
+            if constexpr (SH) sb = ld_dev2(pws);
+            if (ok(pa, sa)) {
                 pv = pa;
+                sv = sa;
                 break;
             }
             pa = ld_dev2(pw);
-            if (ok(pb)) {
+            if constexpr (SH) sa = ld_dev2(pws);
+            if (ok(pb, sb)) {
                 pv = pb;
+                sv = sb;
                 break;
             }
             if (++spins >= FSYNC_SPIN_LIMIT / 2) {
                 if (lane == 0) atomicOr(a.err, 4);
                 pv = pb;
+                sv = sb;
                 break;
             }
         }
@@ -1824,50 +1903,67 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
             const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rw), (int)k));
             y = fmaf(w, __shfl(v, (int)(k * TRC + c), WAVE), y);
         }
+        if constexpr (SH) {
+            const float vs = __uint_as_float((uint32_t)sv);
+            float sh = 0.0f;
+#pragma unroll
+            for (uint32_t k = 0; k < U; k++) sh += __shfl(vs, (int)(k * TRC + c), WAVE);   // unit order
+            y = fmaf(1.0f, sh, y);   // the shared expert, last
+        }
         if (lane < TRC) a.y[row0 + xs * TRC + lane] = y;
     }
 }
 
-template <int NB, int C, class QD, int S, int IPL, int IW>
+template <int NB, int C, class QD, int S, int IPL, int IW, bool SH>
 static hipError_t go_xcd(const MoeArgs &a, hipStream_t s) {
-    const uint32_t lds = lds_a(a.hidden, NB).total + act_bytes(32 * IW);
+    const uint32_t lds = lds_a(a.hidden, NB).total + (SH ? 2 : 1) * act_bytes(32 * IW);
     if (lds > 64 * 1024) {
-        const hipError_t e = hipFuncSetAttribute((const void *)k_moe_xcd<NB, C, QD, S, IPL, IW>,
+        const hipError_t e = hipFuncSetAttribute((const void *)k_moe_xcd<NB, C, QD, S, IPL, IW, SH>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL((k_moe_xcd<NB, C, QD, S, IPL, IW>), dim3(XCD_G), dim3(a1_threads<NB>()), lds, s, a);
+    hipLaunchKernelGGL((k_moe_xcd<NB, C, QD, S, IPL, IW, SH>), dim3(XCD_G), dim3(a1_threads<NB>()), lds, s, a);
     return hipGetLastError();
 }
 // 16 lanes per down row: Q6_K 4 items x 4 block slots (ffn <= 1024: one
 // block per lane), Q4_K 8 items x 2 block slots (up to two)
-template <int NB, int C, int IW>
+template <int NB, int C, int IW, bool SH>
 static hipError_t go_xcd_q(const MoeArgs &a, hipStream_t s) {
-    if (a.down_type == T_Q6_K) return go_xcd<NB, C, Q6K, 16, 1, IW>(a, s);
-    if constexpr (IW <= 16) return go_xcd<NB, C, Q4K, 16, 1, IW>(a, s);
-    else return go_xcd<NB, C, Q4K, 16, 2, IW>(a, s);
+    if (a.down_type == T_Q6_K) return go_xcd<NB, C, Q6K, 16, 1, IW, SH>(a, s);
+    if constexpr (IW <= 16) return go_xcd<NB, C, Q4K, 16, 1, IW, SH>(a, s);
+    else return go_xcd<NB, C, Q4K, 16, 2, IW, SH>(a, s);
 }
-template <int NB, int C>
+template <int NB, int C, bool SH>
 static hipError_t go_xcd_f(const MoeArgs &a, hipStream_t s) {
     switch (a.ffn) {
-        case 256: return go_xcd_q<NB, C, 8>(a, s);
-        case 512: return go_xcd_q<NB, C, 16>(a, s);
-        case 768: return go_xcd_q<NB, C, 24>(a, s);
-        case 1024: return go_xcd_q<NB, C, 32>(a, s);
+        case 256: return go_xcd_q<NB, C, 8, SH>(a, s);
+        case 512: return go_xcd_q<NB, C, 16, SH>(a, s);
+        case 768:
+            if constexpr (!SH) return go_xcd_q<NB, C, 24, SH>(a, s);   // the shared units must divide the eight XCDs
+            else return hipErrorNotSupported;
+        case 1024:
+            if constexpr (!SH) return go_xcd_q<NB, C, 32, SH>(a, s);   // shared rows would not fit 64 per workgroup
+            else return hipErrorNotSupported;
         default: return hipErrorNotSupported;
     }
 }
-template <int NB>
+template <int NB, bool SH>
 static hipError_t go_xcd_c(const MoeArgs &a, hipStream_t s) {
-    return a.n_expert <= 128 ? go_xcd_f<NB, 2>(a, s) : go_xcd_f<NB, 4>(a, s);
+    return a.n_expert <= 128 ? go_xcd_f<NB, 2, SH>(a, s) : go_xcd_f<NB, 4, SH>(a, s);
 }
-// hipErrorNotSupported when the shape does not fit the XCD-sliced layer
-static hipError_t launch_moe_xcd(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
+// hipErrorNotSupported when the shape does not fit the XCD-sliced layer:
+// eight slots (one per XCD), or with shared_units eight routed experts plus
+// the shared expert in 128-value units (ffn 256 or 512 then; measured
+// slower than kernels A and B at the 2048/512 top-8-of-256 shape: 14.2
+// against 13.7 us per layer, so opt-in)
+static hipError_t launch_moe_xcd(const MoeArgs &a, uint32_t n_slots, bool shared_units, hipStream_t s) {
     const uint32_t nb = a.hidden / 256;
-    if (!a.fsync || n_slots != XCD_SLOTS || a.n_sel < 1 || !(nb == 4 || nb == 8) || a.n_expert > 256 ||
-        a.ffn > 1024 || device_cu_count() != (int)XCD_G)
+    const bool spread = shared_units && a.n_sel == (int)XCD_SLOTS && a.has_shared;
+    if (!a.fsync || !(n_slots == XCD_SLOTS || spread) || a.n_sel < 1 || !(nb == 4 || nb == 8) ||
+        a.n_expert > 256 || a.ffn > 1024 || (spread && a.ffn > 512) || device_cu_count() != (int)XCD_G)
         return hipErrorNotSupported;
-    return nb == 8 ? go_xcd_c<8>(a, s) : go_xcd_c<4>(a, s);
+    if (spread) return nb == 8 ? go_xcd_c<8, true>(a, s) : go_xcd_c<4, true>(a, s);
+    return nb == 8 ? go_xcd_c<8, false>(a, s) : go_xcd_c<4, false>(a, s);
 }
 
 uint64_t moe_route_words() { return 2 * MAX_SLOTS; }
@@ -2043,12 +2139,13 @@ hipError_t launch_route_batch(const float *logits, uint32_t n_tokens, uint32_t n
     return hipGetLastError();
 }
 
-hipError_t launch_moe(const MoeArgs &a, hipStream_t s, bool allow_fused, bool *fused, bool allow_xcd) {
+hipError_t launch_moe(const MoeArgs &a, hipStream_t s, bool allow_fused, bool *fused, bool allow_xcd,
+                      bool xcd_shared_units) {
     if (a.n_expert > MAX_EXPERT || a.n_sel > MAX_SEL) return hipErrorInvalidValue;
     const uint32_t n_slots = (uint32_t)a.n_sel + (a.has_shared ? 1u : 0u);
     if (fused) *fused = false;
     if (allow_xcd) {
-        const hipError_t f = launch_moe_xcd(a, n_slots, s);
+        const hipError_t f = launch_moe_xcd(a, n_slots, xcd_shared_units, s);
         if (f != hipErrorNotSupported) {
             if (fused) *fused = f == hipSuccess;
             return f;

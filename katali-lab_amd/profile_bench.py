@@ -133,7 +133,7 @@ def main():
         if wl != "moe48":
             sys.exit("--two-launch applies to moe48")
         extra_env = {"KATALI_HIP_XCD": "0"}
-        kernels, profile_name, traffic_name = ("k_moe_gu", "k_moe_down"), "k_moe_gu_k_moe_down_moe48", "two_launch_moe48"
+        kernels, profile_name, traffic_name = ("k_moe_gu", "k_moe_down"), "k_moe_gu_k_moe_down_" + wl, "two_launch_" + wl
     if args.one_stream:
         if wl != "moebatch":
             sys.exit("--one-stream applies to moebatch")

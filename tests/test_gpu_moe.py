@@ -76,19 +76,28 @@ CASES = [
     (2048, 512, 256, 7, True, Q6_K),
     (1024, 1024, 64, 8, False, Q4_K),
     (2048, 256, 32, 8, False, Q6_K),
+    # eight routed experts and the shared expert in 128-value units in the
+    # XCD-sliced layer (the 2048/512 top-8 + shared case above is another):
+    # hidden 1024 with a Q4_K down (four items per unit and row), and ffn 256
+    # (two units, four XCDs each)
+    (1024, 512, 64, 8, True, Q4_K),
+    (2048, 256, 64, 8, True, Q6_K),
 ]
-# the cases whose shape the XCD-sliced layer takes (eight slots, hidden 1024
-# or 2048, ffn <= 1024, <= 256 experts); every other shape runs kernels A and B
-XCD_CASES = [c for c in CASES if c[3] + (1 if c[4] else 0) == 8 and c[0] in (1024, 2048) and c[1] <= 1024
-             and c[2] <= 256]
-# two_launch: kernels A and B; one_launch: k_moe_fused; xcd: the default,
-# the XCD-sliced layer where the shape fits it
+# the cases whose shape the XCD-sliced layer takes (eight slots, or eight
+# routed experts plus the shared expert with ffn 256 or 512; hidden 1024 or
+# 2048, ffn <= 1024, <= 256 experts); every other shape runs kernels A and B
+XCD_CASES = [c for c in CASES if (c[3] + (1 if c[4] else 0) == 8 or (c[3] == 8 and c[4] and c[1] in (256, 512)))
+             and c[0] in (1024, 2048) and c[1] <= 1024 and c[2] <= 256]
+# two_launch: kernels A and B; one_launch: k_moe_fused; xcd: the XCD-sliced
+# layer where the shape fits it (the default for eight slots; eight routed
+# experts plus the shared expert in 128-value units only with
+# KATALI_HIP_XCD_SHARED=1)
 MODES = {"two_launch": {"KATALI_HIP_XCD": "0"}, "one_launch": {"KATALI_HIP_FUSED": "1", "KATALI_HIP_XCD": "0"},
-         "xcd": {}}
+         "xcd": {"KATALI_HIP_XCD_SHARED": "1"}}
 
 
 def set_mode(monkeypatch, mode):
-    for k in ("KATALI_HIP_FUSED", "KATALI_HIP_XCD"):
+    for k in ("KATALI_HIP_FUSED", "KATALI_HIP_XCD", "KATALI_HIP_XCD_SHARED"):
         monkeypatch.delenv(k, raising=False)
     for k, v in MODES[mode].items():
         monkeypatch.setenv(k, v)
@@ -369,15 +378,17 @@ def test_moe_back_to_back_layers(hip, oracle, moes):
         assert np.array_equal(y1.view(np.uint32), ys[i].download(np.uint32))
 
 
-@pytest.mark.parametrize("mode", list(MODES))
-def test_moe_graph_replay_matches_eager(hip, oracle, moes, mode, monkeypatch):
+@pytest.mark.parametrize("mode,n_sel", [("two_launch", 8), ("one_launch", 8), ("xcd", 7), ("xcd", 8)],
+                         ids=["two_launch", "one_launch", "xcd", "xcd_shared_units"])
+def test_moe_graph_replay_matches_eager(hip, oracle, moes, mode, n_sel, monkeypatch):
     """A captured per-token sequence (two layers and a step advance) replayed
     over a ring of router logits; every replay is checked against an eager
     run, with eager work and syncs between replays. One launch: the layer's
     generation-tagged exchange across replays of the same nodes (xcd: seven
-    routed experts and the shared one, the eight slots that layer takes)."""
+    routed experts and the shared one as eight slots, and eight with the
+    shared expert in 128-value units)."""
     set_mode(monkeypatch, mode)
-    hidden, ffn, n_expert, n_sel = 2048, 512, 256, 7 if mode == "xcd" else 8
+    hidden, ffn, n_expert = 2048, 512, 256
     m = moes(hidden, ffn, n_expert, True, Q6_K)
     rng = np.random.default_rng(7)
     steps, layers = 4, 2
