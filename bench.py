@@ -1030,8 +1030,9 @@ def main():
             "layers": L, "hidden": hidden, "ffn": ffn, "n_expert": n_expert, "n_sel": n_sel, "vocab": vocab,
             "bytes_per_token": res["bytes_per_token"], "parallelism": "single GPU",
         }
-        kernel = ("whole token graph (3 per layer + 4 launches: k_norm_router, k_moe_gu, k_moe_down; output norm, "
-                  "head, argmax)" if not args.normed_layer else
+        layer = layer_kernels(hip, hidden, ffn, n_expert, n_sel + (1 if shared else 0), shared)
+        kernel = (f"whole token graph (per layer k_norm_router + the MoE layer, {layer}; then 4 launches: output "
+                  "norm, head, argmax)" if not args.normed_layer else
                   "whole token graph (2 per layer + 4 launches: k_moe_gu with the norm and router, k_moe_down; "
                   "output norm, head, argmax)")
         extra = {"tok_s": round(res["tok_s"], 2)}
