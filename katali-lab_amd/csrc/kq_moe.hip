@@ -1770,38 +1770,41 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
         const uint32_t pt = tid - first_poller;
         constexpr int NW = (HW + 64 * XCD_POLL_WAVES - 1) / (64 * XCD_POLL_WAVES);
         auto word = [&](uint32_t e) { return e < F ? hx + 2 * e : hxs + 2 * (e - F); };
-        // two rounds in flight: the next round goes out before the previous
-        // one is checked, so a word is sampled twice per round trip
+        // Two rounds in flight: the next round goes out before the previous
+        // one is checked, so a word is sampled twice per round trip. A word
+        // already seen with this call's tag is kept, and its lane's later
+        // loads read the slot's first word instead (one line per wave
+        // instruction, the value dropped), so late rounds fetch only what
+        // is still missing while the down rows stream. The loads themselves
+        // are unconditional, so both rounds stay countable in flight.
         uint64_t hv[NW], va[NW], vb[NW];
+        uint32_t need = 0;   // bit i: word pt + 256 i still to see
+#pragma unroll
+        for (int i = 0; i < NW; i++)
+            if (pt + 64 * XCD_POLL_WAVES * i < HW) need |= 1u << i;
         auto issue = [&](uint64_t *o) {
 #pragma unroll
-            for (int i = 0; i < NW; i++) o[i] = ld_dev2(word(min(pt + 64 * XCD_POLL_WAVES * i, HW - 1)));
+            for (int i = 0; i < NW; i++)
+                o[i] = ld_dev2(((need >> i) & 1) ? word(pt + 64 * XCD_POLL_WAVES * i) : hx);
         };
-        auto seen = [&](const uint64_t *o) {
-            bool ok = true;
+        auto take = [&](const uint64_t *o) {   // true once every word of the wave is in
 #pragma unroll
-            for (int i = 0; i < NW; i++) ok &= (uint32_t)(o[i] >> 32) == tag;
-            return __all(ok);
-        };
-        auto take = [&](const uint64_t *o) {
-#pragma unroll
-            for (int i = 0; i < NW; i++) hv[i] = o[i];
+            for (int i = 0; i < NW; i++) {
+                if (((need >> i) & 1) && (uint32_t)(o[i] >> 32) == tag) {
+                    hv[i] = o[i];
+                    need &= ~(1u << i);
+                }
+            }
+            return __all(need == 0);
         };
         issue(va);
         for (;;) {
             issue(vb);
-            if (seen(va)) {
-                take(va);
-                break;
-            }
+            if (take(va)) break;
             issue(va);
-            if (seen(vb)) {
-                take(vb);
-                break;
-            }
+            if (take(vb)) break;
             if (++spins >= FSYNC_SPIN_LIMIT / 2) {
                 if (lane == 0) atomicOr(a.err, 4);
-                take(vb);
                 break;
             }
         }
