@@ -38,23 +38,46 @@ HIP_SOURCES = ["kq_gemv.hip", "kq_moe.hip", "kq_moe_batch.hip", "kq_sample.hip",
 C_FLAGS = ["-std=c11", "-O2", "-fPIC", "-Wall", "-Wextra", "-I" + INCLUDE, "-D_POSIX_C_SOURCE=200809L"]
 
 
-def _run(cmd: list[str]) -> None:
+def _run(cmd: list[str]) -> str:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(" ".join(cmd) + "\n" + r.stdout + r.stderr)
         raise RuntimeError(f"build step failed: {cmd[0]} ... {cmd[-1]}")
     if r.stderr.strip():
         # keep real warnings visible, drop the host-pass note about the
-        # device-only target feature
-        lines = [l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l and l.strip()]
+        # device-only target feature and the resource remarks (read below)
+        lines = [l for l in r.stderr.splitlines()
+                 if "packed-fp32-ops" not in l and "kernel-resource-usage" not in l and l.strip()]
         if lines:
             sys.stderr.write("\n".join(lines) + "\n")
+    return r.stderr
+
+
+def scratch_kernels(remarks: str) -> list[tuple[str, int]]:
+    """(kernel, bytes per lane) for every kernel whose resource remark shows
+    private (scratch) memory: a stack frame or spills, which turn every wave's
+    launch into a scratch allocation and cost the MoE layer several times
+    its time (a pointer conditional once copied the argument block there)."""
+    out, name = [], None
+    for line in remarks.splitlines():
+        if "Function Name:" in line:
+            name = line.split("Function Name:", 1)[1].split("[")[0].strip()
+        elif "ScratchSize [bytes/lane]:" in line and name:
+            n = int(line.split("ScratchSize [bytes/lane]:", 1)[1].split("[")[0])
+            if n:
+                out.append((name, n))
+    return out
 
 
 def _hip_object(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
     lang = ["-x", "hip"] if src.endswith(".hip") else ["-x", "hip"]
-    _run([HIPCC, *HIP_FLAGS, *lang, "-c", os.path.join(CSRC, src), "-o", obj])
+    remarks = _run([HIPCC, *HIP_FLAGS, "-Rpass-analysis=kernel-resource-usage", *lang, "-c",
+                    os.path.join(CSRC, src), "-o", obj])
+    bad = scratch_kernels(remarks)
+    if bad:
+        raise RuntimeError(f"{src}: kernels with scratch memory (bytes per lane): " +
+                           ", ".join(f"{n} ({b})" for n, b in bad[:8]))
     return obj
 
 
