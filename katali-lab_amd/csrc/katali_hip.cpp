@@ -283,6 +283,15 @@ int moe_impl(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, 
     a.dbg_gu = gu_dbg;
     a.err = g_err_dev;
     a.fsync = g_fsync;
+    // KATALI_HIP_TEST_SKEW=1, a test hook: workgroup 0's generation word of
+    // the XCD-sliced layer is set off before the launch, so its words carry a
+    // tag no other workgroup waits for and every wait of that call runs to
+    // its bound and expires (about a second); the sync then reports the
+    // expiry and clears the exchange area. Not for capture.
+    if (env_on("KATALI_HIP_TEST_SKEW") && !g_capturing) {
+        const hipError_t e = hipMemsetAsync(g_fsync + kq::FSYNC_X, 0xA5, 4, g_stream);
+        if (e != hipSuccess) return hip_fail(e, "test skew");
+    }
     // Eight slots take the XCD-sliced layer (one launch, every CU streaming
     // both phases; 12.0 us per layer at the 2048/768 top-8 shape against
     // 13.7 for kernels A and B); KATALI_HIP_XCD=0 keeps kernels A and B. The

@@ -87,6 +87,10 @@ class KataliHipMoeNorm(C.Structure):
                 ("norm_w", _vp), ("eps", _f32), ("xn_out", _vp), ("router", _vp), ("logits_out", _vp)]
 
 
+# error codes of include/katali_hip.h
+E_INVALID, E_NODEVICE, E_RUNTIME, E_UNSUPPORTED, E_NOMEM, E_TIMEOUT = -1, -2, -3, -4, -5, -6
+
+
 class HipError(RuntimeError):
     def __init__(self, rc: int, msg: str):
         super().__init__(f"katali_hip error {rc}: {msg}")

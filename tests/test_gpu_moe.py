@@ -294,6 +294,32 @@ def test_xcd_layer_matches_two_launches(hip, oracle, moes, case, monkeypatch):
         assert r <= 1e-6
 
 
+def test_xcd_wait_expiry_reports_and_recovers(hip, oracle, moes, monkeypatch):
+    """KATALI_HIP_TEST_SKEW=1, the library's test hook, sets workgroup 0's
+    generation word of the XCD-sliced layer off before a launch: its words
+    then carry a tag no other workgroup waits for, so the waits of that call
+    run to their bound and expire (each workgroup still ends normally, in
+    about a second). The next sync reports KATALI_HIP_E_TIMEOUT and the
+    library clears its exchange words; the calls after it, their generations
+    counting again from zero, give the layer's own bits."""
+    import katali_hip as K
+    hidden, ffn, n_expert, n_sel, shared, down_type = CASES[0]
+    m = moes(hidden, ffn, n_expert, shared, down_type)
+    rng = np.random.default_rng(21)
+    x = S.activation(rng, hidden)
+    logits = rng.standard_normal(n_expert).astype(np.float32)
+    set_mode(monkeypatch, "xcd")
+    y_ref = run_layer(hip, m, x, n_sel, logits=logits)[0]
+    monkeypatch.setenv("KATALI_HIP_TEST_SKEW", "1")
+    with pytest.raises(HipError) as err:
+        run_layer(hip, m, x, n_sel, logits=logits)
+    assert err.value.rc == K.E_TIMEOUT, err.value
+    monkeypatch.delenv("KATALI_HIP_TEST_SKEW")
+    for call in range(3):
+        y = run_layer(hip, m, x, n_sel, logits=logits)[0]
+        assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32)), call
+
+
 ROUTE_CASES = [
     # n_expert, n_sel, logits
     (128, 8, "ties"),      # integer logits: many equal values across the cut
