@@ -119,10 +119,12 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 // n_expert. (A 32-step binary search for the n_sel-th key plus a ranking
 // pass took ~2.5x the instructions: ~1.7 us of every wave's time at 256
 // experts.)
+// rounds (<= n_sel, wave-uniform): the ranks needed; rank r comes out of
+// round r, so a caller that needs only ranks < rounds stops there
 template <int C>
-__device__ __forceinline__ WaveRoute wave_topk(const MoeArgs &a, const float (&lv)[C]) {
+__device__ __forceinline__ WaveRoute wave_topk(const MoeArgs &a, const float (&lv)[C], int rounds) {
     const uint32_t lane = threadIdx.x & 63;
-    const int k = a.n_sel;
+    const int k = rounds;
     uint32_t key[C];
 #pragma unroll
     for (int i = 0; i < C; i++) key[i] = (lane + 64 * i < a.n_expert) ? logit_key(lv[i]) : 0u;
@@ -150,6 +152,10 @@ __device__ __forceinline__ WaveRoute wave_topk(const MoeArgs &a, const float (&l
     r.id = (int)lane < k ? id : -1;
     r.logit = (int)lane < k ? key_logit(mk) : 0.0f;
     return r;
+}
+template <int C>
+__device__ __forceinline__ WaveRoute wave_topk(const MoeArgs &a, const float (&lv)[C]) {
+    return wave_topk<C>(a, lv, a.n_sel);
 }
 
 // Routing weights w_r = exp(l_r - l_0) / sum_{j<n_sel} exp(l_j - l_0), the sum
@@ -343,10 +349,11 @@ __device__ __forceinline__ void route_issue(const MoeArgs &a, float (&lv)[C], Gu
         }
     }
 }
+// rounds: the ranks this wave needs (<= n_sel; -1: all of them)
 template <int C>
-__device__ __forceinline__ void route_finish(const MoeArgs &a, const float (&lv)[C], GuRoute &rt) {
+__device__ __forceinline__ void route_finish(const MoeArgs &a, const float (&lv)[C], GuRoute &rt, int rounds = -1) {
     if (a.logits && a.n_sel > 0) {
-        const WaveRoute r = wave_topk<C>(a, lv);
+        const WaveRoute r = wave_topk<C>(a, lv, rounds < 0 ? a.n_sel : min(rounds, a.n_sel));
         rt.eid = r.id;
         rt.logit = r.logit;
     }
@@ -624,7 +631,10 @@ __device__ __forceinline__ void gu_unit(const MoeArgs &a, uint32_t unit, uint8_t
                 xdv[i] = ld_u16(b);
             }
         }
-        route_finish<C>(a, lv, rt);
+        // a unit needs only its slot's expert (rank slot): slot + 1 rounds,
+        // none for the shared expert; the routing's publisher and the fused
+        // layer (whose down tiles take every slot) rank them all
+        route_finish<C>(a, lv, rt, FUSED || publisher ? -1 : (int)slot < a.n_sel ? (int)slot + 1 : 0);
     }
     // Drain the routing and x loads here, in one place: with loads issued
     // under branches the compiler cannot tell which registers are still
