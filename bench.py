@@ -1017,10 +1017,13 @@ def main():
         unit_ms = res["ms_per_step"]
         unit_bytes = res["bytes_per_token"]
         metric = "decode token HBM GB/s (% of ~8 TB/s peak) + tok/s: MoE FFN chain, LM head and argmax on device"
-        steps_desc = ("one launch for residual add + RMSNorm + F32 router, then the MoE layer's two"
+        layer = layer_kernels(hip, hidden, ffn, n_expert, n_sel + (1 if shared else 0), shared)
+        one = layer.startswith("k_moe_xcd")
+        steps_desc = ("one launch for residual add + RMSNorm + F32 router, then the MoE layer"
                       if not args.normed_layer else
-                      "two launches (katali_hip_moe_layer_normed: kernel A forms the residual add, RMSNorm and "
-                      "F32 router rows itself and exchanges the logits on the device, then kernel B)")
+                      "katali_hip_moe_layer_normed: the residual add, RMSNorm and F32 router rows in the layer's "
+                      "own prologue, the logits exchanged on the device" +
+                      (" (k_moe_xcd: one launch)" if one else " (kernel A, then kernel B)"))
         config = {
             "workload": f"{args.workload}: whole decode tokens of {base} with attention aside: per layer "
                         f"{steps_desc}; router {n_expert}x{hidden} F32, the MoE layer routed on the "
@@ -1030,11 +1033,11 @@ def main():
             "layers": L, "hidden": hidden, "ffn": ffn, "n_expert": n_expert, "n_sel": n_sel, "vocab": vocab,
             "bytes_per_token": res["bytes_per_token"], "parallelism": "single GPU",
         }
-        layer = layer_kernels(hip, hidden, ffn, n_expert, n_sel + (1 if shared else 0), shared)
         kernel = (f"whole token graph (per layer k_norm_router + the MoE layer, {layer}; then 4 launches: output "
                   "norm, head, argmax)" if not args.normed_layer else
-                  "whole token graph (2 per layer + 4 launches: k_moe_gu with the norm and router, k_moe_down; "
-                  "output norm, head, argmax)")
+                  "whole token graph (per layer " +
+                  ("k_moe_xcd with the norm and router in its prologue, one launch" if one else
+                   "k_moe_gu with the norm and router, k_moe_down") + "; output norm, head, argmax)")
         extra = {"tok_s": round(res["tok_s"], 2)}
     elif args.workload == "moe48duty":
         res, shape = bench_duty(hip, "moe48", args.steps, args.warmup)

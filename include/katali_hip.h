@@ -197,14 +197,17 @@ typedef struct KataliHipMoeRoute {
 int katali_hip_moe_layer(const KataliHipMoe *moe, const KataliHipMoeRoute *route,
                          const float *x_dev, const void *xq8_dev, float *y_dev);
 
-/* The steps before a MoE layer and the layer, in two launches where the
- * separate calls take three: katali_hip_rmsnorm_matvec_f32(x, delta, scale,
+/* The steps before a MoE layer and the layer, in one launch for the eight-slot
+ * shapes that katali_hip_moe_layer runs as one (the XCD-sliced layer; unless
+ * KATALI_HIP_XCD=0) and two for the others, where the separate calls take one
+ * more: katali_hip_rmsnorm_matvec_f32(x, delta, scale,
  * x_out, norm_w, hidden, eps, xn_out, router, n_expert, logits_out)
  * followed by katali_hip_moe_layer routed from those logits (n_sel experts,
  * ids_out / weights_out optional) on xn, with every output bit-identical to
  * that pair's (V/src/gguf_model.c:677-683, the F32 router product, the MoE
- * layer). Kernel A forms the residual step, the norm and the router rows in
- * its own workgroups and exchanges the logits between them on the device
+ * layer). The layer's first kernel forms the residual step, the norm and the
+ * router rows in its own workgroups and exchanges the logits between them on
+ * the device
  * (its workgroups wait for each other: on a device busy with other work the
  * wait can expire, reported as KATALI_HIP_E_TIMEOUT by the next
  * katali_hip_sync, the outputs then invalid). When kernel A has more

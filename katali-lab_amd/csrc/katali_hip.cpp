@@ -747,7 +747,8 @@ int katali_hip_moe_layer_normed(const KataliHipMoe *m, const KataliHipMoeNorm *n
     a.nxn_out = xn;
     a.router = w;
     a.logits_out = lg;
-    return launched(kq::launch_moe_normed(a, g_nbuf, g_nbuf + 4096, g_stream), "moe normed launch");
+    return launched(kq::launch_moe_normed(a, g_nbuf, g_nbuf + 4096, g_stream, nullptr, !env_off("KATALI_HIP_XCD")),
+                    "moe normed launch");
 }
 
 int katali_hip_moe_layer_debug(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, const void *xq,

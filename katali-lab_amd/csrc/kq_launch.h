@@ -150,8 +150,10 @@ hipError_t launch_moe(const MoeArgs &a, hipStream_t s, bool allow_fused = false,
 // values [slot][ffn <= 1024], then from FSYNC_XP its unweighted down
 // partials [slot][hidden], then with the shared expert in 128-value units
 // from FSYNC_XS each XCD's copy of its unit's h [xcd][128] and from
-// FSYNC_XSP the units' unweighted down partials [unit][hidden]; each value
-// one 8-byte word {float, generation}. Each exchange has its own generations, so no
+// FSYNC_XSP the units' unweighted down partials [unit][hidden]; from
+// FSYNC_XR, with the steps before the layer in its prologue, FSYNC_REP
+// copies of its router logits [512] (an area of its own: its generations
+// are the XCD layer's); each value one 8-byte word {float, generation}. Each exchange has its own generations, so no
 // word one of them writes can pass for another's.
 constexpr uint32_t FSYNC_H = 64;
 constexpr uint32_t FUSED_MAX_G = 256;   // workgroups of the fused layer
@@ -167,7 +169,8 @@ constexpr uint32_t FSYNC_XP = FSYNC_XH + 2 * XCD_SLOTS * XCD_MAX_FFN;
 constexpr uint32_t XCD_MAX_UNITS = 4;   // the shared expert's 128-value units (ffn <= 512)
 constexpr uint32_t FSYNC_XS = FSYNC_XP + 2 * XCD_SLOTS * XCD_MAX_HIDDEN;
 constexpr uint32_t FSYNC_XSP = FSYNC_XS + 2 * XCD_SLOTS * 128;
-constexpr uint32_t fsync_words() { return FSYNC_XSP + 2 * XCD_MAX_UNITS * XCD_MAX_HIDDEN; }
+constexpr uint32_t FSYNC_XR = FSYNC_XSP + 2 * XCD_MAX_UNITS * XCD_MAX_HIDDEN;
+constexpr uint32_t fsync_words() { return FSYNC_XR + FSYNC_REP * 2 * 512; }
 static_assert(FSYNC_H + 2 * 9 * FUSED_MAX_G <= FSYNC_R, "exchange areas overlap");
 // The steps before the layer and the layer in two launches (MoeArgs' n*
 // fields and router set, n_sel >= 1, hidden <= 4096): kernel A forms the
@@ -177,7 +180,10 @@ static_assert(FSYNC_H + 2 * 9 * FUSED_MAX_G <= FSYNC_R, "exchange areas overlap"
 // When the router rows do not spread over kernel A's workgroups (more than
 // 4 rows each), launch_norm_router into xn_buf / logits_buf first, then
 // launch_moe. *merged tells which ran.
-hipError_t launch_moe_normed(MoeArgs a, float *xn_buf, float *logits_buf, hipStream_t s, bool *merged = nullptr);
+// allow_xcd: eight-slot layers of the XCD-sliced layer's shapes run as that
+// layer with the steps before it in its prologue, in one launch.
+hipError_t launch_moe_normed(MoeArgs a, float *xn_buf, float *logits_buf, hipStream_t s, bool *merged = nullptr,
+                             bool allow_xcd = false);
 // Top-n_sel routing of n_tokens rows of logits [n_tokens][n_expert] (<= 512
 // experts, 1 <= n_sel <= min(16, n_expert)): ids / weights [n_tokens][n_sel],
 // each row as the single-token layer routes it.

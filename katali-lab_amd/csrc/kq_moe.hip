@@ -388,9 +388,11 @@ __host__ __device__ constexpr uint32_t normed_area_bytes(uint32_t H) {
     return 4 * (H + 64) * (1 + NORMED_MAX_R) + 32 + 128;
 }
 
+// gen: this call's exchange generation (its load issued by the caller
+// before anything else); xr: the logits words, FSYNC_REP copies of 512.
 template <int NB, int C, int NT, int XPT>
 __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area, uint32_t U, GuRoute &rt,
-                                                float4 (&xv)[XPT]) {
+                                                float4 (&xv)[XPT], uint32_t gen, uint32_t *xr) {
     constexpr uint32_t H = 256 * NB;
     constexpr uint32_t KN = H <= 2048 ? 2 : 4;   // k_norm_router's float4 per thread
     constexpr uint32_t Q4 = H / 4;
@@ -407,7 +409,6 @@ __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area,
     float *rtl = (float *)(rte + 16);
     auto at = [](uint32_t c) { return (c & 15) * TS + (c >> 4); };
     const uint32_t R = (a.n_expert + U - 1) / U;   // the host keeps R <= NORMED_MAX_R
-    const uint32_t gen = ld_dev(a.fsync + 1);        // issued first, used last
 
     // 1. every load: x, delta and the norm weights (threads < 256, whole
     //    waves), the router rows (all threads; clamped)
@@ -511,12 +512,12 @@ __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area,
         // + 0.0f: a zero sum's sign as k_norm_router leaves it
         const float logit = hsum16_avx2_order(acc) + 0.0f;   // every lane of the row holds it
         if (lane == 0 && a.logits_out) a.logits_out[r] = logit;
-        st_dev2(a.fsync + FSYNC_R + 2 * (512 * lane + r), ((uint64_t)tag << 32) | __float_as_uint(logit));
+        st_dev2(xr + 2 * (512 * lane + r), ((uint64_t)tag << 32) | __float_as_uint(logit));
     }
     // 5. wave 0: every row's word (from this workgroup's copy), the routing
     //    from those logits, into LDS for the other waves
     if (wave == 0) {
-        const uint32_t *rep = a.fsync + FSYNC_R + 2 * 512 * (w % FSYNC_REP);
+        const uint32_t *rep = xr + 2 * 512 * (w % FSYNC_REP);
         uint64_t va[C], vb[C];
         auto issue = [&](uint64_t *o) {
 #pragma unroll
@@ -612,7 +613,7 @@ __device__ __forceinline__ void gu_unit(const MoeArgs &a, uint32_t unit, uint8_t
     uint32_t xqv[XPT], xdv[XPT];
     if constexpr (NORMED) {
         // the steps before the layer, here: xn and the routing from its logits
-        normed_prologue<NB, C, NT, XPT>(a, lds + L.scl, gridDim.x, rt, xv);
+        normed_prologue<NB, C, NT, XPT>(a, lds + L.scl, gridDim.x, rt, xv, ld_dev(a.fsync + 1), a.fsync + FSYNC_R);
     } else {
         // every wave routes on its own: no barrier before its weight loads
         // (routing by rank over the workgroup, 8 threads per expert, measured
@@ -1509,10 +1510,13 @@ constexpr int XCD_HW = 4;                // h words per polling thread at most: 
 // (rows past R in the last of them are loaded and dropped); the others stage
 // x with them. `down` issues the caller's down loads (after the wave's dots,
 // or once x is staged on waves without rows). Leaves the R gate/up values in
-// LDS at lds + lds_a(..).gu.
-template <int NB, int C, int IW, int IWS, class Down>
+// LDS at lds + lds_a(..).gu. NORMED: the steps before the layer first
+// (normed_prologue, with the caller's generation gen and the logits words
+// at FSYNC_XR); x is the normalized vector it forms, the routing comes from
+// its logits.
+template <int NB, int C, int IW, int IWS, class Down, bool NORMED = false>
 __device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_t li, uint8_t *lds, GuRoute &rt,
-                                        Down down, uint32_t shb = 0, bool sh_dbg = false) {
+                                        Down down, uint32_t shb = 0, bool sh_dbg = false, uint32_t gen = 0) {
     constexpr int RW = 4;                      // rows per wave (kernel A's at these widths)
     static_assert(a1_rw<NB>() == RW, "gu_part: kernel A's 4-row waves");
     constexpr int R = 2 * IW + 2 * IWS, GW = (R + RW - 1) / RW;   // rows, waves with rows
@@ -1532,7 +1536,9 @@ __device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_
     constexpr int XPT = (XTASKS + NT - 1) / NT;
     float4 xv[XPT];
     uint32_t xqv[XPT], xdv[XPT];
-    {
+    if constexpr (NORMED) {
+        normed_prologue<NB, C, NT, XPT>(a, lds + L.scl, XCD_G, rt, xv, gen, a.fsync + FSYNC_XR);
+    } else {
         float lv[C];
         route_issue<C>(a, lv, rt);
         if (a.xq == nullptr) {
@@ -1593,7 +1599,7 @@ __device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_
         for (int k = 0; k < LPG; k++) q[k] = ld16(chunk(k));
     }
     if (slot == 0 && li == 0 && wave == 0)
-        route_publish(a, rt.eid, a.logits && a.n_sel > 0 ? route_weight(rt.logit, a.n_sel) : rt.w);
+        route_publish(a, rt.eid, (NORMED || a.logits) && a.n_sel > 0 ? route_weight(rt.logit, a.n_sel) : rt.w);
 
     // x -> q8_1 in LDS while the weights stream in
     const Act xa = act_carve(lds + L.xact, a.hidden);
@@ -1693,7 +1699,7 @@ __device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_
 // partial per row and unit. Wave 0 sums, per row, the eight slots in rank
 // order and then the U shared partials in unit order, weight 1 (the shared
 // expert enters last, as in kernel B).
-template <int NB, int C, class QD, int S, int IPL, int IW, bool SH>
+template <int NB, int C, class QD, int S, int IPL, int IW, bool SH, bool NORMED>
 __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
     constexpr uint32_t NT = a1_threads<NB>();
     constexpr uint32_t P = S / QD::IPB;
@@ -1745,7 +1751,8 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
                 rawS = QD::load(a.down_sh + (uint64_t)rowS * rbd + bkS * QD::BB, (int)itemS);
         }
     };
-    gu_part<NB, C, IW, IWS>(a, xs, li, lds, rt, load_down, 128 * u + IWS * li, part == 0);
+    gu_part<NB, C, IW, IWS, decltype(load_down), NORMED>(a, xs, li, lds, rt, load_down, 128 * u + IWS * li,
+                                                         part == 0, gen);
 
     uint32_t tag = gen;
     asm volatile("" : "+v"(tag));
@@ -1874,7 +1881,7 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
     // 4. wave 0: rows row0 + xs * TRC + c (c < TRC) over the eight slots, then
     //    the shared expert's U partials
     if (wave == 0) {
-        float rw = a.logits && a.n_sel > 0 ? route_weight(rt.logit, a.n_sel) : rt.w;
+        float rw = (NORMED || a.logits) && a.n_sel > 0 ? route_weight(rt.logit, a.n_sel) : rt.w;
         rw = (int)lane < a.n_sel ? rw : ((int)lane == a.n_sel && a.has_shared ? 1.0f : 0.0f);
         if (lane == 0) st_dev(gw, tag);   // gen was read at the start: advance it now
         const uint32_t q = lane / TRC, c = lane % TRC;   // lane: slot (or unit) q, row c
@@ -1927,42 +1934,45 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
     }
 }
 
-template <int NB, int C, class QD, int S, int IPL, int IW, bool SH>
+template <int NB, int C, class QD, int S, int IPL, int IW, bool SH, bool NORMED>
 static hipError_t go_xcd(const MoeArgs &a, hipStream_t s) {
-    const uint32_t lds = lds_a(a.hidden, NB).total + (SH ? 2 : 1) * act_bytes(32 * IW);
+    uint32_t lds = lds_a(a.hidden, NB).total + (SH ? 2 : 1) * act_bytes(32 * IW);
+    // the normed prologue's area starts at the scale records, which are
+    // written only after its last read
+    if (NORMED) lds = max(lds, lds_a(a.hidden, NB).scl + normed_area_bytes(a.hidden));
     if (lds > 64 * 1024) {
-        const hipError_t e = hipFuncSetAttribute((const void *)k_moe_xcd<NB, C, QD, S, IPL, IW, SH>,
+        const hipError_t e = hipFuncSetAttribute((const void *)k_moe_xcd<NB, C, QD, S, IPL, IW, SH, NORMED>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL((k_moe_xcd<NB, C, QD, S, IPL, IW, SH>), dim3(XCD_G), dim3(a1_threads<NB>()), lds, s, a);
+    hipLaunchKernelGGL((k_moe_xcd<NB, C, QD, S, IPL, IW, SH, NORMED>), dim3(XCD_G), dim3(a1_threads<NB>()), lds, s, a);
     return hipGetLastError();
 }
 // 16 lanes per down row: Q6_K 4 items x 4 block slots (ffn <= 1024: one
 // block per lane), Q4_K 8 items x 2 block slots (up to two)
-template <int NB, int C, int IW, bool SH>
+template <int NB, int C, int IW, bool SH, bool NORMED>
 static hipError_t go_xcd_q(const MoeArgs &a, hipStream_t s) {
-    if (a.down_type == T_Q6_K) return go_xcd<NB, C, Q6K, 16, 1, IW, SH>(a, s);
-    if constexpr (IW <= 16) return go_xcd<NB, C, Q4K, 16, 1, IW, SH>(a, s);
-    else return go_xcd<NB, C, Q4K, 16, 2, IW, SH>(a, s);
+    if (a.down_type == T_Q6_K) return go_xcd<NB, C, Q6K, 16, 1, IW, SH, NORMED>(a, s);
+    if constexpr (IW <= 16) return go_xcd<NB, C, Q4K, 16, 1, IW, SH, NORMED>(a, s);
+    else return go_xcd<NB, C, Q4K, 16, 2, IW, SH, NORMED>(a, s);
 }
-template <int NB, int C, bool SH>
+template <int NB, int C, bool SH, bool NORMED>
 static hipError_t go_xcd_f(const MoeArgs &a, hipStream_t s) {
     switch (a.ffn) {
-        case 256: return go_xcd_q<NB, C, 8, SH>(a, s);
-        case 512: return go_xcd_q<NB, C, 16, SH>(a, s);
+        case 256: return go_xcd_q<NB, C, 8, SH, NORMED>(a, s);
+        case 512: return go_xcd_q<NB, C, 16, SH, NORMED>(a, s);
         case 768:
-            if constexpr (!SH) return go_xcd_q<NB, C, 24, SH>(a, s);   // the shared units must divide the eight XCDs
+            if constexpr (!SH) return go_xcd_q<NB, C, 24, SH, NORMED>(a, s);   // the shared units must divide the eight XCDs
             else return hipErrorNotSupported;
         case 1024:
-            if constexpr (!SH) return go_xcd_q<NB, C, 32, SH>(a, s);   // shared rows would not fit 64 per workgroup
+            if constexpr (!SH) return go_xcd_q<NB, C, 32, SH, NORMED>(a, s);   // shared rows would not fit 64 per workgroup
             else return hipErrorNotSupported;
         default: return hipErrorNotSupported;
     }
 }
-template <int NB, bool SH>
+template <int NB, bool SH, bool NORMED = false>
 static hipError_t go_xcd_c(const MoeArgs &a, hipStream_t s) {
-    return a.n_expert <= 128 ? go_xcd_f<NB, 2, SH>(a, s) : go_xcd_f<NB, 4, SH>(a, s);
+    return a.n_expert <= 128 ? go_xcd_f<NB, 2, SH, NORMED>(a, s) : go_xcd_f<NB, 4, SH, NORMED>(a, s);
 }
 // hipErrorNotSupported when the shape does not fit the XCD-sliced layer:
 // eight slots (one per XCD), or with shared_units eight routed experts plus
@@ -2187,11 +2197,28 @@ static hipError_t go_a_any(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
     }
 }
 
-hipError_t launch_moe_normed(MoeArgs a, float *xn_buf, float *logits_buf, hipStream_t s, bool *merged) {
+hipError_t launch_moe_normed(MoeArgs a, float *xn_buf, float *logits_buf, hipStream_t s, bool *merged,
+                             bool allow_xcd) {
     if (merged) *merged = false;
     if (!a.router || a.n_sel < 1 || a.n_expert > MAX_EXPERT || a.n_sel > MAX_SEL || a.hidden > 4096)
         return hipErrorInvalidValue;
     const uint32_t n_slots = (uint32_t)a.n_sel + (a.has_shared ? 1u : 0u);
+    // eight slots on 256 CUs: the XCD-sliced layer with the steps before it
+    // in its prologue, one launch (each workgroup dots at most one router
+    // row at <= 256 experts)
+    if (allow_xcd && a.fsync && n_slots == XCD_SLOTS && (a.hidden == 1024 || a.hidden == 2048) && a.ffn <= 1024 &&
+        a.n_expert <= XCD_G && device_cu_count() == (int)XCD_G) {
+        MoeArgs b = a;
+        b.x = nullptr;
+        b.xq = nullptr;
+        b.logits = nullptr;
+        b.step = nullptr;
+        const hipError_t e = a.hidden == 2048 ? go_xcd_c<8, false, true>(b, s) : go_xcd_c<4, false, true>(b, s);
+        if (e != hipErrorNotSupported) {
+            if (merged) *merged = e == hipSuccess;
+            return e;
+        }
+    }
     const uint32_t U = n_slots * (a.ffn / 32);
     // kernel A's workgroups wait for each other's router rows: all of them
     // must be resident at once (one per CU at most), each with <= 4 rows

@@ -6,7 +6,11 @@ bit-identical: the new residual, xn, the logits, the routing and y. Shapes
 cover the merged path (router rows spread over kernel A's workgroups, one or
 several rows each) and the fallback (more than four rows per workgroup), with
 and without the residual step and the shared expert; queued layers, graph
-replays with eager work between them, and bad arguments."""
+replays with eager work between them, and bad arguments. The tests run the
+layer as kernels A and B (KATALI_HIP_XCD=0) unless they name the XCD mode:
+eight-slot layers then run as the XCD-sliced layer with the steps before it
+in its prologue (one launch), against the same steps as separate calls whose
+layer is the XCD-sliced one too."""
 import numpy as np
 import pytest
 
@@ -25,6 +29,25 @@ CASES = [
     (1024, 256, 512, 2, False, Q6_K, 1.0),     # 16 workgroups for 512 rows: the two-step fallback
     (512, 256, 60, 3, False, Q6_K, 0.25),      # rows not a multiple of the workgroups
 ]
+
+
+XCD_CASES = [
+    # eight slots: hidden 1024 or 2048, ffn <= 1024, <= 256 experts
+    (2048, 768, 128, 8, False, Q6_K, 1.0),     # the decode layer
+    (2048, 768, 128, 8, False, Q6_K, None),
+    (2048, 512, 256, 7, True, Q6_K, 0.5),      # seven routed and the shared expert; one router row per workgroup
+    (1024, 1024, 64, 8, False, Q4_K, 1.0),     # narrow hidden, the widest ffn, Q4_K down
+    (1024, 256, 200, 8, False, Q6_K, 0.25),    # rows not a multiple of 64
+]
+
+
+def set_mode(monkeypatch, mode):
+    monkeypatch.setenv("KATALI_HIP_XCD", "1" if mode == "xcd" else "0")
+
+
+def case_id(c):
+    return (f"h{c[0]}_f{c[1]}_e{c[2]}_k{c[3]}{'_sh' if c[4] else ''}"
+            f"{'_q4down' if c[5] == Q4_K else ''}_s{c[6]}")
 
 
 class Layer:
@@ -85,11 +108,12 @@ def layers(hip):
     return get
 
 
-@pytest.mark.parametrize("case", CASES, ids=[f"h{c[0]}_f{c[1]}_e{c[2]}_k{c[3]}{'_sh' if c[4] else ''}"
-                                             f"{'_q4down' if c[5] == Q4_K else ''}_s{c[6]}" for c in CASES])
-def test_normed_layer_matches_separate_steps(hip, layers, case):
-    hidden, ffn, n_expert, n_sel, shared, down, scale = case
-    print(f"[moe-normed] case={case}", flush=True)
+@pytest.mark.parametrize("case", [("two_launch", c) for c in CASES] + [("xcd", c) for c in XCD_CASES],
+                         ids=[f"two_launch-{case_id(c)}" for c in CASES] + [f"xcd-{case_id(c)}" for c in XCD_CASES])
+def test_normed_layer_matches_separate_steps(hip, layers, case, monkeypatch):
+    mode, (hidden, ffn, n_expert, n_sel, shared, down, scale) = case
+    set_mode(monkeypatch, mode)
+    print(f"[moe-normed] mode={mode} case={case[1]}", flush=True)
     L = layers(hidden, ffn, n_expert, shared, down)
     rng = np.random.default_rng(hidden + n_expert + n_sel)
     x = hip.to_device(rng.standard_normal(hidden).astype(np.float32))
@@ -111,9 +135,12 @@ def test_normed_layer_matches_separate_steps(hip, layers, case):
         assert np.any(y != 0)
 
 
-def test_normed_layers_queued_back_to_back(hip, layers):
+@pytest.mark.parametrize("mode", ["two_launch", "xcd"])
+def test_normed_layers_queued_back_to_back(hip, layers, mode, monkeypatch):
     """24 normed layers queued without a wait (each call's exchange a new
     generation): every one equals its separate-steps run."""
+    set_mode(monkeypatch, mode)
+    print(f"[moe-normed] queued mode={mode}", flush=True)
     hidden, ffn, n_expert, n_sel = 2048, 768, 128, 8
     L = layers(hidden, ffn, n_expert, False, Q6_K)
     rng = np.random.default_rng(9)
@@ -129,11 +156,13 @@ def test_normed_layers_queued_back_to_back(hip, layers):
             assert same(outs[i][k], want[k], hidden), (i, name)
 
 
-def test_normed_layer_graph_replays(hip, layers):
+@pytest.mark.parametrize("mode,n_sel", [("two_launch", 8), ("xcd", 7)])
+def test_normed_layer_graph_replays(hip, layers, mode, n_sel, monkeypatch):
     """Two chained normed layers (the second's residual step adds the first's
     y) captured once and replayed with eager work between the replays: every
     replay equals the eager run."""
-    hidden, ffn, n_expert, n_sel = 2048, 512, 256, 8
+    set_mode(monkeypatch, mode)
+    hidden, ffn, n_expert = 2048, 512, 256
     L = layers(hidden, ffn, n_expert, True, Q6_K)
     rng = np.random.default_rng(10)
     x0 = hip.to_device(rng.standard_normal(hidden).astype(np.float32))
