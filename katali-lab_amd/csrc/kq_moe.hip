@@ -1778,14 +1778,34 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
     //    first, then the unit's), quantized where 32 lanes hold one 32-value
     //    block (kernel A's quantizer)
     uint32_t spins = 0;
-    const uint32_t first_poller = NT - 64 * XCD_POLL_WAVES;
+    constexpr uint32_t first_poller = NT - 64 * XCD_POLL_WAVES;
     const bool poller = tid >= first_poller;   // whole waves
     const uint32_t LT = lds_a(a.hidden, NB).total;
     const Act act = act_carve(lds + LT, F);
     const Act actS = act_carve(lds + LT + act_bytes(F), F);   // SH only: the unit's blocks
+    // The pollers' down items go to the helper waves through LDS (over the
+    // scale records, dead once the gate/up dots are done), and the pollers
+    // leave after h is staged. Their last poll round is still in flight
+    // when h is complete; a wave that waited on its own down items after it
+    // would wait on that round too (the load counter retires in issue order),
+    // about 0.6 us on the layer's critical path.
+    constexpr uint32_t HELP0 = 4 * 64;   // waves 4 .. 4 + XCD_POLL_WAVES - 1 (wave 0 combines; SH: 0, 1 dot the unit)
+    static_assert(first_poller % S == 0 && HELP0 % S == 0 && HELP0 + 64 * XCD_POLL_WAVES <= first_poller &&
+                      (!SH || ((RS * IH + 63) & ~63u) <= HELP0),
+                  "XCD layer helper waves");
+    static_assert(64 * XCD_POLL_WAVES * IPL * sizeof(typename QD::Raw) <= 64 * NB * 64, "XCD layer down stash");
+    typename QD::Raw *stash = (typename QD::Raw *)(lds + lds_a(a.hidden, NB).scl);
+    // The poll rounds' registers stay allocated to the pollers' end (an empty
+    // use there), so the quantizer never reuses the registers that the last
+    // round, never waited for, still loads into.
+    constexpr int NW = (HW + 64 * XCD_POLL_WAVES - 1) / (64 * XCD_POLL_WAVES);
+    uint64_t va[NW], vb[NW];
+#pragma unroll
+    for (int i = 0; i < NW; i++) va[i] = vb[i] = 0;
     if (poller) {
         const uint32_t pt = tid - first_poller;
-        constexpr int NW = (HW + 64 * XCD_POLL_WAVES - 1) / (64 * XCD_POLL_WAVES);
+#pragma unroll
+        for (int i = 0; i < IPL; i++) stash[IPL * pt + i] = raw[i];
         auto word = [&](uint32_t e) { return e < F ? hx + 2 * e : hxs + 2 * (e - F); };
         // Two rounds in flight: the next round goes out before the previous
         // one is checked, so a word is sampled twice per round trip. A word
@@ -1794,7 +1814,7 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
         // instruction, the value dropped), so late rounds fetch only what
         // is still missing while the down rows stream. The loads themselves
         // are unconditional, so both rounds stay countable in flight.
-        uint64_t hv[NW], va[NW], vb[NW];
+        uint64_t hv[NW];
         uint32_t need = 0;   // bit i: word pt + 256 i still to see
 #pragma unroll
         for (int i = 0; i < NW; i++)
@@ -1860,16 +1880,28 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
     __syncthreads();
 
     // the tile's unweighted down partials (and, with SH, the unit's shared ones)
-    float x = 0.0f;
+    auto tile_dot = [&](const typename QD::Raw *rw, uint32_t row) {   // whole waves
+        float x = 0.0f;
 #pragma unroll
-    for (int i = 0; i < IPL; i++) {
-        const uint32_t blk = bs + P * i;
-        const float d = QD::dot_q8(raw[i], (int)item, act, min(blk, NBK - 1));
-        x += blk < NBK ? d : 0.0f;
+        for (int i = 0; i < IPL; i++) {
+            const uint32_t blk = bs + P * i;
+            const float d = QD::dot_q8(rw[i], (int)item, act, min(blk, NBK - 1));
+            x += blk < NBK ? d : 0.0f;
+        }
+        x = group_sum<S>(x);
+        if (row < TRX && s == 0)
+            st_dev2(a.fsync + FSYNC_XP + 2 * (xs * H + row0 + row), ((uint64_t)tag << 32) | __float_as_uint(x));
+    };
+    if (!poller) {
+        tile_dot(raw, r);
+        if (tid >= HELP0 && tid < HELP0 + 64 * XCD_POLL_WAVES) {   // a poller's items: same lane in its row
+            const uint32_t pt = tid - HELP0;
+            typename QD::Raw rp[IPL];
+#pragma unroll
+            for (int i = 0; i < IPL; i++) rp[i] = stash[IPL * pt + i];
+            tile_dot(rp, (first_poller + pt) / S);
+        }
     }
-    x = group_sum<S>(x);
-    if (r < TRX && s == 0)
-        st_dev2(a.fsync + FSYNC_XP + 2 * (xs * H + row0 + r), ((uint64_t)tag << 32) | __float_as_uint(x));
     if constexpr (SH) {
         if (tid < ((RS * IH + 63) & ~63u)) {   // whole waves
             const float xsh = group_sum<IH>(QD::dot_q8(rawS, (int)itemS, actS, bkS));
@@ -1931,6 +1963,10 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
             y = fmaf(1.0f, sh, y);   // the shared expert, last
         }
         if (lane < TRC) a.y[row0 + xs * TRC + lane] = y;
+    }
+    if (poller) {
+#pragma unroll
+        for (int i = 0; i < NW; i++) asm volatile("" ::"v"(va[i]), "v"(vb[i]));
     }
 }
 
