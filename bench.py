@@ -93,13 +93,13 @@ TOKEN_WORKLOADS = {
 def xcd_layer(hip, hidden, ffn, n_expert, n_slots, shared=False):
     """Whether the library runs this layer shape as the XCD-sliced one-launch
     layer (k_moe_xcd) rather than kernels A and B: the rule launch_moe
-    applies (eight slots, or with KATALI_HIP_XCD_SHARED=1 eight routed
-    experts plus the shared expert with ffn 256 or 512; hidden 1024 or 2048,
+    applies (eight slots, or eight routed experts plus the shared expert with
+    ffn 256 or 512 unless KATALI_HIP_XCD_SHARED=0; hidden 1024 or 2048,
     ffn <= 1024, <= 256 experts, a 256-CU device, KATALI_HIP_XCD not 0)."""
     if os.environ.get("KATALI_HIP_XCD", "1")[:1] in ("0", "n", "N"):
         return False
     spread = (n_slots == 9 and shared and ffn in (256, 512)
-              and os.environ.get("KATALI_HIP_XCD_SHARED", "")[:1] in ("1", "y", "Y"))
+              and os.environ.get("KATALI_HIP_XCD_SHARED", "1")[:1] not in ("0", "n", "N"))
     return ((n_slots == 8 or spread) and hidden in (1024, 2048) and ffn <= 1024 and n_expert <= 256
             and " 256 CUs" in hip.status())
 

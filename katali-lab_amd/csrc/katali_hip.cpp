@@ -293,17 +293,18 @@ int moe_impl(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, 
         if (e != hipSuccess) return hip_fail(e, "test skew");
     }
     // Eight slots take the XCD-sliced layer (one launch, every CU streaming
-    // both phases; 12.0 us per layer at the 2048/768 top-8 shape against
-    // 13.7 for kernels A and B); KATALI_HIP_XCD=0 keeps kernels A and B. The
-    // other one-launch layer is opt-in (KATALI_HIP_FUSED=1): measured slower
-    // than kernels A and B (its all-slots h exchange costs more than the
-    // launch it saves).
-    // Eight routed experts plus the shared expert can take it too, the shared
-    // expert in 128-value units (KATALI_HIP_XCD_SHARED=1): measured slower
-    // than kernels A and B at the 2048/512 top-8-of-256 shape.
+    // both phases; 11.6-11.9 us per layer at the 2048/768 top-8 shape
+    // against 13.7 for kernels A and B); KATALI_HIP_XCD=0 keeps kernels A and
+    // B. The other one-launch layer is opt-in (KATALI_HIP_FUSED=1): measured
+    // slower than kernels A and B (its all-slots h exchange costs more than
+    // the launch it saves).
+    // Eight routed experts plus the shared expert take it too, the shared
+    // expert in 128-value units (12.65 us per layer at the 2048/512
+    // top-8-of-256 shape against 13.5 for kernels A and B);
+    // KATALI_HIP_XCD_SHARED=0 keeps those on kernels A and B.
     const bool allow_fused = env_on("KATALI_HIP_FUSED");
     const bool allow_xcd = !env_off("KATALI_HIP_XCD");
-    const bool xcd_units = env_on("KATALI_HIP_XCD_SHARED");
+    const bool xcd_units = !env_off("KATALI_HIP_XCD_SHARED");
     rc = launched(kq::launch_moe(a, g_stream, allow_fused, nullptr, allow_xcd, xcd_units), "moe launch");
     if (rc) return rc;
     if (hq8_dbg) {

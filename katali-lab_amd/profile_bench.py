@@ -29,7 +29,7 @@ COPY_MIB = 256
 # kernels summed per workload unit; the first is launched once per unit
 KERNELS = {
     "moe48": ("k_moe_xcd",),
-    "moe40cold": ("k_moe_gu", "k_moe_down"),
+    "moe40cold": ("k_moe_xcd",),
     "gemv6144": ("k_gemv",),
     "qwen8b": ("k_moe_down", "k_moe_gu", "k_gemv_multi", "k_gemv"),
     "moe48tok": ("k_argmax_final", "k_norm_router", "k_moe_xcd", "k_rmsnorm", "k_gemv", "k_argmax_part"),
@@ -40,7 +40,8 @@ UNIT_NAME = {"moe48": "MoE layer", "moe40cold": "MoE layer", "gemv6144": "GEMV",
              "moebatch": "batched MoE layer (n_sel 8, 64 tokens)", "moe48tok": "decode token"}
 EXTRA_ARGS = {"moebatch": ["--batch-points", "8x64"]}
 PROFILE_NAME = {"moebatch": "batched_moe_moebatch_8x64", "moe48tok": "decode_token_moe48tok", "qwen8b": "k_gemv_k_moe_gu_k_moe_down_qwen8b"}
-# eight-slot layers run as k_moe_xcd unless KATALI_HIP_XCD=0 (--two-launch)
+# eight-slot layers (and eight routed experts plus the shared expert at ffn
+# 256 or 512) run as k_moe_xcd unless KATALI_HIP_XCD=0 (--two-launch)
 
 
 def run(cmd, log, extra_env=None):
@@ -116,7 +117,7 @@ def main():
                     help="the all-slots one-launch MoE layer (KATALI_HIP_FUSED=1, KATALI_HIP_XCD=0; moe48 and "
                          "moe40cold)")
     ap.add_argument("--two-launch", action="store_true",
-                    help="moe48: kernels A and B instead of the XCD-sliced layer (KATALI_HIP_XCD=0)")
+                    help="moe48, moe40cold: kernels A and B instead of the XCD-sliced layer (KATALI_HIP_XCD=0)")
     ap.add_argument("--one-stream", action="store_true",
                     help="moebatch: the grouped GEMM on the library stream (KATALI_HIP_ONE_STREAM=1), so "
                          "per-kernel times add up to the layer")
@@ -130,8 +131,8 @@ def main():
         extra_env = {"KATALI_HIP_FUSED": "1", "KATALI_HIP_XCD": "0"}
         kernels, profile_name, traffic_name = ("k_moe_fused",), "k_moe_fused_" + wl, "fused_" + wl
     if args.two_launch:
-        if wl != "moe48":
-            sys.exit("--two-launch applies to moe48")
+        if wl not in ("moe48", "moe40cold"):
+            sys.exit("--two-launch applies to moe48 and moe40cold")
         extra_env = {"KATALI_HIP_XCD": "0"}
         kernels, profile_name, traffic_name = ("k_moe_gu", "k_moe_down"), "k_moe_gu_k_moe_down_" + wl, "two_launch_" + wl
     if args.one_stream:

@@ -89,9 +89,8 @@ CASES = [
 XCD_CASES = [c for c in CASES if (c[3] + (1 if c[4] else 0) == 8 or (c[3] == 8 and c[4] and c[1] in (256, 512)))
              and c[0] in (1024, 2048) and c[1] <= 1024 and c[2] <= 256]
 # two_launch: kernels A and B; one_launch: k_moe_fused; xcd: the XCD-sliced
-# layer where the shape fits it (the default for eight slots; eight routed
-# experts plus the shared expert in 128-value units only with
-# KATALI_HIP_XCD_SHARED=1)
+# layer where the shape fits it (the default for eight slots and for eight
+# routed experts plus the shared expert in 128-value units; set explicitly)
 MODES = {"two_launch": {"KATALI_HIP_XCD": "0"}, "one_launch": {"KATALI_HIP_FUSED": "1", "KATALI_HIP_XCD": "0"},
          "xcd": {"KATALI_HIP_XCD_SHARED": "1"}}
 
