@@ -70,6 +70,18 @@ template <class... T>
 __device__ __forceinline__ void pin_args(T... v) {
     (pin_arg(v), ...);
 }
+// Materialize a register-held value at this point: it is computed (and any
+// load it comes from waited for) here, and later uses read these registers
+// instead of the computation being sunk past later code.
+template <class T>
+__device__ __forceinline__ void pin_vregs(T &v) {
+    static_assert(sizeof(T) % 4 == 0, "pin_vregs: whole dwords");
+    uint32_t w[sizeof(T) / 4];
+    __builtin_memcpy(w, &v, sizeof(T));
+#pragma unroll
+    for (uint32_t k = 0; k < sizeof(T) / 4; k++) asm volatile("" : "+v"(w[k]));
+    __builtin_memcpy(&v, w, sizeof(T));
+}
 __device__ __forceinline__ uint32_t ld4(const uint8_t *p) {
     uint32_t v;
     __builtin_memcpy(&v, p, 4);

@@ -1699,23 +1699,6 @@ __device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_
 // partial per row and unit. Wave 0 sums, per row, the eight slots in rank
 // order and then the U shared partials in unit order, weight 1 (the shared
 // expert enters last, as in kernel B).
-// One down item as the XCD layer's dots take it: the raw block bytes (for
-// the scales) and the values unpacked (h-independent work, done while h is
-// awaited); the pollers hand theirs to the helper waves in LDS, one uint4
-// plane per 16 bytes so that every access is lane-contiguous.
-template <class QD>
-struct XcdItem {
-    typename QD::Raw r;
-    typename QD::Unp u;
-};
-template <class QD>
-constexpr uint32_t xcd_item_planes() { return sizeof(XcdItem<QD>) / 16; }
-// the stash's offset: past kernel A's areas and the act areas of h (and of
-// the shared unit's h)
-__host__ __device__ inline uint32_t xcd_stash_off(uint32_t hidden, uint32_t nb, uint32_t ffn, bool sh) {
-    return (lds_a(hidden, nb).total + (sh ? 2 : 1) * act_bytes(ffn) + 15) & ~15u;
-}
-
 template <int NB, int C, class QD, int S, int IPL, int IW, bool SH, bool NORMED>
 __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
     constexpr uint32_t NT = a1_threads<NB>();
@@ -1800,42 +1783,33 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
     const uint32_t LT = lds_a(a.hidden, NB).total;
     const Act act = act_carve(lds + LT, F);
     const Act actS = act_carve(lds + LT + act_bytes(F), F);   // SH only: the unit's blocks
-    // The pollers' down items go to the helper waves through LDS, and the
-    // pollers leave after h is staged. Their last poll round is still in
-    // flight when h is complete; a wave that waited on its own down items
-    // after it would wait on that round too (the load counter retires in
-    // issue order), about 0.6 us on the layer's critical path. Every down
-    // item is unpacked while h is awaited, so only the dot products and the
-    // scales are left once it is staged.
-    constexpr uint32_t HELP0 = 4 * 64;   // waves 4 .. 4 + XCD_POLL_WAVES - 1 (wave 0 combines; SH: 0, 1 dot the unit)
-    static_assert(first_poller % S == 0 && HELP0 % S == 0 && HELP0 + 64 * XCD_POLL_WAVES <= first_poller &&
-                      (!SH || ((RS * IH + 63) & ~63u) <= HELP0),
-                  "XCD layer helper waves");
-    constexpr uint32_t SQ = xcd_item_planes<QD>(), NP = 64 * XCD_POLL_WAVES;
-    static_assert(sizeof(XcdItem<QD>) == 16 * SQ, "XCD layer item planes");
-    uint4 *stash = (uint4 *)(lds + xcd_stash_off(a.hidden, NB, F, SH));   // [IPL][SQ][NP]
-    XcdItem<QD> it[IPL];   // this thread's items (non-pollers: unpacked before h is staged)
-    // The poll rounds' registers stay allocated to the pollers' end (an empty
-    // use there), so the quantizer never reuses the registers that the last
-    // round, never waited for, still loads into.
+    // Every wave unpacks its down items here, while h is awaited (the
+    // pollers before their first poll), so only the dot products and the
+    // scales follow h. After that no wave waits on a load: the pollers'
+    // last round is still in flight when h is complete, and a wait on any
+    // older load would wait on it too (the load counter retires in issue
+    // order), about 0.6 us on the layer's critical path. For the same reason
+    // the poll rounds' registers stay allocated to the pollers' end (an
+    // empty use there), so nothing after the loop reuses a register that
+    // round still loads into.
+    typename QD::Unp un[IPL], unS;
+#pragma unroll
+    for (int i = 0; i < IPL; i++) {
+        un[i] = QD::unpack(raw[i]);
+        pin_vregs(raw[i]);
+        pin_vregs(un[i]);
+    }
+    if constexpr (SH) {   // (threads past the unit's waves: unused)
+        unS = QD::unpack(rawS);
+        pin_vregs(rawS);
+        pin_vregs(unS);
+    }
     constexpr int NW = (HW + 64 * XCD_POLL_WAVES - 1) / (64 * XCD_POLL_WAVES);
     uint64_t va[NW], vb[NW];
 #pragma unroll
     for (int i = 0; i < NW; i++) va[i] = vb[i] = 0;
-#pragma unroll
-    for (int i = 0; i < IPL; i++) {
-        it[i].r = raw[i];
-        it[i].u = QD::unpack(raw[i]);
-    }
     if (poller) {
         const uint32_t pt = tid - first_poller;
-#pragma unroll
-        for (int i = 0; i < IPL; i++) {
-            uint4 w[SQ];
-            __builtin_memcpy(w, &it[i], sizeof(w));
-#pragma unroll
-            for (uint32_t q = 0; q < SQ; q++) stash[(i * SQ + q) * NP + pt] = w[q];
-        }
         auto word = [&](uint32_t e) { return e < F ? hx + 2 * e : hxs + 2 * (e - F); };
         // Two rounds in flight: the next round goes out before the previous
         // one is checked, so a word is sampled twice per round trip. A word
@@ -1910,40 +1884,19 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
     __syncthreads();
 
     // the tile's unweighted down partials (and, with SH, the unit's shared ones)
-    auto lane_dot = [&](const XcdItem<QD> *xi) {
-        float x = 0.0f;
+    float x = 0.0f;
 #pragma unroll
-        for (int i = 0; i < IPL; i++) {
-            const uint32_t blk = bs + P * i;
-            const float d = QD::dot_q8_u(xi[i].r, xi[i].u, (int)item, act, min(blk, NBK - 1));
-            x += blk < NBK ? d : 0.0f;
-        }
-        return x;
-    };
-    auto publish = [&](float x, uint32_t row) {   // whole waves: x summed over the row's S lanes
-        x = group_sum<S>(x);
-        if (row < TRX && s == 0)
-            st_dev2(a.fsync + FSYNC_XP + 2 * (xs * H + row0 + row), ((uint64_t)tag << 32) | __float_as_uint(x));
-    };
-    if (tid >= HELP0 && tid < HELP0 + 64 * XCD_POLL_WAVES) {   // also a poller's items: same lane in its row
-        const uint32_t pt = tid - HELP0;
-        XcdItem<QD> ip[IPL];
-#pragma unroll
-        for (int i = 0; i < IPL; i++) {
-            uint4 w[SQ];
-#pragma unroll
-            for (uint32_t q = 0; q < SQ; q++) w[q] = stash[(i * SQ + q) * NP + pt];
-            __builtin_memcpy(&ip[i], w, sizeof(w));
-        }
-        const float x = lane_dot(it), xp = lane_dot(ip);   // independent: their latencies overlap
-        publish(x, r);
-        publish(xp, (first_poller + pt) / S);
-    } else if (!poller) {
-        publish(lane_dot(it), r);
+    for (int i = 0; i < IPL; i++) {
+        const uint32_t blk = bs + P * i;
+        const float d = QD::dot_q8_u(raw[i], un[i], (int)item, act, min(blk, NBK - 1));
+        x += blk < NBK ? d : 0.0f;
     }
+    x = group_sum<S>(x);
+    if (r < TRX && s == 0)
+        st_dev2(a.fsync + FSYNC_XP + 2 * (xs * H + row0 + r), ((uint64_t)tag << 32) | __float_as_uint(x));
     if constexpr (SH) {
         if (tid < ((RS * IH + 63) & ~63u)) {   // whole waves
-            const float xsh = group_sum<IH>(QD::dot_q8(rawS, (int)itemS, actS, bkS));
+            const float xsh = group_sum<IH>(QD::dot_q8_u(rawS, unS, (int)itemS, actS, bkS));
             if (sdown && tid % IH == 0)
                 st_dev2(a.fsync + FSYNC_XSP + 2 * (u * H + rowS), ((uint64_t)tag << 32) | __float_as_uint(xsh));
         }
@@ -2000,7 +1953,7 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
 
 template <int NB, int C, class QD, int S, int IPL, int IW, bool SH, bool NORMED>
 static hipError_t go_xcd(const MoeArgs &a, hipStream_t s) {
-    uint32_t lds = xcd_stash_off(a.hidden, NB, 32 * IW, SH) + 64 * XCD_POLL_WAVES * IPL * sizeof(XcdItem<QD>);
+    uint32_t lds = lds_a(a.hidden, NB).total + (SH ? 2 : 1) * act_bytes(32 * IW);
     // the normed prologue's area starts at the scale records, which are
     // written only after its last read
     if (NORMED) lds = max(lds, lds_a(a.hidden, NB).scl + normed_area_bytes(a.hidden));
