@@ -1819,6 +1819,8 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
         // is still missing while the down rows stream. The loads themselves
         // are unconditional, so both rounds stay countable in flight.
         uint64_t hv[NW];
+#pragma unroll
+        for (int i = 0; i < NW; i++) hv[i] = 0;   // (words past HW: never seen, quantized and dropped)
         uint32_t need = 0;   // bit i: word pt + 256 i still to see
 #pragma unroll
         for (int i = 0; i < NW; i++)
@@ -1849,6 +1851,30 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
                 break;
             }
         }
+        // kernel A's quantizer on every word first, with no store between
+        // them (the NW words' dependency chains interleave; one wave per SIMD
+        // runs this, so it is latency-bound), then the stores
+        float dq[NW];
+        int qq[NW], tq[NW], sq[NW];
+        uint32_t d16q[NW];
+#pragma unroll
+        for (int i = 0; i < NW; i++) {
+            const float h = __uint_as_float((uint32_t)hv[i]);
+            const float am = max32(fabsf(h));
+            const float d = am / 127.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+            const int qv = (int)roundf(h * id);
+            int s16 = qv;   // the 16-value half-block sum: a 16-lane row of DPP
+            s16 += dpp_i<DPP_XOR1>(s16);
+            s16 += dpp_i<DPP_XOR2>(s16);
+            s16 += dpp_i<DPP_HALF_MIRROR>(s16);
+            s16 += dpp_i<DPP_MIRROR>(s16);
+            dq[i] = d;
+            qq[i] = qv;
+            tq[i] = sum32(qv);
+            sq[i] = s16;
+            d16q[i] = f2h_rne(d);
+        }
 #pragma unroll
         for (int i = 0; i < NW; i++) {
             const uint32_t w = pt + 64 * XCD_POLL_WAVES * i;   // its 32-lane half is one block of one expert
@@ -1856,19 +1882,10 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
                 const bool shared = SH && w >= F;
                 const uint32_t e = shared ? 128 * u + (w - F) : w;   // the value's index in its expert's h
                 const Act &dst = shared ? actS : act;
-                const float h = __uint_as_float((uint32_t)hv[i]);
-                const float am = max32(fabsf(h));
-                const float d = am / 127.0f;
-                const float id = d != 0.0f ? 1.0f / d : 0.0f;
-                const int qv = (int)roundf(h * id);
-                const int total = sum32(qv);
-                int s16 = qv;   // the 16-value half-block sum: a 16-lane row of DPP
-                s16 += dpp_i<DPP_XOR1>(s16);
-                s16 += dpp_i<DPP_XOR2>(s16);
-                s16 += dpp_i<DPP_HALF_MIRROR>(s16);
-                s16 += dpp_i<DPP_MIRROR>(s16);
+                const float d = dq[i];
+                const int qv = qq[i], total = tq[i], s16 = sq[i];
+                const uint32_t d16 = d16q[i];
                 const uint32_t kb = e / 32, j = e % 32;
-                const uint32_t d16 = f2h_rne(d);
                 dst.qs[e] = (int8_t)qv;
                 if (j == 0) dst.d8[kb] = h2f(d16);
                 if ((j & 15) == 0) dst.qs16[2 * kb + j / 16] = s16;
