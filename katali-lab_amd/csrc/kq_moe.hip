@@ -518,7 +518,7 @@ __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area,
     //    from those logits, into LDS for the other waves
     if (wave == 0) {
         const uint32_t *rep = xr + 2 * 512 * (w % FSYNC_REP);
-        uint64_t va[C], vb[C];
+        uint64_t va[C];
         auto issue = [&](uint64_t *o) {
 #pragma unroll
             for (int i = 0; i < C; i++) o[i] = ld_dev2((uint32_t *)rep + 2 * min(lane + 64 * i, a.n_expert - 1));
@@ -534,22 +534,20 @@ __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area,
 #pragma unroll
             for (int i = 0; i < C; i++) lv[i] = __uint_as_float((uint32_t)o[i]);
         };
-        issue(va);
+        // One round at a time: the layer drains every load before its weight
+        // stream starts, so a second round still in flight once the logits
+        // are complete would hold this wave's weight loads back one round
+        // trip.
         uint32_t spins = 0;
         for (;;) {
-            issue(vb);
+            issue(va);
             if (seen(va)) {
                 take(va);
                 break;
             }
-            issue(va);
-            if (seen(vb)) {
-                take(vb);
-                break;
-            }
-            if (++spins >= FSYNC_SPIN_LIMIT / 2) {
+            if (++spins >= FSYNC_SPIN_LIMIT) {
                 if (lane == 0) atomicOr(a.err, 4);
-                take(vb);
+                take(va);
                 break;
             }
         }
