@@ -188,12 +188,14 @@ typedef struct KataliHipMoeRoute {
  * activation and the SiLU-GLU output are quantized to q8_1 inside the kernel;
  * dots use int8 v_dot4 with fp32 scales; the expert sum is in rank order.
  * Shapes beyond what katali_hip_moe_check admits return an error before
- * anything is enqueued. Eight slots (hidden 1024 or 2048, ffn <= 1024,
- * <= 256 experts, a 256-CU device) run as one launch whose 256 workgroups
+ * anything is enqueued. Eight slots, and eight routed experts plus the
+ * shared expert at ffn 256 or 512 (hidden 1024 or 2048, ffn <= 1024,
+ * <= 256 experts, a 256-CU device), run as one launch whose 256 workgroups
  * wait for each other: on a device busy with other work that wait can
  * expire, reported as KATALI_HIP_E_TIMEOUT by the next katali_hip_sync,
  * the outputs then invalid. KATALI_HIP_XCD=0 in the environment keeps such
- * layers on the two-launch path, which never waits in-kernel. */
+ * layers on the two-launch path, which never waits in-kernel
+ * (KATALI_HIP_XCD_SHARED=0 only the shared-expert shapes). */
 int katali_hip_moe_layer(const KataliHipMoe *moe, const KataliHipMoeRoute *route,
                          const float *x_dev, const void *xq8_dev, float *y_dev);
 
