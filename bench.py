@@ -176,17 +176,33 @@ def moe_free(layers, bufs):
         b.free()
 
 
-def bench_moe(hip, name, steps, warmup, ring=64, vocab=0, normed=False):
+def bench_moe(hip, name, steps, warmup, ring=64, vocab=0, normed=False, stacked=False, stamps=None):
     """One hipGraph per ring position, replayed per token. vocab == 0: the
     MoE layers only (router logits from a ring). vocab > 0: the whole token
-    chain (TOKEN_WORKLOADS), routing from the device router's logits."""
+    chain (TOKEN_WORKLOADS), routing from the device router's logits.
+    stacked: the token's L layers as one stacked launch
+    (katali_hip_moe_stack_*): each layer on its own x, its weight loads held
+    until the previous layer's y is complete (with vocab: the normed stack,
+    x_l = x_{l-1} + y_{l-1}), instead of one call per layer. stamps: a dict
+    that gets the measurement build's phase stamps of the timed replays."""
     L, hidden, ffn, n_expert, n_sel, shared = MOE_WORKLOADS[name]
     rb_g, rb_d = row_bytes(Q4_K, hidden), row_bytes(Q6_K, ffn)
     layers, descs, routes, bufs, xs, ys, seed = moe_setup(hip, name, ring)
+    stacks = []
 
     def token(t):
         for li in range(L):
             hip.moe_layer(descs[li], routes[t][li], ys[li], x=xs[li])
+
+    if stacked and not vocab:
+        # one stack per ring position: its layer table names that position's logits
+        for t in range(ring):
+            stacks.append(hip.moe_stack(descs[0], n_sel, [
+                {"gate": layers[li][0], "up": layers[li][1], "down": layers[li][2], "shared": layers[li][3],
+                 "y": ys[li], "route": routes[t][li], "x": xs[li] if li else None} for li in range(L)]))
+
+        def token(t):  # noqa: F811
+            stacks[t].run(xs[0])
 
     chain_bufs = []
     if vocab:
@@ -208,7 +224,25 @@ def bench_moe(hip, name, steps, warmup, ring=64, vocab=0, normed=False):
         cls = [View(clog.ptr + li * n_expert * 4) for li in range(L)]
         croutes = [hip.moe_route(n_sel, logits=cls[li]) for li in range(L)]
 
+        if stacked:
+            # the token's layers as the normed stack (one launch); then the
+            # output norm adds the last layer's y to the residual entering it
+            xo_last = hip.alloc(L * hidden * 4)
+            chain_bufs.append(xo_last)
+            xol = [View(xo_last.ptr + li * hidden * 4) for li in range(L)]
+            stk = hip.moe_stack(descs[0], n_sel, [
+                {"gate": layers[li][0], "up": layers[li][1], "down": layers[li][2], "shared": layers[li][3],
+                 "y": ys[li], "norm_w": nws[li], "router": routers[li], "x_out": xol[li]} for li in range(L)],
+                normed=True)
+            stacks.append(stk)
+
         def token(t):  # noqa: F811
+            if stacked:
+                stacks[0].run(View(x0.ptr + t * hidden * 4))
+                hip.add_rmsnorm(xol[L - 1], ys[L - 1], 1.0, nws[L], hidden, 1e-6, xn_out)
+                hip.matvec_dp4a(Q6_K, head, vocab, hidden, xn_out, head_logits)
+                hip.argmax(head_logits, vocab, tok)
+                return
             # per layer the residual step, the norm, the router logits and the
             # MoE layer: three launches (katali_hip_rmsnorm_matvec_f32, then
             # the layer), or two with normed (katali_hip_moe_layer_normed);
@@ -252,11 +286,21 @@ def bench_moe(hip, name, steps, warmup, ring=64, vocab=0, normed=False):
     ms = hip.elapsed_ms(e0, e1)
     wall = time.perf_counter() - t0
     hip.sync()
+    if stamps is not None:   # the last 64 layers of the timed replays
+        stamps["stamps"] = hip.phase_stamps()
 
-    # per-launch kernel time: an event pair around each layer, eager
+    # per-launch kernel time: an event pair around each layer (or, stacked,
+    # each stack launch, per layer), eager
     ev = [hip.event() for _ in range(2 * L)]
     per = []
     for t in range(0 if vocab else 3):   # (the token chain reports the graph only)
+        if stacked:
+            hip.record(ev[0])
+            stacks[t].run(xs[0])
+            hip.record(ev[1])
+            hip.sync()
+            per.append(hip.elapsed_ms(ev[0], ev[1]) / L)
+            continue
         for li in range(L):
             hip.record(ev[2 * li])
             hip.moe_layer(descs[li], croutes[li] if vocab else routes[t][li], ys[li], x=xs[li])
@@ -267,6 +311,8 @@ def bench_moe(hip, name, steps, warmup, ring=64, vocab=0, normed=False):
         hip.event_destroy(e)
     for gr in graphs:
         hip.graph_destroy(gr)
+    for stk in stacks:
+        stk.destroy()
 
     layer_bytes, weight_bytes = moe_bytes_per_layer(hidden, ffn, n_sel, shared)
     tok_bytes = L * layer_bytes
@@ -949,6 +995,12 @@ def main():
     ap.add_argument("--normed-layer", action="store_true",
                     help="moe48tok: katali_hip_moe_layer_normed (norm, router and layer in two launches per layer) "
                          "instead of the norm/router launch and the layer (three)")
+    ap.add_argument("--stacked", action="store_true",
+                    help="moe48 / moe40cold / moe48tok: the token's layers as one stacked launch "
+                         "(katali_hip_moe_stack_run), each layer's input the previous layer's output")
+    ap.add_argument("--dump-stamps", default="", metavar="NPY",
+                    help="moe48 / moe40cold / moe48tok with the measurement build (KATALI_HIP_DLL="
+                         "libkatali_hip_stamps.so): save the phase stamps of the timed replays' last 64 layers")
     ap.add_argument("--batch-points", default="", metavar="NxT,...",
                     help="moebatch: only these (n_sel x tokens) points, e.g. 8x64,2x64 (profiling)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -993,33 +1045,51 @@ def main():
 
     traffic = read_traffic(args.workload)
     if args.workload in MOE_WORKLOADS:
-        res, shape = bench_moe(hip, args.workload, args.steps, args.warmup)
+        st = {} if args.dump_stamps else None
+        res, shape = bench_moe(hip, args.workload, args.steps, args.warmup, stacked=args.stacked, stamps=st)
+        if st:
+            np.save(args.dump_stamps, st["stamps"])
         L, hidden, ffn, n_expert, n_sel, shared = shape
         unit_ms = res["ms_per_step"] / L
         unit_bytes = res["layer_bytes"]
         metric = "fused MoE layer HBM GB/s (% of ~8 TB/s peak) + decode tok/s, top-8 Q4_K"
+        how = (f"the {L} layers as one stacked launch per token (katali_hip_moe_stack_run; each layer on its own "
+               f"x, and no layer loads a weight before the previous layer's y is complete, a decode chain's order)"
+               if args.stacked else "one katali_hip_moe_layer call per layer on its own x")
         config = {
             "workload": f"{args.workload}: {L}-layer MoE decode, 1 token, hidden {hidden}, {n_expert} experts, "
                         f"top-{n_sel}{' + shared expert' if shared else ''}, gate/up {hidden}->{ffn} Q4_K, "
                         f"down {ffn}->{hidden} Q6_K, fp32 x quantized to q8_1 in the layer, new routing every "
-                        f"token from a 64-position logit ring (fixed logits addresses per position), hipGraph per token",
+                        f"token from a 64-position logit ring (fixed logits addresses per position), {how}, "
+                        f"hipGraph per token",
             "layers": L, "hidden": hidden, "ffn": ffn, "n_expert": n_expert, "n_sel": n_sel,
             "shared_expert": shared, "expert_pool_gb": round(res["pool_gb"], 2),
             "bytes_per_token": res["bytes_per_token"], "parallelism": "single GPU",
         }
         kernel = "MoE layer: " + layer_kernels(hip, hidden, ffn, n_expert, n_sel + (1 if shared else 0), shared)
+        if args.stacked:
+            kernel = (f"MoE layer in the stacked launch k_moe_stack ({L} layers per launch; unit = one layer, "
+                      f"launch time / {L})" if kernel.startswith("MoE layer: k_moe_xcd") else
+                      kernel + ", layer by layer under katali_hip_moe_stack_run")
         extra = {"tok_s": round(res["tok_s"], 2),
                  "eager_layer_ms_mean": round(res["kernel_ms_mean"], 5)}
     elif args.workload in TOKEN_WORKLOADS:
         base, vocab = TOKEN_WORKLOADS[args.workload]
-        res, shape = bench_moe(hip, base, args.steps, args.warmup, vocab=vocab, normed=args.normed_layer)
+        st = {} if args.dump_stamps else None
+        res, shape = bench_moe(hip, base, args.steps, args.warmup, vocab=vocab, normed=args.normed_layer,
+                               stacked=args.stacked, stamps=st)
+        if st:
+            np.save(args.dump_stamps, st["stamps"])
         L, hidden, ffn, n_expert, n_sel, shared = shape
         unit_ms = res["ms_per_step"]
         unit_bytes = res["bytes_per_token"]
         metric = "decode token HBM GB/s (% of ~8 TB/s peak) + tok/s: MoE FFN chain, LM head and argmax on device"
         layer = layer_kernels(hip, hidden, ffn, n_expert, n_sel + (1 if shared else 0), shared)
         one = layer.startswith("k_moe_xcd")
-        steps_desc = ("one launch for residual add + RMSNorm + F32 router, then the MoE layer"
+        steps_desc = ("the normed stack (katali_hip_moe_stack_run, one launch for all layers): per layer the "
+                      "residual add of the previous layer's y, RMSNorm, F32 router rows and the MoE layer, the "
+                      "logits exchanged on the device" if args.stacked else
+                      "one launch for residual add + RMSNorm + F32 router, then the MoE layer"
                       if not args.normed_layer else
                       "katali_hip_moe_layer_normed: the residual add, RMSNorm and F32 router rows in the layer's "
                       "own prologue, the logits exchanged on the device" +
@@ -1033,7 +1103,9 @@ def main():
             "layers": L, "hidden": hidden, "ffn": ffn, "n_expert": n_expert, "n_sel": n_sel, "vocab": vocab,
             "bytes_per_token": res["bytes_per_token"], "parallelism": "single GPU",
         }
-        kernel = (f"whole token graph (per layer k_norm_router + the MoE layer, {layer}; then 4 launches: output "
+        kernel = ("whole token graph (k_moe_stack: every layer's norm, router and MoE layer in one launch; then "
+                  "output norm, head, argmax)" if args.stacked else
+                  f"whole token graph (per layer k_norm_router + the MoE layer, {layer}; then 4 launches: output "
                   "norm, head, argmax)" if not args.normed_layer else
                   "whole token graph (per layer " +
                   ("k_moe_xcd with the norm and router in its prologue, one launch" if one else

@@ -191,11 +191,17 @@ typedef struct KataliHipMoeRoute {
  * anything is enqueued. Eight slots, and eight routed experts plus the
  * shared expert at ffn 256 or 512 (hidden 1024 or 2048, ffn <= 1024,
  * <= 256 experts, a 256-CU device), run as one launch whose 256 workgroups
- * wait for each other: on a device busy with other work that wait can
- * expire, reported as KATALI_HIP_E_TIMEOUT by the next katali_hip_sync,
- * the outputs then invalid. KATALI_HIP_XCD=0 in the environment keeps such
- * layers on the two-launch path, which never waits in-kernel
- * (KATALI_HIP_XCD_SHARED=0 only the shared-expert shapes). */
+ * wait for each other, so the library takes that form only where the
+ * occupancy API confirms all 256 workgroups fit on the device at once. On a
+ * device busy with other work a wait can still expire: each wait gives up
+ * after about 2^20 polls (about a second, per wait, so a call can stall for
+ * seconds), reported as KATALI_HIP_E_TIMEOUT by the next katali_hip_sync,
+ * the outputs then invalid; from that report on, the library runs every
+ * layer on the two-launch path (graphs captured before keep their kernels;
+ * katali_hip_one_launch(1) allows the one-launch form again).
+ * KATALI_HIP_XCD=0 in the environment keeps such layers on the two-launch
+ * path, which never waits in-kernel (KATALI_HIP_XCD_SHARED=0 only the
+ * shared-expert shapes). */
 int katali_hip_moe_layer(const KataliHipMoe *moe, const KataliHipMoeRoute *route,
                          const float *x_dev, const void *xq8_dev, float *y_dev);
 
@@ -235,6 +241,72 @@ typedef struct KataliHipMoeNorm {
 int katali_hip_moe_layer_normed(const KataliHipMoe *moe, const KataliHipMoeNorm *norm, int32_t n_sel,
                                 int32_t *ids_out, float *weights_out, float *y_dev);
 
+/* ---- a stack of MoE layers in one launch ---------------------------------- */
+/* n_layers layers of one shape, each layer's input the previous layer's
+ * output, run by one launch whose workgroups stay resident from layer to
+ * layer (no launch gap between layers). A layer starts none of its weight
+ * loads before the whole of the previous layer's output is written; it reads
+ * only what does not depend on that output (its routing from given logits,
+ * its router rows and norm weights) before.
+ *   plain (normed == 0): layer 0 runs on run()'s x, layer l on its own x
+ *     or, where that is NULL, on layer l-1's y (either way it waits for that
+ *     y to be complete before its weight loads: a decode chain's order);
+ *     each layer routed by its route (logits, or ids and weights; n_sel as
+ *     the stack's), outputs bit-identical to katali_hip_moe_layer called
+ *     layer by layer on those inputs.
+ *   normed (normed != 0, n_sel >= 1, no shared expert): layer 0 takes
+ *     x_0 = x (+ scale * delta when delta is given), layer l the residual
+ *     x_l = x_{l-1} + y_{l-1}; each layer's norm (norm_w, eps), router
+ *     logits (router) and layer as katali_hip_moe_layer_normed, outputs
+ *     bit-identical to it called layer by layer (x_out, xn_out, logits_out
+ *     optional per layer: the residual entering the layer's norm, the
+ *     normalized vector, the logits).
+ * The one-launch form needs the shapes katali_hip_moe_layer runs as one
+ * launch (eight slots, or eight routed experts plus the shared expert at ffn
+ * 256 or 512 for the plain stack; hidden 1024 or 2048, ffn <= 1024, <= 256
+ * experts, a 256-CU device); elsewhere, with KATALI_HIP_XCD=0, or after an
+ * expired wait, run() calls the layers one by one with the same results.
+ * Its workgroups wait for each other as the one-launch layer's do (each wait
+ * bounded at about 2^20 polls, about a second; an expiry is reported as
+ * KATALI_HIP_E_TIMEOUT by the next katali_hip_sync, the outputs then
+ * invalid). create() copies the layer table to the device (outside graph
+ * capture); run() is one launch on the library stream and may be captured.
+ * Per-layer vectors are 16-byte aligned; a layer's outputs must not overlap
+ * each other, its inputs or the previous layer's y. No counterpart in the
+ * reference: for an engine that keeps a token's MoE stack on the device. */
+typedef struct KataliHipMoeStackLayer {
+    uint32_t struct_size;                  /* sizeof(KataliHipMoeStackLayer) */
+    const float *x;                        /* plain stack, layers 1..: this layer's own
+                                              input [hidden] (NULL: layer l-1's y);
+                                              layer 0's is run()'s x */
+    const void *gate_exps, *up_exps, *down_exps;       /* this layer's experts */
+    const void *gate_shexp, *up_shexp, *down_shexp;    /* with a shared expert */
+    KataliHipMoeRoute route;               /* plain stack: this layer's routing; normed
+                                              stack: only ids_out / weights_out (optional;
+                                              struct_size 0 for none) */
+    const float *norm_w;                   /* normed stack: RMSNorm weights [hidden] */
+    const float *router;                   /* normed stack: F32 router [n_expert][hidden] */
+    float *y;                              /* the layer's output [hidden] */
+    float *x_out, *xn_out, *logits_out;    /* normed stack: optional outputs */
+} KataliHipMoeStackLayer;
+/* shape: types, hidden, ffn, n_expert and which shared-expert pointers are
+ * set (its weight pointers are not used); n_layers 1..4096. */
+int katali_hip_moe_stack_create(const KataliHipMoe *shape, int32_t n_sel, int32_t normed, float eps,
+                                const KataliHipMoeStackLayer *layers, int32_t n_layers, void **stack);
+/* plain: x_dev is layer 0's input (delta_dev NULL); normed: the residual
+ * stream and the optional delta of layer 0's residual step. */
+int katali_hip_moe_stack_run(void *stack, const float *x_dev, const float *delta_dev, float scale);
+int katali_hip_moe_stack_destroy(void *stack);
+
+/* The one-launch layers (the XCD-sliced layer, its normed form and the
+ * stack), whose workgroups wait for each other: mode 0 turns them off (every
+ * layer then runs as kernels A and B, as after an expired wait), 1 turns
+ * them back on (after an expiry, once the device is no longer shared), -1
+ * only asks. Returns the state before the call: 1 on, 0 off. The
+ * environment switch KATALI_HIP_XCD=0 still applies on top. No counterpart
+ * in the reference. */
+int katali_hip_one_launch(int32_t mode);
+
 /* KATALI_HIP_OK when katali_hip_moe_layer (n_tokens 0) or katali_hip_moe_batch
  * (n_tokens 1..64 tokens) runs a layer of this descriptor's shape with n_sel
  * routed experts; else the code and last-error message the call would give.
@@ -254,14 +326,16 @@ int katali_hip_moe_check(const KataliHipMoe *moe, int32_t n_sel, uint32_t n_toke
 /* katali_hip_moe_layer without any allocation, for callers that cannot
  * allocate device memory (code under hipGraph capture, tight serving loops,
  * harnesses that forbid hipMalloc). No counterpart in the reference. Same
- * arguments, results bit-identical to katali_hip_moe_layer (the same
- * kernels); its routing hand-off and q8_1 h blocks live in a fixed static
- * device array of the library (one per GPU, held until the process ends):
- * n_slots * ffn/32 * 36 bytes of h must fit 135168 (n_slots = n_sel + 1 with
- * a shared expert), else KATALI_HIP_E_INVALID; every shape that passes
- * katali_hip_moe_check's LDS rule needs at most 132192. The library must be
- * initialised first (katali_hip_probe); calls that overlap on one GPU share
- * the array and race. */
+ * arguments; it chooses the same kernels as katali_hip_moe_layer (the
+ * one-launch layer where that entry takes it, under the same environment
+ * switches), so its results are bit-identical to it. Its routing hand-off,
+ * q8_1 h blocks and the one-launch layer's exchange words live in a fixed
+ * static device array of the library (one per GPU, about 590 KB, held until
+ * the process ends): n_slots * ffn/32 * 36 bytes of h must fit 135168
+ * (n_slots = n_sel + 1 with a shared expert), else KATALI_HIP_E_INVALID;
+ * every shape that passes katali_hip_moe_check's LDS rule needs at most
+ * 132192. The library must be initialised first (katali_hip_probe); calls
+ * that overlap on one GPU share the array and race. */
 int katali_hip_moe_layer_noalloc(const KataliHipMoe *moe, const KataliHipMoeRoute *route,
                                  const float *x_dev, const void *xq8_dev, float *y_dev);
 
@@ -320,8 +394,10 @@ int katali_hip_step_advance(int32_t *step_dev, int32_t n_steps);
  * the library stream and share that scratch: replays and eager calls run in
  * stream order, never side by side. During a capture, katali_hip_malloc,
  * upload, download, sync, memset and set_stream return KATALI_HIP_E_INVALID
- * (each would end or corrupt the capture), and katali_hip_free is deferred to
- * katali_hip_graph_end. */
+ * (each would end or corrupt the capture). katali_hip_free during a capture
+ * releases nothing then: the buffer belongs to the graph made from that
+ * capture (its replays may use it) and is freed by katali_hip_graph_destroy,
+ * or at once if katali_hip_graph_end makes no graph. */
 int katali_hip_graph_begin(void);
 int katali_hip_graph_end(void **graph);
 int katali_hip_graph_launch(void *graph);
@@ -333,6 +409,15 @@ int katali_hip_event_record(void *event);
 /* Waits for `end`, then *ms = elapsed between the two records. */
 int katali_hip_event_elapsed(void *start, void *end, float *ms);
 int katali_hip_event_destroy(void *event);
+
+/* ---- measurement ------------------------------------------------------------- */
+/* The phase stamps of the one-launch layers: [64][256][16] uint64
+ * s_memrealtime ticks (100 MHz), layer slot tag % 64, workgroup, phase (the
+ * phases listed at kq_stamps in kq_moe.hip). Only the measurement build
+ * records them (libkatali_hip_stamps.so, `build.py --stamps`); the product
+ * library returns KATALI_HIP_E_UNSUPPORTED. Waits for queued work first.
+ * No counterpart in the reference. */
+int katali_hip_phase_stamps(void *host, size_t bytes);
 
 /* ---- self-test and synthetic data for the harnesses ------------------------ */
 /* cuda-dp4a-selftest equivalent (README.md:17): a synthetic Q4_K and Q6_K

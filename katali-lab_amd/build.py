@@ -6,6 +6,10 @@ Outputs (all next to this file, git-ignored, shipped with the tree):
     libkatali_hip.so        the HIP backend (C ABI: include/katali_hip.h)
     libkatali_hip_loader.so the engine-side loader (dlopen, CPU fallback)
     katali-hip              the CLI harness (hip-check, hip-bench, ...)
+
+    python katali-lab_amd/build.py --stamps   # the measurement build only
+    libkatali_hip_stamps.so the same library with the one-launch layers'
+                            phase stamps (KQ_STAMPS), for profile_bench.py --phases
 """
 from __future__ import annotations
 
@@ -69,11 +73,11 @@ def scratch_kernels(remarks: str) -> list[tuple[str, int]]:
     return out
 
 
-def _hip_object(src: str) -> str:
-    obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+def _hip_object(src: str, build: str = BUILD, defines: tuple[str, ...] = ()) -> str:
+    obj = os.path.join(build, os.path.basename(src) + ".o")
     lang = ["-x", "hip"] if src.endswith(".hip") else ["-x", "hip"]
-    remarks = _run([HIPCC, *HIP_FLAGS, "-Rpass-analysis=kernel-resource-usage", *lang, "-c",
-                    os.path.join(CSRC, src), "-o", obj])
+    remarks = _run([HIPCC, *HIP_FLAGS, *[f"-D{d}" for d in defines], "-Rpass-analysis=kernel-resource-usage",
+                    *lang, "-c", os.path.join(CSRC, src), "-o", obj])
     bad = scratch_kernels(remarks)
     if bad:
         raise RuntimeError(f"{src}: kernels with scratch memory (bytes per lane): " +
@@ -81,11 +85,15 @@ def _hip_object(src: str) -> str:
     return obj
 
 
-def build_hip(jobs: int = 3) -> str:
-    os.makedirs(BUILD, exist_ok=True)
+def build_hip(jobs: int = 3, stamps: bool = False) -> str:
+    """The library; stamps: the measurement build (KQ_STAMPS: the one-launch
+    layers record phase stamps), libkatali_hip_stamps.so, off by default."""
+    build = BUILD + ("_stamps" if stamps else "")
+    defines = ("KQ_STAMPS",) if stamps else ()
+    os.makedirs(build, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_hip_object, HIP_SOURCES))
-    out = os.path.join(PKG, "libkatali_hip.so")
+        objs = list(ex.map(lambda src: _hip_object(src, build, defines), HIP_SOURCES))
+    out = os.path.join(PKG, "libkatali_hip_stamps.so" if stamps else "libkatali_hip.so")
     tmp = out + ".tmp"
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp])
     os.replace(tmp, out)
@@ -124,4 +132,7 @@ def build_all(verbose: bool = True) -> list[str]:
 
 
 if __name__ == "__main__":
-    build_all()
+    if "--stamps" in sys.argv[1:]:
+        print("built", os.path.relpath(build_hip(stamps=True), REPO))
+    else:
+        build_all()

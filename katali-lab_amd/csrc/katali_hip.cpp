@@ -15,6 +15,7 @@
 
 #include <mutex>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "../../include/katali_hip.h"
@@ -35,7 +36,9 @@ hipStream_t g_stream = nullptr;
 hipStream_t g_aux_stream = nullptr;
 hipEvent_t g_ev_fork = nullptr, g_ev_join = nullptr;
 bool g_capturing = false;
-std::vector<void *> g_deferred_free;   // katali_hip_free calls made during a capture
+std::vector<void *> g_deferred_free;   // katali_hip_free calls made during the open capture
+// buffers freed during a capture, released with the graph made from it
+std::unordered_map<void *, std::vector<void *>> g_graph_frees;
 
 // MoE scratch. Every buffer is allocated once, at its largest size, on the
 // first call that needs it, and never freed or moved: a graph captured around
@@ -54,10 +57,15 @@ float *g_nbuf = nullptr;      // the normed layer's xn [4096] and logits [512] w
 // katali_hip_sync after it reports), [512, ..) the q8_1 h blocks. Kernel B
 // stages every slot's h in LDS, n_slots * ffn * 11/8 + 2116 <= 163840 bytes,
 // so n_slots * ffn / 256 <= 459 and h takes at most 459 * 288 = 132192
-// bytes: every layer shape the LDS admits fits the maximum below.
+// bytes: every layer shape the LDS admits fits the maximum below. From
+// NOALLOC_FSYNC, the one-launch layers' exchange words (zero from load,
+// generation-tagged, never cleared between calls), so the entry point runs
+// the same kernels as katali_hip_moe_layer.
 constexpr size_t NOALLOC_HQ8_MAX = 132 * 1024;
 constexpr size_t NOALLOC_ERR = 256, NOALLOC_HQ8 = 512;
-__device__ __align__(256) uint8_t scratch[NOALLOC_HQ8 + NOALLOC_HQ8_MAX];
+constexpr size_t NOALLOC_FSYNC = NOALLOC_HQ8 + NOALLOC_HQ8_MAX;
+static_assert(NOALLOC_FSYNC % 256 == 0, "exchange words 256-byte aligned");
+__device__ __align__(256) uint8_t scratch[NOALLOC_FSYNC + kq::fsync_words() * 4];
 uint8_t *g_scratch = nullptr;   // scratch's device address on g_device
 
 int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
@@ -151,15 +159,17 @@ int check_gemv(uint32_t type, const void *w, uint64_t rows, uint64_t cols, const
 
 int launched(hipError_t e, const char *what) { return e == hipSuccess ? KATALI_HIP_OK : hip_fail(e, what); }
 
-// Frees that katali_hip_free deferred while a capture was open.
-int release_deferred() {
-    if (g_deferred_free.empty()) return KATALI_HIP_OK;
+// Frees that katali_hip_free deferred while a capture was open, done once
+// nothing can use the buffers any more: after the stream has drained, when
+// no graph was made from the capture or when that graph is destroyed.
+int release_frees(std::vector<void *> &v) {
+    if (v.empty()) return KATALI_HIP_OK;
     hipError_t e = hipStreamSynchronize(g_stream);
-    for (void *p : g_deferred_free) {
+    for (void *p : v) {
         const hipError_t f = hipFree(p);
         if (e == hipSuccess) e = f;
     }
-    g_deferred_free.clear();
+    v.clear();
     return e == hipSuccess ? KATALI_HIP_OK : hip_fail(e, "deferred hipFree");
 }
 
@@ -420,7 +430,8 @@ int katali_hip_free(void *dev) {
     int rc = ensure();
     if (rc) return rc;
     if (g_capturing) {
-        // a synchronisation would end the capture: released after graph_end
+        // a synchronisation would end the capture, and work being captured
+        // may use the buffer: it is released with the graph (graph_destroy)
         g_deferred_free.push_back(dev);
         return KATALI_HIP_OK;
     }
@@ -481,31 +492,27 @@ int katali_hip_sync(void) {
     if (g_capturing) return fail(KATALI_HIP_E_INVALID, "katali_hip_sync during graph capture");
     hipError_t e = hipStreamSynchronize(g_stream);
     if (e != hipSuccess) return hip_fail(e, "sync");
-    {
-        int32_t err = 0;
-        e = hipMemcpy(&err, g_scratch + NOALLOC_ERR, 4, hipMemcpyDeviceToHost);
-        if (e != hipSuccess) return hip_fail(e, "read error word");
-        if (err) {
-            (void)hipMemset(g_scratch + NOALLOC_ERR, 0, 4);
-            return fail(KATALI_HIP_E_INVALID, "MoE expert id outside [0, n_expert) in the explicit routing");
-        }
+    // both error words are read and cleared before either is reported, so
+    // no error is left for a later, unrelated sync
+    int32_t na = 0, err = 0;
+    e = hipMemcpy(&na, g_scratch + NOALLOC_ERR, 4, hipMemcpyDeviceToHost);
+    if (e == hipSuccess && g_err_dev) e = hipMemcpy(&err, g_err_dev, 4, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(e, "read error word");
+    if (na) (void)hipMemset(g_scratch + NOALLOC_ERR, 0, 4);
+    if (err) (void)hipMemset(g_err_dev, 0, 4);
+    if ((err | na) & 4) {
+        // a one-launch layer gave up waiting for its own workgroups (the
+        // device was shared with other work): its outputs and the exchange
+        // words are void; start over, and from now on run every layer as
+        // kernels A and B, which never wait in-kernel
+        if (g_fsync && (err & 4)) (void)hipMemset(g_fsync, 0, kq::fsync_words() * 4);
+        if (na & 4) (void)hipMemset(g_scratch + NOALLOC_FSYNC, 0, kq::fsync_words() * 4);
+        kq::xcd_disable();
+        return fail(KATALI_HIP_E_TIMEOUT, "MoE layer: in-kernel wait expired (outputs invalid; the one-launch "
+                                          "layers are off from now on)");
     }
-    if (g_err_dev) {
-        int32_t err = 0;
-        e = hipMemcpy(&err, g_err_dev, 4, hipMemcpyDeviceToHost);
-        if (e != hipSuccess) return hip_fail(e, "read error word");
-        if (err) {
-            (void)hipMemset(g_err_dev, 0, 4);
-            if (err & 4) {
-                // a fused or normed layer gave up waiting for its own
-                // workgroups (the device was shared with other work): its
-                // outputs and the exchange words are void; start over
-                if (g_fsync) (void)hipMemset(g_fsync, 0, kq::fsync_words() * 4);
-                return fail(KATALI_HIP_E_TIMEOUT, "MoE layer: in-kernel wait expired (outputs invalid)");
-            }
-            return fail(KATALI_HIP_E_INVALID, "MoE expert id outside [0, n_expert) in the explicit routing");
-        }
-    }
+    if (err | na)
+        return fail(KATALI_HIP_E_INVALID, "MoE expert id outside [0, n_expert) in the explicit routing");
     return KATALI_HIP_OK;
 }
 
@@ -685,7 +692,31 @@ int katali_hip_moe_layer_noalloc(const KataliHipMoe *m, const KataliHipMoeRoute 
     a.route_ids = (int32_t *)g_scratch;
     a.route_w = (float *)(g_scratch + 4 * kq::moe_route_words() / 2);
     a.err = (int32_t *)(g_scratch + NOALLOC_ERR);
-    return launched(kq::launch_moe(a, g_stream), "moe launch");
+    a.fsync = (uint32_t *)(g_scratch + NOALLOC_FSYNC);
+    // the layer choice of katali_hip_moe_layer (moe_impl), so the outputs are its bits
+    return launched(kq::launch_moe(a, g_stream, env_on("KATALI_HIP_FUSED"), nullptr, !env_off("KATALI_HIP_XCD"),
+                                   !env_off("KATALI_HIP_XCD_SHARED")),
+                    "moe launch");
+}
+
+int katali_hip_phase_stamps(void *host, size_t bytes) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!host) return fail(KATALI_HIP_E_INVALID, "null buffer");
+    if (g_capturing) return fail(KATALI_HIP_E_INVALID, "katali_hip_phase_stamps during graph capture");
+    hipError_t e = hipStreamSynchronize(g_stream);
+    if (e != hipSuccess) return hip_fail(e, "sync");
+    e = kq::read_stamps(host, bytes);
+    if (e == hipErrorNotSupported)
+        return fail(KATALI_HIP_E_UNSUPPORTED, "phase stamps: this is not the measurement build (build.py --stamps)");
+    return e == hipSuccess ? KATALI_HIP_OK : hip_fail(e, "phase stamps");
+}
+
+int katali_hip_one_launch(int32_t mode) {
+    const int was = kq::xcd_disabled() ? 0 : 1;
+    if (mode == 0) kq::xcd_disable();
+    else if (mode == 1) kq::xcd_enable();
+    return was;
 }
 
 int katali_hip_moe_check(const KataliHipMoe *m, int32_t n_sel, uint32_t n_tokens) {
@@ -752,6 +783,243 @@ int katali_hip_moe_layer_normed(const KataliHipMoe *m, const KataliHipMoeNorm *n
                     "moe normed launch");
 }
 
+// A stack of layers (katali_hip_moe_stack_*): the host copy of the layer
+// table (for the layer-by-layer path), its device copy (the one-launch
+// path's), and two residual buffers for the normed layer-by-layer path.
+struct MoeStack {
+    KataliHipMoe shape;
+    int32_t n_sel;
+    bool normed;
+    float eps;
+    std::vector<KataliHipMoeStackLayer> layers;
+    kq::StackLayer *table;
+    float *res[2];
+};
+
+static KataliHipMoe stack_layer_desc(const MoeStack &s, const KataliHipMoeStackLayer &L) {
+    KataliHipMoe d = s.shape;
+    d.gate_exps = L.gate_exps;
+    d.up_exps = L.up_exps;
+    d.down_exps = L.down_exps;
+    d.gate_shexp = L.gate_shexp;
+    d.up_shexp = L.up_shexp;
+    d.down_shexp = L.down_shexp;
+    return d;
+}
+
+int katali_hip_moe_stack_create(const KataliHipMoe *shape, int32_t n_sel, int32_t normed, float eps,
+                                const KataliHipMoeStackLayer *layers, int32_t n_layers, void **stack) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!stack) return fail(KATALI_HIP_E_INVALID, "null stack out pointer");
+    *stack = nullptr;
+    if (g_capturing) return fail(KATALI_HIP_E_INVALID, "katali_hip_moe_stack_create during graph capture");
+    if (!layers || n_layers < 1 || n_layers > 4096) return fail(KATALI_HIP_E_INVALID, "n_layers=%d (1..4096)", n_layers);
+    uint32_t n_slots = 0;
+    if ((rc = moe_shape(shape, n_sel, 0, n_slots))) return rc;
+    const bool shared = n_slots > (uint32_t)n_sel;
+    if (normed && n_sel < 1) return fail(KATALI_HIP_E_INVALID, "n_sel=%d: the normed stack routes (1..16)", n_sel);
+    const uint64_t vb = (uint64_t)shape->hidden * 4, rb = (uint64_t)shape->n_expert * vb;
+    for (int32_t l = 0; l < n_layers; l++) {
+        const KataliHipMoeStackLayer &L = layers[l];
+        if (L.struct_size < sizeof(KataliHipMoeStackLayer)) return fail(KATALI_HIP_E_INVALID, "layer %d: short struct", l);
+        if (n_sel > 0 && (!L.gate_exps || !L.up_exps || !L.down_exps))
+            return fail(KATALI_HIP_E_INVALID, "layer %d: null expert buffer", l);
+        if (shared != (L.gate_shexp && L.up_shexp && L.down_shexp) || (!shared && (L.gate_shexp || L.up_shexp || L.down_shexp)))
+            return fail(KATALI_HIP_E_INVALID, "layer %d: shared expert pointers do not match the shape's", l);
+        if (!L.y) return fail(KATALI_HIP_E_INVALID, "layer %d: null output", l);
+        const void *outs[4] = {L.y, normed ? L.x_out : nullptr, normed ? L.xn_out : nullptr,
+                               normed ? L.logits_out : nullptr};
+        const uint64_t outb[4] = {vb, vb, vb, (uint64_t)shape->n_expert * 4};
+        const void *ins[5] = {normed ? (const void *)L.norm_w : nullptr, normed ? (const void *)L.router : nullptr,
+                              normed ? nullptr : (const void *)L.route.logits, l ? layers[l - 1].y : nullptr,
+                              normed || !l ? nullptr : (const void *)L.x};
+        const uint64_t inb[5] = {vb, rb, (uint64_t)shape->n_expert * 4, vb, vb};
+        if (normed) {
+            if (!L.norm_w || !L.router) return fail(KATALI_HIP_E_INVALID, "layer %d: null norm weights or router", l);
+            if (((uintptr_t)L.norm_w | (uintptr_t)L.router | (uintptr_t)L.y | (uintptr_t)L.x_out | (uintptr_t)L.xn_out) % 16)
+                return fail(KATALI_HIP_E_INVALID, "layer %d: vectors and the router must be 16-byte aligned", l);
+        } else {
+            if (L.route.struct_size < sizeof(KataliHipMoeRoute) || L.route.n_sel != n_sel)
+                return fail(KATALI_HIP_E_INVALID, "layer %d: route missing or n_sel not the stack's", l);
+            if (n_sel > 0 && !L.route.logits && (!L.route.ids || !L.route.weights))
+                return fail(KATALI_HIP_E_INVALID, "layer %d: need logits or ids+weights", l);
+            if (((uintptr_t)L.y | (uintptr_t)L.x) % 16)
+                return fail(KATALI_HIP_E_INVALID, "layer %d: x and y must be 16-byte aligned", l);
+        }
+        for (int o = 0; o < 4; o++) {
+            for (int i = 0; i < 5; i++)
+                if (overlap(outs[o], outb[o], ins[i], inb[i]))
+                    return fail(KATALI_HIP_E_INVALID, "layer %d: an output overlaps an input", l);
+            for (int p = o + 1; p < 4; p++)
+                if (overlap(outs[o], outb[o], outs[p], outb[p]))
+                    return fail(KATALI_HIP_E_INVALID, "layer %d: outputs overlap", l);
+        }
+    }
+    if ((rc = moe_scratch())) return rc;
+    std::vector<kq::StackLayer> t((size_t)n_layers);
+    for (int32_t l = 0; l < n_layers; l++) {
+        const KataliHipMoeStackLayer &L = layers[l];
+        kq::StackLayer &d = t[(size_t)l];
+        memset(&d, 0, sizeof d);
+        d.x = normed || !l ? nullptr : L.x;
+        d.gate = (const uint8_t *)L.gate_exps;
+        d.up = (const uint8_t *)L.up_exps;
+        d.down = (const uint8_t *)L.down_exps;
+        d.gate_sh = (const uint8_t *)L.gate_shexp;
+        d.up_sh = (const uint8_t *)L.up_shexp;
+        d.down_sh = (const uint8_t *)L.down_shexp;
+        if (!normed) {
+            d.logits = L.route.logits;
+            d.step = L.route.step;
+            d.logits_stride = L.route.logits_stride;
+            d.ids = L.route.ids;
+            d.wts = L.route.weights;
+            d.ids_out = L.route.ids_out;
+            d.wts_out = L.route.weights_out;
+        }
+        d.y = L.y;
+        if (normed) {
+            if (L.route.struct_size >= sizeof(KataliHipMoeRoute)) {   // optional routing outputs
+                d.ids_out = L.route.ids_out;
+                d.wts_out = L.route.weights_out;
+            }
+            d.nw = L.norm_w;
+            d.router = L.router;
+            d.x_out = L.x_out;
+            d.xn_out = L.xn_out;
+            d.logits_out = L.logits_out;
+        }
+    }
+    MoeStack *s = new MoeStack();
+    s->shape = *shape;
+    s->n_sel = n_sel;
+    s->normed = normed != 0;
+    s->eps = eps;
+    s->layers.assign(layers, layers + n_layers);
+    s->table = nullptr;
+    s->res[0] = s->res[1] = nullptr;
+    hipError_t e = hipMalloc((void **)&s->table, t.size() * sizeof(kq::StackLayer));
+    if (e == hipSuccess) e = hipMemcpy(s->table, t.data(), t.size() * sizeof(kq::StackLayer), hipMemcpyHostToDevice);
+    if (e == hipSuccess && s->normed) e = hipMalloc((void **)&s->res[0], 2 * vb);
+    if (e != hipSuccess) {
+        if (s->table) (void)hipFree(s->table);
+        if (s->res[0]) (void)hipFree(s->res[0]);
+        delete s;
+        return fail(KATALI_HIP_E_NOMEM, "MoE stack table: %s", hipGetErrorString(e));
+    }
+    if (s->normed) s->res[1] = s->res[0] + shape->hidden;
+    *stack = s;
+    return KATALI_HIP_OK;
+}
+
+// The stack layer by layer (shapes the one-launch form does not take): the
+// same calls an engine would make, with the same results.
+static int stack_layer_by_layer(MoeStack &s, const float *x, const float *delta, float scale) {
+    const size_t n = s.layers.size();
+    const uint64_t vb = (uint64_t)s.shape.hidden * 4;
+    const float *cur = x;   // the residual stream (normed) or the layer input (plain)
+    for (size_t l = 0; l < n; l++) {
+        const KataliHipMoeStackLayer &L = s.layers[l];
+        const KataliHipMoe d = stack_layer_desc(s, L);
+        int rc;
+        if (!s.normed) {
+            rc = moe_impl(&d, &L.route, !l ? x : L.x ? L.x : s.layers[l - 1].y, nullptr, L.y, nullptr, nullptr);
+        } else {
+            const float *dl = l ? s.layers[l - 1].y : delta;
+            float *nxt = s.res[l % 2];
+            KataliHipMoeNorm nrm;
+            memset(&nrm, 0, sizeof nrm);
+            nrm.struct_size = sizeof nrm;
+            nrm.x = cur;
+            nrm.delta = dl;
+            nrm.scale = l ? 1.0f : scale;
+            nrm.x_out = dl ? nxt : nullptr;
+            nrm.norm_w = L.norm_w;
+            nrm.eps = s.eps;
+            nrm.xn_out = L.xn_out;
+            nrm.router = L.router;
+            nrm.logits_out = L.logits_out;
+            const bool ro = L.route.struct_size >= sizeof(KataliHipMoeRoute);
+            rc = katali_hip_moe_layer_normed(&d, &nrm, s.n_sel, ro ? L.route.ids_out : nullptr,
+                                             ro ? L.route.weights_out : nullptr, L.y);
+            if (!rc && dl) cur = nxt;
+            if (!rc && L.x_out) {
+                const hipError_t e = hipMemcpyAsync(L.x_out, cur, vb, hipMemcpyDeviceToDevice, g_stream);
+                if (e != hipSuccess) return hip_fail(e, "stack x_out");
+            }
+        }
+        if (rc) return rc;
+    }
+    return KATALI_HIP_OK;
+}
+
+int katali_hip_moe_stack_run(void *stack, const float *x, const float *delta, float scale) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!stack) return fail(KATALI_HIP_E_INVALID, "null stack");
+    MoeStack &s = *(MoeStack *)stack;
+    if (!x) return fail(KATALI_HIP_E_INVALID, "null input");
+    if (!s.normed && delta) return fail(KATALI_HIP_E_INVALID, "the plain stack takes no delta");
+    if (((uintptr_t)x | (uintptr_t)delta) % 16) return fail(KATALI_HIP_E_INVALID, "x and delta must be 16-byte aligned");
+    const uint64_t vb = (uint64_t)s.shape.hidden * 4;
+    const KataliHipMoeStackLayer &L0 = s.layers[0];
+    const void *outs[4] = {L0.y, L0.x_out, L0.xn_out, L0.logits_out};
+    const uint64_t outb[4] = {vb, vb, vb, (uint64_t)s.shape.n_expert * 4};
+    for (int o = 0; o < 4; o++)
+        if (overlap(outs[o], outb[o], x, vb) || overlap(outs[o], outb[o], delta, vb))
+            return fail(KATALI_HIP_E_INVALID, "layer 0: an output overlaps the input");
+    if ((rc = moe_scratch())) return rc;
+    if (!env_off("KATALI_HIP_XCD")) {
+        kq::MoeArgs a;
+        memset(&a, 0, sizeof a);
+        a.gate_type = s.shape.gate_type;
+        a.up_type = s.shape.up_type;
+        a.down_type = s.shape.down_type;
+        a.hidden = s.shape.hidden;
+        a.ffn = s.shape.ffn;
+        a.n_expert = s.shape.n_expert;
+        a.n_sel = s.n_sel;
+        a.has_shared = s.shape.gate_shexp ? 1 : 0;
+        a.hq8 = g_hq8;
+        a.route_ids = g_route;
+        a.route_w = (float *)(g_route + kq::moe_route_words() / 2);
+        a.err = g_err_dev;
+        a.fsync = g_fsync;
+        if (s.normed) {
+            a.nx = x;
+            a.ndelta = delta;
+            a.nscale = scale;
+            a.neps = s.eps;
+        } else {
+            a.x = x;
+        }
+        // the test hook of moe_impl (KATALI_HIP_TEST_SKEW), for the stack
+        if (env_on("KATALI_HIP_TEST_SKEW") && !g_capturing) {
+            const hipError_t e = hipMemsetAsync(g_fsync + kq::FSYNC_X, 0xA5, 4, g_stream);
+            if (e != hipSuccess) return hip_fail(e, "test skew");
+        }
+        const hipError_t e = kq::launch_moe_stack(a, s.table, (uint32_t)s.layers.size(), s.normed, g_stream);
+        if (e == hipSuccess) return KATALI_HIP_OK;
+        if (e != hipErrorNotSupported) return hip_fail(e, "moe stack launch");
+    }
+    return stack_layer_by_layer(s, x, delta, scale);
+}
+
+int katali_hip_moe_stack_destroy(void *stack) {
+    if (!stack) return KATALI_HIP_OK;
+    int rc = ensure();
+    if (rc) return rc;
+    if (g_capturing) return fail(KATALI_HIP_E_INVALID, "katali_hip_moe_stack_destroy during graph capture");
+    MoeStack *s = (MoeStack *)stack;
+    hipError_t e = hipStreamSynchronize(g_stream);
+    const hipError_t f1 = hipFree(s->table);
+    const hipError_t f2 = s->res[0] ? hipFree(s->res[0]) : hipSuccess;
+    delete s;
+    if (e == hipSuccess) e = f1 != hipSuccess ? f1 : f2;
+    return e == hipSuccess ? KATALI_HIP_OK : hip_fail(e, "katali_hip_moe_stack_destroy");
+}
+
 int katali_hip_moe_layer_debug(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, const void *xq,
                                float *y, float *gu, void *hq8) {
     return moe_impl(m, r, x, xq, y, gu, hq8);
@@ -779,22 +1047,30 @@ int katali_hip_graph_end(void **graph) {
     if (rc) return rc;
     if (!g_capturing) return fail(KATALI_HIP_E_INVALID, "no capture active");
     g_capturing = false;
+    std::vector<void *> frees;
+    frees.swap(g_deferred_free);
     hipGraph_t gr = nullptr;
     hipError_t e = hipStreamEndCapture(g_stream, &gr);
-    if ((rc = release_deferred())) {
+    if (e != hipSuccess) {
         if (gr) (void)hipGraphDestroy(gr);
-        return rc;
+        (void)release_frees(frees);
+        return hip_fail(e, "hipStreamEndCapture");
     }
-    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
     hipGraphExec_t ex = nullptr;
     e = hipGraphInstantiate(&ex, gr, nullptr, nullptr, 0);
     (void)hipGraphDestroy(gr);
-    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    if (e != hipSuccess) {
+        (void)release_frees(frees);
+        return hip_fail(e, "hipGraphInstantiate");
+    }
     if (!graph) {
         (void)hipGraphExecDestroy(ex);
+        (void)release_frees(frees);
         return fail(KATALI_HIP_E_INVALID, "null graph out");
     }
     *graph = (void *)ex;
+    // the graph's replays may use what was freed during its capture
+    if (!frees.empty()) g_graph_frees[(void *)ex].swap(frees);
     return KATALI_HIP_OK;
 }
 
@@ -808,6 +1084,14 @@ int katali_hip_graph_launch(void *graph) {
 int katali_hip_graph_destroy(void *graph) {
     if (!graph) return KATALI_HIP_OK;
     hipError_t e = hipGraphExecDestroy((hipGraphExec_t)graph);
+    auto it = g_graph_frees.find(graph);
+    if (it != g_graph_frees.end()) {
+        std::vector<void *> v;
+        v.swap(it->second);
+        g_graph_frees.erase(it);
+        const int rc = release_frees(v);   // after the stream drains: a replay may still run
+        if (rc && e == hipSuccess) return rc;
+    }
     return e == hipSuccess ? KATALI_HIP_OK : hip_fail(e, "hipGraphExecDestroy");
 }
 

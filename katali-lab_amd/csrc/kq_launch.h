@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "kq_plan.h"
+
 namespace kq {
 
 // Compute units of the current device (cached per device; 256 if unknown).
@@ -170,7 +172,14 @@ constexpr uint32_t XCD_MAX_UNITS = 4;   // the shared expert's 128-value units (
 constexpr uint32_t FSYNC_XS = FSYNC_XP + 2 * XCD_SLOTS * XCD_MAX_HIDDEN;
 constexpr uint32_t FSYNC_XSP = FSYNC_XS + 2 * XCD_SLOTS * 128;
 constexpr uint32_t FSYNC_XR = FSYNC_XSP + 2 * XCD_MAX_UNITS * XCD_MAX_HIDDEN;
-constexpr uint32_t fsync_words() { return FSYNC_XR + FSYNC_REP * 2 * 512; }
+// From FSYNC_XY, the stacked layer's (launch_moe_stack): two areas (layer
+// parity) of a layer's y [hidden] as words {float, generation}, read by the
+// next layer of the stack, then from FSYNC_XF two areas of one completion
+// word per workgroup (its generation, written once its y is stored); its
+// generations are the XCD layer's.
+constexpr uint32_t FSYNC_XY = FSYNC_XR + FSYNC_REP * 2 * 512;
+constexpr uint32_t FSYNC_XF = FSYNC_XY + 2 * 2 * XCD_MAX_HIDDEN;
+constexpr uint32_t fsync_words() { return FSYNC_XF + 2 * XCD_G; }
 static_assert(FSYNC_H + 2 * 9 * FUSED_MAX_G <= FSYNC_R, "exchange areas overlap");
 // The steps before the layer and the layer in two launches (MoeArgs' n*
 // fields and router set, n_sel >= 1, hidden <= 4096): kernel A forms the
@@ -184,6 +193,48 @@ static_assert(FSYNC_H + 2 * 9 * FUSED_MAX_G <= FSYNC_R, "exchange areas overlap"
 // layer with the steps before it in its prologue, in one launch.
 hipError_t launch_moe_normed(MoeArgs a, float *xn_buf, float *logits_buf, hipStream_t s, bool *merged = nullptr,
                              bool allow_xcd = false);
+// One layer of the stacked layer (launch_moe_stack): weights, routing and
+// outputs. Plain stack: logits (with step / logits_stride) or ids / wts route
+// the layer; NORMED: nw and router form its norm and routing, x_out / xn_out
+// / logits_out are optional outputs (the residual entering the layer's norm,
+// the normalized vector, the router logits).
+struct StackLayer {
+    const float *x;   // plain stack, layers past the first: its own input (null: the previous layer's y)
+    const uint8_t *gate, *up, *down;
+    const uint8_t *gate_sh, *up_sh, *down_sh;
+    const float *logits;
+    const int32_t *step;
+    uint64_t logits_stride;
+    const int32_t *ids;
+    const float *wts;
+    int32_t *ids_out;
+    float *wts_out;
+    float *y;
+    const float *nw, *router;
+    float *x_out, *xn_out, *logits_out;
+};
+// n_layers layers of a's shape in one launch of the XCD-sliced layer's
+// workgroups, lt[l] a device table of each layer's pointers (a's own weight,
+// routing and output pointers are ignored). Plain: layer 0's x is a.x or
+// a.xq and layer l's is lt[l].x or, null, layer l - 1's y; a layer issues no
+// weight load before the previous layer's y is complete either way; every
+// output bit-identical to launch_moe's XCD layer run layer by layer on
+// those inputs. normed: a's n*
+// fields give layer 0's residual step (nx, optional ndelta / nscale), layer
+// l adds layer l - 1's y to the residual stream; outputs bit-identical to
+// launch_moe_normed layer by layer. hipErrorNotSupported for shapes the XCD
+// layer does not take (then nothing is launched).
+hipError_t launch_moe_stack(const MoeArgs &a, const StackLayer *lt, uint32_t n_layers, bool normed, hipStream_t s);
+// After an expired in-kernel wait the library stops choosing the layers
+// whose workgroups wait for each other (the XCD-sliced layer and the stack);
+// kernels A and B run every later layer.
+void xcd_disable();
+void xcd_enable();
+bool xcd_disabled();
+// The measurement build's phase stamps of the one-launch layers
+// ([64][256][16] uint64, s_memrealtime ticks); hipErrorNotSupported in the
+// product build.
+hipError_t read_stamps(void *host, size_t bytes);
 // Top-n_sel routing of n_tokens rows of logits [n_tokens][n_expert] (<= 512
 // experts, 1 <= n_sel <= min(16, n_expert)): ids / weights [n_tokens][n_sel],
 // each row as the single-token layer routes it.

@@ -388,20 +388,173 @@ __host__ __device__ constexpr uint32_t normed_area_bytes(uint32_t H) {
     return 4 * (H + 64) * (1 + NORMED_MAX_R) + 32 + 128;
 }
 
+// A value the compiler must take as new at this point. The stacked layer
+// loops over its layers; indexes derived from the thread and workgroup ids
+// would otherwise be hoisted out of that loop and held in registers across
+// the whole layer (measured: 128 VGPRs and spills against 68 without the
+// loop), so its layer body takes its ids through these.
+__device__ __forceinline__ uint32_t opaque_v(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+__device__ __forceinline__ uint32_t opaque_s(uint32_t v) {
+    asm volatile("" : "+s"(v));
+    return v;
+}
+
+// Phase stamps of the one-launch layers, in the measurement build only
+// (KQ_STAMPS; build.py --stamps, libkatali_hip_stamps.so): s_memrealtime
+// (100 MHz) at fixed points of a layer, kept in registers and stored at the
+// layer's end to kq_stamps[tag % 64][workgroup][phase]. Phases: 0 layer
+// start, 1 routing and x in, 2 gate/up loads issued, 3 x staged, 4 wave 0's
+// dots done, 5 down loads issued, 6 h published, 7 first h poll issued, 8 h
+// seen, 9 h staged, 10 partials published, 11 partials seen, 12 y written,
+// 13 y poll started (stack), 14 y seen (stack), 15 logits seen (normed).
+// Wave 0 records every phase but 7 and 8, the first polling wave those.
+// In the product build the marks compile to nothing.
+constexpr uint32_t STAMP_LAYERS = 64, STAMP_PHASES = 16;
+#ifdef KQ_STAMPS
+__device__ uint64_t kq_stamps[STAMP_LAYERS * 256 * STAMP_PHASES];
+struct Stamps {
+    uint64_t t[STAMP_PHASES];
+    __device__ __forceinline__ void mark(int i) { t[i] = __builtin_amdgcn_s_memrealtime(); }
+    __device__ __forceinline__ void begin() {   // phases a layer does not pass stay 0
+#pragma unroll
+        for (int i = 0; i < (int)STAMP_PHASES; i++) t[i] = 0;
+        mark(0);
+    }
+    __device__ __forceinline__ void store(uint32_t tag, uint32_t wg, uint32_t tid, uint32_t poller0) {
+        uint64_t *o = kq_stamps + ((uint64_t)(tag % STAMP_LAYERS) * 256 + wg) * STAMP_PHASES;
+        if (tid == 0) {
+#pragma unroll
+            for (int i = 0; i < (int)STAMP_PHASES; i++)
+                if (i != 7 && i != 8) o[i] = t[i];
+        } else if (tid == poller0) {
+            o[7] = t[7];
+            o[8] = t[8];
+        }
+    }
+};
+#else
+struct Stamps {
+    __device__ __forceinline__ void mark(int) {}
+    __device__ __forceinline__ void begin() {}
+    __device__ __forceinline__ void store(uint32_t, uint32_t, uint32_t, uint32_t) {}
+};
+#endif
+
+// A layer of the stacked layer (k_moe_stack): its index l in the stack, the
+// previous layer's y as tagged words (yw, tag ytag; used when l > 0) and its
+// workgroups' completion words (yf: each workgroup's word takes the tag once
+// that workgroup's part of y is stored), and,
+// for the normed stack, the residual stream entering the layer (threads <
+// 256, k_norm_router's float4 q = t + 256 k), kept in registers from layer
+// to layer.
+struct StkCtx {
+    uint32_t l;
+    uint32_t ytag;
+    uint32_t *yw;
+    uint32_t *yf;   // the previous layer's completion words
+    float4 res[2];
+    Stamps st;   // (the measurement build's phase stamps)
+};
+
+// In the stack, a wait that expired in one layer would make later layers'
+// waits expire one after another (each about a second): every 1024 polls a
+// stack's waits also read the error word and give up once an expiry is
+// recorded there (the outputs are void then anyway).
+__device__ __forceinline__ bool stack_expired(const MoeArgs &a, uint32_t spins) {
+    return (spins & 1023u) == 0 && (ld_dev((uint32_t *)a.err) & 4u) != 0;
+}
+
+// Wait until every workgroup of the previous layer has stored its y: thread
+// t < XCD_G reads workgroup t's completion word (a few bytes per workgroup,
+// where the y itself is 8 KiB: every workgroup sees the whole y complete
+// about one round trip after the last store). Two rounds in flight; whole
+// waves up to XCD_G call it. `between` runs once, after the first round.
+template <class Between>
+__device__ __forceinline__ void poll_done(const MoeArgs &a, StkCtx &ctx, Between between) {
+    uint32_t *f = ctx.yf + min((uint32_t)threadIdx.x, XCD_G - 1);
+    uint32_t va, vb;
+    ctx.st.mark(13);
+    va = ld_dev(f);
+    between();
+    uint32_t spins = 0;
+    for (;;) {
+        vb = ld_dev(f);
+        if (__all(va == ctx.ytag)) break;
+        va = ld_dev(f);
+        if (__all(vb == ctx.ytag)) break;
+        if (++spins >= FSYNC_SPIN_LIMIT / 2 || stack_expired(a, spins)) {
+            if ((threadIdx.x & 63) == 0) atomicOr(a.err, 4);
+            break;
+        }
+    }
+    asm volatile("" ::"v"(va), "v"(vb));   // the round still in flight keeps its registers
+    ctx.st.mark(14);
+}
+
+// Read the previous layer's y words [4 q, 4 q + 4) of every q in qs
+// (tag ytag) and return them, once poll_done has seen every workgroup's y
+// stored (the words carry their tag, so a word not yet visible here is read
+// again). Whole waves call it; lanes with `own` false load word 0 and drop
+// it.
+template <int K>
+__device__ __forceinline__ void read_y(const MoeArgs &a, StkCtx &ctx, const uint32_t (&qs)[K], bool own,
+                                       float4 (&out)[K]) {
+    uint64_t wa[K][4];
+    auto issue = [&](uint64_t (&w)[K][4]) {
+#pragma unroll
+        for (int k = 0; k < K; k++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) w[k][j] = ld_dev2(ctx.yw + (own ? 2 * (4 * qs[k] + j) : 0));
+    };
+    auto seen = [&](const uint64_t (&w)[K][4]) {
+        bool ok = true;
+#pragma unroll
+        for (int k = 0; k < K; k++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) ok &= (uint32_t)(w[k][j] >> 32) == ctx.ytag;
+        return __all(ok || !own);
+    };
+    auto take = [&](const uint64_t (&w)[K][4]) {
+#pragma unroll
+        for (int k = 0; k < K; k++)
+            out[k] = make_float4(__uint_as_float((uint32_t)w[k][0]), __uint_as_float((uint32_t)w[k][1]),
+                                 __uint_as_float((uint32_t)w[k][2]), __uint_as_float((uint32_t)w[k][3]));
+    };
+    issue(wa);
+    uint32_t spins = 0;
+    while (!seen(wa)) {
+        if (++spins >= FSYNC_SPIN_LIMIT || stack_expired(a, spins)) {
+            if ((threadIdx.x & 63) == 0) atomicOr(a.err, 4);
+            break;
+        }
+        issue(wa);
+    }
+    take(wa);
+}
+
 // gen: this call's exchange generation (its load issued by the caller
 // before anything else); xr: the logits words, FSYNC_REP copies of 512.
-template <int NB, int C, int NT, int XPT>
+// STK (the normed stack, H <= 2048): from its second layer on the residual
+// stream comes from registers (ctx.res) and the residual step's delta is
+// the previous layer's y, polled from its tagged words; the new residual
+// goes back to ctx.res. The steps are otherwise the same, so every output is
+// the single normed layer's.
+template <int NB, int C, int NT, int XPT, bool STK = false>
 __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area, uint32_t U, GuRoute &rt,
-                                                float4 (&xv)[XPT], uint32_t gen, uint32_t *xr) {
+                                                float4 (&xv)[XPT], uint32_t gen, uint32_t *xr, StkCtx &ctx) {
     constexpr uint32_t H = 256 * NB;
     constexpr uint32_t KN = H <= 2048 ? 2 : 4;   // k_norm_router's float4 per thread
+    static_assert(!STK || KN == 2, "normed stack: hidden <= 2048");
     constexpr uint32_t Q4 = H / 4;
     constexpr uint32_t M = H / 16, TS = M + 4;   // chain length, transposed row stride
     constexpr uint32_t VT = 16 * TS;             // floats of one transposed vector
     constexpr uint32_t RF = NORMED_MAX_R * Q4;   // router float4s of a full workgroup share
     constexpr uint32_t RPT = (RF + NT - 1) / NT;
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t w = blockIdx.x;
+    const uint32_t tid = STK ? opaque_v(threadIdx.x) : threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t w = STK ? opaque_s(blockIdx.x) : blockIdx.x;
     float *xnT = (float *)area;
     float *rowsT = xnT + VT;
     double *part = (double *)(rowsT + NORMED_MAX_R * VT);
@@ -413,12 +566,15 @@ __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area,
     // 1. every load: x, delta and the norm weights (threads < 256, whole
     //    waves), the router rows (all threads; clamped)
     float4 vx[KN], vd[KN], vn[KN];
+    const bool from_regs = STK && ctx.l > 0;   // the stack past its first layer
     if (tid < 256) {
 #pragma unroll
         for (uint32_t k = 0; k < KN; k++) {
             const uint32_t q = min(tid + k * 256, Q4 - 1);
-            vx[k] = *(const float4 *)&a.nx[4 * q];
-            vd[k] = a.ndelta ? *(const float4 *)&a.ndelta[4 * q] : make_float4(0.f, 0.f, 0.f, 0.f);
+            if (!from_regs) {
+                vx[k] = *(const float4 *)&a.nx[4 * q];
+                vd[k] = a.ndelta ? *(const float4 *)&a.ndelta[4 * q] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
             vn[k] = *(const float4 *)&a.nw[4 * q];
         }
     }
@@ -428,6 +584,24 @@ __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area,
         const uint32_t f = min(tid + NT * i, RF - 1), v = f / Q4, q = f % Q4;
         const uint32_t r = min(w + U * v, a.n_expert - 1);
         rv[i] = *(const float4 *)&a.router[(uint64_t)r * H + 4 * q];
+    }
+    if constexpr (STK) {
+        if (from_regs) {
+            // the delta is the previous layer's y (its tagged words), the
+            // residual the registers; then a barrier: every wave is past its
+            // last LDS read of the previous layer before the rows land there
+            if (tid < 256) {   // (XCD_G: one completion word per thread)
+                uint32_t qs[KN];
+#pragma unroll
+                for (uint32_t k = 0; k < KN; k++) {
+                    qs[k] = min(tid + k * 256, Q4 - 1);
+                    vx[k] = ctx.res[k];
+                }
+                poll_done(a, ctx, [] {});
+                read_y<KN>(a, ctx, qs, true, vd);
+            }
+        }
+        __syncthreads();
     }
     // all NORMED_MAX_R row slots, transposed (those past R hold a copy of the
     // last row; a clamped thread writes what its twin writes)
@@ -443,10 +617,10 @@ __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area,
     // 2. residual step and the sum of squares
     if (tid < 256) {
         double sq = 0.0;
-        const bool unit = a.nscale == 1.0f;
+        const bool unit = from_regs || a.nscale == 1.0f;
 #pragma unroll
         for (uint32_t k = 0; k < KN; k++) {
-            if (a.ndelta) {
+            if (from_regs || a.ndelta) {
                 if (unit) {
                     vx[k].x = vx[k].x + vd[k].x; vx[k].y = vx[k].y + vd[k].y;
                     vx[k].z = vx[k].z + vd[k].z; vx[k].w = vx[k].w + vd[k].w;
@@ -460,6 +634,10 @@ __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area,
             sq += own ? (double)vx[k].y * (double)vx[k].y : 0.0;
             sq += own ? (double)vx[k].z * (double)vx[k].z : 0.0;
             sq += own ? (double)vx[k].w * (double)vx[k].w : 0.0;
+        }
+        if constexpr (STK) {
+#pragma unroll
+            for (uint32_t k = 0; k < KN; k++) ctx.res[k] = vx[k];   // the residual entering the next layer's step
         }
         sq = wave_sum_f64(sq);
         if (lane == 0) part[wave] = sq;
@@ -486,7 +664,7 @@ __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area,
             xnT[at(c + 3)] = o.w;
             if (w == 0) {
                 if (a.nxn_out) *(float4 *)&a.nxn_out[c] = o;
-                if (a.ndelta) *(float4 *)&a.nx_out[c] = vx[k];
+                if (STK ? a.nx_out != nullptr : a.ndelta != nullptr) *(float4 *)&a.nx_out[c] = vx[k];
             }
         }
     }
@@ -545,12 +723,13 @@ __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area,
                 take(va);
                 break;
             }
-            if (++spins >= FSYNC_SPIN_LIMIT) {
+            if (++spins >= FSYNC_SPIN_LIMIT || (STK && stack_expired(a, spins))) {
                 if (lane == 0) atomicOr(a.err, 4);
                 take(va);
                 break;
             }
         }
+        ctx.st.mark(15);
         const WaveRoute wr = wave_topk<C>(a, lv);
         if (lane < 16) {
             rte[lane] = wr.id;
@@ -611,7 +790,9 @@ __device__ __forceinline__ void gu_unit(const MoeArgs &a, uint32_t unit, uint8_t
     uint32_t xqv[XPT], xdv[XPT];
     if constexpr (NORMED) {
         // the steps before the layer, here: xn and the routing from its logits
-        normed_prologue<NB, C, NT, XPT>(a, lds + L.scl, gridDim.x, rt, xv, ld_dev(a.fsync + 1), a.fsync + FSYNC_R);
+        StkCtx none{};
+        normed_prologue<NB, C, NT, XPT>(a, lds + L.scl, gridDim.x, rt, xv, ld_dev(a.fsync + 1), a.fsync + FSYNC_R,
+                                        none);
     } else {
         // every wave routes on its own: no barrier before its weight loads
         // (routing by rank over the workgroup, 8 threads per expert, measured
@@ -1511,10 +1692,13 @@ constexpr int XCD_HW = 4;                // h words per polling thread at most: 
 // LDS at lds + lds_a(..).gu. NORMED: the steps before the layer first
 // (normed_prologue, with the caller's generation gen and the logits words
 // at FSYNC_XR); x is the normalized vector it forms, the routing comes from
-// its logits.
-template <int NB, int C, int IW, int IWS, class Down, bool NORMED = false>
+// its logits. STK: a layer of the stacked layer (ctx); past the stack's
+// first layer x is the previous layer's y, read from its tagged words (or,
+// NORMED, the residual step takes that y as its delta), and no wave issues
+// a weight load before the whole of that y is seen.
+template <int NB, int C, int IW, int IWS, class Down, bool NORMED = false, bool STK = false>
 __device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_t li, uint8_t *lds, GuRoute &rt,
-                                        Down down, uint32_t shb = 0, bool sh_dbg = false, uint32_t gen = 0) {
+                                        Down down, uint32_t shb, bool sh_dbg, uint32_t gen, StkCtx &ctx) {
     constexpr int RW = 4;                      // rows per wave (kernel A's at these widths)
     static_assert(a1_rw<NB>() == RW, "gu_part: kernel A's 4-row waves");
     constexpr int R = 2 * IW + 2 * IWS, GW = (R + RW - 1) / RW;   // rows, waves with rows
@@ -1526,7 +1710,7 @@ __device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_
     constexpr int HPL = (WH + 63) / 64;
     static_assert(R <= 64 && GW <= NT / 64 && LPG <= 16, "gu_part shape");
     const LdsA L = lds_a(a.hidden, NB);
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t tid = STK ? opaque_v(threadIdx.x) : threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const bool rows = wave < (uint32_t)GW;
     pin_args(a.gate, a.up, a.gate_sh, a.up_sh);
 
@@ -1535,11 +1719,34 @@ __device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_
     float4 xv[XPT];
     uint32_t xqv[XPT], xdv[XPT];
     if constexpr (NORMED) {
-        normed_prologue<NB, C, NT, XPT>(a, lds + L.scl, XCD_G, rt, xv, gen, a.fsync + FSYNC_XR);
+        normed_prologue<NB, C, NT, XPT, STK>(a, lds + L.scl, XCD_G, rt, xv, gen, a.fsync + FSYNC_XR, ctx);
     } else {
         float lv[C];
         route_issue<C>(a, lv, rt);
-        if (a.xq == nullptr) {
+        if (STK && ctx.l > 0) {
+            // the routing's logits (and a layer's own x) in flight with the
+            // first round of polls, ranked meanwhile; then a barrier: every
+            // lane task's words of the previous layer's y seen. That y is the
+            // layer's x, or, when the layer has an x of its own, only waited
+            // for (the order of a decode chain)
+            const bool own_x = a.x != nullptr;
+            if (own_x) {
+#pragma unroll
+                for (int i = 0; i < XPT; i++) xv[i] = *(const float4 *)(a.x + 4 * min(tid + NT * i, (uint32_t)XTASKS - 1));
+            }
+            if (tid < XCD_G) {   // whole waves: one completion word each
+                poll_done(a, ctx, [&] { route_finish<C>(a, lv, rt); });
+            } else {
+                route_finish<C>(a, lv, rt);
+            }
+            if (!own_x && tid < (uint32_t)XTASKS) {   // whole waves
+                uint32_t qs[XPT];
+#pragma unroll
+                for (int i = 0; i < XPT; i++) qs[i] = min(tid + NT * i, (uint32_t)XTASKS - 1);
+                read_y<XPT>(a, ctx, qs, true, xv);
+            }
+            __syncthreads();
+        } else if (a.xq == nullptr) {
 #pragma unroll
             for (int i = 0; i < XPT; i++) xv[i] = *(const float4 *)(a.x + 4 * min(tid + NT * i, (uint32_t)XTASKS - 1));
         } else {
@@ -1551,9 +1758,10 @@ __device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_
                 xdv[i] = ld_u16(b);
             }
         }
-        route_finish<C>(a, lv, rt);
+        if (!STK || ctx.l == 0) route_finish<C>(a, lv, rt);
     }
     __builtin_amdgcn_s_waitcnt(VMCNT0);
+    ctx.st.mark(1);
 
     const uint64_t rb = NB * 144;
     const uint8_t *gb, *ub;
@@ -1596,6 +1804,7 @@ __device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_
 #pragma unroll
         for (int k = 0; k < LPG; k++) q[k] = ld16(chunk(k));
     }
+    ctx.st.mark(2);
     if (slot == 0 && li == 0 && wave == 0)
         route_publish(a, rt.eid, (NORMED || a.logits) && a.n_sel > 0 ? route_weight(rt.logit, a.n_sel) : rt.w);
 
@@ -1624,6 +1833,7 @@ __device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_
         }
     }
     __syncthreads();
+    ctx.st.mark(3);
 
     float *gu = (float *)(lds + L.gu);
     if (rows) {
@@ -1672,7 +1882,9 @@ __device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_
             }
         }
     }
+    ctx.st.mark(4);
     down();   // behind this wave's gate/up loads in the CU's queue
+    ctx.st.mark(5);
     __syncthreads();
     if (a.dbg_gu && tid < (uint32_t)R) {
         float *d = a.dbg_gu + (uint64_t)slot * 2 * a.ffn + (tid < (uint32_t)IW ? 0 : a.ffn) + IW * li + tid % IW;
@@ -1697,8 +1909,11 @@ __device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_
 // partial per row and unit. Wave 0 sums, per row, the eight slots in rank
 // order and then the U shared partials in unit order, weight 1 (the shared
 // expert enters last, as in kernel B).
-template <int NB, int C, class QD, int S, int IPL, int IW, bool SH, bool NORMED>
-__global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
+// The body of one layer: k_moe_xcd runs it once; k_moe_stack runs it per
+// layer of a stack (STK, ctx), with that layer's tag gen + 1 + ctx.l; the
+// generation words advance by n_layers at the stack's last layer.
+template <int NB, int C, class QD, int S, int IPL, int IW, bool SH, bool NORMED, bool STK>
+__device__ __forceinline__ void xcd_body(const MoeArgs &a, uint32_t gen, uint32_t n_layers, StkCtx &ctx) {
     constexpr uint32_t NT = a1_threads<NB>();
     constexpr uint32_t P = S / QD::IPB;
     constexpr uint32_t H = 256 * NB;
@@ -1717,12 +1932,12 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
     static_assert(!SH || (XCD_SLOTS % U == 0 && RS * IH <= 128), "XCD layer shared units");
     static_assert(HW <= XCD_HW * 64 * XCD_POLL_WAVES && F % 256 == 0, "XCD layer ffn");
     extern __shared__ __align__(16) uint8_t lds[];
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t b = blockIdx.x, xs = b % XCD_SLOTS, li = b / XCD_SLOTS;
+    const uint32_t tid = STK ? opaque_v(threadIdx.x) : threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t b = STK ? opaque_s(blockIdx.x) : blockIdx.x, xs = b % XCD_SLOTS, li = b / XCD_SLOTS;
     const uint32_t u = xs % U, part = xs / U;   // SH: this XCD's unit and its part of the output rows
     pin_args(a.down, a.down_sh, a.y, a.fsync, a.hq8);
     uint32_t *gw = a.fsync + FSYNC_X + b;
-    const uint32_t gen = ld_dev(gw);   // issued first, used last
+    ctx.st.begin();
 
     // the down share: row r = tid / S of the tile, lane s = tid % S; with SH,
     // threads t < RS * IH also take item IH * (u % 2) + t % IH of block u / 2
@@ -1749,10 +1964,10 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
                 rawS = QD::load(a.down_sh + (uint64_t)rowS * rbd + bkS * QD::BB, (int)itemS);
         }
     };
-    gu_part<NB, C, IW, IWS, decltype(load_down), NORMED>(a, xs, li, lds, rt, load_down, 128 * u + IWS * li,
-                                                         part == 0, gen);
+    gu_part<NB, C, IW, IWS, decltype(load_down), NORMED, STK>(a, xs, li, lds, rt, load_down, 128 * u + IWS * li,
+                                                              part == 0, gen + ctx.l, ctx);
 
-    uint32_t tag = gen;
+    uint32_t tag = gen + ctx.l;
     asm volatile("" : "+v"(tag));
     tag += 1;
     uint32_t *hx = a.fsync + FSYNC_XH + 2 * F * xs;    // slot xs's h words
@@ -1770,6 +1985,7 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
                 st_dev2(hxs + 2 * (IWS * li + j), ((uint64_t)tag << 32) | __float_as_uint(h));
             }
         }
+        ctx.st.mark(6);
     }
 
     // 3. the h words: word t of thread pt is word pt + 256 t (the slot's h
@@ -1838,17 +2054,19 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
             }
             return __all(need == 0);
         };
+        ctx.st.mark(7);
         issue(va);
         for (;;) {
             issue(vb);
             if (take(va)) break;
             issue(va);
             if (take(vb)) break;
-            if (++spins >= FSYNC_SPIN_LIMIT / 2) {
+            if (++spins >= FSYNC_SPIN_LIMIT / 2 || (STK && stack_expired(a, spins))) {
                 if (lane == 0) atomicOr(a.err, 4);
                 break;
             }
         }
+        ctx.st.mark(8);
         // kernel A's quantizer on every word first, with no store between
         // them (the NW words' dependency chains interleave; one wave per SIMD
         // runs this, so it is latency-bound), then the stores
@@ -1897,6 +2115,7 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
         }
     }
     __syncthreads();
+    ctx.st.mark(9);
 
     // the tile's unweighted down partials (and, with SH, the unit's shared ones)
     float x = 0.0f;
@@ -1909,6 +2128,7 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
     x = group_sum<S>(x);
     if (r < TRX && s == 0)
         st_dev2(a.fsync + FSYNC_XP + 2 * (xs * H + row0 + r), ((uint64_t)tag << 32) | __float_as_uint(x));
+    ctx.st.mark(10);
     if constexpr (SH) {
         if (tid < ((RS * IH + 63) & ~63u)) {   // whole waves
             const float xsh = group_sum<IH>(QD::dot_q8_u(rawS, unS, (int)itemS, actS, bkS));
@@ -1922,7 +2142,7 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
     if (wave == 0) {
         float rw = (NORMED || a.logits) && a.n_sel > 0 ? route_weight(rt.logit, a.n_sel) : rt.w;
         rw = (int)lane < a.n_sel ? rw : ((int)lane == a.n_sel && a.has_shared ? 1.0f : 0.0f);
-        if (lane == 0) st_dev(gw, tag);   // gen was read at the start: advance it now
+        if (lane == 0 && ctx.l + 1 == n_layers) st_dev(gw, tag);   // gen was read at the start: advance it now
         const uint32_t q = lane / TRC, c = lane % TRC;   // lane: slot (or unit) q, row c
         const uint32_t yr = row0 + xs * TRC + c;
         uint32_t *pw = a.fsync + FSYNC_XP + 2 * (min(q, XCD_SLOTS - 1) * H + yr);
@@ -1939,11 +2159,12 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
             pv = ld_dev2(pw);
             if constexpr (SH) sv = ld_dev2(pws);
             if (ok(pv, sv)) break;
-            if (++spins >= FSYNC_SPIN_LIMIT) {
+            if (++spins >= FSYNC_SPIN_LIMIT || (STK && stack_expired(a, spins))) {
                 if (lane == 0) atomicOr(a.err, 4);
                 break;
             }
         }
+        ctx.st.mark(11);
         const float v = __uint_as_float((uint32_t)pv);
         float y = 0.0f;
 #pragma unroll
@@ -1958,67 +2179,203 @@ __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
             for (uint32_t k = 0; k < U; k++) sh += __shfl(vs, (int)(k * TRC + c), WAVE);   // unit order
             y = fmaf(1.0f, sh, y);   // the shared expert, last
         }
+        if constexpr (STK) {   // the next layer's x (or delta) as tagged words
+            if (lane < TRC && ctx.l + 1 < n_layers)
+                st_dev2(a.fsync + FSYNC_XY + 2 * ((ctx.l & 1) * XCD_MAX_HIDDEN + row0 + xs * TRC + lane),
+                        ((uint64_t)tag << 32) | __float_as_uint(y));
+        }
         if (lane < TRC) a.y[row0 + xs * TRC + lane] = y;
+        if constexpr (STK) {
+            // this workgroup's y is stored (the stores acknowledged): its
+            // completion word, which the next layer's weight loads wait for
+            if (ctx.l + 1 < n_layers) {
+                __builtin_amdgcn_s_waitcnt(VMCNT0);
+                if (lane == 0) st_dev(a.fsync + FSYNC_XF + (ctx.l & 1) * XCD_G + b, tag);
+            }
+        }
+        ctx.st.mark(12);
     }
     if (poller) {
 #pragma unroll
         for (int i = 0; i < NW; i++) asm volatile("" ::"v"(va[i]), "v"(vb[i]));
     }
+    ctx.st.store(tag, b, tid, first_poller);
 }
 
 template <int NB, int C, class QD, int S, int IPL, int IW, bool SH, bool NORMED>
-static hipError_t go_xcd(const MoeArgs &a, hipStream_t s) {
+__global__ void __launch_bounds__(a1_threads<NB>()) k_moe_xcd(MoeArgs a) {
+    const uint32_t gen = ld_dev(a.fsync + FSYNC_X + blockIdx.x);   // issued first, used last
+    StkCtx ctx{};
+    xcd_body<NB, C, QD, S, IPL, IW, SH, NORMED, false>(a, gen, 1, ctx);
+}
+
+// The stacked layer: n_layers layers of one shape in one launch (the XCD
+// layer's workgroups stay resident from layer to layer, so no launch gap
+// separates them). Layer l takes its weights, routing and outputs from
+// lt[l]. Plain: layer 0's x is a.x (or a.xq), layer l's is its own lt[l].x
+// or, when that is null, layer l - 1's y.
+// NORMED: layer 0's residual step reads a.nx (and a.ndelta), layer l's adds
+// layer l - 1's y to the residual stream, then the norm, the router and the
+// layer as the normed layer runs them. A layer waits for the whole of the
+// previous layer's y before any weight load of its own; only what does not
+// depend on that y (its routing from given logits, its router rows and norm
+// weights) is read before.
+template <int NB, int C, class QD, int S, int IPL, int IW, bool SH, bool NORMED>
+__global__ void __launch_bounds__(a1_threads<NB>()) k_moe_stack(MoeArgs a0, const StackLayer *__restrict__ lt, uint32_t n_layers) {
+    const uint32_t gen = ld_dev(a0.fsync + FSYNC_X + blockIdx.x);
+    StkCtx ctx{};
+    for (uint32_t l = 0; l < n_layers; l++) {
+        const StackLayer &L = lt[l];
+        MoeArgs a = a0;
+        a.gate = L.gate;
+        a.up = L.up;
+        a.down = L.down;
+        a.gate_sh = L.gate_sh;
+        a.up_sh = L.up_sh;
+        a.down_sh = L.down_sh;
+        a.ids_out = L.ids_out;
+        a.wts_out = L.wts_out;
+        a.y = L.y;
+        if constexpr (NORMED) {
+            a.nw = L.nw;
+            a.router = L.router;
+            a.nx_out = L.x_out;
+            a.nxn_out = L.xn_out;
+            a.logits_out = L.logits_out;
+        } else {
+            a.logits = L.logits;
+            a.step = L.step;
+            a.logits_stride = L.logits_stride;
+            a.ids = L.ids;
+            a.wts = L.wts;
+        }
+        if (l > 0) {
+            a.x = NORMED ? nullptr : L.x;   // plain: the layer's own x, or (null) the previous layer's y
+            a.xq = nullptr;
+            a.nx = nullptr;
+            a.ndelta = nullptr;
+        }
+        ctx.l = l;
+        ctx.ytag = gen + l;   // layer l - 1's tag
+        ctx.yw = a0.fsync + FSYNC_XY + 2 * (((l + 1) & 1) * XCD_MAX_HIDDEN);
+        ctx.yf = a0.fsync + FSYNC_XF + ((l + 1) & 1) * XCD_G;
+        xcd_body<NB, C, QD, S, IPL, IW, SH, NORMED, true>(a, gen, n_layers, ctx);
+    }
+}
+
+// Whether every workgroup of kernel k (XCD_G workgroups of nt threads, lds
+// bytes of LDS) can be resident at once on this device: the one-launch
+// layers' workgroups wait for each other, so they may run only then. Asked
+// of the occupancy API once per kernel and LDS size.
+static bool all_resident(const void *k, uint32_t nt, uint32_t lds) {
+    static thread_local const void *last_k = nullptr;
+    static thread_local uint32_t last_lds = 0;
+    static thread_local int last_dev = -1, last_n = 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    if (k != last_k || lds != last_lds || dev != last_dev) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, (int)nt, (size_t)lds) != hipSuccess) n = 0;
+        last_k = k;
+        last_lds = lds;
+        last_dev = dev;
+        last_n = n;
+    }
+    return xcd_coresident(device_cu_count(), last_n, XCD_G);
+}
+
+// lt: the stacked layer's per-layer table (nl layers), else the single layer
+template <int NB, int C, class QD, int S, int IPL, int IW, bool SH, bool NORMED>
+static hipError_t go_xcd(const MoeArgs &a, hipStream_t s, const StackLayer *lt, uint32_t nl) {
     uint32_t lds = lds_a(a.hidden, NB).total + (SH ? 2 : 1) * act_bytes(32 * IW);
     // the normed prologue's area starts at the scale records, which are
     // written only after its last read
     if (NORMED) lds = max(lds, lds_a(a.hidden, NB).scl + normed_area_bytes(a.hidden));
+    const void *k = lt ? (const void *)k_moe_stack<NB, C, QD, S, IPL, IW, SH, NORMED>
+                       : (const void *)k_moe_xcd<NB, C, QD, S, IPL, IW, SH, NORMED>;
     if (lds > 64 * 1024) {
-        const hipError_t e = hipFuncSetAttribute((const void *)k_moe_xcd<NB, C, QD, S, IPL, IW, SH, NORMED>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL((k_moe_xcd<NB, C, QD, S, IPL, IW, SH, NORMED>), dim3(XCD_G), dim3(a1_threads<NB>()), lds, s, a);
+    if (!all_resident(k, a1_threads<NB>(), lds)) return hipErrorNotSupported;
+    if (lt)
+        hipLaunchKernelGGL((k_moe_stack<NB, C, QD, S, IPL, IW, SH, NORMED>), dim3(XCD_G), dim3(a1_threads<NB>()), lds,
+                           s, a, lt, nl);
+    else
+        hipLaunchKernelGGL((k_moe_xcd<NB, C, QD, S, IPL, IW, SH, NORMED>), dim3(XCD_G), dim3(a1_threads<NB>()), lds, s,
+                           a);
     return hipGetLastError();
 }
 // 16 lanes per down row: Q6_K 4 items x 4 block slots (ffn <= 1024: one
 // block per lane), Q4_K 8 items x 2 block slots (up to two)
 template <int NB, int C, int IW, bool SH, bool NORMED>
-static hipError_t go_xcd_q(const MoeArgs &a, hipStream_t s) {
-    if (a.down_type == T_Q6_K) return go_xcd<NB, C, Q6K, 16, 1, IW, SH, NORMED>(a, s);
-    if constexpr (IW <= 16) return go_xcd<NB, C, Q4K, 16, 1, IW, SH, NORMED>(a, s);
-    else return go_xcd<NB, C, Q4K, 16, 2, IW, SH, NORMED>(a, s);
+static hipError_t go_xcd_q(const MoeArgs &a, hipStream_t s, const StackLayer *lt, uint32_t nl) {
+    if (a.down_type == T_Q6_K) return go_xcd<NB, C, Q6K, 16, 1, IW, SH, NORMED>(a, s, lt, nl);
+    if constexpr (IW <= 16) return go_xcd<NB, C, Q4K, 16, 1, IW, SH, NORMED>(a, s, lt, nl);
+    else return go_xcd<NB, C, Q4K, 16, 2, IW, SH, NORMED>(a, s, lt, nl);
 }
 template <int NB, int C, bool SH, bool NORMED>
-static hipError_t go_xcd_f(const MoeArgs &a, hipStream_t s) {
+static hipError_t go_xcd_f(const MoeArgs &a, hipStream_t s, const StackLayer *lt, uint32_t nl) {
     switch (a.ffn) {
-        case 256: return go_xcd_q<NB, C, 8, SH, NORMED>(a, s);
-        case 512: return go_xcd_q<NB, C, 16, SH, NORMED>(a, s);
+        case 256: return go_xcd_q<NB, C, 8, SH, NORMED>(a, s, lt, nl);
+        case 512: return go_xcd_q<NB, C, 16, SH, NORMED>(a, s, lt, nl);
         case 768:
-            if constexpr (!SH) return go_xcd_q<NB, C, 24, SH, NORMED>(a, s);   // the shared units must divide the eight XCDs
+            if constexpr (!SH) return go_xcd_q<NB, C, 24, SH, NORMED>(a, s, lt, nl);   // the shared units must divide the eight XCDs
             else return hipErrorNotSupported;
         case 1024:
-            if constexpr (!SH) return go_xcd_q<NB, C, 32, SH, NORMED>(a, s);   // shared rows would not fit 64 per workgroup
+            if constexpr (!SH) return go_xcd_q<NB, C, 32, SH, NORMED>(a, s, lt, nl);   // shared rows would not fit 64 per workgroup
             else return hipErrorNotSupported;
         default: return hipErrorNotSupported;
     }
 }
 template <int NB, bool SH, bool NORMED = false>
-static hipError_t go_xcd_c(const MoeArgs &a, hipStream_t s) {
-    return a.n_expert <= 128 ? go_xcd_f<NB, 2, SH, NORMED>(a, s) : go_xcd_f<NB, 4, SH, NORMED>(a, s);
+static hipError_t go_xcd_c(const MoeArgs &a, hipStream_t s, const StackLayer *lt = nullptr, uint32_t nl = 0) {
+    return a.n_expert <= 128 ? go_xcd_f<NB, 2, SH, NORMED>(a, s, lt, nl) : go_xcd_f<NB, 4, SH, NORMED>(a, s, lt, nl);
 }
 // hipErrorNotSupported when the shape does not fit the XCD-sliced layer:
 // eight slots (one per XCD), or with shared_units eight routed experts plus
-// the shared expert in 128-value units (ffn 256 or 512 then; measured
-// slower than kernels A and B at the 2048/512 top-8-of-256 shape: 14.2
-// against 13.7 us per layer, so opt-in)
-static hipError_t launch_moe_xcd(const MoeArgs &a, uint32_t n_slots, bool shared_units, hipStream_t s) {
+// the shared expert in 128-value units (ffn 256 or 512 then), hidden 1024 or
+// 2048, ffn <= 1024, <= 256 experts, a 256-CU device on which every
+// workgroup can be resident at once, and the one-launch layers not turned
+// off after an expired wait (xcd_disable)
+static hipError_t launch_moe_xcd(const MoeArgs &a, uint32_t n_slots, bool shared_units, hipStream_t s,
+                                 const StackLayer *lt = nullptr, uint32_t nl = 0) {
     const uint32_t nb = a.hidden / 256;
     const bool spread = shared_units && a.n_sel == (int)XCD_SLOTS && a.has_shared;
-    if (!a.fsync || !(n_slots == XCD_SLOTS || spread) || a.n_sel < 1 || !(nb == 4 || nb == 8) ||
+    if (!a.fsync || xcd_disabled() || !(n_slots == XCD_SLOTS || spread) || a.n_sel < 1 || !(nb == 4 || nb == 8) ||
         a.n_expert > 256 || a.ffn > 1024 || (spread && a.ffn > 512) || device_cu_count() != (int)XCD_G)
         return hipErrorNotSupported;
-    if (spread) return nb == 8 ? go_xcd_c<8, true>(a, s) : go_xcd_c<4, true>(a, s);
-    return nb == 8 ? go_xcd_c<8, false>(a, s) : go_xcd_c<4, false>(a, s);
+    if (spread) return nb == 8 ? go_xcd_c<8, true>(a, s, lt, nl) : go_xcd_c<4, true>(a, s, lt, nl);
+    return nb == 8 ? go_xcd_c<8, false>(a, s, lt, nl) : go_xcd_c<4, false>(a, s, lt, nl);
+}
+
+// The phase stamps (the measurement build), as kq_stamps holds them.
+hipError_t read_stamps(void *host, size_t bytes) {
+#ifdef KQ_STAMPS
+    const size_t n = sizeof(uint64_t) * STAMP_LAYERS * 256 * STAMP_PHASES;
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(kq_stamps), bytes < n ? bytes : n, 0, hipMemcpyDeviceToHost);
+#else
+    (void)host;
+    (void)bytes;
+    return hipErrorNotSupported;
+#endif
+}
+
+static bool g_xcd_off = false;
+void xcd_disable() { g_xcd_off = true; }
+void xcd_enable() { g_xcd_off = false; }
+bool xcd_disabled() { return g_xcd_off; }
+
+hipError_t launch_moe_stack(const MoeArgs &a, const StackLayer *lt, uint32_t n_layers, bool normed, hipStream_t s) {
+    if (!lt || n_layers < 1 || a.n_expert > MAX_EXPERT || a.n_sel > MAX_SEL || a.hidden > XCD_MAX_HIDDEN)
+        return hipErrorInvalidValue;
+    const uint32_t n_slots = (uint32_t)a.n_sel + (a.has_shared ? 1u : 0u);
+    if (!normed) return launch_moe_xcd(a, n_slots, true, s, lt, n_layers);
+    const uint32_t nb = a.hidden / 256;
+    if (!a.fsync || xcd_disabled() || n_slots != XCD_SLOTS || a.has_shared || !(nb == 4 || nb == 8) ||
+        a.n_expert > XCD_G || a.ffn > 1024 || device_cu_count() != (int)XCD_G)
+        return hipErrorNotSupported;
+    return nb == 8 ? go_xcd_c<8, false, true>(a, s, lt, n_layers) : go_xcd_c<4, false, true>(a, s, lt, n_layers);
 }
 
 uint64_t moe_route_words() { return 2 * MAX_SLOTS; }
@@ -2238,7 +2595,8 @@ hipError_t launch_moe_normed(MoeArgs a, float *xn_buf, float *logits_buf, hipStr
     // eight slots on 256 CUs: the XCD-sliced layer with the steps before it
     // in its prologue, one launch (each workgroup dots at most one router
     // row at <= 256 experts)
-    if (allow_xcd && a.fsync && n_slots == XCD_SLOTS && (a.hidden == 1024 || a.hidden == 2048) && a.ffn <= 1024 &&
+    if (allow_xcd && a.fsync && !xcd_disabled() && n_slots == XCD_SLOTS && (a.hidden == 1024 || a.hidden == 2048) &&
+        a.ffn <= 1024 &&
         a.n_expert <= XCD_G && device_cu_count() == (int)XCD_G) {
         MoeArgs b = a;
         b.x = nullptr;

@@ -56,8 +56,11 @@ constexpr uint32_t MB_FORK_PAIRS = 96;   // batches from this many pairs run the
 constexpr uint32_t MB_DN_CHUNK = 8;   // h blocks staged at once by the down kernel beyond 3 blocks
 constexpr uint32_t MB_REC = 20;      // ints per grouped-GEMM entry: 4 + MB_BIG pairs
 __host__ __device__ inline uint32_t mb_small_off() { return 16; }
-__host__ __device__ inline uint32_t mb_big_off(uint32_t P) { return 16 + 3 * P; }
-__host__ __device__ inline uint32_t mb_order_off(uint32_t P) { return 16 + 3 * P + MB_REC * P; }
+// the grouped-GEMM records start on a 16-byte boundary (each is read as
+// int4s, MB_REC a multiple of 4): the small entries' 3 P ints rounded up
+__host__ __device__ inline uint32_t mb_big_off(uint32_t P) { return 16 + ((3 * P + 3) & ~3u); }
+__host__ __device__ inline uint32_t mb_order_off(uint32_t P) { return mb_big_off(P) + MB_REC * P; }
+static_assert(MB_REC % 4 == 0, "grouped-GEMM records: whole int4s");
 uint64_t moe_batch_meta_words(uint32_t P) { return mb_order_off(P) + P; }
 
 // Inclusive prefix sum over the 64 lanes of a wave on the VALU: row_shr 1, 2,

@@ -66,6 +66,11 @@ SIGNATURES = {
     "katali_hip_add_rmsnorm": (C.c_int, [_vp, _vp, _f32, _vp, _u64, _f32, _vp]),
     "katali_hip_moe_route_batch": (C.c_int, [_vp, _u32, _u32, _i32, _vp, _vp]),
     "katali_hip_rmsnorm_matvec_f32": (C.c_int, [_vp, _vp, _f32, _vp, _vp, _u64, _f32, _vp, _vp, _u64, _vp]),
+    "katali_hip_moe_stack_create": (C.c_int, [_vp, _i32, _i32, _f32, _vp, _i32, C.POINTER(_vp)]),
+    "katali_hip_moe_stack_run": (C.c_int, [_vp, _vp, _vp, _f32]),
+    "katali_hip_moe_stack_destroy": (C.c_int, [_vp]),
+    "katali_hip_one_launch": (C.c_int, [_i32]),
+    "katali_hip_phase_stamps": (C.c_int, [_vp, _sz]),
 }
 
 
@@ -85,6 +90,13 @@ class KataliHipMoeRoute(C.Structure):
 class KataliHipMoeNorm(C.Structure):
     _fields_ = [("struct_size", _u32), ("x", _vp), ("delta", _vp), ("scale", _f32), ("x_out", _vp),
                 ("norm_w", _vp), ("eps", _f32), ("xn_out", _vp), ("router", _vp), ("logits_out", _vp)]
+
+
+class KataliHipMoeStackLayer(C.Structure):
+    _fields_ = [("struct_size", _u32), ("x", _vp), ("gate_exps", _vp), ("up_exps", _vp), ("down_exps", _vp),
+                ("gate_shexp", _vp), ("up_shexp", _vp), ("down_shexp", _vp), ("route", KataliHipMoeRoute),
+                ("norm_w", _vp), ("router", _vp), ("y", _vp), ("x_out", _vp), ("xn_out", _vp),
+                ("logits_out", _vp)]
 
 
 # error codes of include/katali_hip.h
@@ -151,6 +163,23 @@ class DeviceBuffer:
             self.free()
         except Exception:
             pass
+
+
+class MoeStack:
+    """A handle from katali_hip_moe_stack_create; holds the buffers its table
+    points at until it is destroyed."""
+
+    def __init__(self, hip: "KataliHip", handle: int, keep):
+        self.hip, self.handle, self._keep = hip, handle, keep
+
+    def run(self, x, delta=None, scale=1.0) -> None:
+        self.hip.check(self.hip.lib.katali_hip_moe_stack_run(self.handle, x.ptr, None if delta is None else delta.ptr,
+                                                             scale))
+
+    def destroy(self) -> None:
+        if self.handle:
+            self.hip.check(self.hip.lib.katali_hip_moe_stack_destroy(self.handle))
+            self.handle = None
 
 
 class KataliHip:
@@ -257,6 +286,18 @@ class KataliHip:
         self.check(self.lib.katali_hip_moe_layer_normed(C.byref(desc), C.byref(nrm), n_sel, p(ids_out),
                                                         p(weights_out), y.ptr))
 
+    def phase_stamps(self) -> np.ndarray:
+        """The measurement build's phase stamps, [64 layer slots][256
+        workgroups][16 phases] s_memrealtime ticks (100 MHz)."""
+        out = np.zeros((64, 256, 16), np.uint64)
+        self.check(self.lib.katali_hip_phase_stamps(out.ctypes.data, out.nbytes))
+        return out
+
+    def one_launch(self, mode: int = -1) -> bool:
+        """The one-launch layers on (1) or off (0), or only asked (-1);
+        returns whether they were on before the call."""
+        return bool(self.lib.katali_hip_one_launch(mode))
+
     def moe_check(self, desc, n_sel, n_tokens=0) -> None:
         """Raises HipError when a layer (n_tokens 0) or a batch of n_tokens of
         this shape would be refused; needs no device."""
@@ -271,6 +312,32 @@ class KataliHip:
         self.check(self.lib.katali_hip_moe_layer_debug(C.byref(desc), C.byref(route),
                                                        None if x is None else x.ptr,
                                                        None if xq is None else xq.ptr, y.ptr, gu.ptr, hq8.ptr))
+
+    def moe_stack(self, desc, n_sel, layers, normed=False, eps=1e-6) -> "MoeStack":
+        """A stack of layers of desc's shape (its weight pointers unused).
+        layers: dicts with keys gate, up, down, y and optionally shared (3
+        buffers), x (plain stack: a layer's own input; absent: the previous
+        layer's y), route (a moe_route), norm_w, router, x_out, xn_out,
+        logits_out."""
+        p = lambda b: None if b is None else b.ptr  # noqa: E731
+        arr = (KataliHipMoeStackLayer * len(layers))()
+        keep = [desc]
+        for i, L in enumerate(layers):
+            sh = L.get("shared")
+            e = arr[i]
+            e.struct_size = C.sizeof(KataliHipMoeStackLayer)
+            e.gate_exps, e.up_exps, e.down_exps = p(L["gate"]), p(L["up"]), p(L["down"])
+            if sh is not None:
+                e.gate_shexp, e.up_shexp, e.down_shexp = sh[0].ptr, sh[1].ptr, sh[2].ptr
+            if L.get("route") is not None:
+                e.route = L["route"]
+            for k in ("x", "norm_w", "router", "y", "x_out", "xn_out", "logits_out"):
+                setattr(e, k, p(L.get(k)))
+            keep.append(L)
+        h = _vp()
+        self.check(self.lib.katali_hip_moe_stack_create(C.byref(desc), n_sel, 1 if normed else 0, eps, arr,
+                                                        len(layers), C.byref(h)))
+        return MoeStack(self, h.value, keep)
 
     def moe_batch(self, desc, n_tokens, n_sel, ids, weights, x, y, mfma_min_tokens=0) -> None:
         b = KataliHipMoeBatch(C.sizeof(KataliHipMoeBatch), n_tokens, n_sel, mfma_min_tokens,

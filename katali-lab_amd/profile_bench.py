@@ -2,6 +2,14 @@
 
     python katali-lab_amd/profile_bench.py --workload moe48 --out DIR [--steps 8]
     python katali-lab_amd/profile_bench.py --workload moe48 --out DIR --summarize-only
+    python katali-lab_amd/profile_bench.py --workload moe48 --out DIR --phases [--stacked]
+
+--phases: no profiler; bench.py runs on the measurement build
+(libkatali_hip_stamps.so, `python katali-lab_amd/build.py --stamps`), whose
+one-launch layers record s_memrealtime phase stamps, and the stamps of the
+timed replays' last 64 layers become profiles/phases_<workload>[_stacked].md
+(per phase, over the layers, the median of the workgroups' median and of
+their latest time after the layer's first workgroup started).
 
 Three runs of bench.py under rocprofv3 (each a child process; rocprofv3
 runs from /tmp with TMPDIR=/tmp):
@@ -106,6 +114,66 @@ def pick(d, sub):
     return [(k, v) for k, v in d.items() if kernel_of(k) == sub]
 
 
+PHASES = ["layer start (first workgroup = 0)", "routing and x in", "gate/up loads issued", "x staged (q8_1 in LDS)",
+          "wave 0's gate/up dots done", "down loads issued", "h published", "first h poll issued (polling wave)",
+          "slot's h seen (polling wave)", "h staged as q8_1", "down partials published", "eight partials seen",
+          "y written", "previous y: poll started (stack)", "previous y seen (stack)", "router logits seen (normed)"]
+
+
+def phases(args, out):
+    """Run bench.py on the measurement build, write the phase table."""
+    import numpy as np
+    lib = os.path.join(REPO, "katali-lab_amd", "libkatali_hip_stamps.so")
+    if not os.path.exists(lib):
+        sys.exit(f"{lib} missing: python katali-lab_amd/build.py --stamps")
+    npy = os.path.join(out, "stamps.npy")
+    extra = ["--stacked"] if args.stacked else []
+    extra += ["--normed-layer"] if args.normed_layer else []
+    cmd = [sys.executable, os.path.join(REPO, "bench.py"), "--workload", args.workload, "--steps", str(args.steps),
+           "--warmup", str(args.warmup), "--no-cpu-baseline", "--dump-stamps", npy] + extra
+    if not args.summarize_only and run(cmd, os.path.join(out, "phases.log"), {"KATALI_HIP_DLL": lib}) != 0:
+        sys.exit(f"bench run failed (see {out}/phases.log)")
+    st = np.load(npy).astype(np.int64)          # [64 layer slots][256 workgroups][16 phases], 10 ns ticks
+    slots = [l for l in range(st.shape[0]) if (st[l, :, 0] > 0).all() and (st[l, :, 12] > 0).any()]
+    t0 = {l: int(st[l, :, 0].min()) for l in slots}
+    order = sorted(slots, key=lambda l: t0[l])
+    med, mx = [[] for _ in PHASES], [[] for _ in PHASES]
+    for l in slots:
+        for p in range(len(PHASES)):
+            v = st[l, :, p]
+            v = v[v > 0]
+            if v.size:
+                rel = (v - t0[l]) / 100.0
+                med[p].append(float(np.median(rel)))
+                mx[p].append(float(rel.max()))
+    period = [(t0[b] - t0[a]) / 100.0 for a, b in zip(order, order[1:]) if 0 < t0[b] - t0[a] < 10000]
+    gap = [(t0[b] - int(st[a, :, 12].max())) / 100.0 for a, b in zip(order, order[1:])
+           if 0 < t0[b] - t0[a] < 10000]
+    name = f"phases_{args.workload}" + ("_stacked" if args.stacked else "") + ("_normed" if args.normed_layer else "")
+    md = os.path.join(REPO, "profiles", f"{name}.md")
+    flags = (" --stacked" if args.stacked else "") + (" --normed-layer" if args.normed_layer else "")
+    with open(md, "w") as f:
+        f.write(f"# Phase stamps: {args.workload}{flags}\n\n")
+        f.write(f"Made by `python katali-lab_amd/build.py --stamps && python katali-lab_amd/profile_bench.py "
+                f"--workload {args.workload} --steps {args.steps} --warmup {args.warmup} --out <out> --phases{flags}`, "
+                f"which runs `KATALI_HIP_DLL=katali-lab_amd/libkatali_hip_stamps.so python3 bench.py --workload "
+                f"{args.workload} --steps {args.steps} --warmup {args.warmup} --no-cpu-baseline --dump-stamps "
+                f"<out>/stamps.npy{flags}` (the measurement build: the one-launch layers record s_memrealtime, "
+                f"100 MHz, at each phase; wave 0 of every workgroup, the first polling wave for the h polls).\n\n")
+        f.write(f"{len(slots)} layers of the timed replays. Times in us after the layer's first workgroup "
+                f"started; per layer the median and the latest over its 256 workgroups, then the median over "
+                f"the layers.\n\n")
+        f.write("| phase | median workgroup | latest workgroup |\n|---|---|---|\n")
+        for p, label in enumerate(PHASES):
+            if med[p]:
+                f.write(f"| {p}: {label} | {np.median(med[p]):.2f} | {np.median(mx[p]):.2f} |\n")
+        if period:
+            f.write(f"\nLayer period (first workgroup to the next layer's first workgroup): median "
+                    f"{np.median(period):.2f} us over {len(period)} layer pairs; from the last y written to the next "
+                    f"layer's first workgroup: median {np.median(gap):.2f} us.\n")
+    print(open(md).read())
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--workload", default="moe48", choices=sorted(KERNELS))
@@ -118,6 +186,10 @@ def main():
                          "moe40cold)")
     ap.add_argument("--two-launch", action="store_true",
                     help="moe48, moe40cold: kernels A and B instead of the XCD-sliced layer (KATALI_HIP_XCD=0)")
+    ap.add_argument("--phases", action="store_true",
+                    help="moe48, moe40cold, moe48tok: the measurement build's phase stamps (no profiler)")
+    ap.add_argument("--stacked", action="store_true", help="with --phases: bench.py --stacked")
+    ap.add_argument("--normed-layer", action="store_true", help="with --phases: bench.py --normed-layer")
     ap.add_argument("--one-stream", action="store_true",
                     help="moebatch: the grouped GEMM on the library stream (KATALI_HIP_ONE_STREAM=1), so "
                          "per-kernel times add up to the layer")
@@ -142,6 +214,9 @@ def main():
         profile_name, traffic_name = profile_name + "_one_stream", wl + "_one_stream"
     out = os.path.join(os.path.abspath(args.out), traffic_name)   # rocprofv3 runs from /tmp
     os.makedirs(out, exist_ok=True)
+    if args.phases:
+        phases(args, out)
+        return
     bench = [sys.executable, os.path.join(REPO, "bench.py"), "--workload", wl, "--steps", str(args.steps),
              "--warmup", str(args.warmup), "--no-cpu-baseline", "--calibrate-copy", str(COPY_MIB)] + \
         EXTRA_ARGS.get(wl, [])

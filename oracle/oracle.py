@@ -193,6 +193,8 @@ class Oracle:
         if shared is not None:
             sffn, sg, su, sd = shared
             d.shared_ffn, d.gate_sh, d.up_sh, d.down_sh = sffn, _ptr(sg), _ptr(su), _ptr(sd)
+        # the struct holds raw pointers: keep the arrays alive with it
+        d._keep = (gate, up, down, shared)
         return d
 
     def moe_layer_q8(self, desc: KqoMoe, x, ids, w, with_stages=False):

@@ -4,7 +4,8 @@ The library allocates its MoE scratch once at its largest size and never
 moves it, so a graph captured around a small call stays valid after larger
 calls (wider layers, a 64-token batch). Calls that would end a capture
 (sync, memset, upload, download, malloc) are refused while one is open, and
-frees are deferred to its end; every replay is checked against an eager run.
+a buffer freed during a capture lives as long as the graph made from it;
+every replay is checked against an eager run.
 """
 import numpy as np
 import pytest
@@ -95,12 +96,45 @@ def test_calls_that_would_end_a_capture_are_refused(hip):
                      lambda: y1.download(np.float32, 4), lambda: hip.alloc(64)):
             with pytest.raises(HipError, match="capture"):
                 call()
-        doomed.free()                     # deferred until the capture ends
+        doomed.free()                     # released with the graph
     finally:
         g = hip.graph_end()
     try:
         hip.graph_launch(g)
         hip.sync()
         assert np.array_equal(y1.download(np.uint32), y0.download(np.uint32))
+    finally:
+        hip.graph_destroy(g)
+
+
+def test_buffer_freed_during_capture_lives_with_the_graph(hip):
+    """A buffer the captured work reads, freed inside the capture, stays
+    allocated as long as the graph: replays keep reading it, while new
+    allocations of its size (filled with other data) are made between them;
+    katali_hip_graph_destroy releases it."""
+    rng = np.random.default_rng(33)
+    m = _layer(hip, 512, 256, 16, False, seed=301)
+    xv = S.activation(rng, 512)
+    route = hip.moe_route(2, logits=hip.to_device(rng.standard_normal(16).astype(np.float32)))
+    y0, y1 = hip.alloc(512 * 4), hip.alloc(512 * 4)
+    hip.moe_layer(m, route, y0, x=hip.to_device(xv))
+    hip.sync()
+    want = y0.download(np.uint32)
+    x = hip.to_device(xv)
+    hip.graph_begin()
+    try:
+        hip.moe_layer(m, route, y1, x=x)
+        x.free()                          # the graph reads x: it lives on with the graph
+    finally:
+        g = hip.graph_end()
+    others = []
+    try:
+        for i in range(3):
+            junk = hip.to_device(rng.standard_normal(512).astype(np.float32) * 1e3)
+            others.append(junk)
+            hip.memset(y1, 0, 512 * 4)
+            hip.graph_launch(g)
+            hip.sync()
+            assert np.array_equal(y1.download(np.uint32), want), i
     finally:
         hip.graph_destroy(g)

@@ -298,22 +298,35 @@ def test_xcd_wait_expiry_reports_and_recovers(hip, oracle, moes, monkeypatch):
     generation word of the XCD-sliced layer off before a launch: its words
     then carry a tag no other workgroup waits for, so the waits of that call
     run to their bound and expire (each workgroup still ends normally, in
-    about a second). The next sync reports KATALI_HIP_E_TIMEOUT and the
-    library clears its exchange words; the calls after it, their generations
-    counting again from zero, give the layer's own bits."""
+    about a second). The next sync reports KATALI_HIP_E_TIMEOUT, the library
+    clears its exchange words and turns the one-launch layers off: the calls
+    after it run kernels A and B (their bits). Turned back on
+    (katali_hip_one_launch(1)), the layer gives its own bits again, its
+    generations counting from zero."""
     import katali_hip as K
     hidden, ffn, n_expert, n_sel, shared, down_type = CASES[0]
     m = moes(hidden, ffn, n_expert, shared, down_type)
     rng = np.random.default_rng(21)
     x = S.activation(rng, hidden)
     logits = rng.standard_normal(n_expert).astype(np.float32)
+    set_mode(monkeypatch, "two_launch")
+    y_two = run_layer(hip, m, x, n_sel, logits=logits)[0]
     set_mode(monkeypatch, "xcd")
     y_ref = run_layer(hip, m, x, n_sel, logits=logits)[0]
+    assert not np.array_equal(y_two.view(np.uint32), y_ref.view(np.uint32))   # the two forms are told apart
+    assert hip.one_launch(-1)
     monkeypatch.setenv("KATALI_HIP_TEST_SKEW", "1")
-    with pytest.raises(HipError) as err:
-        run_layer(hip, m, x, n_sel, logits=logits)
-    assert err.value.rc == K.E_TIMEOUT, err.value
-    monkeypatch.delenv("KATALI_HIP_TEST_SKEW")
+    try:
+        with pytest.raises(HipError) as err:
+            run_layer(hip, m, x, n_sel, logits=logits)
+        assert err.value.rc == K.E_TIMEOUT, err.value
+        monkeypatch.delenv("KATALI_HIP_TEST_SKEW")
+        assert not hip.one_launch(-1)
+        for call in range(2):
+            y = run_layer(hip, m, x, n_sel, logits=logits)[0]
+            assert np.array_equal(y.view(np.uint32), y_two.view(np.uint32)), call
+    finally:
+        hip.one_launch(1)
     for call in range(3):
         y = run_layer(hip, m, x, n_sel, logits=logits)[0]
         assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32)), call

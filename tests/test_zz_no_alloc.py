@@ -1,10 +1,13 @@
 """katali_hip_moe_layer_noalloc against katali_hip_moe_layer through the C ABI.
 
-The allocation-free entry point runs the same kernels on a static device
-scratch, so its output must be bit-identical to the allocating entry point's.
-Two calls in a row, the second with a smaller problem (fewer slots, narrower
-rows); the largest layer shape the LDS admits; a shape beyond it refused
-before any launch.
+The allocation-free entry point chooses the same kernels as the allocating
+one (the one-launch XCD-sliced layer where that takes it, with its exchange
+words in the static scratch; kernels A and B elsewhere or with
+KATALI_HIP_XCD=0) on a static device scratch, so its output must be
+bit-identical to the allocating entry point's, in both modes. Two calls in a
+row, the second with a smaller problem (fewer slots, narrower rows); the
+largest layer shape the LDS admits; a shape beyond it refused before any
+launch.
 """
 import numpy as np
 import pytest
@@ -13,7 +16,7 @@ import kq_synth as S
 from katali_hip import HipError
 from oracle import Q4_K, Q6_K
 
-pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("two_launch_layer")]
+pytestmark = pytest.mark.gpu
 
 
 def _problem(hip, rng, hidden, ffn, n_expert, shared):
@@ -28,11 +31,21 @@ def _problem(hip, rng, hidden, ffn, n_expert, shared):
     return hip.moe_desc(hidden, ffn, n_expert, *dev, shared=dsh), dev, dsh
 
 
-def test_noalloc_layer_matches_allocating_layer(hip):
+@pytest.mark.parametrize("mode", ["default", "two_launch"])
+def test_noalloc_layer_matches_allocating_layer(hip, mode, monkeypatch):
+    """default: the top-8 of 128 layer (2048 -> 768) and the top-8 of 256 plus
+    shared expert layer run as the one-launch layer in both entry points;
+    two_launch (KATALI_HIP_XCD=0): kernels A and B in both."""
+    for k in ("KATALI_HIP_XCD", "KATALI_HIP_XCD_SHARED", "KATALI_HIP_FUSED"):
+        monkeypatch.delenv(k, raising=False)
+    if mode == "two_launch":
+        monkeypatch.setenv("KATALI_HIP_XCD", "0")
     rng = np.random.default_rng(2024)
-    # the larger call first (top-8 of 128, 2048 -> 768), then a smaller one
-    for hidden, ffn, n_expert, n_sel, shared in ((2048, 768, 128, 8, False), (1024, 512, 32, 3, True)):
-        print(f"[noalloc] hidden={hidden} ffn={ffn} n_expert={n_expert} n_sel={n_sel} shared={shared}", flush=True)
+    # the larger calls first, then a smaller one
+    for hidden, ffn, n_expert, n_sel, shared in ((2048, 768, 128, 8, False), (2048, 512, 256, 8, True),
+                                                 (1024, 512, 32, 3, True)):
+        print(f"[noalloc] mode={mode} hidden={hidden} ffn={ffn} n_expert={n_expert} n_sel={n_sel} shared={shared}",
+              flush=True)
         desc, keep, keep_sh = _problem(hip, rng, hidden, ffn, n_expert, shared)
         x = hip.to_device(S.activation(rng, hidden))
         logits = hip.to_device(rng.standard_normal(n_expert).astype(np.float32))
@@ -46,7 +59,7 @@ def test_noalloc_layer_matches_allocating_layer(hip):
         assert np.any(a != 0)
 
 
-def test_noalloc_layer_at_the_largest_shape(hip):
+def test_noalloc_layer_at_the_largest_shape(hip, two_launch_layer):
     """17 slots (16 routed + shared) at ffn 6912: the widest h any layer shape
     takes (17 * 216 * 36 = 132192 bytes, the LDS bound's maximum), inside the
     135168-byte scratch; device-filled weights, bit-identical outputs."""
