@@ -343,6 +343,64 @@ def bench_moe(hip, name, steps, warmup, ring=64, vocab=0, normed=False, stacked=
 
 
 # ---------------------------------------------------------------------------
+# Streaming floors: a MoE layer's bytes with no arithmetic
+# ---------------------------------------------------------------------------
+FLOOR_KINDS = {0: "one launch reading the layer's bytes",
+               1: "gate/up bytes, then down bytes, in two launches",
+               2: "gate/up then down bytes in one launch with the XCD-sliced layer's two in-kernel waits"}
+
+
+def bench_floor(hip, base, steps, warmup, kinds=None):
+    """Each of the three floors (katali_hip_stream_floor) over L units of one
+    layer's weight bytes (distinct per unit, like the layers), one graph per
+    pass of L units; per unit time and GB/s."""
+    L, hidden, ffn, n_expert, n_sel, shared = MOE_WORKLOADS[base]
+    slots = n_sel + (1 if shared else 0)
+    a_bytes = slots * 2 * ffn * row_bytes(Q4_K, hidden)
+    b_bytes = slots * hidden * row_bytes(Q6_K, ffn)
+    unit = a_bytes + b_bytes
+    pool = hip.alloc(L * unit)
+    hip.memset(pool, 1, L * unit)
+    sync = hip.alloc(4096)
+    hip.memset(sync, 0, 4096)
+    hip.sync()
+    out = {}
+    for kind in (kinds or FLOOR_KINDS):
+        def units():
+            for u in range(L):
+                a = View(pool.ptr + u * unit)
+                b = View(pool.ptr + u * unit + a_bytes)
+                if kind == 0:
+                    hip.stream_floor(0, a, unit, None, 0, sync)
+                else:
+                    hip.stream_floor(kind, a, a_bytes, b, b_bytes, sync)
+        units()
+        hip.sync()
+        hip.graph_begin()
+        units()
+        g = hip.graph_end()
+        for _ in range(warmup):
+            hip.graph_launch(g)
+        e0, e1 = hip.event(), hip.event()
+        hip.sync()
+        hip.record(e0)
+        for _ in range(steps):
+            hip.graph_launch(g)
+        hip.record(e1)
+        ms = hip.elapsed_ms(e0, e1)
+        hip.sync()
+        hip.graph_destroy(g)
+        hip.event_destroy(e0)
+        hip.event_destroy(e1)
+        us = ms * 1e3 / steps / L
+        out[kind] = {"what": FLOOR_KINDS[kind], "us_per_unit": round(us, 3), "gbs": round(unit / us / 1e3, 1)}
+        print(f"[bench] floor {kind}: {us:.2f} us per unit, {unit / us / 1e3:.0f} GB/s", file=sys.stderr, flush=True)
+    pool.free()
+    sync.free()
+    return out, (L, a_bytes, b_bytes)
+
+
+# ---------------------------------------------------------------------------
 # Duty cycle: host work between MoE layer submissions
 # ---------------------------------------------------------------------------
 DUTY_INTERVALS_US = (0, 20, 200, 1000)   # host time per layer (200: the engine's ~6 % GPU duty cycle)
@@ -990,7 +1048,7 @@ def main():
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", default="moe48",
-                    choices=sorted(MOE_WORKLOADS) + sorted(TOKEN_WORKLOADS) + sorted(GEMV_WORKLOADS) + sorted(DENSE_WORKLOADS) + ["moebatch", "moe48duty"])
+                    choices=sorted(MOE_WORKLOADS) + sorted(TOKEN_WORKLOADS) + sorted(GEMV_WORKLOADS) + sorted(DENSE_WORKLOADS) + ["moebatch", "moe48duty", "floor48"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--normed-layer", action="store_true",
                     help="moe48tok: katali_hip_moe_layer_normed (norm, router and layer in two launches per layer) "
@@ -1001,6 +1059,8 @@ def main():
     ap.add_argument("--dump-stamps", default="", metavar="NPY",
                     help="moe48 / moe40cold / moe48tok with the measurement build (KATALI_HIP_DLL="
                          "libkatali_hip_stamps.so): save the phase stamps of the timed replays' last 64 layers")
+    ap.add_argument("--floor-kind", type=int, action="append", choices=sorted(FLOOR_KINDS),
+                    help="floor48: only this floor (repeatable; profiling)")
     ap.add_argument("--batch-points", default="", metavar="NxT,...",
                     help="moebatch: only these (n_sel x tokens) points, e.g. 8x64,2x64 (profiling)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -1111,6 +1171,21 @@ def main():
                   ("k_moe_xcd with the norm and router in its prologue, one launch" if one else
                    "k_moe_gu with the norm and router, k_moe_down") + "; output norm, head, argmax)")
         extra = {"tok_s": round(res["tok_s"], 2)}
+    elif args.workload == "floor48":
+        floors, (L, a_bytes, b_bytes) = bench_floor(hip, "moe48", args.steps, args.warmup, args.floor_kind)
+        head = floors[min(floors)]
+        unit_bytes = a_bytes + b_bytes
+        unit_ms = head["us_per_unit"] / 1e3
+        res = {"value": head["gbs"], "ms_per_step": unit_ms * L}
+        metric = "HBM read floor for one MoE layer's weight bytes (top-8 of 128, 2048 -> 768 -> 2048): GB/s"
+        config = {
+            "workload": f"floor48: {L} units of one moe48 layer's weight bytes ({a_bytes} B of gate/up, {b_bytes} B "
+                        f"of down), distinct per unit, streamed with no arithmetic by 256 workgroups of 1024 "
+                        f"threads (katali_hip_stream_floor), one graph per pass; value: the one-launch read",
+            "layers": L, "parallelism": "single GPU",
+        }
+        kernel = "k_floor_read (one launch per unit)"
+        extra = {"floors": floors}
     elif args.workload == "moe48duty":
         res, shape = bench_duty(hip, "moe48", args.steps, args.warmup)
         L, hidden, ffn, n_expert, n_sel, shared = shape

@@ -418,6 +418,18 @@ int katali_hip_event_destroy(void *event);
  * library returns KATALI_HIP_E_UNSUPPORTED. Waits for queued work first.
  * No counterpart in the reference. */
 int katali_hip_phase_stamps(void *host, size_t bytes);
+/* The floors a MoE layer is measured against: the same bytes streamed with
+ * no arithmetic in the layer's launch shape (256 workgroups of 1024
+ * threads, each reading a contiguous 1/256 share with 16-byte loads):
+ * kind 0 one launch reading a; kind 1 a then b in two launches (kernels A
+ * and B's split); kind 2 a then b in one launch with the XCD-sliced layer's
+ * two in-kernel waits (the 32 workgroups of an XCD after a, the 8 sharing
+ * output rows after b; needs a 256-CU device). Sizes are multiples of 16.
+ * sync: a device buffer of 4096 bytes, zeroed once by the caller and kept
+ * for every later call (generation words). No counterpart in the
+ * reference. */
+int katali_hip_stream_floor(int32_t kind, const void *a, size_t a_bytes, const void *b, size_t b_bytes,
+                            void *sync);
 
 /* ---- self-test and synthetic data for the harnesses ------------------------ */
 /* cuda-dp4a-selftest equivalent (README.md:17): a synthetic Q4_K and Q6_K

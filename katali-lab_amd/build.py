@@ -38,7 +38,8 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function", "-I" + INCLUDE,
 ]
-HIP_SOURCES = ["kq_gemv.hip", "kq_moe.hip", "kq_moe_batch.hip", "kq_sample.hip", "kq_norm.hip", "kq_gemv_f32.hip", "katali_hip.cpp"]
+HIP_SOURCES = ["kq_moe.hip", "kq_gemv.hip", "kq_moe_batch.hip", "kq_sample.hip", "kq_norm.hip", "kq_gemv_f32.hip",
+               "kq_floor.hip", "katali_hip.cpp"]
 C_FLAGS = ["-std=c11", "-O2", "-fPIC", "-Wall", "-Wextra", "-I" + INCLUDE, "-D_POSIX_C_SOURCE=200809L"]
 
 

@@ -712,6 +712,21 @@ int katali_hip_phase_stamps(void *host, size_t bytes) {
     return e == hipSuccess ? KATALI_HIP_OK : hip_fail(e, "phase stamps");
 }
 
+int katali_hip_stream_floor(int32_t kind, const void *a, size_t a_bytes, const void *b, size_t b_bytes,
+                            void *sync) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (kind < 0 || kind > 2) return fail(KATALI_HIP_E_INVALID, "floor kind %d (0..2)", kind);
+    if (!a || !sync || (kind && !b)) return fail(KATALI_HIP_E_INVALID, "null buffer");
+    if (!a_bytes || a_bytes % 16 || (kind && (!b_bytes || b_bytes % 16)))
+        return fail(KATALI_HIP_E_INVALID, "floor sizes must be non-zero multiples of 16");
+    const hipError_t e = kq::launch_floor(kind, (const uint8_t *)a, a_bytes, (const uint8_t *)b, b_bytes,
+                                          (uint32_t *)sync, g_stream);
+    if (e == hipErrorNotSupported)
+        return fail(KATALI_HIP_E_UNSUPPORTED, "floor kind 2 needs 256 workgroups resident at once (256 CUs)");
+    return launched(e, "stream floor");
+}
+
 int katali_hip_one_launch(int32_t mode) {
     const int was = kq::xcd_disabled() ? 0 : 1;
     if (mode == 0) kq::xcd_disable();

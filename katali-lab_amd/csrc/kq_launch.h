@@ -235,6 +235,13 @@ bool xcd_disabled();
 // ([64][256][16] uint64, s_memrealtime ticks); hipErrorNotSupported in the
 // product build.
 hipError_t read_stamps(void *host, size_t bytes);
+// The streaming floors (kq_floor.hip): kind 0 one read of a, 1 a then b in
+// two launches, 2 a then b in one launch with the XCD-sliced layer's two
+// in-kernel waits; sync: floor_sync_words() + 1 zeroed words, kept between
+// launches.
+uint32_t floor_sync_words();
+hipError_t launch_floor(int kind, const uint8_t *a, uint64_t a_bytes, const uint8_t *b, uint64_t b_bytes,
+                        uint32_t *sync, hipStream_t s);
 // Top-n_sel routing of n_tokens rows of logits [n_tokens][n_expert] (<= 512
 // experts, 1 <= n_sel <= min(16, n_expert)): ids / weights [n_tokens][n_sel],
 // each row as the single-token layer routes it.

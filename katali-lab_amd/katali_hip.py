@@ -71,6 +71,7 @@ SIGNATURES = {
     "katali_hip_moe_stack_destroy": (C.c_int, [_vp]),
     "katali_hip_one_launch": (C.c_int, [_i32]),
     "katali_hip_phase_stamps": (C.c_int, [_vp, _sz]),
+    "katali_hip_stream_floor": (C.c_int, [_i32, _vp, _sz, _vp, _sz, _vp]),
 }
 
 
@@ -292,6 +293,11 @@ class KataliHip:
         out = np.zeros((64, 256, 16), np.uint64)
         self.check(self.lib.katali_hip_phase_stamps(out.ctypes.data, out.nbytes))
         return out
+
+    def stream_floor(self, kind: int, a, a_bytes: int, b, b_bytes: int, sync) -> None:
+        """The streaming floors (katali_hip_stream_floor)."""
+        self.check(self.lib.katali_hip_stream_floor(kind, a.ptr, a_bytes, None if b is None else b.ptr, b_bytes,
+                                                     sync.ptr))
 
     def one_launch(self, mode: int = -1) -> bool:
         """The one-launch layers on (1) or off (0), or only asked (-1);

@@ -36,6 +36,7 @@ REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 COPY_MIB = 256
 # kernels summed per workload unit; the first is launched once per unit
 KERNELS = {
+    "floor48": ("k_floor_read",),
     "moe48": ("k_moe_xcd",),
     "moe40cold": ("k_moe_xcd",),
     "gemv6144": ("k_gemv",),
@@ -44,9 +45,9 @@ KERNELS = {
     "moebatch": ("k_mb_group", "k_quantize_q8_1", "k_moe_gu_grp", "k_mb_gu_mfma", "k_moe_down_grp", "k_mb_down_mfma",
                  "k_mb_combine"),
 }
-UNIT_NAME = {"moe48": "MoE layer", "moe40cold": "MoE layer", "gemv6144": "GEMV", "qwen8b": "dense layer",
+UNIT_NAME = {"floor48": "one read of a moe48 layer's weight bytes", "moe48": "MoE layer", "moe40cold": "MoE layer", "gemv6144": "GEMV", "qwen8b": "dense layer",
              "moebatch": "batched MoE layer (n_sel 8, 64 tokens)", "moe48tok": "decode token"}
-EXTRA_ARGS = {"moebatch": ["--batch-points", "8x64"]}
+EXTRA_ARGS = {"moebatch": ["--batch-points", "8x64"], "floor48": ["--floor-kind", "0"]}
 PROFILE_NAME = {"moebatch": "batched_moe_moebatch_8x64", "moe48tok": "decode_token_moe48tok", "qwen8b": "k_gemv_k_moe_gu_k_moe_down_qwen8b"}
 # eight-slot layers (and eight routed experts plus the shared expert at ffn
 # 256 or 512) run as k_moe_xcd unless KATALI_HIP_XCD=0 (--two-launch)
