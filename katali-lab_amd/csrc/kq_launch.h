@@ -179,7 +179,13 @@ constexpr uint32_t FSYNC_XR = FSYNC_XSP + 2 * XCD_MAX_UNITS * XCD_MAX_HIDDEN;
 // generations are the XCD layer's.
 constexpr uint32_t FSYNC_XY = FSYNC_XR + FSYNC_REP * 2 * 512;
 constexpr uint32_t FSYNC_XF = FSYNC_XY + 2 * 2 * XCD_MAX_HIDDEN;
-constexpr uint32_t fsync_words() { return FSYNC_XF + 2 * XCD_G; }
+// From FSYNC_DHC, kernel A's half units (a dense FFN): one counter per q8_1
+// block of h (DH_MAX_BLOCKS; every call adds 2 per block), then from
+// FSYNC_DHW each block's 32 values as words {float, generation}.
+constexpr uint32_t DH_MAX_BLOCKS = 512;   // ffn <= 16384
+constexpr uint32_t FSYNC_DHC = FSYNC_XF + 2 * XCD_G;
+constexpr uint32_t FSYNC_DHW = FSYNC_DHC + DH_MAX_BLOCKS;
+constexpr uint32_t fsync_words() { return FSYNC_DHW + 2 * 32 * DH_MAX_BLOCKS; }
 static_assert(FSYNC_H + 2 * 9 * FUSED_MAX_G <= FSYNC_R, "exchange areas overlap");
 // The steps before the layer and the layer in two launches (MoeArgs' n*
 // fields and router set, n_sel >= 1, hidden <= 4096): kernel A forms the

@@ -216,11 +216,11 @@ __device__ __forceinline__ void route_publish(const MoeArgs &a, int32_t id, floa
 struct LdsA {
     uint32_t xact, scl, gu, total;
 };
-__host__ __device__ inline LdsA lds_a(uint32_t hidden, uint32_t nb) {
+__host__ __device__ inline LdsA lds_a(uint32_t hidden, uint32_t nb, uint32_t rows = 64) {
     LdsA L;
     L.xact = 0;
-    L.scl = L.xact + act_bytes(hidden);   // 64 rows x nb headers x 4 groups x float4
-    L.gu = L.scl + 64 * nb * 64;
+    L.scl = L.xact + act_bytes(hidden);   // rows x nb headers x 4 groups x float4
+    L.gu = L.scl + rows * nb * 64;
     L.total = L.gu + 64 * 4;
     return L;
 }
@@ -758,12 +758,23 @@ __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area,
 struct NoMore {
     __device__ void operator()(const GuRoute &) const {}
 };
-template <int NB, int C, bool FUSED, class After = NoMore, bool NORMED = false>
+// HALF (a dense FFN, when 32-row units would leave CUs with uneven counts
+// of workgroups): the workgroup takes half of a unit, 16 gate + 16 up rows,
+// 16 values of the q8_1 block of h. Workgroups b and b + 8 of each run of
+// 16 (one XCD) take the two halves of one block. Each publishes its 16
+// values as tagged words; one atomic per block (a counter that every call
+// raises by 2 and nothing resets: its parity tells first from second, its
+// half the call) elects the second to arrive, which reads the other half and
+// writes the block with kernel A's quantizer (the same values, so the same
+// bits). Nobody waits for a workgroup that has not started.
+template <int NB, int C, bool FUSED, class After = NoMore, bool NORMED = false, bool HALF = false>
 __device__ __forceinline__ void gu_unit(const MoeArgs &a, uint32_t unit, uint8_t *lds, GuRoute &rt, uint32_t flag,
                                         uint32_t *hx = nullptr, After after = After()) {
     // FUSED: flag is this call's generation; h's words are tagged flag + 1
     // and go to hx + 2 * (9 * unit + k), k < 9.
-    constexpr int RW = a1_rw<NB>();
+    static_assert(!(HALF && (FUSED || NORMED)), "half units: the plain dense FFN");
+    constexpr int RW = HALF ? a1_rw<NB>() / 2 : a1_rw<NB>();
+    constexpr int HR = HALF ? 16 : 32;         // gate (and up) rows of the workgroup
     constexpr int NT = a1_threads<NB>();
     constexpr int ITEMS = 8 * NB;              // lane items per row
     constexpr int LPL = RW * ITEMS / 64;       // chunks per lane over the wave's rows
@@ -773,10 +784,14 @@ __device__ __forceinline__ void gu_unit(const MoeArgs &a, uint32_t unit, uint8_t
     constexpr int M = ITEMS >= 64 ? ITEMS / 64 : 1;   // items per lane
     constexpr int WH = RW * NB;                // block headers of one wave's rows
     constexpr int HPL = (WH + 63) / 64;        // header loads per lane
-    const LdsA L = lds_a(a.hidden, NB);
+    const LdsA L = lds_a(a.hidden, NB, 2 * HR);   // half units: half the scale table
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t nblk = a.ffn / 32;
-    const uint32_t slot = unit / nblk, jb = unit % nblk;
+    // HALF: workgroup b of a run of 16 takes half (b % 16) / 8 of block
+    // 8 (b / 16) + b % 8 (of all slots' blocks); else unit = the block
+    const uint32_t hh = HALF ? (unit % 16) / 8 : 0;
+    const uint32_t ub_ = HALF ? 8 * (unit / 16) + unit % 8 : unit;
+    const uint32_t slot = ub_ / nblk, jb = ub_ % nblk;
     const uint8_t *xq = a.xq;
     const bool publisher = unit == 0 && wave == 0;
     pin_args(a.gate, a.up, a.gate_sh, a.up_sh, a.hq8);
@@ -833,8 +848,9 @@ __device__ __forceinline__ void gu_unit(const MoeArgs &a, uint32_t unit, uint8_t
         gb = a.gate_sh;
         ub = a.up_sh;
     }
-    auto row_ptr = [&](uint32_t v) -> const uint8_t * {   // v in [0, 64)
-        return v < 32 ? gb + (uint64_t)(32 * jb + v) * rb : ub + (uint64_t)(32 * jb + v - 32) * rb;
+    auto row_ptr = [&](uint32_t v) -> const uint8_t * {   // v in [0, 2 HR)
+        return v < (uint32_t)HR ? gb + (uint64_t)(32 * jb + HR * hh + v) * rb
+                                : ub + (uint64_t)(32 * jb + HR * hh + v - HR) * rb;
     };
     auto chunk = [&](int grp, int k) -> const uint8_t * {
         uint32_t r, it;
@@ -952,11 +968,44 @@ __device__ __forceinline__ void gu_unit(const MoeArgs &a, uint32_t unit, uint8_t
     }
     __syncthreads();
 
+    // (before wave 0 may leave: the first of a half-unit pair writes no block)
+    if (a.dbg_gu && tid < 2 * (uint32_t)HR) {
+        const bool upr = tid >= (uint32_t)HR;
+        float *d = a.dbg_gu + (uint64_t)slot * 2 * a.ffn + (upr ? a.ffn : 0) + 32 * jb + HR * hh + tid % HR;
+        *d = gu[tid];
+    }
     if (wave == 0) {
         // one h value per lane (lanes 32..63 mirror 0..31), then the q8_1
         // block across 32 lanes: same rules as quant_q8_1_part
         const uint32_t j = lane & 31;
-        const float h = kq_silu_mul(gu[j], gu[32 + j]);
+        float h;
+        if constexpr (HALF) {
+            // this half's 16 values (lane & 15), out as tagged words; the
+            // second of the pair to count itself in reads the other 16
+            const float own = kq_silu_mul(gu[lane & 15], gu[16 + (lane & 15)]);
+            uint32_t old = 0;
+            if (lane == 0)
+                old = __hip_atomic_fetch_add(a.fsync + FSYNC_DHC + ub_, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            old = __builtin_amdgcn_readfirstlane(old);
+            const uint32_t tag = (old >> 1) + 1;
+            uint32_t *words = a.fsync + FSYNC_DHW + 2 * 32 * ub_;
+            if (lane < 16) st_dev2(words + 2 * (16 * hh + lane), ((uint64_t)tag << 32) | __float_as_uint(own));
+            if ((old & 1) == 0) return;   // the first of the pair: the other writes the block (whole wave)
+            const bool mine = (j >> 4) == hh;
+            uint64_t v = 0;
+            uint32_t spins = 0;
+            for (;;) {
+                v = ld_dev2(words + 2 * j);
+                if (__all(mine || (uint32_t)(v >> 32) == tag)) break;
+                if (++spins >= FSYNC_SPIN_LIMIT) {
+                    if (lane == 0) atomicOr(a.err, 4);
+                    break;
+                }
+            }
+            h = mine ? own : __uint_as_float((uint32_t)v);
+        } else {
+            h = kq_silu_mul(gu[j], gu[32 + j]);
+        }
         const float am = max32(fabsf(h));
         const float d = am / 127.0f;
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
@@ -979,10 +1028,6 @@ __device__ __forceinline__ void gu_unit(const MoeArgs &a, uint32_t unit, uint8_t
                 st_dev2(hx + 2 * (9 * unit + lane), ((uint64_t)(g + 1) << 32) | ((const uint32_t *)stage)[lane]);
         }
     }
-    if (a.dbg_gu && tid < 64) {
-        float *d = a.dbg_gu + (uint64_t)slot * 2 * a.ffn + (tid < 32 ? 0 : a.ffn) + 32 * jb + (tid & 31);
-        *d = gu[tid];
-    }
     if constexpr (FUSED) {
         // h is out: now the fused layer's down-tile loads (a barrier that
         // orders LDS alone, so nobody waits for h's stores to be acknowledged)
@@ -993,11 +1038,11 @@ __device__ __forceinline__ void gu_unit(const MoeArgs &a, uint32_t unit, uint8_t
     }
 }
 
-template <int NB, int C, bool NORMED = false>
+template <int NB, int C, bool NORMED = false, bool HALF = false>
 __global__ void __launch_bounds__(a1_threads<NB>()) k_moe_gu(MoeArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
     GuRoute rt;
-    gu_unit<NB, C, false, NoMore, NORMED>(a, blockIdx.x, lds, rt, 0);
+    gu_unit<NB, C, false, NoMore, NORMED, HALF>(a, blockIdx.x, lds, rt, 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -2380,12 +2425,27 @@ hipError_t launch_moe_stack(const MoeArgs &a, const StackLayer *lt, uint32_t n_l
 
 uint64_t moe_route_words() { return 2 * MAX_SLOTS; }
 
+// KATALI_HIP_HALF_UNITS=0: kernel A keeps whole units on a dense FFN
+static bool env_half_off() {
+    const char *e = getenv("KATALI_HIP_HALF_UNITS");
+    return e && (e[0] == '0' || e[0] == 'n' || e[0] == 'N');
+}
+
 template <int NB, bool NORMED = false>
 static hipError_t go_a(const MoeArgs &a, uint32_t n_slots, hipStream_t s) {
     const LdsA L = lds_a(a.hidden, NB);
-    const dim3 grid(n_slots * (a.ffn / 32));
+    const uint32_t units = n_slots * (a.ffn / 32);
+    const dim3 grid(units);
     uint32_t lds = L.total;
     if (NORMED && L.scl + normed_area_bytes(a.hidden) > lds) lds = L.scl + normed_area_bytes(a.hidden);
+    if constexpr (!NORMED && NB >= 8) {   // hidden 2048 and 4096
+        if (a.n_sel == 0 && a.fsync && half_units(units, (uint32_t)device_cu_count()) &&
+            units <= DH_MAX_BLOCKS && !env_half_off()) {
+            hipLaunchKernelGGL((k_moe_gu<NB, 2, false, true>), dim3(2 * units), dim3(a1_threads<NB>()),
+                               lds_a(a.hidden, NB, 32).total, s, a);
+            return hipGetLastError();
+        }
+    }
     if (a.n_expert <= 128)
         hipLaunchKernelGGL((k_moe_gu<NB, 2, NORMED>), grid, dim3(a1_threads<NB>()), lds, s, a);
     else if (a.n_expert <= 256)

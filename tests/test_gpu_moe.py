@@ -506,6 +506,47 @@ def test_dense_ffn_shared_expert_only(hip, oracle, case):
     assert rf < 3e-2
 
 
+def test_dense_ffn_half_units_match_whole_units(hip, monkeypatch):
+    """At 4096 -> 12288 (384 q8_1 blocks of h on 256 CUs) kernel A runs half
+    units: two workgroups per block, the second to arrive writing it. Its
+    gate/up values, h blocks and y must be the bits of whole units
+    (KATALI_HIP_HALF_UNITS=0), in eager calls and in graph replays (the
+    blocks' counters are never reset, only raised by 2 per call)."""
+    hidden, ffn = 4096, 12288
+    rng = np.random.default_rng(4096)
+    g, u = S.matrix(rng, Q4_K, ffn, hidden), S.matrix(rng, Q4_K, ffn, hidden)
+    d = S.matrix(rng, Q6_K, hidden, ffn)
+    dev = tuple(hip.to_device(a) for a in (g, u, d))
+    desc = hip.moe_desc(hidden, ffn, 0, None, None, None, shared=dev)
+    x = hip.to_device(S.activation(rng, hidden))
+    out = {}
+    for mode in ("whole", "half"):
+        if mode == "whole":
+            monkeypatch.setenv("KATALI_HIP_HALF_UNITS", "0")
+        else:
+            monkeypatch.delenv("KATALI_HIP_HALF_UNITS", raising=False)
+        y, gu, hq = hip.alloc(hidden * 4), hip.alloc(2 * ffn * 4), hip.alloc(ffn // 32 * 36)
+        for _ in range(2):
+            hip.moe_layer_debug(desc, hip.moe_route(0), y, gu, hq, x=x)
+        hip.sync()
+        out[mode] = (y.download(np.uint32), gu.download(np.uint32), hq.download(np.uint8))
+    for a, b, what in zip(out["whole"], out["half"], ("y", "gate/up", "h blocks")):
+        assert np.array_equal(a, b), what
+    y = hip.alloc(hidden * 4)
+    hip.graph_begin()
+    hip.moe_layer(desc, hip.moe_route(0), y, x=x)
+    gr = hip.graph_end()
+    try:
+        for rep in range(4):
+            hip.memset(y, 0, hidden * 4)
+            hip.graph_launch(gr)
+            hip.moe_layer(desc, hip.moe_route(0), y, x=x)   # eager work between replays
+            hip.sync()
+            assert np.array_equal(y.download(np.uint32), out["half"][0]), rep
+    finally:
+        hip.graph_destroy(gr)
+
+
 def test_moe_rejects_bad_arguments(hip, moes):
     m = moes(512, 256, 16, False, Q4_K)
     y, x = hip.alloc(512 * 4), hip.alloc(512 * 4)
