@@ -1,6 +1,6 @@
 """Benchmark of the quantized expert-GEMV path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload moe48|moe40cold|gemv6144|qwen8b|moebatch]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload moe48|moe40cold|gemv6144|qwen8b|moebatch|tier48|...]
 
 Workloads:
   moe48     (default) one decode token through 48 fused MoE layers,
@@ -35,6 +35,14 @@ replay, and consecutive steps replay consecutive positions.
             int8 MFMA grouped GEMM, the rest on the GEMV kernels; 16 layers
             of distinct weights per pass; the JSON value is the n_sel = 8,
             64-token point, the whole sweep is in "sweep".
+  tier48    48 host-routed layers of the moe48 expert shape whose experts
+            come through the expert VRAM tier (64 slots) from a GGUF file
+            written on the box, m in {0, 1, 2, 4} misses per layer call,
+            synchronous vs pipelined uploads (pinned ring + copy stream), in
+            the engine flow (y downloaded per layer) and the queued flow (one
+            wait per token); the JSON value is tok/s at one miss per layer,
+            pipelined, engine flow; roofline: the upload rate against PCIe 5.0
+            x16.
 
 Printed: ONE JSON line. value = algorithmic HBM GB/s of the whole token
 (selected expert weights + q8_1 activation + fp32 output, per layer) with
@@ -481,6 +489,172 @@ def bench_duty(hip, name, steps, warmup, intervals=DUTY_INTERVALS_US):
         "back_to_back_unit_ms": base["gpu_us_per_layer"] / 1e3,
     }
     return res, (L, hidden, ffn, n_expert, n_sel, shared)
+
+
+# ---------------------------------------------------------------------------
+# Expert VRAM tier: host-routed layers whose experts come from a GGUF file
+# ---------------------------------------------------------------------------
+TIER_SHAPE = (2048, 768, 128, 8)   # hidden, ffn, experts, top-k: the moe48 expert shape
+TIER_MISSES = (0, 1, 2, 4)         # misses per layer call (of 8 experts)
+PCIE5_X16_GBS = 64.0               # published PCIe 5.0 x16 rate per direction
+
+
+def host_blocks(rng, t, nblocks):
+    """Random Q4_K / Q6_K blocks on the host with d (and dmin) ~ |N(0, 0.02)|."""
+    bb = 144 if t == Q4_K else 210
+    b = rng.integers(0, 256, (nblocks, bb), dtype=np.uint8)
+    d = np.abs(rng.standard_normal((nblocks, 2)) * 0.02).astype(np.float16).view(np.uint8).reshape(nblocks, 4)
+    if t == Q4_K:
+        b[:, 0:4] = d
+    else:
+        b[:, 208:210] = d[:, 0:2]
+    return b
+
+
+def tier_file(path, file_layers, seed=900):
+    import gguf_writer as W
+    hidden, ffn, E, k = TIER_SHAPE
+    rng = np.random.default_rng(seed)
+    w = W.GgufWriter(alignment=32)
+    w.kv("general.architecture", W.STR, "qwen3moe").kv("qwen3moe.block_count", W.U32, file_layers)
+    w.kv("qwen3moe.embedding_length", W.U32, hidden).kv("qwen3moe.expert_count", W.U32, E)
+    w.kv("qwen3moe.expert_used_count", W.U32, k)
+    for li in range(file_layers):
+        w.tensor(f"blk.{li}.ffn_gate_exps.weight", [hidden, ffn, E], Q4_K, host_blocks(rng, Q4_K, E * ffn * hidden // 256))
+        w.tensor(f"blk.{li}.ffn_up_exps.weight", [hidden, ffn, E], Q4_K, host_blocks(rng, Q4_K, E * ffn * hidden // 256))
+        w.tensor(f"blk.{li}.ffn_down_exps.weight", [ffn, hidden, E], Q6_K, host_blocks(rng, Q6_K, E * hidden * ffn // 256))
+    w.write(path)
+
+
+def tier_calls(m, layers, file_layers, n_calls, seed=901):
+    """n_calls layer calls of top-8 experts with exactly m misses each once
+    warm: per file layer a fixed hot set of 8 - m experts (asked for at every
+    call of that layer, so never the least recently used) and m experts from
+    a rotation over the other 120, which come back only after every other
+    cold expert of the layer has been asked for (long after the slots
+    evicted them)."""
+    hidden, ffn, E, k = TIER_SHAPE
+    rng = np.random.default_rng(seed)
+    perm = [rng.permutation(E) for _ in range(file_layers)]
+    hot = [p[:k - m].tolist() for p in perm]
+    cold = [p[k - m:].tolist() for p in perm]
+    ptr = [0] * file_layers
+    calls = []
+    for c in range(n_calls):
+        fl = (c % layers) % file_layers
+        ids = hot[fl] + [cold[fl][(ptr[fl] + j) % len(cold[fl])] for j in range(m)]
+        ptr[fl] += m
+        calls.append((fl, ids))
+    return calls
+
+
+def tier_slots(n_slots, calls):
+    """The tier's slot numbers for each call (its rule: the least recently
+    used slot not asked for in the same call, the lowest among equals)."""
+    slots = [(-1, 0)] * n_slots
+    out = []
+    for tick, (layer, ids) in enumerate(calls, 1):
+        got = []
+        for e in ids:
+            key = layer * 65536 + e
+            s = next((i for i, (kk, _) in enumerate(slots) if kk == key), None)
+            if s is None:
+                s = min((i for i, (_, u) in enumerate(slots) if u != tick), key=lambda i: (slots[i][1], i))
+            slots[s] = (key, tick)
+            got.append(s)
+        out.append(got)
+    return out
+
+
+class _View:
+    """A device address inside a buffer the caller keeps alive."""
+
+    def __init__(self, ptr):
+        self.ptr = ptr
+
+
+def bench_tier(hip, steps, warmup, misses=TIER_MISSES, layers=48, file_layers=2, n_slots=64):
+    """Decode tokens of `layers` host-routed MoE layers (the moe48 expert
+    shape) whose experts come through the expert VRAM tier (n_slots slots)
+    from a GGUF file of file_layers layers (layer l uses file layer
+    l % file_layers), at m misses per layer call. Per m, uploads synchronous
+    (each miss copied from the mapped file and waited for) or pipelined
+    (pinned ring + copy stream), in two submission flows:
+      engine: per layer the tier call, the slot ids uploaded, the layer, and
+              y downloaded (the host router of the next layer needs it);
+      queued: the expert ids of the whole token known up front (slot ids
+              uploaded once per token from the tier's rule), no wait between
+              layers, one per token: uploads overlap the kernels queued
+              before them.
+    tok/s per (m, mode, flow) and the upload rate of the pipelined queued flow."""
+    import tempfile
+
+    from katali_hip_gguf import ExpertTier, Gguf
+    hidden, ffn, E, k = TIER_SHAPE
+    path = os.path.join(tempfile.gettempdir(), f"katali_tier_{os.getpid()}.gguf")
+    print(f"[bench] tier: writing {file_layers} layers of {E} experts to {path}", file=sys.stderr, flush=True)
+    tier_file(path, file_layers)
+    g = Gguf(path)
+    x = hip.alloc(hidden * 4)
+    hip.synth_normal(x, hidden, 77)
+    y = hip.alloc(hidden * 4)
+    wts = hip.to_device(np.full(k, 1.0 / k, np.float32))
+    sbuf, ebuf = hip.alloc(layers * k * 4), hip.alloc(k * 4)
+    per_expert = None
+    points = []
+    try:
+        for m in misses:
+            n_calls = (warmup + steps) * layers
+            calls = tier_calls(m, layers, file_layers, n_calls)
+            for mode in ("sync", "pipelined"):
+                for flow in ("engine", "queued"):
+                    tier = ExpertTier(g, 0, budget=0, max_slots=n_slots)
+                    if mode == "pipelined":
+                        tier.pipeline()
+                    # warm the hot sets (and the file's pages) outside the timing
+                    for c in calls[:file_layers]:
+                        tier.layer(*c)
+                    hip.sync()
+                    pred = tier_slots(n_slots, calls[:file_layers] + calls)[file_layers:]
+                    walls = []
+                    st0 = None
+                    for tok in range(warmup + steps):
+                        if tok == warmup:
+                            st0 = tier.stats()
+                        t0 = time.perf_counter()
+                        batch = calls[tok * layers:(tok + 1) * layers]
+                        if flow == "queued":
+                            sbuf.upload(np.array(pred[tok * layers:(tok + 1) * layers], np.int32).ravel())
+                        for li, c in enumerate(batch):
+                            m_tier, slots = tier.layer(*c)
+                            if flow == "queued":
+                                assert slots == pred[tok * layers + li], "tier slots differ from its rule"
+                                ids = _View(sbuf.ptr + li * k * 4)
+                            else:
+                                ids = ebuf.upload(np.array(slots, np.int32))
+                            hip.moe_layer(m_tier, hip.moe_route(k, ids=ids, weights=wts), y, x=x)
+                            if flow == "engine":
+                                y.download(np.float32, hidden)
+                        hip.sync()
+                        if tok >= warmup:
+                            walls.append(time.perf_counter() - t0)
+                    st = tier.stats()
+                    per_expert = st["uploaded_bytes"] // max(st["misses"], 1) if st["misses"] else per_expert
+                    tier.destroy()
+                    wall = float(np.mean(walls))
+                    up = (st["uploaded_bytes"] - st0["uploaded_bytes"]) / steps
+                    pt = {"misses_per_layer": m, "mode": mode, "flow": flow, "tok_s": round(1.0 / wall, 2),
+                          "ms_per_token": round(wall * 1e3, 3), "upload_mb_per_token": round(up / 1e6, 2),
+                          "upload_gbs": round(up / wall / 1e9, 2),
+                          "misses_measured": (st["misses"] - st0["misses"]) / (steps * layers)}
+                    points.append(pt)
+                    print(f"[bench] tier m={m} {mode:9s} {flow:6s}: {pt['tok_s']:8.2f} tok/s, "
+                          f"{pt['upload_mb_per_token']:.1f} MB/token uploaded at {pt['upload_gbs']:.2f} GB/s",
+                          file=sys.stderr, flush=True)
+    finally:
+        g.close()
+        os.unlink(path)
+    return points, per_expert, (layers, file_layers, n_slots)
 
 
 # ---------------------------------------------------------------------------
@@ -1048,7 +1222,7 @@ def main():
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", default="moe48",
-                    choices=sorted(MOE_WORKLOADS) + sorted(TOKEN_WORKLOADS) + sorted(GEMV_WORKLOADS) + sorted(DENSE_WORKLOADS) + ["moebatch", "moe48duty", "floor48"])
+                    choices=sorted(MOE_WORKLOADS) + sorted(TOKEN_WORKLOADS) + sorted(GEMV_WORKLOADS) + sorted(DENSE_WORKLOADS) + ["moebatch", "moe48duty", "floor48", "tier48"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--normed-layer", action="store_true",
                     help="moe48tok: katali_hip_moe_layer_normed (norm, router and layer in two launches per layer) "
@@ -1102,6 +1276,40 @@ def main():
         a.free()
         b.free()
         print(f"[bench] calibration copy: {n} bytes read + {n} bytes written", file=sys.stderr, flush=True)
+
+    if args.workload == "tier48":
+        points, per_expert, (L, file_layers, n_slots) = bench_tier(hip, args.steps, args.warmup)
+        hidden, ffn, E, k = TIER_SHAPE
+        head = next(p for p in points if p["misses_per_layer"] == 1 and p["mode"] == "pipelined"
+                    and p["flow"] == "engine")
+        top = max((p for p in points if p["mode"] == "pipelined" and p["flow"] == "queued"),
+                  key=lambda p: p["misses_per_layer"])
+        line = {
+            "metric": "expert-tier decode tok/s at 1 miss per layer (pipelined uploads, host-routed engine flow)",
+            "value": head["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": head["ms_per_token"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "q4_k/q6_k weights x q8_1 activations (int8 dot4, fp32 scales)",
+            "data": "synthetic (random Q4_K/Q6_K blocks in a GGUF file written on the box)",
+            "config": {
+                "workload": f"tier48: {L} host-routed MoE layers (hidden {hidden}, {E} experts, top-{k}, gate/up "
+                            f"{hidden}->{ffn} Q4_K, down Q6_K) whose experts come through the expert VRAM tier "
+                            f"({n_slots} slots) from a {file_layers}-layer GGUF file; m of the 8 experts of every "
+                            f"layer call miss (m in {list(TIER_MISSES)}); synchronous vs pipelined uploads; engine "
+                            f"flow (y downloaded per layer) and queued flow (one wait per token)",
+                "layers": L, "n_slots": n_slots, "expert_bytes": per_expert, "parallelism": "single GPU",
+            },
+            "tier_points": points,
+            "roofline": {
+                "bound": "pcie", "achieved": top["upload_gbs"], "peak": PCIE5_X16_GBS, "unit": "GB/s",
+                "frac": round(top["upload_gbs"] / PCIE5_X16_GBS, 4), "traffic": None,
+                "kernel": f"host-to-device expert uploads, pipelined queued flow at {top['misses_per_layer']} "
+                          f"misses per layer",
+                "bytes_per_unit": per_expert, "unit_ms": None,
+            },
+            "cpu_baseline": None,
+        }
+        print(json.dumps(line), flush=True)
+        return
 
     traffic = read_traffic(args.workload)
     if args.workload in MOE_WORKLOADS:

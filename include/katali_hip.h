@@ -410,6 +410,34 @@ int katali_hip_event_record(void *event);
 int katali_hip_event_elapsed(void *start, void *end, float *ms);
 int katali_hip_event_destroy(void *event);
 
+/* ---- pipelined uploads (the expert tier's miss path) ------------------------
+ * The closed backend's upload batching and VRAM pool switches
+ * (KATALI_UPLOAD_BATCH, KATALI_VRAM_POOL, README.md:260,329-330, whose
+ * implementation is not in the reference) are replaced by a stager: a pinned
+ * host ring of n_chunks chunks of chunk_bytes and a copy stream of its own.
+ * katali_hip_stager_upload copies host bytes into the ring a chunk at a time
+ * (the CPU copy of one chunk overlaps the DMA of the one before; a chunk is
+ * reused once its DMA is done) and queues the DMAs on the copy stream; it
+ * returns once the host bytes are copied out (the source may change), not
+ * when they have arrived. katali_hip_stager_mark records a point in the
+ * library stream's work (every kernel queued so far) and returns its number
+ * (1, 2, ...); an upload naming mark m (0: none) starts its DMAs only after
+ * the library stream has reached m, so it may overwrite memory that work
+ * before m reads, and overlaps everything queued after m.
+ * katali_hip_stager_fence makes the library stream wait for every DMA
+ * queued so far (no host wait): kernels queued after it see the bytes.
+ * The CPU copy of a chunk is split over the calling thread and
+ * KATALI_HIP_STAGER_THREADS - 1 worker threads (default 4 in all; pieces of
+ * at least 256 KiB). chunk_bytes 4 KiB .. 1 GiB, n_chunks 2 .. 64. One
+ * calling thread per stager;
+ * every call fails with KATALI_HIP_E_INVALID during a graph capture. No
+ * counterpart in the reference's own sources. */
+int katali_hip_stager_create(uint64_t chunk_bytes, uint32_t n_chunks, void **stager);
+int katali_hip_stager_destroy(void *stager);
+int katali_hip_stager_mark(void *stager, uint64_t *mark);
+int katali_hip_stager_upload(void *stager, void *dev, const void *host, uint64_t bytes, uint64_t after_mark);
+int katali_hip_stager_fence(void *stager);
+
 /* ---- measurement ------------------------------------------------------------- */
 /* The phase stamps of the one-launch layers: [64][256][16] uint64
  * s_memrealtime ticks (100 MHz), layer slot tag % 64, workgroup, phase (the

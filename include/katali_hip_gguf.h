@@ -94,7 +94,19 @@ int katali_hip_gguf_moe_layer(KataliHipWeights *w, uint32_t layer, KataliHipMoe 
  * call all stay resident (n_sel <= n_slots). budget_bytes: as above (0:
  * KATALI_VRAM_GB, unset = room for max_slots); the slot count is the budget
  * divided by one expert's gate + up + down bytes, at most max_slots (<= 512).
- * Slots hold one expert shape; layers of another shape are refused. */
+ * Slots hold one expert shape; layers of another shape are refused. A
+ * call's slots are valid for work queued on the library stream before the
+ * next call (which may refill any slot that call does not ask for).
+ *
+ * katali_hip_tier_pipeline turns on pipelined uploads (also at create when
+ * KATALI_UPLOAD_BATCH=1): a miss's bytes go through a stager (pinned ring of
+ * n_chunks x chunk_bytes, 0 = 4 x 4 MiB, and a copy stream; katali_hip.h),
+ * the call returns once the bytes are copied out of the file, and the work
+ * queued after it waits for the DMAs on the device, not on the host. An
+ * upload into a slot waits only for the work that can read the slot's old
+ * expert (queued before the call after that expert's last call), so it
+ * overlaps every later kernel. Synchronous otherwise: each miss is copied
+ * and waited for before the call returns. */
 typedef struct KataliHipExpertTier KataliHipExpertTier;
 typedef struct KataliHipTierStats {
     uint64_t hits, misses, uploaded_bytes;
@@ -106,6 +118,7 @@ void katali_hip_tier_destroy(KataliHipExpertTier *t);
 int katali_hip_tier_layer(KataliHipExpertTier *t, uint32_t layer, const int32_t *expert_ids, int n_sel,
                           int32_t *slot_ids_out, KataliHipMoe *moe);
 void katali_hip_tier_stats(const KataliHipExpertTier *t, KataliHipTierStats *out);
+int katali_hip_tier_pipeline(KataliHipExpertTier *t, uint64_t chunk_bytes, uint32_t n_chunks);
 
 #ifdef __cplusplus
 }

@@ -78,6 +78,13 @@ int katali_gpu_moe_route_batch(const float *logits_dev, uint32_t n_tokens, uint3
 /* The MoE layer over a batch of up to 64 tokens (batched prefill). */
 int katali_gpu_moe_batch(const KataliHipMoe *moe, const KataliHipMoeBatch *batch, const float *x_dev,
                          float *y_dev);
+/* Pipelined uploads through a pinned ring and a copy stream (the expert
+ * tier's miss path; katali_hip_stager_* in katali_hip.h). */
+int katali_gpu_stager_create(uint64_t chunk_bytes, uint32_t n_chunks, void **stager);
+int katali_gpu_stager_destroy(void *stager);
+int katali_gpu_stager_mark(void *stager, uint64_t *mark);
+int katali_gpu_stager_upload(void *stager, void *dev, const void *host, uint64_t bytes, uint64_t after_mark);
+int katali_gpu_stager_fence(void *stager);
 /* The library's last error for this thread ("" when none / not loaded). */
 const char *katali_gpu_last_error(void);
 
@@ -127,6 +134,11 @@ typedef struct KataliHipApi {
     int (*rmsnorm_matvec_f32)(const float *, const float *, float, float *, const float *, uint64_t, float, float *,
                               const float *, uint64_t, float *);
     int (*moe_route_batch)(const float *, uint32_t, uint32_t, int32_t, int32_t *, float *);
+    int (*stager_create)(uint64_t, uint32_t, void **);
+    int (*stager_destroy)(void *);
+    int (*stager_mark)(void *, uint64_t *);
+    int (*stager_upload)(void *, void *, const void *, uint64_t, uint64_t);
+    int (*stager_fence)(void *);
 } KataliHipApi;
 
 /* NULL when the library could not be loaded or an entry point is missing. */

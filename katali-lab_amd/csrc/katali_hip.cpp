@@ -13,8 +13,12 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
+#include <condition_variable>
 #include <mutex>
+#include <new>
 #include <string>
+#include <thread>
 #include <unordered_map>
 #include <vector>
 
@@ -1135,6 +1139,210 @@ int katali_hip_event_elapsed(void *a, void *b, float *ms) {
 int katali_hip_event_destroy(void *ev) {
     if (!ev) return KATALI_HIP_OK;
     return launched(hipEventDestroy((hipEvent_t)ev), "hipEventDestroy");
+}
+
+// ---- pipelined uploads ------------------------------------------------------
+// A pinned host ring of n_chunks chunks and a copy stream of its own
+// (default priority). An upload copies the host bytes into the ring a chunk
+// at a time (the CPU copy of chunk i + 1 overlaps the DMA of chunk i; a
+// chunk is reused once its last DMA is done) and queues each chunk's DMA on
+// the copy stream. Marks are events recorded on the library stream; an
+// upload that names a mark queues its DMAs behind it (the copy stream waits
+// for the library stream's work up to that mark), and a fence makes the
+// library stream wait for every DMA queued so far.
+// The CPU copy into a chunk is split over the calling thread and
+// KATALI_HIP_STAGER_THREADS - 1 workers (default 4 threads in all; one CPU
+// thread copies from a mapped file well below the link's rate).
+constexpr uint32_t STAGER_MARKS = 64;
+constexpr uint64_t STAGER_MIN_PIECE = 256u << 10;   // smaller copies stay on the calling thread
+struct Stager {
+    hipStream_t cs = nullptr;
+    uint8_t *ring = nullptr;
+    uint64_t chunk = 0;
+    uint32_t n_chunks = 0, next = 0;
+    std::vector<hipEvent_t> done;   // per chunk: its last DMA has finished
+    std::vector<char> busy;         // per chunk: a DMA was queued from it
+    hipEvent_t marks[STAGER_MARKS] = {};
+    uint64_t n_marks = 0;           // mark m (1-based) is marks[(m - 1) % STAGER_MARKS]
+    uint64_t waited = 0;            // the newest mark the copy stream already waits behind
+    hipEvent_t tail = nullptr;
+    // the copy workers: job `gen` copies len bytes src -> dst in `parts`
+    // pieces, piece 0 on the calling thread, piece i on worker i - 1
+    std::vector<std::thread> workers;
+    std::mutex mu;
+    std::condition_variable cv_job, cv_done;
+    uint64_t gen = 0;
+    uint32_t parts = 1, pending = 0;
+    bool quit = false;
+    uint8_t *dst = nullptr;
+    const uint8_t *src = nullptr;
+    uint64_t len = 0;
+};
+
+// piece i of n of a len-byte copy (64-byte aligned bounds)
+static void stager_piece(uint32_t i, uint32_t n, uint8_t *dst, const uint8_t *src, uint64_t len) {
+    const uint64_t step = ((len + n - 1) / n + 63) & ~63ull;
+    const uint64_t lo = std::min(len, step * i), hi = std::min(len, lo + step);
+    if (hi > lo) memcpy(dst + lo, src + lo, hi - lo);
+}
+
+static void stager_worker(Stager *s, uint32_t idx) {
+    uint64_t seen = 0;
+    for (;;) {
+        uint8_t *dst;
+        const uint8_t *src;
+        uint64_t len;
+        uint32_t parts;
+        {
+            std::unique_lock<std::mutex> lk(s->mu);
+            s->cv_job.wait(lk, [&] { return s->quit || s->gen != seen; });
+            if (s->quit) return;
+            seen = s->gen;
+            dst = s->dst, src = s->src, len = s->len, parts = s->parts;
+        }
+        if (idx + 1 < parts) stager_piece(idx + 1, parts, dst, src, len);
+        std::lock_guard<std::mutex> lk(s->mu);
+        if (--s->pending == 0) s->cv_done.notify_one();
+    }
+}
+
+// memcpy(dst, src, len) over the calling thread and the workers
+static void stager_copy(Stager *s, uint8_t *dst, const uint8_t *src, uint64_t len) {
+    const uint32_t nw = (uint32_t)s->workers.size();
+    const uint32_t parts = (uint32_t)std::min<uint64_t>(nw + 1, std::max<uint64_t>(1, len / STAGER_MIN_PIECE));
+    if (parts <= 1) {
+        memcpy(dst, src, len);
+        return;
+    }
+    {
+        std::lock_guard<std::mutex> lk(s->mu);
+        s->dst = dst, s->src = src, s->len = len, s->parts = parts;
+        s->pending = nw;   // every worker answers each job, with a piece or without
+        s->gen++;
+    }
+    s->cv_job.notify_all();
+    stager_piece(0, parts, dst, src, len);
+    std::unique_lock<std::mutex> lk(s->mu);
+    s->cv_done.wait(lk, [&] { return s->pending == 0; });
+}
+
+static void stager_release(Stager *s) {
+    if (!s) return;
+    {
+        std::lock_guard<std::mutex> lk(s->mu);
+        s->quit = true;
+    }
+    s->cv_job.notify_all();
+    for (std::thread &t : s->workers) t.join();
+    if (s->cs) (void)hipStreamSynchronize(s->cs);
+    for (hipEvent_t e : s->done)
+        if (e) (void)hipEventDestroy(e);
+    for (hipEvent_t e : s->marks)
+        if (e) (void)hipEventDestroy(e);
+    if (s->tail) (void)hipEventDestroy(s->tail);
+    if (s->ring) (void)hipHostFree(s->ring);
+    if (s->cs) (void)hipStreamDestroy(s->cs);
+    delete s;
+}
+
+int katali_hip_stager_create(uint64_t chunk_bytes, uint32_t n_chunks, void **out) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!out) return fail(KATALI_HIP_E_INVALID, "null out pointer");
+    *out = nullptr;
+    if (g_capturing) return fail(KATALI_HIP_E_INVALID, "katali_hip_stager_create during graph capture");
+    if (chunk_bytes < 4096 || chunk_bytes > (1ull << 30) || n_chunks < 2 || n_chunks > 64)
+        return fail(KATALI_HIP_E_INVALID, "stager: chunk %llu bytes (4 KiB .. 1 GiB), %u chunks (2 .. 64)",
+                    (unsigned long long)chunk_bytes, n_chunks);
+    Stager *s = new (std::nothrow) Stager;
+    if (!s) return fail(KATALI_HIP_E_NOMEM, "stager: out of memory");
+    s->chunk = chunk_bytes;
+    s->n_chunks = n_chunks;
+    s->done.assign(n_chunks, nullptr);
+    s->busy.assign(n_chunks, 0);
+    hipError_t e = hipStreamCreateWithFlags(&s->cs, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipHostMalloc((void **)&s->ring, chunk_bytes * n_chunks, hipHostMallocDefault);
+    for (uint32_t i = 0; i < n_chunks && e == hipSuccess; i++)
+        e = hipEventCreateWithFlags(&s->done[i], hipEventDisableTiming);
+    for (uint32_t i = 0; i < STAGER_MARKS && e == hipSuccess; i++)
+        e = hipEventCreateWithFlags(&s->marks[i], hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&s->tail, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        stager_release(s);
+        return hip_fail(e, "stager create");
+    }
+    const char *nt = getenv("KATALI_HIP_STAGER_THREADS");
+    const long threads = nt && *nt ? std::max(1L, std::min(16L, strtol(nt, nullptr, 10))) : 4;
+    try {
+        for (long i = 0; i + 1 < threads; i++) s->workers.emplace_back(stager_worker, s, (uint32_t)i);
+    } catch (...) {
+        stager_release(s);
+        return fail(KATALI_HIP_E_NOMEM, "stager: cannot start copy threads");
+    }
+    *out = s;
+    return KATALI_HIP_OK;
+}
+
+int katali_hip_stager_destroy(void *stager) {
+    if (!stager) return KATALI_HIP_OK;
+    if (g_capturing) return fail(KATALI_HIP_E_INVALID, "katali_hip_stager_destroy during graph capture");
+    stager_release((Stager *)stager);
+    return KATALI_HIP_OK;
+}
+
+int katali_hip_stager_mark(void *stager, uint64_t *mark) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!stager || !mark) return fail(KATALI_HIP_E_INVALID, "null argument");
+    if (g_capturing) return fail(KATALI_HIP_E_INVALID, "katali_hip_stager_mark during graph capture");
+    Stager *s = (Stager *)stager;
+    const hipError_t e = hipEventRecord(s->marks[s->n_marks % STAGER_MARKS], g_stream);
+    if (e != hipSuccess) return hip_fail(e, "stager mark");
+    *mark = ++s->n_marks;
+    return KATALI_HIP_OK;
+}
+
+int katali_hip_stager_upload(void *stager, void *dev, const void *host, uint64_t bytes, uint64_t after_mark) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!stager || (bytes && (!dev || !host))) return fail(KATALI_HIP_E_INVALID, "null argument");
+    if (g_capturing) return fail(KATALI_HIP_E_INVALID, "katali_hip_stager_upload during graph capture");
+    Stager *s = (Stager *)stager;
+    if (after_mark > s->n_marks)
+        return fail(KATALI_HIP_E_INVALID, "stager: mark %llu not taken yet", (unsigned long long)after_mark);
+    hipError_t e = hipSuccess;
+    // a mark older than the event ring waits on the newer mark that reused
+    // its event: later than needed, never earlier
+    if (after_mark > s->waited) {
+        e = hipStreamWaitEvent(s->cs, s->marks[(after_mark - 1) % STAGER_MARKS], 0);
+        if (e != hipSuccess) return hip_fail(e, "stager wait");
+        s->waited = after_mark;
+    }
+    for (uint64_t off = 0; off < bytes;) {
+        const uint64_t len = std::min(s->chunk, bytes - off);
+        const uint32_t c = s->next;
+        s->next = (c + 1) % s->n_chunks;
+        if (s->busy[c] && (e = hipEventSynchronize(s->done[c])) != hipSuccess) return hip_fail(e, "stager chunk");
+        uint8_t *buf = s->ring + (uint64_t)c * s->chunk;
+        stager_copy(s, buf, (const uint8_t *)host + off, len);
+        e = hipMemcpyAsync((uint8_t *)dev + off, buf, len, hipMemcpyHostToDevice, s->cs);
+        if (e == hipSuccess) e = hipEventRecord(s->done[c], s->cs);
+        if (e != hipSuccess) return hip_fail(e, "stager DMA");
+        s->busy[c] = 1;
+        off += len;
+    }
+    return KATALI_HIP_OK;
+}
+
+int katali_hip_stager_fence(void *stager) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (!stager) return fail(KATALI_HIP_E_INVALID, "null argument");
+    if (g_capturing) return fail(KATALI_HIP_E_INVALID, "katali_hip_stager_fence during graph capture");
+    Stager *s = (Stager *)stager;
+    hipError_t e = hipEventRecord(s->tail, s->cs);
+    if (e == hipSuccess) e = hipStreamWaitEvent(g_stream, s->tail, 0);
+    return e == hipSuccess ? KATALI_HIP_OK : hip_fail(e, "stager fence");
 }
 
 int katali_hip_synth_fill(uint32_t type, void *dev, uint64_t nblocks, uint64_t seed, float d_sigma) {

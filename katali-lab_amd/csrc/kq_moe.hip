@@ -412,7 +412,7 @@ __device__ __forceinline__ uint32_t opaque_s(uint32_t v) {
 // 13 y poll started (stack), 14 y seen (stack), 15 logits seen (normed).
 // Wave 0 records every phase but 7 and 8, the first polling wave those.
 // In the product build the marks compile to nothing.
-constexpr uint32_t STAMP_LAYERS = 64, STAMP_PHASES = 16;
+[[maybe_unused]] constexpr uint32_t STAMP_LAYERS = 64, STAMP_PHASES = 16;
 #ifdef KQ_STAMPS
 __device__ uint64_t kq_stamps[STAMP_LAYERS * 256 * STAMP_PHASES];
 struct Stamps {

@@ -1,4 +1,5 @@
-"""A small GGUF writer for tests: the public container format (little-endian
+"""A small GGUF writer (synthetic model files for the tests and the expert-tier
+benchmark): the public container format (little-endian
 header "GGUF", version, tensor and metadata counts; key/value metadata;
 tensor infos; the data section at the file's alignment), plus hooks to write
 malformed files on purpose."""

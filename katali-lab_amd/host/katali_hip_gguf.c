@@ -533,6 +533,7 @@ int katali_hip_gguf_moe_layer(KataliHipWeights *w, uint32_t layer, KataliHipMoe 
 typedef struct TierSlot {
     int64_t key;         /* layer * 65536 + expert, -1 when empty */
     uint64_t used;       /* tick of the last call that asked for it */
+    uint64_t ready;      /* pipelined: the stager mark after which no queued work reads it (0: none) */
 } TierSlot;
 
 struct KataliHipExpertTier {
@@ -543,8 +544,16 @@ struct KataliHipExpertTier {
     uint32_t n_slots;
     TierSlot *slot;
     uint64_t tick;
+    void *stager;                   /* pipelined uploads, or NULL (synchronous) */
+    uint64_t mark_call;             /* pipelined: slots used at calls >= this have no ready mark yet */
     KataliHipTierStats st;
 };
+
+/* KATALI_UPLOAD_BATCH=1: tiers start pipelined with the default ring */
+static int upload_batch_from_env(void) {
+    const char *e = getenv("KATALI_UPLOAD_BATCH");
+    return e && e[0] == '1';
+}
 
 int katali_hip_tier_create(const KataliHipGguf *g, uint32_t layer, uint64_t budget, uint32_t max_slots,
                            KataliHipExpertTier **out) {
@@ -582,12 +591,52 @@ int katali_hip_tier_create(const KataliHipGguf *g, uint32_t layer, uint64_t budg
             return -1;
         }
     t->st.n_slots = t->n_slots;
+    if (upload_batch_from_env() && katali_hip_tier_pipeline(t, 0, 0)) {
+        katali_hip_tier_destroy(t);
+        return -1;
+    }
     *out = t;
+    return 0;
+}
+
+int katali_hip_tier_pipeline(KataliHipExpertTier *t, uint64_t chunk_bytes, uint32_t n_chunks) {
+    if (!t) return gguf_fail("tier: null argument");
+    if (t->stager) return 0;
+    if (!chunk_bytes) chunk_bytes = 4u << 20;
+    if (!n_chunks) n_chunks = 4;
+    if (katali_gpu_stager_create(chunk_bytes, n_chunks, &t->stager) != KATALI_GPU_OK) {
+        t->stager = NULL;
+        return gguf_fail("tier: stager: %s", katali_gpu_last_error());
+    }
+    /* everything queued so far may still read any slot: the first upload
+     * into each waits for this point */
+    uint64_t mark = 0;
+    if (katali_gpu_stager_mark(t->stager, &mark) != KATALI_GPU_OK) {
+        katali_gpu_stager_destroy(t->stager);
+        t->stager = NULL;
+        return gguf_fail("tier: stager mark: %s", katali_gpu_last_error());
+    }
+    for (uint32_t k = 0; k < t->n_slots; k++) t->slot[k].ready = mark;
+    t->mark_call = t->tick + 1;
+    return 0;
+}
+
+/* A mark covering the work queued so far, taken at a call's first miss:
+ * the slots used by the calls since the last mark (whose readers are all
+ * queued by now) get it as their ready mark. */
+static int tier_mark(KataliHipExpertTier *t, uint64_t tick) {
+    uint64_t mark = 0;
+    if (katali_gpu_stager_mark(t->stager, &mark) != KATALI_GPU_OK)
+        return gguf_fail("tier: stager mark: %s", katali_gpu_last_error());
+    for (uint32_t k = 0; k < t->n_slots; k++)
+        if (t->slot[k].used >= t->mark_call && t->slot[k].used < tick) t->slot[k].ready = mark;
+    t->mark_call = tick;
     return 0;
 }
 
 void katali_hip_tier_destroy(KataliHipExpertTier *t) {
     if (!t) return;
+    if (t->stager) katali_gpu_stager_destroy(t->stager);
     for (int k = 0; k < 3; k++)
         if (t->pool[k]) katali_gpu_free(t->pool[k]);
     free(t->slot);
@@ -605,10 +654,12 @@ int katali_hip_tier_layer(KataliHipExpertTier *t, uint32_t layer, const int32_t 
     if (m.hidden != t->shape.hidden || m.ffn != t->shape.ffn || m.gate_type != t->shape.gate_type ||
         m.down_type != t->shape.down_type)
         return gguf_fail("tier: layer %u's experts have another shape than the slots", layer);
-    const uint64_t tick = ++t->tick;
-    for (int i = 0; i < n_sel; i++) {
+    for (int i = 0; i < n_sel; i++)   /* before any slot changes */
         if (ids[i] < 0 || (uint32_t)ids[i] >= m.n_expert)
             return gguf_fail("tier: expert id %d outside 0..%u", ids[i], m.n_expert - 1);
+    const uint64_t tick = ++t->tick;
+    int uploads = 0;
+    for (int i = 0; i < n_sel; i++) {
         const int64_t key = (int64_t)layer * 65536 + ids[i];
         uint32_t s = t->n_slots;
         for (uint32_t k = 0; k < t->n_slots; k++)
@@ -620,12 +671,23 @@ int katali_hip_tier_layer(KataliHipExpertTier *t, uint32_t layer, const int32_t 
              * empty slot first: its tick is 0) */
             for (uint32_t k = 0; k < t->n_slots; k++)
                 if (t->slot[k].used != tick && (s == t->n_slots || t->slot[k].used < t->slot[s].used)) s = k;
-            for (int p = 0; p < 3; p++)
-                if (katali_gpu_upload(t->pool[p] + t->eb[p] * s, ts[p]->data + t->eb[p] * (uint64_t)ids[i],
-                                      (size_t)t->eb[p]) != KATALI_GPU_OK) {
+            if (t->stager && t->mark_call != tick && tier_mark(t, tick)) {
+                if (uploads) katali_gpu_stager_fence(t->stager);
+                return -1;
+            }
+            for (int p = 0; p < 3; p++) {
+                uint8_t *dst = t->pool[p] + t->eb[p] * s;
+                const uint8_t *src = ts[p]->data + t->eb[p] * (uint64_t)ids[i];
+                const int rc = t->stager ? katali_gpu_stager_upload(t->stager, dst, src, t->eb[p], t->slot[s].ready)
+                                         : katali_gpu_upload(dst, src, (size_t)t->eb[p]);
+                if (rc != KATALI_GPU_OK) {
                     t->slot[s].key = -1;
-                    return gguf_fail("tier: upload: %s", katali_gpu_last_error());
+                    gguf_fail("tier: upload: %s", katali_gpu_last_error());
+                    if (t->stager && uploads) katali_gpu_stager_fence(t->stager);   /* the slots filled before it */
+                    return -1;
                 }
+            }
+            uploads++;
             t->slot[s].key = key;
             t->st.misses++;
             t->st.uploaded_bytes += t->eb[0] + t->eb[1] + t->eb[2];
@@ -633,6 +695,9 @@ int katali_hip_tier_layer(KataliHipExpertTier *t, uint32_t layer, const int32_t 
         t->slot[s].used = tick;
         slots[i] = (int32_t)s;
     }
+    /* the work the caller queues next waits for this call's DMAs */
+    if (t->stager && uploads && katali_gpu_stager_fence(t->stager) != KATALI_GPU_OK)
+        return gguf_fail("tier: stager fence: %s", katali_gpu_last_error());
     m.n_expert = t->n_slots;
     m.gate_exps = t->pool[0];
     m.up_exps = t->pool[1];

@@ -113,6 +113,11 @@ static int load(void) {
     LOAD(add_rmsnorm, "katali_hip_add_rmsnorm");
     LOAD(rmsnorm_matvec_f32, "katali_hip_rmsnorm_matvec_f32");
     LOAD(moe_route_batch, "katali_hip_moe_route_batch");
+    LOAD(stager_create, "katali_hip_stager_create");
+    LOAD(stager_destroy, "katali_hip_stager_destroy");
+    LOAD(stager_mark, "katali_hip_stager_mark");
+    LOAD(stager_upload, "katali_hip_stager_upload");
+    LOAD(stager_fence, "katali_hip_stager_fence");
     if (g_api.abi_version() != KATALI_HIP_ABI_VERSION) {
         snprintf(g_status, sizeof g_status, "%s: ABI version %d, loader expects %d", tried, g_api.abi_version(),
                  KATALI_HIP_ABI_VERSION);
@@ -201,3 +206,12 @@ int katali_gpu_rmsnorm_matvec_f32(const float *x, const float *delta, float scal
 int katali_gpu_moe_batch(const KataliHipMoe *moe, const KataliHipMoeBatch *batch, const float *x, float *y) {
     FORWARD(g_api.moe_batch(moe, batch, x, y));
 }
+int katali_gpu_stager_create(uint64_t chunk_bytes, uint32_t n_chunks, void **stager) {
+    FORWARD(g_api.stager_create(chunk_bytes, n_chunks, stager));
+}
+int katali_gpu_stager_destroy(void *stager) { FORWARD(g_api.stager_destroy(stager)); }
+int katali_gpu_stager_mark(void *stager, uint64_t *mark) { FORWARD(g_api.stager_mark(stager, mark)); }
+int katali_gpu_stager_upload(void *stager, void *dev, const void *host, uint64_t bytes, uint64_t after_mark) {
+    FORWARD(g_api.stager_upload(stager, dev, host, bytes, after_mark));
+}
+int katali_gpu_stager_fence(void *stager) { FORWARD(g_api.stager_fence(stager)); }

@@ -72,6 +72,11 @@ SIGNATURES = {
     "katali_hip_one_launch": (C.c_int, [_i32]),
     "katali_hip_phase_stamps": (C.c_int, [_vp, _sz]),
     "katali_hip_stream_floor": (C.c_int, [_i32, _vp, _sz, _vp, _sz, _vp]),
+    "katali_hip_stager_create": (C.c_int, [_u64, _u32, C.POINTER(_vp)]),
+    "katali_hip_stager_destroy": (C.c_int, [_vp]),
+    "katali_hip_stager_mark": (C.c_int, [_vp, C.POINTER(_u64)]),
+    "katali_hip_stager_upload": (C.c_int, [_vp, _vp, _vp, _u64, _u64]),
+    "katali_hip_stager_fence": (C.c_int, [_vp]),
 }
 
 

@@ -44,6 +44,7 @@ _SIG = {
     "katali_hip_tier_layer": (C.c_int, [_vp, _u32, C.POINTER(_i32), C.c_int, C.POINTER(_i32),
                                         C.POINTER(KataliHipMoe)]),
     "katali_hip_tier_stats": (None, [_vp, C.POINTER(TierStats)]),
+    "katali_hip_tier_pipeline": (C.c_int, [_vp, _u64, _u32]),
 }
 
 
@@ -159,6 +160,11 @@ class ExpertTier:
         if self.lib.katali_hip_tier_layer(self.h, layer, a, n, s, C.byref(m)) != 0:
             raise GgufError(self.lib.katali_hip_gguf_last_error().decode())
         return m, list(s)[:n]
+
+    def pipeline(self, chunk_bytes=0, n_chunks=0):
+        """Pipelined uploads from here on (a pinned ring and a copy stream)."""
+        if self.lib.katali_hip_tier_pipeline(self.h, chunk_bytes, n_chunks) != 0:
+            raise GgufError(self.lib.katali_hip_gguf_last_error().decode())
 
     def stats(self):
         st = TierStats()

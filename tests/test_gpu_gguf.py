@@ -110,10 +110,14 @@ def test_gguf_weight_budget_refuses(hip, model):
         g.close()
 
 
-def lru_model(n_slots, calls):
+def lru_model(n_slots, calls, picks=None):
+    """Hits and misses of the tier's rule (least recently used slot not asked
+    for in the same call, the lowest slot among equals); picks, when given,
+    gets each call's slot numbers."""
     slots = [(-1, 0)] * n_slots
     hits = misses = 0
     for tick, (layer, ids) in enumerate(calls, 1):
+        got = []
         for e in ids:
             key = layer * 65536 + e
             s = next((i for i, (kk, _) in enumerate(slots) if kk == key), None)
@@ -124,6 +128,9 @@ def lru_model(n_slots, calls):
                 cand = [i for i, (_, u) in enumerate(slots) if u != tick]
                 s = min(cand, key=lambda i: (slots[i][1], i))
             slots[s] = (key, tick)
+            got.append(s)
+        if picks is not None:
+            picks.append(got)
     return hits, misses
 
 
@@ -164,6 +171,66 @@ def test_expert_tier_matches_resident_layer(hip, oracle, model):
             tier.layer(0, list(range(7)))      # more experts than slots
         with pytest.raises(GgufError):
             tier.layer(0, [E])                 # id outside the layer
+    finally:
+        tier.destroy()
+        wts.destroy()
+        g.close()
+
+
+@pytest.mark.parametrize("chunk", [64 << 10, 4 << 20])
+def test_expert_tier_pipelined_matches_resident_layer(hip, oracle, model, chunk):
+    """Pipelined uploads with as many slots as experts per call, so every
+    call's misses refill slots the kernel queued just before still reads:
+    no host synchronisation between calls (ids, weights and slot numbers are
+    on the device beforehand, the slot numbers from the LRU model), each
+    upload must wait for that kernel on the device, and the layer after it
+    for the upload. Every call's output equals the resident layer's, bit for
+    bit. Some calls repeat the previous call's experts (all hits, no
+    uploads), so the next misses must also wait for the kernels of calls
+    that took no mark. 64 KiB chunks wrap the three-chunk ring inside one
+    expert (and are copied by the calling thread alone); 4 MiB chunks are
+    copied by the worker threads too."""
+    path, H = model
+    L, h, ffn, E, k = H["L"], H["hidden"], H["ffn"], H["E"], H["n_sel"]
+    g = Gguf(path)
+    wts = Weights(g)
+    per = ffn * (h // 256 * 144) * 2 + h * (ffn // 256 * 210)
+    tier = ExpertTier(g, 0, budget=k * per + per // 2, max_slots=64)
+    try:
+        assert tier.stats()["n_slots"] == k
+        tier.pipeline(chunk_bytes=chunk, n_chunks=3)
+        rng = np.random.default_rng(5)
+        calls, wsel = [], []
+        for t in range(6):
+            for li in range(L):
+                calls.append((li, rng.choice(E, k, replace=False).astype(np.int32).tolist()))
+                wsel.append(rng.dirichlet(np.ones(k)).astype(np.float32))
+                if t % 2 == 0:   # the same experts again: all hits, a call that takes no mark
+                    calls.append(calls[-1])
+                    wsel.append(rng.dirichlet(np.ones(k)).astype(np.float32))
+        picks = []
+        hits, misses = lru_model(k, calls, picks)
+        x = hip.to_device(S.activation(rng, h))
+        sdev = [hip.to_device(np.array(p, np.int32)) for p in picks]
+        wdev = [hip.to_device(w) for w in wsel]
+        ys = [hip.alloc(h * 4) for _ in calls]
+        hip.sync()
+        print(f"[tier pipelined] chunk {chunk}: {len(calls)} calls, {misses} misses, no sync between them", flush=True)
+        for i, (li, sel) in enumerate(calls):
+            m_tier, slots = tier.layer(li, sel)
+            assert slots == picks[i], i
+            hip.moe_layer(m_tier, hip.moe_route(k, ids=sdev[i], weights=wdev[i]), ys[i], x=x)
+        hip.sync()
+        st = tier.stats()
+        assert (st["hits"], st["misses"]) == (hits, misses)
+        y_res = hip.alloc(h * 4)
+        for i, (li, sel) in enumerate(calls):
+            m_res = wts.moe_layer(li)[0]
+            m_res.gate_shexp = m_res.up_shexp = m_res.down_shexp = None   # routed experts only
+            hip.moe_layer(m_res, hip.moe_route(k, ids=hip.to_device(np.array(sel, np.int32)), weights=wdev[i]),
+                          y_res, x=x)
+            hip.sync()
+            assert np.array_equal(y_res.download(np.uint32, h), ys[i].download(np.uint32, h)), (i, li, sel)
     finally:
         tier.destroy()
         wts.destroy()
