@@ -56,7 +56,7 @@ hipError_t launch_quantize_q8_1(const float *x, uint64_t n, uint8_t *out, hipStr
 // values: fp32 copied (MODE 0), q8_1 bytes copied (MODE 1), or fp32
 // quantized to q8_1 with 8 lanes per block (MODE 2).
 constexpr int XPRE = 4;
-template <int MODE>
+template <int MODE, uint32_t NT = 256>
 struct XStage {
     float4 v[XPRE];
     uint32_t q[XPRE], d[XPRE];
@@ -65,7 +65,7 @@ struct XStage {
         const uint32_t n = tasks(cols);
 #pragma unroll
         for (int i = 0; i < XPRE; i++) {
-            const uint32_t t = min(threadIdx.x + 256 * i, n - 1);   // clamped, not skipped
+            const uint32_t t = min(threadIdx.x + NT * i, n - 1);   // clamped, not skipped
             if constexpr (MODE == 1) {
                 const uint8_t *b = xq + (t >> 3) * 36;
                 q[i] = *(const uint32_t *)(b + 4 + 4 * (t & 7));
@@ -110,10 +110,10 @@ struct XStage {
         const uint32_t n = tasks(cols);
 #pragma unroll
         for (int i = 0; i < XPRE; i++) {
-            const uint32_t t = threadIdx.x + 256 * i;
+            const uint32_t t = threadIdx.x + NT * i;
             if (t < n) put(t, v[i], q[i], d[i], a, af);
         }
-        for (uint32_t t = threadIdx.x + 256 * XPRE; t < n; t += 256) {   // whole 8-lane groups (n % 8 == 0)
+        for (uint32_t t = threadIdx.x + NT * XPRE; t < n; t += NT) {   // whole 8-lane groups (n % 8 == 0)
             float4 x4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             uint32_t qq = 0, dd = 0;
             if constexpr (MODE == 1) {
@@ -127,7 +127,7 @@ struct XStage {
         }
         if constexpr (MODE == 0) {   // half-block sums of the fp32 activation
             __syncthreads();
-            for (uint32_t t = threadIdx.x; t < cols / 16; t += 256) {
+            for (uint32_t t = threadIdx.x; t < cols / 16; t += NT) {
                 float sum = 0.0f;
                 for (int i = 0; i < 16; i++) sum += af.x[16 * t + i];
                 af.xs16[t] = sum;
@@ -137,8 +137,9 @@ struct XStage {
 };
 
 // The row groups of one matrix that workgroup `block` of `nblocks` takes
-// (the workgroups' shares of the matrix interleave: a grid-stride loop).
-template <class QT, int IPL_T, int RPS, int MODE>
+// (the workgroups' shares of the matrix interleave: a grid-stride loop);
+// NW waves per workgroup.
+template <class QT, int IPL_T, int RPS, int MODE, int NW = 4>
 __device__ __forceinline__ void gemv_rows(const uint8_t *__restrict__ w, uint32_t rows, uint32_t cols, uint64_t rb,
                                           uint32_t log2s, const float *xf, const uint8_t *xq, float *__restrict__ y,
                                           uint32_t block, uint32_t nblocks, uint8_t *lds) {
@@ -150,9 +151,9 @@ __device__ __forceinline__ void gemv_rows(const uint8_t *__restrict__ w, uint32_
     const uint32_t slot = lane >> log2s, s = lane & (S - 1);
     const uint32_t items = cols / 256 * QT::IPB;
     const int IPL = IPL_T > 0 ? IPL_T : (int)(items >> log2s);
-    const uint32_t rows_iter = 4 * slots * RPS;
+    const uint32_t rows_iter = NW * slots * RPS;
     const uint32_t base0 = block * rows_iter;
-    auto row_of = [&](uint32_t base, int r) { return base + r * (4 * slots) + wave * slots + slot; };
+    auto row_of = [&](uint32_t base, int r) { return base + r * (NW * slots) + wave * slots + slot; };
 
     // Unrolled items: the activation loads, then the first row group's
     // weight loads, go out before the activation is staged, so the two
@@ -172,7 +173,7 @@ __device__ __forceinline__ void gemv_rows(const uint8_t *__restrict__ w, uint32_
             }
         }
     };
-    XStage<MODE> xs;
+    XStage<MODE, 64 * NW> xs;
     xs.load(xf, xq, cols);   // issued first: waiting for x then waits for nothing else
     // Neither the compiler nor the scheduler may move work across these two
     // points (x is deliberately not __restrict__, so its loads are not
@@ -246,12 +247,12 @@ __device__ __forceinline__ void gemv_rows(const uint8_t *__restrict__ w, uint32_
     }
 }
 
-template <class QT, int IPL_T, int RPS, int MODE>
-__global__ void __launch_bounds__(256)
+template <class QT, int IPL_T, int RPS, int MODE, int NW = 4>
+__global__ void __launch_bounds__(64 * NW)
     k_gemv(const uint8_t *__restrict__ w, uint32_t rows, uint32_t cols, uint64_t rb, uint32_t log2s,
            const float *xf, const uint8_t *xq, float *__restrict__ y) {
     extern __shared__ __align__(16) uint8_t lds[];
-    gemv_rows<QT, IPL_T, RPS, MODE>(w, rows, cols, rb, log2s, xf, xq, y, blockIdx.x, gridDim.x, lds);
+    gemv_rows<QT, IPL_T, RPS, MODE, NW>(w, rows, cols, rb, log2s, xf, xq, y, blockIdx.x, gridDim.x, lds);
 }
 
 // Up to four GEMVs over one activation in one launch (the engine's
@@ -288,6 +289,23 @@ static uint32_t lanes_per_row(uint32_t items) {
     return s;
 }
 
+// Waves per workgroup of a single GEMV: the count (4, 6 or 8) whose grid
+// puts the fewest rows on the busiest CU (each CU streams at most ~25 GB/s,
+// so the busiest one sets the time), the smallest among equals. 6144 rows of
+// 16 per 4-wave workgroup are 384 workgroups, two on half of 256 CUs; 6
+// waves make 256 workgroups of 24 rows, one per CU.
+static int gemv_waves(uint64_t rows, uint32_t rows_per_wave, int cus) {
+    int best = 4;
+    uint64_t best_rows = ~0ull;
+    for (int nw : {4, 6, 8}) {
+        const uint64_t per = (uint64_t)nw * rows_per_wave;
+        const uint64_t iters = (rows + per - 1) / per;
+        const uint64_t busiest = (iters + cus - 1) / cus * per;
+        if (busiest < best_rows) best = nw, best_rows = busiest;
+    }
+    return best;
+}
+
 template <class QT, int MODE>
 static hipError_t gemv_dispatch(const uint8_t *w, uint64_t rows, uint64_t cols, const float *xf, const uint8_t *xq,
                                 float *y, hipStream_t st) {
@@ -298,8 +316,8 @@ static hipError_t gemv_dispatch(const uint8_t *w, uint64_t rows, uint64_t cols, 
     const uint32_t lds = MODE == 0 ? actf_bytes((uint32_t)cols) : act_bytes((uint32_t)cols);
     const int cus = device_cu_count();
     const uint32_t slots = 64 / S;
-    auto go = [&](auto kern, int rps) -> hipError_t {
-        const uint64_t rows_iter = 4ull * slots * rps;
+    auto go = [&](auto kern, int rps, int nw) -> hipError_t {
+        const uint64_t rows_iter = (uint64_t)nw * slots * rps;
         uint64_t iters = (rows + rows_iter - 1) / rows_iter;
         const uint64_t cap = 8ull * cus;
         const uint32_t grid = (uint32_t)(iters < cap ? iters : cap);
@@ -307,16 +325,26 @@ static hipError_t gemv_dispatch(const uint8_t *w, uint64_t rows, uint64_t cols, 
             hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
             if (e != hipSuccess) return e;
         }
-        hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, st, w, (uint32_t)rows, (uint32_t)cols, rb,
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nw), lds, st, w, (uint32_t)rows, (uint32_t)cols, rb,
                            (uint32_t)ilog2(S), xf, xq, y);
         return hipGetLastError();
     };
     constexpr bool Q4 = QT::TYPE == T_Q4_K;
+    auto waves = [&](int rps) { return gemv_waves(rows, slots * rps, cus); };
     switch (ipl) {
-        case 1: return Q4 ? go(k_gemv<QT, 1, 4, MODE>, 4) : go(k_gemv<QT, 1, 2, MODE>, 2);
-        case 2: return Q4 ? go(k_gemv<QT, 2, 2, MODE>, 2) : go(k_gemv<QT, 2, 1, MODE>, 1);
-        case 3: return go(k_gemv<QT, 3, 1, MODE>, 1);
-        default: return go(k_gemv<QT, 0, 1, MODE>, 1);
+        case 1:
+            if constexpr (Q4) {
+                switch (waves(4)) {
+                    case 6: return go(k_gemv<QT, 1, 4, MODE, 6>, 4, 6);
+                    case 8: return go(k_gemv<QT, 1, 4, MODE, 8>, 4, 8);
+                    default: return go(k_gemv<QT, 1, 4, MODE>, 4, 4);
+                }
+            } else {
+                return go(k_gemv<QT, 1, 2, MODE>, 2, 4);
+            }
+        case 2: return Q4 ? go(k_gemv<QT, 2, 2, MODE>, 2, 4) : go(k_gemv<QT, 2, 1, MODE>, 1, 4);
+        case 3: return go(k_gemv<QT, 3, 1, MODE>, 1, 4);
+        default: return go(k_gemv<QT, 0, 1, MODE>, 1, 4);
     }
 }
 
