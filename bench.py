@@ -1225,8 +1225,10 @@ def main():
                     choices=sorted(MOE_WORKLOADS) + sorted(TOKEN_WORKLOADS) + sorted(GEMV_WORKLOADS) + sorted(DENSE_WORKLOADS) + ["moebatch", "moe48duty", "floor48", "tier48"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--normed-layer", action="store_true",
-                    help="moe48tok: katali_hip_moe_layer_normed (norm, router and layer in two launches per layer) "
-                         "instead of the norm/router launch and the layer (three)")
+                    help="moe48tok: katali_hip_moe_layer_normed, the residual add, norm and router in the layer's "
+                         "own launch (the default; kept for older command lines)")
+    ap.add_argument("--separate-norm", action="store_true",
+                    help="moe48tok: a k_norm_router launch (residual add, norm, router) before each layer instead")
     ap.add_argument("--stacked", action="store_true",
                     help="moe48 / moe40cold / moe48tok: the token's layers as one stacked launch "
                          "(katali_hip_moe_stack_run), each layer's input the previous layer's output")
@@ -1344,7 +1346,8 @@ def main():
     elif args.workload in TOKEN_WORKLOADS:
         base, vocab = TOKEN_WORKLOADS[args.workload]
         st = {} if args.dump_stamps else None
-        res, shape = bench_moe(hip, base, args.steps, args.warmup, vocab=vocab, normed=args.normed_layer,
+        normed = not args.separate_norm
+        res, shape = bench_moe(hip, base, args.steps, args.warmup, vocab=vocab, normed=normed,
                                stacked=args.stacked, stamps=st)
         if st:
             np.save(args.dump_stamps, st["stamps"])
@@ -1358,7 +1361,7 @@ def main():
                       "residual add of the previous layer's y, RMSNorm, F32 router rows and the MoE layer, the "
                       "logits exchanged on the device" if args.stacked else
                       "one launch for residual add + RMSNorm + F32 router, then the MoE layer"
-                      if not args.normed_layer else
+                      if not normed else
                       "katali_hip_moe_layer_normed: the residual add, RMSNorm and F32 router rows in the layer's "
                       "own prologue, the logits exchanged on the device" +
                       (" (k_moe_xcd: one launch)" if one else " (kernel A, then kernel B)"))
@@ -1373,8 +1376,8 @@ def main():
         }
         kernel = ("whole token graph (k_moe_stack: every layer's norm, router and MoE layer in one launch; then "
                   "output norm, head, argmax)" if args.stacked else
-                  f"whole token graph (per layer k_norm_router + the MoE layer, {layer}; then 4 launches: output "
-                  "norm, head, argmax)" if not args.normed_layer else
+                  f"whole token graph (per layer k_norm_router + the MoE layer, {layer}; then 3 launches: output "
+                  "norm, head, argmax)" if not normed else
                   "whole token graph (per layer " +
                   ("k_moe_xcd with the norm and router in its prologue, one launch" if one else
                    "k_moe_gu with the norm and router, k_moe_down") + "; output norm, head, argmax)")

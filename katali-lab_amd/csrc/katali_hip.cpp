@@ -177,7 +177,7 @@ int release_frees(std::vector<void *> &v) {
     return e == hipSuccess ? KATALI_HIP_OK : hip_fail(e, "deferred hipFree");
 }
 
-void *g_argmax = nullptr;   // argmax partials (kq::argmax_parts() * 8 bytes)
+void *g_argmax = nullptr;   // argmax partials and count (kq::argmax_scratch_bytes(), zeroed once)
 
 // The single-token layer's scratch (routing hand-off, error word, fused-layer
 // flags, h), allocated and zeroed on the first MoE call, outside any capture.
@@ -666,10 +666,12 @@ int katali_hip_argmax(const float *x, uint64_t n, int32_t *out) {
     if (n == 0 || n >= (1ull << 31)) return fail(KATALI_HIP_E_INVALID, "argmax n=%llu", (unsigned long long)n);
     if (!g_argmax) {
         if (g_capturing) return fail(KATALI_HIP_E_INVALID, "first argmax call must happen outside graph capture");
-        hipError_t e = hipMalloc(&g_argmax, (size_t)kq::argmax_parts() * 8);
+        hipError_t e = hipMalloc(&g_argmax, kq::argmax_scratch_bytes());
+        if (e == hipSuccess) e = hipMemsetAsync(g_argmax, 0, kq::argmax_scratch_bytes(), g_stream);
         if (e != hipSuccess) {
+            if (g_argmax) (void)hipFree(g_argmax);
             g_argmax = nullptr;
-            return hip_fail(e, "hipMalloc(argmax scratch)");
+            return hip_fail(e, "argmax scratch");
         }
     }
     return launched(kq::launch_argmax(x, (uint32_t)n, g_argmax, out, g_stream), "argmax");

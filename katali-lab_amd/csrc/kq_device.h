@@ -182,6 +182,24 @@ __device__ __forceinline__ float reduce_rows(float (&acc)[R]) {
     else return acc[0];
 }
 
+// Device-coherent 32-bit accesses (relaxed, agent scope): the store reaches
+// the point every XCD's L2 reads through and the load does not answer from a
+// stale line of its own XCD's L2, with no cache-wide write-back or
+// invalidate. The one-launch layers' exchanges and the single-launch argmax's
+// partials travel this way.
+__device__ __forceinline__ void st_dev(uint32_t *p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_dev(uint32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_dev2(uint32_t *p) {   // p 8-byte aligned
+    return __hip_atomic_load((uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev2(uint32_t *p, uint64_t v) {   // p 8-byte aligned
+    __hip_atomic_store((uint64_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ---------------------------------------------------------------------------
 // Pairwise sums over lanes (lane bit 0 first): the q8_1 path's row dot sums
 // its per-sub-block terms t_0 .. t_{n-1} pairwise, sum(t[0..n)) =

@@ -64,9 +64,10 @@ hipError_t launch_step_advance(int32_t *step, int32_t n_steps, hipStream_t s);
 hipError_t launch_copy(const uint8_t *src, uint8_t *dst, uint64_t n, hipStream_t s);
 
 // Greedy sampling: *out = index of the largest of n logits (first maximum
-// wins, NaN never, 0 when nothing exceeds -FLT_MAX). scratch holds
-// argmax_parts() * 8 bytes.
-uint32_t argmax_parts();
+// wins, NaN never, 0 when nothing exceeds -FLT_MAX), one launch. scratch:
+// argmax_scratch_bytes(), zeroed once before the first call (the kernel
+// leaves it ready for the next).
+uint32_t argmax_scratch_bytes();
 // out = RMSNorm(x) * w with the engine's arithmetic; the add variant first
 // does x += delta (scale 1) or x += scale * delta in place. One workgroup;
 // out may be x.

@@ -36,22 +36,6 @@ constexpr uint32_t B_MAX_THREADS = 512;   // kernel B's largest workgroup
 constexpr int MAX_SLOTS = MAX_SEL + 1;
 constexpr uint32_t MAX_EXPERT = 512;
 
-// Device-coherent 32-bit accesses (relaxed, agent scope): the store reaches
-// the point every XCD's L2 reads through and the load does not answer from a
-// stale line of its own XCD's L2, with no cache-wide write-back or
-// invalidate. The fused layer's h blocks and flags travel this way only.
-__device__ __forceinline__ void st_dev(uint32_t *p, uint32_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t ld_dev(uint32_t *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t ld_dev2(uint32_t *p) {   // p 8-byte aligned
-    return __hip_atomic_load((uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev2(uint32_t *p, uint64_t v) {   // p 8-byte aligned
-    __hip_atomic_store((uint64_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 // polls of the fused layer's wait before it gives up (each at least one
 // device round trip: ~1 s in all); expiry sets error bit 4
 constexpr uint32_t FSYNC_SPIN_LIMIT = 1u << 20;

@@ -4,8 +4,12 @@
 // gguf_sampler.c:62-66): best = 0, bv = -FLT_MAX, then for i ascending take i
 // when logits[i] > bv. So the first maximum wins, NaN never wins, and when no
 // value exceeds -FLT_MAX the answer is 0. Here: (value, index) pairs reduced
-// with "larger value, then lower index" over candidates v > -FLT_MAX, in two
-// launches (per-workgroup partials, then one workgroup), no atomics.
+// with "larger value, then lower index" over candidates v > -FLT_MAX, in one
+// launch: every workgroup reduces its share and stores its pair as one
+// device-coherent 64-bit word; once that store is acknowledged it counts
+// itself in, and the workgroup that counts last reduces the partials and
+// writes the answer, then puts the count back to zero for the next call
+// (stream order: no two calls overlap, and a graph replay starts from zero).
 #include <float.h>
 
 #include "kq_device.h"
@@ -42,34 +46,46 @@ __device__ __forceinline__ Best block_best(Best b) {
 }
 
 constexpr int32_t NONE = 0x7FFFFFFF;
+constexpr uint32_t ARGMAX_PARTS = 256;
+constexpr uint32_t ARGMAX_COUNT = 2 * ARGMAX_PARTS;   // the count word, after the partials
 
-__global__ void __launch_bounds__(256) k_argmax_part(const float *__restrict__ x, uint32_t n, Best *__restrict__ part) {
+__device__ __forceinline__ uint64_t pack(Best b) { return ((uint64_t)(uint32_t)b.i << 32) | __float_as_uint(b.v); }
+__device__ __forceinline__ Best unpack(uint64_t w) { return Best{__uint_as_float((uint32_t)w), (int32_t)(w >> 32)}; }
+
+// words: ARGMAX_PARTS 64-bit partials, then the count (zero between calls)
+__global__ void __launch_bounds__(256) k_argmax(const float *__restrict__ x, uint32_t n, uint32_t *words,
+                                                int32_t *out) {
+    __shared__ uint32_t last;
     Best b{-FLT_MAX, NONE};
     for (uint32_t t = blockIdx.x * 256 + threadIdx.x; t < n; t += gridDim.x * 256) {
         const float v = x[t];
         if (v > b.v) b = Best{v, (int32_t)t};   // ascending t per thread: strict > keeps the first
     }
     b = block_best(b);
-    if (threadIdx.x == 0) part[blockIdx.x] = b;
+    if (threadIdx.x == 0) {
+        st_dev2(words + 2 * blockIdx.x, pack(b));
+        __builtin_amdgcn_s_waitcnt(VMCNT0);   // the partial is acknowledged before the count
+        last = __hip_atomic_fetch_add(words + ARGMAX_COUNT, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    Best r{-FLT_MAX, NONE};
+    for (uint32_t t = threadIdx.x; t < gridDim.x; t += 256) r = better(r, unpack(ld_dev2(words + 2 * t)));
+    r = block_best(r);
+    if (threadIdx.x == 0) {
+        *out = r.i == NONE ? 0 : r.i;
+        st_dev(words + ARGMAX_COUNT, 0u);
+    }
 }
 
-__global__ void __launch_bounds__(256) k_argmax_final(const Best *__restrict__ part, uint32_t nparts, int32_t *out) {
-    Best b{-FLT_MAX, NONE};
-    for (uint32_t t = threadIdx.x; t < nparts; t += 256) b = better(b, part[t]);
-    b = block_best(b);
-    if (threadIdx.x == 0) *out = b.i == NONE ? 0 : b.i;
-}
-
-uint32_t argmax_parts() { return 256; }
+uint32_t argmax_scratch_bytes() { return 4 * (ARGMAX_COUNT + 1); }
 
 hipError_t launch_argmax(const float *x, uint32_t n, void *scratch, int32_t *out, hipStream_t s) {
     uint32_t g = (n + 2047) / 2048;
     if (g < 1) g = 1;
-    if (g > argmax_parts()) g = argmax_parts();
-    hipLaunchKernelGGL(k_argmax_part, dim3(g), dim3(256), 0, s, x, n, (Best *)scratch);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, s, (const Best *)scratch, g, out);
+    if (g > ARGMAX_PARTS) g = ARGMAX_PARTS;
+    hipLaunchKernelGGL(k_argmax, dim3(g), dim3(256), 0, s, x, n, (uint32_t *)scratch, out);
     return hipGetLastError();
 }
 

@@ -41,7 +41,7 @@ KERNELS = {
     "moe40cold": ("k_moe_xcd",),
     "gemv6144": ("k_gemv",),
     "qwen8b": ("k_moe_down", "k_moe_gu", "k_gemv_multi", "k_gemv"),
-    "moe48tok": ("k_argmax_final", "k_norm_router", "k_moe_xcd", "k_rmsnorm", "k_gemv", "k_argmax_part"),
+    "moe48tok": ("k_argmax", "k_norm_router", "k_moe_xcd", "k_rmsnorm", "k_gemv"),
     "moebatch": ("k_mb_group", "k_quantize_q8_1", "k_moe_gu_grp", "k_mb_gu_mfma", "k_moe_down_grp", "k_mb_down_mfma",
                  "k_mb_combine"),
 }
