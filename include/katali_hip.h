@@ -307,6 +307,16 @@ int katali_hip_moe_stack_destroy(void *stack);
  * in the reference. */
 int katali_hip_one_launch(int32_t mode);
 
+/* How the one-launch layers hand a slot's h values between the workgroups
+ * of that slot, which the dispatcher places on one XCD: 1 inside the XCD
+ * (the words stay in its L2), 0 written through to memory as the
+ * cross-XCD exchanges are. Mode 1 takes effect only where the library's
+ * start-up check found every launch of 256 workgroups dealt to the eight
+ * XCDs round robin (b % 8 classes each on one XCD); mode 0 sets it off, -1
+ * only asks. Both give the same bits. Returns the state before the call. No
+ * counterpart in the reference. */
+int katali_hip_xcd_handoff(int32_t mode);
+
 /* KATALI_HIP_OK when katali_hip_moe_layer (n_tokens 0) or katali_hip_moe_batch
  * (n_tokens 1..64 tokens) runs a layer of this descriptor's shape with n_sel
  * routed experts; else the code and last-error message the call would give.

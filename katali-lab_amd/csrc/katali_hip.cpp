@@ -71,6 +71,7 @@ constexpr size_t NOALLOC_FSYNC = NOALLOC_HQ8 + NOALLOC_HQ8_MAX;
 static_assert(NOALLOC_FSYNC % 256 == 0, "exchange words 256-byte aligned");
 __device__ __align__(256) uint8_t scratch[NOALLOC_FSYNC + kq::fsync_words() * 4];
 uint8_t *g_scratch = nullptr;   // scratch's device address on g_device
+bool g_dispatch_ok = false;     // the start-up XCD dispatch check's result
 
 int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 int fail(int code, const char *fmt, ...) {
@@ -133,9 +134,18 @@ int init_locked() {
         g_status = std::string("device init: allocation-free scratch: ") + hipGetErrorString(e);
         return KATALI_HIP_E_NODEVICE;
     }
+    // the one-launch layers' h hand-off inside each XCD, if the dispatcher
+    // keeps each b % 8 class of a launch on one XCD (checked on g_stream)
+    if ((e = kq::xcd_dispatch_check(g_stream)) != hipSuccess) {
+        g_status = std::string("device init: XCD dispatch check: ") + hipGetErrorString(e);
+        return KATALI_HIP_E_NODEVICE;
+    }
+    g_dispatch_ok = kq::xcd_local();
+    if (env_off("KATALI_HIP_XCD_LOCAL")) kq::xcd_local_set(false);
     char buf[256];
-    snprintf(buf, sizeof buf, "%s (%s, %d CUs, %.0f GiB)", p.name, p.gcnArchName, p.multiProcessorCount,
-             (double)p.totalGlobalMem / (1024.0 * 1024.0 * 1024.0));
+    snprintf(buf, sizeof buf, "%s (%s, %d CUs, %.0f GiB; h hand-off %s)", p.name, p.gcnArchName,
+             p.multiProcessorCount, (double)p.totalGlobalMem / (1024.0 * 1024.0 * 1024.0),
+             kq::xcd_local() ? "inside the XCD" : "written through");
     g_status = buf;
     g_usable = true;
     return KATALI_HIP_OK;
@@ -504,16 +514,18 @@ int katali_hip_sync(void) {
     if (e != hipSuccess) return hip_fail(e, "read error word");
     if (na) (void)hipMemset(g_scratch + NOALLOC_ERR, 0, 4);
     if (err) (void)hipMemset(g_err_dev, 0, 4);
-    if ((err | na) & 4) {
+    if ((err | na) & 12) {
         // a one-launch layer gave up waiting for its own workgroups (the
-        // device was shared with other work): its outputs and the exchange
-        // words are void; start over, and from now on run every layer as
-        // kernels A and B, which never wait in-kernel
-        if (g_fsync && (err & 4)) (void)hipMemset(g_fsync, 0, kq::fsync_words() * 4);
-        if (na & 4) (void)hipMemset(g_scratch + NOALLOC_FSYNC, 0, kq::fsync_words() * 4);
+        // device was shared with other work; bit 4), or one of its
+        // workgroups ran on another XCD than the round-robin dispatch puts it
+        // on (bit 8, whose slot's waits may have expired too): its outputs
+        // and the exchange words are void; start over, and from now on run
+        // every layer as kernels A and B, which never wait in-kernel
+        if (g_fsync && (err & 12)) (void)hipMemset(g_fsync, 0, kq::fsync_words() * 4);
+        if (na & 12) (void)hipMemset(g_scratch + NOALLOC_FSYNC, 0, kq::fsync_words() * 4);
         kq::xcd_disable();
-        return fail(KATALI_HIP_E_TIMEOUT, "MoE layer: in-kernel wait expired (outputs invalid; the one-launch "
-                                          "layers are off from now on)");
+        return fail(KATALI_HIP_E_TIMEOUT, "MoE layer: %s (outputs invalid; the one-launch layers are off from now on)",
+                    ((err | na) & 8) ? "a workgroup ran on another XCD than its slot's" : "in-kernel wait expired");
     }
     if (err | na)
         return fail(KATALI_HIP_E_INVALID, "MoE expert id outside [0, n_expert) in the explicit routing");
@@ -737,6 +749,14 @@ int katali_hip_one_launch(int32_t mode) {
     const int was = kq::xcd_disabled() ? 0 : 1;
     if (mode == 0) kq::xcd_disable();
     else if (mode == 1) kq::xcd_enable();
+    return was;
+}
+
+int katali_hip_xcd_handoff(int32_t mode) {
+    if (ensure() != KATALI_HIP_OK) return 0;
+    const int was = kq::xcd_local() ? 1 : 0;
+    if (mode == 0) kq::xcd_local_set(false);
+    else if (mode == 1) kq::xcd_local_set(g_dispatch_ok);
     return was;
 }
 

@@ -121,6 +121,9 @@ struct MoeArgs {
     float *nxn_out;
     const float *router;   // F32 [n_expert][hidden]
     float *logits_out;
+    // The one-launch layers: h words handed over inside the XCD (set by the
+    // launcher from xcd_local(); callers leave it 0)
+    uint32_t hloc;
 };
 bool moe_shape_supported(uint32_t gate_type, uint32_t down_type, uint32_t hidden, uint32_t ffn);
 // Dynamic LDS (bytes) of the largest workgroup a layer of this shape launches:
@@ -238,6 +241,11 @@ hipError_t launch_moe_stack(const MoeArgs &a, const StackLayer *lt, uint32_t n_l
 void xcd_disable();
 void xcd_enable();
 bool xcd_disabled();
+// Dispatch check for the XCD-local h hand-off (run once, outside capture):
+// on when every launch of XCD_G workgroups puts each b % 8 class on one XCD.
+hipError_t xcd_dispatch_check(hipStream_t s);
+bool xcd_local();
+void xcd_local_set(bool on);
 // The measurement build's phase stamps of the one-launch layers
 // ([64][256][16] uint64, s_memrealtime ticks); hipErrorNotSupported in the
 // product build.

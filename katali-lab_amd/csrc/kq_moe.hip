@@ -448,7 +448,7 @@ struct StkCtx {
 // stack's waits also read the error word and give up once an expiry is
 // recorded there (the outputs are void then anyway).
 __device__ __forceinline__ bool stack_expired(const MoeArgs &a, uint32_t spins) {
-    return (spins & 1023u) == 0 && (ld_dev((uint32_t *)a.err) & 4u) != 0;
+    return (spins & 1023u) == 0 && (ld_dev((uint32_t *)a.err) & 12u) != 0;
 }
 
 // Wait until every workgroup of the previous layer has stored its y: thread
@@ -2003,15 +2003,23 @@ __device__ __forceinline__ void xcd_body(const MoeArgs &a, uint32_t gen, uint32_
     uint32_t *hxs = a.fsync + FSYNC_XS + 2 * 128 * xs;   // this XCD's copy of its unit's
     if (wave == 0) {
         const float *gu = (const float *)(lds + lds_a(a.hidden, NB).gu);
+        // The h words are read only by the slot's own workgroups, which
+        // share one XCD (a.hloc: the dispatch was checked for that): then
+        // the words stay in that XCD's L2, else they are written through.
+        const bool own_xcd = a.hloc != 0;
         if (lane < (uint32_t)IW) {
             const float h = kq_silu_mul(gu[lane], gu[IW + lane]);
-            st_dev2(hx + 2 * (IW * li + lane), ((uint64_t)tag << 32) | __float_as_uint(h));
+            const uint64_t v = ((uint64_t)tag << 32) | __float_as_uint(h);
+            if (own_xcd) st_xcd2(hx + 2 * (IW * li + lane), v);
+            else st_dev2(hx + 2 * (IW * li + lane), v);
         }
         if constexpr (SH) {
             if (lane >= (uint32_t)IW && lane < (uint32_t)(IW + IWS)) {
                 const uint32_t j = lane - IW;
                 const float h = kq_silu_mul(gu[2 * IW + j], gu[2 * IW + IWS + j]);
-                st_dev2(hxs + 2 * (IWS * li + j), ((uint64_t)tag << 32) | __float_as_uint(h));
+                const uint64_t v = ((uint64_t)tag << 32) | __float_as_uint(h);
+                if (own_xcd) st_xcd2(hxs + 2 * (IWS * li + j), v);
+                else st_dev2(hxs + 2 * (IWS * li + j), v);
             }
         }
         ctx.st.mark(6);
@@ -2367,8 +2375,10 @@ static hipError_t go_xcd_c(const MoeArgs &a, hipStream_t s, const StackLayer *lt
 // 2048, ffn <= 1024, <= 256 experts, a 256-CU device on which every
 // workgroup can be resident at once, and the one-launch layers not turned
 // off after an expired wait (xcd_disable)
-static hipError_t launch_moe_xcd(const MoeArgs &a, uint32_t n_slots, bool shared_units, hipStream_t s,
+static hipError_t launch_moe_xcd(const MoeArgs &a0, uint32_t n_slots, bool shared_units, hipStream_t s,
                                  const StackLayer *lt = nullptr, uint32_t nl = 0) {
+    MoeArgs a = a0;
+    a.hloc = xcd_local() ? 1u : 0u;
     const uint32_t nb = a.hidden / 256;
     const bool spread = shared_units && a.n_sel == (int)XCD_SLOTS && a.has_shared;
     if (!a.fsync || xcd_disabled() || !(n_slots == XCD_SLOTS || spread) || a.n_sel < 1 || !(nb == 4 || nb == 8) ||
@@ -2395,6 +2405,40 @@ void xcd_disable() { g_xcd_off = true; }
 void xcd_enable() { g_xcd_off = false; }
 bool xcd_disabled() { return g_xcd_off; }
 
+// The XCD-local hand-off of the h words (st_xcd2) needs every workgroup b
+// with one b % 8 on one XCD. The dispatcher deals a launch's workgroups to
+// the eight XCDs round robin, starting at an XCD that depends on the queue
+// (measured: workgroup b on XCD (b + k) % 8, k fixed per hardware queue, for
+// every workgroup of every launch). xcd_dispatch_check launches XCD_G
+// workgroups of the layer's size four times and keeps the hand-off on only
+// if each launch shows one k for all of them; otherwise the h words are
+// written through (st_dev2), as the partials are.
+static __device__ uint32_t xcc_seen[4 * XCD_G];
+static int g_xcd_local = 0;
+__global__ void __launch_bounds__(1024) k_xcc_map(uint32_t *out) {
+    if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
+}
+hipError_t xcd_dispatch_check(hipStream_t s) {
+    uint32_t *dev = nullptr;
+    hipError_t e = hipGetSymbolAddress((void **)&dev, HIP_SYMBOL(xcc_seen));
+    for (int r = 0; r < 4 && e == hipSuccess; r++) {
+        hipLaunchKernelGGL(k_xcc_map, dim3(XCD_G), dim3(1024), 0, s, dev + r * XCD_G);
+        e = hipGetLastError();
+    }
+    uint32_t h[4 * XCD_G];
+    if (e == hipSuccess) e = hipMemcpyAsync(h, dev, sizeof h, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    bool ok = e == hipSuccess && device_cu_count() == (int)XCD_G;
+    for (int r = 0; r < 4 && ok; r++) {
+        const uint32_t k = (h[r * XCD_G] + 8) % 8;
+        for (uint32_t b = 0; b < XCD_G && ok; b++) ok = h[r * XCD_G + b] < 8 && (h[r * XCD_G + b] + 8 - b % 8) % 8 == k;
+    }
+    g_xcd_local = ok ? 1 : 0;
+    return e;
+}
+bool xcd_local() { return g_xcd_local != 0; }
+void xcd_local_set(bool on) { g_xcd_local = on ? 1 : 0; }
+
 hipError_t launch_moe_stack(const MoeArgs &a, const StackLayer *lt, uint32_t n_layers, bool normed, hipStream_t s) {
     if (!lt || n_layers < 1 || a.n_expert > MAX_EXPERT || a.n_sel > MAX_SEL || a.hidden > XCD_MAX_HIDDEN)
         return hipErrorInvalidValue;
@@ -2404,7 +2448,9 @@ hipError_t launch_moe_stack(const MoeArgs &a, const StackLayer *lt, uint32_t n_l
     if (!a.fsync || xcd_disabled() || n_slots != XCD_SLOTS || a.has_shared || !(nb == 4 || nb == 8) ||
         a.n_expert > XCD_G || a.ffn > 1024 || device_cu_count() != (int)XCD_G)
         return hipErrorNotSupported;
-    return nb == 8 ? go_xcd_c<8, false, true>(a, s, lt, n_layers) : go_xcd_c<4, false, true>(a, s, lt, n_layers);
+    MoeArgs b = a;
+    b.hloc = xcd_local() ? 1u : 0u;
+    return nb == 8 ? go_xcd_c<8, false, true>(b, s, lt, n_layers) : go_xcd_c<4, false, true>(b, s, lt, n_layers);
 }
 
 uint64_t moe_route_words() { return 2 * MAX_SLOTS; }
@@ -2647,6 +2693,7 @@ hipError_t launch_moe_normed(MoeArgs a, float *xn_buf, float *logits_buf, hipStr
         b.xq = nullptr;
         b.logits = nullptr;
         b.step = nullptr;
+        b.hloc = xcd_local() ? 1u : 0u;
         const hipError_t e = a.hidden == 2048 ? go_xcd_c<8, false, true>(b, s) : go_xcd_c<4, false, true>(b, s);
         if (e != hipErrorNotSupported) {
             if (merged) *merged = e == hipSuccess;

@@ -70,6 +70,7 @@ SIGNATURES = {
     "katali_hip_moe_stack_run": (C.c_int, [_vp, _vp, _vp, _f32]),
     "katali_hip_moe_stack_destroy": (C.c_int, [_vp]),
     "katali_hip_one_launch": (C.c_int, [_i32]),
+    "katali_hip_xcd_handoff": (C.c_int, [_i32]),
     "katali_hip_phase_stamps": (C.c_int, [_vp, _sz]),
     "katali_hip_stream_floor": (C.c_int, [_i32, _vp, _sz, _vp, _sz, _vp]),
     "katali_hip_stager_create": (C.c_int, [_u64, _u32, C.POINTER(_vp)]),
@@ -308,6 +309,11 @@ class KataliHip:
         """The one-launch layers on (1) or off (0), or only asked (-1);
         returns whether they were on before the call."""
         return bool(self.lib.katali_hip_one_launch(mode))
+
+    def xcd_handoff(self, mode: int = -1) -> bool:
+        """The one-launch layers' h hand-off inside the XCD (1) or written
+        through (0), or only asked (-1); returns the state before the call."""
+        return bool(self.lib.katali_hip_xcd_handoff(mode))
 
     def moe_check(self, desc, n_sel, n_tokens=0) -> None:
         """Raises HipError when a layer (n_tokens 0) or a batch of n_tokens of

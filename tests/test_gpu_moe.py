@@ -332,6 +332,44 @@ def test_xcd_wait_expiry_reports_and_recovers(hip, oracle, moes, monkeypatch):
         assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32)), call
 
 
+HANDOFF_CASES = [CASES[0], CASES[1], CASES[12], CASES[14]]
+
+
+@pytest.mark.parametrize("case", HANDOFF_CASES, ids=[case_id(c) for c in HANDOFF_CASES])
+def test_xcd_handoff_modes_bit_identical(hip, moes, case, monkeypatch):
+    """The one-launch layer's h words handed over inside each XCD (the default
+    where the start-up check finds the round-robin dispatch, as on a 256-CU
+    MI355X) or written through to memory: the same bits in y, gate/up, the
+    q8_1 h blocks and the routing, on two calls in a row each; only the
+    words' path differs."""
+    set_mode(monkeypatch, "xcd")
+    hidden, ffn, n_expert, n_sel, shared, down_type = case
+    m = moes(hidden, ffn, n_expert, shared, down_type)
+    rng = np.random.default_rng(77 + hidden + n_sel)
+    x = S.activation(rng, hidden)
+    logits = rng.standard_normal(n_expert).astype(np.float32)
+    st = hip.status()
+    print(f"[handoff] case={case} status={st}", flush=True)
+    if " 256 CUs" in st:
+        assert "h hand-off inside the XCD" in st
+        assert hip.xcd_handoff(-1)
+    was = hip.xcd_handoff(-1)
+    outs = {}
+    try:
+        for mode in (1, 0, 1):
+            hip.xcd_handoff(mode)
+            for call in range(2):
+                r = run_layer(hip, m, x, n_sel, logits=logits)
+                outs.setdefault(mode, []).append(r)
+    finally:
+        hip.xcd_handoff(1 if was else 0)
+    ref = outs[0][0]
+    for mode, rs in outs.items():
+        for k, r in enumerate(rs):
+            for a, b in zip(r, ref):
+                assert np.array_equal(np.asarray(a).view(np.uint8), np.asarray(b).view(np.uint8)), (mode, k)
+
+
 ROUTE_CASES = [
     # n_expert, n_sel, logits
     (128, 8, "ties"),      # integer logits: many equal values across the cut
