@@ -322,10 +322,10 @@ int moe_impl(const KataliHipMoe *m, const KataliHipMoeRoute *r, const float *x, 
     // B. The other one-launch layer is opt-in (KATALI_HIP_FUSED=1): measured
     // slower than kernels A and B (its all-slots h exchange costs more than
     // the launch it saves).
-    // Eight routed experts plus the shared expert take it too, the shared
-    // expert in 128-value units (12.65 us per layer at the 2048/512
-    // top-8-of-256 shape against 13.5 for kernels A and B);
-    // KATALI_HIP_XCD_SHARED=0 keeps those on kernels A and B.
+    // Eight routed experts plus the shared expert (ffn 256 or 512) take it
+    // too, the shared expert spread over all its workgroups (12.1 us per
+    // layer at the 2048/512 top-8-of-256 shape against 13.6 for kernels A
+    // and B); KATALI_HIP_XCD_SHARED=0 keeps those on kernels A and B.
     const bool allow_fused = env_on("KATALI_HIP_FUSED");
     const bool allow_xcd = !env_off("KATALI_HIP_XCD");
     const bool xcd_units = !env_off("KATALI_HIP_XCD_SHARED");

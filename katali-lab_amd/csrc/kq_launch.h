@@ -154,9 +154,9 @@ hipError_t launch_moe(const MoeArgs &a, hipStream_t s, bool allow_fused = false,
 // From FSYNC_X, the XCD-sliced layer's (launch_moe with allow_xcd): one
 // generation word per workgroup (XCD_G of them), then from FSYNC_XH its h
 // values [slot][ffn <= 1024], then from FSYNC_XP its unweighted down
-// partials [slot][hidden], then with the shared expert in 128-value units
-// from FSYNC_XS each XCD's copy of its unit's h [xcd][128] and from
-// FSYNC_XSP the units' unweighted down partials [unit][hidden]; from
+// partials [slot][hidden], then with the shared expert from FSYNC_XS its h
+// [ffn <= 512] (each workgroup's share written through, read on every XCD)
+// and from FSYNC_XSP its unweighted down partials [hidden]; from
 // FSYNC_XR, with the steps before the layer in its prologue, FSYNC_REP
 // copies of its router logits [512] (an area of its own: its generations
 // are the XCD layer's); each value one 8-byte word {float, generation}. Each exchange has its own generations, so no
@@ -172,10 +172,10 @@ constexpr uint32_t FSYNC_X = FSYNC_R + FSYNC_REP * 2 * 512;
 constexpr uint32_t FSYNC_XH = FSYNC_X + XCD_G;
 constexpr uint32_t XCD_MAX_FFN = 1024;
 constexpr uint32_t FSYNC_XP = FSYNC_XH + 2 * XCD_SLOTS * XCD_MAX_FFN;
-constexpr uint32_t XCD_MAX_UNITS = 4;   // the shared expert's 128-value units (ffn <= 512)
+constexpr uint32_t XCD_MAX_SH_FFN = 512;   // the shared expert's ffn in that layer
 constexpr uint32_t FSYNC_XS = FSYNC_XP + 2 * XCD_SLOTS * XCD_MAX_HIDDEN;
-constexpr uint32_t FSYNC_XSP = FSYNC_XS + 2 * XCD_SLOTS * 128;
-constexpr uint32_t FSYNC_XR = FSYNC_XSP + 2 * XCD_MAX_UNITS * XCD_MAX_HIDDEN;
+constexpr uint32_t FSYNC_XSP = FSYNC_XS + 2 * XCD_MAX_SH_FFN;
+constexpr uint32_t FSYNC_XR = FSYNC_XSP + 2 * XCD_MAX_HIDDEN;
 // From FSYNC_XY, the stacked layer's (launch_moe_stack): two areas (layer
 // parity) of a layer's y [hidden] as words {float, generation}, read by the
 // next layer of the stack, then from FSYNC_XF two areas of one completion

@@ -26,6 +26,8 @@
 // an equal logit and a lower index); ranks 0..n_sel-1 are selected. Weights
 // w_r = exp(l_r - l_max) / sum_sel exp(l_j - l_max) in rank order, which is
 // softmax followed by renormalisation over the selection.
+#include <type_traits>
+
 #include "kq_device.h"
 #include "kq_launch.h"
 
@@ -1710,14 +1712,141 @@ static hipError_t launch_moe_fused(const MoeArgs &a, uint32_t n_slots, hipStream
 constexpr uint32_t XCD_POLL_WAVES = 4;   // waves that poll the slot's h
 constexpr int XCD_HW = 4;                // h words per polling thread at most: 1024 <= 4 * 256
 
+// The shared expert of the XCD-sliced layer (SH): every byte of its weights
+// is read once, by whole rows, and none of it depends on the routing.
+//   gate/up: workgroup b forms shared h values b * IWS .. + IWS - 1 (IWS =
+//     ffn / XCD_G; gate and up rows of those values on wave SW, kernel A's
+//     item mapping, scale records, term order and reductions, so every value
+//     is kernel A's) and publishes each as one tagged device-coherent word
+//     once x is staged; (single layer) its loads went out before the
+//     routing's, so the values are out before the slots' gate/up data is
+//     in, and their exchange across the XCDs is hidden behind the stream;
+//   down: XCD x takes shared rows [x H / 8, (x + 1) H / 8), RSW of them per
+//     workgroup on waves SD.., 16 lanes per row over the whole ffn (the
+//     routed slots' lane split), dotted against the shared h the pollers
+//     stage with the slot's; one unweighted partial per row.
+// The combine adds that partial last with weight 1, as kernel B does.
+template <int NB, class QD, int S, int IW>
+struct XcdShared {
+    static constexpr int RW = 4, ITEMS = 8 * NB, LPG = RW * ITEMS / 64, M = ITEMS >= 64 ? ITEMS / 64 : 1;
+    static constexpr int WH = RW * NB, HPL = (WH + 63) / 64;
+    static constexpr uint32_t H = 256 * NB, F = 32 * IW;
+    static constexpr uint32_t IWS = F / XCD_G;                 // shared h values per workgroup
+    static constexpr uint32_t SW = 9, SD = 10;                 // the gate/up wave, the first down wave
+    static constexpr uint32_t RSW = H / XCD_G;                 // shared down rows per workgroup
+    static constexpr uint32_t NWD = (RSW * S + 63) / 64;       // down waves
+    static constexpr uint32_t NBK = F / 256;
+    static constexpr uint64_t RB = NB * 144, RBD = (uint64_t)NBK * QD::BB;
+    static_assert(IWS >= 1 && 2 * IWS <= (uint32_t)RW && NBK <= (uint32_t)(S / QD::IPB) && SD + NWD <= 12,
+                  "XCD layer shared expert shape");
+    static_assert(HPL == (4 * NB + 63) / 64 && LPG == NB / 2, "XCD layer shared expert registers");
+    uint32_t b, xs, li, tid, lane, wave;
+
+    __device__ __forceinline__ bool down_wave() const { return wave >= SD && wave < SD + NWD; }
+    __device__ __forceinline__ uint32_t item() const { return ((tid - 64 * SD) % S) % QD::IPB; }
+    __device__ __forceinline__ uint32_t bslot() const { return ((tid - 64 * SD) % S) / QD::IPB; }
+    // the shared down row this thread's item belongs to (threads past RSW * S: a real row, dropped)
+    __device__ __forceinline__ uint32_t row() const {
+        return xs * (H / XCD_SLOTS) + li * RSW + min((tid - 64 * SD) / S, RSW - 1);
+    }
+    __device__ __forceinline__ const uint8_t *gu_row(const MoeArgs &a, uint32_t v) const {   // v < RW (clamped)
+        v = min(v, 2 * IWS - 1);
+        return v < IWS ? a.gate_sh + (uint64_t)(b * IWS + v) * RB : a.up_sh + (uint64_t)(b * IWS + v - IWS) * RB;
+    }
+    __device__ __forceinline__ void issue_down(const MoeArgs &a, typename QD::Raw &raw) const {
+        if (down_wave())
+            raw = QD::load(a.down_sh + (uint64_t)row() * RBD + min(bslot(), NBK - 1) * QD::BB, (int)item());
+    }
+    __device__ __forceinline__ void issue_gu(const MoeArgs &a, uint4 (&hv)[HPL], uint4 (&q)[LPG]) const {
+        if (wave == SW) {   // whole wave
+#pragma unroll
+            for (int i = 0; i < HPL; i++) {
+                const uint32_t h = min(lane + 64 * i, (uint32_t)WH - 1);
+                hv[i] = ld16(gu_row(a, h / NB) + (h % NB) * 144);
+            }
+#pragma unroll
+            for (int k = 0; k < LPG; k++) {
+                uint32_t r, it;
+                if constexpr (ITEMS >= 64) {
+                    r = k / M;
+                    it = 64 * (k % M) + lane;
+                } else {
+                    r = lane / ITEMS + k * (64 / ITEMS);
+                    it = lane % ITEMS;
+                }
+                q[k] = ld16(gu_row(a, r) + (it / 8) * 144 + 16 + 16 * (it % 8));
+            }
+            // keeps this branch's last load its own: the down waves' branch
+            // ends in a 16-byte load too, and merging the two would turn the
+            // registers they load into stack slots
+            asm volatile("");
+        }
+    }
+    // wave SW, once x is staged at xa: the IWS shared h values, published as
+    // tagged words (and the gate/up values to dbg_gu, slot n_sel)
+    __device__ __forceinline__ void dots(const MoeArgs &a, uint8_t *lds, const Act &xa, uint32_t tag,
+                                         const uint4 (&hv)[HPL], const uint4 (&q)[LPG]) const {
+        const LdsA L = lds_a(a.hidden, NB);
+        XSlice xsl[M];
+#pragma unroll
+        for (int m = 0; m < M; m++) xsl[m] = x_slice(xa, ITEMS >= 64 ? 64 * m + lane : lane % ITEMS);
+        float4 *scl = (float4 *)(lds + L.scl) + 4 * WH * SW;   // the wave's own slice of the scale records
+#pragma unroll
+        for (int i = 0; i < HPL; i++) {
+            const uint32_t h = lane + 64 * i;
+            if (h < (uint32_t)WH) {
+                Q4K::Raw rw;
+                rw.h = hv[i];
+                const uint32_t bb = h % NB;
+                const float4 dA = *(const float4 *)(xa.d8 + 8 * bb), dB = *(const float4 *)(xa.d8 + 8 * bb + 4);
+                const float d8[8] = {dA.x, dA.y, dA.z, dA.w, dB.x, dB.y, dB.z, dB.w};
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    float ds0, ds1, dm0, dm1;
+                    Q4K::scales(rw, g, ds0, ds1, dm0, dm1);
+                    scl[4 * h + g] = make_float4(ds0 * d8[2 * g], ds1 * d8[2 * g + 1], dm0 * d8[2 * g], dm1 * d8[2 * g + 1]);
+                }
+            }
+        }
+        wave_sync_lds();
+        float *gu = (float *)(lds + L.gu) + RW * SW;
+        if constexpr (ITEMS >= 64) {
+            float acc[LPG];
+#pragma unroll
+            for (int k = 0; k < LPG; k++) {
+                const uint32_t it = 64 * (k % M) + lane, r = k / M;
+                acc[k] = q4k_term(q[k], scl[4 * (r * NB + it / 8) + (it % 8) / 2], xsl[k % M]);
+            }
+            const float v = pw_rows<LPG, M>(acc);
+            if (lane < (uint32_t)RW) gu[pw_rows_row<LPG, M>(lane)] = v;
+        } else {
+            const uint32_t it = lane % ITEMS;
+#pragma unroll
+            for (int k = 0; k < LPG; k++) {
+                const uint32_t r = lane / ITEMS + k * (64 / ITEMS);
+                const float v = group_sum<ITEMS>(q4k_term(q[k], scl[4 * (r * NB + it / 8) + (it % 8) / 2], xsl[0]));
+                if (it == 0) gu[r] = v;
+            }
+        }
+        wave_sync_lds();
+        if (lane < IWS) {
+            const float h = kq_silu_mul(gu[lane], gu[IWS + lane]);
+            st_dev2(a.fsync + FSYNC_XS + 2 * (b * IWS + lane), ((uint64_t)tag << 32) | __float_as_uint(h));
+        }
+        if (a.dbg_gu && lane < 2 * IWS)   // the shared expert is slot n_sel
+            a.dbg_gu[(uint64_t)a.n_sel * 2 * a.ffn + (lane < IWS ? 0 : a.ffn) + b * IWS + lane % IWS] = gu[lane];
+    }
+};
+
 // One workgroup's gate/up part: rows v < R of slot `slot` (v < IW: gate row
-// IW * li + v, v < 2 IW: up row IW * li + v - IW) and, with IWS > 0, of the
-// shared expert (v < 2 IW + IWS: gate row shb + v - 2 IW; then the up rows;
-// written to dbg_gu only when sh_dbg), kernel A's item mapping, scale records, term
-// order and reductions (so every value is kernel A's), on waves 0 .. R/4 - 1
-// (rows past R in the last of them are loaded and dropped); the others stage
-// x with them. `down` issues the caller's down loads (after the wave's dots,
-// or once x is staged on waves without rows). Leaves the R gate/up values in
+// IW * li + v, v < 2 IW: up row IW * li + v - IW), kernel A's item mapping,
+// scale records, term order and reductions (so every value is kernel A's),
+// on waves 0 .. R/4 - 1 (rows past R in the last of them are loaded and
+// dropped); the others stage x with them. `down` issues the caller's down
+// loads (after the wave's dots, or once x is staged on waves without rows).
+// The shared expert's part (XcdShared): sh_start issues its single-layer
+// weight loads right behind the routing's, sh_late forms its gate/up values
+// once x is staged (in the stack it loads them first). Leaves the R gate/up values in
 // LDS at lds + lds_a(..).gu. NORMED: the steps before the layer first
 // (normed_prologue, with the caller's generation gen and the logits words
 // at FSYNC_XR); x is the normalized vector it forms, the routing comes from
@@ -1725,12 +1854,12 @@ constexpr int XCD_HW = 4;                // h words per polling thread at most: 
 // first layer x is the previous layer's y, read from its tagged words (or,
 // NORMED, the residual step takes that y as its delta), and no wave issues
 // a weight load before the whole of that y is seen.
-template <int NB, int C, int IW, int IWS, class Down, bool NORMED = false, bool STK = false>
+template <int NB, int C, int IW, class Down, class ShStart, class ShLate, bool NORMED = false, bool STK = false>
 __device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_t li, uint8_t *lds, GuRoute &rt,
-                                        Down down, uint32_t shb, bool sh_dbg, uint32_t gen, StkCtx &ctx) {
+                                        Down down, ShStart sh_start, ShLate sh_late, uint32_t gen, StkCtx &ctx) {
     constexpr int RW = 4;                      // rows per wave (kernel A's at these widths)
     static_assert(a1_rw<NB>() == RW, "gu_part: kernel A's 4-row waves");
-    constexpr int R = 2 * IW + 2 * IWS, GW = (R + RW - 1) / RW;   // rows, waves with rows
+    constexpr int R = 2 * IW, GW = (R + RW - 1) / RW;   // rows, waves with rows
     constexpr int NT = a1_threads<NB>();
     constexpr int ITEMS = 8 * NB;
     constexpr int LPG = RW * ITEMS / 64;       // chunks per lane (one group: LPG <= 16)
@@ -1787,6 +1916,7 @@ __device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_
                 xdv[i] = ld_u16(b);
             }
         }
+        if constexpr (!STK) sh_start();   // routing-independent weights, behind only the routing's loads
         if (!STK || ctx.l == 0) route_finish<C>(a, lv, rt);
     }
     __builtin_amdgcn_s_waitcnt(VMCNT0);
@@ -1806,9 +1936,7 @@ __device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_
     auto row_ptr = [&](uint32_t v) -> const uint8_t * {   // v < R (clamped past it)
         v = min(v, (uint32_t)R - 1);
         if (v < (uint32_t)IW) return gb + (uint64_t)(IW * li + v) * rb;
-        if (v < (uint32_t)(2 * IW)) return ub + (uint64_t)(IW * li + v - IW) * rb;
-        if (v < (uint32_t)(2 * IW + IWS)) return a.gate_sh + (uint64_t)(shb + v - 2 * IW) * rb;
-        return a.up_sh + (uint64_t)(shb + v - 2 * IW - IWS) * rb;
+        return ub + (uint64_t)(IW * li + v - IW) * rb;
     };
     auto chunk = [&](int k) -> const uint8_t * {
         uint32_t r, it;
@@ -1913,31 +2041,117 @@ __device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_
     }
     ctx.st.mark(4);
     down();   // behind this wave's gate/up loads in the CU's queue
+    sh_late(xa, gen + 1);   // (the shared wave: no rows of the slot's)
     ctx.st.mark(5);
     __syncthreads();
-    if (a.dbg_gu && tid < (uint32_t)R) {
-        float *d = a.dbg_gu + (uint64_t)slot * 2 * a.ffn + (tid < (uint32_t)IW ? 0 : a.ffn) + IW * li + tid % IW;
-        if constexpr (IWS > 0) {
-            if (tid >= (uint32_t)(2 * IW) && !sh_dbg) return;
-            if (tid >= (uint32_t)(2 * IW))   // the shared expert is slot n_sel
-                d = a.dbg_gu + (uint64_t)a.n_sel * 2 * a.ffn + (tid < (uint32_t)(2 * IW + IWS) ? 0 : a.ffn) + shb +
-                    (tid - 2 * IW) % IWS;
+    if (a.dbg_gu && tid < (uint32_t)R)
+        a.dbg_gu[(uint64_t)slot * 2 * a.ffn + (tid < (uint32_t)IW ? 0 : a.ffn) + IW * li + tid % IW] = gu[tid];
+}
+
+// SH: eight routed slots plus the shared expert (XcdShared): its h values
+// come from all 256 workgroups and are exchanged across the XCDs, long
+// before the slots' h is complete; the pollers stage the whole shared h
+// with the slot's, and wave 0 adds each row's shared partial after the
+// eight slots, weight 1 (the shared expert enters last, as in kernel B).
+// A group of GT threads (whole waves; thread pt of the group) polls nw
+// tagged words, word pt + GT i on thread pt (word(e) its address), until
+// every one carries tag, then stages them as q8_1 blocks in dst with kernel
+// A's quantizer (32 lanes hold one block) and, with hq, writes the blocks
+// there as kernel A writes them. Two rounds in flight: the next round goes
+// out before the previous one is checked, so a word is sampled twice per
+// round trip (ROUNDS 2; with ROUNDS 1 one round at a time, half the poll
+// traffic). A word already seen is kept, and its lane's later loads read
+// `rest` instead (one line per wave instruction, the value dropped), so late
+// rounds fetch only what is still missing while the down rows stream. The
+// loads themselves are unconditional, so both rounds stay countable in
+// flight; va and vb hold the rounds (the caller keeps them allocated to its
+// end: a round is still in flight when the words are complete).
+template <int NW, uint32_t GT, bool STK, int ROUNDS, class Word>
+__device__ __forceinline__ void poll_stage(const MoeArgs &a, uint32_t pt, uint32_t nw, Word word, uint32_t *rest,
+                                           uint32_t tag, const Act &dst, uint8_t *hq, uint32_t &spins,
+                                           uint64_t (&va)[NW], uint64_t (&vb)[NW]) {
+    const uint32_t lane = threadIdx.x & 63;
+    uint64_t hv[NW];
+#pragma unroll
+    for (int i = 0; i < NW; i++) hv[i] = 0;   // (words past nw: never seen, quantized and dropped)
+    uint32_t need = 0;   // bit i: word pt + GT i still to see
+#pragma unroll
+    for (int i = 0; i < NW; i++)
+        if (pt + GT * i < nw) need |= 1u << i;
+    auto issue = [&](uint64_t *o) {
+#pragma unroll
+        for (int i = 0; i < NW; i++) o[i] = ld_dev2(((need >> i) & 1) ? word(pt + GT * i) : rest);
+    };
+    auto take = [&](const uint64_t *o) {   // true once every word of the wave is in
+#pragma unroll
+        for (int i = 0; i < NW; i++) {
+            if (((need >> i) & 1) && (uint32_t)(o[i] >> 32) == tag) {
+                hv[i] = o[i];
+                need &= ~(1u << i);
+            }
         }
-        *d = gu[tid];
+        return __all(need == 0);
+    };
+    issue(va);
+    for (;;) {
+        if constexpr (ROUNDS == 2) {
+            issue(vb);
+            if (take(va)) break;
+            issue(va);
+            if (take(vb)) break;
+        } else {
+            if (take(va)) break;
+            issue(va);
+        }
+        if (++spins >= FSYNC_SPIN_LIMIT / ROUNDS || (STK && stack_expired(a, spins))) {
+            if (lane == 0) atomicOr(a.err, 4);
+            break;
+        }
+    }
+    // kernel A's quantizer on every word first, with no store between them
+    // (the NW words' dependency chains interleave; one wave per SIMD runs
+    // this, so it is latency-bound), then the stores
+    float dq[NW];
+    int qq[NW], tq[NW], sq[NW];
+    uint32_t d16q[NW];
+#pragma unroll
+    for (int i = 0; i < NW; i++) {
+        const float h = __uint_as_float((uint32_t)hv[i]);
+        const float am = max32(fabsf(h));
+        const float d = am / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        const int qv = (int)roundf(h * id);
+        int s16 = qv;   // the 16-value half-block sum: a 16-lane row of DPP
+        s16 += dpp_i<DPP_XOR1>(s16);
+        s16 += dpp_i<DPP_XOR2>(s16);
+        s16 += dpp_i<DPP_HALF_MIRROR>(s16);
+        s16 += dpp_i<DPP_MIRROR>(s16);
+        dq[i] = d;
+        qq[i] = qv;
+        tq[i] = sum32(qv);
+        sq[i] = s16;
+        d16q[i] = f2h_rne(d);
+    }
+#pragma unroll
+    for (int i = 0; i < NW; i++) {
+        const uint32_t e = pt + GT * i;   // its 32-lane half is one block
+        if (e < nw) {                     // whole 32-lane halves (nw a multiple of 32)
+            const float d = dq[i];
+            const int qv = qq[i], total = tq[i], s16 = sq[i];
+            const uint32_t d16 = d16q[i];
+            const uint32_t kb = e / 32, j = e % 32;
+            dst.qs[e] = (int8_t)qv;
+            if (j == 0) dst.d8[kb] = h2f(d16);
+            if ((j & 15) == 0) dst.qs16[2 * kb + j / 16] = s16;
+            if (hq) {
+                uint8_t *blk = hq + (uint64_t)kb * 36;
+                blk[4 + j] = (uint8_t)(qv & 255);
+                if (j == 0) *(uint32_t *)blk = d16 | (f2h_rne((float)total * d) << 16);
+            }
+        }
     }
 }
 
-// SH: eight routed slots plus the shared expert. The shared expert's ffn is
-// cut into U = ffn / 128 units of 128 intermediate values (one half n of
-// down block bk: 2 bk + n = u), so every q8_1 block of its h lies in one
-// unit. XCD x takes unit u = x % U: its 32 workgroups compute the unit's
-// 128 h values (4 each: gate and up rows 128 u + 4 li + [0, 4), the same
-// values on each of the Q = 8 / U XCDs of a unit), exchange them inside
-// the XCD, and dot the unit's down items (half n of block bk: IPB / 2 items
-// per row) over the XCD's part x / U of the output rows, one unweighted
-// partial per row and unit. Wave 0 sums, per row, the eight slots in rank
-// order and then the U shared partials in unit order, weight 1 (the shared
-// expert enters last, as in kernel B).
 // The body of one layer: k_moe_xcd runs it once; k_moe_stack runs it per
 // layer of a stack (STK, ctx), with that layer's tag gen + 1 + ctx.l; the
 // generation words advance by n_layers at the stack's last layer.
@@ -1951,36 +2165,46 @@ __device__ __forceinline__ void xcd_body(const MoeArgs &a, uint32_t gen, uint32_
     constexpr uint32_t TRX = H / PER;             // down rows per workgroup
     constexpr uint32_t TRC = TRX / XCD_SLOTS;     // rows each workgroup sums
     constexpr uint32_t NBK = F / 256;             // blocks per down row
-    constexpr uint32_t U = SH ? F / 128 : 1;      // shared units
-    constexpr uint32_t Q = XCD_SLOTS / U;         // XCDs per unit
-    constexpr int IWS = SH ? 4 : 0;               // shared h values per workgroup (128 / 32)
-    constexpr uint32_t HW = F + (SH ? 128 : 0);   // h words polled: the slot's, then the unit's
-    constexpr uint32_t IH = QD::IPB / 2;          // down items of one half block
-    constexpr uint32_t RS = H / Q / PER;          // shared down rows per workgroup
-    static_assert(S * TRX <= NT && TRC >= 1 && XCD_SLOTS * TRC <= 64 && (!SH || U * TRC <= 64), "XCD layer tile");
-    static_assert(!SH || (XCD_SLOTS % U == 0 && RS * IH <= 128), "XCD layer shared units");
-    static_assert(HW <= XCD_HW * 64 * XCD_POLL_WAVES && F % 256 == 0, "XCD layer ffn");
+    static_assert(S * TRX <= NT && TRC >= 1 && XCD_SLOTS * TRC <= 64, "XCD layer tile");
+    static_assert(!SH || (!NORMED && (2 * IW + 3) / 4 <= 8 && F <= XCD_MAX_SH_FFN && H <= XCD_MAX_HIDDEN),
+                  "XCD layer shared expert: plain layers, rows below wave 8, its exchange areas");
+    static_assert(F <= XCD_HW * 64 * XCD_POLL_WAVES && F % 256 == 0, "XCD layer ffn");
     extern __shared__ __align__(16) uint8_t lds[];
     const uint32_t tid = STK ? opaque_v(threadIdx.x) : threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t b = STK ? opaque_s(blockIdx.x) : blockIdx.x, xs = b % XCD_SLOTS, li = b / XCD_SLOTS;
-    const uint32_t u = xs % U, part = xs / U;   // SH: this XCD's unit and its part of the output rows
     pin_args(a.down, a.down_sh, a.y, a.fsync, a.hq8);
     uint32_t *gw = a.fsync + FSYNC_X + b;
     ctx.st.begin();
 
-    // the down share: row r = tid / S of the tile, lane s = tid % S; with SH,
-    // threads t < RS * IH also take item IH * (u % 2) + t % IH of block u / 2
-    // of shared row part * H / Q + li * RS + t / IH
+    // the down share: row r = tid / S of the tile, lane s = tid % S
     const uint32_t s = tid % S, r = tid / S;
     const uint32_t item = s % QD::IPB, bs = s / QD::IPB;
     const uint32_t row0 = li * TRX, rr = min(r, TRX - 1);   // idle threads load a real row and drop it
-    const bool sdown = SH && tid < RS * IH;                   // whole waves up to RS * IH (a multiple of 32)
-    const uint32_t itemS = IH * (u % 2) + tid % IH, bkS = u / 2;
-    const uint32_t rowS = part * (H / Q) + li * RS + min(tid / IH, RS - 1);
     constexpr uint64_t rbd = (uint64_t)NBK * QD::BB;
     typename QD::Raw raw[IPL];
-    typename QD::Raw rawS;
     GuRoute rt;
+    // the shared expert's registers (SH): gate/up rows on its gate/up wave,
+    // down items on its down waves
+    constexpr int SHPL = (4 * NB + 63) / 64, SLPG = NB / 2;
+    uint4 shv[SHPL], shq[SLPG];
+    typename QD::Raw shr;
+    typename QD::Unp shu;
+    auto sh_start = [&]() {   // the single layer: its loads ahead of the routing's
+        if constexpr (SH) {
+            const XcdShared<NB, QD, S, IW> sh{b, xs, li, tid, lane, wave};
+            sh.issue_gu(a, shv, shq);
+            sh.issue_down(a, shr);
+        }
+    };
+    auto sh_late = [&](const Act &xa, uint32_t tg) {
+        if constexpr (SH) {
+            const XcdShared<NB, QD, S, IW> sh{b, xs, li, tid, lane, wave};
+            if (wave == XcdShared<NB, QD, S, IW>::SW) {
+                if constexpr (STK) sh.issue_gu(a, shv, shq);
+                sh.dots(a, lds, xa, tg, shv, shq);
+            }
+        }
+    };
     auto load_down = [&]() {
         int32_t sid = __builtin_amdgcn_readlane(rt.eid, (int)xs);
         if ((uint32_t)sid >= a.n_expert) sid = 0;   // bad explicit id: reported by route_publish
@@ -1988,19 +2212,16 @@ __device__ __forceinline__ void xcd_body(const MoeArgs &a, uint32_t gen, uint32_
                             (uint64_t)(row0 + rr) * rbd;
 #pragma unroll
         for (int i = 0; i < IPL; i++) raw[i] = QD::load(rp + min(bs + P * i, NBK - 1) * QD::BB, (int)item);
-        if constexpr (SH) {
-            if (tid < ((RS * IH + 63) & ~63u))   // whole waves; threads past RS * IH load a real row and drop it
-                rawS = QD::load(a.down_sh + (uint64_t)rowS * rbd + bkS * QD::BB, (int)itemS);
-        }
+        if constexpr (SH && STK) XcdShared<NB, QD, S, IW>{b, xs, li, tid, lane, wave}.issue_down(a, shr);
     };
-    gu_part<NB, C, IW, IWS, decltype(load_down), NORMED, STK>(a, xs, li, lds, rt, load_down, 128 * u + IWS * li,
-                                                              part == 0, gen + ctx.l, ctx);
+    gu_part<NB, C, IW, decltype(load_down), decltype(sh_start), decltype(sh_late), NORMED, STK>(
+        a, xs, li, lds, rt, load_down, sh_start, sh_late, gen + ctx.l, ctx);
 
     uint32_t tag = gen + ctx.l;
     asm volatile("" : "+v"(tag));
     tag += 1;
     uint32_t *hx = a.fsync + FSYNC_XH + 2 * F * xs;    // slot xs's h words
-    uint32_t *hxs = a.fsync + FSYNC_XS + 2 * 128 * xs;   // this XCD's copy of its unit's
+    uint32_t *hxs = a.fsync + FSYNC_XS;                   // the shared expert's (SH)
     if (wave == 0) {
         const float *gu = (const float *)(lds + lds_a(a.hidden, NB).gu);
         // The h words are read only by the slot's own workgroups, which
@@ -2013,27 +2234,17 @@ __device__ __forceinline__ void xcd_body(const MoeArgs &a, uint32_t gen, uint32_
             if (own_xcd) st_xcd2(hx + 2 * (IW * li + lane), v);
             else st_dev2(hx + 2 * (IW * li + lane), v);
         }
-        if constexpr (SH) {
-            if (lane >= (uint32_t)IW && lane < (uint32_t)(IW + IWS)) {
-                const uint32_t j = lane - IW;
-                const float h = kq_silu_mul(gu[2 * IW + j], gu[2 * IW + IWS + j]);
-                const uint64_t v = ((uint64_t)tag << 32) | __float_as_uint(h);
-                if (own_xcd) st_xcd2(hxs + 2 * (IWS * li + j), v);
-                else st_dev2(hxs + 2 * (IWS * li + j), v);
-            }
-        }
         ctx.st.mark(6);
     }
 
-    // 3. the h words: word t of thread pt is word pt + 256 t (the slot's h
-    //    first, then the unit's), quantized where 32 lanes hold one 32-value
-    //    block (kernel A's quantizer)
+    // 3. the h words, quantized as q8_1 blocks in LDS: the slot's by the
+    //    pollers, the shared expert's (SH) by waves 8 to 11 (poll_stage)
     uint32_t spins = 0;
     constexpr uint32_t first_poller = NT - 64 * XCD_POLL_WAVES;
     const bool poller = tid >= first_poller;   // whole waves
     const uint32_t LT = lds_a(a.hidden, NB).total;
     const Act act = act_carve(lds + LT, F);
-    const Act actS = act_carve(lds + LT + act_bytes(F), F);   // SH only: the unit's blocks
+    const Act actS = act_carve(lds + LT + act_bytes(F), F);   // SH only: the shared expert's blocks
     // Every wave unpacks its down items here, while h is awaited (the
     // pollers before their first poll), so only the dot products and the
     // scales follow h. After that no wave waits on a load: the pollers'
@@ -2043,24 +2254,33 @@ __device__ __forceinline__ void xcd_body(const MoeArgs &a, uint32_t gen, uint32_
     // the poll rounds' registers stay allocated to the pollers' end (an
     // empty use there), so nothing after the loop reuses a register that
     // round still loads into.
-    typename QD::Unp un[IPL], unS;
+    typename QD::Unp un[IPL];
 #pragma unroll
     for (int i = 0; i < IPL; i++) {
         un[i] = QD::unpack(raw[i]);
         pin_vregs(raw[i]);
         pin_vregs(un[i]);
     }
-    if constexpr (SH) {   // (threads past the unit's waves: unused)
-        unS = QD::unpack(rawS);
-        pin_vregs(rawS);
-        pin_vregs(unS);
+    if constexpr (SH) {   // (threads past the shared down waves: unused)
+        shu = QD::unpack(shr);
+        pin_vregs(shr);
+        pin_vregs(shu);
     }
-    constexpr int NW = (HW + 64 * XCD_POLL_WAVES - 1) / (64 * XCD_POLL_WAVES);
-    uint64_t va[NW], vb[NW];
+    constexpr uint32_t GT = 64 * XCD_POLL_WAVES;
+    constexpr int NW = (F + GT - 1) / GT;             // the slot's words per poller
+    constexpr int NWS = SH ? (F + GT - 1) / GT : 1;   // the shared expert's per shared poller (waves 8 to 11)
+    uint64_t va[NW], vb[NW], sva[NWS], svb[NWS];
 #pragma unroll
     for (int i = 0; i < NW; i++) va[i] = vb[i] = 0;
+#pragma unroll
+    for (int i = 0; i < NWS; i++) sva[i] = svb[i] = 0;
+    // the shared h, published long before the slot's, by the four waves
+    // below the pollers (no gate/up rows of the slot's there: GW <= 8)
+    const bool spoller = SH && wave >= 8 && wave < 12;
     if (poller) {
         const uint32_t pt = tid - first_poller;
+        // (only words e < F are ever asked for; the other arm keeps this
+        // loop's code as it is measured)
         auto word = [&](uint32_t e) { return e < F ? hx + 2 * e : hxs + 2 * (e - F); };
         // Two rounds in flight: the next round goes out before the previous
         // one is checked, so a word is sampled twice per round trip. A word
@@ -2069,17 +2289,18 @@ __device__ __forceinline__ void xcd_body(const MoeArgs &a, uint32_t gen, uint32_
         // instruction, the value dropped), so late rounds fetch only what
         // is still missing while the down rows stream. The loads themselves
         // are unconditional, so both rounds stay countable in flight.
+        // (poll_stage is the same loop for the shared pollers; written out
+        // here, the slot's loop keeps the registers of its rounds in place.)
         uint64_t hv[NW];
 #pragma unroll
-        for (int i = 0; i < NW; i++) hv[i] = 0;   // (words past HW: never seen, quantized and dropped)
+        for (int i = 0; i < NW; i++) hv[i] = 0;   // (words past F: never seen, quantized and dropped)
         uint32_t need = 0;   // bit i: word pt + 256 i still to see
 #pragma unroll
         for (int i = 0; i < NW; i++)
-            if (pt + 64 * XCD_POLL_WAVES * i < HW) need |= 1u << i;
+            if (pt + GT * i < F) need |= 1u << i;
         auto issue = [&](uint64_t *o) {
 #pragma unroll
-            for (int i = 0; i < NW; i++)
-                o[i] = ld_dev2(((need >> i) & 1) ? word(pt + 64 * XCD_POLL_WAVES * i) : hx);
+            for (int i = 0; i < NW; i++) o[i] = ld_dev2(((need >> i) & 1) ? word(pt + GT * i) : hx);
         };
         auto take = [&](const uint64_t *o) {   // true once every word of the wave is in
 #pragma unroll
@@ -2130,31 +2351,31 @@ __device__ __forceinline__ void xcd_body(const MoeArgs &a, uint32_t gen, uint32_
         }
 #pragma unroll
         for (int i = 0; i < NW; i++) {
-            const uint32_t w = pt + 64 * XCD_POLL_WAVES * i;   // its 32-lane half is one block of one expert
-            if (w < HW) {   // whole 32-lane halves (F and 128 multiples of 32)
-                const bool shared = SH && w >= F;
-                const uint32_t e = shared ? 128 * u + (w - F) : w;   // the value's index in its expert's h
-                const Act &dst = shared ? actS : act;
+            const uint32_t e = pt + GT * i;   // its 32-lane half is one block
+            if (e < F) {                      // whole 32-lane halves (F a multiple of 32)
                 const float d = dq[i];
                 const int qv = qq[i], total = tq[i], s16 = sq[i];
                 const uint32_t d16 = d16q[i];
                 const uint32_t kb = e / 32, j = e % 32;
-                dst.qs[e] = (int8_t)qv;
-                if (j == 0) dst.d8[kb] = h2f(d16);
-                if ((j & 15) == 0) dst.qs16[2 * kb + j / 16] = s16;
-                if (li == 0 && (!shared || part == 0)) {   // the q8_1 blocks of h, as kernel A writes them
-                    const uint32_t hs = shared ? (uint32_t)a.n_sel : xs;   // the shared expert is slot n_sel
-                    uint8_t *blk = a.hq8 + ((uint64_t)hs * (F / 32) + kb) * 36;
+                act.qs[e] = (int8_t)qv;
+                if (j == 0) act.d8[kb] = h2f(d16);
+                if ((j & 15) == 0) act.qs16[2 * kb + j / 16] = s16;
+                if (li == 0) {   // the q8_1 blocks of h, as kernel A writes them
+                    uint8_t *blk = a.hq8 + ((uint64_t)xs * (F / 32) + kb) * 36;
                     blk[4 + j] = (uint8_t)(qv & 255);
                     if (j == 0) *(uint32_t *)blk = d16 | (f2h_rne((float)total * d) << 16);
                 }
             }
         }
+    } else if (spoller) {   // (the shared expert is slot n_sel)
+        poll_stage<NWS, GT, STK, 1>(a, tid - 512, F, [&](uint32_t e) { return hxs + 2 * e; }, hx, tag, actS,
+                                  li == 0 && xs == 0 ? a.hq8 + (uint64_t)a.n_sel * (F / 32) * 36 : nullptr, spins,
+                                  sva, svb);
     }
     __syncthreads();
     ctx.st.mark(9);
 
-    // the tile's unweighted down partials (and, with SH, the unit's shared ones)
+    // the tile's unweighted down partials (and, with SH, the shared rows')
     float x = 0.0f;
 #pragma unroll
     for (int i = 0; i < IPL; i++) {
@@ -2167,15 +2388,19 @@ __device__ __forceinline__ void xcd_body(const MoeArgs &a, uint32_t gen, uint32_
         st_dev2(a.fsync + FSYNC_XP + 2 * (xs * H + row0 + r), ((uint64_t)tag << 32) | __float_as_uint(x));
     ctx.st.mark(10);
     if constexpr (SH) {
-        if (tid < ((RS * IH + 63) & ~63u)) {   // whole waves
-            const float xsh = group_sum<IH>(QD::dot_q8_u(rawS, unS, (int)itemS, actS, bkS));
-            if (sdown && tid % IH == 0)
-                st_dev2(a.fsync + FSYNC_XSP + 2 * (u * H + rowS), ((uint64_t)tag << 32) | __float_as_uint(xsh));
+        using XS = XcdShared<NB, QD, S, IW>;
+        const XS sh{b, xs, li, tid, lane, wave};
+        if (sh.down_wave()) {   // whole waves
+            const uint32_t bk = sh.bslot();
+            const float d = QD::dot_q8_u(shr, shu, (int)sh.item(), actS, min(bk, NBK - 1));
+            const float xsh = group_sum<S>(bk < NBK ? d : 0.0f);
+            if (tid - 64 * XS::SD < XS::RSW * S && (tid - 64 * XS::SD) % S == 0)
+                st_dev2(a.fsync + FSYNC_XSP + 2 * sh.row(), ((uint64_t)tag << 32) | __float_as_uint(xsh));
         }
     }
 
     // 4. wave 0: rows row0 + xs * TRC + c (c < TRC) over the eight slots, then
-    //    the shared expert's U partials
+    //    the shared expert's partial
     if (wave == 0) {
         float rw = (NORMED || a.logits) && a.n_sel > 0 ? route_weight(rt.logit, a.n_sel) : rt.w;
         rw = (int)lane < a.n_sel ? rw : ((int)lane == a.n_sel && a.has_shared ? 1.0f : 0.0f);
@@ -2183,10 +2408,10 @@ __device__ __forceinline__ void xcd_body(const MoeArgs &a, uint32_t gen, uint32_
         const uint32_t q = lane / TRC, c = lane % TRC;   // lane: slot (or unit) q, row c
         const uint32_t yr = row0 + xs * TRC + c;
         uint32_t *pw = a.fsync + FSYNC_XP + 2 * (min(q, XCD_SLOTS - 1) * H + yr);
-        uint32_t *pws = a.fsync + FSYNC_XSP + 2 * (min(q, U - 1) * H + yr);
+        uint32_t *pws = a.fsync + FSYNC_XSP + 2 * yr;   // lanes c < TRC: the shared partial of row yr
         auto ok = [&](uint64_t v, uint64_t vs) {
             return __all((lane >= XCD_SLOTS * TRC || (uint32_t)(v >> 32) == tag) &&
-                         (!SH || lane >= U * TRC || (uint32_t)(vs >> 32) == tag));
+                         (!SH || lane >= TRC || (uint32_t)(vs >> 32) == tag));
         };
         // One round in flight: a wave ends only once its loads are back, so
         // a second round still in flight when the partials are complete
@@ -2211,10 +2436,7 @@ __device__ __forceinline__ void xcd_body(const MoeArgs &a, uint32_t gen, uint32_
         }
         if constexpr (SH) {
             const float vs = __uint_as_float((uint32_t)sv);
-            float sh = 0.0f;
-#pragma unroll
-            for (uint32_t k = 0; k < U; k++) sh += __shfl(vs, (int)(k * TRC + c), WAVE);   // unit order
-            y = fmaf(1.0f, sh, y);   // the shared expert, last
+            y = fmaf(1.0f, __shfl(vs, (int)c, WAVE), y);   // the shared expert, last
         }
         if constexpr (STK) {   // the next layer's x (or delta) as tagged words
             if (lane < TRC && ctx.l + 1 < n_layers)
@@ -2235,6 +2457,9 @@ __device__ __forceinline__ void xcd_body(const MoeArgs &a, uint32_t gen, uint32_
     if (poller) {
 #pragma unroll
         for (int i = 0; i < NW; i++) asm volatile("" ::"v"(va[i]), "v"(vb[i]));
+    } else if (spoller) {
+#pragma unroll
+        for (int i = 0; i < NWS; i++) asm volatile("" ::"v"(sva[i]), "v"(svb[i]));
     }
     ctx.st.store(tag, b, tid, first_poller);
 }
@@ -2324,23 +2549,32 @@ static bool all_resident(const void *k, uint32_t nt, uint32_t lds) {
 // lt: the stacked layer's per-layer table (nl layers), else the single layer
 template <int NB, int C, class QD, int S, int IPL, int IW, bool SH, bool NORMED>
 static hipError_t go_xcd(const MoeArgs &a, hipStream_t s, const StackLayer *lt, uint32_t nl) {
-    uint32_t lds = lds_a(a.hidden, NB).total + (SH ? 2 : 1) * act_bytes(32 * IW);
+    uint32_t lds = lds_a(a.hidden, NB).total + (SH ? 2 : 1) * act_bytes(32 * IW);   // (SH: the shared h blocks)
     // the normed prologue's area starts at the scale records, which are
     // written only after its last read
     if (NORMED) lds = max(lds, lds_a(a.hidden, NB).scl + normed_area_bytes(a.hidden));
-    const void *k = lt ? (const void *)k_moe_stack<NB, C, QD, S, IPL, IW, SH, NORMED>
-                       : (const void *)k_moe_xcd<NB, C, QD, S, IPL, IW, SH, NORMED>;
+    // The stack at hidden 1024 with 256 experts and the shared expert does
+    // not fit the registers (it would need scratch): those stacks run layer
+    // by layer.
+    constexpr bool STACK = !(SH && NB == 4 && C == 4);
+    if (lt && !STACK) return hipErrorNotSupported;
+    const void *k = (const void *)k_moe_xcd<NB, C, QD, S, IPL, IW, SH, NORMED>;
+    if constexpr (STACK) {
+        if (lt) k = (const void *)k_moe_stack<NB, C, QD, S, IPL, IW, SH, NORMED>;
+    }
     if (lds > 64 * 1024) {
         const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
     if (!all_resident(k, a1_threads<NB>(), lds)) return hipErrorNotSupported;
-    if (lt)
-        hipLaunchKernelGGL((k_moe_stack<NB, C, QD, S, IPL, IW, SH, NORMED>), dim3(XCD_G), dim3(a1_threads<NB>()), lds,
-                           s, a, lt, nl);
-    else
-        hipLaunchKernelGGL((k_moe_xcd<NB, C, QD, S, IPL, IW, SH, NORMED>), dim3(XCD_G), dim3(a1_threads<NB>()), lds, s,
-                           a);
+    if constexpr (STACK) {
+        if (lt) {
+            hipLaunchKernelGGL((k_moe_stack<NB, C, QD, S, IPL, IW, SH, NORMED>), dim3(XCD_G), dim3(a1_threads<NB>()),
+                               lds, s, a, lt, nl);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((k_moe_xcd<NB, C, QD, S, IPL, IW, SH, NORMED>), dim3(XCD_G), dim3(a1_threads<NB>()), lds, s, a);
     return hipGetLastError();
 }
 // 16 lanes per down row: Q6_K 4 items x 4 block slots (ffn <= 1024: one
@@ -2357,7 +2591,7 @@ static hipError_t go_xcd_f(const MoeArgs &a, hipStream_t s, const StackLayer *lt
         case 256: return go_xcd_q<NB, C, 8, SH, NORMED>(a, s, lt, nl);
         case 512: return go_xcd_q<NB, C, 16, SH, NORMED>(a, s, lt, nl);
         case 768:
-            if constexpr (!SH) return go_xcd_q<NB, C, 24, SH, NORMED>(a, s, lt, nl);   // the shared units must divide the eight XCDs
+            if constexpr (!SH) return go_xcd_q<NB, C, 24, SH, NORMED>(a, s, lt, nl);   // the shared gate/up rows must fit one wave
             else return hipErrorNotSupported;
         case 1024:
             if constexpr (!SH) return go_xcd_q<NB, C, 32, SH, NORMED>(a, s, lt, nl);   // shared rows would not fit 64 per workgroup
@@ -2371,7 +2605,7 @@ static hipError_t go_xcd_c(const MoeArgs &a, hipStream_t s, const StackLayer *lt
 }
 // hipErrorNotSupported when the shape does not fit the XCD-sliced layer:
 // eight slots (one per XCD), or with shared_units eight routed experts plus
-// the shared expert in 128-value units (ffn 256 or 512 then), hidden 1024 or
+// the shared expert (ffn 256 or 512 then; XcdShared), hidden 1024 or
 // 2048, ffn <= 1024, <= 256 experts, a 256-CU device on which every
 // workgroup can be resident at once, and the one-launch layers not turned
 // off after an expired wait (xcd_disable)

@@ -76,8 +76,8 @@ CASES = [
     (2048, 512, 256, 7, True, Q6_K),
     (1024, 1024, 64, 8, False, Q4_K),
     (2048, 256, 32, 8, False, Q6_K),
-    # eight routed experts and the shared expert in 128-value units in the
-    # XCD-sliced layer (the 2048/512 top-8 + shared case above is another):
+    # eight routed experts and the shared expert (spread over every
+    # workgroup) in the XCD-sliced layer (the 2048/512 top-8 + shared case above is another):
     # hidden 1024 with a Q4_K down (four items per unit and row), and ffn 256
     # (two units, four XCDs each)
     (1024, 512, 64, 8, True, Q4_K),
@@ -90,7 +90,7 @@ XCD_CASES = [c for c in CASES if (c[3] + (1 if c[4] else 0) == 8 or (c[3] == 8 a
              and c[0] in (1024, 2048) and c[1] <= 1024 and c[2] <= 256]
 # two_launch: kernels A and B; one_launch: k_moe_fused; xcd: the XCD-sliced
 # layer where the shape fits it (the default for eight slots and for eight
-# routed experts plus the shared expert in 128-value units; set explicitly)
+# routed experts plus the shared expert; set explicitly)
 MODES = {"two_launch": {"KATALI_HIP_XCD": "0"}, "one_launch": {"KATALI_HIP_FUSED": "1", "KATALI_HIP_XCD": "0"},
          "xcd": {"KATALI_HIP_XCD_SHARED": "1"}}
 
@@ -462,7 +462,7 @@ def test_moe_graph_replay_matches_eager(hip, oracle, moes, mode, n_sel, monkeypa
     run, with eager work and syncs between replays. One launch: the layer's
     generation-tagged exchange across replays of the same nodes (xcd: seven
     routed experts and the shared one as eight slots, and eight with the
-    shared expert in 128-value units)."""
+    shared expert spread over every workgroup)."""
     set_mode(monkeypatch, mode)
     hidden, ffn, n_expert = 2048, 512, 256
     m = moes(hidden, ffn, n_expert, True, Q6_K)

@@ -128,7 +128,7 @@ def compare(st, a, b, with_residual=True):
 PLAIN = [
     # hidden, ffn, n_expert, n_sel, shared, down, layers (each layer its own x)
     (2048, 768, 128, 8, False, Q6_K, 5),    # the decode layer's shape
-    (2048, 512, 256, 8, True, Q6_K, 4),     # top-8 of 256 plus the shared expert in 128-value units
+    (2048, 512, 256, 8, True, Q6_K, 4),     # top-8 of 256 plus the shared expert (spread over every workgroup)
     (2048, 512, 256, 7, True, Q6_K, 3),     # seven routed plus the shared expert
     (1024, 1024, 64, 8, False, Q4_K, 4),    # narrow hidden, the widest ffn, Q4_K down
     (1024, 256, 200, 8, False, Q6_K, 3),
