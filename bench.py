@@ -184,7 +184,29 @@ def moe_free(layers, bufs):
         b.free()
 
 
-def bench_moe(hip, name, steps, warmup, ring=64, vocab=0, normed=False, stacked=False, stamps=None):
+def host_routes(hip, logits, ring, L, n_expert, n_sel):
+    """Routes with the selection given, as the engine's CPU router hands it
+    to the reference's layer call: per ring position and layer, the top
+    n_sel experts of the same logits (larger logit first, lower index on
+    ties) and their weights exp(l - l_0) / sum over the selection, computed
+    on the host and uploaded once. Returns the routes and the two buffers."""
+    lg = logits.download(np.float32).reshape(ring, L, n_expert).astype(np.float64)
+    ids = np.zeros((ring, L, n_sel), np.int32)
+    wts = np.zeros((ring, L, n_sel), np.float32)
+    for t in range(ring):
+        for li in range(L):
+            o = np.lexsort((np.arange(n_expert), -lg[t, li]))[:n_sel]
+            e = np.exp(lg[t, li][o] - lg[t, li][o[0]])
+            ids[t, li], wts[t, li] = o, e / e.sum()
+    dids, dwts = hip.to_device(ids), hip.to_device(wts)
+    routes = [[hip.moe_route(n_sel, ids=View(dids.ptr + 4 * n_sel * (t * L + li)),
+                             weights=View(dwts.ptr + 4 * n_sel * (t * L + li))) for li in range(L)]
+              for t in range(ring)]
+    return routes, (dids, dwts)
+
+
+def bench_moe(hip, name, steps, warmup, ring=64, vocab=0, normed=False, stacked=False, stamps=None,
+              given=False):
     """One hipGraph per ring position, replayed per token. vocab == 0: the
     MoE layers only (router logits from a ring). vocab > 0: the whole token
     chain (TOKEN_WORKLOADS), routing from the device router's logits.
@@ -192,10 +214,15 @@ def bench_moe(hip, name, steps, warmup, ring=64, vocab=0, normed=False, stacked=
     (katali_hip_moe_stack_*): each layer on its own x, its weight loads held
     until the previous layer's y is complete (with vocab: the normed stack,
     x_l = x_{l-1} + y_{l-1}), instead of one call per layer. stamps: a dict
-    that gets the measurement build's phase stamps of the timed replays."""
+    that gets the measurement build's phase stamps of the timed replays.
+    given: each layer call gets its selection (host_routes) instead of
+    ranking the logits on the device."""
     L, hidden, ffn, n_expert, n_sel, shared = MOE_WORKLOADS[name]
     rb_g, rb_d = row_bytes(Q4_K, hidden), row_bytes(Q6_K, ffn)
     layers, descs, routes, bufs, xs, ys, seed = moe_setup(hip, name, ring)
+    given_bufs = ()
+    if given:
+        routes, given_bufs = host_routes(hip, bufs[2], ring, L, n_expert, n_sel)
     stacks = []
 
     def token(t):
@@ -346,7 +373,7 @@ def bench_moe(hip, name, steps, warmup, ring=64, vocab=0, normed=False, stacked=
         "layer_bytes": layer_bytes,
         "pool_gb": L * (n_expert * (2 * ffn * rb_g + hidden * rb_d)) / 1e9,
     }
-    moe_free(layers, bufs)
+    moe_free(layers, bufs + tuple(given_bufs))
     return res, (L, hidden, ffn, n_expert, n_sel, shared)
 
 
@@ -1229,6 +1256,10 @@ def main():
                          "own launch (the default; kept for older command lines)")
     ap.add_argument("--separate-norm", action="store_true",
                     help="moe48tok: a k_norm_router launch (residual add, norm, router) before each layer instead")
+    ap.add_argument("--given-routing", action="store_true",
+                    help="moe48 / moe40cold: each layer call gets its experts and weights (ranked on the host from "
+                         "the same logit ring, as the reference's layer call takes them) instead of ranking "
+                         "the logits on the device")
     ap.add_argument("--stacked", action="store_true",
                     help="moe48 / moe40cold / moe48tok: the token's layers as one stacked launch "
                          "(katali_hip_moe_stack_run), each layer's input the previous layer's output")
@@ -1316,7 +1347,8 @@ def main():
     traffic = read_traffic(args.workload)
     if args.workload in MOE_WORKLOADS:
         st = {} if args.dump_stamps else None
-        res, shape = bench_moe(hip, args.workload, args.steps, args.warmup, stacked=args.stacked, stamps=st)
+        res, shape = bench_moe(hip, args.workload, args.steps, args.warmup, stacked=args.stacked, stamps=st,
+                               given=args.given_routing)
         if st:
             np.save(args.dump_stamps, st["stamps"])
         L, hidden, ffn, n_expert, n_sel, shared = shape
@@ -1326,6 +1358,9 @@ def main():
         how = (f"the {L} layers as one stacked launch per token (katali_hip_moe_stack_run; each layer on its own "
                f"x, and no layer loads a weight before the previous layer's y is complete, a decode chain's order)"
                if args.stacked else "one katali_hip_moe_layer call per layer on its own x")
+        if args.given_routing:
+            how += (", each call given its selection (ids and weights of the same logits, ranked on the host "
+                    "once, as the engine's CPU router hands them to the reference's layer call)")
         config = {
             "workload": f"{args.workload}: {L}-layer MoE decode, 1 token, hidden {hidden}, {n_expert} experts, "
                         f"top-{n_sel}{' + shared expert' if shared else ''}, gate/up {hidden}->{ffn} Q4_K, "
