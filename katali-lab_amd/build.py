@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import concurrent.futures as cf
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -32,10 +33,13 @@ CC = os.environ.get("CC", "gcc")
 # -ffp-contract=off: the only fused multiply-adds are explicit fmaf() calls, so
 #   the q8_1 quantizer and SiLU round exactly like the CPU oracle.
 # -packed-fp32-ops: never emit v_pk_{add,mul,fma}_f32.
+# -amdgpu-mfma-vgpr-form: MFMA results land in VGPRs (the AGPR form costs a
+#   v_accvgpr_read per result element before the fp32 scale arithmetic).
 HIP_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wall", "-Wno-unused-function", "-I" + INCLUDE,
 ]
 HIP_SOURCES = ["kq_moe.hip", "kq_gemv.hip", "kq_moe_batch.hip", "kq_sample.hip", "kq_norm.hip", "kq_gemv_f32.hip",
@@ -50,9 +54,11 @@ def _run(cmd: list[str]) -> str:
         raise RuntimeError(f"build step failed: {cmd[0]} ... {cmd[-1]}")
     if r.stderr.strip():
         # keep real warnings visible, drop the host-pass note about the
-        # device-only target feature and the resource remarks (read below)
+        # device-only target feature, the resource remarks (read below) and
+        # the source lines they quote
         lines = [l for l in r.stderr.splitlines()
-                 if "packed-fp32-ops" not in l and "kernel-resource-usage" not in l and l.strip()]
+                 if "packed-fp32-ops" not in l and "kernel-resource-usage" not in l and l.strip()
+                 and not re.match(r"\s*\d*\s*\|", l)]
         if lines:
             sys.stderr.write("\n".join(lines) + "\n")
     return r.stderr

@@ -154,7 +154,7 @@ __device__ __forceinline__ WaveRoute wave_topk(const MoeArgs &a, const float (&l
     int32_t id = -1;
     uint32_t mk = 0;
     if constexpr (C >= 4) {
-#pragma unroll
+#pragma nounroll   // (a loop with a wave-uniform exit: stays a loop)
         for (int j = 0; j < MAX_SEL; j++) {
             if (j >= k) break;   // uniform
             uint32_t m = key[0];
@@ -178,7 +178,7 @@ __device__ __forceinline__ WaveRoute wave_topk(const MoeArgs &a, const float (&l
         return r;
     }
     lane_sort<C>(key, eid);
-#pragma unroll
+#pragma nounroll   // (a loop with a wave-uniform exit: stays a loop)
     for (int j = 0; j < MAX_SEL; j++) {
         if (j >= k) break;   // uniform
         const uint32_t M = wave_max_u32(key[0]);

@@ -193,26 +193,27 @@ __global__ void __launch_bounds__(1024) k_mb_group(const int32_t *__restrict__ i
 // The activation chunk of one 256-value block for the 16 pairs of a column
 // group, staged in LDS: int8 values [16][MBX_ROW] (rows padded by 16 bytes
 // so the 16 pair columns one MFMA operand read touches start in different
-// banks), their q8_1 scales d8 [16][8] and exact sums of each 32 values qs
-// [16][8].
+// banks), their q8_1 scales d8 [8 sub-blocks][16 pairs] and exact sums of
+// each 32 values (as floats) qs [8][16] (four pairs of one sub-block: one
+// 16-byte read).
 constexpr uint32_t MBX_ROW = 272;
 struct MbX {
     int8_t *q;
     float *d8;
-    int32_t *qs;
+    float *qs;
 };
 __device__ __forceinline__ MbX mbx_carve(uint8_t *base) {
     MbX x;
     x.q = (int8_t *)base;
     x.d8 = (float *)(base + 16 * MBX_ROW);
-    x.qs = (int32_t *)(base + 16 * MBX_ROW + 16 * 8 * 4);
+    x.qs = (float *)(base + 16 * MBX_ROW + 16 * 8 * 4);
     return x;
 }
 constexpr uint32_t MBX_BYTES = 16 * MBX_ROW + 2 * 16 * 8 * 4;
 
-// Staging split (16 pairs per workgroup): thread t takes local pair t / 16,
-// q8_1 block 8b + (t / 2) % 8 of that pair's row and half t % 2 of its
-// values.
+// Staging split (16 pairs per 256 threads): thread t takes local pair
+// (t / 16) % 16, q8_1 block 8b + (t / 2) % 8 of that pair's row and half
+// t % 2 of its values.
 struct XPart {
     uint4 q;
     uint32_t h;
@@ -227,7 +228,7 @@ __device__ __forceinline__ XPart mbx_load(const uint8_t *row, uint32_t b) {
 }
 // Pairs past the group's count stage zeros (their B columns add nothing).
 __device__ __forceinline__ void mbx_put(const MbX &x, const XPart &v, bool valid) {
-    const uint32_t i = threadIdx.x >> 4, sb = (threadIdx.x >> 1) & 7, half = threadIdx.x & 1;
+    const uint32_t i = (threadIdx.x >> 4) & 15, sb = (threadIdx.x >> 1) & 7, half = threadIdx.x & 1;
     const uint4 q = valid ? v.q : make_uint4(0, 0, 0, 0);
     *(uint4 *)(x.q + MBX_ROW * i + 32 * sb + 16 * half) = q;
     int s = dot4(q.x, 0x01010101u, 0);
@@ -236,8 +237,8 @@ __device__ __forceinline__ void mbx_put(const MbX &x, const XPart &v, bool valid
     s = dot4(q.w, 0x01010101u, s);
     s += dpp_i<DPP_XOR1>(s);   // the block's other half
     if (half == 0) {
-        x.d8[8 * i + sb] = valid ? h2f(v.h & 0xFFFFu) : 0.0f;
-        x.qs[8 * i + sb] = s;
+        x.d8[16 * sb + i] = valid ? h2f(v.h & 0xFFFFu) : 0.0f;
+        x.qs[16 * sb + i] = (float)s;   // |s| <= 32 * 128: exact
     }
 }
 
@@ -247,11 +248,10 @@ __device__ __forceinline__ long mbx_b(const MbX &x, uint32_t col, uint32_t sb, u
 }
 
 // Four 6-bit values 0..63 (one per byte) -> int8 q6 - 32 per byte without
-// cross-byte borrows: x = q ^ 32 is q - 32 as a 6-bit two's complement
-// number; copy its bit 5 into bits 6 and 7.
+// cross-byte carries: q + 96 <= 159 stays in its byte and is (q - 32) + 128,
+// so flipping bit 7 leaves q - 32 in two's complement.
 __device__ __forceinline__ uint32_t q6_minus_32(uint32_t q) {
-    const uint32_t x = q ^ 0x20202020u, m = x & 0x20202020u;
-    return x | (m << 1) | (m << 2);
+    return (q + 0x60606060u) ^ 0x80808080u;
 }
 
 // Pairwise sum of a stream of terms t_0, t_1, ... pushed in index order (J
@@ -268,6 +268,20 @@ __device__ __forceinline__ void pw_push(float (&stk)[LV], float c) {
     else stk[L] = c;
 }
 
+// The pending groups after N pushes (levels L with bit L of N set), for 4
+// stacks, formed at this point of the program (an empty asm that reads and
+// writes each one)
+template <int N, int LV, int L = 0>
+__device__ __forceinline__ void pw_pin(float (&stk)[4][LV]) {
+    if constexpr (L < LV) {
+        if constexpr ((N >> L) & 1) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) asm volatile("" : "+v"(stk[i][L]));
+        }
+        pw_pin<N, LV, L + 1>(stk);
+    }
+}
+
 __device__ __forceinline__ v4i mfma16(long a, long b) {
     const v4i z = {0, 0, 0, 0};
     return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, z, 0, 0, 0);
@@ -279,6 +293,23 @@ __device__ __forceinline__ v4i mfma16(long a, long b) {
 // scale table [16 rows][NS].
 template <class QD>
 struct MbW;
+// 8 bytes of LDS at byte offset o (2-byte aligned): three dwords, funnel-shifted
+__device__ __forceinline__ uint2 lds_ld8_a2(const uint8_t *l, uint32_t o) {
+    const uint32_t *w = (const uint32_t *)(l + (o & ~3u));
+    const uint32_t s = o & 3u, w0 = w[0], w1 = w[1], w2 = w[2];
+    return make_uint2(__builtin_amdgcn_alignbyte(w1, w0, s), __builtin_amdgcn_alignbyte(w2, w1, s));
+}
+__device__ __forceinline__ uint32_t lds_ld4_a2(const uint8_t *l, uint32_t o) {
+    const uint32_t *w = (const uint32_t *)(l + (o & ~3u));
+    return __builtin_amdgcn_alignbyte(w[1], w[0], o & 3u);
+}
+__device__ __forceinline__ uint4 lds_ld16_a2(const uint8_t *l, uint32_t o) {
+    const uint32_t *w = (const uint32_t *)(l + (o & ~3u));
+    const uint32_t s = o & 3u, w0 = w[0], w1 = w[1], w2 = w[2], w3 = w[3], w4 = w[4];
+    return make_uint4(__builtin_amdgcn_alignbyte(w1, w0, s), __builtin_amdgcn_alignbyte(w2, w1, s),
+                      __builtin_amdgcn_alignbyte(w3, w2, s), __builtin_amdgcn_alignbyte(w4, w3, s));
+}
+
 template <>
 struct MbW<Q4K> {
     static constexpr uint32_t NS = 8;   // {d*sc, dmin*m} per 32-value sub-block
@@ -288,6 +319,30 @@ struct MbW<Q4K> {
 #pragma unroll
         for (int m = 0; m < 4; m++) q[m] = ld8(ablk + 16 + 32 * m + 8 * kc);
         h = ld16(hblk);
+    }
+    // Row-per-lane use (the lane's row is the A row it loads): the quants
+    // and its own row's header, from global memory or from a copy of the
+    // rows in LDS (block byte offset ao, 16-byte aligned as every Q4_K block
+    // of a row is)
+    __device__ __forceinline__ void load_row(const uint8_t *ablk, uint32_t kc) { load(ablk, ablk, kc); }
+    __device__ __forceinline__ void load_row_lds(const uint8_t *l, uint32_t ao, uint32_t kc) {
+#pragma unroll
+        for (int m = 0; m < 4; m++) q[m] = *(const uint2 *)(l + ao + 16 + 32 * m + 8 * kc);
+        h = *(const uint4 *)(l + ao);
+    }
+    // the row's {d*sc_j, dmin*m_j} for the 8 sub-blocks j: rs[2j], rs[2j+1]
+    __device__ __forceinline__ void row_scales(float (&rs)[16]) const {
+        Q4K::Raw raw;
+        raw.h = h;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            float ds0, ds1, dm0, dm1;
+            Q4K::scales(raw, g, ds0, ds1, dm0, dm1);
+            rs[4 * g] = ds0;
+            rs[4 * g + 1] = dm0;
+            rs[4 * g + 2] = ds1;
+            rs[4 * g + 3] = dm1;
+        }
     }
     __device__ __forceinline__ void put_scales(float2 *scl) const {
         const uint32_t lane = threadIdx.x & 63, g = lane & 3, r = lane >> 2;
@@ -308,24 +363,40 @@ struct MbW<Q4K> {
 };
 template <>
 struct MbW<Q6K> {
-    static constexpr uint32_t NS = 16;   // {d*sc, 0} per 16-value group
     uint2 ql[4], qh[2];
-    uint32_t sc, d;
-    __device__ __forceinline__ void load(const uint8_t *ablk, const uint8_t *hblk, uint32_t kc) {
+    uint32_t d;
+    // Row-per-lane use (the lane's row is the A row it loads): the quants
+    // and its own row's 16 scales and d, from global memory or from a copy
+    // of the rows in LDS (block byte offset ao: 2-byte aligned, 210-byte
+    // blocks)
+    uint4 sc16;
+    __device__ __forceinline__ void load_row(const uint8_t *ablk, uint32_t kc) {
 #pragma unroll
         for (int n = 0; n < 2; n++) {
             ql[2 * n] = ld8(ablk + 64 * n + 8 * kc);
             ql[2 * n + 1] = ld8(ablk + 64 * n + 32 + 8 * kc);
             qh[n] = ld8(ablk + 128 + 32 * n + 8 * kc);
         }
-        sc = ld4(hblk + 192 + 4 * (threadIdx.x & 3));
-        d = ld_u16(hblk + 208);
+        sc16 = ld16(ablk + 192);
+        d = ld_u16(ablk + 208);
     }
-    __device__ __forceinline__ void put_scales(float2 *scl) const {
-        const uint32_t lane = threadIdx.x & 63, g = lane & 3, r = lane >> 2;
-        const float dd = h2f(d);
+    __device__ __forceinline__ void load_row_lds(const uint8_t *l, uint32_t ao, uint32_t kc) {
 #pragma unroll
-        for (int k = 0; k < 4; k++) scl[NS * r + 4 * g + k] = make_float2(dd * (float)(int)(int8_t)(sc >> (8 * k)), 0.0f);
+        for (int n = 0; n < 2; n++) {
+            ql[2 * n] = lds_ld8_a2(l, ao + 64 * n + 8 * kc);
+            ql[2 * n + 1] = lds_ld8_a2(l, ao + 64 * n + 32 + 8 * kc);
+            qh[n] = lds_ld8_a2(l, ao + 128 + 32 * n + 8 * kc);
+        }
+        sc16 = lds_ld16_a2(l, ao + 192);
+        d = *(const uint16_t *)(l + ao + 208);
+    }
+    // the row's d * scale for the 16 groups of 16 values (groups 2j, 2j + 1
+    // of sub-block j)
+    __device__ __forceinline__ void row_scales(float (&rs)[16]) const {
+        const float dd = h2f(d);
+        const uint32_t w[4] = {sc16.x, sc16.y, sc16.z, sc16.w};
+#pragma unroll
+        for (int g = 0; g < 16; g++) rs[g] = dd * (float)(int)(int8_t)(w[g >> 2] >> (8 * (g & 3)));
     }
     // 8 int8 (q6 - 32) at values 32j + 8kc .. +7 of the block: ql nibble + 2
     // qh bits, in the block's interleave (half n = j / 4, quarter j % 4)
@@ -347,123 +418,131 @@ struct MbW<Q6K> {
 // loads. The entries of one expert are consecutive, so the tiles that share a
 // weight tile are nblk workgroups apart: with nblk a multiple of 8 they run
 // on one XCD and share its L2 copy of the weights. Per tile: the entry count
-// and the entry's record (pairs inline) at once, every weight load behind
-// them, then the pairs' activation blocks: up to 8 blocks all staged in LDS
-// at once behind one barrier (one LDS buffer per block), else a ring of
-// three in registers two blocks ahead over two LDS buffers.
+// and the entry's record (pairs inline) at once, then the pairs' activation
+// blocks (all NB staged in LDS behind one barrier; they come from L2) and
+// the first two weight blocks of each wave. The NB blocks are split into S
+// slices of NB / S consecutive blocks, one per group of four waves (wave w:
+// rows 16 (w % 4) .. +15, slice w / 4), so each SIMD runs S of the tile's
+// sub-block chains at once: a wave's per-block chain (scale table, MFMA,
+// fp32 terms) is latency-bound, not VALU-bound. A slice's weights stream
+// through a ring of three blocks in registers: block b + 2 is issued
+// before block b's arithmetic. A slice's value is the pairwise sum over
+// its blocks; the slices join as the top levels of the same tree.
 // ---------------------------------------------------------------------------
-template <int NB>
-__global__ void __launch_bounds__(256) k_mb_gu_mfma(MoeArgs a, const int32_t *__restrict__ meta, uint32_t P) {
+// (at most 128 VGPRs: two 8-wave tiles per CU)
+template <int NB, int S>
+__global__ void __launch_bounds__(256 * S, 4) k_mb_gu_mfma(MoeArgs a, const int32_t *__restrict__ meta, uint32_t P) {
+    static_assert(NB % S == 0 && (S == 1 || S == 2 || S == 4), "k_mb_gu_mfma: slices");
     extern __shared__ __align__(16) uint8_t lds[];
     const uint32_t nblk = a.ffn / 32;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t rg = wave & 3, sl = wave >> 2;   // row group, slice
     const uint64_t rb = NB * 144;
-    const uint32_t arow = lane % 16, kc = lane / 16;   // A: row, k chunk
-    const uint32_t dcol = lane % 16, drow0 = 4 * (lane / 16);   // D: pair column, first row
-    const uint32_t si = tid >> 4;   // this thread's staging pair
-    constexpr bool UP = NB <= 8;   // every block's weights in registers, every x block in LDS, at once
-    constexpr uint32_t NBUF = UP ? NB : 2;
-    {
-        const uint32_t t = blockIdx.x;
+    const uint32_t arow = lane % 16, kc = lane / 16;   // operands: weight row / pair column, k chunk
+    const uint32_t p0 = 4 * (lane / 16);               // D: pairs p0 .. p0 + 3 of weight row arow
+    const uint32_t si = (tid >> 4) & 15;   // this thread's staging pair
+    constexpr int NBS = NB / S;               // blocks per slice
+    constexpr int RING = NBS < 3 ? NBS : 3;   // weight blocks in registers: the current one and two ahead
+    constexpr int XC = NBS < 8 ? NBS : 8;     // activation blocks loaded per staging round
+    const uint32_t nent = (uint32_t)meta[1];
+    for (uint32_t t = blockIdx.x;; t += gridDim.x) {
         const uint32_t bi = t / nblk, jb = t % nblk;
-        // (a grid sized for the most entries a batch could hold has tiles past
-        // the P records: they read the last record and leave)
+        // (tiles past the entries read the last record and leave)
         const int32_t *rec = meta + mb_big_off(P) + MB_REC * min(bi, P - 1);
-        // independent loads: the entry count, the record, this thread's pair
-        // (slots past the count hold pair 0)
-        const uint32_t nent = (uint32_t)meta[1];
+        // independent loads: the record, this thread's pair (slots past the
+        // count hold pair 0)
         const int4 hd = *(const int4 *)rec;
         const uint32_t sp = (uint32_t)rec[4 + si];
-        if (bi >= nent) return;   // whole workgroup, before any barrier
+        if (bi >= nent) break;   // whole workgroup
         uint8_t *const lt = lds;
-        float2 *scl = (float2 *)(lt + NBUF * MBX_BYTES) + 16 * 8 * wave;   // this wave's [16 rows][8 sub-blocks] {d*sc, dmin*m}
-        float *gu = (float *)(lt + NBUF * MBX_BYTES + 4 * 16 * 8 * 8);      // [64 rows][16 pairs]
+        float2 *scl = (float2 *)(lt + NB * MBX_BYTES) + 16 * 8 * wave;   // this wave's [16 rows][8 sub-blocks] {d*sc, dmin*m}
+        float *gu = (float *)(lt + NB * MBX_BYTES + 4 * S * 16 * 8 * 8);  // [S slices][64 rows][16 pairs]
         const int32_t e = hd.x;
         const uint32_t cnt = (uint32_t)hd.z;
         const int32_t *pairs = rec + 4;
         const bool shared = (uint32_t)e == a.n_expert;
         const uint8_t *gb = shared ? a.gate_sh : a.gate + (uint64_t)e * a.ffn * rb;
         const uint8_t *ub = shared ? a.up_sh : a.up + (uint64_t)e * a.ffn * rb;
-        // wave w: rows 16w..16w+15 of the 64 (waves 0-1 gate, 2-3 up)
-        const uint8_t *wbase = wave < 2 ? gb + (uint64_t)(32 * jb + 16 * wave) * rb
-                                        : ub + (uint64_t)(32 * jb + 16 * (wave - 2)) * rb;
+        // row group g: rows 16g..16g+15 of the 64 (groups 0-1 gate, 2-3 up),
+        // from the slice's first block
+        const uint8_t *wbase = (rg < 2 ? gb + (uint64_t)(32 * jb + 16 * rg) * rb
+                                       : ub + (uint64_t)(32 * jb + 16 * (rg - 2)) * rb) + sl * NBS * 144;
         const uint8_t *ap = wbase + (uint64_t)arow * rb, *hp = wbase + (uint64_t)(lane >> 2) * rb;
         const uint8_t *xrow = a.xq + (uint64_t)(sp / a.bS) * a.xq_stride;
-        MbW<Q4K> w[UP ? NB : 1];
-        XPart xv[UP ? NB : 3];
+        MbW<Q4K> w[RING];
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (UP) {
-            // x first: its wait (in issue order) then waits for no weight
+        // the activations first (L2 hits, but behind the record), then the
+        // first two weight blocks: issued after the activations are in LDS, so
+        // the activation loads do not queue behind weight loads. The threads
+        // of slice s stage its activation blocks.
+        static_for<0, NBS / XC>([&](auto rc) {
+            constexpr int r = decltype(rc)::value;
+            XPart xv[XC];
 #pragma unroll
-            for (int b = 0; b < NB; b++) xv[b] = mbx_load(xrow, b);
+            for (int c = 0; c < XC; c++) xv[c] = mbx_load(xrow, sl * NBS + XC * r + c);
 #pragma unroll
-            for (int b = 0; b < NB; b++) w[b].load(ap + b * 144, hp + b * 144, kc);
-        } else {
-            w[0].load(ap, hp, kc);
-            xv[0] = mbx_load(xrow, 0);
-            xv[1] = mbx_load(xrow, NB > 1 ? 1 : 0);
-        }
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (UP) {
+            for (int c = 0; c < XC; c++) mbx_put(mbx_carve(lt + (sl * NBS + XC * r + c) * MBX_BYTES), xv[c], si < cnt);
+        });
 #pragma unroll
-            for (int b = 0; b < NB; b++) mbx_put(mbx_carve(lt + b * MBX_BYTES), xv[b], si < cnt);
-            __syncthreads();
-        }
+        for (int b = 0; b < RING - 1; b++) w[b].load(ap + b * 144, hp + b * 144, kc);
+        __syncthreads();
         // each (row, pair) value is the pairwise sum of its sub-block terms,
-        // pushed in sub-block order (kernel A's q8_1-path dot, bit for bit)
-        constexpr int LV = log2c<NB>() + 1;
+        // pushed in sub-block order (kernel A's q8_1-path dot, bit for bit):
+        // 8 sub-blocks per block, so a block's 8 terms form one subtree
+        constexpr int LV = log2c<8 * NBS>() + 1;
         float stk[4][LV];
-        static_for<0, NB>([&](auto bc) {   // unrolled: registers indexed by constants
-            constexpr uint32_t b = decltype(bc)::value;
+        static_for<0, NBS>([&](auto bc) {   // unrolled: registers indexed by constants
+            constexpr uint32_t b = decltype(bc)::value;   // the slice's block b
             __builtin_amdgcn_sched_barrier(0);   // one block's operands live at a time
-            if constexpr (!UP) {
-                if constexpr (b % 2 == 0) __syncthreads();   // the buffers written next are free (blocks b-2, b-1)
-                mbx_put(mbx_carve(lt + (b % 2) * MBX_BYTES), xv[b % 3], si < cnt);
-                xv[(b + 2) % 3] = mbx_load(xrow, b + 2 < (uint32_t)NB ? b + 2 : NB - 1);   // clamped, not skipped
-                if constexpr (b > 0) w[0].load(ap + b * 144, hp + b * 144, kc);
-                __syncthreads();
-            }
-            const MbW<Q4K> &wc = w[UP ? b : 0];
-            const MbX x = mbx_carve(lt + (UP ? b : b % 2) * MBX_BYTES);
+            if constexpr (b + RING - 1 < (uint32_t)NBS)   // (a one-block ring loads block b itself here)
+                w[(b + RING - 1) % RING].load(ap + (b + RING - 1) * 144, hp + (b + RING - 1) * 144, kc);
+            const MbW<Q4K> &wc = w[b % RING];
+            const MbX x = mbx_carve(lt + (sl * NBS + b) * MBX_BYTES);
             wc.put_scales(scl);   // wave-private table
             wave_sync_lds();
-            float t[4][8];   // the block's 8 sub-block terms per (row, pair)
+            float4 rs[4];   // the lane's row: {d*sc, dmin*m} of sub-blocks 2k, 2k + 1
 #pragma unroll
-            for (uint32_t j = 0; j < 8; j++) {
-                const long av = wc.a_op(j);
-                const v4i d = mfma16(av, mbx_b(x, arow, j, kc));   // exact isum of sub-block 8b + j
-                const float d8 = x.d8[8 * dcol + j], qs = (float)x.qs[8 * dcol + j];
+            for (int k2 = 0; k2 < 4; k2++) rs[k2] = *(const float4 *)(scl + 8 * arow + 2 * k2);
+            static_for<0, 8>([&](auto jc) {
+                constexpr uint32_t j = decltype(jc)::value;
+                const long wv = wc.a_op(j);
+                // activations as A, weights as B: d[i] = isum of (pair p0 + i, row arow), sub-block 8b + j
+                const v4i d = mfma16(mbx_b(x, arow, j, kc), wv);
+                const float4 d8 = *(const float4 *)(x.d8 + 16 * j + p0), qs = *(const float4 *)(x.qs + 16 * j + p0);
+                const float d8v[4] = {d8.x, d8.y, d8.z, d8.w}, qsv[4] = {qs.x, qs.y, qs.z, qs.w};
+                const float sA = (j & 1) ? rs[j >> 1].z : rs[j >> 1].x, sB = (j & 1) ? rs[j >> 1].w : rs[j >> 1].y;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const float2 sc = scl[8 * (drow0 + i) + j];
-                    const float A = sc.x * d8, B = sc.y * d8;
-                    t[i][j] = fmaf(A, (float)d[i], -(B * qs));
+                    const float A = sA * d8v[i], B = sB * d8v[i];
+                    pw_push<8 * b + j, 0>(stk[i], fmaf(A, (float)d[i], -(B * qsv[i])));
                 }
-            }
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float s = ((t[i][0] + t[i][1]) + (t[i][2] + t[i][3])) + ((t[i][4] + t[i][5]) + (t[i][6] + t[i][7]));
-                float sb = s;
-                asm volatile("" : "+v"(sb));   // formed here: sinking the block's arithmetic past the
-                                               // next barriers would keep its LDS reads live and spill
-                pw_push<b, 0>(stk[i], sb);   // blocks: the tree's levels above 8 sub-blocks
-            }
+            });
+            // the pending sums formed here (levels L with bit L of 8 (b + 1)
+            // set): sinking the block's arithmetic past the next barriers
+            // would keep its LDS reads live and spill
+            pw_pin<8 * (b + 1)>(stk);
             wave_sync_lds();   // the table is rewritten for the next block
         });
-        // gate/up of (row, pair) -> LDS, then SiLU-GLU and one q8_1 block per pair
+        // the slice's sums of (row, pair) -> LDS; then each value joins its
+        // slices pairwise, then SiLU-GLU and one q8_1 block per pair
 #pragma unroll
-        for (int i = 0; i < 4; i++) gu[16 * (16 * wave + drow0 + i) + dcol] = stk[i][LV - 1];   // after block NB - 1: the whole row
+        for (int i = 0; i < 4; i++) gu[16 * (64 * sl + 16 * rg + arow) + p0 + i] = stk[i][LV - 1];
         __syncthreads();
         if (tid < 16 * 8) {
             const uint32_t i = tid / 8, part = tid % 8;
             if (i < cnt) {   // whole 8-lane groups take this branch together
+                auto row = [&](uint32_t r) {   // the whole row over the NB blocks
+                    const float *g = gu + 16 * r + i;
+                    if constexpr (S == 1) return g[0];
+                    else if constexpr (S == 2) return g[0] + g[16 * 64];
+                    else return (g[0] + g[16 * 64]) + (g[2 * 16 * 64] + g[3 * 16 * 64]);
+                };
                 float4 h;
-                h.x = kq_silu_mul(gu[16 * (4 * part + 0) + i], gu[16 * (32 + 4 * part + 0) + i]);
-                h.y = kq_silu_mul(gu[16 * (4 * part + 1) + i], gu[16 * (32 + 4 * part + 1) + i]);
-                h.z = kq_silu_mul(gu[16 * (4 * part + 2) + i], gu[16 * (32 + 4 * part + 2) + i]);
-                h.w = kq_silu_mul(gu[16 * (4 * part + 3) + i], gu[16 * (32 + 4 * part + 3) + i]);
+                h.x = kq_silu_mul(row(4 * part + 0), row(32 + 4 * part + 0));
+                h.y = kq_silu_mul(row(4 * part + 1), row(32 + 4 * part + 1));
+                h.z = kq_silu_mul(row(4 * part + 2), row(32 + 4 * part + 2));
+                h.w = kq_silu_mul(row(4 * part + 3), row(32 + 4 * part + 3));
                 uint32_t d16, s16;
                 int lo, hi;
                 float dd;
@@ -479,119 +558,133 @@ __global__ void __launch_bounds__(256) k_mb_gu_mfma(MoeArgs a, const int32_t *__
 // ---------------------------------------------------------------------------
 // Down of the grouped-GEMM entries: a tile is 64 output rows (rt) x one
 // entry's <= 16 pairs -> yp, workgroup t = entry * ntile + rt as in the
-// gate/up kernel; the pairs' h rows staged once per tile.
+// gate/up kernel; the pairs' h rows staged once per tile. Up to three
+// blocks per row (a compile-time count), the tile's 64 rows, one contiguous
+// run of 64 * rb bytes (16-byte aligned), are copied to LDS in coalesced
+// 16-byte chunks and each wave builds its MFMA operands from there: per-lane
+// loads in the MFMA layout read 8 bytes from each of 16 rows per
+// instruction, at the 2-byte alignment of 210-byte Q6_K blocks, and cost
+// the L1 several times the tag lookups of the copy. Longer rows load their
+// operands from global memory one block at a time.
+// The MFMA takes the activations as A and the weights as B, so a lane holds
+// one weight row (the row whose operand it loads) for four pairs: its row's
+// scales are computed in its registers, and the q8_1 scales of its four
+// pairs come in one LDS read per sub-block. Q6_K's two 16-value scale groups
+// per 32 k: the same weight operand against activations with the other
+// group's half read from a zeroed LDS area (per lane, by address), two
+// MFMAs.
 // ---------------------------------------------------------------------------
 template <class QD, int NBD>
 __global__ void __launch_bounds__(256) k_mb_down_mfma(MoeArgs a, const int32_t *__restrict__ meta, uint32_t P) {
     extern __shared__ __align__(16) uint8_t lds[];
-    const uint32_t ntile = (a.hidden + 63) / 64;
+    const uint32_t ntile = a.hidden / 64;   // hidden is a multiple of 256: whole tiles
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t nb = NBD > 0 ? (uint32_t)NBD : a.ffn / 256;
     const uint64_t rb = (uint64_t)nb * QD::BB;
-    const uint32_t arow = lane % 16, kc = lane / 16;
-    const uint32_t dcol = lane % 16, drow0 = 4 * (lane / 16);
+    const uint32_t arow = lane % 16, kc = lane / 16;   // operands: weight row / pair column, k chunk
+    const uint32_t p0 = 4 * (lane / 16);               // D: pairs p0 .. p0 + 3 of weight row arow
     const uint32_t si = tid >> 4;
     const uint64_t hstride = (uint64_t)(a.ffn / 32) * 36;
     using W = MbW<QD>;
-    constexpr uint32_t NS = W::NS;
     constexpr bool UP = NBD > 0;
-    // every block's weights and activations at once for a compile-time block
-    // count (up to 3 blocks: more spills); else one block at a time
-    {
-        const uint32_t t = blockIdx.x;
+    constexpr uint32_t WB = UP ? 64 * NBD * QD::BB : 0;   // the tile's weight bytes (a multiple of 16)
+    constexpr uint32_t WCH = WB / 16, WPT = UP ? (WCH + 255) / 256 : 1;   // 16-byte chunks, per thread
+    // LDS: [the tile's rows WB][h blocks][256 zero bytes]
+    uint8_t *const lt = lds;
+    const uint32_t xo = WB, zo = xo + (UP ? nb : MB_DN_CHUNK) * MBX_BYTES;
+    if (tid < 64) *(uint32_t *)(lt + zo + 4 * tid) = 0u;   // read only after the tile's first barrier
+    const uint32_t nent = (uint32_t)meta[1];
+    for (uint32_t t = blockIdx.x;; t += gridDim.x) {
         const uint32_t bi = t / ntile, rt = t % ntile;
-        // (a grid sized for the most entries a batch could hold has tiles past
-        // the P records: they read the last record and leave)
+        // (tiles past the entries read the last record and leave)
         const int32_t *rec = meta + mb_big_off(P) + MB_REC * min(bi, P - 1);
-        // independent loads: the entry count, the record, this thread's pair
-        // (slots past the count hold pair 0)
-        const uint32_t nent = (uint32_t)meta[1];
+        // independent loads: the record, this thread's pair (slots past the
+        // count hold pair 0)
         const int4 hd = *(const int4 *)rec;
         const uint32_t sp = (uint32_t)rec[4 + si];
-        if (bi >= nent) return;   // whole workgroup, before any barrier
-        uint8_t *const lt = lds;
-        float2 *scl = (float2 *)(lt + (UP ? nb : MB_DN_CHUNK) * MBX_BYTES) + 16 * 16 * wave;   // [16 rows][NS] {scale, min}
+        if (bi >= nent) break;   // whole workgroup
         const int32_t e = hd.x;
         const uint32_t cnt = (uint32_t)hd.z;
         const int32_t *pairs = rec + 4;
         const bool shared = (uint32_t)e == a.n_expert;
         const uint8_t *db = shared ? a.down_sh : a.down + (uint64_t)e * a.hidden * rb;
         const uint32_t row0 = 64 * rt + 16 * wave;   // this wave's 16 rows
-        // rows past hidden read the last row and are not written
-        const uint8_t *ap = db + (uint64_t)min(row0 + arow, a.hidden - 1) * rb;
-        const uint8_t *hp = db + (uint64_t)min(row0 + (lane >> 2), a.hidden - 1) * rb;
-        W w[UP ? NBD : 1];
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int b = 0; b < (UP ? NBD : 1); b++) w[b].load(ap + b * QD::BB, hp + b * QD::BB, kc);
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t *ap = db + (uint64_t)(row0 + arow) * rb;
         const uint8_t *xrow = a.hq8 + (uint64_t)sp * hstride;
         if constexpr (UP) {
+            const uint8_t *tw = db + (uint64_t)(64 * rt) * rb;
+            uint4 wv[WPT];
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (uint32_t k = 0; k < WPT; k++) wv[k] = ld16(tw + 16 * min(tid + 256 * k, WCH - 1));   // (clamped)
             XPart xv[NBD];
 #pragma unroll
             for (int b = 0; b < NBD; b++) xv[b] = mbx_load(xrow, b);
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
             __syncthreads();   // the previous tile is done with the LDS
 #pragma unroll
-            for (int b = 0; b < NBD; b++) mbx_put(mbx_carve(lt + b * MBX_BYTES), xv[b], si < cnt);
+            for (uint32_t k = 0; k < WPT; k++)
+                if (tid + 256 * k < WCH) *(uint4 *)(lt + 16 * (tid + 256 * k)) = wv[k];
+#pragma unroll
+            for (int b = 0; b < NBD; b++) mbx_put(mbx_carve(lt + xo + b * MBX_BYTES), xv[b], si < cnt);
             __syncthreads();
         }
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll(UP ? NBD : 1)
+        constexpr int UNR = UP ? NBD : 1;
+#pragma unroll UNR
         for (uint32_t b = 0; b < nb; b++) {
+            W wc;
             if constexpr (!UP) {
                 // long rows: the h blocks go through LDS MB_DN_CHUNK at a time
                 if (b % MB_DN_CHUNK == 0) {
                     const uint32_t n = min(MB_DN_CHUNK, nb - b);
                     __syncthreads();   // the previous chunk (or tile) is done with the LDS
                     for (uint32_t c = 0; c < n; c++)
-                        mbx_put(mbx_carve(lt + c * MBX_BYTES), mbx_load(xrow, b + c), si < cnt);
+                        mbx_put(mbx_carve(lt + xo + c * MBX_BYTES), mbx_load(xrow, b + c), si < cnt);
                     __syncthreads();
                 }
-                w[0].load(ap + b * QD::BB, hp + b * QD::BB, kc);
+                wc.load_row(ap + b * QD::BB, kc);
+            } else {
+                wc.load_row_lds(lt, (16 * wave + arow) * (uint32_t)rb + b * QD::BB, kc);
             }
-            const W &wc = w[UP ? b : 0];
-            const MbX x = mbx_carve(lt + (UP ? b : b % MB_DN_CHUNK) * MBX_BYTES);
-            wc.put_scales(scl);   // wave-private table
-            wave_sync_lds();
+            const uint32_t xs = xo + (UP ? b : b % MB_DN_CHUNK) * MBX_BYTES;
+            const MbX x = mbx_carve(lt + xs);
+            float rs[16];   // the lane's row scales for this block
+            wc.row_scales(rs);
+            // activation operand of lane (pair column arow, k chunk kc);
+            // Q6_K's group-masked halves by address
+            const uint32_t bo = xs + MBX_ROW * arow + 8 * kc, zk = zo + 8 * kc;
+            const uint32_t b_lo = kc < 2 ? bo : zk, b_hi = kc < 2 ? zk : bo;
 #pragma unroll
             for (uint32_t j = 0; j < 8; j++) {   // 32-value sub-blocks
-                const long av = wc.a_op(j);
-                const long bv = mbx_b(x, arow, j, kc);
-                const float d8 = x.d8[8 * dcol + j];
+                const long wv = wc.a_op(j);
+                const float4 d8 = *(const float4 *)(x.d8 + 16 * j + p0);
+                const float d8v[4] = {d8.x, d8.y, d8.z, d8.w};
                 if constexpr (QD::TYPE == T_Q6_K) {
-                    // two 16-value scale groups: A halves zeroed in turn
-                    const long a_lo = kc < 2 ? av : 0, a_hi = kc < 2 ? 0 : av;
-                    const v4i d1 = mfma16(a_lo, bv), d2 = mfma16(a_hi, bv);
+                    const v4i d1 = mfma16(*(const long *)(lt + b_lo + 32 * j), wv);   // [pair][row]
+                    const v4i d2 = mfma16(*(const long *)(lt + b_hi + 32 * j), wv);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const float s_lo = scl[NS * (drow0 + i) + 2 * j].x, s_hi = scl[NS * (drow0 + i) + 2 * j + 1].x;
-                        acc[i] = fmaf(d8, fmaf(s_lo, (float)d1[i], s_hi * (float)d2[i]), acc[i]);
-                    }
+                    for (int i = 0; i < 4; i++)
+                        acc[i] = fmaf(d8v[i], fmaf(rs[2 * j], (float)d1[i], rs[2 * j + 1] * (float)d2[i]), acc[i]);
                 } else {
-                    const v4i d = mfma16(av, bv);
-                    const float qs = (float)x.qs[8 * dcol + j];
+                    const v4i d = mfma16(mbx_b(x, arow, j, kc), wv);
+                    const float4 qs = *(const float4 *)(x.qs + 16 * j + p0);
+                    const float qsv[4] = {qs.x, qs.y, qs.z, qs.w};
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const float2 sc = scl[NS * (drow0 + i) + j];
-                        acc[i] = fmaf(d8, fmaf(sc.x, (float)d[i], -(sc.y * qs)), acc[i]);
-                    }
+                    for (int i = 0; i < 4; i++)
+                        acc[i] = fmaf(d8v[i], fmaf(rs[2 * j], (float)d[i], -(rs[2 * j + 1] * qsv[i])), acc[i]);
                 }
-                // the sums formed here: sunk into the store branch below, the
-                // arithmetic kept every block's MFMA results live at once
-                asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
             }
-            wave_sync_lds();   // the table is rewritten for the next block
+            // the sums formed here: sunk into the store branch below, the
+            // arithmetic kept every block's MFMA results live at once
+            asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
         }
-        if (dcol < cnt) {
-            float *yrow = a.yp + (uint64_t)pairs[dcol] * a.hidden;
+        const uint32_t row = row0 + arow;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t row = row0 + drow0 + i;
-                if (row < a.hidden) yrow[row] = acc[i];
-            }
-        }
+        for (int i = 0; i < 4; i++)
+            if (p0 + i < cnt) a.yp[(uint64_t)pairs[p0 + i] * a.hidden + row] = acc[i];
     }
 }
 
@@ -613,16 +706,57 @@ __global__ void __launch_bounds__(256) k_mb_combine(const float *__restrict__ yp
 // dynamic LDS of the MFMA gate/up kernel (two x tiles, the block scales, the
 // epilogue's sums) and of the MFMA down kernel (up to MB_DN_CHUNK staged h
 // blocks and the scale table)
-static uint32_t mb_lds_gu(uint32_t nb) { return (nb <= 8 ? nb : 2) * MBX_BYTES + 4 * 16 * 8 * 8 + 64 * 16 * 4; }
-static uint32_t mb_lds_dn(uint32_t ffn) {
+// slices of the gate/up tile: two from two blocks (eight waves per tile)
+static uint32_t mb_gu_slices(uint32_t nb) { return nb >= 2 ? 2 : 1; }
+static uint32_t mb_lds_gu(uint32_t nb) {
+    const uint32_t S = mb_gu_slices(nb);
+    return nb * MBX_BYTES + 4 * S * 16 * 8 * 8 + S * 64 * 16 * 4;
+}
+// bb: the down type's block bytes
+static uint32_t mb_lds_dn(uint32_t ffn, uint32_t bb) {
     const uint32_t nb = ffn / 256;
-    return (nb <= 3 ? nb : MB_DN_CHUNK) * MBX_BYTES + 4 * 16 * 16 * 8;
+    const uint32_t w = nb <= 3 ? 64 * nb * bb : 0;   // the tile's rows
+    return w + (nb <= 3 ? nb : MB_DN_CHUNK) * MBX_BYTES + 256;
+}
+
+// Workgroups of kernel k (nt threads, lds bytes of LDS) resident at once on
+// the current device (the occupancy API, asked once per kernel, LDS size
+// and device; at least one per CU).
+static uint32_t resident_wgs(const void *k, uint32_t nt, uint32_t lds) {
+    struct Entry {
+        const void *k;
+        uint32_t lds;
+        int dev, n;
+    };
+    static thread_local Entry cache[16];
+    static thread_local uint32_t used = 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+    for (uint32_t i = 0; i < used; i++)
+        if (cache[i].k == k && cache[i].lds == lds && cache[i].dev == dev) return cache[i].n * (uint32_t)device_cu_count();
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, (int)nt, (size_t)lds) != hipSuccess || n < 1) n = 1;
+    cache[used % 16] = Entry{k, lds, dev, n};
+    used++;
+    return (uint32_t)n * (uint32_t)device_cu_count();
+}
+
+// The grouped-GEMM grids: every tile the worst case could hold, but no more
+// workgroups than fit at once; each workgroup strides over the tiles
+// (tile t on workgroup t mod grid). Workgroups past the resident set would
+// only queue behind the real tiles to learn that they have none. A strided
+// grid is kept a multiple of 8, so tiles nblk (a multiple of 8) apart share
+// an XCD as they do unstrided.
+static uint32_t mb_grid(uint32_t tiles, uint32_t resident) {
+    if (tiles <= resident) return tiles;
+    return resident >= 8 ? resident / 8 * 8 : resident;
 }
 
 uint32_t moe_batch_lds(uint32_t hidden, uint32_t ffn) {
     uint32_t m = moe_groups_lds(hidden, ffn);
     m = m > mb_lds_gu(hidden / 256) ? m : mb_lds_gu(hidden / 256);
-    return m > mb_lds_dn(ffn) ? m : mb_lds_dn(ffn);
+    const uint32_t dn = mb_lds_dn(ffn, Q6K::BB);   // the larger block of the two down types
+    return m > dn ? m : dn;
 }
 
 hipError_t launch_moe_batch(const MoeArgs &base, uint32_t T, uint32_t min_big, const float *x, float *y, uint8_t *xq,
@@ -669,7 +803,9 @@ hipError_t launch_moe_batch(const MoeArgs &base, uint32_t T, uint32_t min_big, c
     // grouped entries: each holds 1..16 pairs of one expert with >= min_big
     // pairs, so there are at most P / 16 + P / min_big + 1 of them
     const uint32_t max_big = P / MB_BIG + P / (min_big > 0 ? min_big : 1) + 1;
-    auto grid_for = [&](uint32_t tiles_per_entry) { return dim3(max_big * tiles_per_entry); };
+    auto grid_for = [&](const void *k, uint32_t nt, uint32_t lds, uint32_t tiles_per_entry) {
+        return dim3(mb_grid(max_big * tiles_per_entry, resident_wgs(k, nt, lds)));
+    };
     const uint32_t nblk = base.ffn / 32;
     const uint32_t nb_gu = base.hidden / 256;
     const uint32_t lds_gu = mb_lds_gu(base.hidden / 256);
@@ -680,21 +816,22 @@ hipError_t launch_moe_batch(const MoeArgs &base, uint32_t T, uint32_t min_big, c
                                                      (int)lds_gu);
             if (r != hipSuccess) return r;
         }
-        hipLaunchKernelGGL(kern, grid_for(nblk), dim3(256), lds_gu, sb, a, meta, P);
+        const uint32_t nt = 256 * mb_gu_slices(nb_gu);
+        hipLaunchKernelGGL(kern, grid_for((const void *)kern, nt, lds_gu, nblk), dim3(nt), lds_gu, sb, a, meta, P);
         return hipGetLastError();
     };
     switch (nb_gu) {
-        case 1: e = go_gu(k_mb_gu_mfma<1>); break;
-        case 2: e = go_gu(k_mb_gu_mfma<2>); break;
-        case 4: e = go_gu(k_mb_gu_mfma<4>); break;
-        case 8: e = go_gu(k_mb_gu_mfma<8>); break;
-        case 16: e = go_gu(k_mb_gu_mfma<16>); break;
+        case 1: e = go_gu(k_mb_gu_mfma<1, 1>); break;
+        case 2: e = go_gu(k_mb_gu_mfma<2, 2>); break;
+        case 4: e = go_gu(k_mb_gu_mfma<4, 2>); break;
+        case 8: e = go_gu(k_mb_gu_mfma<8, 2>); break;
+        case 16: e = go_gu(k_mb_gu_mfma<16, 2>); break;
         default: return joined(hipErrorInvalidValue);
     }
     if (e != hipSuccess) return joined(e);
     const uint32_t ntile = (base.hidden + 63) / 64;
     const uint32_t nb_dn = base.ffn / 256;
-    const uint32_t lds_dn = mb_lds_dn(base.ffn);
+    const uint32_t lds_dn = mb_lds_dn(base.ffn, base.down_type == T_Q6_K ? Q6K::BB : Q4K::BB);
     auto go_dn = [&](auto kern) -> hipError_t {
         if (!any_big) return hipSuccess;
         if (lds_dn > 64 * 1024) {
@@ -702,7 +839,7 @@ hipError_t launch_moe_batch(const MoeArgs &base, uint32_t T, uint32_t min_big, c
                                                      (int)lds_dn);
             if (r != hipSuccess) return r;
         }
-        hipLaunchKernelGGL(kern, grid_for(ntile), dim3(256), lds_dn, sb, a, meta, P);
+        hipLaunchKernelGGL(kern, grid_for((const void *)kern, 256, lds_dn, ntile), dim3(256), lds_dn, sb, a, meta, P);
         return hipGetLastError();
     };
     if (base.down_type == T_Q6_K) {

@@ -54,6 +54,7 @@ CASES = [
     (1024, 512, 16, 4, 33, True, Q4_K),      # Q4_K down
     (2048, 768, 128, 1, 64, False, Q6_K),    # n_sel 1
     (512, 256, 16, 2, 5, False, Q6_K),       # a short batch: every expert small
+    (256, 512, 4, 2, 40, False, Q6_K),       # hidden of one block: one-block gate/up slices
     (4096, 256, 8, 2, 20, False, Q6_K),      # wide hidden
     (1024, 2304, 8, 2, 12, True, Q6_K),      # 9 down blocks: h staged 8 blocks at a time
     (512, 2304, 4, 2, 9, False, Q4_K),       # the same with a Q4_K down
