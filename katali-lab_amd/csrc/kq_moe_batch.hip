@@ -15,10 +15,12 @@
 //    single-token layer do; h to the pair's q8_1 row, the unweighted down
 //    output to yp.
 // 4. Grouped GEMM list: k_mb_gu_mfma and k_mb_down_mfma, int8 MFMA
-//    v_mfma_i32_16x16x32_i8 (A = 16 weight rows x 32 k, B = 32 k x 16 pairs)
-//    with the block scales applied per 32-value sub-block in fp32 (per
-//    16-value group for Q6_K: two MFMAs per 32 k, each with the other half of
-//    A zeroed), same q8_1 definitions as the GEMV path.
+//    v_mfma_i32_16x16x32_i8 (one operand 16 pairs x 32 k of activations,
+//    the other 32 k x 16 weight rows) with the block scales applied per
+//    32-value sub-block in fp32 (per 16-value group for Q6_K: two MFMAs per
+//    32 k on the same weight operand, each against activations whose other
+//    half is read from a zeroed LDS area), same q8_1 definitions as the
+//    GEMV path.
 // 5. k_mb_combine: y_t = fmaf over the slots in rank order (deterministic).
 #include "kq_device.h"
 #include "kq_launch.h"
