@@ -408,6 +408,90 @@ __device__ __forceinline__ void route_finish(const MoeArgs &a, const float (&lv)
     }
 }
 
+// Routing by the whole workgroup (>= 512 threads, n_expert <= 64 C), where
+// wave_topk takes n_sel dependent rounds per wave (~1.1 us at top-8 of 128).
+// The rank of expert e is the number of experts whose key is above e's:
+//   1. wave 0 stores the 64 C keys (logit_key; 0 past n_expert) in LDS;
+//   2. thread t < 512 counts, for its experts g + 64 i (g = t / 8, i < C),
+//      the keys above theirs among the 8 C keys of chunk t % 8 (broadcast
+//      reads); the 8 lanes of g sum their counts (DPP);
+//   3. each valid expert whose count r is below n_sel stores its index and
+//      key at slot r and adds 1 to hit[r].
+// Equal keys get equal counts, so if two experts share a count below n_sel
+// some hit[r] is not 1: then each wave ranks the keys from LDS with
+// wave_topk, whose order (the lower expert index first among equal keys)
+// decides. Without such a tie the counts are the ranks wave_topk gives and
+// the selection is its selection, bit for bit. lane r < n_sel of every wave
+// ends with rank r's expert and canonical logit, as after route_finish.
+// Every wave of the workgroup calls it (two barriers); lv: wave 0's logits
+// (load_keys). scr: 64 C + 48 words of LDS that nothing else uses until every
+// wave has returned.
+template <int C>
+__device__ __forceinline__ void block_route(const MoeArgs &a, const float (&lv)[C], uint32_t *scr, GuRoute &rt) {
+    constexpr uint32_t K = 64 * C, CK = K / 8;   // keys, keys per chunk
+    uint32_t *keys = scr, *hit = scr + K, *sel = hit + 16, *selk = sel + 16;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (wave == 0) {
+#pragma unroll
+        for (int i = 0; i < C; i++) {
+            const uint32_t e = lane + 64 * i;
+            keys[e] = e < a.n_expert ? logit_key(lv[i]) : 0u;
+        }
+        if (lane < 16) hit[lane] = 0;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    if (tid < 512) {   // whole waves
+        const uint32_t g = tid >> 3, c = tid & 7;
+        uint32_t own[C], cnt[C];
+#pragma unroll
+        for (int i = 0; i < C; i++) {
+            own[i] = keys[g + 64 * i];
+            cnt[i] = 0;
+        }
+        const uint4 *ck = (const uint4 *)(keys + CK * c);
+#pragma unroll
+        for (uint32_t q = 0; q < CK / 4; q++) {
+            const uint4 v = ck[q];
+            const uint32_t kv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int i = 0; i < C; i++) cnt[i] += kv[j] > own[i] ? 1u : 0u;
+        }
+#pragma unroll
+        for (int i = 0; i < C; i++) {
+            int r = (int)cnt[i];
+            r += dpp_i<DPP_XOR1>(r);
+            r += dpp_i<DPP_XOR2>(r);
+            r += dpp_i<DPP_HALF_MIRROR>(r);
+            const uint32_t e = g + 64 * i;
+            if (c == 0 && e < a.n_expert && r < a.n_sel) {
+                atomicAdd(&hit[r], 1u);
+                sel[r] = e;
+                selk[r] = own[i];
+            }
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    const bool ranked = (int)lane < a.n_sel;
+    const uint32_t r = min(lane, 15u);
+    if (__any(ranked && hit[r] != 1u)) {   // (uniform: the same LDS for every wave)
+        float kv[C];
+#pragma unroll
+        for (int i = 0; i < C; i++) kv[i] = key_logit(keys[lane + 64 * i]);
+        const WaveRoute w = wave_topk<C>(a, kv);
+        rt.eid = w.id;
+        rt.logit = w.logit;
+    } else {
+        rt.eid = ranked ? (int32_t)sel[r] : -1;
+        rt.logit = ranked ? key_logit(selk[r]) : 0.0f;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // The normed layer's prologue (kernel A of launch_moe_normed): the steps
 // before the layer, formed by every workgroup of kernel A itself.
@@ -423,18 +507,21 @@ __device__ __forceinline__ void route_finish(const MoeArgs &a, const float (&lv)
 //   FSYNC_REP copies (lane k < 16 writes copy k). The rows and xn sit in LDS
 //   transposed by accumulator (column c at [c % 16][c / 16], row stride
 //   H / 16 + 4 floats: 16-byte chain reads, no bank conflicts).
-//   Wave 0 then waits for every row's word (two rounds of loads in flight),
-//   routes from those logits and hands the routing to the other waves in
-//   LDS.
+//   Wave 0 then waits for every row's word (one round of loads in flight),
+//   and the workgroup ranks those logits with block_route (up to 256
+//   experts; more: wave 0 ranks them and hands the routing to the other
+//   waves in LDS).
 // LDS at `area`: xn and NORMED_MAX_R rows (16 (H/16 + 4) floats each),
-// 4 doubles, the routing (16 ids, 16 logits). Returns this thread's xn
-// float4s for the q8_1 staging. (Ranking the experts over the whole
-// workgroup instead of wave 0's wave_topk measured slower: 1.65 us against
-// 1.2 us, bound by the LDS reads of 1024 threads.)
+// 4 doubles, the routing (16 ids, 16 logits), block_route's keys and slots.
+// Returns this thread's xn float4s for the q8_1 staging. (An earlier
+// whole-workgroup ranking, every thread reading every key, measured slower
+// than wave 0's wave_topk: 1.65 us against 1.2 us, bound by the LDS reads of
+// 1024 threads; block_route's threads read one eighth of the keys each.)
 // ---------------------------------------------------------------------------
 constexpr uint32_t NORMED_MAX_R = 4;
+// (+ the block routing's keys and slots: at most 256 + 48 words)
 __host__ __device__ constexpr uint32_t normed_area_bytes(uint32_t H) {
-    return 4 * (H + 64) * (1 + NORMED_MAX_R) + 32 + 128;
+    return 4 * (H + 64) * (1 + NORMED_MAX_R) + 32 + 128 + 4 * (256 + 48);
 }
 
 // A value the compiler must take as new at this point. The stacked layer
@@ -741,8 +828,12 @@ __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area,
         if (lane == 0 && a.logits_out) a.logits_out[r] = logit;
         st_dev2(xr + 2 * (512 * lane + r), ((uint64_t)tag << 32) | __float_as_uint(logit));
     }
-    // 5. wave 0: every row's word (from this workgroup's copy), the routing
-    //    from those logits, into LDS for the other waves
+    // 5. wave 0: every row's word (from this workgroup's copy); the routing
+    //    from those logits by the whole workgroup (block_route, up to 256
+    //    experts), else by wave 0 into LDS for the other waves
+    float lv[C];
+#pragma unroll
+    for (int i = 0; i < C; i++) lv[i] = 0.0f;
     if (wave == 0) {
         const uint32_t *rep = xr + 2 * 512 * (w % FSYNC_REP);
         uint64_t va[C];
@@ -756,7 +847,6 @@ __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area,
             for (int i = 0; i < C; i++) ok &= (uint32_t)(o[i] >> 32) == tag;
             return __all(ok);
         };
-        float lv[C];
         auto take = [&](const uint64_t *o) {
 #pragma unroll
             for (int i = 0; i < C; i++) lv[i] = __uint_as_float((uint32_t)o[i]);
@@ -779,19 +869,25 @@ __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area,
             }
         }
         ctx.st.mark(15);
-        const WaveRoute wr = wave_topk<C>(a, lv);
-        if (lane < 16) {
-            rte[lane] = wr.id;
-            rtl[lane] = wr.logit;
+        if constexpr (C > 4) {
+            const WaveRoute wr = wave_topk<C>(a, lv);
+            if (lane < 16) {
+                rte[lane] = wr.id;
+                rtl[lane] = wr.logit;
+            }
         }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     // 6. every wave's routing (lane r < n_sel: rank r); 7. xn for the staging
-    const bool ranked = lane < 16 && (int)lane < a.n_sel;
-    rt.eid = ranked ? rte[min(lane, 15u)] : -1;
-    rt.logit = ranked ? rtl[min(lane, 15u)] : 0.0f;
+    if constexpr (C <= 4) {
+        block_route<C>(a, lv, (uint32_t *)(rtl + 16), rt);
+    } else {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        const bool ranked = lane < 16 && (int)lane < a.n_sel;
+        rt.eid = ranked ? rte[min(lane, 15u)] : -1;
+        rt.logit = ranked ? rtl[min(lane, 15u)] : 0.0f;
+    }
     rt.w = 0.0f;
 #pragma unroll
     for (int i = 0; i < XPT; i++) {
@@ -1980,7 +2076,11 @@ __device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_
             }
         }
         if constexpr (!STK) sh_start();   // routing-independent weights, behind only the routing's loads
-        if (!STK || ctx.l == 0) route_finish<C>(a, lv, rt);
+        if constexpr (!STK) {
+            if (a.logits && a.n_sel > 0) block_route<C>(a, lv, (uint32_t *)(lds + L.scl), rt);   // (uniform)
+        } else if (ctx.l == 0) {
+            route_finish<C>(a, lv, rt);
+        }
     }
     __builtin_amdgcn_s_waitcnt(VMCNT0);
     ctx.st.mark(1);

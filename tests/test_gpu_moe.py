@@ -419,6 +419,51 @@ def test_moe_routing_matches_oracle(hip, oracle, moes, case):
     assert rel_l2(y, yd) <= 1e-5
 
 
+XCD_ROUTE_CASES = [
+    # hidden, ffn, n_expert, shared, logits: eight-slot shapes, so the
+    # XCD-sliced layer routes (the whole workgroup ranks the keys; equal keys
+    # in the first eight ranks send every wave to the per-wave ranking)
+    (1024, 256, 128, False, "ties"),
+    (1024, 256, 128, False, "special"),
+    (1024, 256, 128, False, "topties"),   # the twelve largest logits equal
+    (1024, 256, 256, False, "ties"),
+    (1024, 256, 256, False, "topties"),
+    (1024, 256, 200, False, "special"),   # n_expert not a multiple of 64
+    (1024, 256, 64, True, "ties"),        # eight routed plus the shared expert
+    (1024, 256, 8, False, "normal"),      # every expert selected
+    (1024, 256, 9, False, "topties"),
+]
+
+
+@pytest.mark.parametrize("case", XCD_ROUTE_CASES,
+                         ids=[f"e{c[2]}{'_sh' if c[3] else ''}_{c[4]}" for c in XCD_ROUTE_CASES])
+def test_moe_routing_xcd_matches_oracle(hip, oracle, moes, case, monkeypatch):
+    """The XCD-sliced layer's routing against the oracle router: the same
+    eight experts in the same order and bit-identical weights, through ties
+    (the lower index first), NaN (as -inf), +-inf and -0/+0."""
+    hidden, ffn, n_expert, shared, kind = case
+    print(f"[moe-route-xcd] case={case}", flush=True)
+    set_mode(monkeypatch, "xcd")
+    m = moes(hidden, ffn, n_expert, shared, Q6_K)
+    rng = np.random.default_rng(n_expert * 7 + len(kind))
+    x = S.activation(rng, hidden)
+    if kind == "topties":
+        logits = rng.standard_normal(n_expert).astype(np.float32)
+        logits[rng.permutation(n_expert)[:min(12, n_expert)]] = 4.5
+    else:
+        logits = route_logits(rng, n_expert, kind)
+    ids, w = oracle.router_topk(logits, 8)
+    y, gu, hq, ido, wo = run_layer(hip, m, x, 8, logits=logits)
+    assert ido.tolist() == ids.tolist()
+    if np.all(np.isfinite(w)):
+        assert np.array_equal(wo.view(np.uint32), w.view(np.uint32))
+    else:
+        assert np.array_equal(np.isnan(wo), np.isnan(w))
+        return
+    yd = oracle.moe_down_q8(m.odesc, ids, w, hq)
+    assert rel_l2(y, yd) <= 1e-5
+
+
 @pytest.mark.parametrize("case", CASES[:2], ids=["e128_k8", "e256_k8_sh"])
 def test_moe_repeatable(hip, oracle, moes, case):
     hidden, ffn, n_expert, n_sel, shared, down_type = case

@@ -11,6 +11,8 @@ layer as kernels A and B (KATALI_HIP_XCD=0) unless they name the XCD mode:
 eight-slot layers then run as the XCD-sliced layer with the steps before it
 in its prologue (one launch), against the same steps as separate calls whose
 layer is the XCD-sliced one too."""
+import copy
+
 import numpy as np
 import pytest
 
@@ -193,6 +195,43 @@ def test_normed_layer_graph_replays(hip, layers, mode, n_sel, monkeypatch):
             assert np.array_equal(y1.download(np.uint32), want[1]), i
     finally:
         hip.graph_destroy(g)
+
+
+@pytest.mark.parametrize("n_expert", [128, 256])
+def test_normed_xcd_routing_ties_match_oracle(hip, oracle, layers, n_expert, monkeypatch):
+    """Twelve equal router rows whose logits rise above the rest, so the
+    logits tie across the first eight ranks: the one-launch normed layer's
+    routing (the workgroup's ranking, then each wave's ranking once it sees
+    the tie) selects what the oracle router selects from the same logits
+    (the lower index first), and every output equals the separate steps'."""
+    set_mode(monkeypatch, "xcd")
+    hidden, ffn, n_sel = 1024, 256, 8
+    print(f"[moe-normed] ties n_expert={n_expert}", flush=True)
+    L = copy.copy(layers(hidden, ffn, n_expert, False, Q6_K))
+    rng = np.random.default_rng(n_expert)
+    xh = rng.standard_normal(hidden).astype(np.float32)
+    dh = rng.standard_normal(hidden).astype(np.float32)
+    nw = L.norm_w.download(np.float32, hidden).astype(np.float64)
+    r = xh.astype(np.float64) + dh
+    xn = r / np.sqrt(np.mean(r * r) + 1e-6) * nw
+    router = (rng.standard_normal((n_expert, hidden)) * 0.05).astype(np.float32)
+    tied = rng.permutation(n_expert)[:12]
+    router[tied] = (0.1 * np.sign(xn)).astype(np.float32)
+    L.router = hip.to_device(router)
+    x, delta = hip.to_device(xh), hip.to_device(dh)
+    want = separate(hip, L, n_sel, x, delta, 1.0)
+    got = normed(hip, L, n_sel, x, delta, 1.0)
+    hip.sync()
+    lg = got[2].download(np.float32, n_expert)
+    rest = np.delete(lg, tied)
+    assert np.all(lg[tied] == lg[tied[0]]) and lg[tied[0]] > rest.max(), "the twelve logits tie at the top"
+    assert same(got[2], want[2], n_expert), "logits"
+    ids, w = oracle.router_topk(lg, n_sel)
+    assert ids.tolist() == sorted(tied.tolist())[:n_sel]
+    for path, o in (("normed", got), ("separate", want)):
+        assert o[3].download(np.int32, n_sel).tolist() == ids.tolist(), path
+        assert np.array_equal(o[4].download(np.uint32, n_sel), w.view(np.uint32)), path
+    assert same(got[5], want[5], hidden), "y"
 
 
 def test_normed_layer_rejects_bad_arguments(hip, layers):
