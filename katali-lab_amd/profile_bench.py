@@ -130,6 +130,7 @@ def phases(args, out):
     npy = os.path.join(out, "stamps.npy")
     extra = ["--stacked"] if args.stacked else []
     extra += ["--normed-layer"] if args.normed_layer else []
+    extra += ["--given-routing"] if args.given_routing else []
     cmd = [sys.executable, os.path.join(REPO, "bench.py"), "--workload", args.workload, "--steps", str(args.steps),
            "--warmup", str(args.warmup), "--no-cpu-baseline", "--dump-stamps", npy] + extra
     if not args.summarize_only and run(cmd, os.path.join(out, "phases.log"), {"KATALI_HIP_DLL": lib}) != 0:
@@ -150,9 +151,11 @@ def phases(args, out):
     period = [(t0[b] - t0[a]) / 100.0 for a, b in zip(order, order[1:]) if 0 < t0[b] - t0[a] < 10000]
     gap = [(t0[b] - int(st[a, :, 12].max())) / 100.0 for a, b in zip(order, order[1:])
            if 0 < t0[b] - t0[a] < 10000]
-    name = f"phases_{args.workload}" + ("_stacked" if args.stacked else "") + ("_normed" if args.normed_layer else "")
+    name = f"phases_{args.workload}" + ("_stacked" if args.stacked else "") + ("_normed" if args.normed_layer else "") \
+        + ("_given" if args.given_routing else "")
     md = os.path.join(REPO, "profiles", f"{name}.md")
-    flags = (" --stacked" if args.stacked else "") + (" --normed-layer" if args.normed_layer else "")
+    flags = (" --stacked" if args.stacked else "") + (" --normed-layer" if args.normed_layer else "") \
+        + (" --given-routing" if args.given_routing else "")
     with open(md, "w") as f:
         f.write(f"# Phase stamps: {args.workload}{flags}\n\n")
         f.write(f"Made by `python katali-lab_amd/build.py --stamps && python katali-lab_amd/profile_bench.py "
@@ -191,6 +194,8 @@ def main():
                     help="moe48, moe40cold, moe48tok: the measurement build's phase stamps (no profiler)")
     ap.add_argument("--stacked", action="store_true", help="with --phases: bench.py --stacked")
     ap.add_argument("--normed-layer", action="store_true", help="with --phases: bench.py --normed-layer")
+    ap.add_argument("--given-routing", action="store_true",
+                    help="with --phases: bench.py --given-routing (the selection passed with each call)")
     ap.add_argument("--one-stream", action="store_true",
                     help="moebatch: the grouped GEMM on the library stream (KATALI_HIP_ONE_STREAM=1), so "
                          "per-kernel times add up to the layer")
