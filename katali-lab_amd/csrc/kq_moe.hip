@@ -504,7 +504,10 @@ __device__ __forceinline__ void block_route(const MoeArgs &a, const float (&lv)[
 //   dot, accumulator j's FMA chain over columns j, j + 16, ... on lane j < 16,
 //   then its horizontal sum (bit-identical to k_norm_router's rows), each
 //   published as one 8-byte device-coherent word {logit, generation + 1} in
-//   FSYNC_REP copies (lane k < 16 writes copy k). The rows and xn sit in LDS
+//   FSYNC_REP copies (lane k < 16 writes copy k). XL (the XCD layer up to
+//   128 experts): each XCD group (workgroups w with one w % 8) forms every
+//   row itself, rows w / 8 + 32 v, and publishes them in its own area
+//   through the XCD's L2, so no logit crosses an XCD. The rows and xn sit in LDS
 //   transposed by accumulator (column c at [c % 16][c / 16], row stride
 //   H / 16 + 4 floats: 16-byte chain reads, no bank conflicts).
 //   Wave 0 then waits for every row's word (one round of loads in flight),
@@ -678,7 +681,7 @@ __device__ __forceinline__ void read_y(const MoeArgs &a, StkCtx &ctx, const uint
 // the previous layer's y, polled from its tagged words; the new residual
 // goes back to ctx.res. The steps are otherwise the same, so every output is
 // the single normed layer's.
-template <int NB, int C, int NT, int XPT, bool STK = false>
+template <int NB, int C, int NT, int XPT, bool STK = false, bool XL = false>
 __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area, uint32_t U, GuRoute &rt,
                                                 float4 (&xv)[XPT], uint32_t gen, uint32_t *xr, StkCtx &ctx) {
     constexpr uint32_t H = 256 * NB;
@@ -697,7 +700,13 @@ __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area,
     int32_t *rte = (int32_t *)(part + 4);
     float *rtl = (float *)(rte + 16);
     auto at = [](uint32_t c) { return (c & 15) * TS + (c >> 4); };
-    const uint32_t R = (a.n_expert + U - 1) / U;   // the host keeps R <= NORMED_MAX_R
+    // XL (the XCD layer, n_expert <= 128): every XCD forms all the logits,
+    // workgroup w the rows w / 8 + 32 v of XCD group w % 8, exchanged in
+    // that group's area (through the XCD's L2 when the dispatch check holds,
+    // a.hloc); otherwise workgroup w forms rows w + U v for every workgroup
+    // (FSYNC_REP copies).
+    const uint32_t rw = XL ? w / XCD_SLOTS : w, ru = XL ? XCD_G / XCD_SLOTS : U;
+    const uint32_t R = (a.n_expert + ru - 1) / ru;   // the host keeps R <= NORMED_MAX_R
 
     // 1. every load: x, delta and the norm weights (threads < 256, whole
     //    waves), the router rows (all threads; clamped)
@@ -718,7 +727,7 @@ __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area,
 #pragma unroll
     for (uint32_t i = 0; i < RPT; i++) {
         const uint32_t f = min(tid + NT * i, RF - 1), v = f / Q4, q = f % Q4;
-        const uint32_t r = min(w + U * v, a.n_expert - 1);
+        const uint32_t r = min(rw + ru * v, a.n_expert - 1);
         rv[i] = *(const float4 *)&a.router[(uint64_t)r * H + 4 * q];
     }
     if constexpr (STK) {
@@ -811,7 +820,7 @@ __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area,
     uint32_t tag = gen;
     asm volatile("" : "+v"(tag));
     tag += 1;
-    const uint32_t r = w + U * wave;
+    const uint32_t r = rw + ru * wave;
     if (wave < R && r < a.n_expert && lane < 16) {
         const float *pw = rowsT + wave * VT + lane * TS, *px = xnT + lane * TS;
         float acc = 0.0f;
@@ -825,8 +834,18 @@ __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area,
         }
         // + 0.0f: a zero sum's sign as k_norm_router leaves it
         const float logit = hsum16_avx2_order(acc) + 0.0f;   // every lane of the row holds it
-        if (lane == 0 && a.logits_out) a.logits_out[r] = logit;
-        st_dev2(xr + 2 * (512 * lane + r), ((uint64_t)tag << 32) | __float_as_uint(logit));
+        const uint64_t word = ((uint64_t)tag << 32) | __float_as_uint(logit);
+        if constexpr (XL) {
+            if (lane == 0) {
+                if (w % XCD_SLOTS == 0 && a.logits_out) a.logits_out[r] = logit;
+                uint32_t *o = xr + 2 * (512 * (w % XCD_SLOTS) + r);
+                if (a.hloc) st_xcd2(o, word);
+                else st_dev2(o, word);
+            }
+        } else {
+            if (lane == 0 && a.logits_out) a.logits_out[r] = logit;
+            st_dev2(xr + 2 * (512 * lane + r), word);
+        }
     }
     // 5. wave 0: every row's word (from this workgroup's copy); the routing
     //    from those logits by the whole workgroup (block_route, up to 256
@@ -835,7 +854,7 @@ __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area,
 #pragma unroll
     for (int i = 0; i < C; i++) lv[i] = 0.0f;
     if (wave == 0) {
-        const uint32_t *rep = xr + 2 * 512 * (w % FSYNC_REP);
+        const uint32_t *rep = xr + 2 * 512 * (XL ? w % XCD_SLOTS : w % FSYNC_REP);
         uint64_t va[C];
         auto issue = [&](uint64_t *o) {
 #pragma unroll
@@ -2036,7 +2055,7 @@ __device__ __forceinline__ void gu_part(const MoeArgs &a, uint32_t slot, uint32_
     float4 xv[XPT];
     uint32_t xqv[XPT], xdv[XPT];
     if constexpr (NORMED) {
-        normed_prologue<NB, C, NT, XPT, STK>(a, lds + L.scl, XCD_G, rt, xv, gen, a.fsync + FSYNC_XR, ctx);
+        normed_prologue<NB, C, NT, XPT, STK, C == 2>(a, lds + L.scl, XCD_G, rt, xv, gen, a.fsync + FSYNC_XR, ctx);
     } else {
         float lv[C];
         route_issue<C>(a, lv, rt);
