@@ -548,7 +548,9 @@ __device__ __forceinline__ uint32_t opaque_s(uint32_t v) {
 // start, 1 routing and x in, 2 gate/up loads issued, 3 x staged, 4 wave 0's
 // dots done, 5 down loads issued, 6 h published, 7 first h poll issued, 8 h
 // seen, 9 h staged, 10 partials published, 11 partials seen, 12 y written,
-// 13 y poll started (stack), 14 y seen (stack), 15 logits seen (normed).
+// 13 y poll started (stack) or the sum of squares done (normed, single
+// layer), 14 y seen (stack) or xn staged (normed, single layer), 15 logits
+// seen (normed).
 // Wave 0 records every phase but 7 and 8, the first polling wave those.
 // In the product build the marks compile to nothing.
 [[maybe_unused]] constexpr uint32_t STAMP_LAYERS = 64, STAMP_PHASES = 16;
@@ -748,17 +750,6 @@ __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area,
         }
         __syncthreads();
     }
-    // all NORMED_MAX_R row slots, transposed (those past R hold a copy of the
-    // last row; a clamped thread writes what its twin writes)
-#pragma unroll
-    for (uint32_t i = 0; i < RPT; i++) {
-        const uint32_t f = min(tid + NT * i, RF - 1), c = 4 * (f % Q4);
-        float *rt_ = rowsT + (f / Q4) * VT;
-        rt_[at(c)] = rv[i].x;
-        rt_[at(c + 1)] = rv[i].y;
-        rt_[at(c + 2)] = rv[i].z;
-        rt_[at(c + 3)] = rv[i].w;
-    }
     // 2. residual step and the sum of squares
     if (tid < 256) {
         double sq = 0.0;
@@ -790,6 +781,19 @@ __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area,
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    if constexpr (!STK) ctx.st.mark(13);
+    // all NORMED_MAX_R row slots, transposed (those past R hold a copy of the
+    // last row; a clamped thread writes what its twin writes), only now: the
+    // sum of squares above waits for x and delta alone, not for the rows
+#pragma unroll
+    for (uint32_t i = 0; i < RPT; i++) {
+        const uint32_t f = min(tid + NT * i, RF - 1), c = 4 * (f % Q4);
+        float *rt_ = rowsT + (f / Q4) * VT;
+        rt_[at(c)] = rv[i].x;
+        rt_[at(c + 1)] = rv[i].y;
+        rt_[at(c + 2)] = rv[i].z;
+        rt_[at(c + 3)] = rv[i].w;
+    }
     // 3. xn into LDS, transposed (and from workgroup 0 to memory, with the
     //    new residual)
     if (tid < 256) {
@@ -816,6 +820,7 @@ __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area,
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    if constexpr (!STK) ctx.st.mark(14);
     // 4. this workgroup's router rows: wave v, lanes 0..15
     uint32_t tag = gen;
     asm volatile("" : "+v"(tag));

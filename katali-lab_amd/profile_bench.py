@@ -118,7 +118,8 @@ def pick(d, sub):
 PHASES = ["layer start (first workgroup = 0)", "routing and x in", "gate/up loads issued", "x staged (q8_1 in LDS)",
           "wave 0's gate/up dots done", "down loads issued", "h published", "first h poll issued (polling wave)",
           "slot's h seen (polling wave)", "h staged as q8_1", "down partials published", "eight partials seen",
-          "y written", "previous y: poll started (stack)", "previous y seen (stack)", "router logits seen (normed)"]
+          "y written", "stack: previous y poll started; normed: sum of squares done",
+          "stack: previous y seen; normed: xn staged", "router logits seen (normed)"]
 
 
 def phases(args, out):
