@@ -35,6 +35,13 @@ replay, and consecutive steps replay consecutive positions.
             int8 MFMA grouped GEMM, the rest on the GEMV kernels; 16 layers
             of distinct weights per pass; the JSON value is the n_sel = 8,
             64-token point, the whole sweep is in "sweep".
+  floor48   one moe48 layer's 24.5 MB of weights streamed with no arithmetic
+            in the layer's launch shape (katali_hip_stream_floor): one read,
+            two launches, and one launch with the layer's two in-kernel waits;
+            then the exchange probe (katali_hip_exchange_probe): the time of
+            one word handed from one workgroup to a waiting one inside an XCD
+            group (through its L2, or written through) and across XCDs, in
+            "exchanges"; the JSON value is the one-launch read.
   tier48    48 host-routed layers of the moe48 expert shape whose experts
             come through the expert VRAM tier (64 slots) from a GGUF file
             written on the box, m in {0, 1, 2, 4} misses per layer call,
@@ -433,6 +440,44 @@ def bench_floor(hip, base, steps, warmup, kinds=None):
     pool.free()
     sync.free()
     return out, (L, a_bytes, b_bytes)
+
+
+XCHG_KINDS = {0: "inside one XCD group, through its L2", 1: "inside one XCD group, written through",
+              2: "across two XCDs, written through"}
+
+
+def bench_xchg(hip, rounds=2000, reps=5):
+    """The exchange probe (katali_hip_exchange_probe): per kind, the median
+    over reps calls of the time per one-way hand-off (a call makes
+    2 * rounds of them), with the XCC ids the pairs ran on."""
+    words = hip.alloc(4 * 1025)
+    hip.memset(words, 0, 4 * 1025)
+    hip.sync()
+    out = {}
+    for kind, what in XCHG_KINDS.items():
+        hip.exchange_probe(kind, 64, words)   # warm-up
+        hip.sync()
+        us = []
+        for _ in range(reps):
+            e0, e1 = hip.event(), hip.event()
+            hip.record(e0)
+            hip.exchange_probe(kind, rounds, words)
+            hip.record(e1)
+            hip.sync()
+            us.append(hip.elapsed_ms(e0, e1) * 1e3 / (2 * rounds))
+            hip.event_destroy(e0)
+            hip.event_destroy(e1)
+        w = words.download(np.uint32, 1025)
+        ids, err = w[768:1024], int(w[1024])
+        part = np.arange(256) ^ (1 if kind == 2 else 8)
+        same = int(np.sum(ids == ids[part]))
+        out[kind] = {"what": what, "us_one_way": round(float(np.median(us)), 3),
+                     "us_range": [round(min(us), 3), round(max(us), 3)], "rounds": rounds,
+                     "pairs_on_one_xcd": f"{same // 2} of 128", "wait_expired": bool(err & 1)}
+        print(f"[bench] exchange {kind} ({what}): {np.median(us):.3f} us one way, "
+              f"{same // 2} of 128 pairs on one XCD", file=sys.stderr, flush=True)
+    words.free()
+    return out
 
 
 # ---------------------------------------------------------------------------
@@ -1432,6 +1477,8 @@ def main():
         }
         kernel = "k_floor_read (one launch per unit)"
         extra = {"floors": floors}
+        if not args.floor_kind:   # (profiling runs name their floors)
+            extra["exchanges"] = bench_xchg(hip)
     elif args.workload == "moe48duty":
         res, shape = bench_duty(hip, "moe48", args.steps, args.warmup)
         L, hidden, ffn, n_expert, n_sel, shared = shape

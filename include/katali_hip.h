@@ -468,6 +468,19 @@ int katali_hip_phase_stamps(void *host, size_t bytes);
  * reference. */
 int katali_hip_stream_floor(int32_t kind, const void *a, size_t a_bytes, const void *b, size_t b_bytes,
                             void *sync);
+/* The exchange probe: the latency of the one-launch layers' word hand-offs
+ * with nothing else running. 256 single-wave workgroups; workgroup b and its
+ * partner p pass one tagged 64-bit word back and forth `rounds` times (1 ..
+ * 2^20; a round is two one-way hand-offs), each waiting for the other's
+ * word before sending its own: kind 0 p = b ^ 8 (one XCD) through that XCD's
+ * L2 (written through where the dispatch check failed), kind 1 p = b ^ 8
+ * written through, kind 2 p = b ^ 1 (another XCD) written through. words: a
+ * device buffer of 4 * 1025 bytes, zeroed once by the caller and kept for
+ * every later call: [256] generations, [256] 64-bit words, [256] each
+ * workgroup's XCC id in the last call, [1] error bits (bit 0: a wait ran out
+ * of polls). Time it with events around the call. No counterpart in the
+ * reference. */
+int katali_hip_exchange_probe(int32_t kind, uint32_t rounds, void *words);
 
 /* ---- self-test and synthetic data for the harnesses ------------------------ */
 /* cuda-dp4a-selftest equivalent (README.md:17): a synthetic Q4_K and Q6_K

@@ -745,6 +745,15 @@ int katali_hip_stream_floor(int32_t kind, const void *a, size_t a_bytes, const v
     return launched(e, "stream floor");
 }
 
+int katali_hip_exchange_probe(int32_t kind, uint32_t rounds, void *words) {
+    int rc = ensure();
+    if (rc) return rc;
+    if (kind < 0 || kind > 2) return fail(KATALI_HIP_E_INVALID, "exchange probe kind %d (0..2)", kind);
+    if (!words) return fail(KATALI_HIP_E_INVALID, "null buffer");
+    if (rounds < 1 || rounds > (1u << 20)) return fail(KATALI_HIP_E_INVALID, "rounds %u (1..2^20)", rounds);
+    return launched(kq::launch_xchg(kind, rounds, (uint32_t *)words, g_stream), "exchange probe");
+}
+
 int katali_hip_one_launch(int32_t mode) {
     const int was = kq::xcd_disabled() ? 0 : 1;
     if (mode == 0) kq::xcd_disable();

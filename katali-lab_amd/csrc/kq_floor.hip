@@ -120,6 +120,59 @@ __global__ void __launch_bounds__(FLOOR_NT) k_floor_two_phase(const uint4 *a, ui
     if (acc == 0x9E3779B9u) sink[0] = acc;
 }
 
+// The exchange probe: how long one word takes from a workgroup to a waiting
+// workgroup, with nothing else running. XCHG_G single-wave workgroups; lane 0
+// of workgroup b and of its partner p take turns for `rounds` rounds (b < p
+// sends first: one round is two one-way exchanges), each waiting for the
+// other's word with this call's tag before it sends its own. kind 0: p = b ^ 8
+// (the same XCD group as the XCD-sliced layer uses), words through that XCD's
+// L2 when the dispatch check holds (st_xcd2), else written through; kind 1:
+// p = b ^ 8, written through (st_dev2); kind 2: p = b ^ 1 (another XCD),
+// written through. Loads are ld_dev2. Words: [XCHG_G generations][XCHG_G
+// 64-bit mailboxes][XCHG_G XCC ids of the last call]; tags run on from each
+// workgroup's generation (every workgroup runs every call, so they stay
+// equal), nothing is cleared between calls; every wait is bounded
+// (FLOOR_SPIN_LIMIT polls, then bit 0 of the error word after the ids).
+constexpr uint32_t XCHG_G = 256;
+__global__ void __launch_bounds__(64) k_xchg(uint32_t *words, uint32_t rounds, uint32_t kind, uint32_t local) {
+    if (threadIdx.x != 0) return;
+    const uint32_t b = blockIdx.x, p = kind == 2 ? (b ^ 1u) : (b ^ 8u);
+    uint32_t *gen = words, *box = words + XCHG_G, *ids = words + 3 * XCHG_G, *err = ids + XCHG_G;
+    ids[b] = xcc_id();
+    const uint32_t base = floor_ld(gen + b);
+    const bool l2 = kind == 0 && local;
+    auto send = [&](uint32_t tag) {
+        if (l2) st_xcd2(box + 2 * b, tag);
+        else st_dev2(box + 2 * b, tag);
+    };
+    auto wait = [&](uint32_t tag) {
+        for (uint32_t spins = 0; spins < FLOOR_SPIN_LIMIT; spins++)
+            if ((uint32_t)ld_dev2(box + 2 * p) == tag) return true;
+        return false;
+    };
+    bool ok = true;
+    for (uint32_t r = 0; r < rounds && ok; r++) {
+        const uint32_t t1 = base + 2 * r + 1, t2 = t1 + 1;
+        if (b < p) {
+            send(t1);
+            ok = wait(t2);
+        } else {
+            ok = wait(t1);
+            if (ok) send(t2);
+        }
+    }
+    if (!ok) atomicOr(err, 1u);
+    floor_st(gen + b, base + 2 * rounds);
+}
+
+uint32_t xchg_words() { return 4 * XCHG_G + 1; }
+
+hipError_t launch_xchg(int kind, uint32_t rounds, uint32_t *words, hipStream_t s) {
+    if (kind < 0 || kind > 2 || !rounds || !words) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_xchg, dim3(XCHG_G), dim3(64), 0, s, words, rounds, (uint32_t)kind, xcd_local() ? 1u : 0u);
+    return hipGetLastError();
+}
+
 uint32_t floor_sync_words() { return FLOOR_SYNC_WORDS; }
 
 hipError_t launch_floor(int kind, const uint8_t *a, uint64_t a_bytes, const uint8_t *b, uint64_t b_bytes,

@@ -257,6 +257,12 @@ hipError_t read_stamps(void *host, size_t bytes);
 uint32_t floor_sync_words();
 hipError_t launch_floor(int kind, const uint8_t *a, uint64_t a_bytes, const uint8_t *b, uint64_t b_bytes,
                         uint32_t *sync, hipStream_t s);
+// The exchange probe (kq_floor.hip, k_xchg): rounds of a word passed back
+// and forth between workgroup pairs, kind 0 inside an XCD group through its
+// L2, 1 inside it written through, 2 across XCDs; words: xchg_words()
+// zeroed words, kept between launches.
+uint32_t xchg_words();
+hipError_t launch_xchg(int kind, uint32_t rounds, uint32_t *words, hipStream_t s);
 // Top-n_sel routing of n_tokens rows of logits [n_tokens][n_expert] (<= 512
 // experts, 1 <= n_sel <= min(16, n_expert)): ids / weights [n_tokens][n_sel],
 // each row as the single-token layer routes it.

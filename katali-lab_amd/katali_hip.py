@@ -73,6 +73,7 @@ SIGNATURES = {
     "katali_hip_xcd_handoff": (C.c_int, [_i32]),
     "katali_hip_phase_stamps": (C.c_int, [_vp, _sz]),
     "katali_hip_stream_floor": (C.c_int, [_i32, _vp, _sz, _vp, _sz, _vp]),
+    "katali_hip_exchange_probe": (C.c_int, [_i32, C.c_uint32, _vp]),
     "katali_hip_stager_create": (C.c_int, [_u64, _u32, C.POINTER(_vp)]),
     "katali_hip_stager_destroy": (C.c_int, [_vp]),
     "katali_hip_stager_mark": (C.c_int, [_vp, C.POINTER(_u64)]),
@@ -299,6 +300,10 @@ class KataliHip:
         out = np.zeros((64, 256, 16), np.uint64)
         self.check(self.lib.katali_hip_phase_stamps(out.ctypes.data, out.nbytes))
         return out
+
+    def exchange_probe(self, kind: int, rounds: int, words) -> None:
+        """The exchange probe (katali_hip_exchange_probe)."""
+        self.check(self.lib.katali_hip_exchange_probe(kind, rounds, words.ptr))
 
     def stream_floor(self, kind: int, a, a_bytes: int, b, b_bytes: int, sync) -> None:
         """The streaming floors (katali_hip_stream_floor)."""

@@ -35,3 +35,39 @@ def test_floor_kinds_run(hip):
     for bad in ((3, n), (0, 17)):
         with pytest.raises(HipError):
             hip.stream_floor(bad[0], a, bad[1], None, 0, sync)
+
+
+def test_exchange_probe_pairs_and_latency(hip):
+    """Each kind of the exchange probe runs its rounds without a wait running
+    out, with the pairs where the kind puts them (b and b ^ 8 on one XCD,
+    b and b ^ 1 on two), and one hand-off takes between 0.05 and 20 us."""
+    words = hip.alloc(4 * 1025)
+    hip.memset(words, 0, 4 * 1025)
+    try:
+        for kind in (0, 1, 2):
+            print(f"[xchg] kind={kind}", flush=True)
+            for rounds in (1, 300):   # tags run on from call to call
+                e0, e1 = hip.event(), hip.event()
+                hip.record(e0)
+                hip.exchange_probe(kind, rounds, words)
+                hip.record(e1)
+                hip.sync()
+                ms = hip.elapsed_ms(e0, e1)
+                hip.event_destroy(e0)
+                hip.event_destroy(e1)
+            w = words.download(np.uint32, 1025)
+            assert int(w[1024]) & 1 == 0, "a wait ran out of polls"
+            ids = w[768:1024]
+            part = np.arange(256) ^ (1 if kind == 2 else 8)
+            if kind < 2:
+                assert np.array_equal(ids, ids[part])
+            else:
+                assert not np.any(ids == ids[part])
+            us = ms * 1e3 / (2 * 300)
+            assert 0.05 < us < 20.0, us
+        with pytest.raises(HipError):
+            hip.exchange_probe(3, 10, words)
+        with pytest.raises(HipError):
+            hip.exchange_probe(0, 0, words)
+    finally:
+        words.free()
