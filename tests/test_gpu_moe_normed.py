@@ -40,6 +40,10 @@ XCD_CASES = [
     (2048, 512, 256, 7, True, Q6_K, 0.5),      # seven routed and the shared expert; one router row per workgroup
     (1024, 1024, 64, 8, False, Q4_K, 1.0),     # narrow hidden, the widest ffn, Q4_K down
     (1024, 256, 200, 8, False, Q6_K, 0.25),    # rows not a multiple of 64
+    # up to 128 experts each XCD forms every logit itself, rows w / 8 + 32 v:
+    # expert counts that leave the last row group partly empty
+    (1024, 256, 100, 8, False, Q6_K, 1.0),
+    (2048, 256, 40, 8, False, Q6_K, None),
 ]
 
 
