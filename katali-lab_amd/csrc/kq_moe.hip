@@ -507,9 +507,12 @@ __device__ __forceinline__ void block_route(const MoeArgs &a, const float (&lv)[
 //   FSYNC_REP copies (lane k < 16 writes copy k). XL (the XCD layer up to
 //   128 experts): each XCD group (workgroups w with one w % 8) forms every
 //   row itself, rows w / 8 + 32 v, and publishes them in its own area
-//   through the XCD's L2, so no logit crosses an XCD. The rows and xn sit in LDS
-//   transposed by accumulator (column c at [c % 16][c / 16], row stride
-//   H / 16 + 4 floats: 16-byte chain reads, no bank conflicts).
+//   through the XCD's L2 (written through where the dispatch check failed,
+//   a.hloc 0), so no logit has to cross an XCD.
+//   The rows land in LDS after the sum of squares (which then waits for x
+//   and delta alone); rows and xn sit there transposed by accumulator
+//   (column c at [c % 16][c / 16], row stride H / 16 + 4 floats: 16-byte
+//   chain reads, no bank conflicts).
 //   Wave 0 then waits for every row's word (one round of loads in flight),
 //   and the workgroup ranks those logits with block_route (up to 256
 //   experts; more: wave 0 ranks them and hands the routing to the other
