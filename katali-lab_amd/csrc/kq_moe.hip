@@ -408,6 +408,97 @@ __device__ __forceinline__ void route_finish(const MoeArgs &a, const float (&lv)
     }
 }
 
+// lanes of this wave below this one whose bit is set in b
+__device__ __forceinline__ uint32_t lanes_below(uint64_t b) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+}
+
+// Routing of more than 128 experts (C >= 4) by wave 0 from a candidate set,
+// handed to every wave behind one barrier. The experts fall into eight
+// disjoint groups (expert index mod 8: each holds valid experts once
+// n_expert >= 8); at least eight keys lie at or above T, the least of the
+// eight group maxima, so whenever the keys >= T (the candidates) number at
+// least n_sel, every expert left out ranks below all of them and the top
+// n_sel are candidates. The candidates go to LDS in ascending expert order
+// as 64-bit words (key << 32 | ~expert): unique, and ordered as wave_topk
+// orders (larger key, then the lower expert index), so the words above a
+// candidate's own count its rank, ties included. Random logits leave about
+// 20 candidates of 256 (the all-pairs count compares 256 x 256 keys). With
+// more than 64 candidates (heavy ties, or T = 0 below eight experts) or
+// fewer than n_sel, wave 0 ranks with wave_topk instead. lane r <
+// n_sel of every wave ends with rank r's expert and canonical logit. scr:
+// 160 words of LDS that nothing else uses until every wave has returned.
+template <int C>
+__device__ __forceinline__ void wave0_route(const MoeArgs &a, const float (&lv)[C], uint32_t *scr, GuRoute &rt) {
+    uint64_t *cw = (uint64_t *)scr;                  // 64 candidate words
+    uint32_t *sel = scr + 128, *sell = sel + 16;     // rank r: expert, logit bits
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    if (tid < 64) {
+        uint32_t key[C];
+#pragma unroll
+        for (int i = 0; i < C; i++) {
+            const uint32_t e = lane + 64 * i;
+            key[i] = e < a.n_expert ? logit_key(lv[i]) : 0u;
+        }
+        uint32_t g = key[0];
+#pragma unroll
+        for (int i = 1; i < C; i++) g = max(g, key[i]);
+        g = max(g, (uint32_t)dpp_i<DPP_ROR8>((int)g));   // lanes l and l ^ 8 of a row
+        const auto r16 = __builtin_amdgcn_permlane16_swap(g, g, false, false);
+        g = max((uint32_t)r16[0], (uint32_t)r16[1]);
+        const auto r32 = __builtin_amdgcn_permlane32_swap(g, g, false, false);
+        g = max((uint32_t)r32[0], (uint32_t)r32[1]);      // lane l: the maximum of group l % 8
+        g = min(g, (uint32_t)dpp_i<DPP_XOR1>((int)g));
+        g = min(g, (uint32_t)dpp_i<DPP_XOR2>((int)g));
+        g = min(g, (uint32_t)dpp_i<DPP_HALF_MIRROR>((int)g));
+        const uint32_t T = (uint32_t)__builtin_amdgcn_readfirstlane((int)g);
+        uint64_t bal[C];
+        uint32_t m = 0;
+#pragma unroll
+        for (int i = 0; i < C; i++) {
+            bal[i] = __ballot(key[i] >= T);
+            m += (uint32_t)__builtin_popcountll(bal[i]);
+        }
+        if (m >= (uint32_t)a.n_sel && m <= 64) {   // (uniform)
+            uint32_t base = 0;
+#pragma unroll
+            for (int i = 0; i < C; i++) {
+                if (key[i] >= T)
+                    cw[base + lanes_below(bal[i])] = ((uint64_t)key[i] << 32) | (uint32_t)~(lane + 64 * i);
+                base += (uint32_t)__builtin_popcountll(bal[i]);
+            }
+            if (lane >= m) cw[lane] = 0;   // below every candidate word (keys of candidates are > 0)
+            wave_sync_lds();
+            const uint64_t own = cw[lane];
+            const uint4 *q = (const uint4 *)cw;
+            uint32_t r = 0;
+#pragma nounroll
+            for (uint32_t j = 0; j < (m + 1) / 2; j++) {   // (uniform)
+                const uint4 v = q[j];
+                r += (((uint64_t)v.y << 32) | v.x) > own ? 1u : 0u;
+                r += (((uint64_t)v.w << 32) | v.z) > own ? 1u : 0u;
+            }
+            if (lane < m && r < (uint32_t)a.n_sel) {
+                sel[r] = ~(uint32_t)own;
+                sell[r] = __float_as_uint(key_logit((uint32_t)(own >> 32)));
+            }
+        } else {
+            const WaveRoute w = wave_topk<C>(a, lv, a.n_sel);
+            if ((int)lane < a.n_sel) {
+                sel[lane] = (uint32_t)w.id;
+                sell[lane] = __float_as_uint(w.logit);
+            }
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    const bool ranked = (int)lane < a.n_sel;
+    const uint32_t r = min(lane, 15u);
+    rt.eid = ranked ? (int32_t)sel[r] : -1;
+    rt.logit = ranked ? __uint_as_float(sell[r]) : 0.0f;
+}
+
 // Routing by the whole workgroup (>= 512 threads, n_expert <= 64 C), where
 // wave_topk takes n_sel dependent rounds per wave (~1.1 us at top-8 of 128).
 // The rank of expert e is the number of experts whose key is above e's:
@@ -425,9 +516,14 @@ __device__ __forceinline__ void route_finish(const MoeArgs &a, const float (&lv)
 // ends with rank r's expert and canonical logit, as after route_finish.
 // Every wave of the workgroup calls it (two barriers); lv: wave 0's logits
 // (load_keys). scr: 64 C + 48 words of LDS that nothing else uses until every
-// wave has returned.
+// wave has returned. More than 128 experts (C >= 4): wave0_route, whose
+// candidate set needs ~1/100 of the compares.
 template <int C>
 __device__ __forceinline__ void block_route(const MoeArgs &a, const float (&lv)[C], uint32_t *scr, GuRoute &rt) {
+    if constexpr (C >= 4) {
+        wave0_route<C>(a, lv, scr, rt);
+        return;
+    }
     constexpr uint32_t K = 64 * C, CK = K / 8;   // keys, keys per chunk
     uint32_t *keys = scr, *hit = scr + K, *sel = hit + 16, *selk = sel + 16;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
