@@ -472,11 +472,21 @@ __device__ __forceinline__ void wave0_route(const MoeArgs &a, const float (&lv)[
             const uint64_t own = cw[lane];
             const uint4 *q = (const uint4 *)cw;
             uint32_t r = 0;
-#pragma nounroll
-            for (uint32_t j = 0; j < (m + 1) / 2; j++) {   // (uniform)
+            // the first 32 words in one batch of loads (m <= 32 in ~92 % of
+            // random cases; the words past m are 0 and count nothing)
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
                 const uint4 v = q[j];
                 r += (((uint64_t)v.y << 32) | v.x) > own ? 1u : 0u;
                 r += (((uint64_t)v.w << 32) | v.z) > own ? 1u : 0u;
+            }
+            if (m > 32) {   // (uniform)
+#pragma unroll
+                for (int j = 16; j < 32; j++) {
+                    const uint4 v = q[j];
+                    r += (((uint64_t)v.y << 32) | v.x) > own ? 1u : 0u;
+                    r += (((uint64_t)v.w << 32) | v.z) > own ? 1u : 0u;
+                }
             }
             if (lane < m && r < (uint32_t)a.n_sel) {
                 sel[r] = ~(uint32_t)own;
