@@ -472,18 +472,13 @@ __device__ __forceinline__ void wave0_route(const MoeArgs &a, const float (&lv)[
             const uint64_t own = cw[lane];
             const uint4 *q = (const uint4 *)cw;
             uint32_t r = 0;
-            // the first 32 words in one batch of loads (m <= 32 in ~92 % of
-            // random cases; the words past m are 0 and count nothing)
+            // 16 words per batch of loads (about 20 candidates at random; the
+            // words past m are 0 and count nothing)
+#pragma nounroll
+            for (uint32_t b = 0; b < (m + 15) / 16; b++) {   // (uniform)
 #pragma unroll
-            for (int j = 0; j < 16; j++) {
-                const uint4 v = q[j];
-                r += (((uint64_t)v.y << 32) | v.x) > own ? 1u : 0u;
-                r += (((uint64_t)v.w << 32) | v.z) > own ? 1u : 0u;
-            }
-            if (m > 32) {   // (uniform)
-#pragma unroll
-                for (int j = 16; j < 32; j++) {
-                    const uint4 v = q[j];
+                for (uint32_t j = 0; j < 8; j++) {
+                    const uint4 v = q[8 * b + j];
                     r += (((uint64_t)v.y << 32) | v.x) > own ? 1u : 0u;
                     r += (((uint64_t)v.w << 32) | v.z) > own ? 1u : 0u;
                 }
@@ -493,7 +488,10 @@ __device__ __forceinline__ void wave0_route(const MoeArgs &a, const float (&lv)[
                 sell[r] = __float_as_uint(key_logit((uint32_t)(own >> 32)));
             }
         } else {
-            const WaveRoute w = wave_topk<C>(a, lv, a.n_sel);
+            float kv[C];   // (from the keys: lv is dead by now)
+#pragma unroll
+            for (int i = 0; i < C; i++) kv[i] = key_logit(key[i]);
+            const WaveRoute w = wave_topk<C>(a, kv, a.n_sel);
             if ((int)lane < a.n_sel) {
                 sel[lane] = (uint32_t)w.id;
                 sell[lane] = __float_as_uint(w.logit);
@@ -526,11 +524,11 @@ __device__ __forceinline__ void wave0_route(const MoeArgs &a, const float (&lv)[
 // ends with rank r's expert and canonical logit, as after route_finish.
 // Every wave of the workgroup calls it (two barriers); lv: wave 0's logits
 // (load_keys). scr: 64 C + 48 words of LDS that nothing else uses until every
-// wave has returned. More than 128 experts (C >= 4): wave0_route, whose
-// candidate set needs ~1/100 of the compares.
-template <int C>
+// wave has returned. CAND (the default for more than 128 experts, C >= 4):
+// wave0_route, whose candidate set needs ~1/100 of the compares.
+template <int C, bool CAND = (C >= 4)>
 __device__ __forceinline__ void block_route(const MoeArgs &a, const float (&lv)[C], uint32_t *scr, GuRoute &rt) {
-    if constexpr (C >= 4) {
+    if constexpr (CAND) {
         wave0_route<C>(a, lv, scr, rt);
         return;
     }
@@ -1012,7 +1010,8 @@ __device__ __forceinline__ void normed_prologue(const MoeArgs &a, uint8_t *area,
     }
     // 6. every wave's routing (lane r < n_sel: rank r); 7. xn for the staging
     if constexpr (C <= 4) {
-        block_route<C>(a, lv, (uint32_t *)(rtl + 16), rt);
+        // (the stacked layer keeps the all-pairs count: its registers are at the limit)
+        block_route<C, C >= 4 && !STK>(a, lv, (uint32_t *)(rtl + 16), rt);
     } else {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
         __builtin_amdgcn_s_barrier();
